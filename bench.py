@@ -1,0 +1,183 @@
+"""Benchmark of the fused NVFP4 sparse-attention decode on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload gqa_decode_b32] [--layers L] [--splits S]
+
+A step is one layer-step of batched GQA sparse decode: batch 32, 32 query / 4 KV heads, head size 128, context
+32768 per request, top-2048 sorted unique indices per request, NVFP4 paged KV (page 64, shuffled pages) built from
+bf16 N(0,1) with 1% outlier channels x8. The timed region replays a HIP graph of L layer-steps, each on its own
+layer's pool (distinct HBM, as the layers of a decode step), so the gathered rows come from HBM rather than from the
+previous step's cache lines; ms_per_step is the event-timed mean over the K steps.
+
+Prints one JSON line: value = achieved algorithmic HBM bandwidth (gathered KV payload + scales per step / step
+time), plus the µs per layer-step, the roofline record, and the CPU oracle timed on the host as a reported
+baseline.
+"""
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = 'NVFP4-KV sparse-attn decode µs/layer-step + achieved HBM GB/s (% peak)'
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_model():
+    try:
+        for line in open('/proc/cpuinfo'):
+            if line.startswith('model name'):
+                return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or 'unknown'
+
+
+def build_layer(w, gen, ops, workloads):
+    k = workloads.kv_tensor(w.slots, w.kv_heads, w.dim, gen, 'cuda')
+    k_pay, k_sf, gk = ops.nvfp4_encode(k)
+    del k
+    v = workloads.kv_tensor(w.slots, w.kv_heads, w.dim, gen, 'cuda')
+    v_pay, v_sf, gv = ops.nvfp4_encode(v)
+    del v
+    return (k_pay, v_pay, k_sf, v_sf, gk, gv)
+
+
+def cpu_baseline(raw, q, pt, idx, seq, w, scale, seconds):
+    """The CPU oracle (numpy, one thread) on the same workload: per request gather through the page table, NVFP4
+    dequant, FP32 softmax attention. Timed on a bounded sample of requests and scaled to the layer-step."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import attention
+
+    pt_h, idx_h, seq_h = pt.cpu().numpy(), idx.cpu().numpy(), seq.cpu().numpy()
+    batch = idx_h.shape[0]
+    slots = (pt_h[np.arange(batch)[:, None], idx_h // w.page].astype(np.int64) * w.page + idx_h % w.page)
+    uniq, inv = np.unique(slots, return_inverse=True)
+    inv = inv.reshape(slots.shape)
+    import torch
+    sel = torch.from_numpy(uniq).cuda()
+    host = tuple(t.index_select(0, sel).cpu().numpy() for t in raw[:4]) + (raw[4].item(), raw[5].item())
+    # the compact pool's token table: position -> compact row
+    table = np.zeros((batch, w.ctx), np.int32)
+    table[np.arange(batch)[:, None], idx_h] = inv
+    qf = q.float().cpu().numpy()
+
+    def run(rows):
+        return attention.sparse_decode(qf[rows], host, table, 1, rows, idx_h[rows], None, seq_h[rows], scale,
+                                       dtype=np.float32)
+
+    with threadpool_limits(1):
+        t0 = time.perf_counter()
+        run(np.array([0]))
+        per_row = time.perf_counter() - t0
+        n = int(max(1, min(batch, seconds / max(per_row, 1e-6))))
+        rows = np.arange(n)
+        t0 = time.perf_counter()
+        run(rows)
+        dt = time.perf_counter() - t0
+    us_step = dt / n * batch * 1e6
+    sample_bytes = n * w.topk * w.kv_heads * 2 * (w.dim // 2 + w.dim // 16)
+    return {'value': round(sample_bytes / dt / 1e9, 4), 'unit': 'GB/s', 'cores': 1, 'kind': 'port',
+            'us_per_layer_step': round(us_step, 1),
+            'sample': f'{n} of {batch} requests of one layer-step (oracle: numpy gather + NVFP4 dequant + FP32 '
+                      f'softmax attention, one thread, {cpu_model()}, {os.cpu_count()} host cores)'}
+
+
+def main():
+    p = argparse.ArgumentParser()
+    p.add_argument('--gpus', type=int, default=1)
+    p.add_argument('--steps', type=int, default=512)
+    p.add_argument('--warmup', type=int, default=64)
+    p.add_argument('--workload', default='gqa_decode_b32')
+    p.add_argument('--layers', type=int, default=16)
+    p.add_argument('--splits', type=int, default=None)
+    p.add_argument('--cpu-seconds', type=float, default=10.0)
+    p.add_argument('--no-cpu-baseline', action='store_true')
+    args = p.parse_args()
+    if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
+        print(json.dumps({'error': 'this benchmark runs on one GPU only: the sparse decode shards by request or KV '
+                                   'head with no exchange, and no multi-GPU figure is produced'}))
+        sys.exit(2)
+
+    import torch
+
+    from xtier_amd import ops, workloads
+
+    w = workloads.WORKLOADS[args.workload]
+    torch.cuda.set_device(0)
+    gen = workloads.generator('cuda', 20261029)
+    t0 = time.time()
+    layers = [build_layer(w, gen, ops, workloads) for _ in range(args.layers)]
+    q = (torch.randn(w.batch, w.q_heads, w.dim, generator=gen, device='cuda') * w.q_std).to(torch.bfloat16)
+    pt = workloads.page_table(w.batch, w.ctx, w.page, gen, 'cuda')
+    idx = workloads.index_lists(w.batch, w.ctx, w.topk, gen, 'cuda', w.index_mode)
+    seq = torch.full((w.batch,), w.ctx, dtype=torch.int32, device='cuda')
+    torch.cuda.synchronize()
+    log(f'built {args.layers} layer pools ({w.slots} slots each) in {time.time() - t0:.1f} s')
+    scale = 1.0 / math.sqrt(w.dim)
+    splits = args.splits or ops.default_splits(w.batch, w.kv_heads, w.topk)
+    ws = torch.empty(ops.decode_workspace_bytes(w.batch, w.q_heads, w.dim, splits), dtype=torch.uint8,
+                     device='cuda')
+    out = torch.empty(w.batch, w.q_heads, w.dim, dtype=torch.bfloat16, device='cuda')
+
+    def step(layer):
+        ops.sparse_decode(q, layers[layer], pt, idx, seq, scale, page_size=w.page, out=out, splits=splits, ws=ws)
+
+    for i in range(args.warmup):
+        step(i % args.layers)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for layer in range(args.layers):
+            step(layer)
+    graph.replay()
+    torch.cuda.synchronize()
+    replays = max(1, math.ceil(args.steps / args.layers))
+    steps = replays * args.layers
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    nbytes = w.algorithmic_bytes()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    props = torch.cuda.get_device_properties(0)
+    log(f'{w.name}: {ms * 1e3:.2f} us per layer-step, {gbs:.0f} GB/s algorithmic ({gbs / HBM_PEAK_GBS:.1%} of '
+        f'{HBM_PEAK_GBS:.0f}), splits {splits}, {props.multi_processor_count} CUs')
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(layers[0], q, pt, idx, seq, w, scale, args.cpu_seconds)
+        log(f'cpu baseline: {cpu}')
+    record = {
+        'metric': METRIC, 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1, 'steps': steps,
+        'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'higher_is_better': True, 'scaling': 'weak',
+        'vs_baseline': None, 'dtype': 'f16', 'data': 'synthetic',
+        'config': {'workload': w.name, 'batch': w.batch, 'q_heads': w.q_heads, 'kv_heads': w.kv_heads,
+                   'head_dim': w.dim, 'context': w.ctx, 'topk': w.topk, 'page': w.page, 'kv_format': 'nvfp4',
+                   'layers_rotated': args.layers, 'splits': splits},
+        'us_per_layer_step': round(ms * 1e3, 3),
+        'tokens_per_s': round(w.batch / (ms * 1e-3), 1),
+        'hbm_frac': round(gbs / HBM_PEAK_GBS, 4),
+        'roofline': {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+                     'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None},
+        'cpu_baseline': cpu,
+    }
+    print(json.dumps(record), flush=True)
+
+
+if __name__ == '__main__':
+    main()

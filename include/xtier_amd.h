@@ -1,0 +1,118 @@
+/* C ABI of libxtier_amd.so: sparse attention over an NVFP4 paged KV pool on AMD Instinct MI355X (gfx950).
+ *
+ * Every entry point takes raw device pointers, element strides and sizes, runs on the caller's HIP stream, allocates
+ * nothing, never synchronizes and copies nothing between host and device, so a call can be captured in a HIP graph.
+ * Buffers are caller-owned; outputs are written in place. Return value: XT_OK or a negative status; the text of the
+ * last error of the calling thread is in xt_last_error().
+ *
+ * Pool layout (SGLang's NVFP4 KV pool as the reference reads it, xtier/packs/qwen4_exp/qsa_fp4.py:43-58, :94-101):
+ *   payload  uint8 [slots, kv_heads, dim / 2]   byte i of a head row = element 2i (bits 0-3), element 2i+1 (bits 4-7)
+ *   scales   uint8 [slots, kv_heads, dim / 16]  OCP E4M3, one per 16 elements
+ *   global   float [1] on the device            value = (e2m1 * e4m3) * global
+ * Slot lookup: page_size 1 -> table is token-granular (SGLang req_to_token, qsa_fp4.py:135);
+ *              page_size P > 1 -> table holds page ids, slot = table[pos / P] * P + pos % P.
+ */
+#ifndef XTIER_AMD_H
+#define XTIER_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define XT_OK 0
+#define XT_EINVAL (-1)       /* bad shape, stride, alignment or pointer: the reference raises ValueError */
+#define XT_EUNSUPPORTED (-2) /* shape the kernels do not cover: the reference raises NotImplementedError */
+#define XT_ELAUNCH (-3)      /* the HIP launch failed */
+#define XT_EWORKSPACE (-4)   /* workspace smaller than the *_workspace_bytes query returned */
+
+#define XT_DTYPE_BF16 0
+#define XT_DTYPE_F16 1
+
+typedef struct ihipStream_t* xt_stream_t; /* hipStream_t; 0 = the null stream */
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int xt_version(void);
+
+/* Text of the last error returned to the calling thread ("" if none). */
+const char* xt_last_error(void);
+
+/* --- NVFP4 quantization --------------------------------------------------------------------------------------- */
+
+/* Per-tensor global scale of the reference quantizer, on the device: g = max(amax(|src|) / (6 * 448), 1e-12) in FP32
+ * (xtier/backend/formats.py:122). src: BF16 [n_rows, heads, dim] with element strides src_row_stride and
+ * src_head_stride (last dim contiguous). workspace: at least 4 bytes of device memory (an atomic maximum).
+ * Replaces the global-scale half of nvfp4_encode (formats.py:114-128). */
+int xt_nvfp4_global_scale(const void* src, int64_t n_rows, int heads, int dim, int64_t src_row_stride,
+                          int64_t src_head_stride, float* g_out, void* workspace, xt_stream_t stream);
+
+/* NVFP4 quantize-on-append: row r of src (BF16 [n_rows, heads, dim], strided as above, 16-byte aligned rows) is
+ * quantized with the device global scale *g and written to pool slot slots[r] (payload [pool_slots, heads, dim/2],
+ * scales [pool_slots, heads, dim/16]); a negative slot skips the row. Per 16-element block (formats.py:123-128):
+ *   s = e4m3(blockamax / (6 * g)); q = x / max(s * g, 1e-30); code = nearest E2M1 magnitude of min(|q|, 6), a value
+ *   on a midpoint taking the smaller one; sign bit when q < 0 and code > 0.
+ * saturate = 0: a scale that rounds above 448 becomes E4M3 NaN, as the reference's torch cast (formats.py:124);
+ * saturate = 1: it becomes 448 (the satfinite conversion of xtier/arch.py:57-75), so a row that exceeds a fixed
+ * global scale never stores NaN. The reference's GPU write path is SGLang's quantizer behind the hook at
+ * xtier/packs/qwen4_exp/qsa_fp4.py:202-205 (fused store: xtier/packs/minimax_m3/kv_fp4.py:546-559). */
+int xt_nvfp4_quantize_append(const void* src, int64_t n_rows, int heads, int dim, int64_t src_row_stride,
+                             int64_t src_head_stride, const int64_t* slots, const float* g, uint8_t* pay,
+                             uint8_t* scales, int64_t pool_slots, int saturate, xt_stream_t stream);
+
+/* --- QSA gather and pack (bit-exact BF16/FP16 rows) -------------------------------------------------------------- */
+
+/* QSA decode/verify gather (xtier/packs/qwen4_exp/qsa_fp4.py:119-143, :174-180; hook extraction :223-228):
+ * for request b < batch and column c of indices[b] (int32, row stride idx_stride, topk columns):
+ *   pos = indices[b, c]; valid = c < cu_k[b+1] - cu_k[b] && 0 <= pos < seq_lens[b];
+ *   slot = req_to_token[req_indices[b] * req_stride + pos];
+ *   out[cu_k[b] + c, h, :] = dtype((e2m1 * e4m3) * g) for every head h (K with gk, V with gv).
+ * zero_fill_cols = 0: only valid columns are written; > 0: every column below zero_fill_cols is written, invalid
+ * ones as zeros. out_k / out_v: [rows, heads, dim] contiguous, out_dtype XT_DTYPE_BF16 or XT_DTYPE_F16. */
+int xt_qsa_gather_nvfp4(const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_scales, const uint8_t* v_scales,
+                        const float* gk, const float* gv, int64_t pool_slots, int heads, int dim,
+                        const int32_t* req_to_token, int64_t req_stride, const int64_t* req_indices,
+                        const int32_t* indices, int64_t idx_stride, const int32_t* seq_lens, const int32_t* cu_k,
+                        void* out_k, void* out_v, int out_dtype, int batch, int topk, int zero_fill_cols,
+                        xt_stream_t stream);
+
+/* QSA prefill prefix packing (qsa_fp4.py:146-162, :183-192; hook pack_qsa_prefill_kv :216-220): request b's
+ * positions t < cu_k[b+1] - cu_k[b] -> out[cu_k[b] + t] from slot req_to_token[req_indices[b] * sr0 + t * sr1]. */
+int xt_qsa_pack_nvfp4(const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_scales, const uint8_t* v_scales,
+                      const float* gk, const float* gv, int64_t pool_slots, int heads, int dim,
+                      const int32_t* req_to_token, int64_t sr0, int64_t sr1, const int64_t* req_indices, int batch,
+                      const int32_t* cu_k, int max_k, void* out_k, void* out_v, int out_dtype, xt_stream_t stream);
+
+/* --- fused sparse attention over the NVFP4 pool ------------------------------------------------------------------ */
+
+/* Device workspace the fused decode needs for `rows` query rows, q_heads heads of size dim and `splits` key splits
+ * (split-K partials: running max, sum and unnormalized output per row, split and head). 0 on a bad argument. */
+size_t xt_sparse_decode_workspace_bytes(int rows, int q_heads, int dim, int splits);
+
+/* Fused NVFP4 sparse GQA attention, one query per row (decode, verify, or a chunked prefill with one row per query
+ * token). Replaces the QSA decode pipeline gather -> varlen attention (qsa_fp4.py:231-268 with qsa_decode.py:89-113)
+ * and the MiniMax fused decode (xtier/packs/minimax_m3/kv_fp4.py:52-153, token-granular indices here).
+ * Row r (q: [rows, q_heads, dim] BF16, strides q_row_stride / q_head_stride elements) attends to the keys at the
+ * positions indices[r, c] (int32, row stride idx_stride, topk columns) that are valid:
+ *   c < counts[r] (counts NULL: all topk columns), 0 <= pos < seq_lens[r], and pos <= query_pos[r] when query_pos is
+ *   not NULL (causal prefill);
+ * resolved to pool slots through table row row_req[r] (row_req NULL: row r) with the page_size rule above.
+ * K/V are dequantized in registers; out[r, h] = sum_k softmax_k(q.k * scale) v_k in the dtype out_dtype, a row
+ * without valid keys writing 0. lse (optional, FP32 [rows, q_heads]): natural log-sum-exp of the scaled scores,
+ * -inf for an empty row. q_heads must be a multiple of kv_heads with q_heads / kv_heads <= 16; dim = 128.
+ * splits: key splits per row (1..64); workspace: xt_sparse_decode_workspace_bytes(rows, q_heads, dim, splits). */
+int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, const uint8_t* k_pay,
+                           const uint8_t* v_pay, const uint8_t* k_scales, const uint8_t* v_scales, const float* gk,
+                           const float* gv, int64_t pool_slots, int kv_heads, int q_heads, int dim,
+                           const int32_t* table, int64_t table_stride, int page_size, const int64_t* row_req,
+                           const int32_t* indices, int64_t idx_stride, int topk, const int32_t* counts,
+                           const int32_t* seq_lens, const int32_t* query_pos, float scale, void* out,
+                           int64_t out_row_stride, int64_t out_head_stride, int out_dtype, float* lse, int rows,
+                           int splits, void* workspace, size_t workspace_bytes, xt_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XTIER_AMD_H */

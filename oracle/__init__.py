@@ -1,0 +1,19 @@
+"""CPU oracle for the NVFP4-KV sparse-attention path: test infrastructure, not product code.
+
+A numpy restatement of the reference's algorithms (each function cites the reference file:line it follows). Only the
+test suite, ``__graft_entry__.smoke()`` and the CPU-baseline leg of ``bench.py`` may import this package, and only as
+the checker; the library under ``xtier_amd`` never calls into it.
+
+Pinning (what each function is checked against, in ``tests/``):
+- ``nvfp4.e2m1_*``: the 16-entry table the reference's tests hold (tests/draft_bf16_check.py:25,
+  tests/fp4_decode_check.py:15), exhaustively over all 256 bytes.
+- ``nvfp4.e4m3_decode``: torch's float8_e4m3fn values for all 256 bytes (the method of tests/fp8_decode_check.py).
+- ``nvfp4.e4m3_encode``: torch's float8_e4m3fn cast (reference semantics) and the satfinite variant on the grid of
+  tests/fp8_encode_check.py (every top-20-bit pattern and its halfway neighbours, plus the edge list).
+- ``nvfp4.nvfp4_encode`` / ``quantize_blocks``: brute-force nearest-value search with the ties-to-lower rule, the
+  one-block-scale round-trip bound of tests/draft_bf16_check.py:41-44, torch.bucketize on the same quotients, and
+  special cases (zero blocks, exact midpoints, negative values rounding to zero).
+- ``attention.*``: float64 softmax computed directly (no online/split form), single-key and empty-row special
+  cases, split-K merge against one pass.
+- ``attention.sparse_mla``: float64 reference with sink and LSE, as tests/ds_sparse_mla_check.py:44-67.
+"""

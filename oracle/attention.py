@@ -1,0 +1,223 @@
+"""Sparse attention over an NVFP4 paged KV pool, on the CPU (numpy): the oracle for the gather, the fused decode,
+the split-K merge, the chunked prefill and sparse MLA.
+
+Test infrastructure only. Conventions (reference: qsa_fp4.py:131-140; sparse_mla.py:42-46; qsa_decode.py:75, :83):
+an index is valid when it is >= 0 and below the row's length (and, for a causal query, not after the query's own
+position); invalid entries are masked before any load; a row without a valid key writes 0 (LSE -inf).
+"""
+import numpy as np
+
+from . import nvfp4
+
+LOG2E = 1.4426950408889634
+
+
+# --- slot lookup ---------------------------------------------------------------------------------------------------
+
+def slots_of(table, table_row, positions, page_size):
+    """Pool slots of token positions of one request. page_size 1: ``table`` is token-granular (req_to_token,
+    qsa_fp4.py:135); page_size P > 1: ``table`` holds page ids and slot = table[pos // P] * P + pos % P."""
+    positions = np.asarray(positions, dtype=np.int64)
+    row = np.asarray(table)[table_row]
+    if page_size == 1:
+        return row[positions].astype(np.int64)
+    return row[positions // page_size].astype(np.int64) * page_size + positions % page_size
+
+
+# --- QSA gather / pack (bit-exact BF16 rows) --------------------------------------------------------------------------
+
+def gather_qsa(raw, req_to_token, req_indices, indices, seq_lens, cu_k, out_k, out_v, batch, topk, zero_fill_cols=0):
+    """qsa_fp4.py:119-143 and :174-180 in numpy. raw = (k_pay u8 [m, H, D/2], v_pay, k_sf u8 [m, H, D/16], v_sf,
+    gk, gv); out_k/out_v are uint16 arrays of BF16 bits [rows, H, D], written in place where the reference stores.
+    Rows are (e2m1 * e4m3) * g in FP32 rounded to BF16; zero-fill mode writes zeros for the invalid columns below
+    zero_fill_cols."""
+    k_pay, v_pay, k_sf, v_sf, gk, gv = raw
+    heads = k_pay.shape[1]
+    num_cols = zero_fill_cols if zero_fill_cols > 0 else topk
+    span = -(-num_cols // 16) * 16
+    indices = np.asarray(indices)
+    for b in range(batch):
+        length = int(seq_lens[b])
+        req = int(req_indices[b])
+        start = int(cu_k[b])
+        valid_count = int(cu_k[b + 1]) - start
+        cols = np.arange(span)
+        pos = np.where(cols < topk, indices[b, np.minimum(cols, topk - 1)], -1).astype(np.int64)
+        valid = (cols < valid_count) & (pos >= 0) & (pos < length)
+        store = (cols < zero_fill_cols) if zero_fill_cols > 0 else valid
+        slots = np.where(valid, np.asarray(req_to_token)[req, np.where(valid, pos, 0)], 0).astype(np.int64)
+        for pay, sf, g, out in ((k_pay, k_sf, gk, out_k), (v_pay, v_sf, gv, out_v)):
+            p = np.where(valid[:, None, None], pay[slots], 0).astype(np.uint8)
+            s = np.where(valid[:, None, None], sf[slots], 0).astype(np.uint8)
+            rows = nvfp4.bf16_bits(nvfp4.dequant(p, s, g))
+            dst = start + cols[store]
+            out[dst] = rows[store]
+    return out_k, out_v
+
+
+def pack_qsa(raw, req_to_token, req_indices, cu_k, total_k, heads_dim=None):
+    """qsa_fp4.py:146-162 and :183-192: request b's first cu_k[b+1]-cu_k[b] positions, in order, as BF16 bits rows
+    [total_k, H, D] (rows not covered stay 0 here; the reference leaves them unwritten)."""
+    k_pay, v_pay, k_sf, v_sf, gk, gv = raw
+    heads, half = k_pay.shape[1], k_pay.shape[2]
+    out_k = np.zeros((total_k, heads, half * 2), dtype=np.uint16)
+    out_v = np.zeros_like(out_k)
+    for b in range(len(req_indices)):
+        start, end = int(cu_k[b]), int(cu_k[b + 1])
+        slots = np.asarray(req_to_token)[int(req_indices[b]), :end - start].astype(np.int64)
+        out_k[start:end] = nvfp4.bf16_bits(nvfp4.dequant(k_pay[slots], k_sf[slots], gk))
+        out_v[start:end] = nvfp4.bf16_bits(nvfp4.dequant(v_pay[slots], v_sf[slots], gv))
+    return out_k, out_v
+
+
+# --- attention references -----------------------------------------------------------------------------------------
+
+def softmax_attention(q, k, v, valid, scale, dtype=np.float64):
+    """One query row: q [Hq, D]; k, v [N, Hkv, Dk|Dv]; valid [N] bool. Softmax over the valid keys in ``dtype``
+    (the FP64 reference of tests/qsa_decode_check.py:14-26 in closed form); a row without valid keys gives 0."""
+    hq = q.shape[0]
+    hkv = k.shape[1]
+    group = hq // hkv
+    out = np.zeros((hq, v.shape[-1]), dtype=dtype)
+    idx = np.nonzero(np.asarray(valid))[0]
+    if idx.size == 0:
+        return out
+    kd = np.asarray(k, dtype=dtype)[idx]
+    vd = np.asarray(v, dtype=dtype)[idx]
+    qd = np.asarray(q, dtype=dtype)
+    for h in range(hq):
+        s = kd[:, h // group] @ qd[h] * dtype(scale)
+        p = np.exp(s - s.max())
+        out[h] = (p @ vd[:, h // group]) / p.sum()
+    return out
+
+
+def flash_precision_attention(q, k, v, valid, scale):
+    """The flash kernels' precision (tests/qsa_decode_check.py:29-45): FP32 scores, P rounded to BF16 for the PV
+    product, FP32 sums, the output rounded to BF16; returned as float64."""
+    hq = q.shape[0]
+    group = hq // k.shape[1]
+    out = np.zeros((hq, v.shape[-1]), dtype=np.float64)
+    idx = np.nonzero(np.asarray(valid))[0]
+    if idx.size == 0:
+        return out
+    kf = np.asarray(k, np.float32)[idx]
+    vf = np.asarray(v, np.float32)[idx]
+    qf = np.asarray(q, np.float32)
+    for h in range(hq):
+        s = (kf[:, h // group] @ qf[h]) * np.float32(scale)
+        p = np.exp(s - s.max()).astype(np.float32)
+        o = (nvfp4.f32_to_bf16_f32(p) @ vf[:, h // group]) / p.sum(dtype=np.float32)
+        out[h] = nvfp4.f32_to_bf16_f32(o.astype(np.float32))
+    return out
+
+
+def key_validity(indices, count, length, query_pos=None):
+    """valid[c] for one row's index list: c < count, 0 <= idx < length, and idx <= query_pos when causal."""
+    indices = np.asarray(indices, dtype=np.int64)
+    cols = np.arange(indices.shape[0])
+    valid = (cols < count) & (indices >= 0) & (indices < length)
+    if query_pos is not None:
+        valid &= indices <= query_pos
+    return valid
+
+
+def gather_dequant(pay, sf, g, slots, valid):
+    """FP32 (e2m1 * e4m3) * g rows of ``slots`` (invalid ones 0)."""
+    slots = np.where(valid, slots, 0)
+    rows = nvfp4.dequant(pay[slots], sf[slots], g)
+    rows[~valid] = 0.0
+    return rows
+
+
+def sparse_decode(q, pool, table, page_size, rows, indices, counts, seq_lens, scale, query_pos=None,
+                  dtype=np.float64):
+    """Fused NVFP4 sparse GQA decode/prefill, reference values: for query row r (q [R, Hq, D]) of request rows[r],
+    keys = the valid entries of indices[r] (token positions) resolved through the page table, K and V dequantized
+    to FP32 (e2m1 * e4m3) * g, softmax(q.k * scale) v computed in ``dtype``. pool = (k_pay, v_pay, k_sf, v_sf, gk,
+    gv) in the [slots, Hkv, D/2] / [slots, Hkv, D/16] layout. Returns float [R, Hq, D]."""
+    k_pay, v_pay, k_sf, v_sf, gk, gv = pool
+    q = np.asarray(q)
+    out = np.zeros(q.shape, dtype=dtype)
+    for r in range(q.shape[0]):
+        idx = np.asarray(indices[r], dtype=np.int64)
+        qp = None if query_pos is None else int(query_pos[r])
+        valid = key_validity(idx, int(counts[r]) if counts is not None else idx.shape[0], int(seq_lens[r]), qp)
+        slots = np.zeros(idx.shape[0], dtype=np.int64)
+        if valid.any():
+            slots[valid] = slots_of(table, int(rows[r]), idx[valid], page_size)
+        k = gather_dequant(k_pay, k_sf, gk, slots, valid)
+        v = gather_dequant(v_pay, v_sf, gv, slots, valid)
+        out[r] = softmax_attention(q[r], k, v, valid, scale, dtype)
+    return out
+
+
+def split_partials(q, k, v, valid, scale, keys_per_split):
+    """Split-K partials of one row in the form of qsa_decode.py:25-60: per split the running max m (log2 domain),
+    the sum l and the unnormalized accumulator acc (FP64 here). Returns m [S, Hq], l [S, Hq], acc [S, Hq, Dv]."""
+    n = k.shape[0]
+    splits = max(1, -(-n // keys_per_split))
+    hq = q.shape[0]
+    group = hq // k.shape[1]
+    m = np.full((splits, hq), -np.inf)
+    l = np.zeros((splits, hq))
+    acc = np.zeros((splits, hq, v.shape[-1]))
+    for s in range(splits):
+        sel = np.arange(s * keys_per_split, min(n, (s + 1) * keys_per_split))
+        sel = sel[np.asarray(valid)[sel]]
+        if sel.size == 0:
+            continue
+        for h in range(hq):
+            sc = (np.asarray(k[sel, h // group], np.float64) @ np.asarray(q[h], np.float64)) * scale * LOG2E
+            m[s, h] = sc.max()
+            p = np.exp2(sc - m[s, h])
+            l[s, h] = p.sum()
+            acc[s, h] = p @ np.asarray(v[sel, h // group], np.float64)
+    return m, l, acc
+
+
+def merge_partials(m, l, acc):
+    """qsa_decode.py:63-86: weights 2^(m - max m) (a row without keys: every weight 0), out = sum(w acc) / sum(w l),
+    0 where the total is 0."""
+    top = m.max(0)
+    top = np.where(np.isneginf(top), 0.0, top)
+    w = np.exp2(m - top[None])
+    total = (w * l).sum(0)
+    out = (w[..., None] * acc).sum(0)
+    with np.errstate(invalid='ignore', divide='ignore'):
+        return np.where(total[:, None] > 0, out / total[:, None], 0.0)
+
+
+# --- sparse MLA ---------------------------------------------------------------------------------------------------
+
+def sparse_mla(q, latent_pay, latent_sf, rope, g, indices, topk_length, sink, scale, dtype=np.float64):
+    """Sparse MLA over an NVFP4 latent + BF16 rope cache, reference values (the FP64 reference of
+    tests/ds_sparse_mla_check.py:44-67 on this layout): q [R, H, Dl + Dr]; per token the key is
+    [(e2m1 * e4m3) * g latent (Dl), rope (Dr)] and the value is the latent; indices [R, K] are pool slots (-1 none),
+    topk_length [R] or None; sink [H] or None enters the denominator as exp(sink - m). Returns (out [R, H, Dl],
+    lse [R, H] natural log of the keys' sum, -inf for a row without keys)."""
+    q = np.asarray(q, dtype=dtype)
+    rows_n, heads, _ = q.shape
+    dl = latent_pay.shape[-1] * 2
+    out = np.zeros((rows_n, heads, dl), dtype=dtype)
+    lse = np.full((rows_n, heads), -np.inf, dtype=dtype)
+    for r in range(rows_n):
+        idx = np.asarray(indices[r], dtype=np.int64)
+        cols = np.arange(idx.shape[0])
+        valid = idx >= 0
+        if topk_length is not None:
+            valid &= cols < int(topk_length[r])
+        sel = idx[valid]
+        if sel.size == 0:
+            continue
+        lat = nvfp4.dequant(latent_pay[sel], latent_sf[sel], g).astype(dtype)
+        key = np.concatenate([lat, np.asarray(rope[sel], dtype=dtype)], -1)
+        s = (key @ q[r].T) * dtype(scale)        # [n, H]
+        m = s.max(0)
+        p = np.exp(s - m[None])
+        total = p.sum(0)
+        lse[r] = m + np.log(total)
+        if sink is not None:
+            total = total + np.exp(np.asarray(sink, dtype=dtype) - m)
+        out[r] = (p.T @ lat) / total[:, None]
+    return out, lse

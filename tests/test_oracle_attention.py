@@ -1,0 +1,161 @@
+"""The CPU oracle's attention, gather and merge pinned against torch float64 softmax (a separate implementation),
+closed-form special cases and the invariants the reference's tests check."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention, nvfp4
+
+
+def _torch_ref(q, k, v, valid, scale):
+    """tests/qsa_decode_check.py:14-26 form: per head softmax(k q * scale) @ v in float64, 0 without keys."""
+    hq, group = q.shape[0], q.shape[0] // k.shape[1]
+    out = torch.zeros(hq, v.shape[-1], dtype=torch.float64)
+    sel = torch.from_numpy(np.nonzero(valid)[0])
+    if sel.numel() == 0:
+        return out.numpy()
+    qd, kd, vd = (torch.from_numpy(np.asarray(t, np.float64)) for t in (q, k, v))
+    for h in range(hq):
+        s = (kd[sel, h // group] @ qd[h]) * scale
+        out[h] = torch.softmax(s, 0) @ vd[sel, h // group]
+    return out.numpy()
+
+
+@pytest.mark.parametrize('n,hq,hkv', [(1, 8, 1), (37, 8, 2), (300, 32, 4)])
+def test_softmax_matches_torch(n, hq, hkv):
+    rng = np.random.default_rng(n)
+    q = rng.standard_normal((hq, 64))
+    k = rng.standard_normal((n, hkv, 64))
+    v = rng.standard_normal((n, hkv, 64))
+    valid = rng.random(n) < 0.8
+    valid[0] = True
+    got = attention.softmax_attention(q, k, v, valid, 0.125)
+    assert np.allclose(got, _torch_ref(q, k, v, valid, 0.125), rtol=0, atol=1e-12)
+
+
+def test_special_cases():
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal((4, 32))
+    k = rng.standard_normal((5, 1, 32))
+    v = rng.standard_normal((5, 1, 32))
+    one = np.zeros(5, bool)
+    one[3] = True
+    assert np.array_equal(attention.softmax_attention(q, k, v, one, 0.3), np.repeat(v[3], 4, 0))   # P = 1
+    assert not attention.softmax_attention(q, k, v, np.zeros(5, bool), 0.3).any()                   # empty row
+
+
+@pytest.mark.parametrize('keys_per_split', [1, 7, 128, 1000])
+def test_split_merge_equals_one_pass(keys_per_split):
+    rng = np.random.default_rng(keys_per_split)
+    q = rng.standard_normal((8, 128)) * 2
+    k = rng.standard_normal((513, 1, 128))
+    v = rng.standard_normal((513, 1, 128))
+    valid = rng.random(513) < 0.7
+    m, l, acc = attention.split_partials(q, k, v, valid, 0.09, keys_per_split)
+    got = attention.merge_partials(m, l, acc)
+    assert np.allclose(got, attention.softmax_attention(q, k, v, valid, 0.09), rtol=0, atol=1e-12)
+    m0, l0, a0 = attention.split_partials(q, k, v, np.zeros(513, bool), 0.09, keys_per_split)
+    assert not attention.merge_partials(m0, l0, a0).any()
+
+
+def _pool(rng, slots, heads, dim):
+    x = nvfp4.f32_to_bf16_f32(rng.standard_normal((slots, heads, dim)).astype(np.float32))
+    pay, sc, g = nvfp4.nvfp4_encode(x)
+    return pay, sc, g
+
+
+def test_gather_equals_dequantize_then_gather():
+    """The reference test's property (tests/qsa_fp4_check.py:52-66): the gather from the packed pool equals the
+    pool dequantized to BF16 and then gathered; zero-fill writes zeros for invalid columns."""
+    rng = np.random.default_rng(5)
+    heads, dim, slots = 2, 64, 500
+    kp, ks, gk = _pool(rng, slots, heads, dim)
+    vp, vs, gv = _pool(rng, slots, heads, dim)
+    raw = (kp, vp, ks, vs, gk, gv)
+    kref = nvfp4.bf16_bits(nvfp4.dequant(kp, ks, gk))
+    batch, topk, width = 3, 40, 300
+    r2t = rng.integers(0, slots, (4, width)).astype(np.int32)
+    req = np.array([2, 0, 3])
+    seq = np.array([250, 30, 290], np.int32)
+    idx = np.full((batch, topk), -1, np.int32)
+    counts = [40, 17, 33]
+    for b, n in enumerate(counts):
+        idx[b, :n] = rng.permutation(int(seq[b]))[:n]
+    idx[1, 5] = 299   # beyond the request's length: invalid
+    cu = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    canary = np.uint16(0x7FC1)
+    out_k = np.full((cu[-1], heads, dim), canary, np.uint16)
+    out_v = out_k.copy()
+    attention.gather_qsa(raw, r2t, req, idx, seq, cu, out_k, out_v, batch, topk)
+    for b in range(batch):
+        for c in range(counts[b]):
+            pos = idx[b, c]
+            if 0 <= pos < seq[b]:
+                assert np.array_equal(out_k[cu[b] + c], kref[r2t[req[b], pos]])
+            else:
+                assert np.all(out_k[cu[b] + c] == canary)
+    zf = 48
+    cu2 = (np.arange(batch + 1) * zf).astype(np.int32)
+    zk = np.full((batch * zf, heads, dim), canary, np.uint16)
+    zv = zk.copy()
+    attention.gather_qsa(raw, r2t, req, idx, seq, cu2, zk, zv, batch, topk, zero_fill_cols=zf)
+    assert not np.any(zk == canary)
+    assert np.all(zk[1 * zf + 5] == 0) and np.all(zk[0 * zf + 45] == 0)
+
+
+def test_decode_page_table_equals_token_table():
+    rng = np.random.default_rng(9)
+    heads, dim, page, ctx, batch = 2, 128, 64, 512, 3
+    slots = batch * ctx
+    kp, ks, gk = _pool(rng, slots, heads, dim)
+    vp, vs, gv = _pool(rng, slots, heads, dim)
+    pool = (kp, vp, ks, vs, gk, gv)
+    pt = rng.permutation(slots // page).reshape(batch, ctx // page).astype(np.int32)
+    tt = (pt[:, :, None] * page + np.arange(page)[None, None]).reshape(batch, ctx)
+    idx = np.stack([np.sort(rng.permutation(ctx)[:100]) for _ in range(batch)]).astype(np.int32)
+    q = rng.standard_normal((batch, 8, dim)).astype(np.float32)
+    seq = np.full(batch, ctx)
+    rows = np.arange(batch)
+    a = attention.sparse_decode(q, pool, pt, page, rows, idx, None, seq, 0.088)
+    b = attention.sparse_decode(q, pool, tt, 1, rows, idx, None, seq, 0.088)
+    assert np.array_equal(a, b)
+
+
+def _mla_torch(q, keys, vals, idx, length, sink, scale):
+    """tests/ds_sparse_mla_check.py:44-67 form in torch float64 (masked_fill, sink in the denominator)."""
+    qd = torch.from_numpy(q)
+    kd = torch.from_numpy(keys)
+    vd = torch.from_numpy(vals)
+    ix = torch.from_numpy(idx).long()
+    pos = torch.arange(ix.shape[1])
+    valid = (ix >= 0) & (pos[None] < torch.from_numpy(length)[:, None])
+    k = kd[ix.clamp_min(0)]
+    v = vd[ix.clamp_min(0)]
+    s = torch.einsum('rhd,rnd->rhn', qd, k) * scale
+    s = s.masked_fill(~valid[:, None, :], float('-inf'))
+    m = s.amax(-1, keepdim=True)
+    m = torch.where(torch.isfinite(m), m, torch.zeros_like(m))
+    p = torch.exp(s - m)
+    total = p.sum(-1, keepdim=True) + torch.exp(torch.from_numpy(sink)[None, :, None] - m)
+    o = torch.einsum('rhn,rnd->rhd', p, v) / total
+    return torch.where(valid.any(1)[:, None, None], o, torch.zeros_like(o)).numpy()
+
+
+def test_sparse_mla_matches_torch_with_sink():
+    rng = np.random.default_rng(11)
+    tokens, heads, dl, dr = 300, 16, 128, 32
+    lat = nvfp4.f32_to_bf16_f32(rng.standard_normal((tokens, dl)).astype(np.float32))
+    pay, sc, g = nvfp4.nvfp4_encode(lat)
+    rope = nvfp4.f32_to_bf16_f32(rng.standard_normal((tokens, dr)).astype(np.float32))
+    deq = nvfp4.dequant(pay, sc, g).astype(np.float64)
+    keys = np.concatenate([deq, rope.astype(np.float64)], -1)
+    rows, topk = 5, 64
+    idx = rng.integers(0, tokens, (rows, topk)).astype(np.int32)
+    idx[rng.random(idx.shape) < 0.1] = -1
+    length = np.array([64, 10, 0, 1, 50], np.int32)
+    sink = rng.standard_normal(heads)
+    q = rng.standard_normal((rows, heads, dl + dr)) * 0.5
+    out, lse = attention.sparse_mla(q, pay, sc, rope, g, idx, length, sink, 0.07)
+    want = _mla_torch(q, keys, deq, idx, length, sink, 0.07)
+    assert np.allclose(out, want, rtol=0, atol=1e-12)
+    assert np.all(np.isneginf(lse[2])) and not out[2].any()

@@ -1,0 +1,78 @@
+"""ctypes binding of libxtier_amd.so (the C ABI declared in include/xtier_amd.h).
+
+The library is built in-tree by ``python -m xtier_amd.build``; loading fails loudly when it is missing, and nothing in
+this package falls back to another implementation.
+"""
+import ctypes
+import re
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / 'libxtier_amd.so'
+HEADER = Path(__file__).resolve().parent.parent / 'include' / 'xtier_amd.h'
+
+XT_OK, XT_EINVAL, XT_EUNSUPPORTED, XT_ELAUNCH, XT_EWORKSPACE = 0, -1, -2, -3, -4
+XT_DTYPE_BF16, XT_DTYPE_F16 = 0, 1
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+_Z = ctypes.c_size_t
+
+SIGNATURES = {
+    'xt_version': (_I, []),
+    'xt_last_error': (ctypes.c_char_p, []),
+    'xt_nvfp4_global_scale': (_I, [_P, _L, _I, _I, _L, _L, _P, _P, _P]),
+    'xt_nvfp4_quantize_append': (_I, [_P, _L, _I, _I, _L, _L, _P, _P, _P, _P, _L, _I, _P]),
+    'xt_qsa_gather_nvfp4': (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _P, _L, _P, _P, _L, _P, _P, _P, _P, _I, _I, _I,
+                                 _I, _P]),
+    'xt_qsa_pack_nvfp4': (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _P, _L, _L, _P, _I, _P, _I, _P, _P, _I, _P]),
+    'xt_sparse_decode_workspace_bytes': (_Z, [_I, _I, _I, _I]),
+    'xt_sparse_decode_nvfp4': (_I, [_P, _L, _L, _P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _P, _L, _I, _P, _P, _L, _I,
+                                    _P, _P, _P, _F, _P, _L, _L, _I, _P, _I, _I, _P, _Z, _P]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class XTierError(RuntimeError):
+    """A launch or runtime failure reported by the library."""
+
+
+def declared_symbols():
+    """Names of the functions include/xtier_amd.h declares."""
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r'^\s*(?:const\s+)?[\w\s\*]*?\b(xt_\w+)\s*\(', text, re.M)))
+
+
+def lib():
+    """The loaded library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not LIB_PATH.exists():
+                    raise ImportError(f'{LIB_PATH} is missing: build it with `python -m xtier_amd.build` '
+                                      '(no other implementation is used)')
+                handle = ctypes.CDLL(str(LIB_PATH))
+                for name, (res, args) in SIGNATURES.items():
+                    fn = getattr(handle, name)
+                    fn.restype = res
+                    fn.argtypes = args
+                _lib = handle
+    return _lib
+
+
+def check(status, what):
+    """Raises the reference's exception type for a negative status (ValueError for bad layouts,
+    NotImplementedError for unsupported shapes, XTierError otherwise)."""
+    if status == XT_OK:
+        return
+    msg = lib().xt_last_error().decode(errors='replace') or f'{what} failed with status {status}'
+    if status == XT_EINVAL or status == XT_EWORKSPACE:
+        raise ValueError(msg)
+    if status == XT_EUNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise XTierError(msg)

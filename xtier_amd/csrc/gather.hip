@@ -1,0 +1,177 @@
+// QSA decode gather and prefill packing over the NVFP4 pool: bit-exact dequantized rows.
+//
+// Each value is (e2m1 * e4m3) * g computed as two FP32 multiplies in this order and rounded to nearest even into the
+// output dtype, as xtier/packs/qwen4_exp/qsa_fp4.py:94-101 and :142-143 compute it. One thread per 16-element block:
+// 8 payload bytes and one scale byte in, 32 bytes out.
+#include "xt_common.h"
+#include "xt_host.h"
+
+namespace xt {
+namespace {
+
+// 16 output values of one block; `valid` false gives +0.0 everywhere (masked loads read 0 bytes).
+__device__ inline void dequant_block(const uint8_t* __restrict__ pay, const uint8_t* __restrict__ sf, float g,
+                                     bool valid, int out_dtype, void* __restrict__ dst) {
+  uint2 w = make_uint2(0u, 0u);
+  uint32_t sbyte = 0u;
+  if (valid) {
+    w = *reinterpret_cast<const uint2*>(pay);
+    sbyte = *sf;
+  }
+  const float s = e4m3_decode(sbyte);
+  float v[16];
+  const uint32_t ws[2] = {w.x, w.y};
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    float2_t p0 = fp4x2_to_f32<0>(ws[k]);
+    float2_t p1 = fp4x2_to_f32<1>(ws[k]);
+    float2_t p2 = fp4x2_to_f32<2>(ws[k]);
+    float2_t p3 = fp4x2_to_f32<3>(ws[k]);
+    v[8 * k + 0] = p0.x; v[8 * k + 1] = p0.y; v[8 * k + 2] = p1.x; v[8 * k + 3] = p1.y;
+    v[8 * k + 4] = p2.x; v[8 * k + 5] = p2.y; v[8 * k + 6] = p3.x; v[8 * k + 7] = p3.y;
+  }
+  uint32_t o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float a = (v[2 * e] * s) * g;
+    const float b = (v[2 * e + 1] * s) * g;
+    if (out_dtype == XT_DTYPE_BF16)
+      o[e] = f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
+    else
+      o[e] = f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
+  }
+  uint4* d = reinterpret_cast<uint4*>(dst);
+  d[0] = make_uint4(o[0], o[1], o[2], o[3]);
+  d[1] = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
+__global__ void qsa_gather_kernel(const uint8_t* __restrict__ k_pay, const uint8_t* __restrict__ v_pay,
+                                  const uint8_t* __restrict__ k_sf, const uint8_t* __restrict__ v_sf,
+                                  const float* __restrict__ gk, const float* __restrict__ gv, int64_t pool_slots,
+                                  int heads, int dim, const int32_t* __restrict__ req_to_token, int64_t req_stride,
+                                  const int64_t* __restrict__ req_indices, const int32_t* __restrict__ indices,
+                                  int64_t idx_stride, const int32_t* __restrict__ seq_lens,
+                                  const int32_t* __restrict__ cu_k, uint16_t* __restrict__ out_k,
+                                  uint16_t* __restrict__ out_v, int out_dtype, int batch, int topk, int num_cols,
+                                  int zero_fill) {
+  const int blocks = dim / 16;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)batch * num_cols * heads * blocks;
+  if (i >= total) return;
+  const int blk = (int)(i % blocks);
+  const int h = (int)((i / blocks) % heads);
+  const int64_t bc = i / ((int64_t)blocks * heads);
+  const int c = (int)(bc % num_cols);
+  const int b = (int)(bc / num_cols);
+  const int32_t start = cu_k[b];
+  const int32_t valid_count = cu_k[b + 1] - start;
+  const int32_t length = seq_lens[b];
+  const int32_t pos = (c < topk) ? indices[(int64_t)b * idx_stride + c] : -1;
+  bool valid = (c < valid_count) && (pos >= 0) && (pos < length);
+  int64_t slot = 0;
+  if (valid) {
+    slot = req_to_token[req_indices[b] * req_stride + pos];
+    valid = slot >= 0 && slot < pool_slots;   // a slot outside the pool reads as an invalid column
+  }
+  if (!valid && !zero_fill) return;
+  const int64_t row_bytes = (int64_t)heads * (dim / 2), row_scales = (int64_t)heads * (dim / 16);
+  const int64_t dst = ((int64_t)(start + c) * heads + h) * dim + blk * 16;
+  const int64_t po = slot * row_bytes + (int64_t)h * (dim / 2) + blk * 8;
+  const int64_t so = slot * row_scales + (int64_t)h * (dim / 16) + blk;
+  dequant_block(k_pay + po, k_sf + so, *gk, valid, out_dtype, out_k + dst);
+  dequant_block(v_pay + po, v_sf + so, *gv, valid, out_dtype, out_v + dst);
+}
+
+__global__ void qsa_pack_kernel(const uint8_t* __restrict__ k_pay, const uint8_t* __restrict__ v_pay,
+                                const uint8_t* __restrict__ k_sf, const uint8_t* __restrict__ v_sf,
+                                const float* __restrict__ gk, const float* __restrict__ gv, int64_t pool_slots,
+                                int heads, int dim, const int32_t* __restrict__ req_to_token, int64_t sr0, int64_t sr1,
+                                const int64_t* __restrict__ req_indices, int batch, const int32_t* __restrict__ cu_k,
+                                int max_k, uint16_t* __restrict__ out_k, uint16_t* __restrict__ out_v,
+                                int out_dtype) {
+  const int blocks = dim / 16;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)batch * max_k * heads * blocks;
+  if (i >= total) return;
+  const int blk = (int)(i % blocks);
+  const int h = (int)((i / blocks) % heads);
+  const int64_t bt = i / ((int64_t)blocks * heads);
+  const int t = (int)(bt % max_k);
+  const int b = (int)(bt / max_k);
+  const int32_t start = cu_k[b];
+  if (t >= cu_k[b + 1] - start) return;
+  int64_t slot = req_to_token[req_indices[b] * sr0 + (int64_t)t * sr1];
+  const bool valid = slot >= 0 && slot < pool_slots;
+  if (!valid) slot = 0;
+  const int64_t row_bytes = (int64_t)heads * (dim / 2), row_scales = (int64_t)heads * (dim / 16);
+  const int64_t dst = ((int64_t)(start + t) * heads + h) * dim + blk * 16;
+  const int64_t po = slot * row_bytes + (int64_t)h * (dim / 2) + blk * 8;
+  const int64_t so = slot * row_scales + (int64_t)h * (dim / 16) + blk;
+  dequant_block(k_pay + po, k_sf + so, *gk, valid, out_dtype, out_k + dst);
+  dequant_block(v_pay + po, v_sf + so, *gv, valid, out_dtype, out_v + dst);
+}
+
+int check_pool(const char* what, const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_sf,
+               const uint8_t* v_sf, const float* gk, const float* gv, int64_t pool_slots, int heads, int dim) {
+  // the reference's precondition (qsa_fp4.py:165-171): a power-of-2 head size, a multiple of 32
+  if (heads <= 0 || dim < 32 || (dim & (dim - 1)) != 0)
+    return fail(XT_EINVAL, "%s: packed [m, heads, dim/2] rows with a power-of-2 head size >= 32 expected, got "
+                "heads=%d dim=%d", what, heads, dim);
+  if (!k_pay || !v_pay || !k_sf || !v_sf || !gk || !gv || pool_slots <= 0)
+    return fail(XT_EINVAL, "%s: pool buffers and global scales are required (pool_slots %lld)", what,
+                (long long)pool_slots);
+  if (!aligned(k_pay, 8) || !aligned(v_pay, 8)) return fail(XT_EINVAL, "%s: payload must be 8-byte aligned", what);
+  return XT_OK;
+}
+
+}  // namespace
+}  // namespace xt
+
+using namespace xt;
+
+extern "C" int xt_qsa_gather_nvfp4(const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_scales,
+                                   const uint8_t* v_scales, const float* gk, const float* gv, int64_t pool_slots,
+                                   int heads, int dim, const int32_t* req_to_token, int64_t req_stride,
+                                   const int64_t* req_indices, const int32_t* indices, int64_t idx_stride,
+                                   const int32_t* seq_lens, const int32_t* cu_k, void* out_k, void* out_v,
+                                   int out_dtype, int batch, int topk, int zero_fill_cols, xt_stream_t stream) {
+  const char* what = "xt_qsa_gather_nvfp4";
+  if (int e = check_pool(what, k_pay, v_pay, k_scales, v_scales, gk, gv, pool_slots, heads, dim)) return e;
+  if (out_dtype != XT_DTYPE_BF16 && out_dtype != XT_DTYPE_F16)
+    return fail(XT_EINVAL, "%s: output dtype must be BF16 or FP16", what);
+  if (batch < 0 || topk < 0 || zero_fill_cols < 0) return fail(XT_EINVAL, "%s: negative batch/topk/zero_fill", what);
+  const int num_cols = zero_fill_cols > 0 ? zero_fill_cols : topk;
+  if (batch == 0 || num_cols == 0) return ok();
+  if (!req_to_token || !req_indices || !indices || !seq_lens || !cu_k || !out_k || !out_v)
+    return fail(XT_EINVAL, "%s: a required pointer is null", what);
+  if (!aligned(out_k, 16) || !aligned(out_v, 16)) return fail(XT_EINVAL, "%s: outputs must be 16-byte aligned", what);
+  const int64_t total = (int64_t)batch * num_cols * heads * (dim / 16);
+  hipLaunchKernelGGL(qsa_gather_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), k_pay, v_pay, k_scales, v_scales, gk, gv, pool_slots,
+                     heads, dim, req_to_token, req_stride, req_indices, indices, idx_stride, seq_lens, cu_k,
+                     static_cast<uint16_t*>(out_k), static_cast<uint16_t*>(out_v), out_dtype, batch, topk, num_cols,
+                     zero_fill_cols > 0 ? 1 : 0);
+  return check_launch(what);
+}
+
+extern "C" int xt_qsa_pack_nvfp4(const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_scales,
+                                 const uint8_t* v_scales, const float* gk, const float* gv, int64_t pool_slots,
+                                 int heads, int dim, const int32_t* req_to_token, int64_t sr0, int64_t sr1,
+                                 const int64_t* req_indices, int batch, const int32_t* cu_k, int max_k, void* out_k,
+                                 void* out_v, int out_dtype, xt_stream_t stream) {
+  const char* what = "xt_qsa_pack_nvfp4";
+  if (int e = check_pool(what, k_pay, v_pay, k_scales, v_scales, gk, gv, pool_slots, heads, dim)) return e;
+  if (out_dtype != XT_DTYPE_BF16 && out_dtype != XT_DTYPE_F16)
+    return fail(XT_EINVAL, "%s: output dtype must be BF16 or FP16", what);
+  if (batch < 0 || max_k < 0) return fail(XT_EINVAL, "%s: negative batch/max_k", what);
+  if (batch == 0 || max_k == 0) return ok();
+  if (!req_to_token || !req_indices || !cu_k || !out_k || !out_v)
+    return fail(XT_EINVAL, "%s: a required pointer is null", what);
+  if (!aligned(out_k, 16) || !aligned(out_v, 16)) return fail(XT_EINVAL, "%s: outputs must be 16-byte aligned", what);
+  const int64_t total = (int64_t)batch * max_k * heads * (dim / 16);
+  hipLaunchKernelGGL(qsa_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), k_pay, v_pay, k_scales, v_scales, gk, gv, pool_slots,
+                     heads, dim, req_to_token, sr0, sr1, req_indices, batch, cu_k, max_k,
+                     static_cast<uint16_t*>(out_k), static_cast<uint16_t*>(out_v), out_dtype);
+  return check_launch(what);
+}

@@ -1,0 +1,108 @@
+// Device helpers shared by the NVFP4 kernels (gfx950 only).
+//
+// NVFP4 as stored in the KV pool: payload byte i of a head row holds element 2i in bits 0-3 and element 2i+1 in
+// bits 4-7 (an E2M1 code: sign bit 3, magnitude index into {0, .5, 1, 1.5, 2, 3, 4, 6}); one OCP E4M3 scale byte per
+// 16 elements; value = (e2m1 * e4m3) * g with g the per-tensor FP32 global scale.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/xtier_amd.h"
+
+namespace xt {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef short short2_t __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// FP32 -> E4M3 (fn) byte with round-to-nearest-even. Below 2^-6 the magnitude is rounded in subnormal steps of
+// 2^-9; from 2^-6 up the FP32 bits are rounded at mantissa bit 20, a carry moving into the exponent. A magnitude
+// that rounds above 448 becomes 448 (saturate) or NaN 0x7F (as torch's float8_e4m3fn cast); NaN becomes 0x7F.
+// The sign bit is kept in every case.
+__host__ __device__ inline uint32_t e4m3_encode(float x, bool saturate) {
+  uint32_t bits;
+  __builtin_memcpy(&bits, &x, 4);
+  const uint32_t sign = (bits >> 24) & 0x80u;
+  const uint32_t a = bits & 0x7FFFFFFFu;
+  uint32_t code;
+  if (a > 0x7F800000u) {
+    code = 0x7Fu;
+  } else if (a < 0x3C800000u) {
+    float f;
+    __builtin_memcpy(&f, &a, 4);
+    code = (uint32_t)__builtin_rintf(f * 512.0f);   // exact scaling; rint rounds half to even
+  } else {
+    const uint32_t r = a + 0x7FFFFu + ((a >> 20) & 1u);
+    code = (((r >> 23) - 120u) << 3) | ((r >> 20) & 7u);
+    if (code > 0x7Eu) code = saturate ? 0x7Eu : 0x7Fu;
+  }
+  return code | sign;
+}
+
+// E4M3 (fn) byte -> FP32: e > 0 is 2^(e-7) * (1 + m/8), e = 0 is m * 2^-9, 0x7F / 0xFF are NaN.
+__host__ __device__ inline float e4m3_decode(uint32_t b) {
+  const uint32_t e = (b >> 3) & 15u, m = b & 7u;
+  float mag;
+  if ((b & 0x7Fu) == 0x7Fu) {
+    mag = __builtin_nanf("");
+  } else if (e == 0) {
+    mag = (float)m * 0.001953125f;
+  } else {
+    const uint32_t fb = ((e + 120u) << 23) | (m << 20);
+    __builtin_memcpy(&mag, &fb, 4);
+  }
+  return (b & 0x80u) ? -mag : mag;
+}
+
+#if defined(__HIP_DEVICE_COMPILE__)
+// Two E2M1 codes (byte `sel` of `packed`: low nibble first) -> two exact FP32 values. The conversion's scale operand
+// contributes only its exponent, so it is 1.0 here and block scales are applied separately.
+template <int SEL>
+__device__ inline float2_t fp4x2_to_f32(uint32_t packed) {
+  return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(packed, 1.0f, SEL);
+}
+template <int SEL>
+__device__ inline half2_t fp4x2_to_f16(uint32_t packed) {
+  return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(packed, 1.0f, SEL);
+}
+// Two E4M3 bytes (bytes 0,1 or 2,3 of `packed`) -> two exact FP16 values (every E4M3 value is an FP16 value).
+template <bool HI>
+__device__ inline half2_t fp8x2_to_f16(uint32_t packed) {
+  return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(packed, 1.0f, HI);
+}
+#else
+// The host pass parses device code without the gfx950 builtins; these declarations are never code-generated.
+template <int SEL>
+__device__ float2_t fp4x2_to_f32(uint32_t packed);
+template <int SEL>
+__device__ half2_t fp4x2_to_f16(uint32_t packed);
+template <bool HI>
+__device__ half2_t fp8x2_to_f16(uint32_t packed);
+#endif
+
+// FP32 -> BF16 bits, round to nearest even; NaN -> quiet NaN with its sign.
+__host__ __device__ inline uint32_t f32_to_bf16_bits(float f) {
+  uint32_t b;
+  __builtin_memcpy(&b, &f, 4);
+  if ((b & 0x7FFFFFFFu) > 0x7F800000u) return ((b >> 16) & 0x8000u) | 0x7FC0u;
+  return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+__host__ __device__ inline float bf16_bits_to_f32(uint32_t h) {
+  const uint32_t b = h << 16;
+  float f;
+  __builtin_memcpy(&f, &b, 4);
+  return f;
+}
+__host__ __device__ inline uint32_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)f;
+  uint16_t u;
+  __builtin_memcpy(&u, &h, 2);
+  return u;
+}
+
+}  // namespace xt

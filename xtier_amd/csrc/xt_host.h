@@ -1,0 +1,20 @@
+// Host-side helpers of the C ABI: the per-thread last-error text and launch checks.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/xtier_amd.h"
+
+namespace xt {
+
+// Records the message for xt_last_error() and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clears the last error and returns XT_OK.
+int ok();
+// XT_OK, or XT_ELAUNCH with the HIP error text, after a kernel launch.
+int check_launch(const char* what);
+
+inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace xt

@@ -1,0 +1,187 @@
+"""Python entry points over the C ABI, with the argument order, keywords and error types of the reference pack
+functions they replace (xtier/packs/qwen4_exp/qsa_fp4.py, qsa_decode.py; xtier/packs/minimax_m3/kv_fp4.py;
+xtier/backend/formats.py). Tensors are torch tensors on the GPU; every call runs on the current HIP stream.
+
+``raw`` is the reference's tuple of a layer's pool buffers (qsa_fp4.py:43-58):
+(k_pay u8 [slots, kv_heads, dim/2], v_pay, k_scales u8 [slots, kv_heads, dim/16], v_scales, gk f32 [1], gv f32 [1]).
+"""
+import math
+
+import torch
+
+from . import _lib
+
+LOG2E = 1.4426950408889634
+_DTYPES = {torch.bfloat16: _lib.XT_DTYPE_BF16, torch.float16: _lib.XT_DTYPE_F16}
+_workspaces = {}   # device index -> uint8 tensor, grown on demand (never during a graph capture)
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need_cuda(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError('xtier_amd: GPU tensors expected')
+
+
+def _check_raw(raw):
+    """The reference's _check (qsa_fp4.py:165-171): contiguous packed rows with a power-of-2 head size."""
+    k, v, k_sf, v_sf, gk, gv = raw
+    if k_sf is None:
+        raise NotImplementedError('xtier_amd: FP8 pools are not covered; NVFP4 pools only')
+    dim = k.shape[2] * 2
+    if not (k.is_contiguous() and v.is_contiguous() and k_sf.is_contiguous() and v_sf.is_contiguous()
+            and dim % 32 == 0 and dim & (dim - 1) == 0):
+        raise ValueError(f'xtier qsa_fp4: packed [m, heads, dim / 2] rows with a power-of-2 head size expected, got '
+                         f'{tuple(k.shape)}')
+    if k.dtype != torch.uint8:
+        k, v, k_sf, v_sf = (t.view(torch.uint8) for t in (k, v, k_sf, v_sf))
+    _need_cuda(k, v, k_sf, v_sf, gk, gv)
+    return (k, v, k_sf, v_sf, gk.float() if gk.dtype != torch.float32 else gk,
+            gv.float() if gv.dtype != torch.float32 else gv), k.shape[1], dim
+
+
+def workspace(device, nbytes):
+    """A device byte buffer of at least nbytes, kept per device (allocate it before a graph capture)."""
+    device = torch.device(device)
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    buf = _workspaces.get(idx)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        _workspaces[idx] = buf
+    return buf
+
+
+# --- NVFP4 quantization --------------------------------------------------------------------------------------------
+
+def global_scale(x, out=None):
+    """FP32 [1] device tensor g = max(amax|x| / (6 * 448), 1e-12) of a BF16 tensor [..., heads, dim] or [..., dim]
+    (formats.py:122)."""
+    _need_cuda(x)
+    x3 = x.reshape(-1, 1, x.shape[-1]) if x.dim() < 3 else x.reshape(-1, *x.shape[-2:])
+    if out is None:
+        out = torch.empty(1, dtype=torch.float32, device=x.device)
+    ws = torch.empty(4, dtype=torch.uint8, device=x.device)
+    _lib.check(_lib.lib().xt_nvfp4_global_scale(_ptr(x3), x3.shape[0], x3.shape[1], x3.shape[2], x3.stride(0),
+                                                 x3.stride(1), _ptr(out), _ptr(ws), _stream(x)), 'global_scale')
+    return out
+
+
+def quantize_append(x, slots, g, pay, scales, saturate=True):
+    """NVFP4 quantize-on-append: rows x [n, heads, dim] BF16 (strided rows allowed, last dim contiguous) into the pool
+    at slots [n] (int64; a negative slot skips its row) with the device global scale g [1]. saturate=True stores 448
+    for a block scale that rounds above the E4M3 range (never NaN); False reproduces the reference's torch cast."""
+    _need_cuda(x, slots, g, pay, scales)
+    if x.dtype != torch.bfloat16 or x.dim() != 3 or x.stride(-1) != 1:
+        raise ValueError(f'xtier_amd.quantize_append: BF16 [n, heads, dim] rows expected, got {x.dtype} '
+                         f'{tuple(x.shape)}')
+    if slots.dtype != torch.int64:
+        slots = slots.to(torch.int64)
+    slots = slots.contiguous()
+    _lib.check(_lib.lib().xt_nvfp4_quantize_append(
+        _ptr(x), x.shape[0], x.shape[1], x.shape[2], x.stride(0), x.stride(1), _ptr(slots), _ptr(g),
+        _ptr(pay), _ptr(scales), pay.shape[0], 1 if saturate else 0, _stream(x)), 'quantize_append')
+
+
+def nvfp4_encode(x, saturate=False):
+    """formats.py:114-128 on the GPU for a BF16 tensor [slots, heads, dim] (or [rows, dim]): (payload u8
+    [..., dim/2], scale bytes u8 [..., dim/16], g f32 [1])."""
+    shape = x.shape
+    x3 = x.reshape(-1, 1, shape[-1]) if x.dim() == 2 else x
+    if x3.stride(-1) != 1:
+        x3 = x3.contiguous()
+    n, heads, dim = x3.shape
+    pay = torch.empty(n, heads, dim // 2, dtype=torch.uint8, device=x.device)
+    sc = torch.empty(n, heads, dim // 16, dtype=torch.uint8, device=x.device)
+    g = global_scale(x3)
+    quantize_append(x3, torch.arange(n, device=x.device, dtype=torch.int64), g, pay, sc, saturate=saturate)
+    return pay.reshape(*shape[:-1], dim // 2), sc.reshape(*shape[:-1], dim // 16), g
+
+
+# --- QSA gather / pack --------------------------------------------------------------------------------------------
+
+def gather(raw, req_to_token, req_indices, indices, seq_lens, cu_k, out_k, out_v, batch, topk, zero_fill_cols=0):
+    """qsa_fp4.gather (qsa_fp4.py:174-180): the decode/verify rows of ``indices`` dequantized into out_k / out_v
+    (compact, or page-aligned and zero-filled up to zero_fill_cols)."""
+    raw, heads, dim = _check_raw(raw)
+    if out_k.dtype not in _DTYPES or not out_k.is_contiguous() or not out_v.is_contiguous():
+        raise ValueError('xtier_amd.gather: contiguous BF16/FP16 outputs expected')
+    _need_cuda(req_to_token, req_indices, indices, seq_lens, cu_k, out_k, out_v)
+    req_indices = req_indices.to(torch.int64) if req_indices.dtype != torch.int64 else req_indices
+    _lib.check(_lib.lib().xt_qsa_gather_nvfp4(
+        *map(_ptr, raw), raw[0].shape[0], heads, dim, _ptr(req_to_token), req_to_token.stride(0),
+        _ptr(req_indices.contiguous()), _ptr(indices), indices.stride(0), _ptr(seq_lens), _ptr(cu_k), _ptr(out_k),
+        _ptr(out_v), _DTYPES[out_k.dtype], int(batch), int(topk), int(zero_fill_cols), _stream(out_k)), 'gather')
+
+
+def pack(raw, req_to_token, req_indices, cu_k, total_k, max_k, output_dtype):
+    """qsa_fp4.pack (qsa_fp4.py:183-192): whole prefixes as (packed_k, packed_v) [total_k, heads, dim]."""
+    raw, heads, dim = _check_raw(raw)
+    device = raw[0].device
+    packed_k = torch.empty((total_k, heads, dim), dtype=output_dtype, device=device)
+    packed_v = torch.empty((total_k, heads, dim), dtype=output_dtype, device=device)
+    batch = req_indices.numel()
+    req_indices = req_indices.to(torch.int64).contiguous()
+    _lib.check(_lib.lib().xt_qsa_pack_nvfp4(
+        *map(_ptr, raw), raw[0].shape[0], heads, dim, _ptr(req_to_token), req_to_token.stride(0),
+        req_to_token.stride(1), _ptr(req_indices), batch, _ptr(cu_k), int(max_k), _ptr(packed_k), _ptr(packed_v),
+        _DTYPES[output_dtype], _stream(packed_k)), 'pack')
+    return packed_k, packed_v
+
+
+# --- fused sparse attention ---------------------------------------------------------------------------------------
+
+def default_splits(rows, kv_heads, topk):
+    """Key splits per row: enough wavefronts for the 256 CUs (about 1024) with at least 64 keys per split."""
+    if topk <= 0:
+        return 1
+    units = max(1, rows * kv_heads)
+    splits = max(1, min(64, math.ceil(1024 / units), math.ceil(topk / 64)))
+    while math.ceil(math.ceil(topk / splits) / 32) * 32 * 4 * 4 > 48 * 1024:   # LDS for the slot lists
+        splits += 1
+    return splits
+
+
+def decode_workspace_bytes(rows, q_heads, dim, splits):
+    return int(_lib.lib().xt_sparse_decode_workspace_bytes(rows, q_heads, dim, splits))
+
+
+def sparse_decode(q, raw, table, indices, seq_lens, scale, page_size=1, row_req=None, counts=None, query_pos=None,
+                  out=None, lse=None, splits=None, ws=None):
+    """Fused NVFP4 sparse attention, one query per row: q [rows, q_heads, dim] BF16 attends to the valid positions of
+    indices [rows, topk] (int32; valid: column < counts[r], 0 <= pos < seq_lens[r], pos <= query_pos[r] when given),
+    resolved through ``table`` (token-granular req_to_token for page_size 1, else a page table) row row_req[r].
+    Returns out [rows, q_heads, dim] (BF16 unless ``out`` is given); lse [rows, q_heads] FP32 is filled if given."""
+    raw, kv_heads, dim = _check_raw(raw)
+    rows, q_heads, qdim = q.shape
+    if qdim != dim:
+        raise ValueError(f'xtier_amd.sparse_decode: q head size {qdim} != pool head size {dim}')
+    _need_cuda(q, table, indices, seq_lens, row_req, counts, query_pos, out, lse)
+    if q.dtype != torch.bfloat16 or q.stride(-1) != 1:
+        q = q.to(torch.bfloat16).contiguous()
+    if out is None:
+        out = torch.empty((rows, q_heads, dim), dtype=torch.bfloat16, device=q.device)
+    if out.dtype not in _DTYPES or out.stride(-1) != 1:
+        raise ValueError('xtier_amd.sparse_decode: BF16/FP16 output with a contiguous last dim expected')
+    if indices.dtype != torch.int32 or indices.stride(-1) != 1:
+        indices = indices.to(torch.int32).contiguous()
+    topk = indices.shape[1] if indices.dim() == 2 else 0
+    if row_req is not None and row_req.dtype != torch.int64:
+        row_req = row_req.to(torch.int64)
+    if splits is None:
+        splits = default_splits(rows, kv_heads, topk)
+    need = decode_workspace_bytes(rows, q_heads, dim, splits)
+    if ws is None:
+        ws = workspace(q.device, need)
+    _lib.check(_lib.lib().xt_sparse_decode_nvfp4(
+        _ptr(q), q.stride(0), q.stride(1), *map(_ptr, raw), raw[0].shape[0], kv_heads, q_heads, dim, _ptr(table),
+        table.stride(0), int(page_size), _ptr(row_req), _ptr(indices), indices.stride(0), topk, _ptr(counts),
+        _ptr(seq_lens), _ptr(query_pos), float(scale), _ptr(out), out.stride(0), out.stride(1), _DTYPES[out.dtype],
+        _ptr(lse), rows, int(splits), _ptr(ws), ws.numel(), _stream(q)), 'sparse_decode')
+    return out

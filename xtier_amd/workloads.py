@@ -1,0 +1,136 @@
+"""Seeded synthetic inputs for the sparse-attention workloads (bf16 activations, NVFP4 paged KV pools, page tables
+and top-k index lists), generated with torch on any device from a torch.Generator.
+
+Generators (the same rules for every workload):
+- K/V and latents: bf16 N(0, 1) with round(1% of heads * dim) channels (at least one) multiplied by 8, chosen once
+  per tensor;
+- the global scale of a tensor is amax / (6 * 448) (NVFP4 with its own amax);
+- page tables: each request owns ctx / page pages of the pool, in a random permutation;
+- index lists: unique positions, sorted, int32.
+"""
+from dataclasses import dataclass
+
+import torch
+
+
+@dataclass(frozen=True)
+class DecodeWorkload:
+    name: str
+    batch: int
+    q_heads: int
+    kv_heads: int
+    dim: int
+    ctx: int
+    topk: int
+    page: int = 64
+    index_mode: str = 'uniform'     # 'uniform' | 'recent_half'
+    q_std: float = 1.0
+
+    @property
+    def slots(self):
+        return self.batch * self.ctx
+
+    def algorithmic_bytes(self):
+        """Gathered KV payload plus scales: batch * topk * kv_heads * 2 * (dim/2 + dim/16)."""
+        return self.batch * self.topk * self.kv_heads * 2 * (self.dim // 2 + self.dim // 16)
+
+    def flops(self):
+        return self.batch * self.q_heads * self.topk * 4 * self.dim
+
+
+WORKLOADS = {
+    # 1 request, 8 q heads / 1 KV head, d 128, context 4096, top-512 uniform (the CPU-reference case)
+    'cpu_ref_decode': DecodeWorkload('cpu_ref_decode', 1, 8, 1, 128, 4096, 512),
+    # batch 32, 32 q / 4 KV heads, d 128, context 32768, top-2048 sorted unique per request, page 64
+    'gqa_decode_b32': DecodeWorkload('gqa_decode_b32', 32, 32, 4, 128, 32768, 2048),
+    # batch 4, context 524288, top-2048: half from the last 4096 tokens, half uniform over the rest
+    'long_ctx_decode_b4': DecodeWorkload('long_ctx_decode_b4', 4, 32, 4, 128, 524288, 2048,
+                                         index_mode='recent_half'),
+}
+
+
+def generator(device, seed):
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def kv_tensor(n, heads, dim, gen, device, outlier_frac=0.01, outlier_scale=8.0):
+    """bf16 [n, heads, dim] N(0, 1) with round(outlier_frac * heads * dim) channels (>= 1) scaled by outlier_scale."""
+    x = torch.randn(n, heads, dim, generator=gen, device=device, dtype=torch.float32)
+    channels = heads * dim
+    k = max(1, round(outlier_frac * channels))
+    pick = torch.randperm(channels, generator=gen, device=device)[:k]
+    scale = torch.ones(channels, device=device)
+    scale[pick] = outlier_scale
+    x.mul_(scale.view(1, heads, dim))
+    return x.to(torch.bfloat16)
+
+
+def page_table(batch, ctx, page, gen, device):
+    """int32 [batch, ctx/page]: every request's pages, the pool's pages in a random order."""
+    n_pages = batch * (ctx // page)
+    return torch.randperm(n_pages, generator=gen, device=device).to(torch.int32).view(batch, ctx // page)
+
+
+def token_table(pt, page):
+    """The token-granular form of a page table (SGLang's req_to_token): int32 [batch, ctx]."""
+    batch, pages = pt.shape
+    off = torch.arange(page, device=pt.device, dtype=torch.int32)
+    return (pt[:, :, None] * page + off[None, None, :]).reshape(batch, pages * page)
+
+
+def index_lists(batch, ctx, topk, gen, device, mode='uniform'):
+    """int32 [batch, topk] sorted unique positions below ctx."""
+    out = torch.empty(batch, topk, dtype=torch.int32, device=device)
+    for b in range(batch):
+        if mode == 'uniform':
+            pick = torch.randperm(ctx, generator=gen, device=device)[:topk]
+        elif mode == 'recent_half':
+            recent = min(4096, ctx)
+            half = topk // 2
+            a = ctx - recent + torch.randperm(recent, generator=gen, device=device)[:half]
+            rest = torch.randperm(ctx - recent, generator=gen, device=device)[:topk - half]
+            pick = torch.cat([rest, a])
+        else:
+            raise ValueError(mode)
+        out[b] = torch.sort(pick).values.to(torch.int32)
+    return out
+
+
+def causal_index_lists(q_positions, topk, recent, gen, device):
+    """Per query position p: the `recent` most recent positions (p-recent+1 .. p) and topk-recent uniform ones below
+    p-recent+1, sorted; int32 [n, topk]."""
+    n = q_positions.numel()
+    out = torch.empty(n, topk, dtype=torch.int32, device=device)
+    for i, p in enumerate(q_positions.tolist()):
+        lo = p - recent + 1
+        far = torch.randperm(lo, generator=gen, device=device)[:topk - recent]
+        near = torch.arange(lo, p + 1, device=device)
+        out[i] = torch.sort(torch.cat([far, near])).values.to(torch.int32)
+    return out
+
+
+@dataclass
+class DecodeInputs:
+    workload: DecodeWorkload
+    q: torch.Tensor            # bf16 [batch, q_heads, dim]
+    k: torch.Tensor            # bf16 [slots, kv_heads, dim] (None when not kept)
+    v: torch.Tensor
+    page_table: torch.Tensor   # int32 [batch, ctx/page]
+    indices: torch.Tensor      # int32 [batch, topk]
+    seq_lens: torch.Tensor     # int32 [batch]
+
+
+def decode_inputs(w, seed, device='cpu', batch=None):
+    """Seeded activations and index lists of a decode workload (optionally with fewer requests)."""
+    b = w.batch if batch is None else batch
+    gen = generator(device, seed)
+    slots = b * w.ctx
+    k = kv_tensor(slots, w.kv_heads, w.dim, gen, device)
+    v = kv_tensor(slots, w.kv_heads, w.dim, gen, device)
+    q = (torch.randn(b, w.q_heads, w.dim, generator=gen, device=device) * w.q_std).to(torch.bfloat16)
+    pt = page_table(b, w.ctx, w.page, gen, device)
+    idx = index_lists(b, w.ctx, w.topk, gen, device, w.index_mode)
+    seq = torch.full((b,), w.ctx, dtype=torch.int32, device=device)
+    return DecodeInputs(w, q, k, v, pt, idx, seq)
