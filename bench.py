@@ -127,8 +127,7 @@ def main():
     log(f'built {args.layers} layer pools ({w.slots} slots each) in {time.time() - t0:.1f} s')
     scale = 1.0 / math.sqrt(w.dim)
     splits = args.splits or ops.default_splits(w.batch, w.kv_heads, w.topk)
-    ws = torch.empty(ops.decode_workspace_bytes(w.batch, w.q_heads, w.dim, splits), dtype=torch.uint8,
-                     device='cuda')
+    ws = ops.new_workspace('cuda', w.batch, w.q_heads, w.dim, splits)
     out = torch.empty(w.batch, w.q_heads, w.dim, dtype=torch.bfloat16, device='cuda')
 
     def step(layer):

@@ -101,7 +101,10 @@ size_t xt_sparse_decode_workspace_bytes(int rows, int q_heads, int dim, int spli
  * K/V are dequantized in registers; out[r, h] = sum_k softmax_k(q.k * scale) v_k in the dtype out_dtype, a row
  * without valid keys writing 0. lse (optional, FP32 [rows, q_heads]): natural log-sum-exp of the scaled scores,
  * -inf for an empty row. q_heads must be a multiple of kv_heads with q_heads / kv_heads <= 16; dim = 128.
- * splits: key splits per row (1..64); workspace: xt_sparse_decode_workspace_bytes(rows, q_heads, dim, splits). */
+ * splits: key splits per row (1..64); workspace: xt_sparse_decode_workspace_bytes(rows, q_heads, dim, splits) bytes,
+ * 256-byte aligned and zero-filled before its first use; every call leaves its counter region zero again, so one
+ * workspace serves any sequence of calls on one stream (calls that overlap in time need separate workspaces).
+ * One launch: the last workgroup of each (row, group of 4 KV heads) merges the split partials. */
 int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, const uint8_t* k_pay,
                            const uint8_t* v_pay, const uint8_t* k_scales, const uint8_t* v_scales, const float* gk,
                            const float* gv, int64_t pool_slots, int kv_heads, int q_heads, int dim,

@@ -188,7 +188,7 @@ def test_graph_replay_equals_eager():
     pool, pt, idx, q = _small_case(seed=5, batch=8)
     seq = torch.full((8,), 3008, dtype=torch.int32, device='cuda')
     splits = 4
-    ws = torch.empty(ops.decode_workspace_bytes(8, 32, 128, splits), dtype=torch.uint8, device='cuda')
+    ws = ops.new_workspace('cuda', 8, 32, 128, splits)
     qs = q.cuda().clone()
     out = torch.empty(8, 32, 128, dtype=torch.bfloat16, device='cuda')
     args = (pool.raw, pt.cuda(), idx.cuda(), seq, 0.0884)

@@ -1,30 +1,47 @@
-// Fused sparse GQA attention over the NVFP4 paged pool: gather through the page table, dequantize in registers,
-// QK and PV on MFMA (v_mfma_f32_16x16x32_f16), online softmax in the exp2 domain, split-K partials, then a combine.
+// Fused sparse GQA attention over the NVFP4 paged pool: gather through the page table, dequantize in registers, QK
+// and PV on MFMA (v_mfma_f32_16x16x32_f16), online softmax in the exp2 domain. Two launches: the split kernel writes
+// one partial result per (row, key split, head), the combine kernel merges them (skipped when there is one split).
 //
-// Work unit = one wavefront: (query row, KV head, key split). A workgroup holds 4 units with the KV head fastest, so
-// for 4 KV heads the 4 waves of a workgroup read the 4 adjacent 64-byte head rows of the same tokens.
+// Work decomposition: a workgroup = 8 wavefronts = 4 consecutive KV heads x 2 key halves of one (query row, key
+// split); each wave owns one (row, KV head, split, half) and walks its keys in steps of 32. The workgroup computes the
+// split's pool slots once into LDS, and merges the two halves of each head through LDS before writing the partial.
+// Workgroups are numbered so that all splits of a row run on the same XCD (round-robin dispatch puts workgroup g on
+// XCD g % 8): their K/V pages and partials share one L2.
+//
+// Memory pipeline: per step a wave issues 6 loads (K and V payload as 16-byte row pieces, K and V scales as one dword
+// per lane) and keeps P steps in flight in a register ring. V is transposed for the PV operand through a padded LDS
+// tile; the K scales reach their lanes with one ds_bpermute per 16-key tile.
 //
 // Numerics: e2m1 * e4m3 is exact in FP16 (at most 6 significant bits, magnitudes 2^-10 .. 2688), so K and V enter
 // the MFMA exactly without their global scales; the query enters as FP16 of q * scale * log2(e); the K global scale
-// multiplies the FP32 scores and the V global scale the final output. P is FP16 for the PV product, all sums FP32.
+// multiplies the FP32 scores and the V global scale the merged output. P is FP16 for the PV product, sums are FP32.
+// The running maximum is raised only when a score exceeds it by more than 2^8 (lazy rescale), so P <= 256.
 //
 // Lane layouts (16x16x32 MFMA: A[i][k] = lane i + 16*(k/8), element k%8; B[k][j] = lane j + 16*(k/8), element k%8;
 // C[i][j] = lane j + 16*(i/4), element i%4). With hl = lane % 16 and j = lane / 16:
-//   QK: C = S^T [16 tokens x 16 heads]; A = K tile, lane (token hl, 16 payload bytes j*16..j*16+15 of the head row);
-//       MFMA kk (0..3) contracts dword kk of those 16 bytes, i.e. d = 32j + 8kk + e; B = Q^T with the same d order.
-//       So lane (hl, j) ends up with the scores of head hl for tokens 4j..4j+3 (tile 0) and 16+4j..16+4j+3 (tile 1).
-//   PV: C = O^T [16 rows x 16 heads] where row c is payload dword c of the head row; MFMA i (0..7) takes nibble i of
-//       every dword, i.e. d = 8c + i. A = V^T, lane (dword hl, the 8 tokens above); B = P^T, lane (head hl, the same 8
-//       tokens in the same order). Lane (hl, j) ends up with O^T for head hl, d = 32j .. 32j+31.
+//   QK: C = S^T [16 keys x 16 heads]; A = K tile, lane (key hl, payload bytes 16j .. 16j+15 of the head row); MFMA kk
+//       (0..3) contracts dword kk of those 16 bytes, d = 32j + 8kk + e; B = Q^T in the same d order. Lane (hl, j)
+//       ends up with the scores of head hl for keys T(j) = {4j..4j+3, 16+4j..16+4j+3} of the step.
+//   PV: C = O^T [16 rows x 16 heads], row c = payload dword c of the head row; MFMA i (0..7) takes nibble i of every
+//       dword, d = 8c + i. A = V^T, lane (dword hl, keys T(j)); B = P^T, lane (head hl, keys T(j)) in the same order.
+//       Lane (hl, j) ends up with O^T of head hl for d = 32j .. 32j+31.
 #include "xt_common.h"
 #include "xt_host.h"
 
 namespace xt {
 namespace {
 
-constexpr int kDim = 128;            // head size (payload 64 bytes, 8 scale bytes per head row)
-constexpr int kStep = 32;            // keys per step
-constexpr int kWavesPerBlock = 4;
+constexpr int kDim = 128;          // head size: 64 payload bytes, 8 scale bytes per head row
+constexpr int kStep = 32;          // keys per step
+constexpr int kHeadsPerGroup = 4;  // KV heads per workgroup
+constexpr int kHalves = 2;         // key halves per workgroup
+constexpr int kWaves = kHeadsPerGroup * kHalves;
+constexpr int kVRow = 80;          // LDS bytes per key in the V transpose tile (64 + 16: no bank conflicts)
+constexpr int kWaveLds = kStep * kVRow + kStep * 8;   // V tile + V scale tile per wave
+constexpr int kPrefetch = 4;       // steps of loads in flight per wave
+constexpr float kRescale = 8.0f;   // log2 of the largest P before the running maximum is raised
+constexpr int kPartStride = kDim + 4;   // floats per partial (split, head): 128 accumulators, max, sum, 2 pad
+constexpr int kMergeLds = kHeadsPerGroup * 64 * 36 * 4;   // a half's (acc, max, sum) per lane for 4 waves
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -36,7 +53,7 @@ struct DecodeArgs {
   const float* gk;
   const float* gv;
   int64_t pool_slots;
-  int kv_heads, q_heads, group;
+  int kv_heads, q_heads, group, kv_groups;
   const int32_t* table;
   int64_t table_stride;
   int page_size;
@@ -49,48 +66,25 @@ struct DecodeArgs {
   const int32_t* query_pos;
   float qscale;                      // softmax scale * log2(e)
   int rows, splits, keys_per_split;  // keys_per_split: a multiple of kStep
-  float* part_acc;                   // [rows, splits, q_heads, kDim]
-  float* part_ml;                    // [rows, splits, q_heads, 2]: running max (log2 domain), sum
+  int slot_lds_bytes;                // LDS bytes of the slot list (padded to whole prefetch groups per half)
+  uint16_t* out;
+  int64_t o_rs, o_hs;
+  int out_dtype;
+  float* lse;
+  float* part;                       // [rows, splits, q_heads, kPartStride]: accumulators, max (log2), sum
+  int64_t n_units;                   // rows * kv_groups * splits workgroups
+  int64_t per_xcd;                   // launched workgroups / 8
+  int xcd_map;                       // 1: number units XCD-major (rows >= 8), 0: unit = workgroup
 };
 
-struct StepData {
-  uint4 kw[2];        // K payload: 16 bytes of token (16 * tile + hl)
-  uint32_t ks[2];     // K scales: the 2 bytes for those 16 payload bytes
-  uint32_t vw[8];     // V payload dword hl of tokens T(j)[e]
-  uint32_t vs[8];     // V scale byte (block hl / 2) of the same tokens; 0 for invalid tokens
-  uint32_t valid;     // bit e: token T(j)[e] is valid
+struct Step {
+  uint4 kw[2];   // K payload bytes 16j..16j+15 of key 16*tt + hl
+  uint4 vw[2];   // V payload, same keys and bytes
+  uint32_t ks;   // K scale bytes 4*(lane&1) .. +3 of key lane/2
+  uint32_t vs;   // V scale bytes, same
 };
 
-// Token (within a step) of the e-th of the 8 tokens a lane of group j holds scores for.
-__device__ inline int tok_of(int j, int e) { return (e < 4) ? (4 * j + e) : (16 + 4 * j + (e - 4)); }
-
-__device__ inline void load_step(const DecodeArgs& a, const int32_t* __restrict__ lds_slots, int step, int kvh,
-                                 int hl, int j, StepData& d) {
-  const int64_t row_bytes = (int64_t)a.kv_heads * (kDim / 2);
-  const int64_t row_scales = (int64_t)a.kv_heads * (kDim / 16);
-  const uint8_t* kp = a.k_pay + (int64_t)kvh * (kDim / 2);
-  const uint8_t* vp = a.v_pay + (int64_t)kvh * (kDim / 2);
-  const uint8_t* ksf = a.k_sf + (int64_t)kvh * (kDim / 16);
-  const uint8_t* vsf = a.v_sf + (int64_t)kvh * (kDim / 16);
-  const int base = step * kStep;
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    const int32_t s = lds_slots[base + 16 * tt + hl];
-    const int64_t slot = s < 0 ? 0 : s;
-    d.kw[tt] = *reinterpret_cast<const uint4*>(kp + slot * row_bytes + 16 * j);
-    d.ks[tt] = *reinterpret_cast<const uint16_t*>(ksf + slot * row_scales + 2 * j);
-  }
-  d.valid = 0;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int32_t s = lds_slots[base + tok_of(j, e)];
-    const int64_t slot = s < 0 ? 0 : s;
-    d.vw[e] = *reinterpret_cast<const uint32_t*>(vp + slot * row_bytes + 4 * hl);
-    const uint32_t sb = vsf[slot * row_scales + (hl >> 1)];
-    d.vs[e] = s < 0 ? 0u : sb;
-    d.valid |= (s >= 0 ? 1u : 0u) << e;
-  }
-}
+__device__ inline int key_of(int j, int e) { return (e < 4) ? (4 * j + e) : (16 + 4 * j + (e - 4)); }
 
 __device__ inline half8_t dequant_k(uint32_t w, half2_t sc) {
   const half2_t p0 = fp4x2_to_f16<0>(w) * sc;
@@ -100,196 +94,334 @@ __device__ inline half8_t dequant_k(uint32_t w, half2_t sc) {
   return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
 
-__global__ void __launch_bounds__(256) decode_split_kernel(const DecodeArgs a) {
-  extern __shared__ int32_t lds[];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int hl = lane & 15, j = lane >> 4;
-  const int64_t unit = (int64_t)blockIdx.x * kWavesPerBlock + wave;
-  const int64_t n_units = (int64_t)a.rows * a.kv_heads * a.splits;
-  if (unit >= n_units) return;   // the whole wave leaves; no workgroup barrier is used below
-  const int kvh = (int)(unit % a.kv_heads);
-  const int split = (int)((unit / a.kv_heads) % a.splits);
-  const int row = (int)(unit / ((int64_t)a.kv_heads * a.splits));
-  int32_t* slots = lds + wave * (a.keys_per_split + kStep);
+struct WaveCtx {
+  const uint8_t* kp;    // this head's payload column
+  const uint8_t* vp;
+  const uint8_t* ksf;   // this head's scale column
+  const uint8_t* vsf;
+  int64_t row_bytes, row_scales;
+  const int32_t* slots;  // this wave's slot list in LDS (-1: invalid)
+  int lane, hl, j;
+};
 
-  // 1. slots of this unit's keys into LDS (-1: invalid)
-  const int count = a.counts ? min(a.counts[row], a.topk) : a.topk;
-  const int t0 = split * a.keys_per_split;
-  const int t1 = min(t0 + a.keys_per_split, count);
-  const int n = max(0, t1 - t0);
-  const int32_t seqlen = a.seq_lens[row];
-  const int32_t qpos = a.query_pos ? a.query_pos[row] : 0x7FFFFFFF;
-  const int64_t trow = a.row_req ? a.row_req[row] : row;
-  const int32_t* trow_ptr = a.table + trow * a.table_stride;
-  const int steps = (n + kStep - 1) / kStep;
-  for (int i = lane; i < steps * kStep; i += 64) {
-    int32_t slot = -1;
-    if (i < n) {
-      const int32_t pos = a.indices[(int64_t)row * a.idx_stride + t0 + i];
-      if (pos >= 0 && pos < seqlen && pos <= qpos) {
-        int64_t s;
-        if (a.page_size == 1)
-          s = trow_ptr[pos];
-        else
-          s = (int64_t)trow_ptr[pos / a.page_size] * a.page_size + pos % a.page_size;
-        if (s >= 0 && s < a.pool_slots) slot = (int32_t)s;
-      }
-    }
-    slots[i] = slot;
+__device__ inline void load_step(const WaveCtx& w, int step, Step& d) {
+  const int base = step * kStep;
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const int32_t s = w.slots[base + 16 * tt + w.hl];
+    const int64_t slot = s < 0 ? 0 : s;
+    d.kw[tt] = *reinterpret_cast<const uint4*>(w.kp + slot * w.row_bytes + 16 * w.j);
+    d.vw[tt] = *reinterpret_cast<const uint4*>(w.vp + slot * w.row_bytes + 16 * w.j);
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  const int32_t s = w.slots[base + (w.lane >> 1)];
+  const int64_t slot = s < 0 ? 0 : s;
+  d.ks = *reinterpret_cast<const uint32_t*>(w.ksf + slot * w.row_scales + 4 * (w.lane & 1));
+  d.vs = *reinterpret_cast<const uint32_t*>(w.vsf + slot * w.row_scales + 4 * (w.lane & 1));
+}
 
-  // 2. query: B operand of the 4 QK MFMAs, FP16 of q * scale * log2(e); heads beyond the group are zero
-  half8_t qb[4];
-  {
-    const bool hv = hl < a.group;
-    const int head = kvh * a.group + (hv ? hl : 0);
-    const uint16_t* qp = a.q + (int64_t)row * a.q_rs + (int64_t)head * a.q_hs;
+struct SoftmaxState {
+  float m;            // reference maximum of head hl (log2 domain), identical on the 4 lanes of the head
+  float l;            // this lane's share of the sum of 2^(s - m)
+  float4_t acc[8];    // O^T of head hl, d = 32j + 8r + i in acc[i][r]
+};
+
+__device__ inline void compute_step(const WaveCtx& w, int step, const Step& d, const half8_t (&qb)[4], float gk,
+                                    uint8_t* vtile, SoftmaxState& st) {
+  const int lane = w.lane, hl = w.hl, j = w.j;
+  // validity of the step's 32 keys (bit t: key t), uniform over the wave
+  const uint32_t valid =
+      (uint32_t)__builtin_amdgcn_ballot_w64(lane < kStep && w.slots[step * kStep + (lane & 31)] >= 0);
+  const bool my_scale_valid = (valid >> (lane >> 1)) & 1u;
+  const uint32_t ks = d.ks;
+  const uint32_t vs = my_scale_valid ? d.vs : 0u;   // invalid keys: V scale 0, so V = 0 whatever slot 0 holds
+
+  // V: stage payload and scales in LDS, transposed reads below
+  uint8_t* vscale = vtile + kStep * kVRow;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      uint4 w = make_uint4(0u, 0u, 0u, 0u);
-      if (hv) w = *reinterpret_cast<const uint4*>(qp + 32 * j + 8 * kk);
-      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  for (int tt = 0; tt < 2; ++tt)
+    *reinterpret_cast<uint4*>(vtile + (16 * tt + hl) * kVRow + 16 * j) = d.vw[tt];
+  *reinterpret_cast<uint32_t*>(vscale + (lane >> 1) * 8 + 4 * (lane & 1)) = vs;
+
+  // QK
+  float4_t s[2];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        qb[kk][2 * e] = (_Float16)(bf16_bits_to_f32(ws[e] & 0xFFFFu) * a.qscale);
-        qb[kk][2 * e + 1] = (_Float16)(bf16_bits_to_f32(ws[e] >> 16) * a.qscale);
-      }
-    }
+  for (int tt = 0; tt < 2; ++tt) {
+    const uint32_t src = (uint32_t)__shfl((int)ks, 2 * (16 * tt + hl) + (j >> 1));
+    const half2_t sc2 = fp8x2_to_f16<false>(src >> (16 * (j & 1)));
+    const half2_t sc_lo = half2_t{sc2.x, sc2.x}, sc_hi = half2_t{sc2.y, sc2.y};
+    const uint32_t kw[4] = {d.kw[tt].x, d.kw[tt].y, d.kw[tt].z, d.kw[tt].w};
+    s[tt] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      s[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant_k(kw[kk], kk < 2 ? sc_lo : sc_hi), qb[kk], s[tt], 0, 0,
+                                                     0);
   }
-  const float gk = *a.gk;
-
-  float m_run = -__builtin_inff();
-  float l_run = 0.0f;
-  float4_t acc[8];
+  // online softmax of head hl over keys T(j), lazy rescale
+  float sv[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-  StepData cur;
-  if (steps > 0) load_step(a, slots, 0, kvh, hl, j, cur);
-  for (int st = 0; st < steps; ++st) {
-    StepData nxt;
-    if (st + 1 < steps) load_step(a, slots, st + 1, kvh, hl, j, nxt);
-
-    // QK: S^T tiles for tokens 0..15 and 16..31 of the step
-    float4_t s[2];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const half2_t sc2 = fp8x2_to_f16<false>(cur.ks[tt]);
-      const half2_t sc_lo = half2_t{sc2.x, sc2.x}, sc_hi = half2_t{sc2.y, sc2.y};
-      const uint32_t w[4] = {cur.kw[tt].x, cur.kw[tt].y, cur.kw[tt].z, cur.kw[tt].w};
-      s[tt] = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-        s[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant_k(w[kk], kk < 2 ? sc_lo : sc_hi), qb[kk], s[tt], 0,
-                                                       0, 0);
-    }
-    // online softmax (log2 domain): scores of head hl for tokens T(j)[0..7]
-    float sv[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x = s[e >> 2][e & 3] * gk;
-      sv[e] = ((cur.valid >> e) & 1u) ? x : -__builtin_inff();
-    }
-    float mt = sv[0];
-#pragma unroll
-    for (int e = 1; e < 8; ++e) mt = fmaxf(mt, sv[e]);
-    mt = fmaxf(mt, __shfl_xor(mt, 16));
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
-    const float m_new = fmaxf(m_run, mt);
-    const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    float p[8];
-    float psum = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      p[e] = __builtin_amdgcn_exp2f(sv[e] - m_use);
-      psum += p[e];
-    }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] *= alpha;
-    const half8_t pb = half8_t{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3],
-                               (_Float16)p[4], (_Float16)p[5], (_Float16)p[6], (_Float16)p[7]};
-    // V^T operands: for tokens (e, e+1) build bytes (nibble of token e, same nibble of token e+1)
-    half8_t av[8];
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      const uint32_t w0 = cur.vw[e], w1 = cur.vw[e + 1];
-      const uint32_t lo = (w0 & 0x0F0F0F0Fu) | ((w1 & 0x0F0F0F0Fu) << 4);
-      const uint32_t hi = ((w0 >> 4) & 0x0F0F0F0Fu) | (w1 & 0xF0F0F0F0u);
-      const half2_t sp = fp8x2_to_f16<false>(cur.vs[e] | (cur.vs[e + 1] << 8));
-      half2_t x;
-      x = fp4x2_to_f16<0>(lo) * sp; av[0][e] = x.x; av[0][e + 1] = x.y;
-      x = fp4x2_to_f16<0>(hi) * sp; av[1][e] = x.x; av[1][e + 1] = x.y;
-      x = fp4x2_to_f16<1>(lo) * sp; av[2][e] = x.x; av[2][e + 1] = x.y;
-      x = fp4x2_to_f16<1>(hi) * sp; av[3][e] = x.x; av[3][e + 1] = x.y;
-      x = fp4x2_to_f16<2>(lo) * sp; av[4][e] = x.x; av[4][e + 1] = x.y;
-      x = fp4x2_to_f16<2>(hi) * sp; av[5][e] = x.x; av[5][e + 1] = x.y;
-      x = fp4x2_to_f16<3>(lo) * sp; av[6][e] = x.x; av[6][e + 1] = x.y;
-      x = fp4x2_to_f16<3>(hi) * sp; av[7][e] = x.x; av[7][e + 1] = x.y;
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], pb, acc[i], 0, 0, 0);
-    cur = nxt;
+  for (int e = 0; e < 8; ++e) {
+    const float x = s[e >> 2][e & 3] * gk;
+    sv[e] = ((valid >> key_of(j, e)) & 1u) ? x : -__builtin_inff();
   }
-
-  // 3. partials: the 4 lanes of a head hold disjoint token subsets of l; acc is already complete per lane
-  float l_tot = l_run + __shfl_xor(l_run, 16);
-  l_tot += __shfl_xor(l_tot, 32);
-  if (hl < a.group) {
-    const int head = kvh * a.group + hl;
-    const int64_t at = ((int64_t)row * a.splits + split) * a.q_heads + head;
-    float* dst = a.part_acc + at * kDim + 32 * j;
+  float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+  mt = fmaxf(mt, __shfl_xor(mt, 16));
+  mt = fmaxf(mt, __shfl_xor(mt, 32));
+  if (__builtin_amdgcn_ballot_w64(mt > st.m + kRescale)) {   // rare after the first steps
+    const float m_new = (mt > st.m + kRescale) ? mt : st.m;
+    const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+    st.l *= alpha;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      reinterpret_cast<float4_t*>(dst + 8 * r)[0] = float4_t{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
-      reinterpret_cast<float4_t*>(dst + 8 * r)[1] = float4_t{acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
-    }
-    if (j == 0) reinterpret_cast<float2_t*>(a.part_ml)[at] = float2_t{m_run, l_tot};
+    for (int i = 0; i < 8; ++i) st.acc[i] *= alpha;
+    st.m = m_new;
+  }
+  const float m_use = (st.m == -__builtin_inff()) ? 0.0f : st.m;
+  float p[8];
+  float psum = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    p[e] = __builtin_amdgcn_exp2f(sv[e] - m_use);
+    psum += p[e];
+  }
+  st.l += psum;
+  const half8_t pb = half8_t{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3],
+                             (_Float16)p[4], (_Float16)p[5], (_Float16)p[6], (_Float16)p[7]};
+  // V^T operands: dword hl of keys T(j), and the scale byte of block hl/2 of those keys
+  asm volatile("" ::: "memory");
+  uint32_t vw[8], vb[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int key = key_of(j, e);
+    vw[e] = *reinterpret_cast<const uint32_t*>(vtile + key * kVRow + 4 * hl);
+    vb[e] = vscale[key * 8 + (hl >> 1)];
+  }
+  half8_t av[8];
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const uint32_t w0 = vw[e], w1 = vw[e + 1];
+    const uint32_t lo = (w0 & 0x0F0F0F0Fu) | ((w1 & 0x0F0F0F0Fu) << 4);   // byte b: nibble 2b of keys e, e+1
+    const uint32_t hi = ((w0 >> 4) & 0x0F0F0F0Fu) | (w1 & 0xF0F0F0F0u);   // byte b: nibble 2b+1
+    const half2_t sp = fp8x2_to_f16<false>(vb[e] | (vb[e + 1] << 8));
+    half2_t x;
+    x = fp4x2_to_f16<0>(lo) * sp; av[0][e] = x.x; av[0][e + 1] = x.y;
+    x = fp4x2_to_f16<0>(hi) * sp; av[1][e] = x.x; av[1][e + 1] = x.y;
+    x = fp4x2_to_f16<1>(lo) * sp; av[2][e] = x.x; av[2][e + 1] = x.y;
+    x = fp4x2_to_f16<1>(hi) * sp; av[3][e] = x.x; av[3][e + 1] = x.y;
+    x = fp4x2_to_f16<2>(lo) * sp; av[4][e] = x.x; av[4][e + 1] = x.y;
+    x = fp4x2_to_f16<2>(hi) * sp; av[5][e] = x.x; av[5][e + 1] = x.y;
+    x = fp4x2_to_f16<3>(lo) * sp; av[6][e] = x.x; av[6][e + 1] = x.y;
+    x = fp4x2_to_f16<3>(hi) * sp; av[7][e] = x.x; av[7][e + 1] = x.y;
+  }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < 8; ++i) st.acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], pb, st.acc[i], 0, 0, 0);
+}
+
+__device__ inline void store_out(const DecodeArgs& a, int row, int head, int d0, const float* v, int n) {
+  uint16_t* o = a.out + (int64_t)row * a.o_rs + (int64_t)head * a.o_hs + d0;
+  for (int e = 0; e < n; e += 2) {
+    uint32_t packed;
+    if (a.out_dtype == XT_DTYPE_BF16)
+      packed = f32_to_bf16_bits(v[e]) | (f32_to_bf16_bits(v[e + 1]) << 16);
+    else
+      packed = f32_to_f16_bits(v[e]) | (f32_to_f16_bits(v[e + 1]) << 16);
+    *reinterpret_cast<uint32_t*>(o + e) = packed;
   }
 }
 
-// One wave per (row, head): merge the splits in FP32 (weights 2^(m - max m); a row without keys gives 0), apply the
-// V global scale, write the output and the natural log-sum-exp.
-__global__ void __launch_bounds__(256) decode_combine_kernel(const float* __restrict__ part_acc,
-                                                             const float* __restrict__ part_ml, int rows, int q_heads,
-                                                             int splits, const float* __restrict__ gv,
-                                                             uint16_t* __restrict__ out, int64_t o_rs, int64_t o_hs,
-                                                             int out_dtype, float* __restrict__ lse) {
-  const int lane = threadIdx.x & 63;
-  const int64_t unit = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  if (unit >= (int64_t)rows * q_heads) return;
-  const int head = (int)(unit % q_heads);
-  const int row = (int)(unit / q_heads);
-  const float2_t* ml = reinterpret_cast<const float2_t*>(part_ml);
-  float top = -__builtin_inff();
-  for (int s = 0; s < splits; ++s) top = fmaxf(top, ml[((int64_t)row * splits + s) * q_heads + head].x);
-  const float top_use = (top == -__builtin_inff()) ? 0.0f : top;
-  float total = 0.0f;
-  float2_t o = float2_t{0.f, 0.f};
-  for (int s = 0; s < splits; ++s) {
-    const int64_t at = ((int64_t)row * splits + s) * q_heads + head;
-    const float2_t v = ml[at];
-    const float w = __builtin_amdgcn_exp2f(v.x - top_use);
-    total += w * v.y;
-    const float2_t x = reinterpret_cast<const float2_t*>(part_acc + at * kDim)[lane];
-    o += w * x;
+template <int P>
+__global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  // XCD-aware numbering: launched workgroup g runs on XCD g % 8; unit u = (g % 8) * per_xcd + g / 8 keeps a row's
+  // consecutive units (its splits) on one XCD.
+  const int64_t g = blockIdx.x;
+  const int64_t u = a.xcd_map ? (g % 8) * a.per_xcd + g / 8 : g;
+  if (u >= a.n_units) return;   // uniform over the workgroup
+  const int split = (int)(u % a.splits);
+  const int kvg = (int)((u / a.splits) % a.kv_groups);
+  const int row = (int)(u / ((int64_t)a.splits * a.kv_groups));
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int kvh = kvg * kHeadsPerGroup + (wave & (kHeadsPerGroup - 1));
+  const int half = wave / kHeadsPerGroup;
+  const bool active = kvh < a.kv_heads;
+
+  int32_t* slots = reinterpret_cast<int32_t*>(lds);
+  uint8_t* vtile = lds + a.slot_lds_bytes + wave * kWaveLds;
+
+  // 1. the split's pool slots (-1: invalid key), shared by the workgroup's waves; each half owns a whole number of
+  // prefetch groups, padded with invalid keys that compute to no-ops (P = 0, V = 0, maximum unchanged)
+  const int count = a.counts ? min(a.counts[row], a.topk) : a.topk;
+  const int t0 = split * a.keys_per_split;
+  const int n = max(0, min(t0 + a.keys_per_split, count) - t0);
+  const int half_steps = (((n + kStep - 1) / kStep + kHalves * P - 1) / (kHalves * P)) * P;
+  {
+    const int32_t seqlen = a.seq_lens[row];
+    const int32_t qpos = a.query_pos ? a.query_pos[row] : 0x7FFFFFFF;
+    const int64_t trow = a.row_req ? a.row_req[row] : row;
+    const int32_t* tp = a.table + trow * a.table_stride;
+    const int32_t* ip = a.indices + (int64_t)row * a.idx_stride + t0;
+    for (int i = threadIdx.x; i < kHalves * half_steps * kStep; i += blockDim.x) {
+      int32_t slot = -1;
+      if (i < n) {
+        const int32_t pos = ip[i];
+        if (pos >= 0 && pos < seqlen && pos <= qpos) {
+          const int64_t sl = (a.page_size == 1) ? (int64_t)tp[pos]
+                                                : (int64_t)tp[pos / a.page_size] * a.page_size + pos % a.page_size;
+          if (sl >= 0 && sl < a.pool_slots) slot = (int32_t)sl;
+        }
+      }
+      slots[i] = slot;
+    }
   }
-  const float g = *gv;
-  const float inv = total > 0.0f ? g / total : 0.0f;
-  const float a0 = o.x * inv, a1 = o.y * inv;
-  uint32_t packed;
-  if (out_dtype == XT_DTYPE_BF16)
-    packed = f32_to_bf16_bits(a0) | (f32_to_bf16_bits(a1) << 16);
-  else
-    packed = f32_to_f16_bits(a0) | (f32_to_f16_bits(a1) << 16);
-  reinterpret_cast<uint32_t*>(out + (int64_t)row * o_rs + (int64_t)head * o_hs)[lane] = packed;
-  if (lse && lane == 0)
-    lse[unit] = total > 0.0f ? (top_use + __builtin_log2f(total)) * kLn2 : -__builtin_inff();
+  __syncthreads();
+
+  const int hl = lane & 15, j = lane >> 4;
+  SoftmaxState st;
+  st.m = -__builtin_inff();
+  st.l = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) st.acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  if (active && half_steps > 0) {
+    WaveCtx w;
+    w.row_bytes = (int64_t)a.kv_heads * (kDim / 2);
+    w.row_scales = (int64_t)a.kv_heads * (kDim / 16);
+    w.kp = a.k_pay + (int64_t)kvh * (kDim / 2);
+    w.vp = a.v_pay + (int64_t)kvh * (kDim / 2);
+    w.ksf = a.k_sf + (int64_t)kvh * (kDim / 16);
+    w.vsf = a.v_sf + (int64_t)kvh * (kDim / 16);
+    w.slots = slots + half * half_steps * kStep;
+    w.lane = lane;
+    w.hl = hl;
+    w.j = j;
+    Step buf[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) load_step(w, p, buf[p]);
+    // query: B operand of the QK MFMAs, FP16 of q * scale * log2(e); heads beyond the group are zero
+    half8_t qb[4];
+    {
+      const bool hv = hl < a.group;
+      const int head = kvh * a.group + (hv ? hl : 0);
+      const uint16_t* qp = a.q + (int64_t)row * a.q_rs + (int64_t)head * a.q_hs;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        uint4 v4 = make_uint4(0u, 0u, 0u, 0u);
+        if (hv) v4 = *reinterpret_cast<const uint4*>(qp + 32 * j + 8 * kk);
+        const uint32_t ws[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          qb[kk][2 * e] = (_Float16)(bf16_bits_to_f32(ws[e] & 0xFFFFu) * a.qscale);
+          qb[kk][2 * e + 1] = (_Float16)(bf16_bits_to_f32(ws[e] >> 16) * a.qscale);
+        }
+      }
+    }
+    const float gk = *a.gk;
+    int s0 = 0;
+    for (; s0 + P < half_steps; s0 += P) {
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        compute_step(w, s0 + p, buf[p], qb, gk, vtile, st);
+        load_step(w, s0 + p + P, buf[p]);
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p) compute_step(w, s0 + p, buf[p], qb, gk, vtile, st);
+  }
+  // the 4 lanes of a head hold disjoint key subsets of l
+  float l_tot = st.l + __shfl_xor(st.l, 16);
+  l_tot += __shfl_xor(l_tot, 32);
+
+  // 2. the second half hands (max, sum, acc) to the first through LDS
+  __syncthreads();
+  float* mg = reinterpret_cast<float*>(lds) + (wave & (kHeadsPerGroup - 1)) * 64 * 36 + lane * 36;
+  if (half == 1) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) reinterpret_cast<float4_t*>(mg)[i] = st.acc[i];
+    mg[32] = st.m;
+    mg[33] = l_tot;
+  }
+  __syncthreads();
+  if (half == 1 || !active || hl >= a.group) return;
+  {
+    const float m1 = mg[32], l1 = mg[33];
+    const float mx = fmaxf(st.m, m1);
+    const float mu = (mx == -__builtin_inff()) ? 0.0f : mx;
+    const float a0 = __builtin_amdgcn_exp2f(st.m - mu), a1 = __builtin_amdgcn_exp2f(m1 - mu);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st.acc[i] = st.acc[i] * a0 + reinterpret_cast<const float4_t*>(mg)[i] * a1;
+    l_tot = l_tot * a0 + l1 * a1;
+    st.m = mx;
+  }
+  const int head = kvh * a.group + hl;
+  if (a.splits == 1) {   // no partials: normalize and write
+    const float gv = *a.gv;
+    const float inv = l_tot > 0.0f ? gv / l_tot : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = st.acc[i][r] * inv;
+      store_out(a, row, head, 32 * j + 8 * r, v, 8);
+    }
+    if (a.lse && j == 0)
+      a.lse[(int64_t)row * a.q_heads + head] =
+          l_tot > 0.0f ? (st.m + __builtin_log2f(l_tot)) * kLn2 : -__builtin_inff();
+    return;
+  }
+  float* dst = a.part + (((int64_t)row * a.splits + split) * a.q_heads + head) * kPartStride;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    reinterpret_cast<float4_t*>(dst + 32 * j + 8 * r)[0] = float4_t{st.acc[0][r], st.acc[1][r], st.acc[2][r],
+                                                                     st.acc[3][r]};
+    reinterpret_cast<float4_t*>(dst + 32 * j + 8 * r)[1] = float4_t{st.acc[4][r], st.acc[5][r], st.acc[6][r],
+                                                                     st.acc[7][r]};
+  }
+  if (j == 0) reinterpret_cast<float4_t*>(dst + kDim)[0] = float4_t{st.m, l_tot, 0.0f, 0.0f};
+}
+
+// One wave per (row, head): merge the splits in FP32 (weights 2^(m - max m); a row without keys gives 0), apply the V
+// global scale, write the output (2 values per lane) and the natural log-sum-exp. The loads of up to 16 splits are
+// issued together.
+__global__ void __launch_bounds__(256) decode_combine_kernel(const DecodeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (unit >= (int64_t)a.rows * a.q_heads) return;
+  const int head = (int)(unit % a.q_heads);
+  const int row = (int)(unit / a.q_heads);
+  const float* base = a.part + ((int64_t)row * a.splits * a.q_heads + head) * kPartStride;
+  const int64_t sstride = (int64_t)a.q_heads * kPartStride;
+  float m_run = -__builtin_inff(), l_run = 0.0f;
+  float2_t o = float2_t{0.f, 0.f};
+  for (int s0 = 0; s0 < a.splits; s0 += 16) {
+    float2_t ml[16], x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {   // past the last split: reload the last one, weight 0 below
+      const float* pp = base + min(s0 + i, a.splits - 1) * sstride;
+      ml[i] = reinterpret_cast<const float2_t*>(pp + kDim)[0];
+      x[i] = reinterpret_cast<const float2_t*>(pp)[lane];
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (s0 + i >= a.splits) ml[i].x = -__builtin_inff();
+    float mc = m_run;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mc = fmaxf(mc, ml[i].x);
+    const float mu = (mc == -__builtin_inff()) ? 0.0f : mc;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - mu);
+    l_run *= alpha;
+    o *= alpha;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float wgt = __builtin_amdgcn_exp2f(ml[i].x - mu);
+      l_run += wgt * ml[i].y;
+      o += wgt * x[i];
+    }
+    m_run = mc;
+  }
+  const float inv = l_run > 0.0f ? *a.gv / l_run : 0.0f;
+  const float v[2] = {o.x * inv, o.y * inv};
+  store_out(a, row, head, 2 * lane, v, 2);
+  if (a.lse && lane == 0)
+    a.lse[unit] = l_run > 0.0f ? (m_run + __builtin_log2f(l_run)) * kLn2 : -__builtin_inff();
 }
 
 }  // namespace
@@ -299,8 +431,8 @@ using namespace xt;
 
 extern "C" size_t xt_sparse_decode_workspace_bytes(int rows, int q_heads, int dim, int splits) {
   if (rows < 0 || q_heads <= 0 || dim <= 0 || splits <= 0) return 0;
-  const size_t units = (size_t)rows * splits * q_heads;
-  return units * (size_t)(dim + 2) * sizeof(float) + 256;
+  if (splits == 1) return 256;
+  return (size_t)rows * splits * q_heads * (size_t)(dim + 4) * sizeof(float) + 256;
 }
 
 extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride,
@@ -331,8 +463,8 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
   if (!aligned(q, 16) || q_row_stride % 8 || q_head_stride % 8 || !aligned(out, 16) || out_row_stride % 8 ||
       out_head_stride % 8)
     return fail(XT_EINVAL, "%s: q and out rows must be 16-byte aligned (strides in elements: multiples of 8)", what);
-  if (!aligned(k_pay, 16) || !aligned(v_pay, 16) || !aligned(k_scales, 2) || !aligned(v_scales, 2))
-    return fail(XT_EINVAL, "%s: payload must be 16-byte and scales 2-byte aligned", what);
+  if (!aligned(k_pay, 16) || !aligned(v_pay, 16) || !aligned(k_scales, 4) || !aligned(v_scales, 4))
+    return fail(XT_EINVAL, "%s: payload must be 16-byte and scales 4-byte aligned", what);
   if (lse && !aligned(lse, 4)) return fail(XT_EINVAL, "%s: lse must be 4-byte aligned", what);
   const size_t need = xt_sparse_decode_workspace_bytes(rows, q_heads, dim, splits);
   if (workspace_bytes < need)
@@ -340,7 +472,10 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
   if (!aligned(workspace, 16)) return fail(XT_EINVAL, "%s: workspace must be 16-byte aligned", what);
   const int per_split = (topk + splits - 1) / splits;
   const int kps = ((per_split + kStep - 1) / kStep) * kStep;
-  const size_t lds_bytes = (size_t)kWavesPerBlock * (kps + kStep) * sizeof(int32_t);
+  const int half_steps = ((kps / kStep + kHalves * kPrefetch - 1) / (kHalves * kPrefetch)) * kPrefetch;
+  const int slot_bytes = kHalves * half_steps * kStep * (int)sizeof(int32_t);
+  size_t lds_bytes = (size_t)slot_bytes + (size_t)kWaves * kWaveLds;
+  if (lds_bytes < (size_t)kMergeLds) lds_bytes = kMergeLds;
   if (lds_bytes > 64 * 1024)
     return fail(XT_EUNSUPPORTED, "%s: %d keys per split needs %zu bytes of LDS; use more splits", what, kps,
                 lds_bytes);
@@ -359,6 +494,7 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
   a.kv_heads = kv_heads;
   a.q_heads = q_heads;
   a.group = group;
+  a.kv_groups = (kv_heads + kHeadsPerGroup - 1) / kHeadsPerGroup;
   a.table = table;
   a.table_stride = table_stride;
   a.page_size = page_size;
@@ -373,19 +509,29 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
   a.rows = rows;
   a.splits = splits;
   a.keys_per_split = kps;
-  char* ws = static_cast<char*>(workspace);
-  const size_t units = (size_t)rows * splits * q_heads;
-  a.part_acc = reinterpret_cast<float*>(ws);
-  a.part_ml = reinterpret_cast<float*>(ws + units * kDim * sizeof(float));
+  a.slot_lds_bytes = slot_bytes;
+  a.out = static_cast<uint16_t*>(out);
+  a.o_rs = out_row_stride;
+  a.o_hs = out_head_stride;
+  a.out_dtype = out_dtype;
+  a.lse = lse;
+  a.part = static_cast<float*>(workspace);
+  a.n_units = (int64_t)rows * a.kv_groups * splits;
+  // per-XCD ranges of whole rows, so that a row's splits share an XCD (with fewer than 8 rows, plain numbering keeps
+  // every XCD busy)
+  const int64_t per_row = (int64_t)a.kv_groups * splits;
+  a.xcd_map = rows >= 8;
+  a.per_xcd = ((rows + 7) / 8) * per_row;
+  const int64_t launched = a.xcd_map ? 8 * a.per_xcd : a.n_units;
+  if (launched > 0x7FFFFFFFLL) return fail(XT_EUNSUPPORTED, "%s: %lld workgroups", what, (long long)launched);
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int64_t waves = (int64_t)rows * kv_heads * splits;
-  const int64_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
-  hipLaunchKernelGGL(decode_split_kernel, dim3((unsigned)blocks), dim3(64 * kWavesPerBlock), lds_bytes, s, a);
+  hipLaunchKernelGGL(decode_split_kernel<kPrefetch>, dim3((unsigned)launched), dim3(64 * kWaves), lds_bytes, s, a);
   if (int e = check_launch(what)) return e;
-  const int64_t cwaves = (int64_t)rows * q_heads;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)((cwaves + kWavesPerBlock - 1) / kWavesPerBlock)),
-                     dim3(64 * kWavesPerBlock), 0, s, a.part_acc, a.part_ml, rows, q_heads, splits, gv,
-                     static_cast<uint16_t*>(out), out_row_stride, out_head_stride, out_dtype, lse);
-  return check_launch(what);
+  if (splits > 1) {
+    const int64_t waves = (int64_t)rows * q_heads;
+    hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, a);
+    return check_launch(what);
+  }
+  return XT_OK;
 }

@@ -48,14 +48,20 @@ def _check_raw(raw):
 
 
 def workspace(device, nbytes):
-    """A device byte buffer of at least nbytes, kept per device (allocate it before a graph capture)."""
+    """A zero-filled device byte buffer of at least nbytes, kept per device (allocate it before a graph capture).
+    The decode kernels need it zero before first use and leave it so."""
     device = torch.device(device)
     idx = device.index if device.index is not None else torch.cuda.current_device()
     buf = _workspaces.get(idx)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
         _workspaces[idx] = buf
     return buf
+
+
+def new_workspace(device, rows, q_heads, dim, splits):
+    """A dedicated zero-filled workspace for sparse_decode calls of this shape (one per stream / graph)."""
+    return torch.zeros(decode_workspace_bytes(rows, q_heads, dim, splits), dtype=torch.uint8, device=device)
 
 
 # --- NVFP4 quantization --------------------------------------------------------------------------------------------
