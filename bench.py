@@ -42,14 +42,16 @@ def cpu_model():
     return platform.processor() or 'unknown'
 
 
-def build_layer(w, gen, ops, workloads):
+def build_layer(w, gen, layout, workloads, KVPool):
+    """One layer's pool: K and V drawn as bf16 N(0,1) with 1% outlier channels x8, per-tensor global scales
+    amax / 2688, quantized on the GPU into every slot."""
+    import torch
+    pool = KVPool(w.slots, w.kv_heads, w.dim, 'cuda', layout=layout)
     k = workloads.kv_tensor(w.slots, w.kv_heads, w.dim, gen, 'cuda')
-    k_pay, k_sf, gk = ops.nvfp4_encode(k)
-    del k
     v = workloads.kv_tensor(w.slots, w.kv_heads, w.dim, gen, 'cuda')
-    v_pay, v_sf, gv = ops.nvfp4_encode(v)
-    del v
-    return (k_pay, v_pay, k_sf, v_sf, gk, gv)
+    pool.set_global_scales(k, v)
+    pool.append(k, v, torch.arange(w.slots, device='cuda'), saturate=False)
+    return pool.raw
 
 
 def cpu_baseline(raw, q, pt, idx, seq, w, scale, seconds):
@@ -102,6 +104,8 @@ def main():
     p.add_argument('--workload', default='gqa_decode_b32')
     p.add_argument('--layers', type=int, default=16)
     p.add_argument('--splits', type=int, default=None)
+    p.add_argument('--layout', default='interleaved', choices=['interleaved', 'split'],
+                   help='pool layout: interleaved (per slot [K pay | K sf | V pay | V sf]) or split (SGLang buffers)')
     p.add_argument('--cpu-seconds', type=float, default=10.0)
     p.add_argument('--no-cpu-baseline', action='store_true')
     args = p.parse_args()
@@ -113,12 +117,13 @@ def main():
     import torch
 
     from xtier_amd import ops, workloads
+    from xtier_amd.pool import KVPool
 
     w = workloads.WORKLOADS[args.workload]
     torch.cuda.set_device(0)
     gen = workloads.generator('cuda', 20261029)
     t0 = time.time()
-    layers = [build_layer(w, gen, ops, workloads) for _ in range(args.layers)]
+    layers = [build_layer(w, gen, args.layout, workloads, KVPool) for _ in range(args.layers)]
     q = (torch.randn(w.batch, w.q_heads, w.dim, generator=gen, device='cuda') * w.q_std).to(torch.bfloat16)
     pt = workloads.page_table(w.batch, w.ctx, w.page, gen, 'cuda')
     idx = workloads.index_lists(w.batch, w.ctx, w.topk, gen, 'cuda', w.index_mode)
@@ -156,7 +161,7 @@ def main():
     gbs = nbytes / (ms * 1e-3) / 1e9
     props = torch.cuda.get_device_properties(0)
     log(f'{w.name}: {ms * 1e3:.2f} us per layer-step, {gbs:.0f} GB/s algorithmic ({gbs / HBM_PEAK_GBS:.1%} of '
-        f'{HBM_PEAK_GBS:.0f}), splits {splits}, {props.multi_processor_count} CUs')
+        f'{HBM_PEAK_GBS:.0f}), splits {splits}, {args.layout} pool, {props.multi_processor_count} CUs')
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(layers[0], q, pt, idx, seq, w, scale, args.cpu_seconds)
@@ -167,7 +172,7 @@ def main():
         'vs_baseline': None, 'dtype': 'f16', 'data': 'synthetic',
         'config': {'workload': w.name, 'batch': w.batch, 'q_heads': w.q_heads, 'kv_heads': w.kv_heads,
                    'head_dim': w.dim, 'context': w.ctx, 'topk': w.topk, 'page': w.page, 'kv_format': 'nvfp4',
-                   'layers_rotated': args.layers, 'splits': splits},
+                   'layers_rotated': args.layers, 'splits': splits, 'pool_layout': args.layout},
         'us_per_layer_step': round(ms * 1e3, 3),
         'tokens_per_s': round(w.batch / (ms * 1e-3), 1),
         'hbm_frac': round(gbs / HBM_PEAK_GBS, 4),

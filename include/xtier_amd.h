@@ -9,6 +9,9 @@
  *   payload  uint8 [slots, kv_heads, dim / 2]   byte i of a head row = element 2i (bits 0-3), element 2i+1 (bits 4-7)
  *   scales   uint8 [slots, kv_heads, dim / 16]  OCP E4M3, one per 16 elements
  *   global   float [1] on the device            value = (e2m1 * e4m3) * global
+ * pay_stride / sf_stride arguments (bytes from one slot to the next; 0 = the packed values heads*dim/2 and heads*dim/16)
+ * also admit the interleaved pool of this library: per slot [K payload | K scales | V payload | V scales] in one buffer,
+ * so one key's K and V (576 bytes at 4 heads x 128) are contiguous in HBM.
  * Slot lookup: page_size 1 -> table is token-granular (SGLang req_to_token, qsa_fp4.py:135);
  *              page_size P > 1 -> table holds page ids, slot = table[pos / P] * P + pos % P.
  */
@@ -59,7 +62,8 @@ int xt_nvfp4_global_scale(const void* src, int64_t n_rows, int heads, int dim, i
  * xtier/packs/qwen4_exp/qsa_fp4.py:202-205 (fused store: xtier/packs/minimax_m3/kv_fp4.py:546-559). */
 int xt_nvfp4_quantize_append(const void* src, int64_t n_rows, int heads, int dim, int64_t src_row_stride,
                              int64_t src_head_stride, const int64_t* slots, const float* g, uint8_t* pay,
-                             uint8_t* scales, int64_t pool_slots, int saturate, xt_stream_t stream);
+                             uint8_t* scales, int64_t pool_slots, int64_t pay_stride, int64_t sf_stride, int saturate,
+                             xt_stream_t stream);
 
 /* --- QSA gather and pack (bit-exact BF16/FP16 rows) -------------------------------------------------------------- */
 
@@ -102,12 +106,13 @@ size_t xt_sparse_decode_workspace_bytes(int rows, int q_heads, int dim, int spli
  * without valid keys writing 0. lse (optional, FP32 [rows, q_heads]): natural log-sum-exp of the scaled scores,
  * -inf for an empty row. q_heads must be a multiple of kv_heads with q_heads / kv_heads <= 16; dim = 128.
  * splits: key splits per row (1..64); workspace: xt_sparse_decode_workspace_bytes(rows, q_heads, dim, splits) bytes,
- * 256-byte aligned and zero-filled before its first use; every call leaves its counter region zero again, so one
- * workspace serves any sequence of calls on one stream (calls that overlap in time need separate workspaces).
- * One launch: the last workgroup of each (row, group of 4 KV heads) merges the split partials. */
+ * 256-byte aligned and zero-filled before its first use (split partials and arrival counters; every call leaves the
+ * counters zero again; calls that overlap in time need separate workspaces). One launch on `stream`: the last
+ * workgroup of each (row, group of 4 KV heads) to finish merges the split partials. */
 int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, const uint8_t* k_pay,
                            const uint8_t* v_pay, const uint8_t* k_scales, const uint8_t* v_scales, const float* gk,
-                           const float* gv, int64_t pool_slots, int kv_heads, int q_heads, int dim,
+                           const float* gv, int64_t pool_slots, int64_t pay_stride, int64_t sf_stride, int kv_heads,
+                           int q_heads, int dim,
                            const int32_t* table, int64_t table_stride, int page_size, const int64_t* row_req,
                            const int32_t* indices, int64_t idx_stride, int topk, const int32_t* counts,
                            const int32_t* seq_lens, const int32_t* query_pos, float scale, void* out,

@@ -11,6 +11,7 @@ import torch
 from oracle import attention, nvfp4
 from tests._pools import Pool, bf16_numpy
 from xtier_amd import ops, workloads
+from xtier_amd.pool import KVPool
 
 pytestmark = pytest.mark.gpu
 MAX_ABS, MEAN_ABS = 2e-2, 2e-3
@@ -230,3 +231,18 @@ def test_decode_full_gqa_workload():
     ref, flash, _ = _oracle(raw, bf16_numpy(q), pt.cpu().numpy(), w.page, np.arange(w.batch), idx.cpu().numpy(),
                             None, seq.cpu().numpy(), scale)
     _check(out, ref, flash, strict=True)
+
+
+def test_interleaved_pool_equals_split_pool():
+    """The same bytes in the interleaved layout (one buffer, per slot [K pay | K sf | V pay | V sf]) and in SGLang's
+    four buffers give the same bits."""
+    pool, pt, idx, q = _small_case(seed=21, batch=4)
+    slots = pool.raw[0].shape[0]
+    il = KVPool(slots, 4, 128, layout='interleaved', gk=pool.raw[4].clone(), gv=pool.raw[5].clone())
+    for dst, src in zip((il.k_pay, il.v_pay, il.k_sf, il.v_sf), pool.raw[:4]):
+        dst.copy_(src)
+    assert il.k_pay.stride(0) == 576 and not il.k_pay.is_contiguous()
+    seq = torch.full((4,), 3008, dtype=torch.int32, device='cuda')
+    a = ops.sparse_decode(q.cuda(), pool.raw, pt.cuda(), idx.cuda(), seq, 0.09, page_size=64)
+    b = ops.sparse_decode(q.cuda(), il.raw, pt.cuda(), idx.cuda(), seq, 0.09, page_size=64)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))

@@ -6,6 +6,7 @@ import torch
 
 from oracle import nvfp4
 from xtier_amd import ops, workloads
+from xtier_amd.pool import KVPool
 
 pytestmark = pytest.mark.gpu
 
@@ -80,3 +81,27 @@ def test_golden_fixture():
     pay, sc, g = ops.nvfp4_encode(x.cuda())
     assert np.float32(g.item()) == data['g'][0]
     assert np.array_equal(pay.cpu().numpy(), data['pay']) and np.array_equal(sc.cpu().numpy(), data['sc'])
+
+
+@pytest.mark.parametrize('layout', ['interleaved', 'split'])
+def test_pool_append_layouts(layout):
+    """KVPool: device global scales, then K and V appended at shuffled slots; every payload / scale byte equal to the
+    oracle's in either layout, the interleaved buffer's bytes in place."""
+    n, heads, dim = 500, 4, 128
+    gen = workloads.generator('cpu', 17)
+    k = workloads.kv_tensor(n, heads, dim, gen, 'cpu')
+    v = workloads.kv_tensor(n, heads, dim, gen, 'cpu')
+    slots = torch.randperm(1024, generator=gen)[:n]
+    pool = KVPool(1024, heads, dim, layout=layout)
+    pool.set_global_scales(k.cuda(), v.cuda())
+    pool.append(k.cuda(), v.cuda(), slots.cuda())
+    for x, pay, sc, g in ((k, pool.k_pay, pool.k_sf, pool.gk), (v, pool.v_pay, pool.v_sf, pool.gv)):
+        og = nvfp4.global_scale(x.float().numpy())
+        assert np.float32(g.item()) == og
+        opay, osc = nvfp4.quantize_blocks(x.float().numpy(), og, saturate=True)
+        assert np.array_equal(pay.cpu().numpy()[slots.numpy()], opay)
+        assert np.array_equal(sc.cpu().numpy()[slots.numpy()], osc)
+    if layout == 'interleaved':
+        row = pool.buffer[slots[0]].cpu().numpy()
+        assert np.array_equal(row[:256], pool.k_pay[slots[0]].cpu().numpy().ravel())
+        assert np.array_equal(row[288:544], pool.v_pay[slots[0]].cpu().numpy().ravel())

@@ -1,6 +1,6 @@
 // Fused sparse GQA attention over the NVFP4 paged pool: gather through the page table, dequantize in registers, QK
-// and PV on MFMA (v_mfma_f32_16x16x32_f16), online softmax in the exp2 domain. Two launches: the split kernel writes
-// one partial result per (row, key split, head), the combine kernel merges them (skipped when there is one split).
+// and PV on MFMA (v_mfma_f32_16x16x32_f16), online softmax in the exp2 domain, in one launch: each workgroup writes one
+// partial result per (row, key split, head), and the last workgroup of a row to finish merges the row's partials.
 //
 // Work decomposition: a workgroup = 8 wavefronts = 4 consecutive KV heads x 2 key halves of one (query row, key
 // split); each wave owns one (row, KV head, split, half) and walks its keys in steps of 32. The workgroup computes the
@@ -53,6 +53,7 @@ struct DecodeArgs {
   const float* gk;
   const float* gv;
   int64_t pool_slots;
+  int64_t pay_stride, sf_stride;     // bytes from one slot to the next in the payload / scale buffers
   int kv_heads, q_heads, group, kv_groups;
   const int32_t* table;
   int64_t table_stride;
@@ -72,6 +73,7 @@ struct DecodeArgs {
   int out_dtype;
   float* lse;
   float* part;                       // [rows, splits, q_heads, kPartStride]: accumulators, max (log2), sum
+  int32_t* counters;                 // [rows * kv_groups] arrivals per (row, KV group); zero between launches
   int64_t n_units;                   // rows * kv_groups * splits workgroups
   int64_t per_xcd;                   // launched workgroups / 8
   int xcd_map;                       // 1: number units XCD-major (rows >= 8), 0: unit = workgroup
@@ -216,6 +218,14 @@ __device__ inline void compute_step(const WaveCtx& w, int step, const Step& d, c
   for (int i = 0; i < 8; ++i) st.acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], pb, st.acc[i], 0, 0, 0);
 }
 
+// A partial's 16-byte piece, written through to memory (sc1): visible to the merging workgroup on any XCD, whose plain
+// loads cannot hit a stale copy (no workgroup reads these addresses before the merge within a launch).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ inline void store_through(__amdgpu_buffer_rsrc_t r, int byte_off, float4_t v) {
+  const u32x4_t w = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+  __builtin_amdgcn_raw_buffer_store_b128(w, r, byte_off, 0, 16);
+}
+
 __device__ inline void store_out(const DecodeArgs& a, int row, int head, int d0, const float* v, int n) {
   uint16_t* o = a.out + (int64_t)row * a.o_rs + (int64_t)head * a.o_hs + d0;
   for (int e = 0; e < n; e += 2) {
@@ -247,6 +257,18 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   int32_t* slots = reinterpret_cast<int32_t*>(lds);
   uint8_t* vtile = lds + a.slot_lds_bytes + wave * kWaveLds;
 
+  // the query's raw words first, before any other load (loads complete in order); converted after the slot list
+  const int hl = lane & 15, j = lane >> 4;
+  const bool q_valid = active && hl < a.group;
+  uint4 qraw[4];
+  {
+    const int head = (active ? kvh : 0) * a.group + (q_valid ? hl : 0);
+    const uint16_t* qp = a.q + (int64_t)row * a.q_rs + (int64_t)head * a.q_hs;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      qraw[kk] = q_valid ? *reinterpret_cast<const uint4*>(qp + 32 * j + 8 * kk) : make_uint4(0u, 0u, 0u, 0u);
+  }
+
   // 1. the split's pool slots (-1: invalid key), shared by the workgroup's waves; each half owns a whole number of
   // prefetch groups, padded with invalid keys that compute to no-ops (P = 0, V = 0, maximum unchanged)
   const int count = a.counts ? min(a.counts[row], a.topk) : a.topk;
@@ -274,7 +296,17 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   }
   __syncthreads();
 
-  const int hl = lane & 15, j = lane >> 4;
+  // B operand of the QK MFMAs: FP16 of q * scale * log2(e); heads beyond the group are zero
+  half8_t qb[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    const uint32_t ws[4] = {qraw[kk].x, qraw[kk].y, qraw[kk].z, qraw[kk].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      qb[kk][2 * e] = (_Float16)(bf16_bits_to_f32(ws[e] & 0xFFFFu) * a.qscale);
+      qb[kk][2 * e + 1] = (_Float16)(bf16_bits_to_f32(ws[e] >> 16) * a.qscale);
+    }
+  }
   SoftmaxState st;
   st.m = -__builtin_inff();
   st.l = 0.0f;
@@ -283,8 +315,8 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
 
   if (active && half_steps > 0) {
     WaveCtx w;
-    w.row_bytes = (int64_t)a.kv_heads * (kDim / 2);
-    w.row_scales = (int64_t)a.kv_heads * (kDim / 16);
+    w.row_bytes = a.pay_stride;
+    w.row_scales = a.sf_stride;
     w.kp = a.k_pay + (int64_t)kvh * (kDim / 2);
     w.vp = a.v_pay + (int64_t)kvh * (kDim / 2);
     w.ksf = a.k_sf + (int64_t)kvh * (kDim / 16);
@@ -296,24 +328,6 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
     Step buf[P];
 #pragma unroll
     for (int p = 0; p < P; ++p) load_step(w, p, buf[p]);
-    // query: B operand of the QK MFMAs, FP16 of q * scale * log2(e); heads beyond the group are zero
-    half8_t qb[4];
-    {
-      const bool hv = hl < a.group;
-      const int head = kvh * a.group + (hv ? hl : 0);
-      const uint16_t* qp = a.q + (int64_t)row * a.q_rs + (int64_t)head * a.q_hs;
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        uint4 v4 = make_uint4(0u, 0u, 0u, 0u);
-        if (hv) v4 = *reinterpret_cast<const uint4*>(qp + 32 * j + 8 * kk);
-        const uint32_t ws[4] = {v4.x, v4.y, v4.z, v4.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          qb[kk][2 * e] = (_Float16)(bf16_bits_to_f32(ws[e] & 0xFFFFu) * a.qscale);
-          qb[kk][2 * e + 1] = (_Float16)(bf16_bits_to_f32(ws[e] >> 16) * a.qscale);
-        }
-      }
-    }
     const float gk = *a.gk;
     int s0 = 0;
     for (; s0 + P < half_steps; s0 += P) {
@@ -340,8 +354,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
     mg[33] = l_tot;
   }
   __syncthreads();
-  if (half == 1 || !active || hl >= a.group) return;
-  {
+  if (half == 0 && active && hl < a.group) {
     const float m1 = mg[32], l1 = mg[33];
     const float mx = fmaxf(st.m, m1);
     const float mu = (mx == -__builtin_inff()) ? 0.0f : mx;
@@ -353,6 +366,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   }
   const int head = kvh * a.group + hl;
   if (a.splits == 1) {   // no partials: normalize and write
+    if (half == 1 || !active || hl >= a.group) return;
     const float gv = *a.gv;
     const float inv = l_tot > 0.0f ? gv / l_tot : 0.0f;
 #pragma unroll
@@ -367,61 +381,76 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
           l_tot > 0.0f ? (st.m + __builtin_log2f(l_tot)) * kLn2 : -__builtin_inff();
     return;
   }
-  float* dst = a.part + (((int64_t)row * a.splits + split) * a.q_heads + head) * kPartStride;
+  // 3. partials of this row, written through; the last workgroup of (row, KV group) to arrive merges them
+  float* row_part = a.part + (int64_t)row * a.splits * a.q_heads * kPartStride;
+  const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+      row_part, (short)0, (int)((int64_t)a.splits * a.q_heads * kPartStride * 4), 0x00020000);
+  if (half == 0 && active && hl < a.group) {
+    const int at = ((split * a.q_heads + head) * kPartStride) * 4;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    reinterpret_cast<float4_t*>(dst + 32 * j + 8 * r)[0] = float4_t{st.acc[0][r], st.acc[1][r], st.acc[2][r],
-                                                                     st.acc[3][r]};
-    reinterpret_cast<float4_t*>(dst + 32 * j + 8 * r)[1] = float4_t{st.acc[4][r], st.acc[5][r], st.acc[6][r],
-                                                                     st.acc[7][r]};
-  }
-  if (j == 0) reinterpret_cast<float4_t*>(dst + kDim)[0] = float4_t{st.m, l_tot, 0.0f, 0.0f};
-}
-
-// One wave per (row, head): merge the splits in FP32 (weights 2^(m - max m); a row without keys gives 0), apply the V
-// global scale, write the output (2 values per lane) and the natural log-sum-exp. The loads of up to 16 splits are
-// issued together.
-__global__ void __launch_bounds__(256) decode_combine_kernel(const DecodeArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (unit >= (int64_t)a.rows * a.q_heads) return;
-  const int head = (int)(unit % a.q_heads);
-  const int row = (int)(unit / a.q_heads);
-  const float* base = a.part + ((int64_t)row * a.splits * a.q_heads + head) * kPartStride;
-  const int64_t sstride = (int64_t)a.q_heads * kPartStride;
-  float m_run = -__builtin_inff(), l_run = 0.0f;
-  float2_t o = float2_t{0.f, 0.f};
-  for (int s0 = 0; s0 < a.splits; s0 += 16) {
-    float2_t ml[16], x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {   // past the last split: reload the last one, weight 0 below
-      const float* pp = base + min(s0 + i, a.splits - 1) * sstride;
-      ml[i] = reinterpret_cast<const float2_t*>(pp + kDim)[0];
-      x[i] = reinterpret_cast<const float2_t*>(pp)[lane];
+    for (int r = 0; r < 4; ++r) {
+      store_through(pr, at + (32 * j + 8 * r) * 4, float4_t{st.acc[0][r], st.acc[1][r], st.acc[2][r], st.acc[3][r]});
+      store_through(pr, at + (32 * j + 8 * r + 4) * 4,
+                    float4_t{st.acc[4][r], st.acc[5][r], st.acc[6][r], st.acc[7][r]});
     }
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-      if (s0 + i >= a.splits) ml[i].x = -__builtin_inff();
-    float mc = m_run;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) mc = fmaxf(mc, ml[i].x);
-    const float mu = (mc == -__builtin_inff()) ? 0.0f : mc;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - mu);
-    l_run *= alpha;
-    o *= alpha;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float wgt = __builtin_amdgcn_exp2f(ml[i].x - mu);
-      l_run += wgt * ml[i].y;
-      o += wgt * x[i];
-    }
-    m_run = mc;
+    if (j == 0) store_through(pr, at + kDim * 4, float4_t{st.m, l_tot, 0.0f, 0.0f});
   }
-  const float inv = l_run > 0.0f ? *a.gv / l_run : 0.0f;
-  const float v[2] = {o.x * inv, o.y * inv};
-  store_out(a, row, head, 2 * lane, v, 2);
-  if (a.lse && lane == 0)
-    a.lse[unit] = l_run > 0.0f ? (m_run + __builtin_log2f(l_run)) * kLn2 : -__builtin_inff();
+  __builtin_amdgcn_s_waitcnt(0);   // this thread's stores have reached memory
+  __syncthreads();
+  __shared__ int32_t s_last;
+  int32_t* counter = a.counters + (int64_t)row * a.kv_groups + kvg;
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.splits - 1;
+  __syncthreads();
+  if (!s_last) return;
+  // 512 threads, 8 consecutive outputs each: head h0 + o / 128, d0 = o % 128; loads of 8 splits at a time together
+  const int h0 = kvg * kHeadsPerGroup * a.group;
+  const int nh = min(kHeadsPerGroup * a.group, a.q_heads - h0);
+  const float gv = *a.gv;
+  for (int o = threadIdx.x * 8; o < nh * kDim; o += blockDim.x * 8) {
+    const int hh = h0 + o / kDim, d0 = o % kDim;
+    const float* base = row_part + (int64_t)hh * kPartStride;
+    const int64_t sstride = (int64_t)a.q_heads * kPartStride;
+    float m_run = -__builtin_inff(), l_run = 0.0f;
+    float4_t o0 = float4_t{0.f, 0.f, 0.f, 0.f}, o1 = o0;
+    for (int s0 = 0; s0 < a.splits; s0 += 8) {
+      float4_t ml[8], x0[8], x1[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {   // past the last split: reload the last one, weight 0 below
+        const float* pp = base + min(s0 + i, a.splits - 1) * sstride;
+        ml[i] = reinterpret_cast<const float4_t*>(pp + kDim)[0];
+        x0[i] = reinterpret_cast<const float4_t*>(pp + d0)[0];
+        x1[i] = reinterpret_cast<const float4_t*>(pp + d0)[1];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (s0 + i >= a.splits) ml[i][0] = -__builtin_inff();
+      float mc = m_run;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) mc = fmaxf(mc, ml[i][0]);
+      const float mu = (mc == -__builtin_inff()) ? 0.0f : mc;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - mu);
+      l_run *= alpha;
+      o0 *= alpha;
+      o1 *= alpha;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float wgt = __builtin_amdgcn_exp2f(ml[i][0] - mu);
+        l_run += wgt * ml[i][1];
+        o0 += wgt * x0[i];
+        o1 += wgt * x1[i];
+      }
+      m_run = mc;
+    }
+    const float inv = l_run > 0.0f ? gv / l_run : 0.0f;
+    const float v[8] = {o0[0] * inv, o0[1] * inv, o0[2] * inv, o0[3] * inv,
+                        o1[0] * inv, o1[1] * inv, o1[2] * inv, o1[3] * inv};
+    store_out(a, row, hh, d0, v, 8);
+    if (a.lse && d0 == 0)
+      a.lse[(int64_t)row * a.q_heads + hh] =
+          l_run > 0.0f ? (m_run + __builtin_log2f(l_run)) * kLn2 : -__builtin_inff();
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
@@ -429,16 +458,20 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(const DecodeArgs a)
 
 using namespace xt;
 
+// Workspace: [counters: rows * q_heads int32 (an upper bound of rows * KV groups), padded to 256 B][partials]
+static size_t counter_bytes(int rows, int q_heads) { return (((size_t)rows * q_heads * 4 + 255) / 256) * 256; }
+
 extern "C" size_t xt_sparse_decode_workspace_bytes(int rows, int q_heads, int dim, int splits) {
   if (rows < 0 || q_heads <= 0 || dim <= 0 || splits <= 0) return 0;
   if (splits == 1) return 256;
-  return (size_t)rows * splits * q_heads * (size_t)(dim + 4) * sizeof(float) + 256;
+  return counter_bytes(rows, q_heads) + (size_t)rows * splits * q_heads * (size_t)(dim + 4) * sizeof(float);
 }
 
 extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride,
                                       const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_scales,
                                       const uint8_t* v_scales, const float* gk, const float* gv, int64_t pool_slots,
-                                      int kv_heads, int q_heads, int dim, const int32_t* table, int64_t table_stride,
+                                      int64_t pay_stride, int64_t sf_stride, int kv_heads, int q_heads, int dim,
+                                      const int32_t* table, int64_t table_stride,
                                       int page_size, const int64_t* row_req, const int32_t* indices,
                                       int64_t idx_stride, int topk, const int32_t* counts, const int32_t* seq_lens,
                                       const int32_t* query_pos, float scale, void* out, int64_t out_row_stride,
@@ -463,13 +496,19 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
   if (!aligned(q, 16) || q_row_stride % 8 || q_head_stride % 8 || !aligned(out, 16) || out_row_stride % 8 ||
       out_head_stride % 8)
     return fail(XT_EINVAL, "%s: q and out rows must be 16-byte aligned (strides in elements: multiples of 8)", what);
+  if (pay_stride == 0) pay_stride = (int64_t)kv_heads * (dim / 2);
+  if (sf_stride == 0) sf_stride = (int64_t)kv_heads * (dim / 16);
+  if (pay_stride < (int64_t)kv_heads * (dim / 2) || sf_stride < (int64_t)kv_heads * (dim / 16) || pay_stride % 16 ||
+      sf_stride % 4)
+    return fail(XT_EINVAL, "%s: slot strides %lld / %lld bytes must hold the heads' payload / scales and be multiples "
+                "of 16 / 4", what, (long long)pay_stride, (long long)sf_stride);
   if (!aligned(k_pay, 16) || !aligned(v_pay, 16) || !aligned(k_scales, 4) || !aligned(v_scales, 4))
     return fail(XT_EINVAL, "%s: payload must be 16-byte and scales 4-byte aligned", what);
   if (lse && !aligned(lse, 4)) return fail(XT_EINVAL, "%s: lse must be 4-byte aligned", what);
   const size_t need = xt_sparse_decode_workspace_bytes(rows, q_heads, dim, splits);
   if (workspace_bytes < need)
     return fail(XT_EWORKSPACE, "%s: workspace %zu bytes < %zu needed", what, workspace_bytes, need);
-  if (!aligned(workspace, 16)) return fail(XT_EINVAL, "%s: workspace must be 16-byte aligned", what);
+  if (!aligned(workspace, 256)) return fail(XT_EINVAL, "%s: workspace must be 256-byte aligned", what);
   const int per_split = (topk + splits - 1) / splits;
   const int kps = ((per_split + kStep - 1) / kStep) * kStep;
   const int half_steps = ((kps / kStep + kHalves * kPrefetch - 1) / (kHalves * kPrefetch)) * kPrefetch;
@@ -491,6 +530,8 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
   a.gk = gk;
   a.gv = gv;
   a.pool_slots = pool_slots;
+  a.pay_stride = pay_stride;
+  a.sf_stride = sf_stride;
   a.kv_heads = kv_heads;
   a.q_heads = q_heads;
   a.group = group;
@@ -515,7 +556,8 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
   a.o_hs = out_head_stride;
   a.out_dtype = out_dtype;
   a.lse = lse;
-  a.part = static_cast<float*>(workspace);
+  a.counters = static_cast<int32_t*>(workspace);
+  a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + counter_bytes(rows, q_heads));
   a.n_units = (int64_t)rows * a.kv_groups * splits;
   // per-XCD ranges of whole rows, so that a row's splits share an XCD (with fewer than 8 rows, plain numbering keeps
   // every XCD busy)
@@ -525,13 +567,7 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
   const int64_t launched = a.xcd_map ? 8 * a.per_xcd : a.n_units;
   if (launched > 0x7FFFFFFFLL) return fail(XT_EUNSUPPORTED, "%s: %lld workgroups", what, (long long)launched);
 
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(decode_split_kernel<kPrefetch>, dim3((unsigned)launched), dim3(64 * kWaves), lds_bytes, s, a);
-  if (int e = check_launch(what)) return e;
-  if (splits > 1) {
-    const int64_t waves = (int64_t)rows * q_heads;
-    hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, a);
-    return check_launch(what);
-  }
-  return XT_OK;
+  hipLaunchKernelGGL(decode_split_kernel<kPrefetch>, dim3((unsigned)launched), dim3(64 * kWaves), lds_bytes,
+                     reinterpret_cast<hipStream_t>(stream), a);
+  return check_launch(what);
 }

@@ -30,14 +30,21 @@ def _need_cuda(*tensors):
             raise ValueError('xtier_amd: GPU tensors expected')
 
 
-def _check_raw(raw):
-    """The reference's _check (qsa_fp4.py:165-171): contiguous packed rows with a power-of-2 head size."""
+def _check_raw(raw, contiguous=True):
+    """The reference's _check (qsa_fp4.py:165-171): packed [m, heads, dim/2] rows with a power-of-2 head size.
+    contiguous=False also admits pools whose slots are strided (the interleaved layout of KVPool): each head row
+    packed, the slot stride the same for K and V."""
     k, v, k_sf, v_sf, gk, gv = raw
     if k_sf is None:
         raise NotImplementedError('xtier_amd: FP8 pools are not covered; NVFP4 pools only')
     dim = k.shape[2] * 2
-    if not (k.is_contiguous() and v.is_contiguous() and k_sf.is_contiguous() and v_sf.is_contiguous()
-            and dim % 32 == 0 and dim & (dim - 1) == 0):
+    if contiguous:
+        packed = k.is_contiguous() and v.is_contiguous() and k_sf.is_contiguous() and v_sf.is_contiguous()
+    else:
+        packed = (all(t.dim() == 3 and t.stride(2) == 1 and t.stride(1) == t.shape[2] for t in (k, v, k_sf, v_sf))
+                  and k.stride(0) == v.stride(0) and k_sf.stride(0) == v_sf.stride(0)
+                  and k.shape == v.shape and k_sf.shape == v_sf.shape and k_sf.shape[2] * 8 == k.shape[2])
+    if not (packed and dim % 32 == 0 and dim & (dim - 1) == 0):
         raise ValueError(f'xtier qsa_fp4: packed [m, heads, dim / 2] rows with a power-of-2 head size expected, got '
                          f'{tuple(k.shape)}')
     if k.dtype != torch.uint8:
@@ -49,7 +56,7 @@ def _check_raw(raw):
 
 def workspace(device, nbytes):
     """A zero-filled device byte buffer of at least nbytes, kept per device (allocate it before a graph capture).
-    The decode kernels need it zero before first use and leave it so."""
+    The decode kernels need their workspace zero before first use and leave it so."""
     device = torch.device(device)
     idx = device.index if device.index is not None else torch.cuda.current_device()
     buf = _workspaces.get(idx)
@@ -90,9 +97,12 @@ def quantize_append(x, slots, g, pay, scales, saturate=True):
     if slots.dtype != torch.int64:
         slots = slots.to(torch.int64)
     slots = slots.contiguous()
+    if pay.stride(-1) != 1 or scales.stride(-1) != 1 or pay.dtype != torch.uint8 or scales.dtype != torch.uint8:
+        raise ValueError('xtier_amd.quantize_append: uint8 payload / scale views with packed head rows expected')
     _lib.check(_lib.lib().xt_nvfp4_quantize_append(
         _ptr(x), x.shape[0], x.shape[1], x.shape[2], x.stride(0), x.stride(1), _ptr(slots), _ptr(g),
-        _ptr(pay), _ptr(scales), pay.shape[0], 1 if saturate else 0, _stream(x)), 'quantize_append')
+        _ptr(pay), _ptr(scales), pay.shape[0], pay.stride(0), scales.stride(0), 1 if saturate else 0, _stream(x)),
+        'quantize_append')
 
 
 def nvfp4_encode(x, saturate=False):
@@ -164,7 +174,7 @@ def sparse_decode(q, raw, table, indices, seq_lens, scale, page_size=1, row_req=
     indices [rows, topk] (int32; valid: column < counts[r], 0 <= pos < seq_lens[r], pos <= query_pos[r] when given),
     resolved through ``table`` (token-granular req_to_token for page_size 1, else a page table) row row_req[r].
     Returns out [rows, q_heads, dim] (BF16 unless ``out`` is given); lse [rows, q_heads] FP32 is filled if given."""
-    raw, kv_heads, dim = _check_raw(raw)
+    raw, kv_heads, dim = _check_raw(raw, contiguous=False)
     rows, q_heads, qdim = q.shape
     if qdim != dim:
         raise ValueError(f'xtier_amd.sparse_decode: q head size {qdim} != pool head size {dim}')
@@ -186,7 +196,8 @@ def sparse_decode(q, raw, table, indices, seq_lens, scale, page_size=1, row_req=
     if ws is None:
         ws = workspace(q.device, need)
     _lib.check(_lib.lib().xt_sparse_decode_nvfp4(
-        _ptr(q), q.stride(0), q.stride(1), *map(_ptr, raw), raw[0].shape[0], kv_heads, q_heads, dim, _ptr(table),
+        _ptr(q), q.stride(0), q.stride(1), *map(_ptr, raw), raw[0].shape[0], raw[0].stride(0), raw[2].stride(0),
+        kv_heads, q_heads, dim, _ptr(table),
         table.stride(0), int(page_size), _ptr(row_req), _ptr(indices), indices.stride(0), topk, _ptr(counts),
         _ptr(seq_lens), _ptr(query_pos), float(scale), _ptr(out), out.stride(0), out.stride(1), _DTYPES[out.dtype],
         _ptr(lse), rows, int(splits), _ptr(ws), ws.numel(), _stream(q)), 'sparse_decode')

@@ -1,0 +1,59 @@
+"""A layer's paged NVFP4 KV pool in HBM, in either of two layouts:
+
+- 'interleaved' (this library's layout): one uint8 buffer [slots, 2 * heads * (dim/2 + dim/16)], each slot holding
+  [K payload | K scales | V payload | V scales]. A key's K and V (576 bytes at 4 heads x 128) are contiguous, so a
+  sparse gather reads one burst per key instead of four scattered ones (two payload rows and two 32-byte scale rows).
+- 'split': SGLang's NVFP4 pool buffers (xtier/packs/qwen4_exp/qsa_fp4.py:43-58): k, v uint8 [slots, heads, dim/2] and
+  k_sf, v_sf uint8 [slots, heads, dim/16], each contiguous.
+
+Either way ``raw`` is the reference's tuple (k_pay, v_pay, k_scales, v_scales, gk, gv), the payload and scale entries
+being strided uint8 views, which every entry point of xtier_amd.ops accepts.
+"""
+import torch
+
+from . import ops
+
+
+class KVPool:
+    def __init__(self, slots, kv_heads, dim, device='cuda', layout='interleaved', gk=None, gv=None):
+        if dim % 32 or dim & (dim - 1):
+            raise ValueError(f'head size {dim}: a power of 2, multiple of 32 expected')
+        self.slots, self.kv_heads, self.dim, self.layout = slots, kv_heads, dim, layout
+        half, blocks = kv_heads * dim // 2, kv_heads * dim // 16
+        device = torch.device(device)
+        if layout == 'interleaved':
+            width = 2 * (half + blocks)
+            self.buffer = torch.zeros(slots, width, dtype=torch.uint8, device=device)
+            view = lambda off, n, w: self.buffer[:, off:off + n].unflatten(1, (kv_heads, w))
+            self.k_pay = view(0, half, dim // 2)
+            self.k_sf = view(half, blocks, dim // 16)
+            self.v_pay = view(half + blocks, half, dim // 2)
+            self.v_sf = view(2 * half + blocks, blocks, dim // 16)
+        elif layout == 'split':
+            self.buffer = None
+            self.k_pay = torch.zeros(slots, kv_heads, dim // 2, dtype=torch.uint8, device=device)
+            self.v_pay = torch.zeros_like(self.k_pay)
+            self.k_sf = torch.zeros(slots, kv_heads, dim // 16, dtype=torch.uint8, device=device)
+            self.v_sf = torch.zeros_like(self.k_sf)
+        else:
+            raise ValueError(f'layout {layout!r}')
+        one = lambda: torch.ones(1, dtype=torch.float32, device=device)
+        self.gk = gk if gk is not None else one()
+        self.gv = gv if gv is not None else one()
+
+    @property
+    def raw(self):
+        return (self.k_pay, self.v_pay, self.k_sf, self.v_sf, self.gk, self.gv)
+
+    def nbytes(self):
+        return sum(t.numel() for t in (self.k_pay, self.v_pay, self.k_sf, self.v_sf))
+
+    def set_global_scales(self, k, v):
+        """The per-tensor global scales amax / (6 * 448) of K and V (formats.py:122), computed on the device."""
+        ops.global_scale(k, out=self.gk)
+        ops.global_scale(v, out=self.gv)
+
+    def append(self, k, v, slots, saturate=True):
+        """NVFP4 quantize-on-append of K and V rows [n, kv_heads, dim] (BF16) at pool slots [n]."""
+        ops.quantize_append(k, slots, self.gk, self.k_pay, self.k_sf, saturate=saturate)
+        ops.quantize_append(v, slots, self.gv, self.v_pay, self.v_sf, saturate=saturate)
