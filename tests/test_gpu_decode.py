@@ -210,9 +210,31 @@ def test_graph_replay_equals_eager():
         assert torch.equal(replayed.view(torch.int16), eager.view(torch.int16))
 
 
-def test_decode_full_gqa_workload():
+@pytest.mark.parametrize('heads,qh,batch,ctx,topk,splits', [
+    (1, 16, 5, 3008, 700, 3),    # one KV head, group 16: one head per workgroup
+    (2, 32, 4, 3008, 700, 1),
+    (6, 24, 3, 3008, 700, 2),    # KV heads not a multiple of 4
+    (8, 64, 40, 512, 300, 8),    # 4 heads per workgroup, 2 head groups per row
+    (12, 48, 32, 512, 300, 8),   # 4 heads per workgroup, 3 head groups
+    (4, 32, 64, 512, 300, 4),    # 4 heads per workgroup with cross-workgroup partials
+])
+def test_decode_head_layouts(heads, qh, batch, ctx, topk, splits):
+    """KV head counts and GQA groups over both workgroup shapes (4 KV heads x 2 key slices for many rows, 1 KV head x
+    8 slices for few) and with or without key splits."""
+    pool, pt, idx, q = _small_case(seed=heads * 100 + batch, batch=batch, ctx=ctx, heads=heads, qh=qh, topk=topk)
+    seq = np.full(batch, ctx, np.int32)
+    out = ops.sparse_decode(q.cuda(), pool.raw, pt.cuda(), idx.cuda(), _dev(seq), 0.0884, page_size=64,
+                            splits=splits)
+    ref, flash, _ = _oracle(pool.raw, bf16_numpy(q), pt.numpy(), 64, np.arange(batch), idx.numpy(), None, seq,
+                            0.0884)
+    _check(out, ref, flash)
+
+
+@pytest.mark.parametrize('splits', [1, 8])
+def test_decode_full_gqa_workload(splits):
     """Batch 32, 32 q / 4 KV heads, context 32768, top-2048 over a 1M-slot pool built on the GPU: every row against
-    the oracle on the pool bytes the GPU wrote."""
+    the oracle on the pool bytes the GPU wrote (one key split: 1 KV head per workgroup, 8 slices merged in LDS; 8
+    splits: 4 KV heads per workgroup and cross-workgroup partials)."""
     w = workloads.WORKLOADS['gqa_decode_b32']
     gen = workloads.generator('cuda', 20261029)
     k = workloads.kv_tensor(w.slots, w.kv_heads, w.dim, gen, 'cuda')
@@ -227,7 +249,7 @@ def test_decode_full_gqa_workload():
     idx = workloads.index_lists(w.batch, w.ctx, w.topk, gen, 'cuda')
     seq = torch.full((w.batch,), w.ctx, dtype=torch.int32, device='cuda')
     scale = 1 / math.sqrt(w.dim)
-    out = ops.sparse_decode(q, raw, pt, idx, seq, scale, page_size=w.page)
+    out = ops.sparse_decode(q, raw, pt, idx, seq, scale, page_size=w.page, splits=splits)
     ref, flash, _ = _oracle(raw, bf16_numpy(q), pt.cpu().numpy(), w.page, np.arange(w.batch), idx.cpu().numpy(),
                             None, seq.cpu().numpy(), scale)
     _check(out, ref, flash, strict=True)

@@ -1,12 +1,14 @@
 // Fused sparse GQA attention over the NVFP4 paged pool: gather through the page table, dequantize in registers, QK
-// and PV on MFMA (v_mfma_f32_16x16x32_f16), online softmax in the exp2 domain, in one launch: each workgroup writes one
-// partial result per (row, key split, head), and the last workgroup of a row to finish merges the row's partials.
+// and PV on MFMA (v_mfma_f32_16x16x32_f16), online softmax in the exp2 domain, in one launch. With one key split per
+// row a workgroup writes its heads' outputs directly; with several, each workgroup writes one partial result per
+// (row, key split, head), and the last workgroup of a (row, KV head group) to finish merges them.
 //
-// Work decomposition: a workgroup = 8 wavefronts = 4 consecutive KV heads x 2 key halves of one (query row, key
-// split); each wave owns one (row, KV head, split, half) and walks its keys in steps of 32. The workgroup computes the
-// split's pool slots once into LDS, and merges the two halves of each head through LDS before writing the partial.
-// Workgroups are numbered so that all splits of a row run on the same XCD (round-robin dispatch puts workgroup g on
-// XCD g % 8): their K/V pages and partials share one L2.
+// Work decomposition: a workgroup = 8 wavefronts = HPW consecutive KV heads x 8 / HPW key slices of one (query row,
+// key split), HPW = 4 (many rows) or 1 (few rows: more workgroups); each wave owns one (row, KV head, split, slice)
+// and walks its keys in steps of 32. The workgroup computes the split's pool slots once into LDS and merges the
+// slices of each head through LDS (a tree of log2(8 / HPW) rounds). Workgroups are numbered so that all units of a row
+// run on the same XCD (round-robin dispatch puts workgroup g on XCD g % 8): their K/V lines, which hold several
+// heads, and their partials share one L2.
 //
 // Memory pipeline: per step a wave issues 6 loads (K and V payload as 16-byte row pieces, K and V scales as one dword
 // per lane) and keeps P steps in flight in a register ring. V is transposed for the PV operand through a padded LDS
@@ -33,15 +35,14 @@ namespace {
 
 constexpr int kDim = 128;          // head size: 64 payload bytes, 8 scale bytes per head row
 constexpr int kStep = 32;          // keys per step
-constexpr int kHeadsPerGroup = 4;  // KV heads per workgroup
-constexpr int kHalves = 2;         // key halves per workgroup
-constexpr int kWaves = kHeadsPerGroup * kHalves;
+constexpr int kWaves = 8;          // wavefronts per workgroup: HPW KV heads x (8 / HPW) key slices
 constexpr int kVRow = 80;          // LDS bytes per key in the V transpose tile (64 + 16: no bank conflicts)
 constexpr int kWaveLds = kStep * kVRow + kStep * 8;   // V tile + V scale tile per wave
 constexpr int kPrefetch = 4;       // steps of loads in flight per wave
+constexpr int kSlotBatch = 4;      // keys per thread whose index / table loads are in flight together
 constexpr float kRescale = 8.0f;   // log2 of the largest P before the running maximum is raised
 constexpr int kPartStride = kDim + 4;   // floats per partial (split, head): 128 accumulators, max, sum, 2 pad
-constexpr int kMergeLds = kHeadsPerGroup * 64 * 36 * 4;   // a half's (acc, max, sum) per lane for 4 waves
+constexpr int kMergeLds = (kWaves / 2) * 64 * 36 * 4;   // (acc, max, sum) per lane of the 4 waves handing over
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -58,6 +59,7 @@ struct DecodeArgs {
   const int32_t* table;
   int64_t table_stride;
   int page_size;
+  int page_shift;                    // log2(page_size) for a power of 2, else -1
   const int64_t* row_req;
   const int32_t* indices;
   int64_t idx_stride;
@@ -67,16 +69,16 @@ struct DecodeArgs {
   const int32_t* query_pos;
   float qscale;                      // softmax scale * log2(e)
   int rows, splits, keys_per_split;  // keys_per_split: a multiple of kStep
-  int slot_lds_bytes;                // LDS bytes of the slot list (padded to whole prefetch groups per half)
+  int slot_lds_bytes;                // LDS bytes of the slot list (padded to whole prefetch groups per slice)
   uint16_t* out;
   int64_t o_rs, o_hs;
   int out_dtype;
   float* lse;
   float* part;                       // [rows, splits, q_heads, kPartStride]: accumulators, max (log2), sum
   int32_t* counters;                 // [rows * kv_groups] arrivals per (row, KV group); zero between launches
-  int64_t n_units;                   // rows * kv_groups * splits workgroups
-  int64_t per_xcd;                   // launched workgroups / 8
-  int xcd_map;                       // 1: number units XCD-major (rows >= 8), 0: unit = workgroup
+  int64_t n_units;                   // rows * kv_groups * splits workgroups, one per unit
+  uint32_t xcd_units;                // n_units / 8
+  uint32_t xcd_extra;                // n_units % 8
 };
 
 struct Step {
@@ -85,6 +87,11 @@ struct Step {
   uint32_t ks;   // K scale bytes 4*(lane&1) .. +3 of key lane/2
   uint32_t vs;   // V scale bytes, same
 };
+
+// A load through the scalar cache (the constant address space) of memory no launch writes: uniform per-row values.
+__device__ inline int32_t scalar_load(const int32_t* p) {
+  return *(const __attribute__((address_space(4))) int32_t*)(p);
+}
 
 __device__ inline int key_of(int j, int e) { return (e < 4) ? (4 * j + e) : (16 + 4 * j + (e - 4)); }
 
@@ -238,60 +245,109 @@ __device__ inline void store_out(const DecodeArgs& a, int row, int head, int d0,
   }
 }
 
-template <int P>
+// HPW: KV heads per workgroup (4 or 1); the workgroup's 8 / HPW key slices of each head merge through LDS.
+template <int P, int HPW>
 __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
+  constexpr int kSlices = kWaves / HPW;
   extern __shared__ __align__(16) uint8_t lds[];
-  // XCD-aware numbering: launched workgroup g runs on XCD g % 8; unit u = (g % 8) * per_xcd + g / 8 keeps a row's
-  // consecutive units (its splits) on one XCD.
-  const int64_t g = blockIdx.x;
-  const int64_t u = a.xcd_map ? (g % 8) * a.per_xcd + g / 8 : g;
-  if (u >= a.n_units) return;   // uniform over the workgroup
-  const int split = (int)(u % a.splits);
-  const int kvg = (int)((u / a.splits) % a.kv_groups);
-  const int row = (int)(u / ((int64_t)a.splits * a.kv_groups));
+  // XCD-aware numbering: workgroup g runs on XCD g % 8 (round-robin dispatch); XCD x takes the contiguous unit range
+  // starting at x * (n / 8) + min(x, n % 8), so a row's units (its heads and splits) share one L2. A bijection on
+  // [0, n): no padding workgroups and no early exit, so the argument loads below issue together.
+  // The arguments of the prologue and the slot phase are read by an empty asm first: their scalar loads then issue
+  // together behind one wait, instead of one round trip each where the compiler would place them next to their uses.
+  asm volatile("" ::"s"(a.xcd_units), "s"(a.xcd_extra), "s"(a.splits), "s"(a.kv_groups), "s"(a.kv_heads),
+               "s"(a.group), "s"(a.keys_per_split), "s"(a.topk), "s"(a.q), "s"(a.q_rs), "s"(a.q_hs), "s"(a.indices),
+               "s"(a.idx_stride), "s"(a.counts), "s"(a.seq_lens), "s"(a.query_pos), "s"(a.row_req), "s"(a.table),
+               "s"(a.table_stride), "s"(a.page_shift), "s"(a.page_size), "s"(a.pool_slots));
+  const uint32_t g = blockIdx.x;
+  const uint32_t xcd = g & 7u;
+  const uint32_t u = xcd * a.xcd_units + min(xcd, a.xcd_extra) + (g >> 3);
+  const uint32_t splits_u = (uint32_t)a.splits, groups_u = (uint32_t)a.kv_groups;
+  const int split = (int)(u % splits_u);
+  const int kvg = (int)((u / splits_u) % groups_u);
+  const int row = (int)(u / splits_u / groups_u);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int kvh = kvg * kHeadsPerGroup + (wave & (kHeadsPerGroup - 1));
-  const int half = wave / kHeadsPerGroup;
+  const int kvh = kvg * HPW + (wave % HPW);
+  const int slice = wave / HPW;
   const bool active = kvh < a.kv_heads;
 
   int32_t* slots = reinterpret_cast<int32_t*>(lds);
   uint8_t* vtile = lds + a.slot_lds_bytes + wave * kWaveLds;
 
-  // the query's raw words first, before any other load (loads complete in order); converted after the slot list
+  // the query's raw words first (loads complete in order); every lane reads a valid address and heads outside the
+  // group are zeroed at conversion, so the loads carry no branch
   const int hl = lane & 15, j = lane >> 4;
   const bool q_valid = active && hl < a.group;
   uint4 qraw[4];
   {
-    const int head = (active ? kvh : 0) * a.group + (q_valid ? hl : 0);
+    const int head = min(kvh, a.kv_heads - 1) * a.group + min(hl, a.group - 1);
     const uint16_t* qp = a.q + (int64_t)row * a.q_rs + (int64_t)head * a.q_hs;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-      qraw[kk] = q_valid ? *reinterpret_cast<const uint4*>(qp + 32 * j + 8 * kk) : make_uint4(0u, 0u, 0u, 0u);
+    for (int kk = 0; kk < 4; ++kk) qraw[kk] = *reinterpret_cast<const uint4*>(qp + 32 * j + 8 * kk);
   }
 
-  // 1. the split's pool slots (-1: invalid key), shared by the workgroup's waves; each half owns a whole number of
-  // prefetch groups, padded with invalid keys that compute to no-ops (P = 0, V = 0, maximum unchanged)
-  const int count = a.counts ? min(a.counts[row], a.topk) : a.topk;
+  // 1. the split's pool slots (-1: invalid key), shared by the workgroup's waves; each slice owns a whole number of
+  // prefetch groups, padded with invalid keys that compute to no-ops (P = 0, V = 0, maximum unchanged). The first
+  // kSlotBatch * 512 index loads go out before the row's count, length and table row are read (they need only launch
+  // constants), so the chain to the first K/V load is two dependent loads: index, then table.
   const int t0 = split * a.keys_per_split;
+  const int kmax = max(0, min(a.keys_per_split, a.topk - t0));
+  const int32_t* ip = a.indices + (int64_t)row * a.idx_stride + t0;
+  int32_t pos[kSlotBatch];
+#pragma unroll
+  for (int b = 0; b < kSlotBatch; ++b) {
+    const int i = b * 512 + (int)threadIdx.x;
+    pos[b] = (i < kmax) ? ip[i] : -1;
+  }
+  // the row's count, length, causal limit and table row: scalar loads from addresses valid whether or not the
+  // optional arrays are given (a missing one reads the row's length and is ignored), so none waits in a branch
+  const int32_t* len_p = a.seq_lens + row;
+  const int32_t* req_p = a.row_req ? reinterpret_cast<const int32_t*>(a.row_req + row) : len_p;
+  int32_t len_v = scalar_load(len_p);
+  int32_t cnt_v = scalar_load(a.counts ? a.counts + row : len_p);
+  int32_t qpos_v = scalar_load(a.query_pos ? a.query_pos + row : len_p);
+  int32_t req_lo = scalar_load(req_p), req_hi = scalar_load(a.row_req ? req_p + 1 : len_p);
+  // every use below follows this asm, so the five loads issue together behind one wait
+  asm volatile("" : "+s"(len_v), "+s"(cnt_v), "+s"(qpos_v), "+s"(req_lo), "+s"(req_hi));
+  const int count = a.counts ? min(cnt_v, a.topk) : a.topk;
   const int n = max(0, min(t0 + a.keys_per_split, count) - t0);
-  const int half_steps = (((n + kStep - 1) / kStep + kHalves * P - 1) / (kHalves * P)) * P;
+  const int slice_steps = (((n + kStep - 1) / kStep + kSlices * P - 1) / (kSlices * P)) * P;
   {
-    const int32_t seqlen = a.seq_lens[row];
-    const int32_t qpos = a.query_pos ? a.query_pos[row] : 0x7FFFFFFF;
-    const int64_t trow = a.row_req ? a.row_req[row] : row;
+    const int32_t seqlen = len_v;
+    const int32_t qpos = a.query_pos ? qpos_v : 0x7FFFFFFF;
+    const int64_t trow = a.row_req ? (int64_t)(((uint64_t)(uint32_t)req_hi << 32) | (uint32_t)req_lo) : row;
     const int32_t* tp = a.table + trow * a.table_stride;
-    const int32_t* ip = a.indices + (int64_t)row * a.idx_stride + t0;
-    for (int i = threadIdx.x; i < kHalves * half_steps * kStep; i += blockDim.x) {
-      int32_t slot = -1;
-      if (i < n) {
-        const int32_t pos = ip[i];
-        if (pos >= 0 && pos < seqlen && pos <= qpos) {
-          const int64_t sl = (a.page_size == 1) ? (int64_t)tp[pos]
-                                                : (int64_t)tp[pos / a.page_size] * a.page_size + pos % a.page_size;
-          if (sl >= 0 && sl < a.pool_slots) slot = (int32_t)sl;
-        }
+    const int total = kSlices * slice_steps * kStep;
+    for (int i0 = 0;;) {
+      // validity and table offsets of all kSlotBatch keys first, then their table loads back to back (a use of an
+      // index between two table loads would wait for the earlier table load too)
+      bool ok[kSlotBatch];
+      int32_t toff[kSlotBatch], ent[kSlotBatch];
+#pragma unroll
+      for (int b = 0; b < kSlotBatch; ++b) {
+        const int i = i0 + b * 512 + (int)threadIdx.x;
+        ok[b] = i < n && pos[b] >= 0 && pos[b] < seqlen && pos[b] <= qpos;
+        toff[b] = a.page_shift >= 0 ? (pos[b] >> a.page_shift) : pos[b] / a.page_size;
       }
-      slots[i] = slot;
+#pragma unroll
+      for (int b = 0; b < kSlotBatch; ++b) ent[b] = ok[b] ? tp[toff[b]] : -1;
+#pragma unroll
+      for (int b = 0; b < kSlotBatch; ++b) {
+        const int i = i0 + b * 512 + (int)threadIdx.x;
+        int32_t slot = -1;
+        if (ok[b] && ent[b] >= 0) {
+          const int64_t sl = (int64_t)ent[b] * a.page_size + (pos[b] - toff[b] * a.page_size);
+          if (sl < a.pool_slots) slot = (int32_t)sl;
+        }
+        if (i < total) slots[i] = slot;
+      }
+      i0 += kSlotBatch * 512;
+      if (i0 >= total) break;
+#pragma unroll
+      for (int b = 0; b < kSlotBatch; ++b) {   // splits longer than kSlotBatch * 512 keys
+        const int i = i0 + b * 512 + (int)threadIdx.x;
+        pos[b] = (i < kmax) ? ip[i] : -1;
+      }
     }
   }
   __syncthreads();
@@ -300,7 +356,8 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   half8_t qb[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
-    const uint32_t ws[4] = {qraw[kk].x, qraw[kk].y, qraw[kk].z, qraw[kk].w};
+    const uint32_t ws[4] = {q_valid ? qraw[kk].x : 0u, q_valid ? qraw[kk].y : 0u, q_valid ? qraw[kk].z : 0u,
+                            q_valid ? qraw[kk].w : 0u};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       qb[kk][2 * e] = (_Float16)(bf16_bits_to_f32(ws[e] & 0xFFFFu) * a.qscale);
@@ -313,7 +370,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) st.acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  if (active && half_steps > 0) {
+  if (active && slice_steps > 0) {
     WaveCtx w;
     w.row_bytes = a.pay_stride;
     w.row_scales = a.sf_stride;
@@ -321,7 +378,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
     w.vp = a.v_pay + (int64_t)kvh * (kDim / 2);
     w.ksf = a.k_sf + (int64_t)kvh * (kDim / 16);
     w.vsf = a.v_sf + (int64_t)kvh * (kDim / 16);
-    w.slots = slots + half * half_steps * kStep;
+    w.slots = slots + slice * slice_steps * kStep;
     w.lane = lane;
     w.hl = hl;
     w.j = j;
@@ -330,7 +387,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
     for (int p = 0; p < P; ++p) load_step(w, p, buf[p]);
     const float gk = *a.gk;
     int s0 = 0;
-    for (; s0 + P < half_steps; s0 += P) {
+    for (; s0 + P < slice_steps; s0 += P) {
 #pragma unroll
       for (int p = 0; p < P; ++p) {
         compute_step(w, s0 + p, buf[p], qb, gk, vtile, st);
@@ -344,29 +401,35 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   float l_tot = st.l + __shfl_xor(st.l, 16);
   l_tot += __shfl_xor(l_tot, 32);
 
-  // 2. the second half hands (max, sum, acc) to the first through LDS
-  __syncthreads();
-  float* mg = reinterpret_cast<float*>(lds) + (wave & (kHeadsPerGroup - 1)) * 64 * 36 + lane * 36;
-  if (half == 1) {
+  // 2. tree merge of the slices through LDS: in each round the upper half of the remaining slices hands
+  // (acc, max, sum) to the lower half
+  const bool head_live = active && hl < a.group;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) reinterpret_cast<float4_t*>(mg)[i] = st.acc[i];
-    mg[32] = st.m;
-    mg[33] = l_tot;
-  }
-  __syncthreads();
-  if (half == 0 && active && hl < a.group) {
-    const float m1 = mg[32], l1 = mg[33];
-    const float mx = fmaxf(st.m, m1);
-    const float mu = (mx == -__builtin_inff()) ? 0.0f : mx;
-    const float a0 = __builtin_amdgcn_exp2f(st.m - mu), a1 = __builtin_amdgcn_exp2f(m1 - mu);
+  for (int width = kSlices / 2; width >= 1; width /= 2) {
+    __syncthreads();
+    if (slice >= width && slice < 2 * width) {
+      float* mg = reinterpret_cast<float*>(lds) + ((slice - width) * HPW + wave % HPW) * 64 * 36 + lane * 36;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) st.acc[i] = st.acc[i] * a0 + reinterpret_cast<const float4_t*>(mg)[i] * a1;
-    l_tot = l_tot * a0 + l1 * a1;
-    st.m = mx;
+      for (int i = 0; i < 8; ++i) reinterpret_cast<float4_t*>(mg)[i] = st.acc[i];
+      mg[32] = st.m;
+      mg[33] = l_tot;
+    }
+    __syncthreads();
+    if (slice < width && head_live) {
+      const float* mg = reinterpret_cast<const float*>(lds) + (slice * HPW + wave % HPW) * 64 * 36 + lane * 36;
+      const float m1 = mg[32], l1 = mg[33];
+      const float mx = fmaxf(st.m, m1);
+      const float mu = (mx == -__builtin_inff()) ? 0.0f : mx;
+      const float a0 = __builtin_amdgcn_exp2f(st.m - mu), a1 = __builtin_amdgcn_exp2f(m1 - mu);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) st.acc[i] = st.acc[i] * a0 + reinterpret_cast<const float4_t*>(mg)[i] * a1;
+      l_tot = l_tot * a0 + l1 * a1;
+      st.m = mx;
+    }
   }
   const int head = kvh * a.group + hl;
   if (a.splits == 1) {   // no partials: normalize and write
-    if (half == 1 || !active || hl >= a.group) return;
+    if (slice != 0 || !head_live) return;
     const float gv = *a.gv;
     const float inv = l_tot > 0.0f ? gv / l_tot : 0.0f;
 #pragma unroll
@@ -385,7 +448,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   float* row_part = a.part + (int64_t)row * a.splits * a.q_heads * kPartStride;
   const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
       row_part, (short)0, (int)((int64_t)a.splits * a.q_heads * kPartStride * 4), 0x00020000);
-  if (half == 0 && active && hl < a.group) {
+  if (slice == 0 && head_live) {
     const int at = ((split * a.q_heads + head) * kPartStride) * 4;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -404,8 +467,8 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   __syncthreads();
   if (!s_last) return;
   // 512 threads, 8 consecutive outputs each: head h0 + o / 128, d0 = o % 128; loads of 8 splits at a time together
-  const int h0 = kvg * kHeadsPerGroup * a.group;
-  const int nh = min(kHeadsPerGroup * a.group, a.q_heads - h0);
+  const int h0 = kvg * HPW * a.group;
+  const int nh = min(HPW * a.group, a.q_heads - h0);
   const float gv = *a.gv;
   for (int o = threadIdx.x * 8; o < nh * kDim; o += blockDim.x * 8) {
     const int hh = h0 + o / kDim, d0 = o % kDim;
@@ -457,6 +520,12 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
 }  // namespace xt
 
 using namespace xt;
+
+// Workgroup shape: 4 KV heads x 2 key slices when that alone yields a full launch (256 workgroups), else 1 KV head x 8
+// slices (more, smaller workgroups: a (row, head) merges its 8 slices in LDS instead of through partials).
+static int heads_per_workgroup(int rows, int kv_heads, int splits) {
+  return (kv_heads % 4 == 0 && (int64_t)rows * (kv_heads / 4) * splits >= 256) ? 4 : 1;
+}
 
 // Workspace: [counters: rows * q_heads int32 (an upper bound of rows * KV groups), padded to 256 B][partials]
 static size_t counter_bytes(int rows, int q_heads) { return (((size_t)rows * q_heads * 4 + 255) / 256) * 256; }
@@ -511,8 +580,10 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
   if (!aligned(workspace, 256)) return fail(XT_EINVAL, "%s: workspace must be 256-byte aligned", what);
   const int per_split = (topk + splits - 1) / splits;
   const int kps = ((per_split + kStep - 1) / kStep) * kStep;
-  const int half_steps = ((kps / kStep + kHalves * kPrefetch - 1) / (kHalves * kPrefetch)) * kPrefetch;
-  const int slot_bytes = kHalves * half_steps * kStep * (int)sizeof(int32_t);
+  const int hpw = heads_per_workgroup(rows, kv_heads, splits);
+  const int slices = kWaves / hpw;
+  const int slice_steps = ((kps / kStep + slices * kPrefetch - 1) / (slices * kPrefetch)) * kPrefetch;
+  const int slot_bytes = slices * slice_steps * kStep * (int)sizeof(int32_t);
   size_t lds_bytes = (size_t)slot_bytes + (size_t)kWaves * kWaveLds;
   if (lds_bytes < (size_t)kMergeLds) lds_bytes = kMergeLds;
   if (lds_bytes > 64 * 1024)
@@ -535,10 +606,11 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
   a.kv_heads = kv_heads;
   a.q_heads = q_heads;
   a.group = group;
-  a.kv_groups = (kv_heads + kHeadsPerGroup - 1) / kHeadsPerGroup;
+  a.kv_groups = (kv_heads + hpw - 1) / hpw;
   a.table = table;
   a.table_stride = table_stride;
   a.page_size = page_size;
+  a.page_shift = (page_size & (page_size - 1)) == 0 ? __builtin_ctz((unsigned)page_size) : -1;
   a.row_req = row_req;
   a.indices = indices;
   a.idx_stride = idx_stride;
@@ -559,15 +631,16 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
   a.counters = static_cast<int32_t*>(workspace);
   a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + counter_bytes(rows, q_heads));
   a.n_units = (int64_t)rows * a.kv_groups * splits;
-  // per-XCD ranges of whole rows, so that a row's splits share an XCD (with fewer than 8 rows, plain numbering keeps
-  // every XCD busy)
-  const int64_t per_row = (int64_t)a.kv_groups * splits;
-  a.xcd_map = rows >= 8;
-  a.per_xcd = ((rows + 7) / 8) * per_row;
-  const int64_t launched = a.xcd_map ? 8 * a.per_xcd : a.n_units;
+  a.xcd_units = (uint32_t)(a.n_units / 8);
+  a.xcd_extra = (uint32_t)(a.n_units % 8);
+  const int64_t launched = a.n_units;
   if (launched > 0x7FFFFFFFLL) return fail(XT_EUNSUPPORTED, "%s: %lld workgroups", what, (long long)launched);
 
-  hipLaunchKernelGGL(decode_split_kernel<kPrefetch>, dim3((unsigned)launched), dim3(64 * kWaves), lds_bytes,
-                     reinterpret_cast<hipStream_t>(stream), a);
+  if (hpw == 4)
+    hipLaunchKernelGGL((decode_split_kernel<kPrefetch, 4>), dim3((unsigned)launched), dim3(64 * kWaves), lds_bytes,
+                       reinterpret_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL((decode_split_kernel<kPrefetch, 1>), dim3((unsigned)launched), dim3(64 * kWaves), lds_bytes,
+                       reinterpret_cast<hipStream_t>(stream), a);
   return check_launch(what);
 }
