@@ -96,6 +96,20 @@ def cpu_baseline(raw, q, pt, idx, seq, w, scale, seconds):
                       f'softmax attention, one thread, {cpu_model()}, {os.cpu_count()} host cores)'}
 
 
+def measured_traffic(workload, splits, layout):
+    """HBM bytes per launch of the decode kernel from the committed rocprofv3 counter summary (FETCH_SIZE and
+    WRITE_SIZE, each scaled by the counter's reading for a copy of known size), when it was taken on this exact
+    configuration; None otherwise."""
+    path = ROOT / 'profiles' / f'decode_split_{workload}_traffic.json'
+    try:
+        rec = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    if rec.get('workload') != workload or rec.get('splits') != splits or rec.get('pool_layout') != layout:
+        return None
+    return rec.get('traffic_bytes')
+
+
 def main():
     p = argparse.ArgumentParser()
     p.add_argument('--gpus', type=int, default=1)
@@ -108,6 +122,9 @@ def main():
                    help='pool layout: interleaved (per slot [K pay | K sf | V pay | V sf]) or split (SGLang buffers)')
     p.add_argument('--cpu-seconds', type=float, default=10.0)
     p.add_argument('--no-cpu-baseline', action='store_true')
+    p.add_argument('--copy-calibration', type=int, default=0, metavar='MIB',
+                   help='only copy MIB MiB between two device buffers 8 times (the known-size kernel that scales the '
+                        'FETCH_SIZE / WRITE_SIZE counters), then exit')
     args = p.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print(json.dumps({'error': 'this benchmark runs on one GPU only: the sparse decode shards by request or KV '
@@ -115,6 +132,15 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.copy_calibration:
+        src = torch.empty(args.copy_calibration << 20, dtype=torch.uint8, device='cuda')
+        dst = torch.empty_like(src)
+        for _ in range(8):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({'copy_calibration_bytes': args.copy_calibration << 20, 'launches': 8}))
+        return
 
     from xtier_amd import ops, workloads
     from xtier_amd.pool import KVPool
@@ -177,7 +203,8 @@ def main():
         'tokens_per_s': round(w.batch / (ms * 1e-3), 1),
         'hbm_frac': round(gbs / HBM_PEAK_GBS, 4),
         'roofline': {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-                     'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None},
+                     'frac': round(gbs / HBM_PEAK_GBS, 4),
+                     'traffic': measured_traffic(w.name, splits, args.layout)},
         'cpu_baseline': cpu,
     }
     print(json.dumps(record), flush=True)

@@ -107,8 +107,9 @@ size_t xt_sparse_decode_workspace_bytes(int rows, int q_heads, int dim, int spli
  * -inf for an empty row. q_heads must be a multiple of kv_heads with q_heads / kv_heads <= 16; dim = 128.
  * splits: key splits per row (1..64); workspace: xt_sparse_decode_workspace_bytes(rows, q_heads, dim, splits) bytes,
  * 256-byte aligned and zero-filled before its first use (split partials and arrival counters; every call leaves the
- * counters zero again; calls that overlap in time need separate workspaces). One launch on `stream`: the last
- * workgroup of each (row, group of 4 KV heads) to finish merges the split partials. */
+ * counters zero again; calls that overlap in time need separate workspaces). One launch on `stream`; a workgroup
+ * handles 4 KV heads (many rows) or 1 KV head (few rows) of one (row, key split), and with splits > 1 the last
+ * workgroup of each (row, head group) to finish merges the split partials. */
 int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, const uint8_t* k_pay,
                            const uint8_t* v_pay, const uint8_t* k_scales, const uint8_t* v_scales, const float* gk,
                            const float* gv, int64_t pool_slots, int64_t pay_stride, int64_t sf_stride, int kv_heads,
