@@ -110,12 +110,82 @@ def measured_traffic(workload, splits, layout):
     return rec.get('traffic_bytes')
 
 
+MFMA_PEAK_TFLOPS = 2500.0   # dense FP16 / BF16
+
+
+def run_prefill(args, w, ops, workloads, KVPool):
+    """A step of chunked sparse prefill: quantize-on-append of the chunk's K and V rows into the pool, then the
+    attention of every chunk query over its own causal top-k positions. One JSON line: attention TFLOP/s against the
+    dense FP16 MFMA peak (the step's MFMA roofline), and the gathered-bytes rate."""
+    import torch
+    torch.cuda.set_device(0)
+    gen = workloads.generator('cuda', 20261029)
+    t0 = time.time()
+    inp = workloads.prefill_inputs(w, 20261029, device='cuda')
+    pool = KVPool(w.slots, w.kv_heads, w.dim, 'cuda', layout=args.layout)
+    pool.set_global_scales(inp.k, inp.v)
+    pos = torch.arange(w.ctx, device='cuda')
+    slot_of = inp.page_table[0, pos // w.page].long() * w.page + pos % w.page
+    pool.append(inp.k[:w.ctx0], inp.v[:w.ctx0], slot_of[:w.ctx0], saturate=False)
+    k_new, v_new, new_slots = inp.k[w.ctx0:].contiguous(), inp.v[w.ctx0:].contiguous(), slot_of[w.ctx0:].contiguous()
+    rows = w.chunk
+    row_req = torch.zeros(rows, dtype=torch.int64, device='cuda')
+    seq = torch.full((rows,), w.ctx, dtype=torch.int32, device='cuda')
+    out = torch.empty(rows, w.q_heads, w.dim, dtype=torch.bfloat16, device='cuda')
+    splits = args.splits or 1
+    ws = ops.new_workspace('cuda', rows, w.q_heads, w.dim, splits)
+    scale = 1.0 / math.sqrt(w.dim)
+    del gen
+    torch.cuda.synchronize()
+    log(f'built the {w.ctx}-slot pool and {rows} causal index lists in {time.time() - t0:.1f} s')
+
+    def step():
+        pool.append(k_new, v_new, new_slots, saturate=False)
+        ops.sparse_decode(inp.q, pool.raw, inp.page_table, inp.indices, seq, scale, page_size=w.page, row_req=row_req,
+                          query_pos=inp.q_pos, out=out, splits=splits, ws=ws)
+
+    for _ in range(max(1, args.warmup)):
+        step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    graph.replay()
+    torch.cuda.synchronize()
+    steps = max(1, args.steps)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    tflops = w.flops() / (ms * 1e-3) / 1e12
+    gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
+    log(f'{w.name}: {ms * 1e3:.1f} us per step, {tflops:.1f} TFLOP/s ({tflops / MFMA_PEAK_TFLOPS:.1%} of '
+        f'{MFMA_PEAK_TFLOPS:.0f}), gathered {gbs:.0f} GB/s')
+    record = {
+        'metric': 'NVFP4-KV sparse prefill attention TFLOP/s (chunk with quantize-on-append)', 'value': round(tflops, 2),
+        'unit': 'TFLOP/s', 'n_gpus': 1, 'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6),
+        'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f16', 'data': 'synthetic',
+        'config': {'workload': w.name, 'q_heads': w.q_heads, 'kv_heads': w.kv_heads, 'head_dim': w.dim,
+                   'context': w.ctx0, 'chunk': w.chunk, 'topk': w.topk, 'recent': w.recent, 'page': w.page,
+                   'kv_format': 'nvfp4', 'splits': splits, 'pool_layout': args.layout},
+        'us_per_step': round(ms * 1e3, 2), 'gathered_gbs': round(gbs, 1),
+        'roofline': {'bound': 'mfma', 'achieved': round(tflops, 2), 'peak': MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
+                     'frac': round(tflops / MFMA_PEAK_TFLOPS, 4), 'traffic': None},
+        'cpu_baseline': None,
+    }
+    print(json.dumps(record), flush=True)
+
+
 def main():
     p = argparse.ArgumentParser()
     p.add_argument('--gpus', type=int, default=1)
     p.add_argument('--steps', type=int, default=512)
     p.add_argument('--warmup', type=int, default=64)
-    p.add_argument('--workload', default='gqa_decode_b32')
+    p.add_argument('--workload', default='gqa_decode_b32',
+                   help='gqa_decode_b32 (default), cpu_ref_decode, long_ctx_decode_b4 or gqa_prefill_chunk4096')
     p.add_argument('--layers', type=int, default=16)
     p.add_argument('--splits', type=int, default=None)
     p.add_argument('--layout', default='interleaved', choices=['interleaved', 'split'],
@@ -145,6 +215,8 @@ def main():
     from xtier_amd import ops, workloads
     from xtier_amd.pool import KVPool
 
+    if args.workload in workloads.PREFILL_WORKLOADS:
+        return run_prefill(args, workloads.PREFILL_WORKLOADS[args.workload], ops, workloads, KVPool)
     w = workloads.WORKLOADS[args.workload]
     torch.cuda.set_device(0)
     gen = workloads.generator('cuda', 20261029)

@@ -49,6 +49,43 @@ WORKLOADS = {
 }
 
 
+@dataclass(frozen=True)
+class PrefillWorkload:
+    """One request: `chunk` new tokens appended after `ctx0` context tokens; query t (position ctx0 + t) attends to
+    its own top-k causal positions (the `recent` most recent, itself included, plus uniform ones below them); the step
+    also quantizes the chunk's K/V rows into the pool."""
+    name: str
+    q_heads: int
+    kv_heads: int
+    dim: int
+    ctx0: int
+    chunk: int
+    topk: int
+    recent: int = 128
+    page: int = 64
+
+    @property
+    def ctx(self):
+        return self.ctx0 + self.chunk
+
+    @property
+    def slots(self):
+        return self.ctx
+
+    def algorithmic_bytes(self):
+        """Gathered KV payload plus scales over all queries (most are cache hits: the unique set is the pool)."""
+        return self.chunk * self.topk * self.kv_heads * 2 * (self.dim // 2 + self.dim // 16)
+
+    def flops(self):
+        return self.chunk * self.q_heads * self.topk * 4 * self.dim
+
+
+PREFILL_WORKLOADS = {
+    # 4096 query tokens appended at 65536 (context 69632), 32 q / 4 KV heads, d 128, top-2048 causal per query
+    'gqa_prefill_chunk4096': PrefillWorkload('gqa_prefill_chunk4096', 32, 4, 128, 65536, 4096, 2048),
+}
+
+
 def generator(device, seed):
     g = torch.Generator(device=device)
     g.manual_seed(seed)
@@ -134,3 +171,26 @@ def decode_inputs(w, seed, device='cpu', batch=None):
     idx = index_lists(b, w.ctx, w.topk, gen, device, w.index_mode)
     seq = torch.full((b,), w.ctx, dtype=torch.int32, device=device)
     return DecodeInputs(w, q, k, v, pt, idx, seq)
+
+
+@dataclass
+class PrefillInputs:
+    workload: PrefillWorkload
+    q: torch.Tensor            # bf16 [chunk, q_heads, dim]
+    k: torch.Tensor            # bf16 [ctx, kv_heads, dim]: context rows then the chunk's rows
+    v: torch.Tensor
+    page_table: torch.Tensor   # int32 [1, ctx/page]
+    indices: torch.Tensor      # int32 [chunk, topk]
+    q_pos: torch.Tensor        # int32 [chunk]: ctx0 + t
+
+
+def prefill_inputs(w, seed, device='cpu'):
+    """Seeded activations, page table and per-query causal index lists of a prefill workload."""
+    gen = generator(device, seed)
+    k = kv_tensor(w.ctx, w.kv_heads, w.dim, gen, device)
+    v = kv_tensor(w.ctx, w.kv_heads, w.dim, gen, device)
+    q = torch.randn(w.chunk, w.q_heads, w.dim, generator=gen, device=device).to(torch.bfloat16)
+    pt = page_table(1, w.ctx, w.page, gen, device)
+    q_pos = torch.arange(w.ctx0, w.ctx, dtype=torch.int32, device=device)
+    idx = causal_index_lists(q_pos, w.topk, w.recent, gen, device)
+    return PrefillInputs(w, q, k, v, pt, idx, q_pos)
