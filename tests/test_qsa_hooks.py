@@ -1,0 +1,107 @@
+"""The QSA hook layer without a GPU: which hooks fall through to `original` and when (qsa_fp4.py:197-268), what
+raw_buffers returns for NVFP4, hybrid and other pools, and that the active-layer stack is restored on errors."""
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from xtier_amd import qsa
+
+
+class _Method:
+    def __init__(self, name, layers=3):
+        self.name = name
+        self.k_scales_gpu = torch.arange(layers, dtype=torch.float32) + 1
+        self.v_scales_gpu = torch.arange(layers, dtype=torch.float32) + 10
+
+
+class _Pool:
+    def __init__(self, name='nvfp4', hybrid=False):
+        self._method = _Method(name)
+        self.bufs = (torch.zeros(8, 2, 64, dtype=torch.uint8), torch.zeros(8, 2, 64, dtype=torch.uint8),
+                     torch.zeros(8, 2, 8, dtype=torch.uint8), torch.zeros(8, 2, 8, dtype=torch.uint8))
+        if hybrid:
+            self.full_kv_pool = object()
+
+    def get_kv_cache_quant_method(self):
+        return self._method
+
+    def get_raw_kv_buffer(self, layer_id):
+        return self.bufs
+
+
+def _calls():
+    log = []
+
+    def original(*args, **kwargs):
+        log.append((args, kwargs, list(qsa._active)))
+        return 'original'
+    return log, original
+
+
+def test_raw_buffers_nvfp4_layer_scales():
+    raw = qsa.raw_buffers(_Pool(), SimpleNamespace(layer_id=2))
+    assert raw[0].dtype == torch.uint8 and raw[2].shape == (8, 2, 8)
+    assert raw[4].tolist() == [3.0] and raw[5].tolist() == [12.0]     # k/v_scales_gpu[layer_id:layer_id + 1]
+
+
+def test_raw_buffers_hybrid_pool_uses_unit_scale():
+    raw = qsa.raw_buffers(_Pool(hybrid=True), SimpleNamespace(layer_id=0))
+    assert raw[4] is raw[5] and raw[4].tolist() == [1.0]
+
+
+def test_raw_buffers_other_pools_fall_through():
+    assert qsa.raw_buffers(_Pool('fp8'), SimpleNamespace(layer_id=0)) is None
+    assert qsa.raw_buffers(object(), SimpleNamespace(layer_id=0)) is None
+
+
+def test_extraction_and_pack_fall_through_without_active_layer():
+    log, original = _calls()
+    assert qsa.extraction(original, 'k', 'v', 'r2t', 'ri', 'idx', 'sl', 'cu', 'ok', 'ov', 3, 4, zero_fill_cols=5) == \
+        'original'
+    assert log[-1][0] == ('k', 'v', 'r2t', 'ri', 'idx', 'sl', 'cu', 'ok', 'ov', 3, 4)
+    assert log[-1][1] == {'zero_fill_cols': 5}
+    assert qsa.pack_qsa_prefill_kv(original, k='k', v='v', req_to_token='r', req_indices='i', cu_k='c', total_k=7,
+                                   max_k=3) == 'original'
+    assert log[-1][1]['total_k'] == 7 and log[-1][1]['output_dtype'] is None
+
+
+def test_forward_extend_activates_layer_and_restores_on_error():
+    log, original = _calls()
+    backend = SimpleNamespace(token_to_kv_pool=_Pool())
+    layer = SimpleNamespace(layer_id=1)
+    assert qsa.forward_extend(original, backend, 'q', 'k', 'v', layer, 'fb', 'extra', flag=True) == 'original'
+    args, kwargs, active = log[-1]
+    assert args == (backend, 'q', 'k', 'v', layer, 'fb', 'extra') and kwargs == {'flag': True}
+    assert len(active) == 1 and active[0][4].tolist() == [2.0]
+    assert qsa._active == []
+
+    def failing(*a, **k):
+        raise KeyError('x')
+    with pytest.raises(KeyError):
+        qsa.forward_extend(failing, backend, 'q', 'k', 'v', layer, 'fb')
+    assert qsa._active == []
+    # a non-NVFP4 pool runs original with nothing active
+    qsa.forward_extend(original, SimpleNamespace(token_to_kv_pool=_Pool('bf16')), 'q', 'k', 'v', layer, 'fb')
+    assert log[-1][2] == []
+
+
+def test_paged_attention_falls_through_for_other_pools_and_cpu():
+    log, original = _calls()
+    layer = SimpleNamespace(layer_id=0)
+    q = torch.zeros(2, 4, 128)
+    assert qsa.paged_attention(original, SimpleNamespace(token_to_kv_pool=_Pool('fp8')), q, layer, 'fb', 'ti') == \
+        'original'
+    backend = SimpleNamespace(token_to_kv_pool=_Pool())
+    assert qsa.paged_attention(original, backend, q, layer, 'fb', 'ti') == 'original'   # CPU q
+    assert log[-1][0] == (backend, q, layer, 'fb', 'ti')
+
+
+def test_quantize_substitutes_device_unit_scale():
+    log, original = _calls()
+    t = torch.zeros(4)
+    qsa.create_buffers({'k_buffer': [t]}, None)
+    qsa.quantize(original, t, 1.0, 'x')
+    assert torch.is_tensor(log[-1][0][1]) and log[-1][0][1].tolist() == [1.0] and log[-1][0][2] == 'x'
+    qsa.quantize(original, t, 0.5)
+    assert log[-1][0][1] == 0.5
