@@ -106,8 +106,10 @@ size_t xt_sparse_decode_workspace_bytes(int rows, int q_heads, int dim, int spli
  * without valid keys writing 0. lse (optional, FP32 [rows, q_heads]): natural log-sum-exp of the scaled scores,
  * -inf for an empty row. q_heads must be a multiple of kv_heads with q_heads / kv_heads <= 16; dim = 128.
  * splits: key splits per row (1..64); workspace: xt_sparse_decode_workspace_bytes(rows, q_heads, dim, splits) bytes,
- * 256-byte aligned and zero-filled before its first use (split partials and arrival counters; every call leaves the
- * counters zero again; calls that overlap in time need separate workspaces). One launch on `stream`; a workgroup
+ * 256-byte aligned. With splits > 1 it holds a fixed 64 KB region of arrival counters (one per row and KV head group,
+ * rows * kv_heads <= 16384) followed by the split partials: zero-filled before its first use, the counters are left
+ * zero by every call, so calls of any shape (and sparse MLA calls) may share one workspace; calls that overlap in time
+ * need separate workspaces. One launch on `stream`; a workgroup
  * handles 4 KV heads (many rows) or 1 KV head (few rows) of one (row, key split), and with splits > 1 the last
  * workgroup of each (row, head group) to finish merges the split partials. */
 int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, const uint8_t* k_pay,
@@ -119,6 +121,51 @@ int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_s
                            const int32_t* seq_lens, const int32_t* query_pos, float scale, void* out,
                            int64_t out_row_stride, int64_t out_head_stride, int out_dtype, float* lse, int rows,
                            int splits, void* workspace, size_t workspace_bytes, xt_stream_t stream);
+
+/* --- sparse MLA over an NVFP4 latent cache ------------------------------------------------------------------------ */
+
+/* One latent cache: per slot a latent row of latent_dim NVFP4 values (payload latent_dim/2 bytes, E4M3 scales
+ * latent_dim/16 bytes, global scale *g) and a rope row of rope_dim BF16 values. Strides are bytes from one slot to the
+ * next (0 = packed: latent_dim/2, latent_dim/16, 2*rope_dim), so one 416-byte record per token
+ * [payload 256 | scales 32 | rope 128] is pay = base, scales = base + 256, rope = base + 288, all strides 416. */
+typedef struct {
+  const uint8_t* pay;
+  const uint8_t* scales;
+  const void* rope;
+  const float* g;
+  int64_t slots;
+  int64_t pay_stride, sf_stride, rope_stride;
+} xt_mla_cache;
+
+/* A key list: indices[r * stride + c] for c < topk are slots of the cache (-1: none); lengths[r] (NULL: topk)
+ * limits the columns of row r. */
+typedef struct {
+  const int32_t* indices;
+  int64_t stride;
+  int topk;
+  const int32_t* lengths;
+} xt_mla_keys;
+
+/* Device workspace of xt_sparse_mla_nvfp4 for `rows` rows, `heads` heads and `splits` key splits. */
+size_t xt_sparse_mla_workspace_bytes(int rows, int heads, int splits);
+
+/* Sparse MLA (DeepSeek-style; replaces sparse_mla / the hook flash_mla_with_kvcache of
+ * xtier/packs/deepseek_v4/sparse_mla.py:167-231 on an NVFP4 latent cache). Row r of q (BF16 [rows, heads,
+ * latent_dim + rope_dim], element strides q_row_stride / q_head_stride) attends to the valid keys of `keys` in `cache`
+ * followed by those of `extra_keys` in `extra_cache` (both NULL: one list), key = [(e2m1 * e4m3) * g latent,
+ * rope], value = the latent:
+ *   out[r, h] = sum_k exp(s_k - m) v_k / (sum_k exp(s_k - m) + exp(sink[h] - m)),  s_k = scale * q[r, h] . key_k,
+ * written in out_dtype to out (BF16/FP16 [rows, heads, latent_dim], strides in elements); sink NULL: no sink term.
+ * lse (optional FP32 [rows, heads]): natural log of sum_k exp(s_k) over the keys only (sparse_mla.py:73-85); a row
+ * without valid keys writes zeros and lse -inf. latent_dim 512, rope_dim 64, heads <= 128 are supported.
+ * splits: key splits per row (1..64; rows <= 16384 with splits > 1); workspace as for the decode:
+ * xt_sparse_mla_workspace_bytes bytes, 256-byte aligned, zero-filled before first use, its counters left zero by
+ * every call (one workspace may serve decode and MLA calls of any shape, one at a time). */
+int xt_sparse_mla_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, int heads, int latent_dim,
+                        int rope_dim, const xt_mla_cache* cache, const xt_mla_keys* keys,
+                        const xt_mla_cache* extra_cache, const xt_mla_keys* extra_keys, const float* sink, float scale,
+                        void* out, int64_t out_row_stride, int64_t out_head_stride, int out_dtype, float* lse, int rows,
+                        int splits, void* workspace, size_t workspace_bytes, xt_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -190,28 +190,39 @@ def merge_partials(m, l, acc):
 
 # --- sparse MLA ---------------------------------------------------------------------------------------------------
 
-def sparse_mla(q, latent_pay, latent_sf, rope, g, indices, topk_length, sink, scale, dtype=np.float64):
+def sparse_mla(q, latent_pay, latent_sf, rope, g, indices, topk_length, sink, scale, dtype=np.float64, extra=None):
     """Sparse MLA over an NVFP4 latent + BF16 rope cache, reference values (the FP64 reference of
-    tests/ds_sparse_mla_check.py:44-67 on this layout): q [R, H, Dl + Dr]; per token the key is
-    [(e2m1 * e4m3) * g latent (Dl), rope (Dr)] and the value is the latent; indices [R, K] are pool slots (-1 none),
-    topk_length [R] or None; sink [H] or None enters the denominator as exp(sink - m). Returns (out [R, H, Dl],
-    lse [R, H] natural log of the keys' sum, -inf for a row without keys)."""
+    tests/ds_sparse_mla_check.py:44-67 on this layout; sparse_mla.py:88-125 for the two key lists): q [R, H, Dl + Dr];
+    per token the key is [(e2m1 * e4m3) * g latent (Dl), rope (Dr)] and the value is the latent; indices [R, K] are
+    pool slots (-1 none), topk_length [R] or None; extra = (latent_pay, latent_sf, rope, g, indices, topk_length) of a
+    second cache whose valid keys follow the first list's; sink [H] or None enters the denominator as exp(sink - m).
+    Returns (out [R, H, Dl], lse [R, H] natural log of the keys' sum, -inf for a row without keys)."""
     q = np.asarray(q, dtype=dtype)
     rows_n, heads, _ = q.shape
     dl = latent_pay.shape[-1] * 2
     out = np.zeros((rows_n, heads, dl), dtype=dtype)
     lse = np.full((rows_n, heads), -np.inf, dtype=dtype)
+    lists = [(latent_pay, latent_sf, rope, g, indices, topk_length)]
+    if extra is not None:
+        lists.append(extra)
     for r in range(rows_n):
-        idx = np.asarray(indices[r], dtype=np.int64)
-        cols = np.arange(idx.shape[0])
-        valid = idx >= 0
-        if topk_length is not None:
-            valid &= cols < int(topk_length[r])
-        sel = idx[valid]
-        if sel.size == 0:
+        keys, lats = [], []
+        for pay, sf, rp, gg, idx_all, lengths in lists:
+            idx = np.asarray(idx_all[r], dtype=np.int64)
+            cols = np.arange(idx.shape[0])
+            valid = (idx >= 0) & (idx < pay.shape[0])
+            if lengths is not None:
+                valid &= cols < int(lengths[r])
+            sel = idx[valid]
+            if sel.size == 0:
+                continue
+            lat = nvfp4.dequant(pay[sel], sf[sel], gg).astype(dtype)
+            keys.append(np.concatenate([lat, np.asarray(rp[sel], dtype=dtype)], -1))
+            lats.append(lat)
+        if not keys:
             continue
-        lat = nvfp4.dequant(latent_pay[sel], latent_sf[sel], g).astype(dtype)
-        key = np.concatenate([lat, np.asarray(rope[sel], dtype=dtype)], -1)
+        key = np.concatenate(keys, 0)
+        lat = np.concatenate(lats, 0)
         s = (key @ q[r].T) * dtype(scale)        # [n, H]
         m = s.max(0)
         p = np.exp(s - m[None])

@@ -207,3 +207,20 @@ def test_interleaved_pool_equals_split_pool():
     a = ops.sparse_decode(q.cuda(), pool.raw, pt.cuda(), idx.cuda(), seq, 0.09, page_size=64)
     b = ops.sparse_decode(q.cuda(), il.raw, pt.cuda(), idx.cuda(), seq, 0.09, page_size=64)
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_one_workspace_serves_calls_of_any_shape():
+    """A workspace left by a call with few rows (its partials written just past the counters) serves a later call
+    with more rows and a sparse-MLA call: every result equals the one from a fresh workspace, bit for bit."""
+    pool, pt, idx, q = _small_case(seed=31, batch=8)
+    seq = torch.full((8,), 3008, dtype=torch.int32, device='cuda')
+    ws = torch.zeros(ops.decode_workspace_bytes(8, 32, 128, 16), dtype=torch.uint8, device='cuda')
+    runs = [(2, 16), (8, 3), (5, 7), (8, 2)]
+    for rows, splits in runs:
+        got = ops.sparse_decode(q[:rows].cuda(), pool.raw, pt[:rows].cuda(), idx[:rows].cuda(), seq[:rows], 0.09,
+                                page_size=64, splits=splits, ws=ws)
+        fresh = ops.sparse_decode(q[:rows].cuda(), pool.raw, pt[:rows].cuda(), idx[:rows].cuda(), seq[:rows], 0.09,
+                                  page_size=64, splits=splits,
+                                  ws=ops.new_workspace('cuda', rows, 32, 128, splits))
+        assert torch.equal(got.view(torch.int16), fresh.view(torch.int16)), (rows, splits)
+    assert not ws[:65536].any()   # the counters are left zero

@@ -159,3 +159,42 @@ def test_sparse_mla_matches_torch_with_sink():
     want = _mla_torch(q, keys, deq, idx, length, sink, 0.07)
     assert np.allclose(out, want, rtol=0, atol=1e-12)
     assert np.all(np.isneginf(lse[2])) and not out[2].any()
+
+
+def test_sparse_mla_two_lists_equal_one_concatenated_cache():
+    """The second key list in its own cache (sparse_mla.py:109-118) gives what one list over the two caches stacked
+    gives (same keys, same order); a row whose lists are both empty writes zeros."""
+    rng = np.random.default_rng(12)
+    dl, dr, heads = 64, 16, 8
+    caches = []
+    for tokens in (200, 90):
+        lat = nvfp4.f32_to_bf16_f32(rng.standard_normal((tokens, dl)).astype(np.float32))
+        pay, sc, g = nvfp4.nvfp4_encode(lat)
+        rope = nvfp4.f32_to_bf16_f32(rng.standard_normal((tokens, dr)).astype(np.float32))
+        caches.append((pay, sc, rope, g))
+    (p1, s1, r1, g1), (p2, s2, r2, g2) = caches
+    rows = 4
+    i1 = rng.integers(0, 200, (rows, 30)).astype(np.int32)
+    i2 = rng.integers(0, 90, (rows, 12)).astype(np.int32)
+    l1 = np.array([30, 5, 0, 30], np.int32)
+    l2 = np.array([12, 0, 0, 3], np.int32)
+    q = rng.standard_normal((rows, heads, dl + dr)) * 0.5
+    sink = rng.standard_normal(heads)
+    out, lse = attention.sparse_mla(q, p1, s1, r1, g1, i1, l1, sink, 0.1, extra=(p2, s2, r2, g2, i2, l2))
+    # one cache: the second cache's rows re-encoded under the first cache's scale are not the same bytes, so stack
+    # the dequantized keys instead and compare against a direct softmax
+    d1 = nvfp4.dequant(p1, s1, g1).astype(np.float64)
+    d2 = nvfp4.dequant(p2, s2, g2).astype(np.float64)
+    for r in range(rows):
+        k1 = np.concatenate([d1[i1[r, :l1[r]]], r1[i1[r, :l1[r]]]], -1)
+        k2 = np.concatenate([d2[i2[r, :l2[r]]], r2[i2[r, :l2[r]]]], -1)
+        keys = np.concatenate([k1, k2], 0)
+        if keys.shape[0] == 0:
+            assert not out[r].any() and np.isneginf(lse[r]).all()
+            continue
+        s = keys @ q[r].T * 0.1
+        m = s.max(0)
+        p = np.exp(s - m)
+        want = (p.T @ keys[:, :dl]) / (p.sum(0) + np.exp(sink - m))[:, None]
+        assert np.allclose(out[r], want, rtol=1e-12, atol=1e-12)
+        assert np.allclose(lse[r], m + np.log(p.sum(0)), rtol=1e-12, atol=1e-12)

@@ -20,6 +20,21 @@ _L = ctypes.c_int64
 _F = ctypes.c_float
 _Z = ctypes.c_size_t
 
+
+
+class MlaCache(ctypes.Structure):
+    """xt_mla_cache: one NVFP4 latent + BF16 rope cache (strides in bytes, 0 = packed)."""
+    _fields_ = [('pay', _P), ('scales', _P), ('rope', _P), ('g', _P), ('slots', _L), ('pay_stride', _L),
+                ('sf_stride', _L), ('rope_stride', _L)]
+
+
+class MlaKeys(ctypes.Structure):
+    """xt_mla_keys: a key list (slots, -1 none) with an optional per-row length."""
+    _fields_ = [('indices', _P), ('stride', _L), ('topk', _I), ('lengths', _P)]
+
+
+_CP, _KP = ctypes.POINTER(MlaCache), ctypes.POINTER(MlaKeys)
+
 SIGNATURES = {
     'xt_version': (_I, []),
     'xt_last_error': (ctypes.c_char_p, []),
@@ -31,6 +46,9 @@ SIGNATURES = {
     'xt_sparse_decode_workspace_bytes': (_Z, [_I, _I, _I, _I]),
     'xt_sparse_decode_nvfp4': (_I, [_P, _L, _L, _P, _P, _P, _P, _P, _P, _L, _L, _L, _I, _I, _I, _P, _L, _I, _P, _P,
                                     _L, _I, _P, _P, _P, _F, _P, _L, _L, _I, _P, _I, _I, _P, _Z, _P]),
+    'xt_sparse_mla_workspace_bytes': (_Z, [_I, _I, _I]),
+    'xt_sparse_mla_nvfp4': (_I, [_P, _L, _L, _I, _I, _I, _CP, _KP, _CP, _KP, _P, _F, _P, _L, _L, _I, _P, _I, _I, _P,
+                                 _Z, _P]),
 }
 
 _lock = threading.Lock()

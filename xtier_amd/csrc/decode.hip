@@ -527,13 +527,12 @@ static int heads_per_workgroup(int rows, int kv_heads, int splits) {
   return (kv_heads % 4 == 0 && (int64_t)rows * (kv_heads / 4) * splits >= 256) ? 4 : 1;
 }
 
-// Workspace: [counters: rows * q_heads int32 (an upper bound of rows * KV groups), padded to 256 B][partials]
-static size_t counter_bytes(int rows, int q_heads) { return (((size_t)rows * q_heads * 4 + 255) / 256) * 256; }
+// Workspace: [arrival counters, kCounterBytes][partials [rows, splits, q_heads, kPartStride] FP32]
 
 extern "C" size_t xt_sparse_decode_workspace_bytes(int rows, int q_heads, int dim, int splits) {
   if (rows < 0 || q_heads <= 0 || dim <= 0 || splits <= 0) return 0;
   if (splits == 1) return 256;
-  return counter_bytes(rows, q_heads) + (size_t)rows * splits * q_heads * (size_t)(dim + 4) * sizeof(float);
+  return kCounterBytes + (size_t)rows * splits * q_heads * (size_t)(dim + 4) * sizeof(float);
 }
 
 extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride,
@@ -574,6 +573,9 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
   if (!aligned(k_pay, 16) || !aligned(v_pay, 16) || !aligned(k_scales, 4) || !aligned(v_scales, 4))
     return fail(XT_EINVAL, "%s: payload must be 16-byte and scales 4-byte aligned", what);
   if (lse && !aligned(lse, 4)) return fail(XT_EINVAL, "%s: lse must be 4-byte aligned", what);
+  if (splits > 1 && (int64_t)rows * kv_heads > kCounterSlots)
+    return fail(XT_EUNSUPPORTED, "%s: %d rows x %d KV heads with key splits exceed %d arrival counters; use splits 1",
+                what, rows, kv_heads, kCounterSlots);
   const size_t need = xt_sparse_decode_workspace_bytes(rows, q_heads, dim, splits);
   if (workspace_bytes < need)
     return fail(XT_EWORKSPACE, "%s: workspace %zu bytes < %zu needed", what, workspace_bytes, need);
@@ -629,7 +631,7 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
   a.out_dtype = out_dtype;
   a.lse = lse;
   a.counters = static_cast<int32_t*>(workspace);
-  a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + counter_bytes(rows, q_heads));
+  a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
   a.n_units = (int64_t)rows * a.kv_groups * splits;
   a.xcd_units = (uint32_t)(a.n_units / 8);
   a.xcd_extra = (uint32_t)(a.n_units % 8);

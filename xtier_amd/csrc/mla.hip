@@ -1,0 +1,480 @@
+// Sparse MLA over an NVFP4 latent cache: 128 query heads share one key per token, [latent (512, NVFP4) | rope (64,
+// BF16)] = 576 wide, whose value is the latent. q.k and p.v on MFMA (v_mfma_f32_16x16x32_f16), online softmax in the
+// exp2 domain, an optional per-head sink in the denominator, one launch (split partials merged by the last
+// workgroup of a row).
+//
+// Work decomposition: a workgroup = 8 wavefronts x 16 heads = 128 heads of one (query row, key split), so every key is
+// read and dequantized once for all heads. Per step of 32 keys the workgroup
+//   1. turns the raw key records (loaded one step ahead into registers) into two LDS tiles: K [32 keys][576] FP16 and
+//      V^T [512][32 keys] FP16, the latent as FP16((e2m1 * e4m3) * g) and the rope widened from BF16;
+//   2. each wave computes S^T [32 keys x 16 heads] = K . Q^T (18 MFMAs per 16-key tile, Q^T resident in registers
+//      as FP16 of q * scale * log2(e)), the softmax, and O^T [512 x 16 heads] += V^T . P^T (32 MFMAs), P^T taken
+//      straight from the score registers (the key order T(j) below matches the V^T operand).
+//
+// Lane layouts (16x16x32 MFMA, hl = lane % 16, j = lane / 16):
+//   QK: A = K tile, lane (key hl, dims 32kk + 8j .. +7); B = Q^T, lane (head hl, same dims); C = S^T, lane (head hl,
+//       keys 4j .. 4j+3 of the 16-key tile).
+//   PV: A = V^T, lane (dim hl of a 16-dim tile, keys T(j) = {4j..4j+3, 16+4j..16+4j+3}); B = P^T, lane (head hl, keys
+//       T(j)); C = O^T, lane (head hl, dims 4j .. 4j+3 of the tile).
+//
+// Numerics: FP16((e2m1 * e4m3) * g) rounds the dequantized latent once (11 significant bits); the rope is exact
+// in FP16 within its range. P is FP16 with the lazy rescale of the decode kernel (P <= 256); sums are FP32.
+#include "xt_common.h"
+#include "xt_host.h"
+
+namespace xt {
+namespace {
+
+constexpr int kDl = 512;                 // latent width (NVFP4): 256 payload bytes, 32 scale bytes per token
+constexpr int kDr = 64;                  // rope width (BF16): 128 bytes per token
+constexpr int kDk = kDl + kDr;           // key width
+constexpr int kMSteps = 32;              // keys per step
+constexpr int kMWaves = 8;
+constexpr int kMHeads = 16 * kMWaves;    // heads per workgroup
+constexpr int kKRow = kDk + 8;           // halves per K tile row (16-byte pad)
+constexpr int kVRow = kMSteps + 8;       // halves per V^T tile row
+constexpr int kKTile = kMSteps * kKRow * 2;
+constexpr int kVTile = kDl * kVRow * 2;
+constexpr int kMPart = kDl + 4;          // floats per partial (row, split, head): 512 accumulators, max, sum, pad
+constexpr int kQChunks = kDk / 32;       // 32-dim chunks of a query row
+constexpr int kQReg = 12;                // chunks kept in registers; the others (4 latent + 2 rope) live in LDS
+constexpr int kQRow = 32 + 8;            // halves per (chunk, head) row of the LDS query block
+constexpr int kQTile = (kQChunks - kQReg) * kMHeads * kQRow * 2;
+constexpr int kRescaleM = 8;
+
+struct CacheDev {
+  const uint8_t* pay;
+  const uint8_t* sf;
+  const uint16_t* rope;
+  const float* g;
+  int64_t slots, pay_stride, sf_stride, rope_stride;   // strides in bytes
+};
+
+struct MlaArgs {
+  const uint16_t* q;
+  int64_t q_rs, q_hs;
+  CacheDev c[2];
+  const int32_t* idx[2];
+  int64_t idx_stride[2];
+  int topk[2];
+  const int32_t* len[2];
+  const float* sink;
+  float qscale;                      // softmax scale * log2(e)
+  uint16_t* out;
+  int64_t o_rs, o_hs;
+  int out_dtype;
+  float* lse;
+  int heads, splits, keys_per_split, steps;
+  float* part;                       // [rows, splits, heads, kMPart]
+  int32_t* counters;                 // [rows]
+  uint32_t xcd_units, xcd_extra;
+};
+
+// Slot list entries: >= 0 a slot of cache 0, <= -2 slot (-e - 2) of cache 1, -1 no key.
+__device__ inline bool entry_valid(int32_t e) { return e != -1; }
+
+struct Raw {
+  uint32_t pay[4];   // payload bytes 4c .. 4c+3 of keys 4kq + i
+  uint32_t sc[4];    // scale byte c / 2 of those keys
+  uint4 rope;        // rope values 8p .. 8p+7 of key t / 8 (threads 0-255)
+};
+
+__device__ inline void load_raw(const MlaArgs& a, const int32_t* slots, int step, Raw& r) {
+  const int t = threadIdx.x, kq = t >> 6, c = t & 63;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int32_t e = slots[step * kMSteps + 4 * kq + i];
+    const int ci = e <= -2 ? 1 : 0;
+    const int64_t s = e >= 0 ? e : (e <= -2 ? (int64_t)(-e - 2) : 0);
+    const CacheDev& cd = a.c[ci];
+    r.pay[i] = *reinterpret_cast<const uint32_t*>(cd.pay + s * cd.pay_stride + 4 * c);
+    r.sc[i] = cd.sf[s * cd.sf_stride + (c >> 1)];
+  }
+  if (t < 256) {
+    const int32_t e = slots[step * kMSteps + (t >> 3)];
+    const int ci = e <= -2 ? 1 : 0;
+    const int64_t s = e >= 0 ? e : (e <= -2 ? (int64_t)(-e - 2) : 0);
+    const CacheDev& cd = a.c[ci];
+    r.rope = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(cd.rope) + s * cd.rope_stride +
+                                             16 * (t & 7));
+  }
+}
+
+// Raw records -> K and V^T tiles. Invalid keys become zeros (their scores are masked; V = 0 keeps P * V finite).
+__device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step, const Raw& r, float g0, float g1,
+                               _Float16* kt, _Float16* vt) {
+  const int t = threadIdx.x, kq = t >> 6, c = t & 63;
+  half8_t vals[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int32_t e = slots[step * kMSteps + 4 * kq + i];
+    const float sg = entry_valid(e) ? e4m3_decode(r.sc[i]) * (e <= -2 ? g1 : g0) : 0.0f;
+    const _Float16 h = (_Float16)sg;
+    const half2_t s2 = half2_t{h, h};
+    const half2_t p0 = fp4x2_to_f16<0>(r.pay[i]) * s2, p1 = fp4x2_to_f16<1>(r.pay[i]) * s2;
+    const half2_t p2 = fp4x2_to_f16<2>(r.pay[i]) * s2, p3 = fp4x2_to_f16<3>(r.pay[i]) * s2;
+    vals[i] = half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+    *reinterpret_cast<half8_t*>(kt + (4 * kq + i) * kKRow + 8 * c) = vals[i];
+  }
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+    *reinterpret_cast<half4_t*>(vt + (8 * c + d) * kVRow + 4 * kq) =
+        half4_t{vals[0][d], vals[1][d], vals[2][d], vals[3][d]};
+  }
+  if (t < 256) {
+    const int key = t >> 3, p = t & 7;
+    const bool ok = entry_valid(slots[step * kMSteps + key]);
+    const uint32_t w[4] = {r.rope.x, r.rope.y, r.rope.z, r.rope.w};
+    half8_t h;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      h[2 * e] = ok ? (_Float16)bf16_bits_to_f32(w[e] & 0xFFFFu) : (_Float16)0.0f;
+      h[2 * e + 1] = ok ? (_Float16)bf16_bits_to_f32(w[e] >> 16) : (_Float16)0.0f;
+    }
+    *reinterpret_cast<half8_t*>(kt + key * kKRow + kDl + 8 * p) = h;
+  }
+}
+
+__device__ inline void store_vals(const MlaArgs& a, int64_t row, int head, int d0, const float* v, int n) {
+  uint16_t* o = a.out + row * a.o_rs + (int64_t)head * a.o_hs + d0;
+  for (int e = 0; e < n; e += 2) {
+    uint32_t packed;
+    if (a.out_dtype == XT_DTYPE_BF16)
+      packed = f32_to_bf16_bits(v[e]) | (f32_to_bf16_bits(v[e + 1]) << 16);
+    else
+      packed = f32_to_f16_bits(v[e]) | (f32_to_f16_bits(v[e + 1]) << 16);
+    *reinterpret_cast<uint32_t*>(o + e) = packed;
+  }
+}
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ inline void store_through(__amdgpu_buffer_rsrc_t r, int byte_off, float4_t v) {
+  const u32x4_t w = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+  __builtin_amdgcn_raw_buffer_store_b128(w, r, byte_off, 0, 16);
+}
+
+__global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  asm volatile("" ::"s"(a.xcd_units), "s"(a.xcd_extra), "s"(a.splits), "s"(a.keys_per_split), "s"(a.topk[0]),
+               "s"(a.topk[1]), "s"(a.idx[0]), "s"(a.idx[1]), "s"(a.idx_stride[0]), "s"(a.idx_stride[1]),
+               "s"(a.len[0]), "s"(a.len[1]), "s"(a.q), "s"(a.q_rs), "s"(a.q_hs), "s"(a.heads));
+  // XCD-aware numbering as in the decode kernel: a row's splits run on one XCD
+  const uint32_t gidx = blockIdx.x;
+  const uint32_t xcd = gidx & 7u;
+  const uint32_t u = xcd * a.xcd_units + min(xcd, a.xcd_extra) + (gidx >> 3);
+  const int split = (int)(u % (uint32_t)a.splits);
+  const int64_t row = u / (uint32_t)a.splits;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane & 15, j = lane >> 4;
+  const int head = 16 * wave + hl;
+  const bool head_live = head < a.heads;
+
+  _Float16* kt = reinterpret_cast<_Float16*>(lds);
+  _Float16* vt = reinterpret_cast<_Float16*>(lds + kKTile);
+  _Float16* qs = reinterpret_cast<_Float16*>(lds + kKTile + kVTile);
+  int32_t* slots = reinterpret_cast<int32_t*>(lds + kKTile + kVTile + kQTile);
+
+  // the query's B operands first: dims 32kk + 8j .. +7 of head `head` (a clamped valid head for padding lanes)
+  uint4 qraw[kQChunks];
+  {
+    const uint16_t* qp = a.q + row * a.q_rs + (int64_t)min(head, a.heads - 1) * a.q_hs;
+#pragma unroll
+    for (int kk = 0; kk < kQChunks; ++kk) qraw[kk] = *reinterpret_cast<const uint4*>(qp + 32 * kk + 8 * j);
+  }
+
+  // 1. the split's key list: columns [t0, t0 + keys_per_split) of list 0 then list 1, as slot entries in LDS
+  const int t0 = split * a.keys_per_split;
+  {
+    const int total = a.steps * kMSteps;
+    for (int i = threadIdx.x; i < total; i += 512) {
+      const int col = t0 + i;
+      int32_t e = -1;
+      if (i < a.keys_per_split) {
+        const int li = col < a.topk[0] ? 0 : 1;
+        const int cc = col - (li ? a.topk[0] : 0);
+        if (cc < a.topk[li]) {
+          const int n = a.len[li] ? min(a.len[li][row], a.topk[li]) : a.topk[li];
+          const int32_t s = cc < n ? a.idx[li][row * a.idx_stride[li] + cc] : -1;
+          if (s >= 0 && s < a.c[li].slots) e = li ? -s - 2 : s;
+        }
+      }
+      slots[i] = e;
+    }
+  }
+  __syncthreads();
+
+  // B operands of q.k: FP16 of q * scale * log2(e), chunks 0..kQReg-1 in registers, the rest in LDS
+  half8_t qb[kQReg];
+#pragma unroll
+  for (int kk = 0; kk < kQChunks; ++kk) {
+    const uint32_t ws[4] = {qraw[kk].x, qraw[kk].y, qraw[kk].z, qraw[kk].w};
+    half8_t h;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      h[2 * e] = head_live ? (_Float16)(bf16_bits_to_f32(ws[e] & 0xFFFFu) * a.qscale) : (_Float16)0.0f;
+      h[2 * e + 1] = head_live ? (_Float16)(bf16_bits_to_f32(ws[e] >> 16) * a.qscale) : (_Float16)0.0f;
+    }
+    if (kk < kQReg)
+      qb[kk < kQReg ? kk : 0] = h;
+    else
+      *reinterpret_cast<half8_t*>(qs + ((kk - kQReg) * kMHeads + 16 * wave + hl) * kQRow + 8 * j) = h;
+  }
+  const float g0 = *a.c[0].g, g1 = *a.c[1].g;
+
+  float m = -__builtin_inff(), l = 0.0f;
+  float4_t acc[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  Raw raw;
+  load_raw(a, slots, 0, raw);
+  for (int step = 0; step < a.steps; ++step) {
+    dequant(a, slots, step, raw, g0, g1, kt, vt);
+    __syncthreads();
+    if (step + 1 < a.steps) load_raw(a, slots, step + 1, raw);
+    const uint32_t valid = (uint32_t)__builtin_amdgcn_ballot_w64(lane < kMSteps &&
+                                                                  entry_valid(slots[step * kMSteps + (lane & 31)]));
+    // S^T for the two 16-key tiles
+    float4_t s[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      s[tt] = float4_t{0.f, 0.f, 0.f, 0.f};
+      const _Float16* kr = kt + (16 * tt + hl) * kKRow + 8 * j;
+#pragma unroll
+      for (int kk = 0; kk < kQChunks; ++kk) {
+        const half8_t qv = kk < kQReg ? qb[kk < kQReg ? kk : 0]
+                                      : *reinterpret_cast<const half8_t*>(
+                                            qs + ((kk - kQReg) * kMHeads + 16 * wave + hl) * kQRow + 8 * j);
+        s[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8_t*>(kr + 32 * kk), qv, s[tt],
+                                                       0, 0, 0);
+      }
+    }
+    // online softmax of head hl over keys T(j), lazy rescale
+    float sv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int key = (e < 4) ? (4 * j + e) : (16 + 4 * j + (e - 4));
+      sv[e] = ((valid >> key) & 1u) ? s[e >> 2][e & 3] : -__builtin_inff();
+    }
+    float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+    mt = fmaxf(mt, __shfl_xor(mt, 16));
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    if (__builtin_amdgcn_ballot_w64(mt > m + kRescaleM)) {
+      const float m_new = (mt > m + kRescaleM) ? mt : m;
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) acc[i] *= alpha;
+      m = m_new;
+    }
+    const float m_use = (m == -__builtin_inff()) ? 0.0f : m;
+    half8_t pb;
+    float psum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p = __builtin_amdgcn_exp2f(sv[e] - m_use);
+      psum += p;
+      pb[e] = (_Float16)p;
+    }
+    l += psum;
+    // O^T += V^T . P^T over the 32 dim tiles
+    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int dt = 0; dt < 32; ++dt) {
+      const _Float16* vr = vt + (16 * dt + hl) * kVRow + 4 * j;
+      const half4_t lo = *reinterpret_cast<const half4_t*>(vr);
+      const half4_t hi = *reinterpret_cast<const half4_t*>(vr + 16);
+      const half8_t av = half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb, acc[dt], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  // the 4 lanes of a head hold disjoint key subsets of l
+  float l_tot = l + __shfl_xor(l, 16);
+  l_tot += __shfl_xor(l_tot, 32);
+
+  if (a.splits == 1) {
+    if (!head_live) return;
+    const float m_use = (m == -__builtin_inff()) ? 0.0f : m;
+    float total = l_tot;
+    if (a.sink) total += __builtin_amdgcn_exp2f(a.sink[head] * kLog2e - m_use);
+    const float inv = l_tot > 0.0f ? 1.0f / total : 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < 32; ++dt) {
+      const float v[4] = {acc[dt][0] * inv, acc[dt][1] * inv, acc[dt][2] * inv, acc[dt][3] * inv};
+      store_vals(a, row, head, 16 * dt + 4 * j, v, 4);
+    }
+    if (a.lse && j == 0)
+      a.lse[row * a.heads + head] = l_tot > 0.0f ? (m + __builtin_log2f(l_tot)) * kLn2 : -__builtin_inff();
+    return;
+  }
+  // 2. partials of this row (written through), the last workgroup of the row merges them
+  float* row_part = a.part + row * a.splits * a.heads * kMPart;
+  const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+      row_part, (short)0, (int)((int64_t)a.splits * a.heads * kMPart * 4), 0x00020000);
+  if (head_live) {
+    const int at = ((split * a.heads + head) * kMPart) * 4;
+#pragma unroll
+    for (int dt = 0; dt < 32; ++dt) store_through(pr, at + (16 * dt + 4 * j) * 4, acc[dt]);
+    if (j == 0) store_through(pr, at + kDl * 4, float4_t{m, l_tot, 0.0f, 0.0f});
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  __shared__ int32_t s_last;
+  int32_t* counter = a.counters + row;
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.splits - 1;
+  __syncthreads();
+  if (!s_last) return;
+  // 512 threads: head t / 4, dims 128 (t % 4) .. +127
+  for (int hh = threadIdx.x >> 2; hh < a.heads; hh += 128) {
+    const int d0 = 128 * (threadIdx.x & 3);
+    const float* base = row_part + (int64_t)hh * kMPart;
+    const int64_t sstride = (int64_t)a.heads * kMPart;
+    float mx = -__builtin_inff();
+    for (int sp = 0; sp < a.splits; ++sp) mx = fmaxf(mx, base[sp * sstride + kDl]);
+    const float mu = (mx == -__builtin_inff()) ? 0.0f : mx;
+    float total = 0.0f;
+    for (int sp = 0; sp < a.splits; ++sp)
+      total += __builtin_amdgcn_exp2f(base[sp * sstride + kDl] - mu) * base[sp * sstride + kDl + 1];
+    const float l_all = total;
+    if (a.sink) total += __builtin_amdgcn_exp2f(a.sink[hh] * kLog2e - mu);
+    const float inv = l_all > 0.0f ? 1.0f / total : 0.0f;
+    for (int c = 0; c < 128; c += 8) {
+      float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int sp = 0; sp < a.splits; ++sp) {
+        const float w = __builtin_amdgcn_exp2f(base[sp * sstride + kDl] - mu) * inv;
+        const float4_t x0 = reinterpret_cast<const float4_t*>(base + sp * sstride + d0 + c)[0];
+        const float4_t x1 = reinterpret_cast<const float4_t*>(base + sp * sstride + d0 + c)[1];
+        o[0] += w * x0[0]; o[1] += w * x0[1]; o[2] += w * x0[2]; o[3] += w * x0[3];
+        o[4] += w * x1[0]; o[5] += w * x1[1]; o[6] += w * x1[2]; o[7] += w * x1[3];
+      }
+      store_vals(a, row, hh, d0 + c, o, 8);
+    }
+    if (a.lse && d0 == 0)
+      a.lse[row * a.heads + hh] = l_all > 0.0f ? (mu + __builtin_log2f(l_all)) * kLn2 : -__builtin_inff();
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+int check_cache(const char* what, const xt_mla_cache* c, int64_t* pay_stride, int64_t* sf_stride,
+                int64_t* rope_stride) {
+  if (!c->pay || !c->scales || !c->rope || !c->g) return fail(XT_EINVAL, "%s: a cache pointer is null", what);
+  if (c->slots <= 0 || c->slots > 0x3FFFFFFFLL)
+    return fail(XT_EINVAL, "%s: cache slots %lld outside 1..2^30-1", what, (long long)c->slots);
+  *pay_stride = c->pay_stride ? c->pay_stride : kDl / 2;
+  *sf_stride = c->sf_stride ? c->sf_stride : kDl / 16;
+  *rope_stride = c->rope_stride ? c->rope_stride : kDr * 2;
+  if (*pay_stride < kDl / 2 || *pay_stride % 4 || *sf_stride < kDl / 16 || *rope_stride < kDr * 2 ||
+      *rope_stride % 16 || !aligned(c->pay, 4) || !aligned(c->rope, 16))
+    return fail(XT_EINVAL, "%s: cache strides %lld / %lld / %lld bytes or alignment do not fit the latent rows", what,
+                (long long)*pay_stride, (long long)*sf_stride, (long long)*rope_stride);
+  return XT_OK;
+}
+
+}  // namespace
+}  // namespace xt
+
+using namespace xt;
+
+// Workspace: [arrival counters, kCounterBytes][partials [rows, splits, heads, kMPart] FP32]
+
+extern "C" size_t xt_sparse_mla_workspace_bytes(int rows, int heads, int splits) {
+  if (rows < 0 || heads <= 0 || splits <= 0) return 0;
+  if (splits == 1) return 256;
+  return kCounterBytes + (size_t)rows * splits * heads * kMPart * sizeof(float);
+}
+
+extern "C" int xt_sparse_mla_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, int heads,
+                                   int latent_dim, int rope_dim, const xt_mla_cache* cache, const xt_mla_keys* keys,
+                                   const xt_mla_cache* extra_cache, const xt_mla_keys* extra_keys, const float* sink,
+                                   float scale, void* out, int64_t out_row_stride, int64_t out_head_stride,
+                                   int out_dtype, float* lse, int rows, int splits, void* workspace,
+                                   size_t workspace_bytes, xt_stream_t stream) {
+  const char* what = "xt_sparse_mla_nvfp4";
+  if (latent_dim != kDl || rope_dim != kDr)
+    return fail(XT_EUNSUPPORTED, "%s: latent %d + rope %d (supported: %d + %d)", what, latent_dim, rope_dim, kDl, kDr);
+  if (heads <= 0 || heads > kMHeads) return fail(XT_EUNSUPPORTED, "%s: %d heads (supported: 1..%d)", what, heads,
+                                                 kMHeads);
+  if (rows < 0 || splits < 1 || splits > 64) return fail(XT_EINVAL, "%s: bad rows %d / splits %d", what, rows, splits);
+  if (out_dtype != XT_DTYPE_BF16 && out_dtype != XT_DTYPE_F16)
+    return fail(XT_EINVAL, "%s: output dtype must be BF16 or FP16", what);
+  if (!cache || !keys) return fail(XT_EINVAL, "%s: the key cache and key list are required", what);
+  if (rows == 0) return ok();
+  if (!q || !out || !workspace || !keys->indices) return fail(XT_EINVAL, "%s: a required pointer is null", what);
+  if (!aligned(q, 16) || q_row_stride % 8 || q_head_stride % 8 || !aligned(out, 16) || out_row_stride % 8 ||
+      out_head_stride % 8)
+    return fail(XT_EINVAL, "%s: q and out rows must be 16-byte aligned (strides in elements: multiples of 8)", what);
+  if (keys->topk < 0 || (extra_keys && extra_keys->topk < 0)) return fail(XT_EINVAL, "%s: negative topk", what);
+  const bool extra = extra_cache && extra_keys && extra_keys->indices && extra_keys->topk > 0;
+  MlaArgs a;
+  int64_t ps, ss, rs;
+  int st = check_cache(what, cache, &ps, &ss, &rs);
+  if (st != XT_OK) return st;
+  a.c[0] = CacheDev{cache->pay, cache->scales, static_cast<const uint16_t*>(cache->rope), cache->g, cache->slots, ps,
+                    ss, rs};
+  if (extra) {
+    st = check_cache(what, extra_cache, &ps, &ss, &rs);
+    if (st != XT_OK) return st;
+    a.c[1] = CacheDev{extra_cache->pay, extra_cache->scales, static_cast<const uint16_t*>(extra_cache->rope),
+                      extra_cache->g, extra_cache->slots, ps, ss, rs};
+  } else {
+    a.c[1] = a.c[0];
+  }
+  if (splits > 1 && rows > kCounterSlots)
+    return fail(XT_EUNSUPPORTED, "%s: %d rows with key splits exceed %d arrival counters; use splits 1", what, rows,
+                kCounterSlots);
+  const size_t need = xt_sparse_mla_workspace_bytes(rows, heads, splits);
+  if (workspace_bytes < need)
+    return fail(XT_EWORKSPACE, "%s: workspace %zu bytes < %zu needed", what, workspace_bytes, need);
+  if (!aligned(workspace, 256)) return fail(XT_EINVAL, "%s: workspace must be 256-byte aligned", what);
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_rs = q_row_stride;
+  a.q_hs = q_head_stride;
+  a.idx[0] = keys->indices;
+  a.idx_stride[0] = keys->stride;
+  a.topk[0] = keys->topk;
+  a.len[0] = keys->lengths;
+  a.idx[1] = extra ? extra_keys->indices : keys->indices;
+  a.idx_stride[1] = extra ? extra_keys->stride : keys->stride;
+  a.topk[1] = extra ? extra_keys->topk : 0;
+  a.len[1] = extra ? extra_keys->lengths : nullptr;
+  a.sink = sink;
+  a.qscale = scale * kLog2e;
+  a.out = static_cast<uint16_t*>(out);
+  a.o_rs = out_row_stride;
+  a.o_hs = out_head_stride;
+  a.out_dtype = out_dtype;
+  a.lse = lse;
+  a.heads = heads;
+  a.splits = splits;
+  const int total_keys = a.topk[0] + a.topk[1];
+  a.keys_per_split = (((total_keys + splits - 1) / splits + kMSteps - 1) / kMSteps) * kMSteps;
+  a.steps = a.keys_per_split / kMSteps;
+  if (a.keys_per_split == 0) {
+    a.keys_per_split = kMSteps;   // no keys: one all-invalid step writes the zero rows
+    a.steps = 1;
+  }
+  const size_t lds_bytes = (size_t)kKTile + kVTile + kQTile + (size_t)a.steps * kMSteps * 4;
+  if (lds_bytes > 160 * 1024 - 256)
+    return fail(XT_EUNSUPPORTED, "%s: %d keys per split need %zu bytes of LDS; use more splits", what,
+                a.keys_per_split, lds_bytes);
+  a.counters = static_cast<int32_t*>(workspace);
+  a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+  const int64_t n_units = (int64_t)rows * splits;
+  if (n_units > 0x7FFFFFFFLL) return fail(XT_EUNSUPPORTED, "%s: %lld workgroups", what, (long long)n_units);
+  a.xcd_units = (uint32_t)(n_units / 8);
+  a.xcd_extra = (uint32_t)(n_units % 8);
+  // dynamic LDS above 64 KB must be allowed per kernel; raised to the largest size asked for so far
+  static size_t lds_allowed = 64 * 1024;
+  if (lds_bytes > lds_allowed) {
+    const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&mla_kernel),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
+    if (err != hipSuccess)
+      return fail(XT_ELAUNCH, "%s: could not allow %zu bytes of LDS: %s", what, lds_bytes, hipGetErrorString(err));
+    lds_allowed = lds_bytes;
+  }
+  hipLaunchKernelGGL(mla_kernel, dim3((unsigned)n_units), dim3(64 * kMWaves), lds_bytes,
+                     reinterpret_cast<hipStream_t>(stream), a);
+  return check_launch(what);
+}

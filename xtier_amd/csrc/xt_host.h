@@ -17,4 +17,10 @@ int check_launch(const char* what);
 
 inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+// Workspaces of the split kernels (fused decode, sparse MLA) begin with a fixed region of arrival counters, one per
+// (row, head group) of a call: zero before the first call, left zero by every call. Split partials follow it, so calls
+// of any shape, of either kernel, may share one workspace as long as they do not overlap in time.
+constexpr int kCounterSlots = 16384;
+constexpr size_t kCounterBytes = (size_t)kCounterSlots * 4;
+
 }  // namespace xt

@@ -5,6 +5,7 @@ xtier/backend/formats.py). Tensors are torch tensors on the GPU; every call runs
 ``raw`` is the reference's tuple of a layer's pool buffers (qsa_fp4.py:43-58):
 (k_pay u8 [slots, kv_heads, dim/2], v_pay, k_scales u8 [slots, kv_heads, dim/16], v_scales, gk f32 [1], gv f32 [1]).
 """
+import ctypes
 import math
 
 import torch
@@ -219,3 +220,97 @@ def sparse_decode(q, raw, table, indices, seq_lens, scale, page_size=1, row_req=
         _ptr(seq_lens), _ptr(query_pos), float(scale), _ptr(out), out.stride(0), out.stride(1), _DTYPES[out.dtype],
         _ptr(lse), rows, int(splits), _ptr(ws), ws.numel(), _stream(q)), 'sparse_decode')
     return out
+
+
+# --- sparse MLA ----------------------------------------------------------------------------------------------------
+
+def _mla_cache(raw):
+    """(pay u8 [slots, Dl/2], scales u8 [slots, Dl/16], rope BF16 [slots, Dr], g f32 [1]) -> xt_mla_cache, dims."""
+    if hasattr(raw, 'raw'):
+        raw = raw.raw
+    pay, sc, rope, g = raw
+    _need_cuda(pay, sc, rope, g)
+    if (pay.dtype != torch.uint8 or sc.dtype != torch.uint8 or rope.dtype != torch.bfloat16 or pay.dim() != 2
+            or pay.stride(1) != 1 or sc.stride(1) != 1 or rope.stride(1) != 1 or sc.shape[1] * 8 != pay.shape[1]
+            or not (pay.shape[0] == sc.shape[0] == rope.shape[0])):
+        raise ValueError('xtier_amd.sparse_mla: cache (pay u8 [slots, latent/2], scales u8 [slots, latent/16], '
+                         'rope BF16 [slots, rope_dim], g f32 [1]) with packed rows expected')
+    g = g if g.dtype == torch.float32 else g.float()
+    c = _lib.MlaCache(_ptr(pay), _ptr(sc), _ptr(rope), _ptr(g), pay.shape[0], pay.stride(0), sc.stride(0),
+                      rope.stride(0) * 2)
+    return c, pay.shape[1] * 2, rope.shape[1], (pay, sc, rope, g)
+
+
+def _mla_keys(indices, lengths, rows):
+    indices = indices.reshape(rows, -1)
+    if indices.dtype != torch.int32 or indices.stride(-1) != 1:
+        indices = indices.to(torch.int32).contiguous()
+    if lengths is not None:
+        lengths = lengths.reshape(rows)
+        if lengths.dtype != torch.int32:
+            lengths = lengths.to(torch.int32)
+        lengths = lengths.contiguous()
+    _need_cuda(indices, lengths)
+    return _lib.MlaKeys(_ptr(indices), indices.stride(0), indices.shape[1], _ptr(lengths)), (indices, lengths)
+
+
+def default_mla_splits(rows, topk):
+    """Key splits per row for sparse MLA: about 256 workgroups (one per CU) and at least 256 keys per split."""
+    return max(1, min(math.ceil(256 / max(1, rows)), max(1, topk // 256), 64))
+
+
+def mla_workspace_bytes(rows, heads, splits):
+    return int(_lib.lib().xt_sparse_mla_workspace_bytes(rows, heads, splits))
+
+
+def sparse_mla(q, k_cache, indices, topk_length, attn_sink, softmax_scale, extra_k_cache=None, extra_indices=None,
+               extra_topk_length=None, out=None, lse=None, splits=None, ws=None):
+    """sparse_mla (xtier/packs/deepseek_v4/sparse_mla.py:167-217) on an NVFP4 latent cache: q [rows, 1, heads, 576]
+    (or [rows, heads, 576]) BF16, indices [rows, 1, topk] slots of k_cache (-1: none), optional extra_* into a second
+    cache, attn_sink [heads] FP32 or None. k_cache: a LatentPool or (pay, scales, rope, g). Returns (out [rows, 1,
+    heads, 512] BF16, lse [rows, heads, 1] FP32, natural log of the keys' sum) as the reference does."""
+    shape4 = q.dim() == 4
+    if shape4:
+        rows, s_q, heads, dim = q.shape
+        if s_q != 1:
+            raise NotImplementedError(f'xtier_amd.sparse_mla: one query per row expected, not {tuple(q.shape)}')
+        q = q.reshape(rows, heads, dim)
+    else:
+        rows, heads, dim = q.shape
+    cache, dl, dr, keep = _mla_cache(k_cache)
+    if dim != dl + dr:
+        raise NotImplementedError(f'xtier_amd.sparse_mla: q head size {dim} != latent {dl} + rope {dr}')
+    _need_cuda(q, attn_sink, out, lse)
+    if q.dtype != torch.bfloat16 or q.stride(-1) != 1:
+        q = q.to(torch.bfloat16).contiguous()
+    keys, keep_k = _mla_keys(indices, topk_length, rows)
+    extra = extra_k_cache is not None and extra_indices is not None
+    cache2 = keys2 = None
+    if extra:
+        cache2, dl2, dr2, keep2 = _mla_cache(extra_k_cache)
+        if (dl2, dr2) != (dl, dr):
+            raise ValueError('xtier_amd.sparse_mla: both caches must have the same latent and rope widths')
+        keys2, keep_k2 = _mla_keys(extra_indices, extra_topk_length, rows)
+    if out is None:
+        out = torch.empty((rows, heads, dl), dtype=torch.bfloat16, device=q.device)
+    if lse is None:
+        lse = torch.empty((rows, heads), dtype=torch.float32, device=q.device)
+    if attn_sink is not None and (attn_sink.dtype != torch.float32 or not attn_sink.is_contiguous()):
+        attn_sink = attn_sink.float().contiguous()
+    topk_all = keys.topk + (keys2.topk if extra else 0)
+    if splits is None:
+        splits = default_mla_splits(rows, topk_all)
+        if ws is None and torch.cuda.is_current_stream_capturing() and rows and \
+                _cached_workspace_bytes(q.device) < mla_workspace_bytes(rows, heads, splits):
+            splits = 1
+    need = mla_workspace_bytes(rows, heads, splits)
+    if ws is None:
+        ws = (workspace(q.device, need) if _cached_workspace_bytes(q.device) >= need
+              or not torch.cuda.is_current_stream_capturing()
+              else torch.empty(need, dtype=torch.uint8, device=q.device))
+    _lib.check(_lib.lib().xt_sparse_mla_nvfp4(
+        _ptr(q), q.stride(0), q.stride(1), heads, dl, dr, ctypes.byref(cache), ctypes.byref(keys),
+        ctypes.byref(cache2) if extra else None, ctypes.byref(keys2) if extra else None, _ptr(attn_sink),
+        float(softmax_scale), _ptr(out), out.stride(0), out.stride(1), _DTYPES[out.dtype], _ptr(lse), rows,
+        int(splits), _ptr(ws), ws.numel(), _stream(q)), 'sparse_mla')
+    return (out.unsqueeze(1), lse.unsqueeze(-1)) if shape4 else (out, lse)

@@ -57,3 +57,44 @@ class KVPool:
         """NVFP4 quantize-on-append of K and V rows [n, kv_heads, dim] (BF16) at pool slots [n]."""
         ops.quantize_append(k, slots, self.gk, self.k_pay, self.k_sf, saturate=saturate)
         ops.quantize_append(v, slots, self.gv, self.v_pay, self.v_sf, saturate=saturate)
+
+
+class LatentPool:
+    """One layer's sparse-MLA cache: per slot an NVFP4 latent row (latent_dim values: payload latent_dim/2 bytes, E4M3
+    scales latent_dim/16 bytes, FP32 global scale g on the device) and a BF16 rope row (rope_dim values).
+
+    layout 'interleaved' (default): one buffer, per slot [payload | scales | rope] (416 bytes at 512 + 64), so a key is
+    one contiguous record; 'split': three buffers. `raw` is (pay [slots, latent/2], scales [slots, latent/16],
+    rope [slots, rope_dim] BF16, g [1]) as strided views either way."""
+
+    def __init__(self, slots, latent_dim=512, rope_dim=64, device='cuda', layout='interleaved', g=None):
+        self.slots, self.latent_dim, self.rope_dim, self.layout = slots, latent_dim, rope_dim, layout
+        pb, sb, rb = latent_dim // 2, latent_dim // 16, rope_dim * 2
+        if layout == 'interleaved':
+            rec = pb + sb + rb
+            self.buffer = torch.zeros(slots, rec, dtype=torch.uint8, device=device)
+            self.pay = self.buffer[:, :pb]
+            self.scales = self.buffer[:, pb:pb + sb]
+            self.rope = self.buffer[:, pb + sb:].view(torch.bfloat16)
+        elif layout == 'split':
+            self.buffer = None
+            self.pay = torch.zeros(slots, pb, dtype=torch.uint8, device=device)
+            self.scales = torch.zeros(slots, sb, dtype=torch.uint8, device=device)
+            self.rope = torch.zeros(slots, rope_dim, dtype=torch.bfloat16, device=device)
+        else:
+            raise ValueError(f'unknown layout {layout!r}')
+        self.g = g if g is not None else torch.ones(1, dtype=torch.float32, device=device)
+
+    @property
+    def raw(self):
+        return (self.pay, self.scales, self.rope, self.g)
+
+    def set_global_scale(self, latent):
+        """g = amax(|latent|) / (6 * 448), computed on the device (formats.py:122)."""
+        self.g = ops.global_scale(latent.reshape(latent.shape[0], 1, -1))
+
+    def append(self, latent, rope, slots, saturate=True):
+        """Quantize BF16 latent rows [n, latent_dim] with the pool's g into `slots` and copy their rope rows."""
+        ops.quantize_append(latent.reshape(latent.shape[0], 1, -1), slots, self.g, self.pay.unsqueeze(1),
+                            self.scales.unsqueeze(1), saturate=saturate)
+        self.rope.index_copy_(0, slots, rope.to(torch.bfloat16))

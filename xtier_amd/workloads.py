@@ -86,6 +86,49 @@ PREFILL_WORKLOADS = {
 }
 
 
+@dataclass(frozen=True)
+class MlaWorkload:
+    """Sparse MLA, DeepSeek-style: `heads` query heads share one latent key per token (latent NVFP4 + rope BF16).
+    Decode: `rows` requests, one query each, top-k uniform over the request's context. Prefill (causal): one request,
+    the last `rows` positions of its context as queries, each with its own causal top-k (the `recent` most recent
+    included)."""
+    name: str
+    rows: int
+    heads: int
+    ctx: int
+    topk: int
+    causal: bool = False
+    latent: int = 512
+    rope: int = 64
+    q_std: float = 0.5
+    recent: int = 128
+    page: int = 64
+
+    @property
+    def requests(self):
+        return 1 if self.causal else self.rows
+
+    @property
+    def slots(self):
+        return self.requests * self.ctx
+
+    def algorithmic_bytes(self):
+        """Gathered latent payload + scales + rope: rows * topk * (latent/2 + latent/16 + 2 * rope)."""
+        return self.rows * self.topk * (self.latent // 2 + self.latent // 16 + 2 * self.rope)
+
+    def flops(self):
+        """q.k over latent + rope and p.v over the latent: rows * heads * topk * (2 (Dl + Dr) + 2 Dl)."""
+        return self.rows * self.heads * self.topk * (2 * (self.latent + self.rope) + 2 * self.latent)
+
+
+MLA_WORKLOADS = {
+    # 64 requests decoding at context 131072, 128 heads, top-2048 uniform
+    'mla_decode_b64': MlaWorkload('mla_decode_b64', 64, 128, 131072, 2048),
+    # a 2048-token prefill chunk at the end of a 131072-token context, top-2048 causal per query
+    'mla_prefill_2048': MlaWorkload('mla_prefill_2048', 2048, 128, 131072, 2048, causal=True),
+}
+
+
 def generator(device, seed):
     g = torch.Generator(device=device)
     g.manual_seed(seed)
@@ -194,3 +237,35 @@ def prefill_inputs(w, seed, device='cpu'):
     q_pos = torch.arange(w.ctx0, w.ctx, dtype=torch.int32, device=device)
     idx = causal_index_lists(q_pos, w.topk, w.recent, gen, device)
     return PrefillInputs(w, q, k, v, pt, idx, q_pos)
+
+
+@dataclass
+class MlaInputs:
+    workload: MlaWorkload
+    q: torch.Tensor            # bf16 [rows, heads, latent + rope]
+    slots: torch.Tensor        # int32 [rows, topk]: cache slots of each row's keys
+    positions: torch.Tensor    # int32 [rows, topk]: their positions in the request's context
+
+
+def mla_cache_rows(w, gen, device, start, n):
+    """Latent BF16 [n, latent] (N(0,1), 1% outlier channels x8) and rope BF16 [n, rope] (N(0,1)) for cache rows
+    start .. start+n-1 of a workload's pool (generated in order from `gen`)."""
+    lat = kv_tensor(n, 1, w.latent, gen, device).view(n, w.latent)
+    rope = torch.randn(n, w.rope, generator=gen, device=device).to(torch.bfloat16)
+    return lat, rope
+
+
+def mla_inputs(w, seed, device='cpu'):
+    """Seeded queries and key lists of an MLA workload (the cache rows come from mla_cache_rows)."""
+    gen = generator(device, seed)
+    q = (torch.randn(w.rows, w.heads, w.latent + w.rope, generator=gen, device=device) * w.q_std).to(torch.bfloat16)
+    pt = page_table(w.requests, w.ctx, w.page, gen, device)
+    if w.causal:
+        q_pos = torch.arange(w.ctx - w.rows, w.ctx, dtype=torch.int32, device=device)
+        pos = causal_index_lists(q_pos, w.topk, w.recent, gen, device)
+        req = torch.zeros(w.rows, dtype=torch.long, device=device)
+    else:
+        pos = index_lists(w.rows, w.ctx, w.topk, gen, device)
+        req = torch.arange(w.rows, device=device)
+    slots = (pt[req[:, None], (pos // w.page).long()].long() * w.page + pos % w.page).to(torch.int32)
+    return MlaInputs(w, q, slots, pos)
