@@ -179,13 +179,91 @@ def run_prefill(args, w, ops, workloads, KVPool):
     print(json.dumps(record), flush=True)
 
 
+def build_latent_pool(w, seed, layout, workloads, LatentPool, chunk=1 << 20):
+    """One layer's latent cache of w.slots tokens, generated in chunks of `chunk` rows (seed + chunk index each): a
+    first pass takes the latent amax for g = amax / 2688, a second quantizes the rows into the pool."""
+    import torch
+    pool = LatentPool(w.slots, w.latent, w.rope, 'cuda', layout=layout)
+    amax = torch.zeros((), device='cuda')
+    starts = list(range(0, w.slots, chunk))
+    for i, st in enumerate(starts):
+        lat, _ = workloads.mla_cache_rows(w, workloads.generator('cuda', seed * 1000 + i), 'cuda', st,
+                                          min(chunk, w.slots - st))
+        amax = torch.maximum(amax, lat.abs().max().float())
+    pool.g = torch.clamp(amax / 2688.0, min=1e-12).reshape(1).to(torch.float32)
+    for i, st in enumerate(starts):
+        n = min(chunk, w.slots - st)
+        lat, rope = workloads.mla_cache_rows(w, workloads.generator('cuda', seed * 1000 + i), 'cuda', st, n)
+        pool.append(lat, rope, torch.arange(st, st + n, device='cuda'), saturate=False)
+    return pool
+
+
+def run_mla(args, w, ops, workloads):
+    """Sparse MLA steps (decode: one query per request; prefill: a causal chunk) over NVFP4 latent caches, rotating
+    `layers` distinct caches for decode. One JSON line: TFLOP/s against the dense FP16 MFMA peak."""
+    import torch
+    from xtier_amd.pool import LatentPool
+    torch.cuda.set_device(0)
+    t0 = time.time()
+    layers = 1 if w.causal else max(1, min(args.layers, 6))
+    pools = [build_latent_pool(w, 17 + l, args.layout, workloads, LatentPool) for l in range(layers)]
+    inp = workloads.mla_inputs(w, 20261029, 'cuda')
+    scale = 1.0 / math.sqrt(w.latent + w.rope)
+    splits = args.splits or ops.default_mla_splits(w.rows, w.topk)
+    ws = ops.workspace('cuda', ops.mla_workspace_bytes(w.rows, w.heads, splits))
+    out = torch.empty(w.rows, w.heads, w.latent, dtype=torch.bfloat16, device='cuda')
+    lse = torch.empty(w.rows, w.heads, dtype=torch.float32, device='cuda')
+    torch.cuda.synchronize()
+    log(f'built {layers} latent caches of {w.slots} tokens in {time.time() - t0:.1f} s')
+
+    def step(layer):
+        ops.sparse_mla(inp.q, pools[layer], inp.slots, None, None, scale, out=out, lse=lse, splits=splits, ws=ws)
+
+    for i in range(max(1, args.warmup)):
+        step(i % layers)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for layer in range(layers):
+            step(layer)
+    graph.replay()
+    torch.cuda.synchronize()
+    replays = max(1, math.ceil(args.steps / layers))
+    steps = replays * layers
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    tflops = w.flops() / (ms * 1e-3) / 1e12
+    gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
+    log(f'{w.name}: {ms * 1e3:.1f} us per step, {tflops:.1f} TFLOP/s ({tflops / MFMA_PEAK_TFLOPS:.1%} of '
+        f'{MFMA_PEAK_TFLOPS:.0f}), {gbs:.0f} GB/s gathered, splits {splits}')
+    record = {
+        'metric': 'NVFP4 sparse MLA attention TFLOP/s', 'value': round(tflops, 2), 'unit': 'TFLOP/s', 'n_gpus': 1,
+        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'higher_is_better': True,
+        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f16', 'data': 'synthetic',
+        'config': {'workload': w.name, 'rows': w.rows, 'heads': w.heads, 'latent': w.latent, 'rope': w.rope,
+                   'context': w.ctx, 'topk': w.topk, 'causal': w.causal, 'kv_format': 'nvfp4 latent + bf16 rope',
+                   'layers_rotated': layers, 'splits': splits, 'cache_layout': args.layout},
+        'us_per_step': round(ms * 1e3, 2), 'gathered_gbs': round(gbs, 1),
+        'roofline': {'bound': 'mfma', 'achieved': round(tflops, 2), 'peak': MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
+                     'frac': round(tflops / MFMA_PEAK_TFLOPS, 4), 'traffic': None},
+        'cpu_baseline': None,
+    }
+    print(json.dumps(record), flush=True)
+
+
 def main():
     p = argparse.ArgumentParser()
     p.add_argument('--gpus', type=int, default=1)
     p.add_argument('--steps', type=int, default=512)
     p.add_argument('--warmup', type=int, default=64)
     p.add_argument('--workload', default='gqa_decode_b32',
-                   help='gqa_decode_b32 (default), cpu_ref_decode, long_ctx_decode_b4 or gqa_prefill_chunk4096')
+                   help='gqa_decode_b32 (default), cpu_ref_decode, long_ctx_decode_b4, gqa_prefill_chunk4096, '
+                        'mla_decode_b64 or mla_prefill_2048')
     p.add_argument('--layers', type=int, default=16)
     p.add_argument('--splits', type=int, default=None)
     p.add_argument('--layout', default='interleaved', choices=['interleaved', 'split'],
@@ -215,6 +293,8 @@ def main():
     from xtier_amd import ops, workloads
     from xtier_amd.pool import KVPool
 
+    if args.workload in workloads.MLA_WORKLOADS:
+        return run_mla(args, workloads.MLA_WORKLOADS[args.workload], ops, workloads)
     if args.workload in workloads.PREFILL_WORKLOADS:
         return run_prefill(args, workloads.PREFILL_WORKLOADS[args.workload], ops, workloads, KVPool)
     w = workloads.WORKLOADS[args.workload]

@@ -32,10 +32,10 @@ constexpr int kMSteps = 32;              // keys per step
 constexpr int kMWaves = 8;
 constexpr int kMHeads = 16 * kMWaves;    // heads per workgroup
 constexpr int kKRow = kDk + 8;           // halves per K tile row (16-byte pad)
-constexpr int kVRow = kMSteps + 8;       // halves per V^T tile row
+constexpr int kVRow = kMSteps + 4;       // halves per V^T tile row (72 bytes: the PV reads and the dequant writes of
+                                         // a wave fall on distinct LDS banks)
 constexpr int kKTile = kMSteps * kKRow * 2;
 constexpr int kVTile = kDl * kVRow * 2;
-constexpr int kMPart = kDl + 4;          // floats per partial (row, split, head): 512 accumulators, max, sum, pad
 constexpr int kQChunks = kDk / 32;       // 32-dim chunks of a query row
 constexpr int kQReg = 12;                // chunks kept in registers; the others (4 latent + 2 rope) live in LDS
 constexpr int kQRow = 32 + 8;            // halves per (chunk, head) row of the LDS query block
@@ -47,7 +47,8 @@ struct CacheDev {
   const uint8_t* sf;
   const uint16_t* rope;
   const float* g;
-  int64_t slots, pay_stride, sf_stride, rope_stride;   // strides in bytes
+  int64_t slots;
+  uint32_t pay_stride, sf_stride, rope_stride;   // bytes from one slot to the next
 };
 
 struct MlaArgs {
@@ -65,7 +66,8 @@ struct MlaArgs {
   int out_dtype;
   float* lse;
   int heads, splits, keys_per_split, steps;
-  float* part;                       // [rows, splits, heads, kMPart]
+  uint16_t* part;                    // [rows, splits, heads, 512] FP16: the split's output normalized by its own sum
+  float* ml;                         // [rows, splits, heads, 2]: the split's running max (log2 domain) and sum
   int32_t* counters;                 // [rows]
   uint32_t xcd_units, xcd_extra;
 };
@@ -73,42 +75,57 @@ struct MlaArgs {
 // Slot list entries: >= 0 a slot of cache 0, <= -2 slot (-e - 2) of cache 1, -1 no key.
 __device__ inline bool entry_valid(int32_t e) { return e != -1; }
 
+// Dequant mapping: thread t handles keys 4kq .. 4kq+3 (kq = t % 8) and latent dims 8c .. 8c+7 (c = t / 8), so a
+// wave's V^T writes spread over 8 key columns and 8 dim rows (no LDS bank conflicts); rope: key t / 8, part t % 8.
 struct Raw {
   uint32_t pay[4];   // payload bytes 4c .. 4c+3 of keys 4kq + i
   uint32_t sc[4];    // scale byte c / 2 of those keys
   uint4 rope;        // rope values 8p .. 8p+7 of key t / 8 (threads 0-255)
 };
 
+// The record of slot list entry e: with one key list the entry is the slot (or -1: slot 0, ignored); with two the
+// cache is chosen per key.
+template <bool TWO>
+__device__ inline const CacheDev& cache_of(const MlaArgs& a, int32_t e, uint32_t& s) {
+  if (!TWO) {
+    s = e < 0 ? 0u : (uint32_t)e;
+    return a.c[0];
+  }
+  s = e >= 0 ? (uint32_t)e : (e <= -2 ? (uint32_t)(-e - 2) : 0u);
+  return a.c[e <= -2 ? 1 : 0];
+}
+
+template <bool TWO>
 __device__ inline void load_raw(const MlaArgs& a, const int32_t* slots, int step, Raw& r) {
-  const int t = threadIdx.x, kq = t >> 6, c = t & 63;
+  const int t = threadIdx.x, kq = t & 7, c = t >> 3;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int32_t e = slots[step * kMSteps + 4 * kq + i];
-    const int ci = e <= -2 ? 1 : 0;
-    const int64_t s = e >= 0 ? e : (e <= -2 ? (int64_t)(-e - 2) : 0);
-    const CacheDev& cd = a.c[ci];
-    r.pay[i] = *reinterpret_cast<const uint32_t*>(cd.pay + s * cd.pay_stride + 4 * c);
-    r.sc[i] = cd.sf[s * cd.sf_stride + (c >> 1)];
+    uint32_t s;
+    const CacheDev& cd = cache_of<TWO>(a, slots[step * kMSteps + 4 * kq + i], s);
+    r.pay[i] = *reinterpret_cast<const uint32_t*>(cd.pay + (uint64_t)s * cd.pay_stride + 4 * c);
+    r.sc[i] = cd.sf[(uint64_t)s * cd.sf_stride + (c >> 1)];
   }
   if (t < 256) {
-    const int32_t e = slots[step * kMSteps + (t >> 3)];
-    const int ci = e <= -2 ? 1 : 0;
-    const int64_t s = e >= 0 ? e : (e <= -2 ? (int64_t)(-e - 2) : 0);
-    const CacheDev& cd = a.c[ci];
-    r.rope = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(cd.rope) + s * cd.rope_stride +
+    uint32_t s;
+    const CacheDev& cd = cache_of<TWO>(a, slots[step * kMSteps + (t >> 3)], s);
+    r.rope = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(cd.rope) + (uint64_t)s * cd.rope_stride +
                                              16 * (t & 7));
   }
 }
 
-// Raw records -> K and V^T tiles. Invalid keys become zeros (their scores are masked; V = 0 keeps P * V finite).
+// Raw records -> K and V^T tiles. An invalid key's latent becomes 0 (so P * V stays finite whatever slot 0 holds);
+// its rope is left as read: its score is masked by a select, never multiplied.
+template <bool TWO>
 __device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step, const Raw& r, float g0, float g1,
                                _Float16* kt, _Float16* vt) {
-  const int t = threadIdx.x, kq = t >> 6, c = t & 63;
+  typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+  const int t = threadIdx.x, kq = t & 7, c = t >> 3;
   half8_t vals[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int32_t e = slots[step * kMSteps + 4 * kq + i];
-    const float sg = entry_valid(e) ? e4m3_decode(r.sc[i]) * (e <= -2 ? g1 : g0) : 0.0f;
+    const float g = (TWO && e <= -2) ? g1 : g0;
+    const float sg = entry_valid(e) ? (float)fp8x2_to_f16<false>(r.sc[i]).x * g : 0.0f;
     const _Float16 h = (_Float16)sg;
     const half2_t s2 = half2_t{h, h};
     const half2_t p0 = fp4x2_to_f16<0>(r.pay[i]) * s2, p1 = fp4x2_to_f16<1>(r.pay[i]) * s2;
@@ -117,22 +134,21 @@ __device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step,
     *reinterpret_cast<half8_t*>(kt + (4 * kq + i) * kKRow + 8 * c) = vals[i];
   }
 #pragma unroll
-  for (int d = 0; d < 8; ++d) {
-    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+  for (int d = 0; d < 8; ++d)
     *reinterpret_cast<half4_t*>(vt + (8 * c + d) * kVRow + 4 * kq) =
         half4_t{vals[0][d], vals[1][d], vals[2][d], vals[3][d]};
-  }
   if (t < 256) {
     const int key = t >> 3, p = t & 7;
-    const bool ok = entry_valid(slots[step * kMSteps + key]);
     const uint32_t w[4] = {r.rope.x, r.rope.y, r.rope.z, r.rope.w};
-    half8_t h;
+    half8_t hv;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      h[2 * e] = ok ? (_Float16)bf16_bits_to_f32(w[e] & 0xFFFFu) : (_Float16)0.0f;
-      h[2 * e + 1] = ok ? (_Float16)bf16_bits_to_f32(w[e] >> 16) : (_Float16)0.0f;
+    for (int e = 0; e < 4; ++e) {   // BF16 -> FP16 is exact in range, so round-toward-zero packing is exact
+      const half2_t pr = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(w[e] << 16),
+                                                                                __uint_as_float(w[e] & 0xFFFF0000u)));
+      hv[2 * e] = pr.x;
+      hv[2 * e + 1] = pr.y;
     }
-    *reinterpret_cast<half8_t*>(kt + key * kKRow + kDl + 8 * p) = h;
+    *reinterpret_cast<half8_t*>(kt + key * kKRow + kDl + 8 * p) = hv;
   }
 }
 
@@ -148,12 +164,13 @@ __device__ inline void store_vals(const MlaArgs& a, int64_t row, int head, int d
   }
 }
 
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-__device__ inline void store_through(__amdgpu_buffer_rsrc_t r, int byte_off, float4_t v) {
-  const u32x4_t w = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
-  __builtin_amdgcn_raw_buffer_store_b128(w, r, byte_off, 0, 16);
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+// 8-byte store written through to L2 (sc1), so the merging workgroup of another CU reads it after the counter
+__device__ inline void store_through(__amdgpu_buffer_rsrc_t r, int byte_off, u32x2_t v) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, byte_off, 0, 16);
 }
 
+template <bool TWO>
 __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
   asm volatile("" ::"s"(a.xcd_units), "s"(a.xcd_extra), "s"(a.splits), "s"(a.keys_per_split), "s"(a.topk[0]),
@@ -219,7 +236,7 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
     else
       *reinterpret_cast<half8_t*>(qs + ((kk - kQReg) * kMHeads + 16 * wave + hl) * kQRow + 8 * j) = h;
   }
-  const float g0 = *a.c[0].g, g1 = *a.c[1].g;
+  const float g0 = *a.c[0].g, g1 = TWO ? *a.c[1].g : g0;
 
   float m = -__builtin_inff(), l = 0.0f;
   float4_t acc[32];
@@ -227,28 +244,36 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
   for (int i = 0; i < 32; ++i) acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   Raw raw;
-  load_raw(a, slots, 0, raw);
+  load_raw<TWO>(a, slots, 0, raw);
   for (int step = 0; step < a.steps; ++step) {
-    dequant(a, slots, step, raw, g0, g1, kt, vt);
+    dequant<TWO>(a, slots, step, raw, g0, g1, kt, vt);
     __syncthreads();
-    if (step + 1 < a.steps) load_raw(a, slots, step + 1, raw);
+    if (step + 1 < a.steps) load_raw<TWO>(a, slots, step + 1, raw);
     const uint32_t valid = (uint32_t)__builtin_amdgcn_ballot_w64(lane < kMSteps &&
                                                                   entry_valid(slots[step * kMSteps + (lane & 31)]));
-    // S^T for the two 16-key tiles
-    float4_t s[2];
+    // S^T for the two 16-key tiles, each as two independent MFMA chains (even / odd dim chunks)
+    float4_t s[2], s2[2];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       s[tt] = float4_t{0.f, 0.f, 0.f, 0.f};
-      const _Float16* kr = kt + (16 * tt + hl) * kKRow + 8 * j;
+      s2[tt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
-      for (int kk = 0; kk < kQChunks; ++kk) {
-        const half8_t qv = kk < kQReg ? qb[kk < kQReg ? kk : 0]
-                                      : *reinterpret_cast<const half8_t*>(
-                                            qs + ((kk - kQReg) * kMHeads + 16 * wave + hl) * kQRow + 8 * j);
-        s[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8_t*>(kr + 32 * kk), qv, s[tt],
-                                                       0, 0, 0);
+    for (int kk = 0; kk < kQChunks; ++kk) {
+      const half8_t qv = kk < kQReg ? qb[kk < kQReg ? kk : 0]
+                                    : *reinterpret_cast<const half8_t*>(
+                                          qs + ((kk - kQReg) * kMHeads + 16 * wave + hl) * kQRow + 8 * j);
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const half8_t kv = *reinterpret_cast<const half8_t*>(kt + (16 * tt + hl) * kKRow + 8 * j + 32 * kk);
+        if (kk & 1)
+          s2[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qv, s2[tt], 0, 0, 0);
+        else
+          s[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qv, s[tt], 0, 0, 0);
       }
     }
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) s[tt] += s2[tt];
     // online softmax of head hl over keys T(j), lazy rescale
     float sv[8];
 #pragma unroll
@@ -308,15 +333,23 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
       a.lse[row * a.heads + head] = l_tot > 0.0f ? (m + __builtin_log2f(l_tot)) * kLn2 : -__builtin_inff();
     return;
   }
-  // 2. partials of this row (written through), the last workgroup of the row merges them
-  float* row_part = a.part + row * a.splits * a.heads * kMPart;
-  const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-      row_part, (short)0, (int)((int64_t)a.splits * a.heads * kMPart * 4), 0x00020000);
+  // 2. the split's output normalized by its own sum (FP16: a convex combination of FP16 latent values) plus its
+  //    max and sum, written through; the last workgroup of the row merges the splits
   if (head_live) {
-    const int at = ((split * a.heads + head) * kMPart) * 4;
+    const int64_t ph = ((int64_t)row * a.splits + split) * a.heads + head;
+    const __amdgpu_buffer_rsrc_t pr =
+        __builtin_amdgcn_make_buffer_rsrc(a.part + ph * kDl, (short)0, kDl * 2, 0x00020000);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
 #pragma unroll
-    for (int dt = 0; dt < 32; ++dt) store_through(pr, at + (16 * dt + 4 * j) * 4, acc[dt]);
-    if (j == 0) store_through(pr, at + kDl * 4, float4_t{m, l_tot, 0.0f, 0.0f});
+    for (int dt = 0; dt < 32; ++dt) {
+      const u32x2_t w = {f32_to_f16_bits(acc[dt][0] * inv) | (f32_to_f16_bits(acc[dt][1] * inv) << 16),
+                         f32_to_f16_bits(acc[dt][2] * inv) | (f32_to_f16_bits(acc[dt][3] * inv) << 16)};
+      store_through(pr, (16 * dt + 4 * j) * 2, w);
+    }
+    if (j == 0) {
+      const __amdgpu_buffer_rsrc_t mr = __builtin_amdgcn_make_buffer_rsrc(a.ml + ph * 2, (short)0, 8, 0x00020000);
+      store_through(mr, 0, u32x2_t{__float_as_uint(m), __float_as_uint(l_tot)});
+    }
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -326,32 +359,49 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
     s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.splits - 1;
   __syncthreads();
   if (!s_last) return;
-  // 512 threads: head t / 4, dims 128 (t % 4) .. +127
-  for (int hh = threadIdx.x >> 2; hh < a.heads; hh += 128) {
-    const int d0 = 128 * (threadIdx.x & 3);
-    const float* base = row_part + (int64_t)hh * kMPart;
-    const int64_t sstride = (int64_t)a.heads * kMPart;
+  // 16 threads per head, 32 heads per pass; thread jj reads and writes dims 8 (16 k + jj) .. +7, k = 0..3, so the
+  // 16 threads of a head cover 256 contiguous bytes per load
+  const int jj = threadIdx.x & 15;
+  const int64_t sstride = (int64_t)a.heads;   // (split, head) records of this row: index sp * heads + head
+  const uint16_t* row_part = a.part + (int64_t)row * a.splits * a.heads * kDl;
+  const float* row_ml = a.ml + (int64_t)row * a.splits * a.heads * 2;
+  for (int hh = threadIdx.x >> 4; hh < a.heads; hh += 32) {
     float mx = -__builtin_inff();
-    for (int sp = 0; sp < a.splits; ++sp) mx = fmaxf(mx, base[sp * sstride + kDl]);
+    for (int sp = 0; sp < a.splits; ++sp) mx = fmaxf(mx, row_ml[(sp * sstride + hh) * 2]);
     const float mu = (mx == -__builtin_inff()) ? 0.0f : mx;
-    float total = 0.0f;
-    for (int sp = 0; sp < a.splits; ++sp)
-      total += __builtin_amdgcn_exp2f(base[sp * sstride + kDl] - mu) * base[sp * sstride + kDl + 1];
-    const float l_all = total;
+    float l_all = 0.0f;
+    for (int sp = 0; sp < a.splits; ++sp) {
+      const float2 ml = *reinterpret_cast<const float2*>(row_ml + (sp * sstride + hh) * 2);
+      l_all += __builtin_amdgcn_exp2f(ml.x - mu) * ml.y;
+    }
+    float total = l_all;
     if (a.sink) total += __builtin_amdgcn_exp2f(a.sink[hh] * kLog2e - mu);
     const float inv = l_all > 0.0f ? 1.0f / total : 0.0f;
-    for (int c = 0; c < 128; c += 8) {
-      float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int sp = 0; sp < a.splits; ++sp) {
-        const float w = __builtin_amdgcn_exp2f(base[sp * sstride + kDl] - mu) * inv;
-        const float4_t x0 = reinterpret_cast<const float4_t*>(base + sp * sstride + d0 + c)[0];
-        const float4_t x1 = reinterpret_cast<const float4_t*>(base + sp * sstride + d0 + c)[1];
-        o[0] += w * x0[0]; o[1] += w * x0[1]; o[2] += w * x0[2]; o[3] += w * x0[3];
-        o[4] += w * x1[0]; o[5] += w * x1[1]; o[6] += w * x1[2]; o[7] += w * x1[3];
+    float o[32];
+#pragma unroll
+    for (int e = 0; e < 32; ++e) o[e] = 0.0f;
+#pragma unroll 2
+    for (int sp = 0; sp < a.splits; ++sp) {
+      const float2 ml = *reinterpret_cast<const float2*>(row_ml + (sp * sstride + hh) * 2);
+      const float w = __builtin_amdgcn_exp2f(ml.x - mu) * ml.y * inv;
+      const uint4* src = reinterpret_cast<const uint4*>(row_part + (sp * sstride + hh) * kDl);
+      uint4 x[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) x[k] = src[16 * k + jj];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t u[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const half2_t h = __builtin_bit_cast(half2_t, u[e]);
+          o[8 * k + 2 * e] += w * (float)h.x;
+          o[8 * k + 2 * e + 1] += w * (float)h.y;
+        }
       }
-      store_vals(a, row, hh, d0 + c, o, 8);
     }
-    if (a.lse && d0 == 0)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) store_vals(a, row, hh, 8 * (16 * k + jj), o + 8 * k, 8);
+    if (a.lse && jj == 0)
       a.lse[row * a.heads + hh] = l_all > 0.0f ? (mu + __builtin_log2f(l_all)) * kLn2 : -__builtin_inff();
   }
   if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -366,7 +416,8 @@ int check_cache(const char* what, const xt_mla_cache* c, int64_t* pay_stride, in
   *sf_stride = c->sf_stride ? c->sf_stride : kDl / 16;
   *rope_stride = c->rope_stride ? c->rope_stride : kDr * 2;
   if (*pay_stride < kDl / 2 || *pay_stride % 4 || *sf_stride < kDl / 16 || *rope_stride < kDr * 2 ||
-      *rope_stride % 16 || !aligned(c->pay, 4) || !aligned(c->rope, 16))
+      *rope_stride % 16 || !aligned(c->pay, 4) || !aligned(c->rope, 16) || *pay_stride > 0xFFFFFFFFLL ||
+      *sf_stride > 0xFFFFFFFFLL || *rope_stride > 0xFFFFFFFFLL)
     return fail(XT_EINVAL, "%s: cache strides %lld / %lld / %lld bytes or alignment do not fit the latent rows", what,
                 (long long)*pay_stride, (long long)*sf_stride, (long long)*rope_stride);
   return XT_OK;
@@ -377,12 +428,13 @@ int check_cache(const char* what, const xt_mla_cache* c, int64_t* pay_stride, in
 
 using namespace xt;
 
-// Workspace: [arrival counters, kCounterBytes][partials [rows, splits, heads, kMPart] FP32]
+// Workspace: [arrival counters, kCounterBytes][partial outputs [rows, splits, heads, 512] FP16][partial max and sum
+// [rows, splits, heads, 2] FP32]
 
 extern "C" size_t xt_sparse_mla_workspace_bytes(int rows, int heads, int splits) {
   if (rows < 0 || heads <= 0 || splits <= 0) return 0;
   if (splits == 1) return 256;
-  return kCounterBytes + (size_t)rows * splits * heads * kMPart * sizeof(float);
+  return kCounterBytes + (size_t)rows * splits * heads * (kDl * 2 + 2 * sizeof(float));
 }
 
 extern "C" int xt_sparse_mla_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, int heads,
@@ -411,13 +463,13 @@ extern "C" int xt_sparse_mla_nvfp4(const void* q, int64_t q_row_stride, int64_t 
   int64_t ps, ss, rs;
   int st = check_cache(what, cache, &ps, &ss, &rs);
   if (st != XT_OK) return st;
-  a.c[0] = CacheDev{cache->pay, cache->scales, static_cast<const uint16_t*>(cache->rope), cache->g, cache->slots, ps,
-                    ss, rs};
+  a.c[0] = CacheDev{cache->pay, cache->scales, static_cast<const uint16_t*>(cache->rope), cache->g, cache->slots,
+                    (uint32_t)ps, (uint32_t)ss, (uint32_t)rs};
   if (extra) {
     st = check_cache(what, extra_cache, &ps, &ss, &rs);
     if (st != XT_OK) return st;
     a.c[1] = CacheDev{extra_cache->pay, extra_cache->scales, static_cast<const uint16_t*>(extra_cache->rope),
-                      extra_cache->g, extra_cache->slots, ps, ss, rs};
+                      extra_cache->g, extra_cache->slots, (uint32_t)ps, (uint32_t)ss, (uint32_t)rs};
   } else {
     a.c[1] = a.c[0];
   }
@@ -460,21 +512,27 @@ extern "C" int xt_sparse_mla_nvfp4(const void* q, int64_t q_row_stride, int64_t 
     return fail(XT_EUNSUPPORTED, "%s: %d keys per split need %zu bytes of LDS; use more splits", what,
                 a.keys_per_split, lds_bytes);
   a.counters = static_cast<int32_t*>(workspace);
-  a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+  a.part = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + kCounterBytes);
+  a.ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes + (size_t)rows * splits * heads * kDl * 2);
   const int64_t n_units = (int64_t)rows * splits;
   if (n_units > 0x7FFFFFFFLL) return fail(XT_EUNSUPPORTED, "%s: %lld workgroups", what, (long long)n_units);
   a.xcd_units = (uint32_t)(n_units / 8);
   a.xcd_extra = (uint32_t)(n_units % 8);
   // dynamic LDS above 64 KB must be allowed per kernel; raised to the largest size asked for so far
-  static size_t lds_allowed = 64 * 1024;
-  if (lds_bytes > lds_allowed) {
-    const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&mla_kernel),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
+  static size_t lds_allowed[2] = {64 * 1024, 64 * 1024};
+  const void* fn = extra ? reinterpret_cast<const void*>(&mla_kernel<true>)
+                         : reinterpret_cast<const void*>(&mla_kernel<false>);
+  if (lds_bytes > lds_allowed[extra]) {
+    const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
     if (err != hipSuccess)
       return fail(XT_ELAUNCH, "%s: could not allow %zu bytes of LDS: %s", what, lds_bytes, hipGetErrorString(err));
-    lds_allowed = lds_bytes;
+    lds_allowed[extra] = lds_bytes;
   }
-  hipLaunchKernelGGL(mla_kernel, dim3((unsigned)n_units), dim3(64 * kMWaves), lds_bytes,
-                     reinterpret_cast<hipStream_t>(stream), a);
+  if (extra)
+    hipLaunchKernelGGL(mla_kernel<true>, dim3((unsigned)n_units), dim3(64 * kMWaves), lds_bytes,
+                       reinterpret_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL(mla_kernel<false>, dim3((unsigned)n_units), dim3(64 * kMWaves), lds_bytes,
+                       reinterpret_cast<hipStream_t>(stream), a);
   return check_launch(what);
 }
