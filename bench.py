@@ -256,6 +256,79 @@ def run_mla(args, w, ops, workloads):
     print(json.dumps(record), flush=True)
 
 
+def build_block_pool(w, gen, workloads, ops):
+    """One layer's head-major NVFP4 pages (unit global scale) from bf16 K/V of w.batch * w.ctx tokens."""
+    import torch
+    slots = w.batch * w.ctx
+    one = torch.ones(1, dtype=torch.float32, device='cuda')
+    out = []
+    for _ in range(2):
+        x = workloads.kv_tensor(slots, w.kv_heads, w.dim, gen, 'cuda')
+        pay = torch.empty(slots, w.kv_heads, w.dim // 2, dtype=torch.uint8, device='cuda')
+        sc = torch.empty(slots, w.kv_heads, w.dim // 16, dtype=torch.uint8, device='cuda')
+        ops.quantize_append(x, torch.arange(slots, device='cuda'), one, pay, sc)
+        del x
+        out += list(workloads.head_major_pages(pay, sc, w.block))
+    return out   # k_pay, k_sc, v_pay, v_sc
+
+
+def run_block(args, w, ops, workloads):
+    """Block-sparse decode steps over head-major NVFP4 pages (MiniMax layout), rotating `layers` distinct pools.
+    One JSON line: GB/s of read KV bytes against the HBM peak."""
+    import torch
+    torch.cuda.set_device(0)
+    t0 = time.time()
+    gen = workloads.generator('cuda', 20261103)
+    layers = max(1, min(args.layers, 8))
+    pools = [build_block_pool(w, gen, workloads, ops) for _ in range(layers)]
+    inp = workloads.block_decode_inputs(w, 20261104, 'cuda')
+    splits = args.splits or ops.default_splits(w.batch, w.kv_heads, w.keys)
+    ws = ops.new_workspace('cuda', w.batch, w.q_heads, w.dim, splits)
+    out = torch.empty(w.batch, w.q_heads, w.dim, dtype=torch.bfloat16, device='cuda')
+    torch.cuda.synchronize()
+    log(f'built {layers} page pools ({w.pages} pages each) in {time.time() - t0:.1f} s')
+
+    def step(layer):
+        k_pay, k_sc, v_pay, v_sc = pools[layer]
+        ops.fp4_sparse_decode(inp.q, k_pay, k_sc, v_pay, v_sc, inp.req_to_token, inp.slot_ids, inp.topk_idx,
+                              inp.seq_lens, w.block, out=out, splits=splits, ws=ws)
+
+    for i in range(max(1, args.warmup)):
+        step(i % layers)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for layer in range(layers):
+            step(layer)
+    graph.replay()
+    torch.cuda.synchronize()
+    replays = max(1, math.ceil(args.steps / layers))
+    steps = replays * layers
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
+    log(f'{w.name}: {ms * 1e3:.2f} us per layer-step, {gbs:.0f} GB/s algorithmic ({gbs / HBM_PEAK_GBS:.1%} of '
+        f'{HBM_PEAK_GBS:.0f}), splits {splits}')
+    record = {
+        'metric': 'NVFP4-KV block-sparse decode HBM GB/s', 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1,
+        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'higher_is_better': True,
+        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f16', 'data': 'synthetic',
+        'config': {'workload': w.name, 'batch': w.batch, 'q_heads': w.q_heads, 'kv_heads': w.kv_heads,
+                   'head_dim': w.dim, 'context': w.ctx, 'topk_blocks': w.topk_blocks, 'block': w.block,
+                   'kv_format': 'nvfp4 head-major pages', 'layers_rotated': layers, 'splits': splits},
+        'us_per_layer_step': round(ms * 1e3, 3), 'tokens_per_s': round(w.batch / (ms * 1e-3), 1),
+        'roofline': {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+                     'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None},
+        'cpu_baseline': None,
+    }
+    print(json.dumps(record), flush=True)
+
+
 def main():
     p = argparse.ArgumentParser()
     p.add_argument('--gpus', type=int, default=1)
@@ -263,7 +336,7 @@ def main():
     p.add_argument('--warmup', type=int, default=64)
     p.add_argument('--workload', default='gqa_decode_b32',
                    help='gqa_decode_b32 (default), cpu_ref_decode, long_ctx_decode_b4, gqa_prefill_chunk4096, '
-                        'mla_decode_b64 or mla_prefill_2048')
+                        'minimax_decode_b32, mla_decode_b64 or mla_prefill_2048')
     p.add_argument('--layers', type=int, default=16)
     p.add_argument('--splits', type=int, default=None)
     p.add_argument('--layout', default='interleaved', choices=['interleaved', 'split'],
@@ -293,6 +366,8 @@ def main():
     from xtier_amd import ops, workloads
     from xtier_amd.pool import KVPool
 
+    if args.workload in workloads.BLOCK_WORKLOADS:
+        return run_block(args, workloads.BLOCK_WORKLOADS[args.workload], ops, workloads)
     if args.workload in workloads.MLA_WORKLOADS:
         return run_mla(args, workloads.MLA_WORKLOADS[args.workload], ops, workloads)
     if args.workload in workloads.PREFILL_WORKLOADS:

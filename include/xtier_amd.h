@@ -122,6 +122,32 @@ int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_s
                            int64_t out_row_stride, int64_t out_head_stride, int out_dtype, float* lse, int rows,
                            int splits, void* workspace, size_t workspace_bytes, xt_stream_t stream);
 
+/* Block-sparse NVFP4 decode over head-major pages (the MiniMax cache layout; replaces
+ * xtier/packs/minimax_m3/kv_fp4.py:119-153, fp4_sparse_decode, behind the hook _decode_main :579-590).
+ * Pool: page p, KV head h, row t (t < block_size) holds payload at k_pay + p * page_stride + h * head_stride +
+ * t * row_stride (dim/2 bytes) and E4M3 scales at k_scales + p * sf_page_stride + h * sf_head_stride + t *
+ * sf_row_stride (dim/16 bytes), V alike; the buffers hold `pages` pages. No global scale: *kv_scale (device FP32)
+ * multiplies the scores and the output. Row b (q [rows, q_heads, dim] BF16) reads request slot_ids[b] (int64): its
+ * length L = min(seq_lens[b], max_kv_len); KV head h's block ids topk_idx[h * idx_head_stride + b * idx_row_stride +
+ * i] (int32, i < topk_blocks, -1: none) name positions c = id * block_size .. c + block_size - 1 below L, stored at
+ * page s / block_size, rows s % block_size + n for s = req_to_token[slot_ids[b] * req_stride + c] (blocks start on a
+ * page row, as the reference assumes; a block that starts mid-page continues on the next page here, where the
+ * reference reads past the page). out[b, h'] = sum softmax(q.k * sm_scale * kv_scale) v * kv_scale over the query
+ * heads h' of KV head h (natural exp, kv_fp4.py:100-113), 0 for a row without keys; lse (optional) as above.
+ * Requirements: dim 128, q_heads / kv_heads <= 16, block_size a power of 2, page_stride / row_stride ==
+ * sf_page_stride / sf_row_stride >= block_size. splits and workspace as xt_sparse_decode_nvfp4 (workgroups hold one
+ * KV head, so the arrival counters need rows * kv_heads <= 16384 when splits > 1). */
+int xt_block_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, const uint8_t* k_pay,
+                                 const uint8_t* v_pay, const uint8_t* k_scales, const uint8_t* v_scales,
+                                 const float* kv_scale, int64_t pages, int kv_heads, int q_heads, int dim,
+                                 int block_size, int64_t page_stride, int64_t head_stride, int64_t row_stride,
+                                 int64_t sf_page_stride, int64_t sf_head_stride, int64_t sf_row_stride,
+                                 const int32_t* req_to_token, int64_t req_stride, int max_kv_len,
+                                 const int64_t* slot_ids, const int32_t* topk_idx, int64_t idx_head_stride,
+                                 int64_t idx_row_stride, int topk_blocks, const int32_t* seq_lens, float sm_scale,
+                                 void* out, int64_t out_row_stride, int64_t out_head_stride, int out_dtype, float* lse,
+                                 int rows, int splits, void* workspace, size_t workspace_bytes, xt_stream_t stream);
+
 /* --- sparse MLA over an NVFP4 latent cache ------------------------------------------------------------------------ */
 
 /* One latent cache: per slot a latent row of latent_dim NVFP4 values (payload latent_dim/2 bytes, E4M3 scales

@@ -1,5 +1,5 @@
 """Sparse attention over an NVFP4 paged KV pool, on the CPU (numpy): the oracle for the gather, the fused decode,
-the split-K merge, the chunked prefill and sparse MLA.
+the split-K merge, the chunked prefill, the block-sparse decode over head-major pages and sparse MLA.
 
 Test infrastructure only. Conventions (reference: qsa_fp4.py:131-140; sparse_mla.py:42-46; qsa_decode.py:75, :83):
 an index is valid when it is >= 0 and below the row's length (and, for a causal query, not after the query's own
@@ -186,6 +186,56 @@ def merge_partials(m, l, acc):
     out = (w[..., None] * acc).sum(0)
     with np.errstate(invalid='ignore', divide='ignore'):
         return np.where(total[:, None] > 0, out / total[:, None], 0.0)
+
+
+# --- block-sparse decode over head-major pages (MiniMax) ----------------------------------------------------------
+
+def block_sparse_decode(q, k_pay, k_sf, v_pay, v_sf, req_to_token, slot_ids, topk_idx, seq_lens, block_size, scale,
+                        kv_scale=1.0, attend=None):
+    """kv_fp4.py:52-116 with the chunk merge of :149-152, reference values. q [B, Hq, D]; pool pages k_pay / v_pay
+    [pages, Hkv, block, D/2] u8 and k_sf / v_sf [pages, Hkv, block, D/16] E4M3 bytes (no global scale: kv_scale
+    multiplies the scores and the output, :100, :112-113); topk_idx [Hkv, B, T] block ids, -1 padded. For row b and KV
+    head h: length L = min(seq_lens[b], req_to_token.shape[1]) (:69); the first (number of ids >= 0) entries are read
+    (:73-76), an id e >= 0 with c = e * block < L naming positions c .. c + block - 1 below L (:86-93) at page
+    req_to_token[slot_ids[b], c] // block, rows req_to_token[...] % block + n (:89-91). A negative id inside the
+    counted prefix is skipped here (the reference would read position -block). ``attend`` (default the FP64 softmax)
+    gets (q [group, D], k [N, 1, D], v [N, 1, D], valid, scale * kv_scale). Returns (out [B, Hq, D] float64, lse
+    [B, Hq] natural log-sum-exp of the scaled scores; 0 and -inf for a (row, head) without keys)."""
+    attend = attend or softmax_attention
+    q = np.asarray(q)
+    b_n, hq, d = q.shape
+    hkv = k_pay.shape[1]
+    group = hq // hkv
+    max_len = req_to_token.shape[1]
+    out = np.zeros((b_n, hq, d))
+    lse = np.full((b_n, hq), -np.inf)
+    for b in range(b_n):
+        length = min(int(seq_lens[b]), max_len)
+        sid = int(slot_ids[b])
+        for h in range(hkv):
+            ids = np.asarray(topk_idx[h, b], dtype=np.int64)
+            real = int((ids >= 0).sum())
+            pages, rows = [], []
+            for e in ids[:real]:
+                c = int(e) * block_size
+                if e < 0 or c >= length:
+                    continue
+                base = int(req_to_token[sid, c])
+                n = min(block_size, length - c)
+                pages.append(np.full(n, base // block_size))
+                rows.append(base % block_size + np.arange(n))
+            if not pages:
+                continue
+            pg, rw = np.concatenate(pages), np.concatenate(rows)
+            k = nvfp4.dequant(k_pay[pg, h, rw], k_sf[pg, h, rw])[:, None]
+            v = nvfp4.dequant(v_pay[pg, h, rw], v_sf[pg, h, rw])[:, None]
+            qs = q[b, h * group:(h + 1) * group]
+            ones = np.ones(k.shape[0], bool)
+            out[b, h * group:(h + 1) * group] = attend(qs, k, v, ones, scale * kv_scale) * kv_scale
+            s = k[:, 0].astype(np.float64) @ qs.astype(np.float64).T * scale * kv_scale
+            top = s.max(0)
+            lse[b, h * group:(h + 1) * group] = top + np.log(np.exp(s - top).sum(0))
+    return out, lse
 
 
 # --- sparse MLA ---------------------------------------------------------------------------------------------------

@@ -1,0 +1,44 @@
+"""The MiniMax decode hook without a GPU: fall-through to `original` for caches without scale bytes, the unit-scale and
+sink / HiSparse checks (kv_fp4.py:562-590), attach_scales and the registration (:632-638)."""
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from xtier_amd import minimax
+
+
+def _original(*args, **kwargs):
+    return ('original', args, kwargs)
+
+
+def test_falls_through_without_scale_bytes():
+    k = torch.zeros(2, 4, 128, 64, dtype=torch.uint8)
+    got = minimax.decode_main(_original, 1, q=torch.zeros(1, 16, 128), k_cache=k, v_cache=k)
+    assert got[0] == 'original' and got[1] == (1,) and got[2]['k_cache'] is k
+
+
+def test_unit_scales_and_unsupported_features():
+    k = torch.zeros(2, 4, 128, 64, dtype=torch.uint8)
+    k._xtier_fp4 = torch.zeros(2, 4, 128, 8, dtype=torch.uint8)
+    base = dict(q=torch.zeros(1, 16, 128), k_cache=k, v_cache=k)
+    with pytest.raises(ValueError):
+        minimax.decode_main(_original, **base, k_scale=0.5)
+    with pytest.raises(NotImplementedError):
+        minimax.decode_main(_original, **base, sink=torch.zeros(16))
+    with pytest.raises(NotImplementedError):
+        minimax.decode_main(_original, **base, k_scale=1.0, hisparse_slots=torch.zeros(1))
+
+
+def test_attach_scales_and_install():
+    pays = [torch.zeros(1), torch.zeros(1)]
+    scs = [torch.ones(1), torch.ones(1)]
+    pool = SimpleNamespace(main_pool=SimpleNamespace(k_buffer=pays, k_scale_buffer=scs, v_buffer=pays[::-1],
+                                                     v_scale_buffer=scs[::-1]),
+                           index_k_pool=SimpleNamespace(k_buffer=[], k_scale_buffer=[]), size=7)
+    minimax.attach_scales(pool)
+    assert minimax._scales(pays[0]) is scs[0] and minimax._scales(pays[1]) is scs[1]
+    seen = []
+    registry = SimpleNamespace(register=lambda name, fn, kind: seen.append((name, fn, kind)))
+    minimax.install(registry, SimpleNamespace(AROUND='around'))
+    assert seen == [(f'{minimax.OPS}.flash_decode_with_gqa_share_sparse', minimax.decode_main, 'around')]

@@ -198,3 +198,56 @@ def test_sparse_mla_two_lists_equal_one_concatenated_cache():
         want = (p.T @ keys[:, :dl]) / (p.sum(0) + np.exp(sink - m))[:, None]
         assert np.allclose(out[r], want, rtol=1e-12, atol=1e-12)
         assert np.allclose(lse[r], m + np.log(p.sum(0)), rtol=1e-12, atol=1e-12)
+
+
+def _block_case(seed, b=3, kh=2, group=4, d=32, ctx=640, block=64, topk=5):
+    rng = np.random.default_rng(seed)
+    pages = b * (ctx // block)
+    k_pay = rng.integers(0, 256, (pages, kh, block, d // 2), dtype=np.uint8)
+    v_pay = rng.integers(0, 256, (pages, kh, block, d // 2), dtype=np.uint8)
+    k_sf = rng.integers(0x20, 0x48, (pages, kh, block, d // 16), dtype=np.uint8)   # E4M3 2^-8 .. 2
+    v_sf = rng.integers(0x20, 0x48, (pages, kh, block, d // 16), dtype=np.uint8)
+    perm = rng.permutation(pages).reshape(b, ctx // block)
+    r2t = (perm[:, :, None] * block + np.arange(block)[None, None, :]).reshape(b, ctx).astype(np.int32)
+    ids = np.stack([np.stack([np.sort(rng.permutation(ctx // block)[:topk]) for _ in range(b)]) for _ in range(kh)])
+    ids = ids.astype(np.int32)
+    ids[1, 0, 3:] = -1                         # a shorter list (padded at the end)
+    seq = np.array([ctx, ctx - 37, 5 * block + 1][:b], dtype=np.int32)
+    q = rng.standard_normal((b, kh * group, d))
+    return q, (k_pay, k_sf, v_pay, v_sf), r2t, np.array([2, 0, 1][:b]), ids, seq
+
+
+def test_block_decode_equals_token_decode_on_the_expanded_lists():
+    """kv_fp4.py's block-granular decode equals the token-granular oracle (pinned above against torch) once the
+    head-major pages are laid out token-major (slot = page * block + row) and every block id is expanded to its
+    positions; LSE equals the log-sum-exp of the expanded keys' scores."""
+    block, scale, kv_scale = 64, 0.2, 0.75
+    q, (k_pay, k_sf, v_pay, v_sf), r2t, sid, ids, seq = _block_case(3, block=block)
+    out, lse = attention.block_sparse_decode(q, k_pay, k_sf, v_pay, v_sf, r2t, sid, ids, seq, block, scale, kv_scale)
+    kh = k_pay.shape[1]
+    group = q.shape[1] // kh
+    tok = lambda a: a.transpose(0, 2, 1, 3).reshape(-1, kh, a.shape[-1])
+    for h in range(kh):
+        pool = (tok(k_pay)[:, h:h + 1], tok(v_pay)[:, h:h + 1], tok(k_sf)[:, h:h + 1], tok(v_sf)[:, h:h + 1],
+                kv_scale, kv_scale)
+        pos = (ids[h].astype(np.int64)[:, :, None] * block + np.arange(block)).reshape(len(sid), -1)
+        pos = np.where(np.repeat(ids[h] >= 0, block, axis=1), pos, -1)
+        ref = attention.sparse_decode(q[:, h * group:(h + 1) * group], pool, r2t, 1, sid, pos, None, seq, scale)
+        np.testing.assert_allclose(out[:, h * group:(h + 1) * group], ref, rtol=1e-12, atol=1e-12)
+    # a (row, head) without keys: out 0, LSE -inf
+    ids2 = ids.copy()
+    ids2[0, 1] = -1
+    out2, lse2 = attention.block_sparse_decode(q, k_pay, k_sf, v_pay, v_sf, r2t, sid, ids2, seq, block, scale)
+    assert np.all(out2[1, :group] == 0) and np.all(np.isneginf(lse2[1, :group]))
+    assert np.isfinite(lse).all()
+
+
+def test_block_decode_clamps_length_to_the_table_and_skips_blocks_past_it():
+    block = 64
+    q, pool, r2t, sid, ids, seq = _block_case(4, block=block)
+    seq_big = seq.copy()
+    seq_big[0] = 10 ** 6                       # clamped to req_to_token.shape[1] (kv_fp4.py:69)
+    a, _ = attention.block_sparse_decode(q, *pool, r2t, sid, ids, seq_big, block, 0.1)
+    b, _ = attention.block_sparse_decode(q, *pool, r2t, sid, ids, np.where(np.arange(3) == 0, r2t.shape[1], seq),
+                                         block, 0.1)
+    np.testing.assert_array_equal(a, b)

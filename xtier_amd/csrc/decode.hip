@@ -53,8 +53,11 @@ struct DecodeArgs {
   const uint8_t* v_sf;
   const float* gk;
   const float* gv;
-  int64_t pool_slots;
+  int64_t pool_slots;                // slots addressable as slot * stride (after the page-row remap below)
   int64_t pay_stride, sf_stride;     // bytes from one slot to the next in the payload / scale buffers
+  int64_t pay_head_stride, sf_head_stride;   // bytes from one KV head to the next within a slot's row
+  int remap_shift;                   // head-major pages: slot s -> (s >> remap_shift) * remap_mul + low bits (0: s)
+  int64_t remap_mul;
   int kv_heads, q_heads, group, kv_groups;
   const int32_t* table;
   int64_t table_stride;
@@ -63,7 +66,10 @@ struct DecodeArgs {
   const int64_t* row_req;
   const int32_t* indices;
   int64_t idx_stride;
-  int topk;
+  int64_t idx_head_stride;           // elements between the index lists of consecutive KV heads (0: one shared list)
+  int block_shift;                   // an index names 2^block_shift consecutive positions (0: one token)
+  int max_len;                       // sequence lengths are clamped to this
+  int topk;                          // keys per row (index entries << block_shift)
   const int32_t* counts;
   const int32_t* seq_lens;
   const int32_t* query_pos;
@@ -258,7 +264,8 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   asm volatile("" ::"s"(a.xcd_units), "s"(a.xcd_extra), "s"(a.splits), "s"(a.kv_groups), "s"(a.kv_heads),
                "s"(a.group), "s"(a.keys_per_split), "s"(a.topk), "s"(a.q), "s"(a.q_rs), "s"(a.q_hs), "s"(a.indices),
                "s"(a.idx_stride), "s"(a.counts), "s"(a.seq_lens), "s"(a.query_pos), "s"(a.row_req), "s"(a.table),
-               "s"(a.table_stride), "s"(a.page_shift), "s"(a.page_size), "s"(a.pool_slots));
+               "s"(a.table_stride), "s"(a.page_shift), "s"(a.page_size), "s"(a.pool_slots), "s"(a.idx_head_stride),
+               "s"(a.block_shift), "s"(a.max_len), "s"(a.remap_shift), "s"(a.remap_mul));
   const uint32_t g = blockIdx.x;
   const uint32_t xcd = g & 7u;
   const uint32_t u = xcd * a.xcd_units + min(xcd, a.xcd_extra) + (g >> 3);
@@ -292,12 +299,14 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   // constants), so the chain to the first K/V load is two dependent loads: index, then table.
   const int t0 = split * a.keys_per_split;
   const int kmax = max(0, min(a.keys_per_split, a.topk - t0));
-  const int32_t* ip = a.indices + (int64_t)row * a.idx_stride + t0;
+  const int32_t* ip = a.indices + (int64_t)row * a.idx_stride + (int64_t)kvg * a.idx_head_stride;
+  const int bmask = (1 << a.block_shift) - 1;
   int32_t pos[kSlotBatch];
 #pragma unroll
   for (int b = 0; b < kSlotBatch; ++b) {
-    const int i = b * 512 + (int)threadIdx.x;
-    pos[b] = (i < kmax) ? ip[i] : -1;
+    const int i = b * 512 + (int)threadIdx.x, k = t0 + i;
+    const int32_t e = (i < kmax) ? ip[k >> a.block_shift] : -1;
+    pos[b] = e < 0 ? -1 : (e << a.block_shift) + (k & bmask);
   }
   // the row's count, length, causal limit and table row: scalar loads from addresses valid whether or not the
   // optional arrays are given (a missing one reads the row's length and is ignored), so none waits in a branch
@@ -313,7 +322,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   const int n = max(0, min(t0 + a.keys_per_split, count) - t0);
   const int slice_steps = (((n + kStep - 1) / kStep + kSlices * P - 1) / (kSlices * P)) * P;
   {
-    const int32_t seqlen = len_v;
+    const int32_t seqlen = min(len_v, a.max_len);
     const int32_t qpos = a.query_pos ? qpos_v : 0x7FFFFFFF;
     const int64_t trow = a.row_req ? (int64_t)(((uint64_t)(uint32_t)req_hi << 32) | (uint32_t)req_lo) : row;
     const int32_t* tp = a.table + trow * a.table_stride;
@@ -327,7 +336,8 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
       for (int b = 0; b < kSlotBatch; ++b) {
         const int i = i0 + b * 512 + (int)threadIdx.x;
         ok[b] = i < n && pos[b] >= 0 && pos[b] < seqlen && pos[b] <= qpos;
-        toff[b] = a.page_shift >= 0 ? (pos[b] >> a.page_shift) : pos[b] / a.page_size;
+        const int32_t tpos = pos[b] & ~bmask;   // a block's slots follow the slot of its first position
+        toff[b] = a.page_shift >= 0 ? (tpos >> a.page_shift) : tpos / a.page_size;
       }
 #pragma unroll
       for (int b = 0; b < kSlotBatch; ++b) ent[b] = ok[b] ? tp[toff[b]] : -1;
@@ -337,7 +347,8 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
         int32_t slot = -1;
         if (ok[b] && ent[b] >= 0) {
           const int64_t sl = (int64_t)ent[b] * a.page_size + (pos[b] - toff[b] * a.page_size);
-          if (sl < a.pool_slots) slot = (int32_t)sl;
+          const int64_t v = (sl >> a.remap_shift) * a.remap_mul + (sl & ((1 << a.remap_shift) - 1));
+          if (v < a.pool_slots) slot = (int32_t)v;
         }
         if (i < total) slots[i] = slot;
       }
@@ -345,8 +356,9 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
       if (i0 >= total) break;
 #pragma unroll
       for (int b = 0; b < kSlotBatch; ++b) {   // splits longer than kSlotBatch * 512 keys
-        const int i = i0 + b * 512 + (int)threadIdx.x;
-        pos[b] = (i < kmax) ? ip[i] : -1;
+        const int i = i0 + b * 512 + (int)threadIdx.x, k = t0 + i;
+        const int32_t e = (i < kmax) ? ip[k >> a.block_shift] : -1;
+        pos[b] = e < 0 ? -1 : (e << a.block_shift) + (k & bmask);
       }
     }
   }
@@ -374,10 +386,10 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
     WaveCtx w;
     w.row_bytes = a.pay_stride;
     w.row_scales = a.sf_stride;
-    w.kp = a.k_pay + (int64_t)kvh * (kDim / 2);
-    w.vp = a.v_pay + (int64_t)kvh * (kDim / 2);
-    w.ksf = a.k_sf + (int64_t)kvh * (kDim / 16);
-    w.vsf = a.v_sf + (int64_t)kvh * (kDim / 16);
+    w.kp = a.k_pay + (int64_t)kvh * a.pay_head_stride;
+    w.vp = a.v_pay + (int64_t)kvh * a.pay_head_stride;
+    w.ksf = a.k_sf + (int64_t)kvh * a.sf_head_stride;
+    w.vsf = a.v_sf + (int64_t)kvh * a.sf_head_stride;
     w.slots = slots + slice * slice_steps * kStep;
     w.lane = lane;
     w.hl = hl;
@@ -527,6 +539,26 @@ static int heads_per_workgroup(int rows, int kv_heads, int splits) {
   return (kv_heads % 4 == 0 && (int64_t)rows * (kv_heads / 4) * splits >= 256) ? 4 : 1;
 }
 
+// Pool and index addressing beyond the token-major pool with one shared index list per row.
+struct Addressing {
+  int64_t pay_head_stride, sf_head_stride;   // bytes between KV heads of a slot row
+  int remap_shift;                           // head-major pages: slot -> (slot >> shift) * mul + low bits
+  int64_t remap_mul;
+  int64_t idx_head_stride;                   // per-KV-head index lists (0: shared; forces 1 KV head per workgroup)
+  int block_shift;                           // an index entry names 2^block_shift positions
+  int max_len;                               // sequence lengths clamped to this
+};
+
+static int decode_impl(const char* what, const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                       const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_scales, const uint8_t* v_scales,
+                       const float* gk, const float* gv, int64_t pool_slots, int64_t pay_stride, int64_t sf_stride,
+                       int kv_heads, int q_heads, const int32_t* table, int64_t table_stride, int page_size,
+                       const int64_t* row_req, const int32_t* indices, int64_t idx_stride, int topk,
+                       const int32_t* counts, const int32_t* seq_lens, const int32_t* query_pos, float scale,
+                       void* out, int64_t out_row_stride, int64_t out_head_stride, int out_dtype, float* lse, int rows,
+                       int splits, void* workspace, size_t workspace_bytes, const Addressing& ad,
+                       xt_stream_t stream);
+
 // Workspace: [arrival counters, kCounterBytes][partials [rows, splits, q_heads, kPartStride] FP32]
 
 extern "C" size_t xt_sparse_decode_workspace_bytes(int rows, int q_heads, int dim, int splits) {
@@ -547,6 +579,74 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
                                       void* workspace, size_t workspace_bytes, xt_stream_t stream) {
   const char* what = "xt_sparse_decode_nvfp4";
   if (dim != kDim) return fail(XT_EUNSUPPORTED, "%s: head size %d (supported: %d)", what, dim, kDim);
+  if (kv_heads <= 0) return fail(XT_EINVAL, "%s: kv_heads %d", what, kv_heads);
+  if (pay_stride == 0) pay_stride = (int64_t)kv_heads * (dim / 2);
+  if (sf_stride == 0) sf_stride = (int64_t)kv_heads * (dim / 16);
+  if (pay_stride < (int64_t)kv_heads * (dim / 2) || sf_stride < (int64_t)kv_heads * (dim / 16))
+    return fail(XT_EINVAL, "%s: slot strides %lld / %lld bytes must hold the heads' payload / scales", what,
+                (long long)pay_stride, (long long)sf_stride);
+  if (pool_slots <= 0 || pool_slots > 0x7FFFFFFFLL)
+    return fail(XT_EINVAL, "%s: pool_slots %lld outside 1..2^31-1", what, (long long)pool_slots);
+  const Addressing ad{dim / 2, dim / 16, 0, 1, 0, 0, 0x7FFFFFFF};
+  return decode_impl(what, q, q_row_stride, q_head_stride, k_pay, v_pay, k_scales, v_scales, gk, gv, pool_slots,
+                     pay_stride, sf_stride, kv_heads, q_heads, table, table_stride, page_size, row_req, indices,
+                     idx_stride, topk, counts, seq_lens, query_pos, scale, out, out_row_stride, out_head_stride,
+                     out_dtype, lse, rows, splits, workspace, workspace_bytes, ad, stream);
+}
+
+extern "C" int xt_block_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                                            const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_scales,
+                                            const uint8_t* v_scales, const float* kv_scale, int64_t pages,
+                                            int kv_heads, int q_heads, int dim, int block_size, int64_t page_stride,
+                                            int64_t head_stride, int64_t row_stride, int64_t sf_page_stride,
+                                            int64_t sf_head_stride, int64_t sf_row_stride,
+                                            const int32_t* req_to_token, int64_t req_stride, int max_kv_len,
+                                            const int64_t* slot_ids, const int32_t* topk_idx,
+                                            int64_t idx_head_stride, int64_t idx_row_stride, int topk_blocks,
+                                            const int32_t* seq_lens, float sm_scale, void* out,
+                                            int64_t out_row_stride, int64_t out_head_stride, int out_dtype,
+                                            float* lse, int rows, int splits, void* workspace,
+                                            size_t workspace_bytes, xt_stream_t stream) {
+  const char* what = "xt_block_sparse_decode_nvfp4";
+  if (dim != kDim) return fail(XT_EUNSUPPORTED, "%s: head size %d (supported: %d)", what, dim, kDim);
+  if (block_size <= 0 || (block_size & (block_size - 1)) || block_size > 4096)
+    return fail(XT_EINVAL, "%s: block_size %d must be a power of 2 up to 4096", what, block_size);
+  if (kv_heads <= 0 || pages <= 0 || topk_blocks < 0 || max_kv_len < 0)
+    return fail(XT_EINVAL, "%s: bad kv_heads / pages / topk / max_kv_len", what);
+  if (row_stride < dim / 2 || sf_row_stride < dim / 16 || row_stride % 16 || sf_row_stride % 4 || head_stride % 16 ||
+      sf_head_stride % 4 || page_stride % row_stride || sf_page_stride % sf_row_stride ||
+      page_stride / row_stride != sf_page_stride / sf_row_stride || page_stride / row_stride < block_size ||
+      head_stride < (int64_t)block_size * row_stride - row_stride + dim / 2 ||
+      sf_head_stride < (int64_t)block_size * sf_row_stride - sf_row_stride + dim / 16 ||
+      page_stride < (int64_t)(kv_heads - 1) * head_stride + (int64_t)block_size * row_stride)
+    return fail(XT_EINVAL, "%s: pool strides (page %lld, head %lld, row %lld; scales %lld, %lld, %lld bytes) do not "
+                "describe [pages, kv_heads, %d, dim/2] / [.., dim/16] pages", what, (long long)page_stride,
+                (long long)head_stride, (long long)row_stride, (long long)sf_page_stride, (long long)sf_head_stride,
+                (long long)sf_row_stride, block_size);
+  const int64_t mul = page_stride / row_stride;
+  if (pages > 0x7FFFFFFFLL / mul) return fail(XT_EUNSUPPORTED, "%s: %lld pages exceed 2^31 rows", what, (long long)pages);
+  if ((int64_t)topk_blocks * block_size > 0x7FFFFFFFLL)
+    return fail(XT_EUNSUPPORTED, "%s: %d blocks of %d keys", what, topk_blocks, block_size);
+  if (!slot_ids) return fail(XT_EINVAL, "%s: slot_ids is null", what);
+  const int shift = __builtin_ctz((unsigned)block_size);
+  const Addressing ad{head_stride, sf_head_stride, shift, mul, idx_head_stride, shift, max_kv_len};
+  return decode_impl(what, q, q_row_stride, q_head_stride, k_pay, v_pay, k_scales, v_scales, kv_scale, kv_scale,
+                     pages * mul, row_stride, sf_row_stride, kv_heads, q_heads, req_to_token, req_stride, 1,
+                     slot_ids, topk_idx, idx_row_stride, topk_blocks * block_size, nullptr, seq_lens, nullptr,
+                     sm_scale, out, out_row_stride, out_head_stride, out_dtype, lse, rows, splits, workspace,
+                     workspace_bytes, ad, stream);
+}
+
+static int decode_impl(const char* what, const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                       const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_scales, const uint8_t* v_scales,
+                       const float* gk, const float* gv, int64_t pool_slots, int64_t pay_stride, int64_t sf_stride,
+                       int kv_heads, int q_heads, const int32_t* table, int64_t table_stride, int page_size,
+                       const int64_t* row_req, const int32_t* indices, int64_t idx_stride, int topk,
+                       const int32_t* counts, const int32_t* seq_lens, const int32_t* query_pos, float scale,
+                       void* out, int64_t out_row_stride, int64_t out_head_stride, int out_dtype, float* lse, int rows,
+                       int splits, void* workspace, size_t workspace_bytes, const Addressing& ad,
+                       xt_stream_t stream) {
+  const int dim = kDim;
   if (kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads != 0)
     return fail(XT_EINVAL, "%s: q_heads %d must be a positive multiple of kv_heads %d", what, q_heads, kv_heads);
   const int group = q_heads / kv_heads;
@@ -559,17 +659,11 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
   if (!q || !k_pay || !v_pay || !k_scales || !v_scales || !gk || !gv || !table || !indices || !seq_lens || !out ||
       !workspace)
     return fail(XT_EINVAL, "%s: a required pointer is null", what);
-  if (pool_slots <= 0 || pool_slots > 0x7FFFFFFFLL)
-    return fail(XT_EINVAL, "%s: pool_slots %lld outside 1..2^31-1", what, (long long)pool_slots);
   if (!aligned(q, 16) || q_row_stride % 8 || q_head_stride % 8 || !aligned(out, 16) || out_row_stride % 8 ||
       out_head_stride % 8)
     return fail(XT_EINVAL, "%s: q and out rows must be 16-byte aligned (strides in elements: multiples of 8)", what);
-  if (pay_stride == 0) pay_stride = (int64_t)kv_heads * (dim / 2);
-  if (sf_stride == 0) sf_stride = (int64_t)kv_heads * (dim / 16);
-  if (pay_stride < (int64_t)kv_heads * (dim / 2) || sf_stride < (int64_t)kv_heads * (dim / 16) || pay_stride % 16 ||
-      sf_stride % 4)
-    return fail(XT_EINVAL, "%s: slot strides %lld / %lld bytes must hold the heads' payload / scales and be multiples "
-                "of 16 / 4", what, (long long)pay_stride, (long long)sf_stride);
+  if (pay_stride % 16 || sf_stride % 4 || ad.pay_head_stride % 16 || ad.sf_head_stride % 4)
+    return fail(XT_EINVAL, "%s: payload / scale strides must be multiples of 16 / 4 bytes", what);
   if (!aligned(k_pay, 16) || !aligned(v_pay, 16) || !aligned(k_scales, 4) || !aligned(v_scales, 4))
     return fail(XT_EINVAL, "%s: payload must be 16-byte and scales 4-byte aligned", what);
   if (lse && !aligned(lse, 4)) return fail(XT_EINVAL, "%s: lse must be 4-byte aligned", what);
@@ -582,7 +676,7 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
   if (!aligned(workspace, 256)) return fail(XT_EINVAL, "%s: workspace must be 256-byte aligned", what);
   const int per_split = (topk + splits - 1) / splits;
   const int kps = ((per_split + kStep - 1) / kStep) * kStep;
-  const int hpw = heads_per_workgroup(rows, kv_heads, splits);
+  const int hpw = ad.idx_head_stride ? 1 : heads_per_workgroup(rows, kv_heads, splits);
   const int slices = kWaves / hpw;
   const int slice_steps = ((kps / kStep + slices * kPrefetch - 1) / (slices * kPrefetch)) * kPrefetch;
   const int slot_bytes = slices * slice_steps * kStep * (int)sizeof(int32_t);
@@ -605,6 +699,13 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
   a.pool_slots = pool_slots;
   a.pay_stride = pay_stride;
   a.sf_stride = sf_stride;
+  a.pay_head_stride = ad.pay_head_stride;
+  a.sf_head_stride = ad.sf_head_stride;
+  a.remap_shift = ad.remap_shift;
+  a.remap_mul = ad.remap_mul;
+  a.idx_head_stride = ad.idx_head_stride;
+  a.block_shift = ad.block_shift;
+  a.max_len = ad.max_len;
   a.kv_heads = kv_heads;
   a.q_heads = q_heads;
   a.group = group;

@@ -204,21 +204,81 @@ def sparse_decode(q, raw, table, indices, seq_lens, scale, page_size=1, row_req=
     seq_lens, counts, query_pos = (None if t is None else (t if t.dtype == torch.int32 else t.to(torch.int32))
                                    for t in (seq_lens, counts, query_pos))
     if splits is None:
-        splits = default_splits(rows, kv_heads, topk)
-        if (ws is None and torch.cuda.is_current_stream_capturing()
-                and _cached_workspace_bytes(q.device) < decode_workspace_bytes(rows, q_heads, dim, splits)):
-            splits = 1   # one key split needs no partials, so no workspace to grow inside the capture
-    need = decode_workspace_bytes(rows, q_heads, dim, splits)
-    if ws is None:
-        ws = (workspace(q.device, need) if _cached_workspace_bytes(q.device) >= need
-              or not torch.cuda.is_current_stream_capturing()
-              else torch.empty(need, dtype=torch.uint8, device=q.device))   # splits 1: the kernel never reads it
+        splits = _capture_splits(q.device, rows, q_heads, dim, default_splits(rows, kv_heads, topk), ws)
+    ws = _decode_ws(q.device, rows, q_heads, dim, splits, ws)
     _lib.check(_lib.lib().xt_sparse_decode_nvfp4(
         _ptr(q), q.stride(0), q.stride(1), *map(_ptr, raw), raw[0].shape[0], raw[0].stride(0), raw[2].stride(0),
         kv_heads, q_heads, dim, _ptr(table),
         table.stride(0), int(page_size), _ptr(row_req), _ptr(indices), indices.stride(0), topk, _ptr(counts),
         _ptr(seq_lens), _ptr(query_pos), float(scale), _ptr(out), out.stride(0), out.stride(1), _DTYPES[out.dtype],
         _ptr(lse), rows, int(splits), _ptr(ws), ws.numel(), _stream(q)), 'sparse_decode')
+    return out
+
+
+def _capture_splits(device, rows, q_heads, dim, splits, ws):
+    """``splits``, or 1 inside a graph capture whose cached workspace is too small (one key split needs no partials,
+    so no workspace has to grow inside the capture)."""
+    if (ws is None and torch.cuda.is_current_stream_capturing()
+            and _cached_workspace_bytes(device) < decode_workspace_bytes(rows, q_heads, dim, splits)):
+        return 1
+    return splits
+
+
+def _decode_ws(device, rows, q_heads, dim, splits, ws):
+    """The caller's workspace, else the per-device one (a throwaway buffer for one split inside a capture that the
+    cached one cannot serve: the kernel never reads it then)."""
+    need = decode_workspace_bytes(rows, q_heads, dim, splits)
+    if ws is not None:
+        return ws
+    if _cached_workspace_bytes(device) >= need or not torch.cuda.is_current_stream_capturing():
+        return workspace(device, need)
+    return torch.empty(need, dtype=torch.uint8, device=device)
+
+
+def fp4_sparse_decode(q, k_pay, k_sc, v_pay, v_sc, req_to_token, slot_ids, topk_idx, seq_lens, block_size,
+                      sm_scale=None, kv_scale=1.0, num_warps=4, num_stages=2, out=None, lse=None, splits=None,
+                      ws=None):
+    """Block-sparse decode over an NVFP4 cache of head-major pages (kv_fp4.py:119-153): q [b, qh, d] BF16; k_pay /
+    v_pay [pages, kh, block, d/2] uint8; k_sc / v_sc [pages, kh, block, d/16] E4M3 bytes (uint8 or float8_e4m3fn);
+    topk_idx [kh, b, topk] block ids (-1 padded at the end); row b reads request slot_ids[b] of req_to_token, its
+    length clamped to req_to_token.shape[1]. kv_scale multiplies the scores and the output. Returns [b, qh, d] (BF16
+    unless ``out`` is given); lse [b, qh] FP32 is filled if given. num_warps / num_stages are accepted for the
+    reference's signature and ignored."""
+    assert block_size == k_pay.shape[2] and k_pay.stride(3) == 1 and k_sc.stride(3) == 1
+    assert k_pay.stride() == v_pay.stride() and k_sc.stride() == v_sc.stride()
+    b, qh, d = q.shape
+    kh = k_pay.shape[1]
+    if k_pay.shape[3] * 2 != d or k_sc.shape[3] * 16 != d or k_pay.shape != v_pay.shape or k_sc.shape != v_sc.shape:
+        raise ValueError(f'xtier_amd.fp4_sparse_decode: pages {tuple(k_pay.shape)} / {tuple(k_sc.shape)} do not hold '
+                         f'head size {d}')
+    if qh % kh:
+        raise ValueError(f'xtier_amd.fp4_sparse_decode: {qh} query heads over {kh} KV heads')
+    _need_cuda(q, k_pay, k_sc, v_pay, v_sc, req_to_token, slot_ids, topk_idx, seq_lens, out, lse)
+    if sm_scale is None:
+        sm_scale = d ** -0.5
+    k_pay, v_pay, k_sc, v_sc = (t if t.dtype == torch.uint8 else t.view(torch.uint8) for t in (k_pay, v_pay, k_sc, v_sc))
+    if q.dtype != torch.bfloat16 or q.stride(-1) != 1:
+        q = q.to(torch.bfloat16).contiguous()
+    if out is None:
+        out = torch.empty((b, qh, d), dtype=torch.bfloat16, device=q.device)
+    if req_to_token.dtype != torch.int32 or req_to_token.stride(1) != 1:
+        req_to_token = req_to_token.to(torch.int32).contiguous()
+    if topk_idx.dtype != torch.int32 or topk_idx.stride(2) != 1:
+        topk_idx = topk_idx.to(torch.int32).contiguous()
+    slot_ids = slot_ids if slot_ids.dtype == torch.int64 else slot_ids.to(torch.int64)
+    seq_lens = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
+    scale_dev = torch.full((1,), float(kv_scale), dtype=torch.float32, device=q.device)
+    topk = topk_idx.shape[2]
+    if splits is None:
+        splits = _capture_splits(q.device, b, qh, d, default_splits(b, kh, topk * block_size), ws)
+    ws = _decode_ws(q.device, b, qh, d, splits, ws)
+    _lib.check(_lib.lib().xt_block_sparse_decode_nvfp4(
+        _ptr(q), q.stride(0), q.stride(1), _ptr(k_pay), _ptr(v_pay), _ptr(k_sc), _ptr(v_sc), _ptr(scale_dev),
+        k_pay.shape[0], kh, qh, d, int(block_size), k_pay.stride(0), k_pay.stride(1), k_pay.stride(2),
+        k_sc.stride(0), k_sc.stride(1), k_sc.stride(2), _ptr(req_to_token), req_to_token.stride(0),
+        req_to_token.shape[1], _ptr(slot_ids), _ptr(topk_idx), topk_idx.stride(0), topk_idx.stride(1), topk,
+        _ptr(seq_lens), float(sm_scale), _ptr(out), out.stride(0), out.stride(1), _DTYPES[out.dtype], _ptr(lse), b,
+        int(splits), _ptr(ws), ws.numel(), _stream(q)), 'fp4_sparse_decode')
     return out
 
 

@@ -129,6 +129,43 @@ MLA_WORKLOADS = {
 }
 
 
+@dataclass(frozen=True)
+class BlockDecodeWorkload:
+    """Block-sparse decode over head-major NVFP4 pages (the MiniMax cache layout): each (request, KV head) attends to
+    `topk_blocks` distinct blocks of `block` tokens of its context (one block = one page row range), chosen uniformly
+    per KV head; the pool has a unit global scale."""
+    name: str
+    batch: int
+    q_heads: int
+    kv_heads: int
+    dim: int
+    ctx: int
+    topk_blocks: int
+    block: int = 128
+    q_std: float = 1.0
+
+    @property
+    def pages(self):
+        return self.batch * (self.ctx // self.block)
+
+    @property
+    def keys(self):
+        return self.topk_blocks * self.block
+
+    def algorithmic_bytes(self):
+        """Read KV payload plus scales: batch * kv_heads * keys * 2 * (dim/2 + dim/16)."""
+        return self.batch * self.kv_heads * self.keys * 2 * (self.dim // 2 + self.dim // 16)
+
+    def flops(self):
+        return self.batch * self.q_heads * self.keys * 4 * self.dim
+
+
+BLOCK_WORKLOADS = {
+    # batch 32, 64 q / 4 KV heads, d 128, context 32768, 16 blocks of 128 tokens per KV head (2048 keys)
+    'minimax_decode_b32': BlockDecodeWorkload('minimax_decode_b32', 32, 64, 4, 128, 32768, 16),
+}
+
+
 def generator(device, seed):
     g = torch.Generator(device=device)
     g.manual_seed(seed)
@@ -269,3 +306,39 @@ def mla_inputs(w, seed, device='cpu'):
         req = torch.arange(w.rows, device=device)
     slots = (pt[req[:, None], (pos // w.page).long()].long() * w.page + pos % w.page).to(torch.int32)
     return MlaInputs(w, q, slots, pos)
+
+
+@dataclass
+class BlockDecodeInputs:
+    workload: BlockDecodeWorkload
+    q: torch.Tensor            # bf16 [batch, q_heads, dim]
+    req_to_token: torch.Tensor  # int32 [batch, ctx]: block-aligned page rows, pages in a random order
+    slot_ids: torch.Tensor     # int64 [batch]
+    topk_idx: torch.Tensor     # int32 [kv_heads, batch, topk_blocks]: sorted distinct block ids
+    seq_lens: torch.Tensor     # int32 [batch]
+
+
+def block_decode_inputs(w, seed, device='cpu', batch=None):
+    """Seeded queries, request tables and per-KV-head block lists of a block-sparse decode workload."""
+    b = w.batch if batch is None else batch
+    gen = generator(device, seed)
+    q = (torch.randn(b, w.q_heads, w.dim, generator=gen, device=device) * w.q_std).to(torch.bfloat16)
+    pt = page_table(b, w.ctx, w.block, gen, device)
+    r2t = token_table(pt, w.block)
+    nb = w.ctx // w.block
+    idx = torch.empty(w.kv_heads, b, w.topk_blocks, dtype=torch.int32, device=device)
+    for h in range(w.kv_heads):
+        for r in range(b):
+            idx[h, r] = torch.sort(torch.randperm(nb, generator=gen, device=device)[:w.topk_blocks]).values
+    seq = torch.full((b,), w.ctx, dtype=torch.int32, device=device)
+    return BlockDecodeInputs(w, q, r2t, torch.arange(b, dtype=torch.int64, device=device), idx, seq)
+
+
+def head_major_pages(x_pay, x_sc, block):
+    """Token-major pool bytes [slots, heads, n] (slot = page * block + row) -> head-major pages [pages, heads, block,
+    n] (the MiniMax cache layout)."""
+    slots, heads, n = x_pay.shape
+    pay = x_pay.view(slots // block, block, heads, n).permute(0, 2, 1, 3).contiguous()
+    m = x_sc.shape[2]
+    sc = x_sc.view(slots // block, block, heads, m).permute(0, 2, 1, 3).contiguous()
+    return pay, sc
