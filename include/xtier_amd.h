@@ -148,6 +148,29 @@ int xt_block_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_
                                  void* out, int64_t out_row_stride, int64_t out_head_stride, int out_dtype, float* lse,
                                  int rows, int splits, void* workspace, size_t workspace_bytes, xt_stream_t stream);
 
+/* --- split-K decode over packed BF16 rows ------------------------------------------------------------------------ */
+
+/* Device workspace of xt_varlen_decode_bf16 for `rows` rows, `heads` query heads of size dim and `splits` key splits
+ * (0 on a bad argument). */
+size_t xt_varlen_decode_workspace_bytes(int rows, int heads, int dim, int splits);
+
+/* Split-K GQA decode over packed BF16 K/V rows (replaces xtier/packs/qwen4_exp/qsa_decode.py:89-113, varlen_decode,
+ * with its kernels _split :25-60 and _merge :63-86). Row r (< rows) has one query, q[cu_seqlens_q[r]] ([*, heads, dim]
+ * BF16, element strides q_row_stride / q_head_stride), which attends to keys cu_seqlens_k[r] .. cu_seqlens_k[r+1]-1
+ * of k / v ([keys, kv_heads, dim] BF16, element strides per key and per KV head); query head h reads KV head
+ * h / (heads / kv_heads). Scores q.k in FP32 times softmax_scale * log2(e), exp2, P rounded to BF16 for the PV
+ * product, FP32 sums; out[cu_seqlens_q[r], h] (out_dtype BF16 or FP16) = the normalized output, 0 for a row without
+ * keys. dim 64, 128 or 256; heads / kv_heads <= 128; max_seqlen_k >= every row's key count (it sizes the splits).
+ * splits 1..64, workspace xt_varlen_decode_workspace_bytes(...) bytes (256-byte aligned, zero before its first use,
+ * left zero; the arrival counters are the fixed region the other decode entry points use, rows * kv_heads <= 16384
+ * when splits > 1). One launch on `stream`. */
+int xt_varlen_decode_bf16(const void* q, int64_t q_row_stride, int64_t q_head_stride, const void* k,
+                          int64_t k_key_stride, int64_t k_head_stride, const void* v, int64_t v_key_stride,
+                          int64_t v_head_stride, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int rows,
+                          int heads, int kv_heads, int dim, int max_seqlen_k, float softmax_scale, void* out,
+                          int64_t out_row_stride, int64_t out_head_stride, int out_dtype, int splits, void* workspace,
+                          size_t workspace_bytes, xt_stream_t stream);
+
 /* --- sparse MLA over an NVFP4 latent cache ------------------------------------------------------------------------ */
 
 /* One latent cache: per slot a latent row of latent_dim NVFP4 values (payload latent_dim/2 bytes, E4M3 scales

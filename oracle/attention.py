@@ -188,6 +188,23 @@ def merge_partials(m, l, acc):
         return np.where(total[:, None] > 0, out / total[:, None], 0.0)
 
 
+def varlen_decode(q, k, v, cu_q, cu_k, scale, keys_per_split=128):
+    """qsa_decode.py:25-113: row r's query q[cu_q[r]] ([T, Hq, D]) attends to the packed keys k / v [cu_k[r],
+    cu_k[r+1]) ([N, Hkv, D]), as the reference computes it: split partials of keys_per_split keys (running max in
+    the log2 domain, sum, unnormalized accumulator) merged with weights 2^(m - max m); FP64 here. Returns
+    [rows, Hq, D] (rows = len(cu_q) - 1); a row without keys gives 0."""
+    rows = len(cu_q) - 1
+    out = np.zeros((rows, q.shape[1], v.shape[-1]))
+    for r in range(rows):
+        a, b = int(cu_k[r]), int(cu_k[r + 1])
+        if b <= a:
+            continue
+        m, l, acc = split_partials(np.asarray(q[int(cu_q[r])], np.float64), k[a:b], v[a:b], np.ones(b - a, bool),
+                                   scale, keys_per_split)
+        out[r] = merge_partials(m, l, acc)
+    return out
+
+
 # --- block-sparse decode over head-major pages (MiniMax) ----------------------------------------------------------
 
 def block_sparse_decode(q, k_pay, k_sf, v_pay, v_sf, req_to_token, slot_ids, topk_idx, seq_lens, block_size, scale,

@@ -1,0 +1,92 @@
+"""Split-K decode over packed BF16 rows (qsa_decode.py:89-113) on the GPU against the oracle's restatement of the
+reference (128-key split partials merged in FP64) and the flash-precision reference: head sizes 64 / 128 / 256, GQA
+groups 8 / 16 / 32, ragged rows including empty ones, explicit splits, strided K/V views, graph replay."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention
+from tests._attn import check
+from xtier_amd import ops, workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(seed, counts, heads, kv_heads, dim, extra_queries=0):
+    gen = workloads.generator('cpu', seed)
+    cu_k = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int32)
+    n = int(cu_k[-1])
+    k = workloads.kv_tensor(max(n, 1), kv_heads, dim, gen, 'cpu')
+    v = workloads.kv_tensor(max(n, 1), kv_heads, dim, gen, 'cpu')
+    rows = len(counts)
+    q = (torch.randn(rows + extra_queries, heads, dim, generator=gen) * 0.5).to(torch.bfloat16)
+    cu_q = torch.arange(rows + 1, dtype=torch.int32)
+    return q, k, v, cu_q, cu_k
+
+
+def _ref(q, k, v, cu_q, cu_k, scale):
+    qf, kf, vf = (t.float().numpy() for t in (q, k, v))
+    ref = attention.varlen_decode(qf, kf, vf, cu_q.numpy(), cu_k.numpy(), scale)
+    flash = np.zeros_like(ref)
+    for r in range(len(cu_q) - 1):
+        a, b = int(cu_k[r]), int(cu_k[r + 1])
+        flash[r] = attention.flash_precision_attention(qf[int(cu_q[r])], kf[a:b], vf[a:b], np.ones(b - a, bool),
+                                                       scale)
+    return ref, flash
+
+
+@pytest.mark.parametrize('dim,heads,kv_heads', [(128, 32, 4), (256, 16, 1), (64, 64, 2), (128, 32, 2)])
+@pytest.mark.parametrize('splits', [None, 1, 5])
+def test_varlen_against_oracle(dim, heads, kv_heads, splits):
+    counts = [2048, 0, 1, 700, 33, 1500]
+    q, k, v, cu_q, cu_k = _case(dim + heads, counts, heads, kv_heads, dim)
+    scale = dim ** -0.5
+    out = ops.varlen_decode(q.cuda(), k.cuda(), v.cuda(), cu_q.cuda(), cu_k.cuda(), 1, max(counts), scale,
+                            splits=splits)
+    assert out.shape == q.shape and out.dtype == torch.bfloat16
+    ref, flash = _ref(q, k, v, cu_q, cu_k, scale)
+    got = out.float().cpu()
+    assert torch.equal(got[1], torch.zeros_like(got[1]))           # a row without keys
+    nonempty = np.array(counts) > 0
+    check(out.cpu()[torch.from_numpy(nonempty)], ref[nonempty], flash[nonempty])
+
+
+def test_varlen_strided_views_and_query_rows():
+    """K/V as head slices of a larger buffer and queries at cu_seqlens_q positions (rows with one query each)."""
+    counts = [300, 129, 64]
+    q, k, v, _, cu_k = _case(5, counts, 16, 2, 128, extra_queries=3)
+    big_k = torch.zeros(k.shape[0], 3, 128, dtype=torch.bfloat16)
+    big_v = torch.zeros_like(big_k)
+    big_k[:, 1:] = k
+    big_v[:, 1:] = v
+    cu_q = torch.tensor([0, 2, 4, 5], dtype=torch.int32)            # queries 0, 2, 4 of q
+    out = torch.full_like(q, float('nan')).cuda()
+    ops.varlen_decode(q.cuda(), big_k.cuda()[:, 1:], big_v.cuda()[:, 1:], cu_q.cuda(), cu_k.cuda(), 1, 300, 0.09,
+                      out=out, splits=2)
+    sel = cu_q[:-1].long()
+    ref, flash = _ref(q, k, v, cu_q, cu_k, 0.09)
+    check(out[sel.cuda()].cpu(), ref, flash)
+    assert torch.isnan(out[1].float()).all()                        # rows not named are untouched
+
+
+def test_varlen_graph_replay_equals_eager():
+    counts = [1000, 17, 512]
+    q, k, v, cu_q, cu_k = _case(8, counts, 32, 4, 128)
+    qd, kd, vd, cq, ck = (t.cuda() for t in (q, k, v, cu_q, cu_k))
+    splits = 3
+    ws = torch.zeros(ops.varlen_workspace_bytes(3, 32, 128, splits), dtype=torch.uint8, device='cuda')
+    out = torch.empty_like(qd)
+    ops.varlen_decode(qd, kd, vd, cq, ck, 1, 1000, 0.1, out=out, splits=splits, ws=ws)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.varlen_decode(qd, kd, vd, cq, ck, 1, 1000, 0.1, out=out, splits=splits, ws=ws)
+    gen = torch.Generator(device='cuda').manual_seed(2)
+    for _ in range(3):
+        qd.copy_(torch.randn(qd.shape, generator=gen, device='cuda').to(torch.bfloat16))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        eager = ops.varlen_decode(qd, kd, vd, cq, ck, 1, 1000, 0.1, splits=splits)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), eager.view(torch.int16))

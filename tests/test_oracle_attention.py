@@ -251,3 +251,20 @@ def test_block_decode_clamps_length_to_the_table_and_skips_blocks_past_it():
     b, _ = attention.block_sparse_decode(q, *pool, r2t, sid, ids, np.where(np.arange(3) == 0, r2t.shape[1], seq),
                                          block, 0.1)
     np.testing.assert_array_equal(a, b)
+
+
+def test_varlen_split_form_equals_one_pass_softmax():
+    """qsa_decode.py's split/merge form (128-key splits) equals the one-pass softmax per row; an empty row is 0."""
+    rng = np.random.default_rng(9)
+    counts = [300, 0, 1, 129, 128]
+    cu_k = np.concatenate([[0], np.cumsum(counts)])
+    k = rng.standard_normal((cu_k[-1], 2, 16))
+    v = rng.standard_normal((cu_k[-1], 2, 16))
+    q = rng.standard_normal((7, 8, 16))
+    cu_q = np.array([0, 2, 3, 4, 6, 7])
+    got = attention.varlen_decode(q, k, v, cu_q, cu_k, 0.3)
+    for r, n in enumerate(counts):
+        a = cu_k[r]
+        want = attention.softmax_attention(q[cu_q[r]], k[a:a + n], v[a:a + n], np.ones(n, bool), 0.3)
+        np.testing.assert_allclose(got[r], want, rtol=1e-12, atol=1e-12)
+    assert np.all(got[1] == 0)

@@ -105,3 +105,10 @@ def test_quantize_substitutes_device_unit_scale():
     assert torch.is_tensor(log[-1][0][1]) and log[-1][0][1].tolist() == [1.0] and log[-1][0][2] == 'x'
     qsa.quantize(original, t, 0.5)
     assert log[-1][0][1] == 0.5
+
+
+def test_resolve_returns_the_varlen_decode():
+    from xtier_amd import ops
+    assert qsa.resolve(lambda: 'original') is ops.varlen_decode
+    with pytest.raises(NotImplementedError):
+        ops.varlen_decode(torch.zeros(2, 4, 64), None, None, torch.zeros(3), torch.zeros(3), 2, 8, 0.1)

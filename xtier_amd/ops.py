@@ -282,6 +282,49 @@ def fp4_sparse_decode(q, k_pay, k_sc, v_pay, v_sc, req_to_token, slot_ids, topk_
     return out
 
 
+# --- split-K decode over packed BF16 rows --------------------------------------------------------------------------
+
+def varlen_workspace_bytes(rows, heads, dim, splits):
+    return int(_lib.lib().xt_varlen_decode_workspace_bytes(rows, heads, dim, splits))
+
+
+def varlen_decode(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, causal=True,
+                  out=None, splits=None, ws=None, **_):
+    """flash_attn_varlen_func for decode-shaped calls (qsa_decode.py:89-113): one query per row, which sees all of the
+    row's packed keys [cu_seqlens_k[r], cu_seqlens_k[r + 1]). q [rows, heads, dim]; k, v [keys, KV heads, dim], BF16.
+    Returns out shaped like q (rows it does not name are left as allocated)."""
+    if max_seqlen_q != 1:
+        raise NotImplementedError('xtier_amd.varlen_decode takes one query per row')
+    q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+    _need_cuda(q, k, v, cu_seqlens_q, cu_seqlens_k, out)
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise ValueError('xtier_amd.varlen_decode: BF16 q, k, v expected')
+    rows = cu_seqlens_q.shape[0] - 1
+    heads, dim = q.shape[1], q.shape[2]
+    kv_heads = k.shape[1]
+    if out is None:
+        out = torch.empty_like(q)
+    if rows <= 0:
+        return out
+    cu_q, cu_k = (t if t.dtype == torch.int32 else t.to(torch.int32) for t in (cu_seqlens_q, cu_seqlens_k))
+    max_k = max(int(max_seqlen_k), 1)
+    if splits is None:
+        splits = default_splits(rows, kv_heads, max_k)
+        if (ws is None and torch.cuda.is_current_stream_capturing()
+                and _cached_workspace_bytes(q.device) < varlen_workspace_bytes(rows, heads, dim, splits)):
+            splits = 1
+    need = varlen_workspace_bytes(rows, heads, dim, splits)
+    if ws is None:
+        ws = (workspace(q.device, need) if _cached_workspace_bytes(q.device) >= need
+              or not torch.cuda.is_current_stream_capturing()
+              else torch.empty(need, dtype=torch.uint8, device=q.device))
+    _lib.check(_lib.lib().xt_varlen_decode_bf16(
+        _ptr(q), q.stride(0), q.stride(1), _ptr(k), k.stride(0), k.stride(1), _ptr(v), v.stride(0), v.stride(1),
+        _ptr(cu_q), _ptr(cu_k), rows, heads, kv_heads, dim, max_k, float(softmax_scale), _ptr(out), out.stride(0),
+        out.stride(1), _DTYPES[out.dtype], int(splits), _ptr(ws), ws.numel(), _stream(q)), 'varlen_decode')
+    return out
+
+
 # --- sparse MLA ----------------------------------------------------------------------------------------------------
 
 def _mla_cache(raw):
