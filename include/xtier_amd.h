@@ -207,9 +207,10 @@ size_t xt_sparse_mla_workspace_bytes(int rows, int heads, int splits);
  * written in out_dtype to out (BF16/FP16 [rows, heads, latent_dim], strides in elements); sink NULL: no sink term.
  * lse (optional FP32 [rows, heads]): natural log of sum_k exp(s_k) over the keys only (sparse_mla.py:73-85); a row
  * without valid keys writes zeros and lse -inf. latent_dim 512, rope_dim 64, heads <= 128 are supported.
- * splits: key splits per row (1..64; rows <= 16384 with splits > 1); workspace as for the decode:
- * xt_sparse_mla_workspace_bytes bytes, 256-byte aligned, zero-filled before first use, its counters left zero by
- * every call (one workspace may serve decode and MLA calls of any shape, one at a time). */
+ * splits: key splits per row (1..64); with splits > 1 a second launch on `stream` merges the split partials.
+ * workspace: xt_sparse_mla_workspace_bytes bytes, 256-byte aligned; its first 64 KB are left untouched (the counter
+ * region of the decode entry points), so one zero-filled workspace may serve decode and MLA calls of any shape, one at
+ * a time. */
 int xt_sparse_mla_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, int heads, int latent_dim,
                         int rope_dim, const xt_mla_cache* cache, const xt_mla_keys* keys,
                         const xt_mla_cache* extra_cache, const xt_mla_keys* extra_keys, const float* sink, float scale,

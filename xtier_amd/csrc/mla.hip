@@ -1,7 +1,8 @@
 // Sparse MLA over an NVFP4 latent cache: 128 query heads share one key per token, [latent (512, NVFP4) | rope (64,
 // BF16)] = 576 wide, whose value is the latent. q.k and p.v on MFMA (v_mfma_f32_16x16x32_f16), online softmax in the
-// exp2 domain, an optional per-head sink in the denominator, one launch (split partials merged by the last
-// workgroup of a row).
+// exp2 domain, an optional per-head sink in the denominator. With key splits, each (row, split) writes its output
+// normalized by its own sum (FP16) with its max and sum, and a second, wide launch merges the splits: one merging
+// workgroup per row would read a row's partials at one CU's bandwidth.
 //
 // Work decomposition: a workgroup = 8 wavefronts x 16 heads = 128 heads of one (query row, key split), so every key is
 // read and dequantized once for all heads. Per step of 32 keys the workgroup
@@ -68,7 +69,6 @@ struct MlaArgs {
   int heads, splits, keys_per_split, steps;
   uint16_t* part;                    // [rows, splits, heads, 512] FP16: the split's output normalized by its own sum
   float* ml;                         // [rows, splits, heads, 2]: the split's running max (log2 domain) and sum
-  int32_t* counters;                 // [rows]
   uint32_t xcd_units, xcd_extra;
 };
 
@@ -164,11 +164,6 @@ __device__ inline void store_vals(const MlaArgs& a, int64_t row, int head, int d
   }
 }
 
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-// 8-byte store written through to L2 (sc1), so the merging workgroup of another CU reads it after the counter
-__device__ inline void store_through(__amdgpu_buffer_rsrc_t r, int byte_off, u32x2_t v) {
-  __builtin_amdgcn_raw_buffer_store_b64(v, r, byte_off, 0, 16);
-}
 
 template <bool TWO>
 __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
@@ -334,77 +329,56 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
     return;
   }
   // 2. the split's output normalized by its own sum (FP16: a convex combination of FP16 latent values) plus its
-  //    max and sum, written through; the last workgroup of the row merges the splits
+  //    max and sum; a second launch merges the splits
   if (head_live) {
     const int64_t ph = ((int64_t)row * a.splits + split) * a.heads + head;
-    const __amdgpu_buffer_rsrc_t pr =
-        __builtin_amdgcn_make_buffer_rsrc(a.part + ph * kDl, (short)0, kDl * 2, 0x00020000);
+    uint16_t* pp = a.part + ph * kDl;
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
 #pragma unroll
     for (int dt = 0; dt < 32; ++dt) {
-      const u32x2_t w = {f32_to_f16_bits(acc[dt][0] * inv) | (f32_to_f16_bits(acc[dt][1] * inv) << 16),
-                         f32_to_f16_bits(acc[dt][2] * inv) | (f32_to_f16_bits(acc[dt][3] * inv) << 16)};
-      store_through(pr, (16 * dt + 4 * j) * 2, w);
+      const uint2 w = {f32_to_f16_bits(acc[dt][0] * inv) | (f32_to_f16_bits(acc[dt][1] * inv) << 16),
+                       f32_to_f16_bits(acc[dt][2] * inv) | (f32_to_f16_bits(acc[dt][3] * inv) << 16)};
+      *reinterpret_cast<uint2*>(pp + 16 * dt + 4 * j) = w;
     }
-    if (j == 0) {
-      const __amdgpu_buffer_rsrc_t mr = __builtin_amdgcn_make_buffer_rsrc(a.ml + ph * 2, (short)0, 8, 0x00020000);
-      store_through(mr, 0, u32x2_t{__float_as_uint(m), __float_as_uint(l_tot)});
+    if (j == 0) *reinterpret_cast<float2*>(a.ml + ph * 2) = float2{m, l_tot};
+  }
+}
+
+// Split merge: one thread per (row, head, 8 dims); 64 threads cover a head's 512 dims with 16-byte loads.
+// out = sum_s w_s o_s with w_s = 2^(m_s - max m) l_s / (sum_s 2^(m_s - max m) l_s + sink term).
+__global__ void __launch_bounds__(256) mla_merge_kernel(const MlaArgs a, int rows) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t rh = t >> 6;                  // row * heads + head
+  if (rh >= (int64_t)rows * a.heads) return;
+  const int c = (int)(t & 63);
+  const int row = (int)(rh / a.heads), head = (int)(rh % a.heads);
+  const int64_t base = (int64_t)row * a.splits * a.heads + head;   // (row, split 0, head)
+  float mx = -__builtin_inff();
+  for (int sp = 0; sp < a.splits; ++sp) mx = fmaxf(mx, a.ml[(base + (int64_t)sp * a.heads) * 2]);
+  const float mu = (mx == -__builtin_inff()) ? 0.0f : mx;
+  float l_all = 0.0f;
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < a.splits; ++sp) {
+    const int64_t ph = base + (int64_t)sp * a.heads;
+    const float2 ml = *reinterpret_cast<const float2*>(a.ml + ph * 2);
+    const uint4 x = *reinterpret_cast<const uint4*>(a.part + ph * kDl + 8 * c);
+    const float w = __builtin_amdgcn_exp2f(ml.x - mu) * ml.y;
+    l_all += w;
+    const uint32_t u[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const half2_t h = __builtin_bit_cast(half2_t, u[e]);
+      o[2 * e] += w * (float)h.x;
+      o[2 * e + 1] += w * (float)h.y;
     }
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  __shared__ int32_t s_last;
-  int32_t* counter = a.counters + row;
-  if (threadIdx.x == 0)
-    s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.splits - 1;
-  __syncthreads();
-  if (!s_last) return;
-  // 16 threads per head, 32 heads per pass; thread jj reads and writes dims 8 (16 k + jj) .. +7, k = 0..3, so the
-  // 16 threads of a head cover 256 contiguous bytes per load
-  const int jj = threadIdx.x & 15;
-  const int64_t sstride = (int64_t)a.heads;   // (split, head) records of this row: index sp * heads + head
-  const uint16_t* row_part = a.part + (int64_t)row * a.splits * a.heads * kDl;
-  const float* row_ml = a.ml + (int64_t)row * a.splits * a.heads * 2;
-  for (int hh = threadIdx.x >> 4; hh < a.heads; hh += 32) {
-    float mx = -__builtin_inff();
-    for (int sp = 0; sp < a.splits; ++sp) mx = fmaxf(mx, row_ml[(sp * sstride + hh) * 2]);
-    const float mu = (mx == -__builtin_inff()) ? 0.0f : mx;
-    float l_all = 0.0f;
-    for (int sp = 0; sp < a.splits; ++sp) {
-      const float2 ml = *reinterpret_cast<const float2*>(row_ml + (sp * sstride + hh) * 2);
-      l_all += __builtin_amdgcn_exp2f(ml.x - mu) * ml.y;
-    }
-    float total = l_all;
-    if (a.sink) total += __builtin_amdgcn_exp2f(a.sink[hh] * kLog2e - mu);
-    const float inv = l_all > 0.0f ? 1.0f / total : 0.0f;
-    float o[32];
+  float total = l_all;
+  if (a.sink) total += __builtin_amdgcn_exp2f(a.sink[head] * kLog2e - mu);
+  const float inv = l_all > 0.0f ? 1.0f / total : 0.0f;
 #pragma unroll
-    for (int e = 0; e < 32; ++e) o[e] = 0.0f;
-#pragma unroll 2
-    for (int sp = 0; sp < a.splits; ++sp) {
-      const float2 ml = *reinterpret_cast<const float2*>(row_ml + (sp * sstride + hh) * 2);
-      const float w = __builtin_amdgcn_exp2f(ml.x - mu) * ml.y * inv;
-      const uint4* src = reinterpret_cast<const uint4*>(row_part + (sp * sstride + hh) * kDl);
-      uint4 x[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) x[k] = src[16 * k + jj];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t u[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const half2_t h = __builtin_bit_cast(half2_t, u[e]);
-          o[8 * k + 2 * e] += w * (float)h.x;
-          o[8 * k + 2 * e + 1] += w * (float)h.y;
-        }
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) store_vals(a, row, hh, 8 * (16 * k + jj), o + 8 * k, 8);
-    if (a.lse && jj == 0)
-      a.lse[row * a.heads + hh] = l_all > 0.0f ? (mu + __builtin_log2f(l_all)) * kLn2 : -__builtin_inff();
-  }
-  if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int e = 0; e < 8; ++e) o[e] *= inv;
+  store_vals(a, row, head, 8 * c, o, 8);
+  if (a.lse && c == 0) a.lse[rh] = l_all > 0.0f ? (mu + __builtin_log2f(l_all)) * kLn2 : -__builtin_inff();
 }
 
 int check_cache(const char* what, const xt_mla_cache* c, int64_t* pay_stride, int64_t* sf_stride,
@@ -428,8 +402,8 @@ int check_cache(const char* what, const xt_mla_cache* c, int64_t* pay_stride, in
 
 using namespace xt;
 
-// Workspace: [arrival counters, kCounterBytes][partial outputs [rows, splits, heads, 512] FP16][partial max and sum
-// [rows, splits, heads, 2] FP32]
+// Workspace: [kCounterBytes, unused here: the counter region of the decode entry points][partial outputs [rows,
+// splits, heads, 512] FP16][partial max and sum [rows, splits, heads, 2] FP32]
 
 extern "C" size_t xt_sparse_mla_workspace_bytes(int rows, int heads, int splits) {
   if (rows < 0 || heads <= 0 || splits <= 0) return 0;
@@ -473,9 +447,6 @@ extern "C" int xt_sparse_mla_nvfp4(const void* q, int64_t q_row_stride, int64_t 
   } else {
     a.c[1] = a.c[0];
   }
-  if (splits > 1 && rows > kCounterSlots)
-    return fail(XT_EUNSUPPORTED, "%s: %d rows with key splits exceed %d arrival counters; use splits 1", what, rows,
-                kCounterSlots);
   const size_t need = xt_sparse_mla_workspace_bytes(rows, heads, splits);
   if (workspace_bytes < need)
     return fail(XT_EWORKSPACE, "%s: workspace %zu bytes < %zu needed", what, workspace_bytes, need);
@@ -511,7 +482,6 @@ extern "C" int xt_sparse_mla_nvfp4(const void* q, int64_t q_row_stride, int64_t 
   if (lds_bytes > 160 * 1024 - 256)
     return fail(XT_EUNSUPPORTED, "%s: %d keys per split need %zu bytes of LDS; use more splits", what,
                 a.keys_per_split, lds_bytes);
-  a.counters = static_cast<int32_t*>(workspace);
   a.part = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + kCounterBytes);
   a.ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes + (size_t)rows * splits * heads * kDl * 2);
   const int64_t n_units = (int64_t)rows * splits;
@@ -534,5 +504,10 @@ extern "C" int xt_sparse_mla_nvfp4(const void* q, int64_t q_row_stride, int64_t 
   else
     hipLaunchKernelGGL(mla_kernel<false>, dim3((unsigned)n_units), dim3(64 * kMWaves), lds_bytes,
                        reinterpret_cast<hipStream_t>(stream), a);
+  if (splits > 1) {
+    const int64_t threads = (int64_t)rows * heads * 64;
+    hipLaunchKernelGGL(mla_merge_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), a, rows);
+  }
   return check_launch(what);
 }
