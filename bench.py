@@ -329,6 +329,63 @@ def run_block(args, w, ops, workloads):
     print(json.dumps(record), flush=True)
 
 
+def run_varlen(args, w, ops, workloads):
+    """Split-K decode over packed BF16 rows, rotating `layers` distinct K/V buffers. One JSON line: GB/s of K/V rows
+    read against the HBM peak."""
+    import torch
+    torch.cuda.set_device(0)
+    gen = workloads.generator('cuda', 20261105)
+    layers = max(1, min(args.layers, 16))
+    n = w.rows * w.keys
+    kv = [(workloads.kv_tensor(n, w.kv_heads, w.dim, gen, 'cuda'), workloads.kv_tensor(n, w.kv_heads, w.dim, gen, 'cuda'))
+          for _ in range(layers)]
+    q = torch.randn(w.rows, w.q_heads, w.dim, generator=gen, device='cuda').to(torch.bfloat16)
+    cu_q = torch.arange(w.rows + 1, dtype=torch.int32, device='cuda')
+    cu_k = cu_q * w.keys
+    splits = args.splits or ops.default_splits(w.rows, w.kv_heads, w.keys)
+    ws = torch.zeros(ops.varlen_workspace_bytes(w.rows, w.q_heads, w.dim, splits), dtype=torch.uint8, device='cuda')
+    out = torch.empty_like(q)
+    scale = w.dim ** -0.5
+
+    def step(layer):
+        ops.varlen_decode(q, kv[layer][0], kv[layer][1], cu_q, cu_k, 1, w.keys, scale, out=out, splits=splits, ws=ws)
+
+    for i in range(max(1, args.warmup)):
+        step(i % layers)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for layer in range(layers):
+            step(layer)
+    graph.replay()
+    torch.cuda.synchronize()
+    replays = max(1, math.ceil(args.steps / layers))
+    steps = replays * layers
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
+    log(f'{w.name}: {ms * 1e3:.2f} us per layer-step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of {HBM_PEAK_GBS:.0f}), '
+        f'splits {splits}')
+    record = {
+        'metric': 'BF16 varlen split-K decode HBM GB/s', 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1,
+        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'higher_is_better': True,
+        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic',
+        'config': {'workload': w.name, 'rows': w.rows, 'q_heads': w.q_heads, 'kv_heads': w.kv_heads,
+                   'head_dim': w.dim, 'keys_per_row': w.keys, 'kv_format': 'bf16 packed rows',
+                   'layers_rotated': layers, 'splits': splits},
+        'us_per_layer_step': round(ms * 1e3, 3),
+        'roofline': {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+                     'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None},
+        'cpu_baseline': None,
+    }
+    print(json.dumps(record), flush=True)
+
+
 def main():
     p = argparse.ArgumentParser()
     p.add_argument('--gpus', type=int, default=1)
@@ -336,7 +393,7 @@ def main():
     p.add_argument('--warmup', type=int, default=64)
     p.add_argument('--workload', default='gqa_decode_b32',
                    help='gqa_decode_b32 (default), cpu_ref_decode, long_ctx_decode_b4, gqa_prefill_chunk4096, '
-                        'minimax_decode_b32, mla_decode_b64 or mla_prefill_2048')
+                        'minimax_decode_b32, qsa_varlen_b32, mla_decode_b64 or mla_prefill_2048')
     p.add_argument('--layers', type=int, default=16)
     p.add_argument('--splits', type=int, default=None)
     p.add_argument('--layout', default='interleaved', choices=['interleaved', 'split'],
@@ -366,6 +423,8 @@ def main():
     from xtier_amd import ops, workloads
     from xtier_amd.pool import KVPool
 
+    if args.workload in workloads.VARLEN_WORKLOADS:
+        return run_varlen(args, workloads.VARLEN_WORKLOADS[args.workload], ops, workloads)
     if args.workload in workloads.BLOCK_WORKLOADS:
         return run_block(args, workloads.BLOCK_WORKLOADS[args.workload], ops, workloads)
     if args.workload in workloads.MLA_WORKLOADS:

@@ -126,8 +126,8 @@ int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_s
  * xtier/packs/minimax_m3/kv_fp4.py:119-153, fp4_sparse_decode, behind the hook _decode_main :579-590).
  * Pool: page p, KV head h, row t (t < block_size) holds payload at k_pay + p * page_stride + h * head_stride +
  * t * row_stride (dim/2 bytes) and E4M3 scales at k_scales + p * sf_page_stride + h * sf_head_stride + t *
- * sf_row_stride (dim/16 bytes), V alike; the buffers hold `pages` pages. No global scale: *kv_scale (device FP32)
- * multiplies the scores and the output. Row b (q [rows, q_heads, dim] BF16) reads request slot_ids[b] (int64): its
+ * sf_row_stride (dim/16 bytes), V alike; the buffers hold `pages` pages. No global scale: kv_scale multiplies the
+ * scores and the output. Row b (q [rows, q_heads, dim] BF16) reads request slot_ids[b] (int64): its
  * length L = min(seq_lens[b], max_kv_len); KV head h's block ids topk_idx[h * idx_head_stride + b * idx_row_stride +
  * i] (int32, i < topk_blocks, -1: none) name positions c = id * block_size .. c + block_size - 1 below L, stored at
  * page s / block_size, rows s % block_size + n for s = req_to_token[slot_ids[b] * req_stride + c] (blocks start on a
@@ -139,7 +139,7 @@ int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_s
  * KV head, so the arrival counters need rows * kv_heads <= 16384 when splits > 1). */
 int xt_block_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, const uint8_t* k_pay,
                                  const uint8_t* v_pay, const uint8_t* k_scales, const uint8_t* v_scales,
-                                 const float* kv_scale, int64_t pages, int kv_heads, int q_heads, int dim,
+                                 float kv_scale, int64_t pages, int kv_heads, int q_heads, int dim,
                                  int block_size, int64_t page_stride, int64_t head_stride, int64_t row_stride,
                                  int64_t sf_page_stride, int64_t sf_head_stride, int64_t sf_row_stride,
                                  const int32_t* req_to_token, int64_t req_stride, int max_kv_len,

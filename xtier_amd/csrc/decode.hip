@@ -51,8 +51,9 @@ struct DecodeArgs {
   const uint8_t* v_pay;
   const uint8_t* k_sf;
   const uint8_t* v_sf;
-  const float* gk;
+  const float* gk;                   // device global scales; NULL: gk_val / gv_val
   const float* gv;
+  float gk_val, gv_val;
   int64_t pool_slots;                // slots addressable as slot * stride (after the page-row remap below)
   int64_t pay_stride, sf_stride;     // bytes from one slot to the next in the payload / scale buffers
   int64_t pay_head_stride, sf_head_stride;   // bytes from one KV head to the next within a slot's row
@@ -397,7 +398,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
     Step buf[P];
 #pragma unroll
     for (int p = 0; p < P; ++p) load_step(w, p, buf[p]);
-    const float gk = *a.gk;
+    const float gk = a.gk ? *a.gk : a.gk_val;
     int s0 = 0;
     for (; s0 + P < slice_steps; s0 += P) {
 #pragma unroll
@@ -442,7 +443,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   const int head = kvh * a.group + hl;
   if (a.splits == 1) {   // no partials: normalize and write
     if (slice != 0 || !head_live) return;
-    const float gv = *a.gv;
+    const float gv = a.gv ? *a.gv : a.gv_val;
     const float inv = l_tot > 0.0f ? gv / l_tot : 0.0f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -481,7 +482,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   // 512 threads, 8 consecutive outputs each: head h0 + o / 128, d0 = o % 128; loads of 8 splits at a time together
   const int h0 = kvg * HPW * a.group;
   const int nh = min(HPW * a.group, a.q_heads - h0);
-  const float gv = *a.gv;
+  const float gv = a.gv ? *a.gv : a.gv_val;
   for (int o = threadIdx.x * 8; o < nh * kDim; o += blockDim.x * 8) {
     const int hh = h0 + o / kDim, d0 = o % kDim;
     const float* base = row_part + (int64_t)hh * kPartStride;
@@ -547,6 +548,8 @@ struct Addressing {
   int64_t idx_head_stride;                   // per-KV-head index lists (0: shared; forces 1 KV head per workgroup)
   int block_shift;                           // an index entry names 2^block_shift positions
   int max_len;                               // sequence lengths clamped to this
+  bool scalar_scales;                        // gk / gv NULL: the scores and outputs use gk_val / gv_val
+  float gk_val, gv_val;
 };
 
 static int decode_impl(const char* what, const void* q, int64_t q_row_stride, int64_t q_head_stride,
@@ -587,7 +590,7 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
                 (long long)pay_stride, (long long)sf_stride);
   if (pool_slots <= 0 || pool_slots > 0x7FFFFFFFLL)
     return fail(XT_EINVAL, "%s: pool_slots %lld outside 1..2^31-1", what, (long long)pool_slots);
-  const Addressing ad{dim / 2, dim / 16, 0, 1, 0, 0, 0x7FFFFFFF};
+  const Addressing ad{dim / 2, dim / 16, 0, 1, 0, 0, 0x7FFFFFFF, false, 0.0f, 0.0f};
   return decode_impl(what, q, q_row_stride, q_head_stride, k_pay, v_pay, k_scales, v_scales, gk, gv, pool_slots,
                      pay_stride, sf_stride, kv_heads, q_heads, table, table_stride, page_size, row_req, indices,
                      idx_stride, topk, counts, seq_lens, query_pos, scale, out, out_row_stride, out_head_stride,
@@ -596,7 +599,7 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
 
 extern "C" int xt_block_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride,
                                             const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_scales,
-                                            const uint8_t* v_scales, const float* kv_scale, int64_t pages,
+                                            const uint8_t* v_scales, float kv_scale, int64_t pages,
                                             int kv_heads, int q_heads, int dim, int block_size, int64_t page_stride,
                                             int64_t head_stride, int64_t row_stride, int64_t sf_page_stride,
                                             int64_t sf_head_stride, int64_t sf_row_stride,
@@ -629,8 +632,9 @@ extern "C" int xt_block_sparse_decode_nvfp4(const void* q, int64_t q_row_stride,
     return fail(XT_EUNSUPPORTED, "%s: %d blocks of %d keys", what, topk_blocks, block_size);
   if (!slot_ids) return fail(XT_EINVAL, "%s: slot_ids is null", what);
   const int shift = __builtin_ctz((unsigned)block_size);
-  const Addressing ad{head_stride, sf_head_stride, shift, mul, idx_head_stride, shift, max_kv_len};
-  return decode_impl(what, q, q_row_stride, q_head_stride, k_pay, v_pay, k_scales, v_scales, kv_scale, kv_scale,
+  const Addressing ad{head_stride, sf_head_stride, shift, mul, idx_head_stride, shift, max_kv_len, true, kv_scale,
+                      kv_scale};
+  return decode_impl(what, q, q_row_stride, q_head_stride, k_pay, v_pay, k_scales, v_scales, nullptr, nullptr,
                      pages * mul, row_stride, sf_row_stride, kv_heads, q_heads, req_to_token, req_stride, 1,
                      slot_ids, topk_idx, idx_row_stride, topk_blocks * block_size, nullptr, seq_lens, nullptr,
                      sm_scale, out, out_row_stride, out_head_stride, out_dtype, lse, rows, splits, workspace,
@@ -656,7 +660,8 @@ static int decode_impl(const char* what, const void* q, int64_t q_row_stride, in
   if (out_dtype != XT_DTYPE_BF16 && out_dtype != XT_DTYPE_F16)
     return fail(XT_EINVAL, "%s: output dtype must be BF16 or FP16", what);
   if (rows == 0) return ok();
-  if (!q || !k_pay || !v_pay || !k_scales || !v_scales || !gk || !gv || !table || !indices || !seq_lens || !out ||
+  if (!q || !k_pay || !v_pay || !k_scales || !v_scales || ((!gk || !gv) && !ad.scalar_scales) || !table || !indices ||
+      !seq_lens || !out ||
       !workspace)
     return fail(XT_EINVAL, "%s: a required pointer is null", what);
   if (!aligned(q, 16) || q_row_stride % 8 || q_head_stride % 8 || !aligned(out, 16) || out_row_stride % 8 ||
@@ -694,8 +699,10 @@ static int decode_impl(const char* what, const void* q, int64_t q_row_stride, in
   a.v_pay = v_pay;
   a.k_sf = k_scales;
   a.v_sf = v_scales;
-  a.gk = gk;
-  a.gv = gv;
+  a.gk = ad.scalar_scales ? nullptr : gk;
+  a.gv = ad.scalar_scales ? nullptr : gv;
+  a.gk_val = ad.gk_val;
+  a.gv_val = ad.gv_val;
   a.pool_slots = pool_slots;
   a.pay_stride = pay_stride;
   a.sf_stride = sf_stride;

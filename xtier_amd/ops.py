@@ -267,13 +267,12 @@ def fp4_sparse_decode(q, k_pay, k_sc, v_pay, v_sc, req_to_token, slot_ids, topk_
         topk_idx = topk_idx.to(torch.int32).contiguous()
     slot_ids = slot_ids if slot_ids.dtype == torch.int64 else slot_ids.to(torch.int64)
     seq_lens = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
-    scale_dev = torch.full((1,), float(kv_scale), dtype=torch.float32, device=q.device)
     topk = topk_idx.shape[2]
     if splits is None:
         splits = _capture_splits(q.device, b, qh, d, default_splits(b, kh, topk * block_size), ws)
     ws = _decode_ws(q.device, b, qh, d, splits, ws)
     _lib.check(_lib.lib().xt_block_sparse_decode_nvfp4(
-        _ptr(q), q.stride(0), q.stride(1), _ptr(k_pay), _ptr(v_pay), _ptr(k_sc), _ptr(v_sc), _ptr(scale_dev),
+        _ptr(q), q.stride(0), q.stride(1), _ptr(k_pay), _ptr(v_pay), _ptr(k_sc), _ptr(v_sc), float(kv_scale),
         k_pay.shape[0], kh, qh, d, int(block_size), k_pay.stride(0), k_pay.stride(1), k_pay.stride(2),
         k_sc.stride(0), k_sc.stride(1), k_sc.stride(2), _ptr(req_to_token), req_to_token.stride(0),
         req_to_token.shape[1], _ptr(slot_ids), _ptr(topk_idx), topk_idx.stride(0), topk_idx.stride(1), topk,

@@ -166,6 +166,30 @@ BLOCK_WORKLOADS = {
 }
 
 
+@dataclass(frozen=True)
+class VarlenWorkload:
+    """Decode over packed BF16 rows (the gathered top-k rows of every request, one query per row)."""
+    name: str
+    rows: int
+    q_heads: int
+    kv_heads: int
+    dim: int
+    keys: int
+
+    def algorithmic_bytes(self):
+        """K and V rows read: rows * keys * kv_heads * 2 * dim * 2 bytes."""
+        return self.rows * self.keys * self.kv_heads * 2 * self.dim * 2
+
+    def flops(self):
+        return self.rows * self.q_heads * self.keys * 4 * self.dim
+
+
+VARLEN_WORKLOADS = {
+    # 32 rows, 32 q / 4 KV heads, d 128, 2048 packed keys per row (the gathered top-2048 of the decode workload)
+    'qsa_varlen_b32': VarlenWorkload('qsa_varlen_b32', 32, 32, 4, 128, 2048),
+}
+
+
 def generator(device, seed):
     g = torch.Generator(device=device)
     g.manual_seed(seed)
