@@ -194,6 +194,30 @@ def test_decode_full_gqa_workload(splits):
     _check(out, ref, flash, strict=True)
 
 
+def test_decode_long_context_workload():
+    """Batch 4 at context 524288 (a 2M-slot pool, 1.2 GB of NVFP4 K/V, far beyond the MALL), top-2048 with half the
+    keys in the last 4096 positions, the default key splits: every row against the oracle."""
+    w = workloads.WORKLOADS['long_ctx_decode_b4']
+    gen = workloads.generator('cuda', 20261106)
+    k = workloads.kv_tensor(w.slots, w.kv_heads, w.dim, gen, 'cuda')
+    k_pay, k_sf, gk = ops.nvfp4_encode(k)
+    del k
+    v = workloads.kv_tensor(w.slots, w.kv_heads, w.dim, gen, 'cuda')
+    v_pay, v_sf, gv = ops.nvfp4_encode(v)
+    del v
+    raw = (k_pay, v_pay, k_sf, v_sf, gk, gv)
+    q = torch.randn(w.batch, w.q_heads, w.dim, generator=gen, device='cuda').to(torch.bfloat16)
+    pt = workloads.page_table(w.batch, w.ctx, w.page, gen, 'cuda')
+    idx = workloads.index_lists(w.batch, w.ctx, w.topk, gen, 'cuda', w.index_mode)
+    seq = torch.full((w.batch,), w.ctx, dtype=torch.int32, device='cuda')
+    scale = 1 / math.sqrt(w.dim)
+    assert ops.default_splits(w.batch, w.kv_heads, w.topk) == 8
+    out = ops.sparse_decode(q, raw, pt, idx, seq, scale, page_size=w.page)
+    ref, flash, _ = _oracle(raw, bf16_numpy(q), pt.cpu().numpy(), w.page, np.arange(w.batch), idx.cpu().numpy(),
+                            None, seq.cpu().numpy(), scale)
+    _check(out, ref, flash, strict=True)
+
+
 def test_interleaved_pool_equals_split_pool():
     """The same bytes in the interleaved layout (one buffer, per slot [K pay | K sf | V pay | V sf]) and in SGLang's
     four buffers give the same bits."""
