@@ -33,8 +33,9 @@ constexpr int kMSteps = 32;              // keys per step
 constexpr int kMWaves = 8;
 constexpr int kMHeads = 16 * kMWaves;    // heads per workgroup
 constexpr int kKRow = kDk + 8;           // halves per K tile row (16-byte pad)
-constexpr int kVRow = kMSteps + 4;       // halves per V^T tile row (72 bytes: the PV reads and the dequant writes of
-                                         // a wave fall on distinct LDS banks)
+constexpr int kVRow = kMSteps + 16;      // halves per V^T tile row (96 bytes); keys stored in the order of the PV
+                                         // operand, position 8j + 4b + s holding key 16b + 4j + s, so a lane's eight
+                                         // keys are one 16-byte read (at this pitch without LDS bank conflicts)
 constexpr int kKTile = kMSteps * kKRow * 2;
 constexpr int kVTile = kDl * kVRow * 2;
 constexpr int kQChunks = kDk / 32;       // 32-dim chunks of a query row
@@ -135,7 +136,7 @@ __device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step,
   }
 #pragma unroll
   for (int d = 0; d < 8; ++d)
-    *reinterpret_cast<half4_t*>(vt + (8 * c + d) * kVRow + 4 * kq) =
+    *reinterpret_cast<half4_t*>(vt + (8 * c + d) * kVRow + 8 * (kq & 3) + 4 * (kq >> 2)) =
         half4_t{vals[0][d], vals[1][d], vals[2][d], vals[3][d]};
   if (t < 256) {
     const int key = t >> 3, p = t & 7;
@@ -298,13 +299,9 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
     }
     l += psum;
     // O^T += V^T . P^T over the 32 dim tiles
-    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int dt = 0; dt < 32; ++dt) {
-      const _Float16* vr = vt + (16 * dt + hl) * kVRow + 4 * j;
-      const half4_t lo = *reinterpret_cast<const half4_t*>(vr);
-      const half4_t hi = *reinterpret_cast<const half4_t*>(vr + 16);
-      const half8_t av = half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      const half8_t av = *reinterpret_cast<const half8_t*>(vt + (16 * dt + hl) * kVRow + 8 * j);
       acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb, acc[dt], 0, 0, 0);
     }
     __syncthreads();
