@@ -217,6 +217,31 @@ int xt_sparse_mla_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stri
                         void* out, int64_t out_row_stride, int64_t out_head_stride, int out_dtype, float* lse, int rows,
                         int splits, void* workspace, size_t workspace_bytes, xt_stream_t stream);
 
+/* DeepSeek V4 FP8 KV pages (the layout of xtier/packs/deepseek_v4/sparse_mla.py:38-59, 156-160): page p holds
+ * page_size token data rows of 576 bytes (448 E4M3 latent values, then 64 BF16 rope values) followed by page_size
+ * scale rows of 8 bytes (7 UE8M0 exponents, one per 64 latent values, value 2^(e - 127); 1 byte of padding); the
+ * next page starts page_stride bytes later. Token t is row t % page_size of page t / page_size. */
+typedef struct {
+  const uint8_t* pages;
+  int64_t num_pages;
+  int page_size;          /* a power of 2 */
+  int64_t page_stride;    /* bytes, >= page_size * 584, a multiple of 16 */
+} xt_mla_fp8_cache;
+
+/* Device workspace of xt_sparse_mla_fp8 (FP32 split partials). */
+size_t xt_sparse_mla_fp8_workspace_bytes(int rows, int heads, int splits);
+
+/* Sparse MLA on DeepSeek V4 FP8 pages (replaces sparse_mla / _attend / _merge of sparse_mla.py:88-217 and the hook
+ * flash_mla_with_kvcache :220-231 on that layout). As xt_sparse_mla_nvfp4, with key = value = [e4m3 * 2^(e - 127)
+ * (448), rope (64)], 512 wide, and q BF16 [rows, heads, 512]: scores are q . key on BF16 operands with FP32
+ * accumulation, times scale; P is rounded to BF16 for the value product; splits merge in FP32. A scale byte of 0
+ * (2^-127) reads as 0. */
+int xt_sparse_mla_fp8(const void* q, int64_t q_row_stride, int64_t q_head_stride, int heads,
+                      const xt_mla_fp8_cache* cache, const xt_mla_keys* keys, const xt_mla_fp8_cache* extra_cache,
+                      const xt_mla_keys* extra_keys, const float* sink, float scale, void* out, int64_t out_row_stride,
+                      int64_t out_head_stride, int out_dtype, float* lse, int rows, int splits, void* workspace,
+                      size_t workspace_bytes, xt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

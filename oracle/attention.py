@@ -299,3 +299,61 @@ def sparse_mla(q, latent_pay, latent_sf, rope, g, indices, topk_length, sink, sc
             total = total + np.exp(np.asarray(sink, dtype=dtype) - m)
         out[r] = (p.T @ lat) / total[:, None]
     return out, lse
+
+
+# --- sparse MLA on DeepSeek V4 FP8 pages ----------------------------------------------------------------------------
+
+V4_NOPE, V4_ROW = 448, 576
+
+
+def v4_keys(pages, page_size, page_stride, tokens=None):
+    """Keys of DeepSeek V4 FP8 pages (sparse_mla.py:38-59): token t = row t % page_size of page t // page_size;
+    key[:448] = e4m3(byte) * 2^(e - 127) with e the UE8M0 byte of its 64-value group (e = 0 as 2^-127, the bit pattern
+    0x00400000 of :52), key[448:] = the 64 BF16 rope values. pages: uint8, page p at byte p * page_stride. Returns
+    float64 [tokens, 512]."""
+    flat = np.asarray(pages, dtype=np.uint8).reshape(-1)
+    n_pages = flat.size // page_stride if tokens is None else -(-tokens // page_size)
+    tokens = n_pages * page_size if tokens is None else tokens
+    t = np.arange(tokens)
+    base = (t // page_size) * page_stride
+    row = t % page_size
+    data = flat[(base + row * V4_ROW)[:, None] + np.arange(V4_ROW)[None, :]]
+    exps = flat[(base + page_size * V4_ROW + row * 8)[:, None] + np.arange(7)[None, :]].astype(np.int64)
+    scale = np.where(exps == 0, 2.0 ** -127, np.exp2(exps.astype(np.float64) - 127))
+    nope = nvfp4.e4m3_decode(data[:, :V4_NOPE]).astype(np.float64) * np.repeat(scale, 64, axis=1)
+    rope = nvfp4.bf16_to_f32(data[:, V4_NOPE:].copy().view(np.uint16)).astype(np.float64)
+    return np.concatenate([nope, rope], 1)
+
+
+def sparse_mla_v4(q, keys1, indices1, length1, sink, scale, keys2=None, indices2=None, length2=None):
+    """Sparse MLA on V4 keys (value = key, 512 wide) in FP64, the reference of tests/ds_sparse_mla_check.py:44-67:
+    row r attends to the valid entries of indices1[r] (>= 0 and column < length1[r]) in keys1 followed by those of
+    indices2[r] in keys2; sink [H] or None enters the denominator as exp(sink - m). Returns (out [R, H, 512], lse
+    [R, H] natural log of the keys' sum, -inf for a row without keys)."""
+    q = np.asarray(q, dtype=np.float64)
+    rows_n, heads, dim = q.shape
+    out = np.zeros((rows_n, heads, dim))
+    lse = np.full((rows_n, heads), -np.inf)
+    for r in range(rows_n):
+        ks = []
+        for keys, idx_all, lengths in ((keys1, indices1, length1), (keys2, indices2, length2)):
+            if keys is None:
+                continue
+            idx = np.asarray(idx_all[r], dtype=np.int64)
+            valid = (idx >= 0) & (idx < keys.shape[0])
+            if lengths is not None:
+                valid &= np.arange(idx.shape[0]) < int(lengths[r])
+            if valid.any():
+                ks.append(keys[idx[valid]])
+        if not ks:
+            continue
+        k = np.concatenate(ks, 0)
+        s = (k @ q[r].T) * scale
+        m = s.max(0)
+        p = np.exp(s - m[None])
+        total = p.sum(0)
+        lse[r] = m + np.log(total)
+        if sink is not None:
+            total = total + np.exp(np.asarray(sink, dtype=np.float64) - m)
+        out[r] = (p.T @ k) / total[:, None]
+    return out, lse

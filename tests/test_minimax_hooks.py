@@ -42,3 +42,18 @@ def test_attach_scales_and_install():
     registry = SimpleNamespace(register=lambda name, fn, kind: seen.append((name, fn, kind)))
     minimax.install(registry, SimpleNamespace(AROUND='around'))
     assert seen == [(f'{minimax.OPS}.flash_decode_with_gqa_share_sparse', minimax.decode_main, 'around')]
+
+
+def test_deepseek_hook_falls_through_and_installs():
+    from xtier_amd import deepseek
+    seen = []
+    original = lambda *a, **k: ('original', a, k)
+    assert deepseek.flash_mla_with_kvcache(original, 1, k_cache=None)[0] == 'original'          # positional call
+    cache = torch.zeros(2, 64, 1, 584, dtype=torch.uint8)
+    assert deepseek.flash_mla_with_kvcache(original, k_cache=cache, indices=None, is_fp8_kvcache=True)[0] == 'original'
+    assert deepseek.flash_mla_with_kvcache(original, k_cache=torch.zeros(2, 64, 1, 656, dtype=torch.uint8),
+                                           indices=torch.zeros(1), is_fp8_kvcache=True)[0] == 'original'
+    assert deepseek.no_sparse_prefill(original, None) is False
+    registry = SimpleNamespace(register=lambda name, fn, kind: seen.append((name, fn, kind)))
+    deepseek.install(registry, SimpleNamespace(AROUND='around'))
+    assert [s[1] for s in seen] == [deepseek.flash_mla_with_kvcache, deepseek.no_sparse_prefill]

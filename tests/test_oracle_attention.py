@@ -268,3 +268,43 @@ def test_varlen_split_form_equals_one_pass_softmax():
         want = attention.softmax_attention(q[cu_q[r]], k[a:a + n], v[a:a + n], np.ones(n, bool), 0.3)
         np.testing.assert_allclose(got[r], want, rtol=1e-12, atol=1e-12)
     assert np.all(got[1] == 0)
+
+
+def test_v4_keys_decode_the_packed_pages():
+    """The oracle's V4 page decoding (sparse_mla.py:38-59) equals the exact keys the packing rule produced, through
+    torch's float8_e4m3fn values: pages of 64 and 128 tokens, padded page strides."""
+    from tests._v4 import pack_v4
+    g = torch.Generator().manual_seed(3)
+    lat = torch.randn(256, 512, generator=g) * torch.rand(256, 1, generator=g) * 4
+    for ps in (64, 128):
+        view, keys, stride = pack_v4(lat, ps)
+        got = attention.v4_keys(view.as_strided((view.shape[0] * stride,), (1,)).numpy(), ps, stride)
+        np.testing.assert_array_equal(got, keys)
+
+
+def test_sparse_mla_v4_matches_torch_with_sink_and_two_lists():
+    """Sparse MLA on V4 keys (value = key): torch float64 softmax with the sink in the denominator; two lists equal
+    one list over the concatenated keys; a row without keys is 0 with LSE -inf."""
+    rng = np.random.default_rng(4)
+    k1, k2 = rng.standard_normal((50, 512)), rng.standard_normal((30, 512))
+    q = rng.standard_normal((3, 4, 512)) * 0.1
+    i1 = rng.integers(-1, 50, (3, 20)).astype(np.int32)
+    i2 = rng.integers(-1, 30, (3, 10)).astype(np.int32)
+    l1 = np.array([20, 5, 0], np.int32)
+    l2 = np.array([10, 10, 0], np.int32)
+    sink = rng.standard_normal(4)
+    out, lse = attention.sparse_mla_v4(q, k1, i1, l1, sink, 0.05, k2, i2, l2)
+    cat = np.concatenate([k1, k2])
+    ic = np.concatenate([np.where((i1 >= 0) & (np.arange(20) < l1[:, None]), i1, -1),
+                         np.where((i2 >= 0) & (np.arange(10) < l2[:, None]), i2 + 50, -1)], 1)
+    out2, lse2 = attention.sparse_mla_v4(q, cat, ic, None, sink, 0.05)
+    np.testing.assert_allclose(out, out2, rtol=1e-12, atol=1e-14)
+    for r in range(2):
+        sel = ic[r][ic[r] >= 0]
+        kd = torch.from_numpy(cat[sel])
+        s = torch.from_numpy(q[r]) @ kd.T * 0.05
+        m = s.max(1, keepdim=True).values
+        p = torch.exp(s - m)
+        o = (p @ kd) / (p.sum(1, keepdim=True) + torch.exp(torch.from_numpy(sink)[:, None] - m))
+        np.testing.assert_allclose(out[r], o.numpy(), rtol=1e-10, atol=1e-12)
+    assert np.all(out[2] == 0) and np.all(np.isneginf(lse[2]))

@@ -33,7 +33,12 @@ class MlaKeys(ctypes.Structure):
     _fields_ = [('indices', _P), ('stride', _L), ('topk', _I), ('lengths', _P)]
 
 
-_CP, _KP = ctypes.POINTER(MlaCache), ctypes.POINTER(MlaKeys)
+class MlaFp8Cache(ctypes.Structure):
+    """xt_mla_fp8_cache: DeepSeek V4 FP8 pages (page stride in bytes)."""
+    _fields_ = [('pages', _P), ('num_pages', _L), ('page_size', _I), ('page_stride', _L)]
+
+
+_CP, _KP, _FP = ctypes.POINTER(MlaCache), ctypes.POINTER(MlaKeys), ctypes.POINTER(MlaFp8Cache)
 
 SIGNATURES = {
     'xt_version': (_I, []),
@@ -53,6 +58,8 @@ SIGNATURES = {
     'xt_varlen_decode_bf16': (_I, [_P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _P, _I, _I, _I, _I, _I, _F, _P, _L, _L, _I,
                                    _I, _P, _Z, _P]),
     'xt_sparse_mla_workspace_bytes': (_Z, [_I, _I, _I]),
+    'xt_sparse_mla_fp8_workspace_bytes': (_Z, [_I, _I, _I]),
+    'xt_sparse_mla_fp8': (_I, [_P, _L, _L, _I, _FP, _KP, _FP, _KP, _P, _F, _P, _L, _L, _I, _P, _I, _I, _P, _Z, _P]),
     'xt_sparse_mla_nvfp4': (_I, [_P, _L, _L, _I, _I, _I, _CP, _KP, _CP, _KP, _P, _F, _P, _L, _L, _I, _P, _I, _I, _P,
                                  _Z, _P]),
 }

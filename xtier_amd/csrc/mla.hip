@@ -1,16 +1,20 @@
-// Sparse MLA over an NVFP4 latent cache: 128 query heads share one key per token, [latent (512, NVFP4) | rope (64,
-// BF16)] = 576 wide, whose value is the latent. q.k and p.v on MFMA (v_mfma_f32_16x16x32_f16), online softmax in the
-// exp2 domain, an optional per-head sink in the denominator. With key splits, each (row, split) writes its output
-// normalized by its own sum (FP16) with its max and sum, and a second, wide launch merges the splits: one merging
-// workgroup per row would read a row's partials at one CU's bandwidth.
+// Sparse MLA: 128 query heads share one key per token. Two cache formats:
+//   NVFP4 latent (kNvfp4): key = [latent (512, NVFP4 with E4M3 block scales and a global scale) | rope (64, BF16)],
+//     576 wide, value = the latent; operands FP16, q pre-scaled by scale * log2(e);
+//   DeepSeek V4 FP8 pages (kFp8V4, sparse_mla.py:38-59): key = [448 E4M3 values x UE8M0 scale per 64 | 64 BF16 rope],
+//     512 wide, value = the key; operands BF16 as in the reference, the scale applied to the FP32 scores.
+// q.k and p.v on MFMA (v_mfma_f32_16x16x32_f16 / _bf16), online softmax in the exp2 domain, an optional per-head sink
+// in the denominator. With key splits, each (row, split) writes its output normalized by its own sum (FP16 for the
+// NVFP4 latent, whose values are FP16; FP32 for V4) with its max and sum, and a second, wide launch merges the splits:
+// one merging workgroup per row would read a row's partials at one CU's bandwidth.
 //
 // Work decomposition: a workgroup = 8 wavefronts x 16 heads = 128 heads of one (query row, key split), so every key is
 // read and dequantized once for all heads. Per step of 32 keys the workgroup
-//   1. turns the raw key records (loaded one step ahead into registers) into two LDS tiles: K [32 keys][576] FP16 and
-//      V^T [512][32 keys] FP16, the latent as FP16((e2m1 * e4m3) * g) and the rope widened from BF16;
-//   2. each wave computes S^T [32 keys x 16 heads] = K . Q^T (18 MFMAs per 16-key tile, Q^T resident in registers
-//      as FP16 of q * scale * log2(e)), the softmax, and O^T [512 x 16 heads] += V^T . P^T (32 MFMAs), P^T taken
-//      straight from the score registers (the key order T(j) below matches the V^T operand).
+//   1. turns the raw key records (loaded one step ahead into registers) into two LDS tiles: K [32 keys][Dk] and
+//      V^T [512][32 keys] (16-bit values);
+//   2. each wave computes S^T [32 keys x 16 heads] = K . Q^T (Dk/32 MFMAs per 16-key tile, Q^T mostly resident in
+//      registers), the softmax, and O^T [512 x 16 heads] += V^T . P^T (32 MFMAs), P^T taken straight from the score
+//      registers (the key order T(j) below matches the V^T operand).
 //
 // Lane layouts (16x16x32 MFMA, hl = lane % 16, j = lane / 16):
 //   QK: A = K tile, lane (key hl, dims 32kk + 8j .. +7); B = Q^T, lane (head hl, same dims); C = S^T, lane (head hl,
@@ -18,39 +22,52 @@
 //   PV: A = V^T, lane (dim hl of a 16-dim tile, keys T(j) = {4j..4j+3, 16+4j..16+4j+3}); B = P^T, lane (head hl, keys
 //       T(j)); C = O^T, lane (head hl, dims 4j .. 4j+3 of the tile).
 //
-// Numerics: FP16((e2m1 * e4m3) * g) rounds the dequantized latent once (11 significant bits); the rope is exact
-// in FP16 within its range. P is FP16 with the lazy rescale of the decode kernel (P <= 256); sums are FP32.
+// Numerics: NVFP4: FP16((e2m1 * e4m3) * g) rounds the dequantized latent once (11 significant bits); the rope is exact
+// in FP16 within its range; P is FP16. V4: e4m3 * 2^(e - 127) is exact in BF16 (4 significant bits) for scales from
+// 2^-126; a zero scale byte (2^-127) reads as 0; P is BF16. The running maximum is raised lazily (P <= 256); sums are
+// FP32.
 #include "xt_common.h"
 #include "xt_host.h"
 
 namespace xt {
 namespace {
 
-constexpr int kDl = 512;                 // latent width (NVFP4): 256 payload bytes, 32 scale bytes per token
+enum { kNvfp4 = 0, kFp8V4 = 1 };
+constexpr int kDl = 512;                 // value width; NVFP4 latent: 256 payload bytes, 32 scale bytes per token
 constexpr int kDr = 64;                  // rope width (BF16): 128 bytes per token
-constexpr int kDk = kDl + kDr;           // key width
+constexpr int kV4Nope = 448;             // V4: E4M3 values per token, one UE8M0 scale per 64
+constexpr int kV4Row = 576;              // V4: bytes of a token's data row (448 + 128)
+template <int F>
+constexpr int kDk = F == kNvfp4 ? kDl + kDr : kDl;   // key width
 constexpr int kMSteps = 32;              // keys per step
 constexpr int kMWaves = 8;
 constexpr int kMHeads = 16 * kMWaves;    // heads per workgroup
-constexpr int kKRow = kDk + 8;           // halves per K tile row (16-byte pad)
+template <int F>
+constexpr int kKRow = kDk<F> + 8;        // 16-bit values per K tile row (16-byte pad)
 constexpr int kVRow = kMSteps + 16;      // halves per V^T tile row (96 bytes); keys stored in the order of the PV
                                          // operand, position 8j + 4b + s holding key 16b + 4j + s, so a lane's eight
                                          // keys are one 16-byte read (at this pitch without LDS bank conflicts)
-constexpr int kKTile = kMSteps * kKRow * 2;
+template <int F>
+constexpr int kKTile = kMSteps * kKRow<F> * 2;
 constexpr int kVTile = kDl * kVRow * 2;
-constexpr int kQChunks = kDk / 32;       // 32-dim chunks of a query row
-constexpr int kQReg = 12;                // chunks kept in registers; the others (4 latent + 2 rope) live in LDS
+template <int F>
+constexpr int kQChunks = kDk<F> / 32;    // 32-dim chunks of a query row
+template <int F>
+constexpr int kQReg = F == kNvfp4 ? 12 : 10;   // chunks kept in registers; the others live in LDS
 constexpr int kQRow = 32 + 8;            // halves per (chunk, head) row of the LDS query block
-constexpr int kQTile = (kQChunks - kQReg) * kMHeads * kQRow * 2;
+template <int F>
+constexpr int kQTile = (kQChunks<F> - kQReg<F>) * kMHeads * kQRow * 2;
 constexpr int kRescaleM = 8;
 
 struct CacheDev {
-  const uint8_t* pay;
+  const uint8_t* pay;                // NVFP4: latent payload; V4: the page buffer
   const uint8_t* sf;
   const uint16_t* rope;
   const float* g;
   int64_t slots;
-  uint32_t pay_stride, sf_stride, rope_stride;   // bytes from one slot to the next
+  uint32_t pay_stride, sf_stride, rope_stride;   // NVFP4: bytes from one slot to the next
+  uint32_t page_shift;               // V4: log2(tokens per page)
+  uint64_t page_bytes;               // V4: bytes from one page to the next (data rows, then 8-byte scale rows)
 };
 
 struct MlaArgs {
@@ -68,20 +85,45 @@ struct MlaArgs {
   int out_dtype;
   float* lse;
   int heads, splits, keys_per_split, steps;
-  uint16_t* part;                    // [rows, splits, heads, 512] FP16: the split's output normalized by its own sum
+  void* part;                        // [rows, splits, heads, 512] FP16 (NVFP4) / FP32 (V4): the split's output
+                                     // normalized by its own sum
   float* ml;                         // [rows, splits, heads, 2]: the split's running max (log2 domain) and sum
   uint32_t xcd_units, xcd_extra;
 };
+
+typedef short short8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// 16x16x32 MFMA on 16-bit operands of the format: FP16 (NVFP4 latent) or BF16 (V4)
+template <int F>
+__device__ inline float4_t mfma16(short8_t a, short8_t b, float4_t c) {
+  if constexpr (F == kNvfp4)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c,
+                                                  0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+}
 
 // Slot list entries: >= 0 a slot of cache 0, <= -2 slot (-e - 2) of cache 1, -1 no key.
 __device__ inline bool entry_valid(int32_t e) { return e != -1; }
 
 // Dequant mapping: thread t handles keys 4kq .. 4kq+3 (kq = t % 8) and latent dims 8c .. 8c+7 (c = t / 8), so a
 // wave's V^T writes spread over 8 key columns and 8 dim rows (no LDS bank conflicts); rope: key t / 8, part t % 8.
-struct Raw {
+// V4 (same mapping, all 512 dims): dims 8c .. 8c+7 are E4M3 bytes (c < 56) or BF16 rope values (c >= 56).
+template <int F>
+struct Raw;
+template <>
+struct Raw<kNvfp4> {
   uint32_t pay[4];   // payload bytes 4c .. 4c+3 of keys 4kq + i
   uint32_t sc[4];    // scale byte c / 2 of those keys
   uint4 rope;        // rope values 8p .. 8p+7 of key t / 8 (threads 0-255)
+};
+template <>
+struct Raw<kFp8V4> {
+  uint4 d[4];        // keys 4kq + i: E4M3 bytes 8c .. 8c+7 in (x, y), or rope values 8(c - 56) .. +7
+  uint32_t sc[4];    // UE8M0 scale byte c / 8 of those keys (c < 56)
 };
 
 // The record of slot list entry e: with one key list the entry is the slot (or -1: slot 0, ignored); with two the
@@ -96,9 +138,29 @@ __device__ inline const CacheDev& cache_of(const MlaArgs& a, int32_t e, uint32_t
   return a.c[e <= -2 ? 1 : 0];
 }
 
-template <bool TWO>
-__device__ inline void load_raw(const MlaArgs& a, const int32_t* slots, int step, Raw& r) {
+template <int F, bool TWO>
+__device__ inline void load_raw(const MlaArgs& a, const int32_t* slots, int step, Raw<F>& r) {
   const int t = threadIdx.x, kq = t & 7, c = t >> 3;
+  if constexpr (F == kFp8V4) {
+    // token s of a cache: page s >> page_shift, row s & (page size - 1); data row at row * 576, scale row after the
+    // page's data rows at row * 8. c < 56 is uniform per wave (waves 0-6 read E4M3 bytes, wave 7 the rope).
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t s;
+      const CacheDev& cd = cache_of<TWO>(a, slots[step * kMSteps + 4 * kq + i], s);
+      const uint32_t ps = 1u << cd.page_shift, rw = s & (ps - 1u);
+      const uint8_t* page = cd.pay + (uint64_t)(s >> cd.page_shift) * cd.page_bytes;
+      if (c < kV4Nope / 8) {
+        const uint2 v = *reinterpret_cast<const uint2*>(page + (uint64_t)rw * kV4Row + 8 * c);
+        r.d[i] = uint4{v.x, v.y, 0u, 0u};
+        r.sc[i] = page[(uint64_t)ps * kV4Row + (uint64_t)rw * 8 + (c >> 3)];
+      } else {
+        r.d[i] = *reinterpret_cast<const uint4*>(page + (uint64_t)rw * kV4Row + kV4Nope + 16 * (c - kV4Nope / 8));
+        r.sc[i] = 0u;
+      }
+    }
+    return;
+  } else {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     uint32_t s;
@@ -112,15 +174,45 @@ __device__ inline void load_raw(const MlaArgs& a, const int32_t* slots, int step
     r.rope = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(cd.rope) + (uint64_t)s * cd.rope_stride +
                                              16 * (t & 7));
   }
+  }
 }
 
-// Raw records -> K and V^T tiles. An invalid key's latent becomes 0 (so P * V stays finite whatever slot 0 holds);
-// its rope is left as read: its score is masked by a select, never multiplied.
-template <bool TWO>
-__device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step, const Raw& r, float g0, float g1,
-                               _Float16* kt, _Float16* vt) {
-  typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+// Raw records -> K and V^T tiles. An invalid key's value becomes 0 (so P * V stays finite whatever slot 0 holds);
+// an NVFP4 key's rope is left as read: its score is masked by a select, never multiplied.
+template <int F, bool TWO>
+__device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step, const Raw<F>& r, float g0, float g1,
+                               uint16_t* kt, uint16_t* vt) {
+  typedef short short4_t __attribute__((ext_vector_type(4)));
   const int t = threadIdx.x, kq = t & 7, c = t >> 3;
+  if constexpr (F == kFp8V4) {
+    short8_t vals[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = entry_valid(slots[step * kMSteps + 4 * kq + i]);
+      uint4 w;
+      if (c < kV4Nope / 8) {
+        // e4m3 * 2^(e - 127): the scaled conversion takes the scale's exponent, exact in BF16; e = 0 reads as 0
+        const float sc = __uint_as_float(r.sc[i] << 23);
+        const bf16x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.d[i].x, sc, false);
+        const bf16x2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.d[i].x, sc, true);
+        const bf16x2_t p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.d[i].y, sc, false);
+        const bf16x2_t p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.d[i].y, sc, true);
+        const bool live = ok && r.sc[i] != 0u;
+        w = uint4{live ? __builtin_bit_cast(uint32_t, p0) : 0u, live ? __builtin_bit_cast(uint32_t, p1) : 0u,
+                  live ? __builtin_bit_cast(uint32_t, p2) : 0u, live ? __builtin_bit_cast(uint32_t, p3) : 0u};
+      } else {
+        w = ok ? r.d[i] : uint4{0u, 0u, 0u, 0u};
+      }
+      vals[i] = __builtin_bit_cast(short8_t, w);
+      *reinterpret_cast<short8_t*>(kt + (4 * kq + i) * kKRow<F> + 8 * c) = vals[i];
+    }
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+      *reinterpret_cast<short4_t*>(vt + (8 * c + d) * kVRow + 8 * (kq & 3) + 4 * (kq >> 2)) =
+          short4_t{vals[0][d], vals[1][d], vals[2][d], vals[3][d]};
+    return;
+  } else {
+  typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
   half8_t vals[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -132,7 +224,7 @@ __device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step,
     const half2_t p0 = fp4x2_to_f16<0>(r.pay[i]) * s2, p1 = fp4x2_to_f16<1>(r.pay[i]) * s2;
     const half2_t p2 = fp4x2_to_f16<2>(r.pay[i]) * s2, p3 = fp4x2_to_f16<3>(r.pay[i]) * s2;
     vals[i] = half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
-    *reinterpret_cast<half8_t*>(kt + (4 * kq + i) * kKRow + 8 * c) = vals[i];
+    *reinterpret_cast<half8_t*>(kt + (4 * kq + i) * kKRow<F> + 8 * c) = vals[i];
   }
 #pragma unroll
   for (int d = 0; d < 8; ++d)
@@ -149,7 +241,8 @@ __device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step,
       hv[2 * e] = pr.x;
       hv[2 * e + 1] = pr.y;
     }
-    *reinterpret_cast<half8_t*>(kt + key * kKRow + kDl + 8 * p) = hv;
+    *reinterpret_cast<half8_t*>(kt + key * kKRow<F> + kDl + 8 * p) = hv;
+  }
   }
 }
 
@@ -166,8 +259,9 @@ __device__ inline void store_vals(const MlaArgs& a, int64_t row, int head, int d
 }
 
 
-template <bool TWO>
+template <int F, bool TWO>
 __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
+  constexpr int kQC = kQChunks<F>, kQR = kQReg<F>;
   extern __shared__ __align__(16) uint8_t lds[];
   asm volatile("" ::"s"(a.xcd_units), "s"(a.xcd_extra), "s"(a.splits), "s"(a.keys_per_split), "s"(a.topk[0]),
                "s"(a.topk[1]), "s"(a.idx[0]), "s"(a.idx[1]), "s"(a.idx_stride[0]), "s"(a.idx_stride[1]),
@@ -182,17 +276,17 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
   const int head = 16 * wave + hl;
   const bool head_live = head < a.heads;
 
-  _Float16* kt = reinterpret_cast<_Float16*>(lds);
-  _Float16* vt = reinterpret_cast<_Float16*>(lds + kKTile);
-  _Float16* qs = reinterpret_cast<_Float16*>(lds + kKTile + kVTile);
-  int32_t* slots = reinterpret_cast<int32_t*>(lds + kKTile + kVTile + kQTile);
+  uint16_t* kt = reinterpret_cast<uint16_t*>(lds);
+  uint16_t* vt = reinterpret_cast<uint16_t*>(lds + kKTile<F>);
+  uint16_t* qs = reinterpret_cast<uint16_t*>(lds + kKTile<F> + kVTile);
+  int32_t* slots = reinterpret_cast<int32_t*>(lds + kKTile<F> + kVTile + kQTile<F>);
 
   // the query's B operands first: dims 32kk + 8j .. +7 of head `head` (a clamped valid head for padding lanes)
-  uint4 qraw[kQChunks];
+  uint4 qraw[kQC];
   {
     const uint16_t* qp = a.q + row * a.q_rs + (int64_t)min(head, a.heads - 1) * a.q_hs;
 #pragma unroll
-    for (int kk = 0; kk < kQChunks; ++kk) qraw[kk] = *reinterpret_cast<const uint4*>(qp + 32 * kk + 8 * j);
+    for (int kk = 0; kk < kQC; ++kk) qraw[kk] = *reinterpret_cast<const uint4*>(qp + 32 * kk + 8 * j);
   }
 
   // 1. the split's key list: columns [t0, t0 + keys_per_split) of list 0 then list 1, as slot entries in LDS
@@ -216,35 +310,46 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
   }
   __syncthreads();
 
-  // B operands of q.k: FP16 of q * scale * log2(e), chunks 0..kQReg-1 in registers, the rest in LDS
-  half8_t qb[kQReg];
+  // B operands of q.k, chunks 0..kQR-1 in registers, the rest in LDS: NVFP4, FP16 of q * scale * log2(e); V4, q
+  // as given (BF16), the scale applied to the FP32 scores
+  short8_t qb[kQR];
 #pragma unroll
-  for (int kk = 0; kk < kQChunks; ++kk) {
-    const uint32_t ws[4] = {qraw[kk].x, qraw[kk].y, qraw[kk].z, qraw[kk].w};
-    half8_t h;
+  for (int kk = 0; kk < kQC; ++kk) {
+    short8_t h;
+    if constexpr (F == kNvfp4) {
+      const uint32_t ws[4] = {qraw[kk].x, qraw[kk].y, qraw[kk].z, qraw[kk].w};
+      half8_t hh;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      h[2 * e] = head_live ? (_Float16)(bf16_bits_to_f32(ws[e] & 0xFFFFu) * a.qscale) : (_Float16)0.0f;
-      h[2 * e + 1] = head_live ? (_Float16)(bf16_bits_to_f32(ws[e] >> 16) * a.qscale) : (_Float16)0.0f;
+      for (int e = 0; e < 4; ++e) {
+        hh[2 * e] = head_live ? (_Float16)(bf16_bits_to_f32(ws[e] & 0xFFFFu) * a.qscale) : (_Float16)0.0f;
+        hh[2 * e + 1] = head_live ? (_Float16)(bf16_bits_to_f32(ws[e] >> 16) * a.qscale) : (_Float16)0.0f;
+      }
+      h = __builtin_bit_cast(short8_t, hh);
+    } else {
+      h = __builtin_bit_cast(short8_t, head_live ? qraw[kk] : uint4{0u, 0u, 0u, 0u});
     }
-    if (kk < kQReg)
-      qb[kk < kQReg ? kk : 0] = h;
+    if (kk < kQR)
+      qb[kk < kQR ? kk : 0] = h;
     else
-      *reinterpret_cast<half8_t*>(qs + ((kk - kQReg) * kMHeads + 16 * wave + hl) * kQRow + 8 * j) = h;
+      *reinterpret_cast<short8_t*>(qs + ((kk - kQR) * kMHeads + 16 * wave + hl) * kQRow + 8 * j) = h;
   }
-  const float g0 = *a.c[0].g, g1 = TWO ? *a.c[1].g : g0;
+  float g0 = 1.0f, g1 = 1.0f;   // NVFP4 global scales (V4 has none)
+  if constexpr (F == kNvfp4) {
+    g0 = *a.c[0].g;
+    g1 = TWO ? *a.c[1].g : g0;
+  }
 
   float m = -__builtin_inff(), l = 0.0f;
   float4_t acc[32];
 #pragma unroll
   for (int i = 0; i < 32; ++i) acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  Raw raw;
-  load_raw<TWO>(a, slots, 0, raw);
+  Raw<F> raw;
+  load_raw<F, TWO>(a, slots, 0, raw);
   for (int step = 0; step < a.steps; ++step) {
-    dequant<TWO>(a, slots, step, raw, g0, g1, kt, vt);
+    dequant<F, TWO>(a, slots, step, raw, g0, g1, kt, vt);
     __syncthreads();
-    if (step + 1 < a.steps) load_raw<TWO>(a, slots, step + 1, raw);
+    if (step + 1 < a.steps) load_raw<F, TWO>(a, slots, step + 1, raw);
     const uint32_t valid = (uint32_t)__builtin_amdgcn_ballot_w64(lane < kMSteps &&
                                                                   entry_valid(slots[step * kMSteps + (lane & 31)]));
     // S^T for the two 16-key tiles, each as two independent MFMA chains (even / odd dim chunks)
@@ -255,21 +360,21 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
       s2[tt] = float4_t{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
-    for (int kk = 0; kk < kQChunks; ++kk) {
-      const half8_t qv = kk < kQReg ? qb[kk < kQReg ? kk : 0]
-                                    : *reinterpret_cast<const half8_t*>(
-                                          qs + ((kk - kQReg) * kMHeads + 16 * wave + hl) * kQRow + 8 * j);
+    for (int kk = 0; kk < kQC; ++kk) {
+      const short8_t qv = kk < kQR ? qb[kk < kQR ? kk : 0]
+                                     : *reinterpret_cast<const short8_t*>(
+                                           qs + ((kk - kQR) * kMHeads + 16 * wave + hl) * kQRow + 8 * j);
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
-        const half8_t kv = *reinterpret_cast<const half8_t*>(kt + (16 * tt + hl) * kKRow + 8 * j + 32 * kk);
+        const short8_t kv = *reinterpret_cast<const short8_t*>(kt + (16 * tt + hl) * kKRow<F> + 8 * j + 32 * kk);
         if (kk & 1)
-          s2[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qv, s2[tt], 0, 0, 0);
+          s2[tt] = mfma16<F>(kv, qv, s2[tt]);
         else
-          s[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qv, s[tt], 0, 0, 0);
+          s[tt] = mfma16<F>(kv, qv, s[tt]);
       }
     }
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) s[tt] += s2[tt];
+    for (int tt = 0; tt < 2; ++tt) s[tt] = (F == kNvfp4) ? s[tt] + s2[tt] : (s[tt] + s2[tt]) * a.qscale;
     // online softmax of head hl over keys T(j), lazy rescale
     float sv[8];
 #pragma unroll
@@ -289,20 +394,23 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
       m = m_new;
     }
     const float m_use = (m == -__builtin_inff()) ? 0.0f : m;
-    half8_t pb;
+    short8_t pb;
     float psum = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float p = __builtin_amdgcn_exp2f(sv[e] - m_use);
       psum += p;
-      pb[e] = (_Float16)p;
+      if constexpr (F == kNvfp4)
+        pb[e] = __builtin_bit_cast(short, (_Float16)p);
+      else
+        pb[e] = __builtin_bit_cast(short, (__bf16)p);
     }
     l += psum;
     // O^T += V^T . P^T over the 32 dim tiles
 #pragma unroll
     for (int dt = 0; dt < 32; ++dt) {
-      const half8_t av = *reinterpret_cast<const half8_t*>(vt + (16 * dt + hl) * kVRow + 8 * j);
-      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb, acc[dt], 0, 0, 0);
+      const short8_t av = *reinterpret_cast<const short8_t*>(vt + (16 * dt + hl) * kVRow + 8 * j);
+      acc[dt] = mfma16<F>(av, pb, acc[dt]);
     }
     __syncthreads();
   }
@@ -325,17 +433,23 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
       a.lse[row * a.heads + head] = l_tot > 0.0f ? (m + __builtin_log2f(l_tot)) * kLn2 : -__builtin_inff();
     return;
   }
-  // 2. the split's output normalized by its own sum (FP16: a convex combination of FP16 latent values) plus its
-  //    max and sum; a second launch merges the splits
+  // 2. the split's output normalized by its own sum (NVFP4: FP16, a convex combination of FP16 latent values; V4:
+  //    FP32) plus its max and sum; a second launch merges the splits
   if (head_live) {
     const int64_t ph = ((int64_t)row * a.splits + split) * a.heads + head;
-    uint16_t* pp = a.part + ph * kDl;
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if constexpr (F == kNvfp4) {
+      uint16_t* pp = static_cast<uint16_t*>(a.part) + ph * kDl;
 #pragma unroll
-    for (int dt = 0; dt < 32; ++dt) {
-      const uint2 w = {f32_to_f16_bits(acc[dt][0] * inv) | (f32_to_f16_bits(acc[dt][1] * inv) << 16),
-                       f32_to_f16_bits(acc[dt][2] * inv) | (f32_to_f16_bits(acc[dt][3] * inv) << 16)};
-      *reinterpret_cast<uint2*>(pp + 16 * dt + 4 * j) = w;
+      for (int dt = 0; dt < 32; ++dt) {
+        const uint2 w = {f32_to_f16_bits(acc[dt][0] * inv) | (f32_to_f16_bits(acc[dt][1] * inv) << 16),
+                         f32_to_f16_bits(acc[dt][2] * inv) | (f32_to_f16_bits(acc[dt][3] * inv) << 16)};
+        *reinterpret_cast<uint2*>(pp + 16 * dt + 4 * j) = w;
+      }
+    } else {
+      float* pp = static_cast<float*>(a.part) + ph * kDl;
+#pragma unroll
+      for (int dt = 0; dt < 32; ++dt) *reinterpret_cast<float4_t*>(pp + 16 * dt + 4 * j) = acc[dt] * inv;
     }
     if (j == 0) *reinterpret_cast<float2*>(a.ml + ph * 2) = float2{m, l_tot};
   }
@@ -343,6 +457,7 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
 
 // Split merge: one thread per (row, head, 8 dims); 64 threads cover a head's 512 dims with 16-byte loads.
 // out = sum_s w_s o_s with w_s = 2^(m_s - max m) l_s / (sum_s 2^(m_s - max m) l_s + sink term).
+template <int F>
 __global__ void __launch_bounds__(256) mla_merge_kernel(const MlaArgs a, int rows) {
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t rh = t >> 6;                  // row * heads + head
@@ -358,15 +473,25 @@ __global__ void __launch_bounds__(256) mla_merge_kernel(const MlaArgs a, int row
   for (int sp = 0; sp < a.splits; ++sp) {
     const int64_t ph = base + (int64_t)sp * a.heads;
     const float2 ml = *reinterpret_cast<const float2*>(a.ml + ph * 2);
-    const uint4 x = *reinterpret_cast<const uint4*>(a.part + ph * kDl + 8 * c);
     const float w = __builtin_amdgcn_exp2f(ml.x - mu) * ml.y;
     l_all += w;
-    const uint32_t u[4] = {x.x, x.y, x.z, x.w};
+    if constexpr (F == kNvfp4) {
+      const uint4 x = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.part) + ph * kDl + 8 * c);
+      const uint32_t u[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const half2_t h = __builtin_bit_cast(half2_t, u[e]);
-      o[2 * e] += w * (float)h.x;
-      o[2 * e + 1] += w * (float)h.y;
+      for (int e = 0; e < 4; ++e) {
+        const half2_t h = __builtin_bit_cast(half2_t, u[e]);
+        o[2 * e] += w * (float)h.x;
+        o[2 * e + 1] += w * (float)h.y;
+      }
+    } else {
+      const float4_t* x = reinterpret_cast<const float4_t*>(static_cast<const float*>(a.part) + ph * kDl + 8 * c);
+      const float4_t x0 = x[0], x1 = x[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[e] += w * x0[e];
+        o[4 + e] += w * x1[e];
+      }
     }
   }
   float total = l_all;
@@ -394,57 +519,35 @@ int check_cache(const char* what, const xt_mla_cache* c, int64_t* pay_stride, in
   return XT_OK;
 }
 
-}  // namespace
-}  // namespace xt
-
-using namespace xt;
-
-// Workspace: [kCounterBytes, unused here: the counter region of the decode entry points][partial outputs [rows,
-// splits, heads, 512] FP16][partial max and sum [rows, splits, heads, 2] FP32]
-
-extern "C" size_t xt_sparse_mla_workspace_bytes(int rows, int heads, int splits) {
-  if (rows < 0 || heads <= 0 || splits <= 0) return 0;
-  if (splits == 1) return 256;
-  return kCounterBytes + (size_t)rows * splits * heads * (kDl * 2 + 2 * sizeof(float));
+int check_pages(const char* what, const xt_mla_fp8_cache* c, CacheDev* cd) {
+  if (!c->pages) return fail(XT_EINVAL, "%s: the page buffer is null", what);
+  if (c->page_size <= 0 || (c->page_size & (c->page_size - 1)) || c->page_size > 4096)
+    return fail(XT_EUNSUPPORTED, "%s: page size %d (supported: powers of 2 up to 4096)", what, c->page_size);
+  const int64_t min_bytes = (int64_t)c->page_size * (kV4Row + 8);
+  if (c->num_pages <= 0 || c->page_stride < min_bytes || c->page_stride % 16 || !aligned(c->pages, 16))
+    return fail(XT_EINVAL, "%s: %lld pages with a %lld-byte stride do not hold %d tokens of 584 bytes (16-byte "
+                "aligned)", what, (long long)c->num_pages, (long long)c->page_stride, c->page_size);
+  if (c->num_pages * c->page_size > 0x3FFFFFFFLL)
+    return fail(XT_EINVAL, "%s: %lld tokens exceed 2^30-1", what, (long long)(c->num_pages * c->page_size));
+  *cd = CacheDev{c->pages, nullptr, nullptr, nullptr, c->num_pages * c->page_size, 0u, 0u, 0u,
+                 (uint32_t)__builtin_ctz((unsigned)c->page_size), (uint64_t)c->page_stride};
+  return XT_OK;
 }
 
-extern "C" int xt_sparse_mla_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, int heads,
-                                   int latent_dim, int rope_dim, const xt_mla_cache* cache, const xt_mla_keys* keys,
-                                   const xt_mla_cache* extra_cache, const xt_mla_keys* extra_keys, const float* sink,
-                                   float scale, void* out, int64_t out_row_stride, int64_t out_head_stride,
-                                   int out_dtype, float* lse, int rows, int splits, void* workspace,
-                                   size_t workspace_bytes, xt_stream_t stream) {
-  const char* what = "xt_sparse_mla_nvfp4";
-  if (latent_dim != kDl || rope_dim != kDr)
-    return fail(XT_EUNSUPPORTED, "%s: latent %d + rope %d (supported: %d + %d)", what, latent_dim, rope_dim, kDl, kDr);
-  if (heads <= 0 || heads > kMHeads) return fail(XT_EUNSUPPORTED, "%s: %d heads (supported: 1..%d)", what, heads,
-                                                 kMHeads);
-  if (rows < 0 || splits < 1 || splits > 64) return fail(XT_EINVAL, "%s: bad rows %d / splits %d", what, rows, splits);
-  if (out_dtype != XT_DTYPE_BF16 && out_dtype != XT_DTYPE_F16)
-    return fail(XT_EINVAL, "%s: output dtype must be BF16 or FP16", what);
-  if (!cache || !keys) return fail(XT_EINVAL, "%s: the key cache and key list are required", what);
-  if (rows == 0) return ok();
-  if (!q || !out || !workspace || !keys->indices) return fail(XT_EINVAL, "%s: a required pointer is null", what);
-  if (!aligned(q, 16) || q_row_stride % 8 || q_head_stride % 8 || !aligned(out, 16) || out_row_stride % 8 ||
-      out_head_stride % 8)
-    return fail(XT_EINVAL, "%s: q and out rows must be 16-byte aligned (strides in elements: multiples of 8)", what);
-  if (keys->topk < 0 || (extra_keys && extra_keys->topk < 0)) return fail(XT_EINVAL, "%s: negative topk", what);
-  const bool extra = extra_cache && extra_keys && extra_keys->indices && extra_keys->topk > 0;
-  MlaArgs a;
-  int64_t ps, ss, rs;
-  int st = check_cache(what, cache, &ps, &ss, &rs);
-  if (st != XT_OK) return st;
-  a.c[0] = CacheDev{cache->pay, cache->scales, static_cast<const uint16_t*>(cache->rope), cache->g, cache->slots,
-                    (uint32_t)ps, (uint32_t)ss, (uint32_t)rs};
-  if (extra) {
-    st = check_cache(what, extra_cache, &ps, &ss, &rs);
-    if (st != XT_OK) return st;
-    a.c[1] = CacheDev{extra_cache->pay, extra_cache->scales, static_cast<const uint16_t*>(extra_cache->rope),
-                      extra_cache->g, extra_cache->slots, (uint32_t)ps, (uint32_t)ss, (uint32_t)rs};
-  } else {
-    a.c[1] = a.c[0];
-  }
-  const size_t need = xt_sparse_mla_workspace_bytes(rows, heads, splits);
+size_t mla_workspace_bytes(int rows, int heads, int splits, size_t part_elem) {
+  if (rows < 0 || heads <= 0 || splits <= 0) return 0;
+  if (splits == 1) return 256;
+  return kCounterBytes + (size_t)rows * splits * heads * (kDl * part_elem + 2 * sizeof(float));
+}
+
+// Everything but the caches: checks, key lists, split sizing, workspace carving and the launches.
+template <int F>
+int mla_launch(const char* what, MlaArgs& a, bool extra, const void* q, int64_t q_row_stride, int64_t q_head_stride,
+               int heads, const xt_mla_keys* keys, const xt_mla_keys* extra_keys, const float* sink, float scale,
+               void* out, int64_t out_row_stride, int64_t out_head_stride, int out_dtype, float* lse, int rows,
+               int splits, void* workspace, size_t workspace_bytes, xt_stream_t stream) {
+  const size_t part_elem = F == kNvfp4 ? 2 : 4;
+  const size_t need = mla_workspace_bytes(rows, heads, splits, part_elem);
   if (workspace_bytes < need)
     return fail(XT_EWORKSPACE, "%s: workspace %zu bytes < %zu needed", what, workspace_bytes, need);
   if (!aligned(workspace, 256)) return fail(XT_EINVAL, "%s: workspace must be 256-byte aligned", what);
@@ -475,20 +578,21 @@ extern "C" int xt_sparse_mla_nvfp4(const void* q, int64_t q_row_stride, int64_t 
     a.keys_per_split = kMSteps;   // no keys: one all-invalid step writes the zero rows
     a.steps = 1;
   }
-  const size_t lds_bytes = (size_t)kKTile + kVTile + kQTile + (size_t)a.steps * kMSteps * 4;
+  const size_t lds_bytes = (size_t)kKTile<F> + kVTile + kQTile<F> + (size_t)a.steps * kMSteps * 4;
   if (lds_bytes > 160 * 1024 - 256)
     return fail(XT_EUNSUPPORTED, "%s: %d keys per split need %zu bytes of LDS; use more splits", what,
                 a.keys_per_split, lds_bytes);
-  a.part = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + kCounterBytes);
-  a.ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes + (size_t)rows * splits * heads * kDl * 2);
+  char* ws = static_cast<char*>(workspace);
+  a.part = ws + kCounterBytes;
+  a.ml = reinterpret_cast<float*>(ws + kCounterBytes + (size_t)rows * splits * heads * kDl * part_elem);
   const int64_t n_units = (int64_t)rows * splits;
   if (n_units > 0x7FFFFFFFLL) return fail(XT_EUNSUPPORTED, "%s: %lld workgroups", what, (long long)n_units);
   a.xcd_units = (uint32_t)(n_units / 8);
   a.xcd_extra = (uint32_t)(n_units % 8);
   // dynamic LDS above 64 KB must be allowed per kernel; raised to the largest size asked for so far
   static size_t lds_allowed[2] = {64 * 1024, 64 * 1024};
-  const void* fn = extra ? reinterpret_cast<const void*>(&mla_kernel<true>)
-                         : reinterpret_cast<const void*>(&mla_kernel<false>);
+  const void* fn = extra ? reinterpret_cast<const void*>(&mla_kernel<F, true>)
+                         : reinterpret_cast<const void*>(&mla_kernel<F, false>);
   if (lds_bytes > lds_allowed[extra]) {
     const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
     if (err != hipSuccess)
@@ -496,15 +600,114 @@ extern "C" int xt_sparse_mla_nvfp4(const void* q, int64_t q_row_stride, int64_t 
     lds_allowed[extra] = lds_bytes;
   }
   if (extra)
-    hipLaunchKernelGGL(mla_kernel<true>, dim3((unsigned)n_units), dim3(64 * kMWaves), lds_bytes,
+    hipLaunchKernelGGL((mla_kernel<F, true>), dim3((unsigned)n_units), dim3(64 * kMWaves), lds_bytes,
                        reinterpret_cast<hipStream_t>(stream), a);
   else
-    hipLaunchKernelGGL(mla_kernel<false>, dim3((unsigned)n_units), dim3(64 * kMWaves), lds_bytes,
+    hipLaunchKernelGGL((mla_kernel<F, false>), dim3((unsigned)n_units), dim3(64 * kMWaves), lds_bytes,
                        reinterpret_cast<hipStream_t>(stream), a);
   if (splits > 1) {
     const int64_t threads = (int64_t)rows * heads * 64;
-    hipLaunchKernelGGL(mla_merge_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+    hipLaunchKernelGGL(mla_merge_kernel<F>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                        reinterpret_cast<hipStream_t>(stream), a, rows);
   }
   return check_launch(what);
+}
+
+// Checks shared by both entry points; returns XT_OK with *done set when there is nothing to launch.
+int mla_common_checks(const char* what, const void* q, int64_t q_row_stride, int64_t q_head_stride, int heads,
+                      const void* cache, const xt_mla_keys* keys, const xt_mla_keys* extra_keys, void* out,
+                      int64_t out_row_stride, int64_t out_head_stride, int out_dtype, int rows, int splits,
+                      void* workspace, bool* done) {
+  *done = false;
+  if (heads <= 0 || heads > kMHeads) return fail(XT_EUNSUPPORTED, "%s: %d heads (supported: 1..%d)", what, heads,
+                                                 kMHeads);
+  if (rows < 0 || splits < 1 || splits > 64) return fail(XT_EINVAL, "%s: bad rows %d / splits %d", what, rows, splits);
+  if (out_dtype != XT_DTYPE_BF16 && out_dtype != XT_DTYPE_F16)
+    return fail(XT_EINVAL, "%s: output dtype must be BF16 or FP16", what);
+  if (!cache || !keys) return fail(XT_EINVAL, "%s: the key cache and key list are required", what);
+  if (rows == 0) {
+    *done = true;
+    return ok();
+  }
+  if (!q || !out || !workspace || !keys->indices) return fail(XT_EINVAL, "%s: a required pointer is null", what);
+  if (!aligned(q, 16) || q_row_stride % 8 || q_head_stride % 8 || !aligned(out, 16) || out_row_stride % 8 ||
+      out_head_stride % 8)
+    return fail(XT_EINVAL, "%s: q and out rows must be 16-byte aligned (strides in elements: multiples of 8)", what);
+  if (keys->topk < 0 || (extra_keys && extra_keys->topk < 0)) return fail(XT_EINVAL, "%s: negative topk", what);
+  return XT_OK;
+}
+
+}  // namespace
+}  // namespace xt
+
+using namespace xt;
+
+// Workspace: [kCounterBytes, unused here: the counter region of the decode entry points][partial outputs [rows,
+// splits, heads, 512] FP16 (NVFP4) or FP32 (V4)][partial max and sum [rows, splits, heads, 2] FP32]
+
+extern "C" size_t xt_sparse_mla_workspace_bytes(int rows, int heads, int splits) {
+  return mla_workspace_bytes(rows, heads, splits, 2);
+}
+
+extern "C" size_t xt_sparse_mla_fp8_workspace_bytes(int rows, int heads, int splits) {
+  return mla_workspace_bytes(rows, heads, splits, 4);
+}
+
+extern "C" int xt_sparse_mla_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, int heads,
+                                   int latent_dim, int rope_dim, const xt_mla_cache* cache, const xt_mla_keys* keys,
+                                   const xt_mla_cache* extra_cache, const xt_mla_keys* extra_keys, const float* sink,
+                                   float scale, void* out, int64_t out_row_stride, int64_t out_head_stride,
+                                   int out_dtype, float* lse, int rows, int splits, void* workspace,
+                                   size_t workspace_bytes, xt_stream_t stream) {
+  const char* what = "xt_sparse_mla_nvfp4";
+  if (latent_dim != kDl || rope_dim != kDr)
+    return fail(XT_EUNSUPPORTED, "%s: latent %d + rope %d (supported: %d + %d)", what, latent_dim, rope_dim, kDl, kDr);
+  bool done;
+  int st = mla_common_checks(what, q, q_row_stride, q_head_stride, heads, cache, keys, extra_keys, out,
+                             out_row_stride, out_head_stride, out_dtype, rows, splits, workspace, &done);
+  if (st != XT_OK || done) return st;
+  const bool extra = extra_cache && extra_keys && extra_keys->indices && extra_keys->topk > 0;
+  MlaArgs a;
+  int64_t ps, ss, rs;
+  st = check_cache(what, cache, &ps, &ss, &rs);
+  if (st != XT_OK) return st;
+  a.c[0] = CacheDev{cache->pay, cache->scales, static_cast<const uint16_t*>(cache->rope), cache->g, cache->slots,
+                    (uint32_t)ps, (uint32_t)ss, (uint32_t)rs, 0u, 0u};
+  if (extra) {
+    st = check_cache(what, extra_cache, &ps, &ss, &rs);
+    if (st != XT_OK) return st;
+    a.c[1] = CacheDev{extra_cache->pay, extra_cache->scales, static_cast<const uint16_t*>(extra_cache->rope),
+                      extra_cache->g, extra_cache->slots, (uint32_t)ps, (uint32_t)ss, (uint32_t)rs, 0u, 0u};
+  } else {
+    a.c[1] = a.c[0];
+  }
+  return mla_launch<kNvfp4>(what, a, extra, q, q_row_stride, q_head_stride, heads, keys, extra_keys, sink, scale, out,
+                            out_row_stride, out_head_stride, out_dtype, lse, rows, splits, workspace,
+                            workspace_bytes, stream);
+}
+
+extern "C" int xt_sparse_mla_fp8(const void* q, int64_t q_row_stride, int64_t q_head_stride, int heads,
+                                 const xt_mla_fp8_cache* cache, const xt_mla_keys* keys,
+                                 const xt_mla_fp8_cache* extra_cache, const xt_mla_keys* extra_keys, const float* sink,
+                                 float scale, void* out, int64_t out_row_stride, int64_t out_head_stride,
+                                 int out_dtype, float* lse, int rows, int splits, void* workspace,
+                                 size_t workspace_bytes, xt_stream_t stream) {
+  const char* what = "xt_sparse_mla_fp8";
+  bool done;
+  int st = mla_common_checks(what, q, q_row_stride, q_head_stride, heads, cache, keys, extra_keys, out,
+                             out_row_stride, out_head_stride, out_dtype, rows, splits, workspace, &done);
+  if (st != XT_OK || done) return st;
+  const bool extra = extra_cache && extra_keys && extra_keys->indices && extra_keys->topk > 0;
+  MlaArgs a;
+  st = check_pages(what, cache, &a.c[0]);
+  if (st != XT_OK) return st;
+  if (extra) {
+    st = check_pages(what, extra_cache, &a.c[1]);
+    if (st != XT_OK) return st;
+  } else {
+    a.c[1] = a.c[0];
+  }
+  return mla_launch<kFp8V4>(what, a, extra, q, q_row_stride, q_head_stride, heads, keys, extra_keys, sink, scale, out,
+                            out_row_stride, out_head_stride, out_dtype, lse, rows, splits, workspace,
+                            workspace_bytes, stream);
 }

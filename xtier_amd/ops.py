@@ -343,6 +343,23 @@ def _mla_cache(raw):
     return c, pay.shape[1] * 2, rope.shape[1], (pay, sc, rope, g)
 
 
+V4_ROW_BYTES = 584   # a DeepSeek V4 FP8 token: 448 E4M3 + 128 B rope + 8 B scale row
+
+
+def is_v4_cache(k_cache):
+    """A DeepSeek V4 FP8 page view [pages, page_size, 1, 584] of 1-byte elements (sparse_mla.py:156-160)."""
+    return torch.is_tensor(k_cache) and k_cache.dim() >= 2 and k_cache.shape[-1] == V4_ROW_BYTES and \
+        k_cache.element_size() == 1
+
+
+def _v4_cache(cache):
+    """A V4 page view -> xt_mla_fp8_cache (page stride from the view, as sparse_mla.py:_views takes it)."""
+    _need_cuda(cache)
+    raw = cache.view(torch.uint8) if cache.dtype != torch.uint8 else cache
+    c = _lib.MlaFp8Cache(_ptr(raw), raw.shape[0], raw.shape[1], raw.stride(0))
+    return c, raw
+
+
 def _mla_keys(indices, lengths, rows):
     indices = indices.reshape(rows, -1)
     if indices.dtype != torch.int32 or indices.stride(-1) != 1:
@@ -361,16 +378,20 @@ def default_mla_splits(rows, topk):
     return max(1, min(math.ceil(256 / max(1, rows)), max(1, topk // 256), 64))
 
 
-def mla_workspace_bytes(rows, heads, splits):
+def mla_workspace_bytes(rows, heads, splits, v4=False):
+    if v4:
+        return int(_lib.lib().xt_sparse_mla_fp8_workspace_bytes(rows, heads, splits))
     return int(_lib.lib().xt_sparse_mla_workspace_bytes(rows, heads, splits))
 
 
 def sparse_mla(q, k_cache, indices, topk_length, attn_sink, softmax_scale, extra_k_cache=None, extra_indices=None,
                extra_topk_length=None, out=None, lse=None, splits=None, ws=None):
-    """sparse_mla (xtier/packs/deepseek_v4/sparse_mla.py:167-217) on an NVFP4 latent cache: q [rows, 1, heads, 576]
-    (or [rows, heads, 576]) BF16, indices [rows, 1, topk] slots of k_cache (-1: none), optional extra_* into a second
-    cache, attn_sink [heads] FP32 or None. k_cache: a LatentPool or (pay, scales, rope, g). Returns (out [rows, 1,
-    heads, 512] BF16, lse [rows, heads, 1] FP32, natural log of the keys' sum) as the reference does."""
+    """sparse_mla (xtier/packs/deepseek_v4/sparse_mla.py:167-217): q [rows, 1, heads, D] (or [rows, heads, D]) BF16,
+    indices [rows, 1, topk] slots of k_cache (-1: none), optional extra_* into a second cache, attn_sink [heads] FP32
+    or None. k_cache: DeepSeek V4 FP8 pages [pages, page_size, 1, 584] (D = 512, value = key, the reference's own
+    layout), or an NVFP4 latent cache (a LatentPool or (pay, scales, rope, g); D = 576, value = the 512-wide latent).
+    Returns (out [rows, 1, heads, 512] BF16, lse [rows, heads, 1] FP32, natural log of the keys' sum) as the reference
+    does."""
     shape4 = q.dim() == 4
     if shape4:
         rows, s_q, heads, dim = q.shape
@@ -379,9 +400,16 @@ def sparse_mla(q, k_cache, indices, topk_length, attn_sink, softmax_scale, extra
         q = q.reshape(rows, heads, dim)
     else:
         rows, heads, dim = q.shape
-    cache, dl, dr, keep = _mla_cache(k_cache)
-    if dim != dl + dr:
-        raise NotImplementedError(f'xtier_amd.sparse_mla: q head size {dim} != latent {dl} + rope {dr}')
+    v4 = is_v4_cache(k_cache)
+    if v4:
+        cache, keep = _v4_cache(k_cache)
+        dl, dr = 512, 0
+        if dim != 512:
+            raise NotImplementedError(f'xtier_amd.sparse_mla: V4 pages take head dim 512, not {tuple(q.shape)}')
+    else:
+        cache, dl, dr, keep = _mla_cache(k_cache)
+        if dim != dl + dr:
+            raise NotImplementedError(f'xtier_amd.sparse_mla: q head size {dim} != latent {dl} + rope {dr}')
     _need_cuda(q, attn_sink, out, lse)
     if q.dtype != torch.bfloat16 or q.stride(-1) != 1:
         q = q.to(torch.bfloat16).contiguous()
@@ -389,9 +417,14 @@ def sparse_mla(q, k_cache, indices, topk_length, attn_sink, softmax_scale, extra
     extra = extra_k_cache is not None and extra_indices is not None
     cache2 = keys2 = None
     if extra:
-        cache2, dl2, dr2, keep2 = _mla_cache(extra_k_cache)
-        if (dl2, dr2) != (dl, dr):
-            raise ValueError('xtier_amd.sparse_mla: both caches must have the same latent and rope widths')
+        if v4 != is_v4_cache(extra_k_cache):
+            raise ValueError('xtier_amd.sparse_mla: both caches must have the same format')
+        if v4:
+            cache2, keep2 = _v4_cache(extra_k_cache)
+        else:
+            cache2, dl2, dr2, keep2 = _mla_cache(extra_k_cache)
+            if (dl2, dr2) != (dl, dr):
+                raise ValueError('xtier_amd.sparse_mla: both caches must have the same latent and rope widths')
         keys2, keep_k2 = _mla_keys(extra_indices, extra_topk_length, rows)
     if out is None:
         out = torch.empty((rows, heads, dl), dtype=torch.bfloat16, device=q.device)
@@ -403,16 +436,24 @@ def sparse_mla(q, k_cache, indices, topk_length, attn_sink, softmax_scale, extra
     if splits is None:
         splits = default_mla_splits(rows, topk_all)
         if ws is None and torch.cuda.is_current_stream_capturing() and rows and \
-                _cached_workspace_bytes(q.device) < mla_workspace_bytes(rows, heads, splits):
+                _cached_workspace_bytes(q.device) < mla_workspace_bytes(rows, heads, splits, v4):
             splits = 1
-    need = mla_workspace_bytes(rows, heads, splits)
+    need = mla_workspace_bytes(rows, heads, splits, v4)
     if ws is None:
         ws = (workspace(q.device, need) if _cached_workspace_bytes(q.device) >= need
               or not torch.cuda.is_current_stream_capturing()
               else torch.empty(need, dtype=torch.uint8, device=q.device))
-    _lib.check(_lib.lib().xt_sparse_mla_nvfp4(
-        _ptr(q), q.stride(0), q.stride(1), heads, dl, dr, ctypes.byref(cache), ctypes.byref(keys),
-        ctypes.byref(cache2) if extra else None, ctypes.byref(keys2) if extra else None, _ptr(attn_sink),
-        float(softmax_scale), _ptr(out), out.stride(0), out.stride(1), _DTYPES[out.dtype], _ptr(lse), rows,
-        int(splits), _ptr(ws), ws.numel(), _stream(q)), 'sparse_mla')
+    if v4:
+        status = _lib.lib().xt_sparse_mla_fp8(
+            _ptr(q), q.stride(0), q.stride(1), heads, ctypes.byref(cache), ctypes.byref(keys),
+            ctypes.byref(cache2) if extra else None, ctypes.byref(keys2) if extra else None, _ptr(attn_sink),
+            float(softmax_scale), _ptr(out), out.stride(0), out.stride(1), _DTYPES[out.dtype], _ptr(lse), rows,
+            int(splits), _ptr(ws), ws.numel(), _stream(q))
+    else:
+        status = _lib.lib().xt_sparse_mla_nvfp4(
+            _ptr(q), q.stride(0), q.stride(1), heads, dl, dr, ctypes.byref(cache), ctypes.byref(keys),
+            ctypes.byref(cache2) if extra else None, ctypes.byref(keys2) if extra else None, _ptr(attn_sink),
+            float(softmax_scale), _ptr(out), out.stride(0), out.stride(1), _DTYPES[out.dtype], _ptr(lse), rows,
+            int(splits), _ptr(ws), ws.numel(), _stream(q))
+    _lib.check(status, 'sparse_mla')
     return (out.unsqueeze(1), lse.unsqueeze(-1)) if shape4 else (out, lse)
