@@ -206,12 +206,15 @@ def run_mla(args, w, ops, workloads):
     torch.cuda.set_device(0)
     t0 = time.time()
     layers = 1 if w.causal else max(1, min(args.layers, 6))
-    pools = [build_latent_pool(w, 17 + l, args.layout, workloads, LatentPool) for l in range(layers)]
+    if w.fmt == 'fp8_v4':
+        pools = [workloads.v4_pages(w.slots, w.page, workloads.generator('cuda', 17 + l), 'cuda') for l in range(layers)]
+    else:
+        pools = [build_latent_pool(w, 17 + l, args.layout, workloads, LatentPool) for l in range(layers)]
     inp = workloads.mla_inputs(w, 20261029, 'cuda')
-    scale = 1.0 / math.sqrt(w.latent + w.rope)
+    scale = 1.0 / math.sqrt(inp.q.shape[-1])
     splits = args.splits or ops.default_mla_splits(w.rows, w.topk)
-    ws = ops.workspace('cuda', ops.mla_workspace_bytes(w.rows, w.heads, splits))
-    out = torch.empty(w.rows, w.heads, w.latent, dtype=torch.bfloat16, device='cuda')
+    ws = ops.workspace('cuda', ops.mla_workspace_bytes(w.rows, w.heads, splits, v4=w.fmt == 'fp8_v4'))
+    out = torch.empty(w.rows, w.heads, 512, dtype=torch.bfloat16, device='cuda')
     lse = torch.empty(w.rows, w.heads, dtype=torch.float32, device='cuda')
     torch.cuda.synchronize()
     log(f'built {layers} latent caches of {w.slots} tokens in {time.time() - t0:.1f} s')
@@ -244,9 +247,10 @@ def run_mla(args, w, ops, workloads):
     record = {
         'metric': 'NVFP4 sparse MLA attention TFLOP/s', 'value': round(tflops, 2), 'unit': 'TFLOP/s', 'n_gpus': 1,
         'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'higher_is_better': True,
-        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f16', 'data': 'synthetic',
+        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16' if w.fmt == 'fp8_v4' else 'f16', 'data': 'synthetic',
         'config': {'workload': w.name, 'rows': w.rows, 'heads': w.heads, 'latent': w.latent, 'rope': w.rope,
-                   'context': w.ctx, 'topk': w.topk, 'causal': w.causal, 'kv_format': 'nvfp4 latent + bf16 rope',
+                   'context': w.ctx, 'topk': w.topk, 'causal': w.causal,
+                   'kv_format': 'fp8 v4 pages' if w.fmt == 'fp8_v4' else 'nvfp4 latent + bf16 rope',
                    'layers_rotated': layers, 'splits': splits, 'cache_layout': args.layout},
         'us_per_step': round(ms * 1e3, 2), 'gathered_gbs': round(gbs, 1),
         'roofline': {'bound': 'mfma', 'achieved': round(tflops, 2), 'peak': MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
@@ -393,7 +397,7 @@ def main():
     p.add_argument('--warmup', type=int, default=64)
     p.add_argument('--workload', default='gqa_decode_b32',
                    help='gqa_decode_b32 (default), cpu_ref_decode, long_ctx_decode_b4, gqa_prefill_chunk4096, '
-                        'minimax_decode_b32, qsa_varlen_b32, mla_decode_b64 or mla_prefill_2048')
+                        'minimax_decode_b32, qsa_varlen_b32, mla_decode_b64, mla_prefill_2048 or mla_v4_decode_b64')
     p.add_argument('--layers', type=int, default=16)
     p.add_argument('--splits', type=int, default=None)
     p.add_argument('--layout', default='interleaved', choices=['interleaved', 'split'],

@@ -103,6 +103,7 @@ class MlaWorkload:
     q_std: float = 0.5
     recent: int = 128
     page: int = 64
+    fmt: str = 'nvfp4'          # 'nvfp4' (latent + rope, value = latent) or 'fp8_v4' (DeepSeek V4 pages, value = key)
 
     @property
     def requests(self):
@@ -113,11 +114,17 @@ class MlaWorkload:
         return self.requests * self.ctx
 
     def algorithmic_bytes(self):
-        """Gathered latent payload + scales + rope: rows * topk * (latent/2 + latent/16 + 2 * rope)."""
+        """Gathered key bytes: NVFP4, rows * topk * (latent/2 + latent/16 + 2 * rope); V4, rows * topk * (448 E4M3 +
+        7 scale bytes + 128 rope bytes)."""
+        if self.fmt == 'fp8_v4':
+            return self.rows * self.topk * (448 + 7 + 128)
         return self.rows * self.topk * (self.latent // 2 + self.latent // 16 + 2 * self.rope)
 
     def flops(self):
-        """q.k over latent + rope and p.v over the latent: rows * heads * topk * (2 (Dl + Dr) + 2 Dl)."""
+        """q.k over the key and p.v over the value: NVFP4 rows * heads * topk * (2 (Dl + Dr) + 2 Dl); V4 (key = value
+        = 512 wide) rows * heads * topk * 4 * 512."""
+        if self.fmt == 'fp8_v4':
+            return self.rows * self.heads * self.topk * 4 * 512
         return self.rows * self.heads * self.topk * (2 * (self.latent + self.rope) + 2 * self.latent)
 
 
@@ -126,6 +133,8 @@ MLA_WORKLOADS = {
     'mla_decode_b64': MlaWorkload('mla_decode_b64', 64, 128, 131072, 2048),
     # a 2048-token prefill chunk at the end of a 131072-token context, top-2048 causal per query
     'mla_prefill_2048': MlaWorkload('mla_prefill_2048', 2048, 128, 131072, 2048, causal=True),
+    # the decode workload on DeepSeek V4 FP8 pages (pages of 64 tokens)
+    'mla_v4_decode_b64': MlaWorkload('mla_v4_decode_b64', 64, 128, 131072, 2048, fmt='fp8_v4'),
 }
 
 
@@ -319,7 +328,8 @@ def mla_cache_rows(w, gen, device, start, n):
 def mla_inputs(w, seed, device='cpu'):
     """Seeded queries and key lists of an MLA workload (the cache rows come from mla_cache_rows)."""
     gen = generator(device, seed)
-    q = (torch.randn(w.rows, w.heads, w.latent + w.rope, generator=gen, device=device) * w.q_std).to(torch.bfloat16)
+    dim = 512 if w.fmt == 'fp8_v4' else w.latent + w.rope
+    q = (torch.randn(w.rows, w.heads, dim, generator=gen, device=device) * w.q_std).to(torch.bfloat16)
     pt = page_table(w.requests, w.ctx, w.page, gen, device)
     if w.causal:
         q_pos = torch.arange(w.ctx - w.rows, w.ctx, dtype=torch.int32, device=device)
@@ -366,3 +376,19 @@ def head_major_pages(x_pay, x_sc, block):
     m = x_sc.shape[2]
     sc = x_sc.view(slots // block, block, heads, m).permute(0, 2, 1, 3).contiguous()
     return pay, sc
+
+
+def v4_pages(tokens, page_size, gen, device):
+    """DeepSeek V4 FP8 pages [pages, page_size, 1, 584] of random valid content: E4M3 bytes other than NaN, UE8M0
+    exponents 120 .. 130 (scales 2^-7 .. 2^3), BF16 N(0, 1) rope values."""
+    pages = tokens // page_size
+    buf = torch.randint(0, 256, (pages, page_size * 584), generator=gen, device=device, dtype=torch.uint8)
+    data = buf[:, :page_size * 576].view(pages, page_size, 576)
+    nope = data[..., :448]
+    nope.copy_(torch.where((nope & 0x7F) == 0x7F, nope ^ 1, nope))
+    rope = torch.randn(pages, page_size, 64, generator=gen, device=device).to(torch.bfloat16)
+    data[..., 448:] = rope.view(torch.uint8).view(pages, page_size, 128)
+    sc = buf[:, page_size * 576:].view(pages, page_size, 8)
+    sc.copy_(torch.randint(120, 131, (pages, page_size, 8), generator=gen, device=device, dtype=torch.uint8))
+    sc[..., 7] = 0
+    return buf.as_strided((pages, page_size, 1, 584), (page_size * 584, 584, 584, 1))
