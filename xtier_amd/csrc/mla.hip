@@ -44,12 +44,8 @@ constexpr int kMWaves = 8;
 constexpr int kMHeads = 16 * kMWaves;    // heads per workgroup
 template <int F>
 constexpr int kKRow = kDk<F> + 8;        // 16-bit values per K tile row (16-byte pad)
-constexpr int kVRow = kMSteps + 16;      // halves per V^T tile row (96 bytes); keys stored in the order of the PV
-                                         // operand, position 8j + 4b + s holding key 16b + 4j + s, so a lane's eight
-                                         // keys are one 16-byte read (at this pitch without LDS bank conflicts)
 template <int F>
 constexpr int kKTile = kMSteps * kKRow<F> * 2;
-constexpr int kVTile = kDl * kVRow * 2;
 template <int F>
 constexpr int kQChunks = kDk<F> / 32;    // 32-dim chunks of a query row
 template <int F>
@@ -177,15 +173,14 @@ __device__ inline void load_raw(const MlaArgs& a, const int32_t* slots, int step
   }
 }
 
-// Raw records -> K and V^T tiles. An invalid key's value becomes 0 (so P * V stays finite whatever slot 0 holds);
-// an NVFP4 key's rope is left as read: its score is masked by a select, never multiplied.
+// Raw records -> the K tile (the value operand is read from it transposed). An invalid key's value becomes 0 (so
+// P * V stays finite whatever slot 0 holds); an NVFP4 key's rope is left as read: its score is masked by a select,
+// never multiplied.
 template <int F, bool TWO>
 __device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step, const Raw<F>& r, float g0, float g1,
-                               uint16_t* kt, uint16_t* vt) {
-  typedef short short4_t __attribute__((ext_vector_type(4)));
+                               uint16_t* kt) {
   const int t = threadIdx.x, kq = t & 7, c = t >> 3;
   if constexpr (F == kFp8V4) {
-    short8_t vals[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const bool ok = entry_valid(slots[step * kMSteps + 4 * kq + i]);
@@ -203,17 +198,10 @@ __device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step,
       } else {
         w = ok ? r.d[i] : uint4{0u, 0u, 0u, 0u};
       }
-      vals[i] = __builtin_bit_cast(short8_t, w);
-      *reinterpret_cast<short8_t*>(kt + (4 * kq + i) * kKRow<F> + 8 * c) = vals[i];
+      *reinterpret_cast<uint4*>(kt + (4 * kq + i) * kKRow<F> + 8 * c) = w;
     }
-#pragma unroll
-    for (int d = 0; d < 8; ++d)
-      *reinterpret_cast<short4_t*>(vt + (8 * c + d) * kVRow + 8 * (kq & 3) + 4 * (kq >> 2)) =
-          short4_t{vals[0][d], vals[1][d], vals[2][d], vals[3][d]};
     return;
   } else {
-  typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-  half8_t vals[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int32_t e = slots[step * kMSteps + 4 * kq + i];
@@ -223,13 +211,9 @@ __device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step,
     const half2_t s2 = half2_t{h, h};
     const half2_t p0 = fp4x2_to_f16<0>(r.pay[i]) * s2, p1 = fp4x2_to_f16<1>(r.pay[i]) * s2;
     const half2_t p2 = fp4x2_to_f16<2>(r.pay[i]) * s2, p3 = fp4x2_to_f16<3>(r.pay[i]) * s2;
-    vals[i] = half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
-    *reinterpret_cast<half8_t*>(kt + (4 * kq + i) * kKRow<F> + 8 * c) = vals[i];
+    *reinterpret_cast<half8_t*>(kt + (4 * kq + i) * kKRow<F> + 8 * c) =
+        half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
   }
-#pragma unroll
-  for (int d = 0; d < 8; ++d)
-    *reinterpret_cast<half4_t*>(vt + (8 * c + d) * kVRow + 8 * (kq & 3) + 4 * (kq >> 2)) =
-        half4_t{vals[0][d], vals[1][d], vals[2][d], vals[3][d]};
   if (t < 256) {
     const int key = t >> 3, p = t & 7;
     const uint32_t w[4] = {r.rope.x, r.rope.y, r.rope.z, r.rope.w};
@@ -276,10 +260,10 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
   const int head = 16 * wave + hl;
   const bool head_live = head < a.heads;
 
-  uint16_t* kt = reinterpret_cast<uint16_t*>(lds);
-  uint16_t* vt = reinterpret_cast<uint16_t*>(lds + kKTile<F>);
-  uint16_t* qs = reinterpret_cast<uint16_t*>(lds + kKTile<F> + kVTile);
-  int32_t* slots = reinterpret_cast<int32_t*>(lds + kKTile<F> + kVTile + kQTile<F>);
+  // two K tiles: step n computes on tile n % 2 while the next step's keys are dequantized into the other
+  uint16_t* ktiles = reinterpret_cast<uint16_t*>(lds);
+  uint16_t* qs = reinterpret_cast<uint16_t*>(lds + 2 * kKTile<F>);
+  int32_t* slots = reinterpret_cast<int32_t*>(lds + 2 * kKTile<F> + kQTile<F>);
 
   // the query's B operands first: dims 32kk + 8j .. +7 of head `head` (a clamped valid head for padding lanes)
   uint4 qraw[kQC];
@@ -346,10 +330,17 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
 
   Raw<F> raw;
   load_raw<F, TWO>(a, slots, 0, raw);
+  dequant<F, TWO>(a, slots, 0, raw, g0, g1, ktiles);
+  if (a.steps > 1) load_raw<F, TWO>(a, slots, 1, raw);
+  __syncthreads();
   for (int step = 0; step < a.steps; ++step) {
-    dequant<F, TWO>(a, slots, step, raw, g0, g1, kt, vt);
-    __syncthreads();
-    if (step + 1 < a.steps) load_raw<F, TWO>(a, slots, step + 1, raw);
+    const uint16_t* kt = ktiles + (step & 1) * (kKTile<F> / 2);
+    // the next step's keys into the other tile (its readers finished before the previous barrier), then its
+    // successor's raw records
+    if (step + 1 < a.steps) {
+      dequant<F, TWO>(a, slots, step + 1, raw, g0, g1, ktiles + ((step + 1) & 1) * (kKTile<F> / 2));
+      if (step + 2 < a.steps) load_raw<F, TWO>(a, slots, step + 2, raw);
+    }
     const uint32_t valid = (uint32_t)__builtin_amdgcn_ballot_w64(lane < kMSteps &&
                                                                   entry_valid(slots[step * kMSteps + (lane & 31)]));
     // S^T for the two 16-key tiles, each as two independent MFMA chains (even / odd dim chunks)
@@ -406,10 +397,18 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
         pb[e] = __builtin_bit_cast(short, (__bf16)p);
     }
     l += psum;
-    // O^T += V^T . P^T over the 32 dim tiles
+    // O^T += V^T . P^T over the 32 dim tiles, V^T read from the K tile with transposing reads: in each 16-lane group
+    // lane L addresses key 4j + L/4, dims 16 dt + 4 (L % 4) .. +3, and lane i receives dim 16 dt + i of keys 4j .. 4j+3
+    // (then 16 + 4j .. from 16 rows further)
+    typedef short short4_t __attribute__((ext_vector_type(4)));
+    const uint16_t* vr = kt + (4 * j + (hl >> 2)) * kKRow<F> + 4 * (hl & 3);
 #pragma unroll
     for (int dt = 0; dt < 32; ++dt) {
-      const short8_t av = *reinterpret_cast<const short8_t*>(vt + (16 * dt + hl) * kVRow + 8 * j);
+      const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) short4_t*)(vr + 16 * dt));
+      const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) short4_t*)(vr + 16 * kKRow<F> + 16 * dt));
+      const short8_t av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       acc[dt] = mfma16<F>(av, pb, acc[dt]);
     }
     __syncthreads();
@@ -578,7 +577,7 @@ int mla_launch(const char* what, MlaArgs& a, bool extra, const void* q, int64_t 
     a.keys_per_split = kMSteps;   // no keys: one all-invalid step writes the zero rows
     a.steps = 1;
   }
-  const size_t lds_bytes = (size_t)kKTile<F> + kVTile + kQTile<F> + (size_t)a.steps * kMSteps * 4;
+  const size_t lds_bytes = (size_t)2 * kKTile<F> + kQTile<F> + (size_t)a.steps * kMSteps * 4;
   if (lds_bytes > 160 * 1024 - 256)
     return fail(XT_EUNSUPPORTED, "%s: %d keys per split need %zu bytes of LDS; use more splits", what,
                 a.keys_per_split, lds_bytes);
