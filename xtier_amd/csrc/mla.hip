@@ -276,7 +276,7 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
   // 1. the split's key list: columns [t0, t0 + keys_per_split) of list 0 then list 1, as slot entries in LDS
   const int t0 = split * a.keys_per_split;
   {
-    const int total = a.steps * kMSteps;
+    const int total = (a.steps + 1) * kMSteps;   // one padding step of invalid keys
     for (int i = threadIdx.x; i < total; i += 512) {
       const int col = t0 + i;
       int32_t e = -1;
@@ -335,12 +335,11 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
   __syncthreads();
   for (int step = 0; step < a.steps; ++step) {
     const uint16_t* kt = ktiles + (step & 1) * (kKTile<F> / 2);
-    // the next step's keys into the other tile (its readers finished before the previous barrier), then its
-    // successor's raw records
-    if (step + 1 < a.steps) {
-      dequant<F, TWO>(a, slots, step + 1, raw, g0, g1, ktiles + ((step + 1) & 1) * (kKTile<F> / 2));
-      if (step + 2 < a.steps) load_raw<F, TWO>(a, slots, step + 2, raw);
-    }
+    // the next step's keys into the other tile (its readers finished before the previous barrier; after the last step
+    // it is the padding step, all zeros, never read), then the raw records of the step after (the last one again at
+    // the end): no branch, so the compiler can interleave this VALU work with the MFMAs below
+    dequant<F, TWO>(a, slots, step + 1, raw, g0, g1, ktiles + ((step + 1) & 1) * (kKTile<F> / 2));
+    load_raw<F, TWO>(a, slots, min(step + 2, a.steps - 1), raw);
     const uint32_t valid = (uint32_t)__builtin_amdgcn_ballot_w64(lane < kMSteps &&
                                                                   entry_valid(slots[step * kMSteps + (lane & 31)]));
     // S^T for the two 16-key tiles, each as two independent MFMA chains (even / odd dim chunks)
@@ -577,7 +576,7 @@ int mla_launch(const char* what, MlaArgs& a, bool extra, const void* q, int64_t 
     a.keys_per_split = kMSteps;   // no keys: one all-invalid step writes the zero rows
     a.steps = 1;
   }
-  const size_t lds_bytes = (size_t)2 * kKTile<F> + kQTile<F> + (size_t)a.steps * kMSteps * 4;
+  const size_t lds_bytes = (size_t)2 * kKTile<F> + kQTile<F> + (size_t)(a.steps + 1) * kMSteps * 4;
   if (lds_bytes > 160 * 1024 - 256)
     return fail(XT_EUNSUPPORTED, "%s: %d keys per split need %zu bytes of LDS; use more splits", what,
                 a.keys_per_split, lds_bytes);
