@@ -42,15 +42,19 @@ constexpr int kDk = F == kNvfp4 ? kDl + kDr : kDl;   // key width
 constexpr int kMSteps = 32;              // keys per step
 constexpr int kMWaves = 8;
 constexpr int kMHeads = 16 * kMWaves;    // heads per workgroup
+// Row pitches of the LDS tiles, measured with SQ_LDS_BANK_CONFLICT (gfx950 LDS: 64 banks; b128 reads served 16 lanes
+// per cycle, b64 32): a K pitch of 32 mod 64 bytes (1184 / 1056) makes both the QK reads (16 key rows x 4 column
+// quarters, b128) and the transposing value reads (16 key rows x 4 dim groups, b64) conflict-free, as a query pitch
+// of 96 bytes does for the LDS query reads.
 template <int F>
-constexpr int kKRow = kDk<F> + 8;        // 16-bit values per K tile row (16-byte pad)
+constexpr int kKRow = kDk<F> + 16;       // 16-bit values per K tile row
 template <int F>
 constexpr int kKTile = kMSteps * kKRow<F> * 2;
 template <int F>
 constexpr int kQChunks = kDk<F> / 32;    // 32-dim chunks of a query row
 template <int F>
 constexpr int kQReg = F == kNvfp4 ? 12 : 10;   // chunks kept in registers; the others live in LDS
-constexpr int kQRow = 32 + 8;            // halves per (chunk, head) row of the LDS query block
+constexpr int kQRow = 32 + 16;           // 16-bit values per (chunk, head) row of the LDS query block
 template <int F>
 constexpr int kQTile = (kQChunks<F> - kQReg<F>) * kMHeads * kQRow * 2;
 constexpr int kRescaleM = 8;
