@@ -148,6 +148,36 @@ int xt_block_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_
                                  void* out, int64_t out_row_stride, int64_t out_head_stride, int out_dtype, float* lse,
                                  int rows, int splits, void* workspace, size_t workspace_bytes, xt_stream_t stream);
 
+/* Block-sparse NVFP4 prefill over head-major pages (replaces xtier/packs/minimax_m3/kv_fp4.py:293-366 and :369-404,
+ * fp4_prefill_gqa_share_sparse, behind the hook _prefill_main :593-598). Pages, kv_scale and outputs as
+ * xt_block_sparse_decode_nvfp4; one row per query token: row r reads request row_req[r] (int64), its block list
+ * topk_idx[h * idx_head_stride + row_idx[r] * idx_row_stride + i] (row_idx: the query block of the row), and attends
+ * to positions c = id * block_size .. + block_size - 1 below row_seq_lens[r] and at most row_query_pos[r] (causal,
+ * kv_fp4.py:330-331, :345), each resolved through its own req_to_token entry (:338-340). */
+int xt_block_sparse_prefill_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, const uint8_t* k_pay,
+                                  const uint8_t* v_pay, const uint8_t* k_scales, const uint8_t* v_scales,
+                                  float kv_scale, int64_t pages, int kv_heads, int q_heads, int dim, int block_size,
+                                  int64_t page_stride, int64_t head_stride, int64_t row_stride,
+                                  int64_t sf_page_stride, int64_t sf_head_stride, int64_t sf_row_stride,
+                                  const int32_t* req_to_token, int64_t req_stride, const int64_t* row_req,
+                                  const int32_t* row_seq_lens, const int32_t* row_query_pos, const int32_t* topk_idx,
+                                  int64_t idx_head_stride, int64_t idx_row_stride, int topk_blocks,
+                                  const int32_t* row_idx, float sm_scale, void* out, int64_t out_row_stride,
+                                  int64_t out_head_stride, int out_dtype, float* lse, int rows, int splits,
+                                  void* workspace, size_t workspace_bytes, xt_stream_t stream);
+
+/* BF16 copy of each request's context from head-major NVFP4 pages (replaces kv_fp4.py:496-530, dequantize_context):
+ * for request b < batch and position pos < min(seq_lens[b], rows_per_req), token slot
+ * s = req_to_token[sid * req_stride + pos] (sid = slot_ids[b]; both wrapped into [0, pages * block_size) as the
+ * reference wraps them) -> out[b * rows_per_req + pos, h, :] (BF16 [batch * rows_per_req, heads, dim], contiguous)
+ * = e2m1 * e4m3 of page s / block_size, row s % block_size (unit global scale, exact in BF16); other rows are left as
+ * they are. Strides as xt_block_sparse_decode_nvfp4 (head strides may be 0 for the one-head index cache). */
+int xt_dequantize_context_nvfp4(const uint8_t* pay, const uint8_t* scales, int64_t pages, int heads, int dim,
+                                int block_size, int64_t page_stride, int64_t head_stride, int64_t row_stride,
+                                int64_t sf_page_stride, int64_t sf_head_stride, int64_t sf_row_stride,
+                                const int32_t* req_to_token, int64_t req_stride, const int64_t* slot_ids,
+                                const int32_t* seq_lens, int batch, int rows_per_req, void* out, xt_stream_t stream);
+
 /* --- split-K decode over packed BF16 rows ------------------------------------------------------------------------ */
 
 /* Device workspace of xt_varlen_decode_bf16 for `rows` rows, `heads` query heads of size dim and `splits` key splits

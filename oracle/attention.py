@@ -1,5 +1,6 @@
 """Sparse attention over an NVFP4 paged KV pool, on the CPU (numpy): the oracle for the gather, the fused decode,
-the split-K merge, the chunked prefill, the block-sparse decode over head-major pages and sparse MLA.
+the split-K merge, the chunked prefill, the block-sparse decode and prefill over head-major pages, the BF16 context
+copy of such pages and sparse MLA.
 
 Test infrastructure only. Conventions (reference: qsa_fp4.py:131-140; sparse_mla.py:42-46; qsa_decode.py:75, :83):
 an index is valid when it is >= 0 and below the row's length (and, for a causal query, not after the query's own
@@ -256,6 +257,64 @@ def block_sparse_decode(q, k_pay, k_sf, v_pay, v_sf, req_to_token, slot_ids, top
 
 
 # --- sparse MLA ---------------------------------------------------------------------------------------------------
+
+def block_sparse_prefill(q, k_pay, k_sf, v_pay, v_sf, req_to_token, slot_ids, topk_idx, cu_seqlens, cu_seqblocks,
+                         seq_lens, prefix_lens, block_size_q, block_size, scale, kv_scale=1.0, attend=None):
+    """kv_fp4.py:293-366 (the causal block-sparse prefill), reference values. q [total_q, Hq, D]; request b's queries
+    are rows cu_seqlens[b] .. cu_seqlens[b+1]-1, query i at position prefix_lens[b] + i (:330-331) with the block list
+    topk_idx[h, cu_seqblocks[b] + i // block_size_q] (:321); the first (number of ids >= 0) entries are read
+    (:323-324, :336). Block id e names positions c = e * block .. c + block - 1 that are below seq_lens[b] (:340) and
+    at most the query's position (:345); each position's slot s = req_to_token[sid, pos] (sid = slot_ids[b]; both
+    wrapped into [0, pages * block), :313, :341-342) is page s // block, row s % block (:272-273). Pages and kv_scale
+    as block_sparse_decode. Returns float64 [total_q, Hq, D] (0 for a (query, head) without keys)."""
+    attend = attend or softmax_attention
+    q = np.asarray(q)
+    total, hq, d = q.shape
+    hkv = k_pay.shape[1]
+    group = hq // hkv
+    max_slots = k_pay.shape[0] * block_size
+    out = np.zeros((total, hq, d))
+    for b in range(len(cu_seqlens) - 1):
+        sid = int(slot_ids[b]) % max_slots
+        for i in range(int(cu_seqlens[b + 1]) - int(cu_seqlens[b])):
+            r = int(cu_seqlens[b]) + i
+            qpos = int(prefix_lens[b]) + i
+            limit = min(int(seq_lens[b]), qpos + 1)
+            for h in range(hkv):
+                ids = np.asarray(topk_idx[h, int(cu_seqblocks[b]) + i // block_size_q], dtype=np.int64)
+                ids = ids[:int((ids >= 0).sum())]
+                pos = (ids[ids >= 0, None] * block_size + np.arange(block_size)).ravel()
+                pos = pos[pos < limit]
+                if pos.size == 0:
+                    continue
+                slot = np.asarray(req_to_token[sid, pos], dtype=np.int64) % max_slots
+                pg, rw = slot // block_size, slot % block_size
+                k = nvfp4.dequant(k_pay[pg, h, rw], k_sf[pg, h, rw])[:, None]
+                v = nvfp4.dequant(v_pay[pg, h, rw], v_sf[pg, h, rw])[:, None]
+                qs = q[r, h * group:(h + 1) * group]
+                out[r, h * group:(h + 1) * group] = attend(qs, k, v, np.ones(pos.size, bool), scale * kv_scale) \
+                    * kv_scale
+    return out
+
+
+def dequantize_context(pay, sf, req_to_token, slot_ids, seq_lens, rows_per_req):
+    """kv_fp4.py:496-530: request b's positions pos < min(seq_lens[b], rows_per_req) as FP32 rows b * rows_per_req +
+    pos of [batch * rows_per_req, heads, D] (other rows NaN: the reference leaves them unwritten); token slot
+    s = req_to_token[sid, pos] (sid, s wrapped into [0, pages * block)) at page s // block, row s % block of pay / sf
+    [pages, heads, block, D/2 | D/16] ([pages, block, ...]: one head)."""
+    if pay.ndim == 3:
+        pay, sf = pay[:, None], sf[:, None]
+    pages, heads, block, half = pay.shape
+    max_slots = pages * block
+    out = np.full((len(slot_ids) * rows_per_req, heads, 2 * half), np.nan, dtype=np.float32)
+    for b, sid in enumerate(slot_ids):
+        n = min(int(seq_lens[b]), rows_per_req)
+        slot = np.asarray(req_to_token[int(sid) % max_slots, :n], dtype=np.int64) % max_slots
+        pg, rw = slot // block, slot % block
+        for h in range(heads):
+            out[b * rows_per_req:b * rows_per_req + n, h] = nvfp4.dequant(pay[pg, h, rw], sf[pg, h, rw])
+    return out
+
 
 def sparse_mla(q, latent_pay, latent_sf, rope, g, indices, topk_length, sink, scale, dtype=np.float64, extra=None):
     """Sparse MLA over an NVFP4 latent + BF16 rope cache, reference values (the FP64 reference of

@@ -41,7 +41,13 @@ def test_attach_scales_and_install():
     seen = []
     registry = SimpleNamespace(register=lambda name, fn, kind: seen.append((name, fn, kind)))
     minimax.install(registry, SimpleNamespace(AROUND='around'))
-    assert seen == [(f'{minimax.OPS}.flash_decode_with_gqa_share_sparse', minimax.decode_main, 'around')]
+    assert seen == [(f'{minimax.OPS}.flash_decode_with_gqa_share_sparse', minimax.decode_main, 'around'),
+                    (f'{minimax.OPS}.flash_prefill_with_gqa_share_sparse', minimax.prefill_main, 'around'),
+                    (f'{minimax.OPS}.minimax_sparse_prefill', minimax.sparse_prefill, 'around')]
+    # caches without scale bytes fall through
+    assert minimax.prefill_main(_original, k_cache=torch.zeros(1))[0] == 'original'
+    got = minimax.sparse_prefill(_original, *range(16), flag=1)
+    assert got[0] == 'original' and got[1] == tuple(range(16)) and got[2] == {'flag': 1}
 
 
 def test_deepseek_hook_falls_through_and_installs():

@@ -253,6 +253,113 @@ def test_block_decode_clamps_length_to_the_table_and_skips_blocks_past_it():
     np.testing.assert_array_equal(a, b)
 
 
+def _prefill_case(seed, kh=2, group=4, d=32, block=64, pages=12, q_lens=(70, 1, 33), prefix=(90, 300, 0),
+                  bq=16, topk=4):
+    """Head-major pages, a token-granular req_to_token whose positions sit on arbitrary slots (no block alignment),
+    and per-(KV head, query block) lists of distinct block ids padded with -1."""
+    rng = np.random.default_rng(seed)
+    k_pay = rng.integers(0, 256, (pages, kh, block, d // 2), dtype=np.uint8)
+    v_pay = rng.integers(0, 256, (pages, kh, block, d // 2), dtype=np.uint8)
+    k_sf = rng.integers(0x20, 0x48, (pages, kh, block, d // 16), dtype=np.uint8)
+    v_sf = rng.integers(0x20, 0x48, (pages, kh, block, d // 16), dtype=np.uint8)
+    b = len(q_lens)
+    seq = np.array([p + n for p, n in zip(prefix, q_lens)], dtype=np.int32)
+    ctx = int(seq.max())
+    r2t = np.stack([rng.permutation(pages * block)[:ctx] for _ in range(b)]).astype(np.int32)
+    cu = np.concatenate([[0], np.cumsum(q_lens)])
+    nqb = [-(-n // bq) for n in q_lens]
+    cu_blk = np.concatenate([[0], np.cumsum(nqb)])
+    ids = np.full((kh, cu_blk[-1], topk), -1, dtype=np.int32)
+    for h in range(kh):
+        for bb in range(b):
+            nb = -(-int(seq[bb]) // block)
+            for j in range(nqb[bb]):
+                n = min(topk, nb) - (j + h) % 2
+                ids[h, cu_blk[bb] + j, :n] = rng.permutation(nb)[:n]
+    q = rng.standard_normal((cu[-1], kh * group, d))
+    return q, (k_pay, k_sf, v_pay, v_sf), r2t, np.roll(np.arange(b), 1), ids, cu, cu_blk, seq, np.array(prefix[:b])
+
+
+def test_block_prefill_equals_token_decode_on_the_expanded_lists():
+    """kv_fp4.py's causal block-sparse prefill equals the token-granular oracle (pinned against torch) given, per query,
+    its block list expanded to positions with the query's position as the causal limit; slots come from per-token
+    lookups, so tokens need not sit on their block's page."""
+    block, scale, kv_scale, bq = 64, 0.3, 0.5, 16
+    q, (k_pay, k_sf, v_pay, v_sf), r2t, sid, ids, cu, cu_blk, seq, prefix = _prefill_case(5, bq=bq)
+    out = attention.block_sparse_prefill(q, k_pay, k_sf, v_pay, v_sf, r2t, sid, ids, cu, cu_blk, seq, prefix, bq, block,
+                                         scale, kv_scale)
+    kh = k_pay.shape[1]
+    group = q.shape[1] // kh
+    tok = lambda a: a.transpose(0, 2, 1, 3).reshape(-1, kh, a.shape[-1])
+    rows = np.repeat(sid, np.diff(cu))
+    local = np.arange(cu[-1]) - np.repeat(cu[:-1], np.diff(cu))
+    qpos = np.repeat(prefix, np.diff(cu)) + local
+    blk = np.repeat(cu_blk[:-1], np.diff(cu)) + local // bq
+    for h in range(kh):
+        pool = (tok(k_pay)[:, h:h + 1], tok(v_pay)[:, h:h + 1], tok(k_sf)[:, h:h + 1], tok(v_sf)[:, h:h + 1],
+                kv_scale, kv_scale)
+        lists = ids[h][blk].astype(np.int64)
+        pos = np.where(np.repeat(lists >= 0, block, axis=1),
+                       (lists[:, :, None] * block + np.arange(block)).reshape(len(blk), -1), -1)
+        ref = attention.sparse_decode(q[:, h * group:(h + 1) * group], pool, r2t, 1, rows, pos, None,
+                                      np.repeat(seq, np.diff(cu)), scale, query_pos=qpos)
+        np.testing.assert_allclose(out[:, h * group:(h + 1) * group], ref, rtol=1e-12, atol=1e-12)
+    # a query whose only block lies in its future has no key: 0
+    ids2 = ids.copy()
+    ids2[:, 0] = -1
+    ids2[:, 0, 0] = 5                           # block 5 (positions 320..383) > every position of query block 0
+    out2 = attention.block_sparse_prefill(q, k_pay, k_sf, v_pay, v_sf, r2t, sid, ids2, cu, cu_blk, seq, prefix, bq,
+                                          block, scale)
+    assert np.all(out2[:bq] == 0)
+
+
+def test_block_prefill_with_every_block_is_dense_causal_attention():
+    """With every block of the context listed, each query attends to exactly positions 0 .. its own: dense causal
+    attention over the dequantized context (the BF16 copy path of kv_fp4.py:601-629 gives the same)."""
+    block, scale, bq = 64, 0.25, 1
+    q, pool, r2t, sid, _, cu, _, seq, prefix = _prefill_case(8, q_lens=(40, 3), prefix=(100, 200), bq=bq)
+    k_pay, k_sf, v_pay, v_sf = pool
+    kh = k_pay.shape[1]
+    nb = -(-int(seq.max()) // block)
+    cu_blk = cu.copy()
+    ids = np.tile(np.arange(nb, dtype=np.int32)[::-1], (kh, cu[-1], 1))          # every block, in reverse order
+    out = attention.block_sparse_prefill(q, *pool, r2t, sid, ids, cu, cu_blk, seq, prefix, bq, block, scale)
+    rows = 256
+    kd = attention.dequantize_context(k_pay, k_sf, r2t, sid, seq, rows)
+    vd = attention.dequantize_context(v_pay, v_sf, r2t, sid, seq, rows)
+    group = q.shape[1] // kh
+    for b in range(len(sid)):
+        for i in range(cu[b + 1] - cu[b]):
+            n = int(prefix[b]) + i + 1
+            k, v = kd[b * rows:b * rows + n], vd[b * rows:b * rows + n]
+            for h in range(kh):
+                qs = q[cu[b] + i, h * group:(h + 1) * group]
+                s = qs @ k[:, h].astype(np.float64).T * scale
+                p = np.exp(s - s.max(1, keepdims=True))
+                want = (p / p.sum(1, keepdims=True)) @ v[:, h].astype(np.float64)
+                np.testing.assert_allclose(out[cu[b] + i, h * group:(h + 1) * group], want, rtol=1e-10, atol=1e-12)
+
+
+def test_dequantize_context_copies_each_position_from_its_slot():
+    """kv_fp4.py:496-530: row b * rows_per_req + pos holds the token at slot req_to_token[sid, pos] (page s // block,
+    row s % block), decoded by the NVFP4 dequantizer; rows at or past seq_lens[b] stay unwritten; the index cache
+    (no head dimension) alike; slot ids past the table wrap modulo the pool size."""
+    _, (k_pay, k_sf, _, _), r2t, sid, _, _, _, seq, _ = _prefill_case(11)
+    pages, kh, block, half = k_pay.shape
+    rows = 448
+    out = attention.dequantize_context(k_pay, k_sf, r2t, sid, seq, rows)
+    assert out.shape == (len(sid) * rows, kh, 2 * half)
+    for b in range(len(sid)):
+        for pos in (0, int(seq[b]) - 1):
+            s = int(r2t[sid[b], pos])
+            np.testing.assert_array_equal(out[b * rows + pos],
+                                          nvfp4.dequant(k_pay[s // block, :, s % block], k_sf[s // block, :, s % block]))
+        assert np.isnan(out[b * rows + int(seq[b]):(b + 1) * rows]).all()
+        assert not np.isnan(out[b * rows:b * rows + int(seq[b])]).any()
+    one = attention.dequantize_context(k_pay[:, 1], k_sf[:, 1], r2t, sid + pages * block, seq, rows)
+    np.testing.assert_array_equal(one[:, 0], out[:, 1])
+
+
 def test_varlen_split_form_equals_one_pass_softmax():
     """qsa_decode.py's split/merge form (128-key splits) equals the one-pass softmax per row; an empty row is 0."""
     rng = np.random.default_rng(9)

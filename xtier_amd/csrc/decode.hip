@@ -69,6 +69,9 @@ struct DecodeArgs {
   int64_t idx_stride;
   int64_t idx_head_stride;           // elements between the index lists of consecutive KV heads (0: one shared list)
   int block_shift;                   // an index names 2^block_shift consecutive positions (0: one token)
+  int lookup_mask;                   // positions resolve through the table entry of (pos & ~lookup_mask): the block's
+                                     // first position (block decode) or every position (0)
+  const int32_t* idx_rows;           // per row, the index row to read (NULL: the row itself)
   int max_len;                       // sequence lengths are clamped to this
   int topk;                          // keys per row (index entries << block_shift)
   const int32_t* counts;
@@ -300,7 +303,8 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   // constants), so the chain to the first K/V load is two dependent loads: index, then table.
   const int t0 = split * a.keys_per_split;
   const int kmax = max(0, min(a.keys_per_split, a.topk - t0));
-  const int32_t* ip = a.indices + (int64_t)row * a.idx_stride + (int64_t)kvg * a.idx_head_stride;
+  const int64_t irow = a.idx_rows ? scalar_load(a.idx_rows + row) : row;
+  const int32_t* ip = a.indices + irow * a.idx_stride + (int64_t)kvg * a.idx_head_stride;
   const int bmask = (1 << a.block_shift) - 1;
   int32_t pos[kSlotBatch];
 #pragma unroll
@@ -337,7 +341,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
       for (int b = 0; b < kSlotBatch; ++b) {
         const int i = i0 + b * 512 + (int)threadIdx.x;
         ok[b] = i < n && pos[b] >= 0 && pos[b] < seqlen && pos[b] <= qpos;
-        const int32_t tpos = pos[b] & ~bmask;   // a block's slots follow the slot of its first position
+        const int32_t tpos = pos[b] & ~a.lookup_mask;   // block decode: a block's slots follow its first position's
         toff[b] = a.page_shift >= 0 ? (tpos >> a.page_shift) : tpos / a.page_size;
       }
 #pragma unroll
@@ -547,6 +551,8 @@ struct Addressing {
   int64_t remap_mul;
   int64_t idx_head_stride;                   // per-KV-head index lists (0: shared; forces 1 KV head per workgroup)
   int block_shift;                           // an index entry names 2^block_shift positions
+  bool token_lookup;                         // resolve every position through the table (else the block start)
+  const int32_t* idx_rows;                   // per-row index row (NULL: the row)
   int max_len;                               // sequence lengths clamped to this
   bool scalar_scales;                        // gk / gv NULL: the scores and outputs use gk_val / gv_val
   float gk_val, gv_val;
@@ -590,11 +596,38 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
                 (long long)pay_stride, (long long)sf_stride);
   if (pool_slots <= 0 || pool_slots > 0x7FFFFFFFLL)
     return fail(XT_EINVAL, "%s: pool_slots %lld outside 1..2^31-1", what, (long long)pool_slots);
-  const Addressing ad{dim / 2, dim / 16, 0, 1, 0, 0, 0x7FFFFFFF, false, 0.0f, 0.0f};
+  const Addressing ad{dim / 2, dim / 16, 0, 1, 0, 0, true, nullptr, 0x7FFFFFFF, false, 0.0f, 0.0f};
   return decode_impl(what, q, q_row_stride, q_head_stride, k_pay, v_pay, k_scales, v_scales, gk, gv, pool_slots,
                      pay_stride, sf_stride, kv_heads, q_heads, table, table_stride, page_size, row_req, indices,
                      idx_stride, topk, counts, seq_lens, query_pos, scale, out, out_row_stride, out_head_stride,
                      out_dtype, lse, rows, splits, workspace, workspace_bytes, ad, stream);
+}
+
+// The head-major page checks shared by the block decode and the block prefill; fills the page-row remap.
+static int block_pages(const char* what, int64_t pages, int kv_heads, int dim, int block_size, int64_t page_stride,
+                       int64_t head_stride, int64_t row_stride, int64_t sf_page_stride, int64_t sf_head_stride,
+                       int64_t sf_row_stride, int topk_blocks, int64_t* mul) {
+  if (dim != kDim) return fail(XT_EUNSUPPORTED, "%s: head size %d (supported: %d)", what, dim, kDim);
+  if (block_size <= 0 || (block_size & (block_size - 1)) || block_size > 4096)
+    return fail(XT_EINVAL, "%s: block_size %d must be a power of 2 up to 4096", what, block_size);
+  if (kv_heads <= 0 || pages <= 0 || topk_blocks < 0)
+    return fail(XT_EINVAL, "%s: bad kv_heads / pages / topk", what);
+  if (row_stride < dim / 2 || sf_row_stride < dim / 16 || row_stride % 16 || sf_row_stride % 4 || head_stride % 16 ||
+      sf_head_stride % 4 || page_stride % row_stride || sf_page_stride % sf_row_stride ||
+      page_stride / row_stride != sf_page_stride / sf_row_stride || page_stride / row_stride < block_size ||
+      head_stride < (int64_t)block_size * row_stride - row_stride + dim / 2 ||
+      sf_head_stride < (int64_t)block_size * sf_row_stride - sf_row_stride + dim / 16 ||
+      page_stride < (int64_t)(kv_heads - 1) * head_stride + (int64_t)block_size * row_stride)
+    return fail(XT_EINVAL, "%s: pool strides (page %lld, head %lld, row %lld; scales %lld, %lld, %lld bytes) do not "
+                "describe [pages, kv_heads, %d, dim/2] / [.., dim/16] pages", what, (long long)page_stride,
+                (long long)head_stride, (long long)row_stride, (long long)sf_page_stride, (long long)sf_head_stride,
+                (long long)sf_row_stride, block_size);
+  *mul = page_stride / row_stride;
+  if (pages > 0x7FFFFFFFLL / *mul)
+    return fail(XT_EUNSUPPORTED, "%s: %lld pages exceed 2^31 rows", what, (long long)pages);
+  if ((int64_t)topk_blocks * block_size > 0x7FFFFFFFLL)
+    return fail(XT_EUNSUPPORTED, "%s: %d blocks of %d keys", what, topk_blocks, block_size);
+  return XT_OK;
 }
 
 extern "C" int xt_block_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride,
@@ -611,34 +644,50 @@ extern "C" int xt_block_sparse_decode_nvfp4(const void* q, int64_t q_row_stride,
                                             float* lse, int rows, int splits, void* workspace,
                                             size_t workspace_bytes, xt_stream_t stream) {
   const char* what = "xt_block_sparse_decode_nvfp4";
-  if (dim != kDim) return fail(XT_EUNSUPPORTED, "%s: head size %d (supported: %d)", what, dim, kDim);
-  if (block_size <= 0 || (block_size & (block_size - 1)) || block_size > 4096)
-    return fail(XT_EINVAL, "%s: block_size %d must be a power of 2 up to 4096", what, block_size);
-  if (kv_heads <= 0 || pages <= 0 || topk_blocks < 0 || max_kv_len < 0)
-    return fail(XT_EINVAL, "%s: bad kv_heads / pages / topk / max_kv_len", what);
-  if (row_stride < dim / 2 || sf_row_stride < dim / 16 || row_stride % 16 || sf_row_stride % 4 || head_stride % 16 ||
-      sf_head_stride % 4 || page_stride % row_stride || sf_page_stride % sf_row_stride ||
-      page_stride / row_stride != sf_page_stride / sf_row_stride || page_stride / row_stride < block_size ||
-      head_stride < (int64_t)block_size * row_stride - row_stride + dim / 2 ||
-      sf_head_stride < (int64_t)block_size * sf_row_stride - sf_row_stride + dim / 16 ||
-      page_stride < (int64_t)(kv_heads - 1) * head_stride + (int64_t)block_size * row_stride)
-    return fail(XT_EINVAL, "%s: pool strides (page %lld, head %lld, row %lld; scales %lld, %lld, %lld bytes) do not "
-                "describe [pages, kv_heads, %d, dim/2] / [.., dim/16] pages", what, (long long)page_stride,
-                (long long)head_stride, (long long)row_stride, (long long)sf_page_stride, (long long)sf_head_stride,
-                (long long)sf_row_stride, block_size);
-  const int64_t mul = page_stride / row_stride;
-  if (pages > 0x7FFFFFFFLL / mul) return fail(XT_EUNSUPPORTED, "%s: %lld pages exceed 2^31 rows", what, (long long)pages);
-  if ((int64_t)topk_blocks * block_size > 0x7FFFFFFFLL)
-    return fail(XT_EUNSUPPORTED, "%s: %d blocks of %d keys", what, topk_blocks, block_size);
+  int64_t mul;
+  const int st = block_pages(what, pages, kv_heads, dim, block_size, page_stride, head_stride, row_stride,
+                             sf_page_stride, sf_head_stride, sf_row_stride, topk_blocks, &mul);
+  if (st != XT_OK) return st;
+  if (max_kv_len < 0) return fail(XT_EINVAL, "%s: max_kv_len %d", what, max_kv_len);
   if (!slot_ids) return fail(XT_EINVAL, "%s: slot_ids is null", what);
   const int shift = __builtin_ctz((unsigned)block_size);
-  const Addressing ad{head_stride, sf_head_stride, shift, mul, idx_head_stride, shift, max_kv_len, true, kv_scale,
-                      kv_scale};
+  const Addressing ad{head_stride, sf_head_stride, shift, mul, idx_head_stride, shift, false, nullptr, max_kv_len, true,
+                      kv_scale, kv_scale};
   return decode_impl(what, q, q_row_stride, q_head_stride, k_pay, v_pay, k_scales, v_scales, nullptr, nullptr,
                      pages * mul, row_stride, sf_row_stride, kv_heads, q_heads, req_to_token, req_stride, 1,
                      slot_ids, topk_idx, idx_row_stride, topk_blocks * block_size, nullptr, seq_lens, nullptr,
                      sm_scale, out, out_row_stride, out_head_stride, out_dtype, lse, rows, splits, workspace,
                      workspace_bytes, ad, stream);
+}
+
+extern "C" int xt_block_sparse_prefill_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                                             const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_scales,
+                                             const uint8_t* v_scales, float kv_scale, int64_t pages,
+                                             int kv_heads, int q_heads, int dim, int block_size, int64_t page_stride,
+                                             int64_t head_stride, int64_t row_stride, int64_t sf_page_stride,
+                                             int64_t sf_head_stride, int64_t sf_row_stride,
+                                             const int32_t* req_to_token, int64_t req_stride,
+                                             const int64_t* row_req, const int32_t* row_seq_lens,
+                                             const int32_t* row_query_pos, const int32_t* topk_idx,
+                                             int64_t idx_head_stride, int64_t idx_row_stride, int topk_blocks,
+                                             const int32_t* row_idx, float sm_scale, void* out,
+                                             int64_t out_row_stride, int64_t out_head_stride, int out_dtype,
+                                             float* lse, int rows, int splits, void* workspace,
+                                             size_t workspace_bytes, xt_stream_t stream) {
+  const char* what = "xt_block_sparse_prefill_nvfp4";
+  int64_t mul;
+  const int st = block_pages(what, pages, kv_heads, dim, block_size, page_stride, head_stride, row_stride,
+                             sf_page_stride, sf_head_stride, sf_row_stride, topk_blocks, &mul);
+  if (st != XT_OK) return st;
+  if (!row_req || !row_query_pos || !row_idx) return fail(XT_EINVAL, "%s: a per-row array is null", what);
+  const int shift = __builtin_ctz((unsigned)block_size);
+  const Addressing ad{head_stride, sf_head_stride, shift, mul, idx_head_stride, shift, true, row_idx, 0x7FFFFFFF, true,
+                      kv_scale, kv_scale};
+  return decode_impl(what, q, q_row_stride, q_head_stride, k_pay, v_pay, k_scales, v_scales, nullptr, nullptr,
+                     pages * mul, row_stride, sf_row_stride, kv_heads, q_heads, req_to_token, req_stride, 1,
+                     row_req, topk_idx, idx_row_stride, topk_blocks * block_size, nullptr, row_seq_lens,
+                     row_query_pos, sm_scale, out, out_row_stride, out_head_stride, out_dtype, lse, rows, splits,
+                     workspace, workspace_bytes, ad, stream);
 }
 
 static int decode_impl(const char* what, const void* q, int64_t q_row_stride, int64_t q_head_stride,
@@ -712,6 +761,8 @@ static int decode_impl(const char* what, const void* q, int64_t q_row_stride, in
   a.remap_mul = ad.remap_mul;
   a.idx_head_stride = ad.idx_head_stride;
   a.block_shift = ad.block_shift;
+  a.lookup_mask = ad.token_lookup ? 0 : (1 << ad.block_shift) - 1;
+  a.idx_rows = ad.idx_rows;
   a.max_len = ad.max_len;
   a.kv_heads = kv_heads;
   a.q_heads = q_heads;

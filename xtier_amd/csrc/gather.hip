@@ -111,6 +111,36 @@ __global__ void qsa_pack_kernel(const uint8_t* __restrict__ k_pay, const uint8_t
   dequant_block(v_pay + po, v_sf + so, *gv, valid, out_dtype, out_v + dst);
 }
 
+// One request's context from head-major NVFP4 pages into BF16 rows (kv_fp4.py:496-530): thread = (request b,
+// position, head, 16-value block); token slot s = req_to_token[sid, pos] wrapped into [0, pages * block) as the
+// reference wraps it, at page s / block, row s % block.
+__global__ void paged_dequant_kernel(const uint8_t* __restrict__ pay, const uint8_t* __restrict__ sf,
+                                     int64_t max_slots, int heads, int dim, int block, int64_t page_stride,
+                                     int64_t head_stride, int64_t row_stride, int64_t sf_page_stride,
+                                     int64_t sf_head_stride, int64_t sf_row_stride,
+                                     const int32_t* __restrict__ req_to_token, int64_t req_stride,
+                                     const int64_t* __restrict__ slot_ids, const int32_t* __restrict__ seq_lens,
+                                     int batch, int rows_per_req, uint16_t* __restrict__ out) {
+  const int blocks = dim / 16;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)batch * rows_per_req * heads * blocks;
+  if (i >= total) return;
+  const int blk = (int)(i % blocks);
+  const int h = (int)((i / blocks) % heads);
+  const int64_t bp = i / ((int64_t)blocks * heads);
+  const int pos = (int)(bp % rows_per_req);
+  const int b = (int)(bp / rows_per_req);
+  if (pos >= seq_lens[b]) return;
+  int64_t sid = slot_ids[b];
+  if (sid < 0) sid += max_slots;
+  int64_t slot = req_to_token[sid * req_stride + pos] % max_slots;
+  if (slot < 0) slot += max_slots;
+  const int64_t page = slot / block, row = slot % block;
+  const int64_t po = page * page_stride + (int64_t)h * head_stride + row * row_stride + blk * 8;
+  const int64_t so = page * sf_page_stride + (int64_t)h * sf_head_stride + row * sf_row_stride + blk;
+  dequant_block(pay + po, sf + so, 1.0f, true, XT_DTYPE_BF16, out + (bp * heads + h) * dim + blk * 16);
+}
+
 int check_pool(const char* what, const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_sf,
                const uint8_t* v_sf, const float* gk, const float* gv, int64_t pool_slots, int heads, int dim) {
   // the reference's precondition (qsa_fp4.py:165-171): a power-of-2 head size, a multiple of 32
@@ -173,5 +203,31 @@ extern "C" int xt_qsa_pack_nvfp4(const uint8_t* k_pay, const uint8_t* v_pay, con
                      reinterpret_cast<hipStream_t>(stream), k_pay, v_pay, k_scales, v_scales, gk, gv, pool_slots,
                      heads, dim, req_to_token, sr0, sr1, req_indices, batch, cu_k, max_k,
                      static_cast<uint16_t*>(out_k), static_cast<uint16_t*>(out_v), out_dtype);
+  return check_launch(what);
+}
+
+extern "C" int xt_dequantize_context_nvfp4(const uint8_t* pay, const uint8_t* scales, int64_t pages, int heads,
+                                           int dim, int block_size, int64_t page_stride, int64_t head_stride,
+                                           int64_t row_stride, int64_t sf_page_stride, int64_t sf_head_stride,
+                                           int64_t sf_row_stride, const int32_t* req_to_token, int64_t req_stride,
+                                           const int64_t* slot_ids, const int32_t* seq_lens, int batch,
+                                           int rows_per_req, void* out, xt_stream_t stream) {
+  const char* what = "xt_dequantize_context_nvfp4";
+  if (heads <= 0 || dim < 32 || (dim & (dim - 1)) || block_size <= 0 || pages <= 0 || batch < 0 || rows_per_req < 0)
+    return fail(XT_EINVAL, "%s: bad heads %d / dim %d / block %d / pages %lld / batch / rows", what, heads, dim,
+                block_size, (long long)pages);
+  if (row_stride < dim / 2 || sf_row_stride < dim / 16 || row_stride % 8 || page_stride < (int64_t)block_size *
+      row_stride || sf_page_stride < (int64_t)block_size * sf_row_stride || head_stride < 0 || sf_head_stride < 0)
+    return fail(XT_EINVAL, "%s: pool strides do not describe [pages, heads, %d, dim/2] pages", what, block_size);
+  if (batch == 0 || rows_per_req == 0) return ok();
+  if (!pay || !scales || !req_to_token || !slot_ids || !seq_lens || !out || !aligned(pay, 8) || !aligned(out, 16))
+    return fail(XT_EINVAL, "%s: a required pointer is null or misaligned", what);
+  const int64_t total = (int64_t)batch * rows_per_req * heads * (dim / 16);
+  if ((total + 255) / 256 > 0x7FFFFFFFLL) return fail(XT_EUNSUPPORTED, "%s: %lld threads", what, (long long)total);
+  hipLaunchKernelGGL(paged_dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), pay, scales, pages * block_size, heads, dim, block_size,
+                     page_stride, head_stride, row_stride, sf_page_stride, sf_head_stride, sf_row_stride,
+                     req_to_token, req_stride, slot_ids, seq_lens, batch, rows_per_req,
+                     static_cast<uint16_t*>(out));
   return check_launch(what);
 }

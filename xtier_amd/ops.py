@@ -281,6 +281,104 @@ def fp4_sparse_decode(q, k_pay, k_sc, v_pay, v_sc, req_to_token, slot_ids, topk_
     return out
 
 
+def _pages(pay, sc, what):
+    """Head-major page views (payload [pages, kh, block, d/2], scales [pages, kh, block, d/16]) -> uint8 views."""
+    if pay.dtype != torch.uint8:
+        pay = pay.view(torch.uint8)
+    if sc.dtype != torch.uint8:
+        sc = sc.view(torch.uint8)
+    if pay.dim() != 4 or sc.dim() != 4 or pay.stride(3) != 1 or sc.stride(3) != 1 or pay.shape[:3] != sc.shape[:3] \
+            or sc.shape[3] * 8 != pay.shape[3]:
+        raise ValueError(f'xtier_amd.{what}: pages [pages, kv_heads, block, d/2] / [.., d/16] expected, got '
+                         f'{tuple(pay.shape)} / {tuple(sc.shape)}')
+    return pay, sc
+
+
+def fp4_prefill_gqa_share_sparse(q, k_cache, v_cache, sink, req_to_token, slot_ids, topk_idx, block_size_q,
+                                 block_size_k, cu_seqlens, seq_lens, prefix_lens, max_seqlen_q, sm_scale=None,
+                                 use_tma=True, cu_seqblocks_q=None, max_seqblock_q=None, q_scale=None, k_scale=None,
+                                 v_scale=None, loc_mapping=None, *, k_sc=None, v_sc=None, kv_scale=1.0, num_warps=4,
+                                 num_stages=2, out=None, splits=None, ws=None):
+    """Causal block-sparse prefill over an NVFP4 cache of head-major pages (kv_fp4.py:369-404): q [total_q, qh, d]
+    BF16, request b's queries are rows cu_seqlens[b] .. cu_seqlens[b+1]-1 at positions prefix_lens[b] + i; the
+    queries of one block of block_size_q share the block list topk_idx[kh, cu_seqblocks_q[b] + i // block_size_q, :]
+    (block ids of block_size_k tokens, -1 padded); k_cache / v_cache payload pages, k_sc / v_sc their scale bytes.
+    Returns o [total_q, qh, d] in q's dtype. Lengths are clamped to req_to_token.shape[1]; a key block wholly after a
+    query's position adds nothing to its softmax (the reference's running max starts at -inf, so such a block listed
+    first gives it NaN). use_tma / num_warps / num_stages / max_seqblock_q are accepted for the reference's signature
+    and ignored."""
+    assert sink is None and loc_mapping is None and block_size_k == k_cache.shape[2]
+    k_pay, k_sc8 = _pages(k_cache, k_sc, 'fp4_prefill_gqa_share_sparse')
+    v_pay, v_sc8 = _pages(v_cache, v_sc, 'fp4_prefill_gqa_share_sparse')
+    assert k_pay.stride() == v_pay.stride() and k_sc8.stride() == v_sc8.stride()
+    total_q, qh, d = q.shape
+    kh = k_pay.shape[1]
+    if k_pay.shape[3] * 2 != d or qh % kh:
+        raise ValueError(f'xtier_amd.fp4_prefill_gqa_share_sparse: q {tuple(q.shape)} does not fit pages '
+                         f'{tuple(k_pay.shape)}')
+    _need_cuda(q, k_pay, v_pay, req_to_token, slot_ids, topk_idx, cu_seqlens, seq_lens, prefix_lens, out)
+    sm_scale = (d ** -0.5 if sm_scale is None else sm_scale) * (1.0 if q_scale is None else q_scale)
+    dev = q.device
+    cu = cu_seqlens.to(torch.int64)
+    if cu_seqblocks_q is None:
+        nblk = (cu[1:] - cu[:-1] + block_size_q - 1) // block_size_q
+        cu_seqblocks_q = torch.cat([torch.zeros(1, dtype=torch.int64, device=dev), torch.cumsum(nblk, 0)])
+    r = torch.arange(total_q, device=dev, dtype=torch.int64)
+    bi = torch.searchsorted(cu[1:].contiguous(), r, right=True)
+    local = r - cu[bi]
+    max_slots = k_pay.shape[0] * block_size_k
+    row_req = torch.remainder(slot_ids.to(torch.int64)[bi], max_slots)
+    row_qpos = (prefix_lens.to(torch.int64)[bi] + local).to(torch.int32)
+    row_seq = torch.clamp(seq_lens.to(torch.int32)[bi], max=req_to_token.shape[1])   # positions within the table
+    row_idx = (cu_seqblocks_q.to(torch.int64)[bi] + local // block_size_q).to(torch.int32)
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    if out is None:
+        out = torch.empty(total_q, qh, d, dtype=q.dtype if q.dtype in _DTYPES else torch.bfloat16, device=dev)
+    if req_to_token.dtype != torch.int32 or req_to_token.stride(1) != 1:
+        req_to_token = req_to_token.to(torch.int32).contiguous()
+    if topk_idx.dtype != torch.int32 or topk_idx.stride(2) != 1:
+        topk_idx = topk_idx.to(torch.int32).contiguous()
+    q16 = q if q.dtype == torch.bfloat16 else q.to(torch.bfloat16)
+    topk = topk_idx.shape[2]
+    if splits is None:
+        splits = _capture_splits(dev, total_q, qh, d, default_splits(total_q, kh, topk * block_size_k), ws)
+    ws = _decode_ws(dev, total_q, qh, d, splits, ws)
+    _lib.check(_lib.lib().xt_block_sparse_prefill_nvfp4(
+        _ptr(q16), q16.stride(0), q16.stride(1), _ptr(k_pay), _ptr(v_pay), _ptr(k_sc8), _ptr(v_sc8), float(kv_scale),
+        k_pay.shape[0], kh, qh, d, int(block_size_k), k_pay.stride(0), k_pay.stride(1), k_pay.stride(2),
+        k_sc8.stride(0), k_sc8.stride(1), k_sc8.stride(2), _ptr(req_to_token), req_to_token.stride(0), _ptr(row_req),
+        _ptr(row_seq), _ptr(row_qpos), _ptr(topk_idx), topk_idx.stride(0), topk_idx.stride(1), topk, _ptr(row_idx),
+        float(sm_scale), _ptr(out), out.stride(0), out.stride(1), _DTYPES[out.dtype], None, total_q, int(splits),
+        _ptr(ws), ws.numel(), _stream(q16)), 'fp4_prefill_gqa_share_sparse')
+    return out
+
+
+def dequantize_context(pay, sc, req_to_token, slot_ids, seq_lens, rows_per_req, out=None):
+    """BF16 [b * rows_per_req, heads, d] of each request's first seq_lens[b] positions (kv_fp4.py:514-530): pay / sc
+    [pages, heads, block, d/2 | d/16] (main) or [pages, block, ...] (the one-head index cache)."""
+    if pay.dim() == 3:
+        pay, sc = pay.unsqueeze(1), sc.unsqueeze(1)
+    pay, sc = _pages(pay, sc, 'dequantize_context')
+    pages, heads, block, half = pay.shape
+    b = slot_ids.shape[0]
+    _need_cuda(pay, sc, req_to_token, slot_ids, seq_lens, out)
+    if out is None:
+        out = torch.empty(b * rows_per_req, heads, 2 * half, dtype=torch.bfloat16, device=pay.device)
+    if out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError('xtier_amd.dequantize_context: a contiguous BF16 output expected')
+    if req_to_token.dtype != torch.int32 or req_to_token.stride(1) != 1:
+        req_to_token = req_to_token.to(torch.int32).contiguous()
+    slot_ids = slot_ids if slot_ids.dtype == torch.int64 else slot_ids.to(torch.int64)
+    seq_lens = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
+    _lib.check(_lib.lib().xt_dequantize_context_nvfp4(
+        _ptr(pay), _ptr(sc), pages, heads, 2 * half, block, pay.stride(0), pay.stride(1) if heads > 1 else 0,
+        pay.stride(2), sc.stride(0), sc.stride(1) if heads > 1 else 0, sc.stride(2), _ptr(req_to_token),
+        req_to_token.stride(0), _ptr(slot_ids), _ptr(seq_lens), b, int(rows_per_req), _ptr(out), _stream(pay)),
+        'dequantize_context')
+    return out
+
+
 # --- split-K decode over packed BF16 rows --------------------------------------------------------------------------
 
 def varlen_workspace_bytes(rows, heads, dim, splits):
