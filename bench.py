@@ -333,6 +333,86 @@ def run_block(args, w, ops, workloads):
     print(json.dumps(record), flush=True)
 
 
+def run_block_prefill(args, w, ops, workloads):
+    """Causal block-sparse prefill chunks over head-major NVFP4 pages (MiniMax layout), rotating `layers` distinct
+    pools; also times the BF16 context copy (main K, V and index K) the prefill entry makes for contexts that fit.
+    One JSON line: TFLOP/s of the attention against the MFMA peak."""
+    import torch
+    torch.cuda.set_device(0)
+    t0 = time.time()
+    gen = workloads.generator('cuda', 20261201)
+    layers = max(1, min(args.layers, 8))
+    shape = workloads.BlockDecodeWorkload(w.name, 1, w.q_heads, w.kv_heads, w.dim, w.ctx, w.topk_blocks, w.block)
+    pools = [build_block_pool(shape, gen, workloads, ops) for _ in range(layers)]
+    ik = build_block_pool(workloads.BlockDecodeWorkload(w.name, 1, 1, 1, w.dim, w.ctx, 1, w.block), gen, workloads,
+                          ops)[:2]
+    ik = [t[:, 0] for t in ik]
+    inp = workloads.block_prefill_inputs(w, 20261202, 'cuda')
+    splits = args.splits or ops.default_splits(w.q_len, w.kv_heads, w.topk_blocks * w.block)
+    ws = ops.new_workspace('cuda', w.q_len, w.q_heads, w.dim, splits)
+    out = torch.empty_like(inp.q)
+    rows = -(-w.ctx // 128) * 128
+    copies = [torch.empty(rows, w.kv_heads, w.dim, dtype=torch.bfloat16, device='cuda') for _ in range(2)]
+    copies.append(torch.empty(rows, 1, w.dim, dtype=torch.bfloat16, device='cuda'))
+    torch.cuda.synchronize()
+    log(f'built {layers} page pools ({w.pages} pages each) in {time.time() - t0:.1f} s')
+
+    def step(layer):
+        k_pay, k_sc, v_pay, v_sc = pools[layer]
+        ops.fp4_prefill_gqa_share_sparse(inp.q, k_pay, v_pay, None, inp.req_to_token, inp.slot_ids, inp.topk_idx, 1,
+                                         w.block, inp.cu_seqlens, inp.seq_lens, inp.prefix_lens, w.q_len, k_sc=k_sc,
+                                         v_sc=v_sc, out=out, splits=splits, ws=ws)
+
+    def copy(layer):
+        k_pay, k_sc, v_pay, v_sc = pools[layer]
+        for (pay, sc), dst in zip(((k_pay, k_sc), (v_pay, v_sc), ik), copies):
+            ops.dequantize_context(pay, sc, inp.req_to_token, inp.slot_ids, inp.seq_lens, rows, out=dst)
+
+    def timed(fn, reps):
+        for i in range(max(1, args.warmup)):
+            fn(i % layers)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for layer in range(layers):
+                fn(layer)
+        graph.replay()
+        torch.cuda.synchronize()
+        n = max(1, math.ceil(reps / layers))
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(n):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / (n * layers), n * layers
+
+    ms, steps = timed(step, args.steps)
+    copy_ms, _ = timed(copy, args.steps)
+    tflops = w.flops() / (ms * 1e-3) / 1e12
+    gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
+    copy_gbs = w.copy_bytes() / (copy_ms * 1e-3) / 1e9
+    log(f'{w.name}: {ms * 1e3:.1f} us per chunk, {tflops:.1f} TFLOP/s ({tflops / MFMA_PEAK_TFLOPS:.1%} of '
+        f'{MFMA_PEAK_TFLOPS:.0f}), {gbs:.0f} GB/s of listed KV, splits {splits}; context copy {copy_ms * 1e3:.1f} us '
+        f'= {copy_gbs:.0f} GB/s ({copy_gbs / HBM_PEAK_GBS:.1%})')
+    record = {
+        'metric': 'NVFP4-KV block-sparse prefill TFLOP/s', 'value': round(tflops, 2), 'unit': 'TFLOP/s',
+        'n_gpus': 1, 'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'higher_is_better': True,
+        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f16', 'data': 'synthetic',
+        'config': {'workload': w.name, 'q_len': w.q_len, 'prefix': w.prefix, 'q_heads': w.q_heads,
+                   'kv_heads': w.kv_heads, 'head_dim': w.dim, 'topk_blocks': w.topk_blocks, 'block': w.block,
+                   'block_size_q': 1, 'kv_format': 'nvfp4 head-major pages', 'layers_rotated': layers,
+                   'splits': splits},
+        'us_per_chunk': round(ms * 1e3, 2), 'listed_kv_gbs': round(gbs, 1),
+        'context_copy': {'us': round(copy_ms * 1e3, 2), 'bytes': w.copy_bytes(), 'gbs': round(copy_gbs, 1),
+                         'frac_hbm': round(copy_gbs / HBM_PEAK_GBS, 4)},
+        'roofline': {'bound': 'mfma', 'achieved': round(tflops, 2), 'peak': MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
+                     'frac': round(tflops / MFMA_PEAK_TFLOPS, 4), 'traffic': None},
+        'cpu_baseline': None,
+    }
+    print(json.dumps(record), flush=True)
+
+
 def run_varlen(args, w, ops, workloads):
     """Split-K decode over packed BF16 rows, rotating `layers` distinct K/V buffers. One JSON line: GB/s of K/V rows
     read against the HBM peak."""
@@ -397,7 +477,8 @@ def main():
     p.add_argument('--warmup', type=int, default=64)
     p.add_argument('--workload', default='gqa_decode_b32',
                    help='gqa_decode_b32 (default), cpu_ref_decode, long_ctx_decode_b4, gqa_prefill_chunk4096, '
-                        'minimax_decode_b32, qsa_varlen_b32, mla_decode_b64, mla_prefill_2048 or mla_v4_decode_b64')
+                        'minimax_decode_b32, minimax_prefill_chunk4096, qsa_varlen_b32, mla_decode_b64, mla_prefill_2048 or '
+                        'mla_v4_decode_b64')
     p.add_argument('--layers', type=int, default=16)
     p.add_argument('--splits', type=int, default=None)
     p.add_argument('--layout', default='interleaved', choices=['interleaved', 'split'],
@@ -431,6 +512,8 @@ def main():
         return run_varlen(args, workloads.VARLEN_WORKLOADS[args.workload], ops, workloads)
     if args.workload in workloads.BLOCK_WORKLOADS:
         return run_block(args, workloads.BLOCK_WORKLOADS[args.workload], ops, workloads)
+    if args.workload in workloads.BLOCK_PREFILL_WORKLOADS:
+        return run_block_prefill(args, workloads.BLOCK_PREFILL_WORKLOADS[args.workload], ops, workloads)
     if args.workload in workloads.MLA_WORKLOADS:
         return run_mla(args, workloads.MLA_WORKLOADS[args.workload], ops, workloads)
     if args.workload in workloads.PREFILL_WORKLOADS:

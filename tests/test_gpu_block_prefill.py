@@ -168,3 +168,34 @@ def test_prefill_hooks(monkeypatch):
     minimax.sparse_prefill(orig, *args)
     a, _ = orig.calls[-1]
     assert a[1] is k_pay and a[5] is ik_pay and a[8] is c['r2t']
+
+
+def test_prefill_chunk_workload_on_sampled_rows():
+    """The benchmarked chunk (4096 queries after 61440 tokens, MiniMax heads, 16 blocks per query) at full size,
+    checked against the oracle on sampled query rows."""
+    w = workloads.BLOCK_PREFILL_WORKLOADS['minimax_prefill_chunk4096']
+    print(f'{w.name}: full size, sampled rows', flush=True)
+    inp = workloads.block_prefill_inputs(w, 20261202, 'cuda')
+    shape = workloads.BlockDecodeWorkload(w.name, 1, w.q_heads, w.kv_heads, w.dim, w.ctx, w.topk_blocks, w.block)
+    gen = workloads.generator('cuda', 31)
+    pool = []
+    one = torch.ones(1, dtype=torch.float32, device='cuda')
+    for _ in range(2):
+        x = workloads.kv_tensor(w.ctx, w.kv_heads, w.dim, gen, 'cuda')
+        pay = torch.empty(w.ctx, w.kv_heads, w.dim // 2, dtype=torch.uint8, device='cuda')
+        sc = torch.empty(w.ctx, w.kv_heads, w.dim // 16, dtype=torch.uint8, device='cuda')
+        ops.quantize_append(x, torch.arange(w.ctx, device='cuda'), one, pay, sc)
+        pool += list(workloads.head_major_pages(pay, sc, shape.block))
+    k_pay, k_sc, v_pay, v_sc = pool
+    out = ops.fp4_prefill_gqa_share_sparse(inp.q, k_pay, v_pay, None, inp.req_to_token, inp.slot_ids, inp.topk_idx, 1,
+                                           w.block, inp.cu_seqlens, inp.seq_lens, inp.prefix_lens, w.q_len,
+                                           k_sc=k_sc, v_sc=v_sc)
+    rows = np.array([0, 1, 127, 128, 1000, 2047, 2048, 3000, 4094, 4095])
+    n = len(rows)
+    host = [t.cpu().numpy() for t in pool]
+    args = (inp.q.float().cpu().numpy()[rows], host[0], host[1], host[2], host[3], inp.req_to_token.cpu().numpy(),
+            np.zeros(n, np.int64), inp.topk_idx.cpu().numpy()[:, rows], np.arange(n + 1), np.arange(n + 1),
+            np.full(n, w.ctx), w.prefix + rows, 1, w.block, w.dim ** -0.5)
+    ref = attention.block_sparse_prefill(*args)
+    flash = attention.block_sparse_prefill(*args, attend=attention.flash_precision_attention)
+    check(out[torch.from_numpy(rows).cuda()], ref, flash)

@@ -111,34 +111,69 @@ __global__ void qsa_pack_kernel(const uint8_t* __restrict__ k_pay, const uint8_t
   dequant_block(v_pay + po, v_sf + so, *gv, valid, out_dtype, out_v + dst);
 }
 
-// One request's context from head-major NVFP4 pages into BF16 rows (kv_fp4.py:496-530): thread = (request b,
-// position, head, 16-value block); token slot s = req_to_token[sid, pos] wrapped into [0, pages * block) as the
-// reference wraps it, at page s / block, row s % block.
-__global__ void paged_dequant_kernel(const uint8_t* __restrict__ pay, const uint8_t* __restrict__ sf,
-                                     int64_t max_slots, int heads, int dim, int block, int64_t page_stride,
-                                     int64_t head_stride, int64_t row_stride, int64_t sf_page_stride,
-                                     int64_t sf_head_stride, int64_t sf_row_stride,
-                                     const int32_t* __restrict__ req_to_token, int64_t req_stride,
-                                     const int64_t* __restrict__ slot_ids, const int32_t* __restrict__ seq_lens,
-                                     int batch, int rows_per_req, uint16_t* __restrict__ out) {
-  const int blocks = dim / 16;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = (int64_t)batch * rows_per_req * heads * blocks;
-  if (i >= total) return;
-  const int blk = (int)(i % blocks);
-  const int h = (int)((i / blocks) % heads);
-  const int64_t bp = i / ((int64_t)blocks * heads);
-  const int pos = (int)(bp % rows_per_req);
-  const int b = (int)(bp / rows_per_req);
-  if (pos >= seq_lens[b]) return;
+constexpr int kDequantPieces = 8;
+
+// One request's context from head-major NVFP4 pages into BF16 rows (kv_fp4.py:496-530). Grid (x, request b). The
+// output of a request is a sequence of 8-value pieces (position, head, piece; piece fastest); a thread takes
+// kDequantPieces of them, 256 apart, so every store of a wave writes 1 KiB of consecutive output and 16 lanes read one
+// head's 64-byte row. Token slot s = req_to_token[sid, pos] wrapped into [0, pages * block) as the reference wraps
+// it, at page s / block, row s % block (block a power of 2); all loads of a thread issue before the first use. The
+// products e2m1 * e4m3 have at most 5 significant bits, so the upper half of their FP32 bits is the BF16 value (NaN
+// stays NaN).
+__global__ __launch_bounds__(256) void paged_dequant_kernel(
+    const uint8_t* __restrict__ pay, const uint8_t* __restrict__ sf, int64_t max_slots, int heads, int piece_shift,
+    int block_shift, int64_t page_stride, int64_t head_stride, int64_t row_stride, int64_t sf_page_stride,
+    int64_t sf_head_stride, int64_t sf_row_stride, const int32_t* __restrict__ req_to_token, int64_t req_stride,
+    const int64_t* __restrict__ slot_ids, const int32_t* __restrict__ seq_lens, int rows_per_req,
+    uint16_t* __restrict__ out) {
+  constexpr int U = kDequantPieces;
+  const int b = blockIdx.y;
+  const int len = min(seq_lens[b], rows_per_req);
   int64_t sid = slot_ids[b];
-  if (sid < 0) sid += max_slots;
-  int64_t slot = req_to_token[sid * req_stride + pos] % max_slots;
-  if (slot < 0) slot += max_slots;
-  const int64_t page = slot / block, row = slot % block;
-  const int64_t po = page * page_stride + (int64_t)h * head_stride + row * row_stride + blk * 8;
-  const int64_t so = page * sf_page_stride + (int64_t)h * sf_head_stride + row * sf_row_stride + blk;
-  dequant_block(pay + po, sf + so, 1.0f, true, XT_DTYPE_BF16, out + (bp * heads + h) * dim + blk * 16);
+  if ((uint64_t)sid >= (uint64_t)max_slots) sid = (sid % max_slots + max_slots) % max_slots;
+  const int32_t* tp = req_to_token + sid * req_stride;
+  int pos[U], h[U], pc[U];
+  int32_t ent[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int g = (blockIdx.x * U + u) * 256 + (int)threadIdx.x;
+    pc[u] = g & ((1 << piece_shift) - 1);
+    const int hp = g >> piece_shift;
+    pos[u] = hp / heads;
+    h[u] = hp - pos[u] * heads;
+    ent[u] = pos[u] < len ? tp[pos[u]] : 0;
+  }
+  uint32_t w[U], sb[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    int64_t slot = ent[u];
+    if ((uint64_t)slot >= (uint64_t)max_slots) slot = (slot % max_slots + max_slots) % max_slots;
+    const int64_t page = slot >> block_shift, row = slot & ((1 << block_shift) - 1);
+    const uint8_t* p = pay + page * page_stride + (int64_t)h[u] * head_stride + row * row_stride + pc[u] * 4;
+    const uint8_t* q = sf + page * sf_page_stride + (int64_t)h[u] * sf_head_stride + row * sf_row_stride + (pc[u] >> 1);
+    if (pos[u] >= len) p = pay, q = sf;     // a valid address; the values are not stored
+    w[u] = *reinterpret_cast<const uint32_t*>(p);
+    sb[u] = *q;
+  }
+  uint16_t* base = out + (int64_t)b * rows_per_req * heads * (8 << piece_shift);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (pos[u] >= len) continue;
+    const float s = e4m3_decode(sb[u]);
+    const float2_t v[4] = {fp4x2_to_f32<0>(w[u]), fp4x2_to_f32<1>(w[u]), fp4x2_to_f32<2>(w[u]),
+                           fp4x2_to_f32<3>(w[u])};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = v[e].x * s, hi = v[e].y * s;
+      uint32_t a, bb;
+      __builtin_memcpy(&a, &lo, 4);
+      __builtin_memcpy(&bb, &hi, 4);
+      o[e] = (a >> 16) | (bb & 0xFFFF0000u);
+    }
+    const int g = (blockIdx.x * U + u) * 256 + (int)threadIdx.x;
+    *reinterpret_cast<uint4*>(base + (int64_t)g * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
 }
 
 int check_pool(const char* what, const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_sf,
@@ -213,8 +248,9 @@ extern "C" int xt_dequantize_context_nvfp4(const uint8_t* pay, const uint8_t* sc
                                            const int64_t* slot_ids, const int32_t* seq_lens, int batch,
                                            int rows_per_req, void* out, xt_stream_t stream) {
   const char* what = "xt_dequantize_context_nvfp4";
-  if (heads <= 0 || dim < 32 || (dim & (dim - 1)) || block_size <= 0 || pages <= 0 || batch < 0 || rows_per_req < 0)
-    return fail(XT_EINVAL, "%s: bad heads %d / dim %d / block %d / pages %lld / batch / rows", what, heads, dim,
+  if (heads <= 0 || dim < 32 || (dim & (dim - 1)) || block_size <= 0 || (block_size & (block_size - 1)) ||
+      pages <= 0 || batch < 0 || rows_per_req < 0)
+    return fail(XT_EINVAL, "%s: bad heads %d / dim %d / block %d (a power of 2) / pages %lld / batch / rows", what, heads, dim,
                 block_size, (long long)pages);
   if (row_stride < dim / 2 || sf_row_stride < dim / 16 || row_stride % 8 || page_stride < (int64_t)block_size *
       row_stride || sf_page_stride < (int64_t)block_size * sf_row_stride || head_stride < 0 || sf_head_stride < 0)
@@ -222,12 +258,14 @@ extern "C" int xt_dequantize_context_nvfp4(const uint8_t* pay, const uint8_t* sc
   if (batch == 0 || rows_per_req == 0) return ok();
   if (!pay || !scales || !req_to_token || !slot_ids || !seq_lens || !out || !aligned(pay, 8) || !aligned(out, 16))
     return fail(XT_EINVAL, "%s: a required pointer is null or misaligned", what);
-  const int64_t total = (int64_t)batch * rows_per_req * heads * (dim / 16);
-  if ((total + 255) / 256 > 0x7FFFFFFFLL) return fail(XT_EUNSUPPORTED, "%s: %lld threads", what, (long long)total);
-  hipLaunchKernelGGL(paged_dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), pay, scales, pages * block_size, heads, dim, block_size,
-                     page_stride, head_stride, row_stride, sf_page_stride, sf_head_stride, sf_row_stride,
-                     req_to_token, req_stride, slot_ids, seq_lens, batch, rows_per_req,
+  const int64_t per_req = (int64_t)rows_per_req * heads * (dim / 8);
+  if (per_req > 0x7FFFFFFFLL - 256 * kDequantPieces || batch > 65535)
+    return fail(XT_EUNSUPPORTED, "%s: %lld pieces per request or %d requests", what, (long long)per_req, batch);
+  const dim3 grid((unsigned)((per_req + 256 * kDequantPieces - 1) / (256 * kDequantPieces)), (unsigned)batch);
+  hipLaunchKernelGGL(paged_dequant_kernel, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream), pay, scales,
+                     pages * block_size, heads, __builtin_ctz((unsigned)(dim / 8)),
+                     __builtin_ctz((unsigned)block_size), page_stride, head_stride, row_stride, sf_page_stride,
+                     sf_head_stride, sf_row_stride, req_to_token, req_stride, slot_ids, seq_lens, rows_per_req,
                      static_cast<uint16_t*>(out));
   return check_launch(what);
 }

@@ -176,6 +176,48 @@ BLOCK_WORKLOADS = {
 
 
 @dataclass(frozen=True)
+class BlockPrefillWorkload:
+    """Causal block-sparse prefill over head-major NVFP4 pages (the MiniMax cache layout): one request appends a chunk
+    of `q_len` queries after `prefix` tokens; each query (query blocks of one, as the NVFP4 prefill runs them) and KV
+    head lists `topk_blocks` blocks of `block` tokens: its own block and topk_blocks - 1 distinct earlier ones."""
+    name: str
+    q_len: int
+    prefix: int
+    q_heads: int
+    kv_heads: int
+    dim: int
+    topk_blocks: int
+    block: int = 128
+
+    @property
+    def ctx(self):
+        return self.prefix + self.q_len
+
+    @property
+    def pages(self):
+        return self.ctx // self.block
+
+    def algorithmic_bytes(self):
+        """KV payload plus scales the queries read, counting whole listed blocks: q_len * kv_heads * topk_blocks *
+        block * 2 * (dim/2 + dim/16)."""
+        return self.q_len * self.kv_heads * self.topk_blocks * self.block * 2 * (self.dim // 2 + self.dim // 16)
+
+    def flops(self):
+        return self.q_len * self.q_heads * self.topk_blocks * self.block * 4 * self.dim
+
+    def copy_bytes(self):
+        """The BF16 context copy of main K, V (kv_heads) and index K (one head): per token read dim/2 + dim/16 and
+        write 2 * dim bytes per head."""
+        return self.ctx * (2 * self.kv_heads + 1) * (self.dim // 2 + self.dim // 16 + 2 * self.dim)
+
+
+BLOCK_PREFILL_WORKLOADS = {
+    # a 4096-query chunk after 61440 tokens (context 65536), 64 q / 4 KV heads, d 128, 16 blocks of 128 per query
+    'minimax_prefill_chunk4096': BlockPrefillWorkload('minimax_prefill_chunk4096', 4096, 61440, 64, 4, 128, 16),
+}
+
+
+@dataclass(frozen=True)
 class VarlenWorkload:
     """Decode over packed BF16 rows (the gathered top-k rows of every request, one query per row)."""
     name: str
@@ -366,6 +408,35 @@ def block_decode_inputs(w, seed, device='cpu', batch=None):
             idx[h, r] = torch.sort(torch.randperm(nb, generator=gen, device=device)[:w.topk_blocks]).values
     seq = torch.full((b,), w.ctx, dtype=torch.int32, device=device)
     return BlockDecodeInputs(w, q, r2t, torch.arange(b, dtype=torch.int64, device=device), idx, seq)
+
+
+@dataclass
+class BlockPrefillInputs:
+    workload: BlockPrefillWorkload
+    q: torch.Tensor            # bf16 [q_len, q_heads, dim]
+    req_to_token: torch.Tensor  # int32 [1, ctx]: pages of `block` tokens in a random order
+    slot_ids: torch.Tensor     # int64 [1]
+    topk_idx: torch.Tensor     # int32 [kv_heads, q_len, topk_blocks]: the query's block first, then earlier ones
+    cu_seqlens: torch.Tensor   # int32 [2]
+    seq_lens: torch.Tensor     # int32 [1]
+    prefix_lens: torch.Tensor  # int32 [1]
+
+
+def block_prefill_inputs(w, seed, device='cpu'):
+    """Seeded queries, a token table over the pool's pages in a random order (as a page allocator hands them out), and
+    per-(KV head, query) block lists."""
+    gen = generator(device, seed)
+    q = torch.randn(w.q_len, w.q_heads, w.dim, generator=gen, device=device).to(torch.bfloat16)
+    r2t = token_table(page_table(1, w.ctx, w.block, gen, device), w.block)
+    own = (w.prefix + torch.arange(w.q_len, device=device)) // w.block
+    nb = w.ctx // w.block
+    score = torch.rand(w.kv_heads, w.q_len, nb, generator=gen, device=device)
+    score = torch.where(torch.arange(nb, device=device)[None, None, :] < own[None, :, None], score, -1.0)
+    far = torch.topk(score, w.topk_blocks - 1, dim=2).indices
+    idx = torch.cat([own[None, :, None].expand(w.kv_heads, -1, 1), far], dim=2).to(torch.int32).contiguous()
+    i32 = lambda v: torch.tensor(v, dtype=torch.int32, device=device)
+    return BlockPrefillInputs(w, q, r2t, torch.zeros(1, dtype=torch.int64, device=device), idx, i32([0, w.q_len]),
+                              i32([w.ctx]), i32([w.prefix]))
 
 
 def head_major_pages(x_pay, x_sc, block):
