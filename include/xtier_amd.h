@@ -171,7 +171,8 @@ int xt_block_sparse_prefill_nvfp4(const void* q, int64_t q_row_stride, int64_t q
  * s = req_to_token[sid * req_stride + pos] (sid = slot_ids[b]; both wrapped into [0, pages * block_size) as the
  * reference wraps them) -> out[b * rows_per_req + pos, h, :] (BF16 [batch * rows_per_req, heads, dim], contiguous)
  * = e2m1 * e4m3 of page s / block_size, row s % block_size (unit global scale, exact in BF16); other rows are left as
- * they are. Strides as xt_block_sparse_decode_nvfp4 (head strides may be 0 for the one-head index cache). */
+ * they are. Strides as xt_block_sparse_decode_nvfp4 (head strides may be 0 for the one-head index cache); dim and
+ * block_size powers of 2, dim >= 32. */
 int xt_dequantize_context_nvfp4(const uint8_t* pay, const uint8_t* scales, int64_t pages, int heads, int dim,
                                 int block_size, int64_t page_stride, int64_t head_stride, int64_t row_stride,
                                 int64_t sf_page_stride, int64_t sf_head_stride, int64_t sf_row_stride,
