@@ -413,6 +413,79 @@ def run_block_prefill(args, w, ops, workloads):
     print(json.dumps(record), flush=True)
 
 
+GATHER_WORKLOADS = {
+    # the decode workload's rows (batch 32, 4 KV heads x 128, context 32768, top-2048, page 64) gathered into BF16
+    'qsa_gather_b32': ('gather', 32, 32768, 2048),
+    # one request's 65536-token prefix packed into BF16 rows (4 KV heads x 128)
+    'qsa_pack_ctx65536': ('pack', 1, 65536, 65536),
+}
+
+
+def run_gather(args, name, ops, workloads, KVPool):
+    """The QSA gather (decode rows through the page table) or prefix pack into BF16 rows, rotating `layers` pools of
+    SGLang's four buffers. One JSON line: GB/s of pool bytes read plus BF16 rows written against the HBM peak."""
+    import torch
+    mode, batch, ctx, topk = GATHER_WORKLOADS[name]
+    kv_heads, dim, page = 4, 128, 64
+    torch.cuda.set_device(0)
+    gen = workloads.generator('cuda', 20261203)
+    layers = max(1, min(args.layers, 4))
+    w = workloads.DecodeWorkload(name, batch, 32, kv_heads, dim, ctx, topk, page)
+    t0 = time.time()
+    pools = [build_layer(w, gen, 'split', workloads, KVPool) for _ in range(layers)]
+    r2t = workloads.token_table(workloads.page_table(batch, ctx, page, gen, 'cuda'), page)
+    req = torch.arange(batch, dtype=torch.int64, device='cuda')
+    cu = (torch.arange(batch + 1, dtype=torch.int32, device='cuda') * topk)
+    seq = torch.full((batch,), ctx, dtype=torch.int32, device='cuda')
+    idx = workloads.index_lists(batch, ctx, topk, gen, 'cuda') if mode == 'gather' else None
+    out_k = torch.empty(batch * topk, kv_heads, dim, dtype=torch.bfloat16, device='cuda')
+    out_v = torch.empty_like(out_k)
+    torch.cuda.synchronize()
+    log(f'built {layers} pools ({w.slots} slots each) in {time.time() - t0:.1f} s')
+
+    def step(layer):
+        if mode == 'gather':
+            ops.gather(pools[layer], r2t, req, idx, seq, cu, out_k, out_v, batch, topk)
+        else:
+            ops.pack(pools[layer], r2t, req, cu, batch * topk, topk, torch.bfloat16)
+
+    for i in range(max(1, args.warmup)):
+        step(i % layers)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for layer in range(layers):
+            step(layer)
+    graph.replay()
+    torch.cuda.synchronize()
+    replays = max(1, math.ceil(args.steps / layers))
+    steps = replays * layers
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    rows = batch * topk * kv_heads
+    nbytes = rows * 2 * (dim // 2 + dim // 16) + rows * 2 * dim * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f'{name}: {ms * 1e3:.2f} us per layer-step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of {HBM_PEAK_GBS:.0f})')
+    record = {
+        'metric': f'NVFP4-KV {mode} into BF16 rows HBM GB/s', 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1,
+        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'higher_is_better': True,
+        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic',
+        'config': {'workload': name, 'batch': batch, 'kv_heads': kv_heads, 'head_dim': dim, 'context': ctx,
+                   'rows_per_request': topk, 'page': page, 'kv_format': 'nvfp4 (SGLang buffers)',
+                   'layers_rotated': layers},
+        'us_per_layer_step': round(ms * 1e3, 3), 'bytes_per_step': nbytes,
+        'roofline': {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+                     'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None},
+        'cpu_baseline': None,
+    }
+    print(json.dumps(record), flush=True)
+
+
 def run_varlen(args, w, ops, workloads):
     """Split-K decode over packed BF16 rows, rotating `layers` distinct K/V buffers. One JSON line: GB/s of K/V rows
     read against the HBM peak."""
@@ -477,8 +550,8 @@ def main():
     p.add_argument('--warmup', type=int, default=64)
     p.add_argument('--workload', default='gqa_decode_b32',
                    help='gqa_decode_b32 (default), cpu_ref_decode, long_ctx_decode_b4, gqa_prefill_chunk4096, '
-                        'minimax_decode_b32, minimax_prefill_chunk4096, qsa_varlen_b32, mla_decode_b64, mla_prefill_2048 or '
-                        'mla_v4_decode_b64')
+                        'minimax_decode_b32, minimax_prefill_chunk4096, qsa_varlen_b32, qsa_gather_b32, qsa_pack_ctx65536, '
+                        'mla_decode_b64, mla_prefill_2048 or mla_v4_decode_b64')
     p.add_argument('--layers', type=int, default=16)
     p.add_argument('--splits', type=int, default=None)
     p.add_argument('--layout', default='interleaved', choices=['interleaved', 'split'],
@@ -512,6 +585,8 @@ def main():
         return run_varlen(args, workloads.VARLEN_WORKLOADS[args.workload], ops, workloads)
     if args.workload in workloads.BLOCK_WORKLOADS:
         return run_block(args, workloads.BLOCK_WORKLOADS[args.workload], ops, workloads)
+    if args.workload in GATHER_WORKLOADS:
+        return run_gather(args, args.workload, ops, workloads, KVPool)
     if args.workload in workloads.BLOCK_PREFILL_WORKLOADS:
         return run_block_prefill(args, workloads.BLOCK_PREFILL_WORKLOADS[args.workload], ops, workloads)
     if args.workload in workloads.MLA_WORKLOADS:

@@ -1,114 +1,139 @@
 // QSA decode gather and prefill packing over the NVFP4 pool: bit-exact dequantized rows.
 //
 // Each value is (e2m1 * e4m3) * g computed as two FP32 multiplies in this order and rounded to nearest even into the
-// output dtype, as xtier/packs/qwen4_exp/qsa_fp4.py:94-101 and :142-143 compute it. One thread per 16-element block:
-// 8 payload bytes and one scale byte in, 32 bytes out.
+// output dtype, as xtier/packs/qwen4_exp/qsa_fp4.py:94-101 and :142-143 compute it. A thread handles 8-value pieces
+// (one payload dword and its scale byte in, 16 bytes out), several of them 256 apart with all loads in flight together;
+// the pieces of a request are numbered in output order, so a wave's stores cover consecutive bytes.
 #include "xt_common.h"
 #include "xt_host.h"
 
 namespace xt {
 namespace {
 
-// 16 output values of one block; `valid` false gives +0.0 everywhere (masked loads read 0 bytes).
-__device__ inline void dequant_block(const uint8_t* __restrict__ pay, const uint8_t* __restrict__ sf, float g,
-                                     bool valid, int out_dtype, void* __restrict__ dst) {
-  uint2 w = make_uint2(0u, 0u);
-  uint32_t sbyte = 0u;
-  if (valid) {
-    w = *reinterpret_cast<const uint2*>(pay);
-    sbyte = *sf;
-  }
+// Eight values of one NVFP4 block (one payload dword, its E4M3 scale byte), (e2m1 * e4m3) * g in FP32 in this order
+// (qsa_fp4.py:96-101), rounded to BF16 or FP16 (round to nearest even).
+__device__ inline uint4 dequant_piece(uint32_t w, uint32_t sbyte, float g, int out_dtype) {
   const float s = e4m3_decode(sbyte);
-  float v[16];
-  const uint32_t ws[2] = {w.x, w.y};
+  const float2_t v[4] = {fp4x2_to_f32<0>(w), fp4x2_to_f32<1>(w), fp4x2_to_f32<2>(w), fp4x2_to_f32<3>(w)};
+  uint32_t o[4];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    float2_t p0 = fp4x2_to_f32<0>(ws[k]);
-    float2_t p1 = fp4x2_to_f32<1>(ws[k]);
-    float2_t p2 = fp4x2_to_f32<2>(ws[k]);
-    float2_t p3 = fp4x2_to_f32<3>(ws[k]);
-    v[8 * k + 0] = p0.x; v[8 * k + 1] = p0.y; v[8 * k + 2] = p1.x; v[8 * k + 3] = p1.y;
-    v[8 * k + 4] = p2.x; v[8 * k + 5] = p2.y; v[8 * k + 6] = p3.x; v[8 * k + 7] = p3.y;
+  for (int e = 0; e < 4; ++e) {
+    const float a = (v[e].x * s) * g, b = (v[e].y * s) * g;
+    o[e] = out_dtype == XT_DTYPE_BF16 ? f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16)
+                                      : f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
   }
-  uint32_t o[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float a = (v[2 * e] * s) * g;
-    const float b = (v[2 * e + 1] * s) * g;
-    if (out_dtype == XT_DTYPE_BF16)
-      o[e] = f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
-    else
-      o[e] = f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
-  }
-  uint4* d = reinterpret_cast<uint4*>(dst);
-  d[0] = make_uint4(o[0], o[1], o[2], o[3]);
-  d[1] = make_uint4(o[4], o[5], o[6], o[7]);
+  return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
-__global__ void qsa_gather_kernel(const uint8_t* __restrict__ k_pay, const uint8_t* __restrict__ v_pay,
-                                  const uint8_t* __restrict__ k_sf, const uint8_t* __restrict__ v_sf,
-                                  const float* __restrict__ gk, const float* __restrict__ gv, int64_t pool_slots,
-                                  int heads, int dim, const int32_t* __restrict__ req_to_token, int64_t req_stride,
-                                  const int64_t* __restrict__ req_indices, const int32_t* __restrict__ indices,
-                                  int64_t idx_stride, const int32_t* __restrict__ seq_lens,
-                                  const int32_t* __restrict__ cu_k, uint16_t* __restrict__ out_k,
-                                  uint16_t* __restrict__ out_v, int out_dtype, int batch, int topk, int num_cols,
-                                  int zero_fill) {
-  const int blocks = dim / 16;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = (int64_t)batch * num_cols * heads * blocks;
-  if (i >= total) return;
-  const int blk = (int)(i % blocks);
-  const int h = (int)((i / blocks) % heads);
-  const int64_t bc = i / ((int64_t)blocks * heads);
-  const int c = (int)(bc % num_cols);
-  const int b = (int)(bc / num_cols);
+constexpr int kPieces = 8;   // 8-value output pieces per thread, 256 apart (all loads issued before the first use)
+
+// Decode gather (qsa_fp4.py:119-143): request b = blockIdx.y; its output is a run of 8-value pieces (column c, head h,
+// piece) in output order, so every store of a wave writes 1 KiB of consecutive rows. Column c < num_cols is valid when
+// c < cu_k[b+1] - cu_k[b], its position indices[b, c] (c < topk) lies in [0, seq_lens[b]) and the slot
+// req_to_token[req_indices[b], pos] in [0, pool_slots); valid columns are dequantized into rows cu_k[b] + c, invalid
+// ones are zeros when zero_fill (columns up to num_cols) and skipped otherwise.
+__global__ __launch_bounds__(256) void qsa_gather_kernel(
+    const uint8_t* __restrict__ k_pay, const uint8_t* __restrict__ v_pay, const uint8_t* __restrict__ k_sf,
+    const uint8_t* __restrict__ v_sf, const float* __restrict__ gk, const float* __restrict__ gv, int64_t pool_slots,
+    int heads, int piece_shift, const int32_t* __restrict__ req_to_token, int64_t req_stride,
+    const int64_t* __restrict__ req_indices, const int32_t* __restrict__ indices, int64_t idx_stride,
+    const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ cu_k, uint16_t* __restrict__ out_k,
+    uint16_t* __restrict__ out_v, int out_dtype, int topk, int num_cols, int zero_fill) {
+  const int b = blockIdx.y;
   const int32_t start = cu_k[b];
   const int32_t valid_count = cu_k[b + 1] - start;
   const int32_t length = seq_lens[b];
-  const int32_t pos = (c < topk) ? indices[(int64_t)b * idx_stride + c] : -1;
-  bool valid = (c < valid_count) && (pos >= 0) && (pos < length);
-  int64_t slot = 0;
-  if (valid) {
-    slot = req_to_token[req_indices[b] * req_stride + pos];
-    valid = slot >= 0 && slot < pool_slots;   // a slot outside the pool reads as an invalid column
+  const int32_t* tp = req_to_token + req_indices[b] * req_stride;
+  const int pieces = 1 << piece_shift;
+  const int items = num_cols * heads * pieces;
+  int c[kPieces], h[kPieces], pc[kPieces];
+  int32_t pos[kPieces];
+#pragma unroll
+  for (int u = 0; u < kPieces; ++u) {
+    const int g = (blockIdx.x * kPieces + u) * 256 + (int)threadIdx.x;
+    pc[u] = g & (pieces - 1);
+    const int hc = g >> piece_shift;
+    c[u] = hc / heads;
+    h[u] = hc - c[u] * heads;
+    pos[u] = (g < items && c[u] < topk && c[u] < valid_count) ? indices[(int64_t)b * idx_stride + c[u]] : -1;
   }
-  if (!valid && !zero_fill) return;
-  const int64_t row_bytes = (int64_t)heads * (dim / 2), row_scales = (int64_t)heads * (dim / 16);
-  const int64_t dst = ((int64_t)(start + c) * heads + h) * dim + blk * 16;
-  const int64_t po = slot * row_bytes + (int64_t)h * (dim / 2) + blk * 8;
-  const int64_t so = slot * row_scales + (int64_t)h * (dim / 16) + blk;
-  dequant_block(k_pay + po, k_sf + so, *gk, valid, out_dtype, out_k + dst);
-  dequant_block(v_pay + po, v_sf + so, *gv, valid, out_dtype, out_v + dst);
+  int64_t slot[kPieces];
+#pragma unroll
+  for (int u = 0; u < kPieces; ++u) {
+    slot[u] = (pos[u] >= 0 && pos[u] < length) ? tp[pos[u]] : -1;
+  }
+  uint32_t kw[kPieces], vw[kPieces], ks[kPieces], vs[kPieces];
+  const int64_t row_bytes = (int64_t)heads * (pieces * 4), row_scales = (int64_t)heads * (pieces / 2);
+#pragma unroll
+  for (int u = 0; u < kPieces; ++u) {
+    const bool valid = slot[u] >= 0 && slot[u] < pool_slots;   // a slot outside the pool reads as invalid
+    const int64_t sl = valid ? slot[u] : 0;
+    const int64_t po = sl * row_bytes + (int64_t)h[u] * (pieces * 4) + pc[u] * 4;
+    const int64_t so = sl * row_scales + (int64_t)h[u] * (pieces / 2) + (pc[u] >> 1);
+    kw[u] = valid ? *reinterpret_cast<const uint32_t*>(k_pay + po) : 0u;
+    vw[u] = valid ? *reinterpret_cast<const uint32_t*>(v_pay + po) : 0u;
+    ks[u] = valid ? k_sf[so] : 0u;
+    vs[u] = valid ? v_sf[so] : 0u;
+    if (!valid) slot[u] = -1;
+  }
+  const float g_k = *gk, g_v = *gv;
+#pragma unroll
+  for (int u = 0; u < kPieces; ++u) {
+    const int g = (blockIdx.x * kPieces + u) * 256 + (int)threadIdx.x;
+    if (g >= items || (slot[u] < 0 && !zero_fill)) continue;
+    const int64_t dst = ((int64_t)(start + c[u]) * heads + h[u]) * (pieces * 8) + pc[u] * 8;
+    *reinterpret_cast<uint4*>(out_k + dst) = dequant_piece(kw[u], ks[u], g_k, out_dtype);
+    *reinterpret_cast<uint4*>(out_v + dst) = dequant_piece(vw[u], vs[u], g_v, out_dtype);
+  }
 }
 
-__global__ void qsa_pack_kernel(const uint8_t* __restrict__ k_pay, const uint8_t* __restrict__ v_pay,
-                                const uint8_t* __restrict__ k_sf, const uint8_t* __restrict__ v_sf,
-                                const float* __restrict__ gk, const float* __restrict__ gv, int64_t pool_slots,
-                                int heads, int dim, const int32_t* __restrict__ req_to_token, int64_t sr0, int64_t sr1,
-                                const int64_t* __restrict__ req_indices, int batch, const int32_t* __restrict__ cu_k,
-                                int max_k, uint16_t* __restrict__ out_k, uint16_t* __restrict__ out_v,
-                                int out_dtype) {
-  const int blocks = dim / 16;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = (int64_t)batch * max_k * heads * blocks;
-  if (i >= total) return;
-  const int blk = (int)(i % blocks);
-  const int h = (int)((i / blocks) % heads);
-  const int64_t bt = i / ((int64_t)blocks * heads);
-  const int t = (int)(bt % max_k);
-  const int b = (int)(bt / max_k);
+// Prefix pack (qsa_fp4.py:146-162): request b = blockIdx.y writes its first cu_k[b+1] - cu_k[b] positions, in order,
+// into rows cu_k[b] + t, as 8-value pieces in output order (see qsa_gather_kernel); a slot outside the pool reads as
+// zeros.
+__global__ __launch_bounds__(256) void qsa_pack_kernel(
+    const uint8_t* __restrict__ k_pay, const uint8_t* __restrict__ v_pay, const uint8_t* __restrict__ k_sf,
+    const uint8_t* __restrict__ v_sf, const float* __restrict__ gk, const float* __restrict__ gv, int64_t pool_slots,
+    int heads, int piece_shift, const int32_t* __restrict__ req_to_token, int64_t sr0, int64_t sr1,
+    const int64_t* __restrict__ req_indices, const int32_t* __restrict__ cu_k, uint16_t* __restrict__ out_k,
+    uint16_t* __restrict__ out_v, int out_dtype) {
+  const int b = blockIdx.y;
   const int32_t start = cu_k[b];
-  if (t >= cu_k[b + 1] - start) return;
-  int64_t slot = req_to_token[req_indices[b] * sr0 + (int64_t)t * sr1];
-  const bool valid = slot >= 0 && slot < pool_slots;
-  if (!valid) slot = 0;
-  const int64_t row_bytes = (int64_t)heads * (dim / 2), row_scales = (int64_t)heads * (dim / 16);
-  const int64_t dst = ((int64_t)(start + t) * heads + h) * dim + blk * 16;
-  const int64_t po = slot * row_bytes + (int64_t)h * (dim / 2) + blk * 8;
-  const int64_t so = slot * row_scales + (int64_t)h * (dim / 16) + blk;
-  dequant_block(k_pay + po, k_sf + so, *gk, valid, out_dtype, out_k + dst);
-  dequant_block(v_pay + po, v_sf + so, *gv, valid, out_dtype, out_v + dst);
+  const int pieces = 1 << piece_shift;
+  const int items = (cu_k[b + 1] - start) * heads * pieces;
+  const int32_t* tp = req_to_token + req_indices[b] * sr0;
+  int t[kPieces], h[kPieces], pc[kPieces];
+  int64_t slot[kPieces];
+#pragma unroll
+  for (int u = 0; u < kPieces; ++u) {
+    const int g = (blockIdx.x * kPieces + u) * 256 + (int)threadIdx.x;
+    pc[u] = g & (pieces - 1);
+    const int ht = g >> piece_shift;
+    t[u] = ht / heads;
+    h[u] = ht - t[u] * heads;
+    slot[u] = g < items ? tp[(int64_t)t[u] * sr1] : -1;
+  }
+  uint32_t kw[kPieces], vw[kPieces], ks[kPieces], vs[kPieces];
+  const int64_t row_bytes = (int64_t)heads * (pieces * 4), row_scales = (int64_t)heads * (pieces / 2);
+#pragma unroll
+  for (int u = 0; u < kPieces; ++u) {
+    const bool valid = slot[u] >= 0 && slot[u] < pool_slots;
+    const int64_t sl = valid ? slot[u] : 0;
+    const int64_t po = sl * row_bytes + (int64_t)h[u] * (pieces * 4) + pc[u] * 4;
+    const int64_t so = sl * row_scales + (int64_t)h[u] * (pieces / 2) + (pc[u] >> 1);
+    kw[u] = valid ? *reinterpret_cast<const uint32_t*>(k_pay + po) : 0u;
+    vw[u] = valid ? *reinterpret_cast<const uint32_t*>(v_pay + po) : 0u;
+    ks[u] = valid ? k_sf[so] : 0u;
+    vs[u] = valid ? v_sf[so] : 0u;
+  }
+  const float g_k = *gk, g_v = *gv;
+#pragma unroll
+  for (int u = 0; u < kPieces; ++u) {
+    const int g = (blockIdx.x * kPieces + u) * 256 + (int)threadIdx.x;
+    if (g >= items) continue;
+    const int64_t dst = ((int64_t)(start + t[u]) * heads + h[u]) * (pieces * 8) + pc[u] * 8;
+    *reinterpret_cast<uint4*>(out_k + dst) = dequant_piece(kw[u], ks[u], g_k, out_dtype);
+    *reinterpret_cast<uint4*>(out_v + dst) = dequant_piece(vw[u], vs[u], g_v, out_dtype);
+  }
 }
 
 constexpr int kDequantPieces = 8;
@@ -210,12 +235,14 @@ extern "C" int xt_qsa_gather_nvfp4(const uint8_t* k_pay, const uint8_t* v_pay, c
   if (!req_to_token || !req_indices || !indices || !seq_lens || !cu_k || !out_k || !out_v)
     return fail(XT_EINVAL, "%s: a required pointer is null", what);
   if (!aligned(out_k, 16) || !aligned(out_v, 16)) return fail(XT_EINVAL, "%s: outputs must be 16-byte aligned", what);
-  const int64_t total = (int64_t)batch * num_cols * heads * (dim / 16);
-  hipLaunchKernelGGL(qsa_gather_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), k_pay, v_pay, k_scales, v_scales, gk, gv, pool_slots,
-                     heads, dim, req_to_token, req_stride, req_indices, indices, idx_stride, seq_lens, cu_k,
-                     static_cast<uint16_t*>(out_k), static_cast<uint16_t*>(out_v), out_dtype, batch, topk, num_cols,
-                     zero_fill_cols > 0 ? 1 : 0);
+  const int64_t per_req = (int64_t)num_cols * heads * (dim / 8);
+  if (per_req > 0x7FFFFFFFLL - 256 * kPieces || batch > 65535)
+    return fail(XT_EUNSUPPORTED, "%s: %lld pieces per request or %d requests", what, (long long)per_req, batch);
+  const dim3 grid((unsigned)((per_req + 256 * kPieces - 1) / (256 * kPieces)), (unsigned)batch);
+  hipLaunchKernelGGL(qsa_gather_kernel, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream), k_pay, v_pay,
+                     k_scales, v_scales, gk, gv, pool_slots, heads, __builtin_ctz((unsigned)(dim / 8)), req_to_token,
+                     req_stride, req_indices, indices, idx_stride, seq_lens, cu_k, static_cast<uint16_t*>(out_k),
+                     static_cast<uint16_t*>(out_v), out_dtype, topk, num_cols, zero_fill_cols > 0 ? 1 : 0);
   return check_launch(what);
 }
 
@@ -233,11 +260,14 @@ extern "C" int xt_qsa_pack_nvfp4(const uint8_t* k_pay, const uint8_t* v_pay, con
   if (!req_to_token || !req_indices || !cu_k || !out_k || !out_v)
     return fail(XT_EINVAL, "%s: a required pointer is null", what);
   if (!aligned(out_k, 16) || !aligned(out_v, 16)) return fail(XT_EINVAL, "%s: outputs must be 16-byte aligned", what);
-  const int64_t total = (int64_t)batch * max_k * heads * (dim / 16);
-  hipLaunchKernelGGL(qsa_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), k_pay, v_pay, k_scales, v_scales, gk, gv, pool_slots,
-                     heads, dim, req_to_token, sr0, sr1, req_indices, batch, cu_k, max_k,
-                     static_cast<uint16_t*>(out_k), static_cast<uint16_t*>(out_v), out_dtype);
+  const int64_t per_req = (int64_t)max_k * heads * (dim / 8);
+  if (per_req > 0x7FFFFFFFLL - 256 * kPieces || batch > 65535)
+    return fail(XT_EUNSUPPORTED, "%s: %lld pieces per request or %d requests", what, (long long)per_req, batch);
+  const dim3 grid((unsigned)((per_req + 256 * kPieces - 1) / (256 * kPieces)), (unsigned)batch);
+  hipLaunchKernelGGL(qsa_pack_kernel, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream), k_pay, v_pay,
+                     k_scales, v_scales, gk, gv, pool_slots, heads, __builtin_ctz((unsigned)(dim / 8)), req_to_token,
+                     sr0, sr1, req_indices, cu_k, static_cast<uint16_t*>(out_k), static_cast<uint16_t*>(out_v),
+                     out_dtype);
   return check_launch(what);
 }
 
