@@ -53,8 +53,11 @@ constexpr int kKTile = kMSteps * kKRow<F> * 2;
 template <int F>
 constexpr int kQChunks = kDk<F> / 32;    // 32-dim chunks of a query row
 template <int F>
-constexpr int kQReg = F == kNvfp4 ? 12 : 10;   // chunks kept in registers; the others live in LDS
-constexpr int kQRow = 32 + 16;           // 16-bit values per (chunk, head) row of the LDS query block
+constexpr int kQReg = F == kNvfp4 ? 9 : 7;     // chunks kept in registers; the others live in LDS
+constexpr int kQRow = 32;                // 16-bit values per (chunk, head) row of the LDS query block; the four 16-byte
+                                         // pieces of row r sit at piece ^ ((r >> 2) & 3), so the 16 rows a b128 read
+                                         // serves in one cycle fall on 16 distinct 4-bank groups
+constexpr int kQAhead = 2;               // chunks of K fragments read ahead of their QK MFMAs
 template <int F>
 constexpr int kQTile = (kQChunks<F> - kQReg<F>) * kMHeads * kQRow * 2;
 constexpr int kRescaleM = 8;
@@ -319,7 +322,7 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
     if (kk < kQR)
       qb[kk < kQR ? kk : 0] = h;
     else
-      *reinterpret_cast<short8_t*>(qs + ((kk - kQR) * kMHeads + 16 * wave + hl) * kQRow + 8 * j) = h;
+      *reinterpret_cast<short8_t*>(qs + ((kk - kQR) * kMHeads + 16 * wave + hl) * kQRow + 8 * (j ^ (hl >> 2))) = h;
   }
   float g0 = 1.0f, g1 = 1.0f;   // NVFP4 global scales (V4 has none)
   if constexpr (F == kNvfp4) {
@@ -346,36 +349,39 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
     load_raw<F, TWO>(a, slots, min(step + 2, a.steps - 1), raw);
     const uint32_t valid = (uint32_t)__builtin_amdgcn_ballot_w64(lane < kMSteps &&
                                                                   entry_valid(slots[step * kMSteps + (lane & 31)]));
-    // S^T for the two 16-key tiles, each as two independent MFMA chains (even / odd dim chunks)
-    float4_t s[2], s2[2];
+    // S^T for the two 16-key tiles, one MFMA chain each. The K fragments (and LDS-resident query chunks) of chunk
+    // kk + kQAhead are read while the MFMAs of chunk kk run; scheduling barriers keep that order, so an MFMA does not
+    // wait for a read issued just before it.
+    float4_t s[2] = {float4_t{0.f, 0.f, 0.f, 0.f}, float4_t{0.f, 0.f, 0.f, 0.f}};
+    short8_t kf[kQC][2], qf[kQC];
+    auto read_chunk = [&](int kk) {
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      s[tt] = float4_t{0.f, 0.f, 0.f, 0.f};
-      s2[tt] = float4_t{0.f, 0.f, 0.f, 0.f};
-    }
+      for (int tt = 0; tt < 2; ++tt)
+        kf[kk][tt] = *reinterpret_cast<const short8_t*>(kt + (16 * tt + hl) * kKRow<F> + 8 * j + 32 * kk);
+      qf[kk] = kk < kQR ? qb[kk < kQR ? kk : 0]
+                        : *reinterpret_cast<const short8_t*>(qs + ((kk - kQR) * kMHeads + 16 * wave + hl) * kQRow +
+                                                             8 * (j ^ (hl >> 2)));
+    };
+#pragma unroll
+    for (int kk = 0; kk < kQAhead; ++kk) read_chunk(kk);
 #pragma unroll
     for (int kk = 0; kk < kQC; ++kk) {
-      const short8_t qv = kk < kQR ? qb[kk < kQR ? kk : 0]
-                                     : *reinterpret_cast<const short8_t*>(
-                                           qs + ((kk - kQR) * kMHeads + 16 * wave + hl) * kQRow + 8 * j);
+      if (kk + kQAhead < kQC) read_chunk(kk + kQAhead);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const short8_t kv = *reinterpret_cast<const short8_t*>(kt + (16 * tt + hl) * kKRow<F> + 8 * j + 32 * kk);
-        if (kk & 1)
-          s2[tt] = mfma16<F>(kv, qv, s2[tt]);
-        else
-          s[tt] = mfma16<F>(kv, qv, s[tt]);
-      }
+      for (int tt = 0; tt < 2; ++tt) s[tt] = mfma16<F>(kf[kk][tt], qf[kk], s[tt]);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (F == kFp8V4) {
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) s[tt] = (F == kNvfp4) ? s[tt] + s2[tt] : (s[tt] + s2[tt]) * a.qscale;
+      for (int tt = 0; tt < 2; ++tt) s[tt] *= a.qscale;
+    }
     // online softmax of head hl over keys T(j), lazy rescale
+    // this lane's keys T(j) as bits 0..7: keys 4j .. 4j+3, then 16+4j .. 16+4j+3
+    const uint32_t vmask = ((valid >> (4 * j)) & 0xFu) | (((valid >> (16 + 4 * j)) & 0xFu) << 4);
     float sv[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int key = (e < 4) ? (4 * j + e) : (16 + 4 * j + (e - 4));
-      sv[e] = ((valid >> key) & 1u) ? s[e >> 2][e & 3] : -__builtin_inff();
-    }
+    for (int e = 0; e < 8; ++e) sv[e] = ((vmask >> e) & 1u) ? s[e >> 2][e & 3] : -__builtin_inff();
     float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
     mt = fmaxf(mt, __shfl_xor(mt, 16));
     mt = fmaxf(mt, __shfl_xor(mt, 32));
