@@ -55,8 +55,8 @@ constexpr int kQChunks = kDk<F> / 32;    // 32-dim chunks of a query row
 template <int F>
 constexpr int kQReg = F == kNvfp4 ? 9 : 7;     // chunks kept in registers; the others live in LDS
 constexpr int kQRow = 32;                // 16-bit values per (chunk, head) row of the LDS query block; the four 16-byte
-                                         // pieces of row r sit at piece ^ ((r >> 2) & 3), so the 16 rows a b128 read
-                                         // serves in one cycle fall on 16 distinct 4-bank groups
+                                         // pieces of row r sit at piece ^ ((r >> 1) & 3), which measures free of bank
+                                         // conflicts for the b128 reads of 16 rows x 4 pieces
 constexpr int kQAhead = 2;               // chunks of K fragments read ahead of their QK MFMAs
 template <int F>
 constexpr int kQTile = (kQChunks<F> - kQReg<F>) * kMHeads * kQRow * 2;
@@ -112,9 +112,10 @@ __device__ inline float4_t mfma16(short8_t a, short8_t b, float4_t c) {
 // Slot list entries: >= 0 a slot of cache 0, <= -2 slot (-e - 2) of cache 1, -1 no key.
 __device__ inline bool entry_valid(int32_t e) { return e != -1; }
 
-// Dequant mapping: thread t handles keys 4kq .. 4kq+3 (kq = t % 8) and latent dims 8c .. 8c+7 (c = t / 8), so a
-// wave's V^T writes spread over 8 key columns and 8 dim rows (no LDS bank conflicts); rope: key t / 8, part t % 8.
-// V4 (same mapping, all 512 dims): dims 8c .. 8c+7 are E4M3 bytes (c < 56) or BF16 rope values (c >= 56).
+// Dequant mapping: thread t handles keys 4kq .. 4kq+3 (kq = t / 64, the wave) and latent dims 8c .. 8c+7 (c = t % 64),
+// so a wave reads one key's record as one contiguous run and writes one 1 KiB K tile row per store (no LDS bank
+// conflicts); rope: key t / 8, part t % 8. V4 (same mapping, all 512 dims): dims 8c .. 8c+7 are E4M3 bytes (c < 56)
+// or BF16 rope values (c >= 56).
 template <int F>
 struct Raw;
 template <>
@@ -143,10 +144,10 @@ __device__ inline const CacheDev& cache_of(const MlaArgs& a, int32_t e, uint32_t
 
 template <int F, bool TWO>
 __device__ inline void load_raw(const MlaArgs& a, const int32_t* slots, int step, Raw<F>& r) {
-  const int t = threadIdx.x, kq = t & 7, c = t >> 3;
+  const int t = threadIdx.x, kq = t >> 6, c = t & 63;
   if constexpr (F == kFp8V4) {
     // token s of a cache: page s >> page_shift, row s & (page size - 1); data row at row * 576, scale row after the
-    // page's data rows at row * 8. c < 56 is uniform per wave (waves 0-6 read E4M3 bytes, wave 7 the rope).
+    // page's data rows at row * 8. Lanes c < 56 read E4M3 bytes, lanes 56-63 the rope.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t s;
@@ -186,7 +187,7 @@ __device__ inline void load_raw(const MlaArgs& a, const int32_t* slots, int step
 template <int F, bool TWO>
 __device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step, const Raw<F>& r, float g0, float g1,
                                uint16_t* kt) {
-  const int t = threadIdx.x, kq = t & 7, c = t >> 3;
+  const int t = threadIdx.x, kq = t >> 6, c = t & 63;
   if constexpr (F == kFp8V4) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -322,7 +323,7 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
     if (kk < kQR)
       qb[kk < kQR ? kk : 0] = h;
     else
-      *reinterpret_cast<short8_t*>(qs + ((kk - kQR) * kMHeads + 16 * wave + hl) * kQRow + 8 * (j ^ (hl >> 2))) = h;
+      *reinterpret_cast<short8_t*>(qs + ((kk - kQR) * kMHeads + 16 * wave + hl) * kQRow + 8 * (j ^ ((hl >> 1) & 3))) = h;
   }
   float g0 = 1.0f, g1 = 1.0f;   // NVFP4 global scales (V4 has none)
   if constexpr (F == kNvfp4) {
@@ -360,7 +361,7 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
         kf[kk][tt] = *reinterpret_cast<const short8_t*>(kt + (16 * tt + hl) * kKRow<F> + 8 * j + 32 * kk);
       qf[kk] = kk < kQR ? qb[kk < kQR ? kk : 0]
                         : *reinterpret_cast<const short8_t*>(qs + ((kk - kQR) * kMHeads + 16 * wave + hl) * kQRow +
-                                                             8 * (j ^ (hl >> 2)));
+                                                             8 * (j ^ ((hl >> 1) & 3)));
     };
 #pragma unroll
     for (int kk = 0; kk < kQAhead; ++kk) read_chunk(kk);
