@@ -142,6 +142,16 @@ __device__ inline const CacheDev& cache_of(const MlaArgs& a, int32_t e, uint32_t
   return a.c[e <= -2 ? 1 : 0];
 }
 
+// The slot entries of keys 4kq .. 4kq+3 of a step as one 16-byte LDS read, issued before any K tile write (a write
+// the compiler cannot tell apart from the slot list would otherwise order each entry's read after the previous write).
+__device__ inline void step_entries(const int32_t* slots, int step, int kq, int32_t (&e)[4]) {
+  const int4 v = *reinterpret_cast<const int4*>(slots + step * kMSteps + 4 * kq);
+  e[0] = v.x;
+  e[1] = v.y;
+  e[2] = v.z;
+  e[3] = v.w;
+}
+
 template <int F, bool TWO>
 __device__ inline void load_raw(const MlaArgs& a, const int32_t* slots, int step, Raw<F>& r) {
   const int t = threadIdx.x, kq = t >> 6, c = t & 63;
@@ -188,10 +198,12 @@ template <int F, bool TWO>
 __device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step, const Raw<F>& r, float g0, float g1,
                                uint16_t* kt) {
   const int t = threadIdx.x, kq = t >> 6, c = t & 63;
+  int32_t ent[4];
+  step_entries(slots, step, kq, ent);
   if constexpr (F == kFp8V4) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const bool ok = entry_valid(slots[step * kMSteps + 4 * kq + i]);
+      const bool ok = entry_valid(ent[i]);
       uint4 w;
       if (c < kV4Nope / 8) {
         // e4m3 * 2^(e - 127): the scaled conversion takes the scale's exponent, exact in BF16; e = 0 reads as 0
@@ -212,7 +224,7 @@ __device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step,
   } else {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int32_t e = slots[step * kMSteps + 4 * kq + i];
+    const int32_t e = ent[i];
     const float g = (TWO && e <= -2) ? g1 : g0;
     const float sg = entry_valid(e) ? (float)fp8x2_to_f16<false>(r.sc[i]).x * g : 0.0f;
     const _Float16 h = (_Float16)sg;
