@@ -126,7 +126,7 @@ struct Raw<kNvfp4> {
 };
 template <>
 struct Raw<kFp8V4> {
-  uint4 d[4];        // keys 4kq + i: E4M3 bytes 8c .. 8c+7 in (x, y), or rope values 8(c - 56) .. +7
+  uint4 d[4];        // keys 4kq + i: E4M3 bytes 8c .. 8c+7 in (x, y) (z, w unused), or rope values 8(c - 56) .. +7
   uint32_t sc[4];    // UE8M0 scale byte c / 8 of those keys (c < 56)
 };
 
@@ -155,30 +155,33 @@ __device__ inline void step_entries(const int32_t* slots, int step, int kq, int3
 template <int F, bool TWO>
 __device__ inline void load_raw(const MlaArgs& a, const int32_t* slots, int step, Raw<F>& r) {
   const int t = threadIdx.x, kq = t >> 6, c = t & 63;
+  int32_t ent[4];
+  step_entries(slots, step, kq, ent);
   if constexpr (F == kFp8V4) {
     // token s of a cache: page s >> page_shift, row s & (page size - 1); data row at row * 576, scale row after the
-    // page's data rows at row * 8. Lanes c < 56 read E4M3 bytes, lanes 56-63 the rope.
+    // page's data rows at row * 8. Lanes c < 56 take E4M3 bytes 8c .. 8c+7 and scale byte c / 8, lanes 56-63 rope
+    // bytes 448 + 16 (c - 56) .. +15; every lane makes the same two 8-byte loads and one byte load (bytes it does not
+    // use stay inside the token's records), so the wave does not branch.
+    const bool nope = c < kV4Nope / 8;
+    const uint32_t off = nope ? 8u * c : kV4Nope + 16u * (c - kV4Nope / 8);
+    const uint32_t sb = nope ? (uint32_t)c >> 3 : 0u;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t s;
-      const CacheDev& cd = cache_of<TWO>(a, slots[step * kMSteps + 4 * kq + i], s);
+      const CacheDev& cd = cache_of<TWO>(a, ent[i], s);
       const uint32_t ps = 1u << cd.page_shift, rw = s & (ps - 1u);
       const uint8_t* page = cd.pay + (uint64_t)(s >> cd.page_shift) * cd.page_bytes;
-      if (c < kV4Nope / 8) {
-        const uint2 v = *reinterpret_cast<const uint2*>(page + (uint64_t)rw * kV4Row + 8 * c);
-        r.d[i] = uint4{v.x, v.y, 0u, 0u};
-        r.sc[i] = page[(uint64_t)ps * kV4Row + (uint64_t)rw * 8 + (c >> 3)];
-      } else {
-        r.d[i] = *reinterpret_cast<const uint4*>(page + (uint64_t)rw * kV4Row + kV4Nope + 16 * (c - kV4Nope / 8));
-        r.sc[i] = 0u;
-      }
+      const uint8_t* rp = page + (uint64_t)rw * kV4Row + off;
+      const uint2 v0 = *reinterpret_cast<const uint2*>(rp), v1 = *reinterpret_cast<const uint2*>(rp + 8);
+      r.d[i] = uint4{v0.x, v0.y, v1.x, v1.y};
+      r.sc[i] = page[(uint64_t)ps * kV4Row + (uint64_t)rw * 8 + sb];
     }
     return;
   } else {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     uint32_t s;
-    const CacheDev& cd = cache_of<TWO>(a, slots[step * kMSteps + 4 * kq + i], s);
+    const CacheDev& cd = cache_of<TWO>(a, ent[i], s);
     r.pay[i] = *reinterpret_cast<const uint32_t*>(cd.pay + (uint64_t)s * cd.pay_stride + 4 * c);
     r.sc[i] = cd.sf[(uint64_t)s * cd.sf_stride + (c >> 1)];
   }
@@ -204,20 +207,20 @@ __device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step,
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const bool ok = entry_valid(ent[i]);
-      uint4 w;
-      if (c < kV4Nope / 8) {
-        // e4m3 * 2^(e - 127): the scaled conversion takes the scale's exponent, exact in BF16; e = 0 reads as 0
-        const float sc = __uint_as_float(r.sc[i] << 23);
-        const bf16x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.d[i].x, sc, false);
-        const bf16x2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.d[i].x, sc, true);
-        const bf16x2_t p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.d[i].y, sc, false);
-        const bf16x2_t p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.d[i].y, sc, true);
-        const bool live = ok && r.sc[i] != 0u;
-        w = uint4{live ? __builtin_bit_cast(uint32_t, p0) : 0u, live ? __builtin_bit_cast(uint32_t, p1) : 0u,
-                  live ? __builtin_bit_cast(uint32_t, p2) : 0u, live ? __builtin_bit_cast(uint32_t, p3) : 0u};
-      } else {
-        w = ok ? r.d[i] : uint4{0u, 0u, 0u, 0u};
-      }
+      // e4m3 * 2^(e - 127): the scaled conversion takes the scale's exponent, exact in BF16; e = 0 reads as 0. Rope
+      // lanes (c >= 56) keep their raw BF16 values; both forms are computed and one selected, without a branch.
+      const float sc = __uint_as_float(r.sc[i] << 23);
+      const bf16x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.d[i].x, sc, false);
+      const bf16x2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.d[i].x, sc, true);
+      const bf16x2_t p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.d[i].y, sc, false);
+      const bf16x2_t p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.d[i].y, sc, true);
+      const bool nope = c < kV4Nope / 8;
+      const bool live = ok && (!nope || r.sc[i] != 0u);
+      const uint4 w = uint4{
+          live ? (nope ? __builtin_bit_cast(uint32_t, p0) : r.d[i].x) : 0u,
+          live ? (nope ? __builtin_bit_cast(uint32_t, p1) : r.d[i].y) : 0u,
+          live ? (nope ? __builtin_bit_cast(uint32_t, p2) : r.d[i].z) : 0u,
+          live ? (nope ? __builtin_bit_cast(uint32_t, p3) : r.d[i].w) : 0u};
       *reinterpret_cast<uint4*>(kt + (4 * kq + i) * kKRow<F> + 8 * c) = w;
     }
     return;
