@@ -480,7 +480,9 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
 }
 
 // Split merge: one thread per (row, head, 8 dims); 64 threads cover a head's 512 dims with 16-byte loads.
-// out = sum_s w_s o_s with w_s = 2^(m_s - max m) l_s / (sum_s 2^(m_s - max m) l_s + sink term).
+// out = sum_s w_s o_s with w_s = 2^(m_s - max m) l_s / (sum_s 2^(m_s - max m) l_s + sink term). The splits are taken
+// four at a time with all their loads issued together and a running maximum across groups, so the usual four splits
+// cost one round trip.
 template <int F>
 __global__ void __launch_bounds__(256) mla_merge_kernel(const MlaArgs a, int rows) {
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -489,42 +491,62 @@ __global__ void __launch_bounds__(256) mla_merge_kernel(const MlaArgs a, int row
   const int c = (int)(t & 63);
   const int row = (int)(rh / a.heads), head = (int)(rh % a.heads);
   const int64_t base = (int64_t)row * a.splits * a.heads + head;   // (row, split 0, head)
-  float mx = -__builtin_inff();
-  for (int sp = 0; sp < a.splits; ++sp) mx = fmaxf(mx, a.ml[(base + (int64_t)sp * a.heads) * 2]);
-  const float mu = (mx == -__builtin_inff()) ? 0.0f : mx;
-  float l_all = 0.0f;
+  float m_run = -__builtin_inff(), l_run = 0.0f;
   float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int sp = 0; sp < a.splits; ++sp) {
-    const int64_t ph = base + (int64_t)sp * a.heads;
-    const float2 ml = *reinterpret_cast<const float2*>(a.ml + ph * 2);
-    const float w = __builtin_amdgcn_exp2f(ml.x - mu) * ml.y;
-    l_all += w;
-    if constexpr (F == kNvfp4) {
-      const uint4 x = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.part) + ph * kDl + 8 * c);
-      const uint32_t u[4] = {x.x, x.y, x.z, x.w};
+  for (int s0 = 0; s0 < a.splits; s0 += 4) {
+    float2 ml[4];
+    float x[4][8];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const half2_t h = __builtin_bit_cast(half2_t, u[e]);
-        o[2 * e] += w * (float)h.x;
-        o[2 * e + 1] += w * (float)h.y;
-      }
-    } else {
-      const float4_t* x = reinterpret_cast<const float4_t*>(static_cast<const float*>(a.part) + ph * kDl + 8 * c);
-      const float4_t x0 = x[0], x1 = x[1];
+    for (int i = 0; i < 4; ++i) {   // past the last split: the last one again, weight 0 below
+      const int64_t ph = base + (int64_t)min(s0 + i, a.splits - 1) * a.heads;
+      ml[i] = *reinterpret_cast<const float2*>(a.ml + ph * 2);
+      if constexpr (F == kNvfp4) {
+        const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.part) + ph * kDl + 8 * c);
+        const uint32_t u[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        o[e] += w * x0[e];
-        o[4 + e] += w * x1[e];
+        for (int e = 0; e < 4; ++e) {
+          const half2_t h = __builtin_bit_cast(half2_t, u[e]);
+          x[i][2 * e] = (float)h.x;
+          x[i][2 * e + 1] = (float)h.y;
+        }
+      } else {
+        const float4_t* v = reinterpret_cast<const float4_t*>(static_cast<const float*>(a.part) + ph * kDl + 8 * c);
+        const float4_t v0 = v[0], v1 = v[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[i][e] = v0[e];
+          x[i][4 + e] = v1[e];
+        }
       }
     }
+    float mc = m_run;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (s0 + i >= a.splits) ml[i].x = -__builtin_inff();
+      mc = fmaxf(mc, ml[i].x);
+    }
+    const float mu = (mc == -__builtin_inff()) ? 0.0f : mc;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - mu);
+    l_run *= alpha;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] *= alpha;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float w = __builtin_amdgcn_exp2f(ml[i].x - mu) * ml[i].y;
+      l_run += w;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] += w * x[i][e];
+    }
+    m_run = mc;
   }
-  float total = l_all;
+  const float mu = (m_run == -__builtin_inff()) ? 0.0f : m_run;
+  float total = l_run;
   if (a.sink) total += __builtin_amdgcn_exp2f(a.sink[head] * kLog2e - mu);
-  const float inv = l_all > 0.0f ? 1.0f / total : 0.0f;
+  const float inv = l_run > 0.0f ? 1.0f / total : 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] *= inv;
   store_vals(a, row, head, 8 * c, o, 8);
-  if (a.lse && c == 0) a.lse[rh] = l_all > 0.0f ? (mu + __builtin_log2f(l_all)) * kLn2 : -__builtin_inff();
+  if (a.lse && c == 0) a.lse[rh] = l_run > 0.0f ? (mu + __builtin_log2f(l_run)) * kLn2 : -__builtin_inff();
 }
 
 int check_cache(const char* what, const xt_mla_cache* c, int64_t* pay_stride, int64_t* sf_stride,
