@@ -183,8 +183,7 @@ __device__ inline void compute_step(const WaveCtx& w, int step, const Step& d, c
     sv[e] = ((valid >> key_of(j, e)) & 1u) ? x : -__builtin_inff();
   }
   float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-  mt = fmaxf(mt, __shfl_xor(mt, 16));
-  mt = fmaxf(mt, __shfl_xor(mt, 32));
+  mt = max4_lanes16(mt);
   if (__builtin_amdgcn_ballot_w64(mt > st.m + kRescale)) {   // rare after the first steps
     const float m_new = (mt > st.m + kRescale) ? mt : st.m;
     const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
@@ -415,8 +414,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
     for (int p = 0; p < P; ++p) compute_step(w, s0 + p, buf[p], qb, gk, vtile, st);
   }
   // the 4 lanes of a head hold disjoint key subsets of l
-  float l_tot = st.l + __shfl_xor(st.l, 16);
-  l_tot += __shfl_xor(l_tot, 32);
+  float l_tot = sum4_lanes16(st.l);
 
   // 2. tree merge of the slices through LDS: in each round the upper half of the remaining slices hands
   // (acc, max, sum) to the lower half

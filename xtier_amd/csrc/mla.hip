@@ -399,8 +399,7 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) sv[e] = ((vmask >> e) & 1u) ? s[e >> 2][e & 3] : -__builtin_inff();
     float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-    mt = fmaxf(mt, __shfl_xor(mt, 16));
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    mt = max4_lanes16(mt);
     if (__builtin_amdgcn_ballot_w64(mt > m + kRescaleM)) {
       const float m_new = (mt > m + kRescaleM) ? mt : m;
       const float alpha = __builtin_amdgcn_exp2f(m - m_new);
@@ -439,8 +438,7 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
     __syncthreads();
   }
   // the 4 lanes of a head hold disjoint key subsets of l
-  float l_tot = l + __shfl_xor(l, 16);
-  l_tot += __shfl_xor(l_tot, 32);
+  const float l_tot = sum4_lanes16(l);
 
   if (a.splits == 1) {
     if (!head_live) return;

@@ -103,8 +103,7 @@ __device__ inline void compute_vstep(const VarlenArgs& a, const VStep<D>& s, int
     sv[e] = vkey_of(j, e) < n_valid ? x : -__builtin_inff();
   }
   float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-  mt = fmaxf(mt, __shfl_xor(mt, 16));
-  mt = fmaxf(mt, __shfl_xor(mt, 32));
+  mt = max4_lanes16(mt);
   if (__builtin_amdgcn_ballot_w64(mt > st.m + kVRescale)) {
     const float m_new = (mt > st.m + kVRescale) ? mt : st.m;
     const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
@@ -219,8 +218,7 @@ __global__ void __launch_bounds__(512) varlen_kernel(const VarlenArgs a) {
       }
     }
   }
-  float l_tot = st.l + __shfl_xor(st.l, 16);
-  l_tot += __shfl_xor(l_tot, 32);
+  float l_tot = sum4_lanes16(st.l);
 
   // slices of a tile merge through LDS (the V tiles' space): slices > 0 hand over (acc, max, sum)
   __syncthreads();

@@ -75,6 +75,21 @@ template <bool HI>
 __device__ inline half2_t fp8x2_to_f16(uint32_t packed) {
   return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(packed, 1.0f, HI);
 }
+// Maximum and sum of x over lanes l, l ^ 16 and l ^ 32 (the four lanes 16 apart), in VALU permutes: with x as both
+// operands, v_permlane16_swap / v_permlane32_swap hand every lane the pair (x[l], x[l ^ 16]) / (x[l], x[l ^ 32]),
+// in an order that does not matter here (ds_bpermute would take two LDS round trips).
+__device__ inline float max4_lanes16(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ inline float sum4_lanes16(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 #else
 // The host pass parses device code without the gfx950 builtins; these declarations are never code-generated.
 template <int SEL>
@@ -83,6 +98,8 @@ template <int SEL>
 __device__ half2_t fp4x2_to_f16(uint32_t packed);
 template <bool HI>
 __device__ half2_t fp8x2_to_f16(uint32_t packed);
+__device__ float max4_lanes16(float x);
+__device__ float sum4_lanes16(float x);
 #endif
 
 // FP32 -> BF16 bits, round to nearest even; NaN -> quiet NaN with its sign.
