@@ -212,7 +212,7 @@ def run_mla(args, w, ops, workloads):
         pools = [build_latent_pool(w, 17 + l, args.layout, workloads, LatentPool) for l in range(layers)]
     inp = workloads.mla_inputs(w, 20261029, 'cuda')
     scale = 1.0 / math.sqrt(inp.q.shape[-1])
-    splits = args.splits or ops.default_mla_splits(w.rows, w.topk)
+    splits = args.splits or ops.default_mla_splits(w.rows, w.topk, w.fmt == 'fp8_v4')
     ws = ops.workspace('cuda', ops.mla_workspace_bytes(w.rows, w.heads, splits, v4=w.fmt == 'fp8_v4'))
     out = torch.empty(w.rows, w.heads, 512, dtype=torch.bfloat16, device='cuda')
     lse = torch.empty(w.rows, w.heads, dtype=torch.float32, device='cuda')

@@ -262,6 +262,11 @@ typedef struct {
 /* Device workspace of xt_sparse_mla_fp8 (FP32 split partials). */
 size_t xt_sparse_mla_fp8_workspace_bytes(int rows, int heads, int splits);
 
+/* The most keys (both lists together) one key split of xt_sparse_mla_nvfp4 (fp8 = 0) or xt_sparse_mla_fp8 (fp8 = 1)
+ * takes: its slot list shares the 160 KB of LDS with the key and query tiles, so rows * ceil(keys / this) splits is
+ * the fewest a call may ask for. No counterpart in the reference (its kernels take any top-k). */
+int xt_sparse_mla_max_split_keys(int fp8);
+
 /* Sparse MLA on DeepSeek V4 FP8 pages (replaces sparse_mla / _attend / _merge of sparse_mla.py:88-217 and the hook
  * flash_mla_with_kvcache :220-231 on that layout). As xt_sparse_mla_nvfp4, with key = value = [e4m3 * 2^(e - 127)
  * (448), rope (64)], 512 wide, and q BF16 [rows, heads, 512]: scores are q . key on BF16 operands with FP32

@@ -150,6 +150,25 @@ def test_mla_causal_prefill_rows():
     _check(out, lse, ref, ref_lse)
 
 
+def test_mla_long_key_list_takes_enough_splits():
+    """A key list longer than one split's LDS slot list holds (4000 keys) over many rows: the default split count
+    rises to fit (2 here, where the one-per-CU heuristic alone gives 1), and the result matches the oracle on sampled
+    rows."""
+    from xtier_amd import _lib
+    limit = _lib.lib().xt_sparse_mla_max_split_keys(0)
+    assert 2048 < limit < 4000
+    assert ops.default_mla_splits(288, 4000) == 2 and ops.default_mla_splits(288, 2048) == 1
+    w, inp = _case(71, rows=288, ctx=8192, topk=4000)
+    pool = _pool(w, 16)
+    scale = 1 / math.sqrt(576)
+    out, lse = ops.sparse_mla(inp.q, pool, inp.slots, None, None, scale)
+    rows = torch.tensor([0, 1, 143, 286, 287], device='cuda')
+    ref, ref_lse = _ref(inp.q[rows], pool, inp.slots[rows], None, None, scale)
+    _check(out[rows], lse[rows], ref, ref_lse)
+    with pytest.raises(NotImplementedError):
+        ops.sparse_mla(inp.q[:2], pool, inp.slots[:2], None, None, scale, splits=1)
+
+
 def test_mla_graph_replay_equals_eager():
     w, inp = _case(61, rows=8)
     pool = _pool(w, 15)

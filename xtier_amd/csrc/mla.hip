@@ -697,6 +697,11 @@ extern "C" size_t xt_sparse_mla_fp8_workspace_bytes(int rows, int heads, int spl
   return mla_workspace_bytes(rows, heads, splits, 4);
 }
 
+extern "C" int xt_sparse_mla_max_split_keys(int fp8) {
+  const size_t fixed = fp8 ? 2 * (size_t)kKTile<kFp8V4> + kQTile<kFp8V4> : 2 * (size_t)kKTile<kNvfp4> + kQTile<kNvfp4>;
+  return (int)(((160 * 1024 - 256 - fixed) / (kMSteps * 4) - 1) * kMSteps);   // one padding step in the slot list
+}
+
 extern "C" int xt_sparse_mla_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, int heads,
                                    int latent_dim, int rope_dim, const xt_mla_cache* cache, const xt_mla_keys* keys,
                                    const xt_mla_cache* extra_cache, const xt_mla_keys* extra_keys, const float* sink,

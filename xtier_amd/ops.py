@@ -471,9 +471,11 @@ def _mla_keys(indices, lengths, rows):
     return _lib.MlaKeys(_ptr(indices), indices.stride(0), indices.shape[1], _ptr(lengths)), (indices, lengths)
 
 
-def default_mla_splits(rows, topk):
-    """Key splits per row for sparse MLA: about 256 workgroups (one per CU) and at least 256 keys per split."""
-    return max(1, min(math.ceil(256 / max(1, rows)), max(1, topk // 256), 64))
+def default_mla_splits(rows, topk, v4=False):
+    """Key splits per row for sparse MLA: about 256 workgroups (one per CU) and at least 256 keys per split, and at
+    least enough that a split's slot list fits in LDS beside the key and query tiles."""
+    fit = math.ceil(topk / _lib.lib().xt_sparse_mla_max_split_keys(int(v4)))
+    return min(64, max(1, min(math.ceil(256 / max(1, rows)), max(1, topk // 256), 64), fit))
 
 
 def mla_workspace_bytes(rows, heads, splits, v4=False):
@@ -532,10 +534,11 @@ def sparse_mla(q, k_cache, indices, topk_length, attn_sink, softmax_scale, extra
         attn_sink = attn_sink.float().contiguous()
     topk_all = keys.topk + (keys2.topk if extra else 0)
     if splits is None:
-        splits = default_mla_splits(rows, topk_all)
+        splits = default_mla_splits(rows, topk_all, v4)
+        fewest = default_mla_splits(1 << 20, topk_all, v4)   # the LDS bound alone
         if ws is None and torch.cuda.is_current_stream_capturing() and rows and \
                 _cached_workspace_bytes(q.device) < mla_workspace_bytes(rows, heads, splits, v4):
-            splits = 1
+            splits = fewest
     need = mla_workspace_bytes(rows, heads, splits, v4)
     if ws is None:
         ws = (workspace(q.device, need) if _cached_workspace_bytes(q.device) >= need
