@@ -1,8 +1,8 @@
 """CPU oracle for the NVFP4-KV sparse-attention path: test infrastructure, not product code.
 
 A numpy restatement of the reference's algorithms (each function cites the reference file:line it follows). Only the
-test suite, ``__graft_entry__.smoke()`` and the CPU-baseline leg of ``bench.py`` may import this package, and only as
-the checker; the library under ``xtier_amd`` never calls into it.
+test suite, ``__graft_entry__.smoke()`` and the CPU-baseline leg of ``bench.py`` may import this package, and only to
+compare against or to time as a CPU baseline; the library under ``xtier_amd`` never calls into it.
 
 Pinning (what each function is checked against, in ``tests/``):
 - ``nvfp4.e2m1_*``: the 16-entry table the reference's tests hold (tests/draft_bf16_check.py:25,
@@ -15,5 +15,10 @@ Pinning (what each function is checked against, in ``tests/``):
   special cases (zero blocks, exact midpoints, negative values rounding to zero).
 - ``attention.*``: float64 softmax computed directly (no online/split form), single-key and empty-row special
   cases, split-K merge against one pass.
-- ``attention.sparse_mla``: float64 reference with sink and LSE, as tests/ds_sparse_mla_check.py:44-67.
+- ``attention.block_sparse_decode`` / ``block_sparse_prefill``: the token-granular ``sparse_decode`` on the expanded
+  block lists (with each query's position as the causal limit for the prefill); with every block listed, dense causal
+  softmax over the copied context.
+- ``attention.dequantize_context``: the NVFP4 dequantizer on each position's slot bytes.
+- ``attention.sparse_mla`` / ``sparse_mla_v4`` / ``v4_keys``: float64 reference with sink and LSE, as
+  tests/ds_sparse_mla_check.py:44-67; V4 page decoding against the exact keys of its packing rule.
 """
