@@ -129,3 +129,59 @@ def test_flash_mla_hook():
     assert torch.equal(got[0].view(torch.int16), want[0].view(torch.int16))
     assert deepseek.flash_mla_with_kvcache(lambda *a, **k: 'original', **dict(kw, is_fp8_kvcache=False)) == 'original'
     assert deepseek.flash_mla_with_kvcache(lambda *a, **k: 'original', **dict(kw, head_dim_v=448)) == 'original'
+
+
+REF_CACHES = None
+
+
+def _reference_caches():
+    """The caches of tests/ds_sparse_mla_check.py:108-120: a 16384-token window cache in pages of 256 and an 8192-slot
+    compressed cache in pages of 128, latents N(0, 1) times U(0, 4) per token."""
+    global REF_CACHES
+    if REF_CACHES is None:
+        g = torch.Generator().manual_seed(20261029)
+        lat1 = torch.randn(16384, 512, generator=g) * torch.rand(16384, 1, generator=g) * 4
+        lat2 = torch.randn(8192, 512, generator=g) * torch.rand(8192, 1, generator=g) * 4
+        c1, k1, _ = pack_v4(lat1, 256)
+        c2, k2, _ = pack_v4(lat2, 128)
+        REF_CACHES = (c1.cuda(), k1, c2.cuda(), k2)
+    return REF_CACHES
+
+
+@pytest.mark.parametrize('rows', [1, 2, 12, 300, 4096])
+@pytest.mark.parametrize('extra', [False, True])
+def test_v4_reference_case_matrix(rows, extra):
+    """The case matrix of tests/ds_sparse_mla_check.py:127-160: 128 heads, window lists of 128 with 10 % holes, a
+    valid first entry and lengths 1..128; compressed lists of 512 with 10 % holes and lengths 0..512 (the first
+    rows / 8 rows empty); the sink. All rows against the oracle (every 64th of the 4096)."""
+    print(f'v4 case rows={rows} extra={extra}', flush=True)
+    c1, k1, c2, k2 = _reference_caches()
+    g = torch.Generator().manual_seed(1000 * rows + extra)
+    heads = 128
+    q = (torch.randn(rows, 1, heads, 512, generator=g) * 2).to(torch.bfloat16)
+    idx1 = torch.randint(0, 16384, (rows, 1, 128), generator=g, dtype=torch.int32)
+    idx1[torch.rand(idx1.shape, generator=g) < 0.1] = -1
+    idx1[:, 0, 0] = torch.randint(0, 16384, (rows,), generator=g, dtype=torch.int32)
+    len1 = torch.randint(1, 129, (rows,), generator=g, dtype=torch.int32)
+    idx2 = len2 = None
+    if extra:
+        idx2 = torch.randint(0, 8192, (rows, 1, 512), generator=g, dtype=torch.int32)
+        idx2[torch.rand(idx2.shape, generator=g) < 0.1] = -1
+        len2 = torch.randint(0, 513, (rows,), generator=g, dtype=torch.int32)
+        len2[:max(1, rows // 8)] = 0
+    sink = torch.randn(heads, generator=g)
+    cuda = lambda t: None if t is None else t.cuda()
+    out, lse = ops.sparse_mla(q.cuda(), c1, idx1.cuda(), len1.cuda(), sink.cuda(), SCALE, c2 if extra else None,
+                              cuda(idx2), cuda(len2))
+    rows_checked = np.arange(0, rows, 64) if rows > 300 else np.arange(rows)
+    sel = torch.from_numpy(rows_checked)
+    ref, ref_lse = attention.sparse_mla_v4(q[sel, 0].float().numpy(), k1, idx1[sel, 0].numpy(), len1[sel].numpy(),
+                                           sink.numpy(), SCALE, k2 if extra else None,
+                                           idx2[sel, 0].numpy() if extra else None,
+                                           len2[sel].numpy() if extra else None)
+    nonempty = np.isfinite(ref_lse).any(1)
+    max_rel, rms_rel = _errors(out[sel.cuda(), 0], ref, nonempty)
+    assert max_rel < 1e-2 and rms_rel < 4e-3, (max_rel, rms_rel)
+    l_ = lse[sel.cuda(), :, 0].cpu().numpy()
+    fin = np.isfinite(ref_lse)
+    assert (np.isfinite(l_) == fin).all() and np.abs(l_[fin] - ref_lse[fin]).max() < 2e-3
