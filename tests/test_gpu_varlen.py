@@ -90,3 +90,45 @@ def test_varlen_graph_replay_equals_eager():
         eager = ops.varlen_decode(qd, kd, vd, cq, ck, 1, 1000, 0.1, splits=splits)
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int16), eager.view(torch.int16))
+
+
+def test_reference_qwen_case():
+    """tests/qsa_decode_check.py:47-113 as the reference runs it: Qwen3.8's shape (24 query heads over 2 KV heads,
+    head_dim 256, top-2048 packed rows), rows with 2048, 1, 0, 37, 128, 129, 1999 and 2048 keys, inputs drawn in the
+    reference's order from its seeded CPU generator (q 2 N(0,1), k 2 N(0,1), v N(0,1) in BF16). Errors against the
+    FP64 reference within the flash kernels' class (max <= 1.5x, mean <= 1.25x the flash-precision reference's), all
+    finite, the empty row exactly zero, and a graph replay on new queries equal to eager bit for bit."""
+    g = torch.Generator(device='cpu').manual_seed(20261029)
+    heads, kv_heads, dim, topk = 24, 2, 256, 2048
+    counts = [2048, 1, 0, 37, 128, 129, 1999, 2048]
+    rows = len(counts)
+    cu_k = torch.zeros(rows + 1, dtype=torch.int32)
+    cu_k[1:] = torch.cumsum(torch.tensor(counts), 0)
+    cu_q = torch.arange(rows + 1, dtype=torch.int32)
+    total = int(cu_k[-1])
+    q = (torch.randn((rows, heads, dim), generator=g) * 2).to(torch.bfloat16)
+    k = (torch.randn((total, kv_heads, dim), generator=g) * 2).to(torch.bfloat16)
+    v = torch.randn((total, kv_heads, dim), generator=g).to(torch.bfloat16)
+    scale = dim ** -0.5
+    qd, kd, vd, cq, ck = (t.cuda() for t in (q, k, v, cu_q, cu_k))
+    got = ops.varlen_decode(qd, kd, vd, cq, ck, 1, topk, scale)
+    ref, flash = _ref(q, k, v, cu_q, cu_k, scale)
+    err = np.abs(got.float().cpu().numpy().astype(np.float64) - ref)
+    ferr = np.abs(flash - ref)
+    assert np.isfinite(got.float().cpu().numpy()).all()
+    assert torch.equal(got[2].float().cpu(), torch.zeros(heads, dim))
+    assert err.max() <= 1.5 * ferr.max() and err.mean() <= 1.25 * ferr.mean(), (err.max(), ferr.max(), err.mean(),
+                                                                                ferr.mean())
+    # graph capture, then a replay on new query values against eager
+    qs = qd.clone()
+    ws = ops.workspace('cuda', ops.varlen_workspace_bytes(rows, heads, dim, ops.default_splits(rows, kv_heads, topk)))
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = ops.varlen_decode(qs, kd, vd, cq, ck, 1, topk, scale, ws=ws)
+    q2 = torch.randn(q.shape, generator=g).to(torch.bfloat16).cuda()
+    qs.copy_(q2)
+    graph.replay()
+    eager = ops.varlen_decode(q2, kd, vd, cq, ck, 1, topk, scale)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), eager.view(torch.int16))
