@@ -95,3 +95,52 @@ def test_gather_rejects_non_power_of_two_head():
         ops.gather(raw, z.view(1, 4), z[:1].long(), z.view(1, 4), z[:1], z[:2], torch.empty(4, 2, 96,
                    dtype=torch.bfloat16, device='cuda'), torch.empty(4, 2, 96, dtype=torch.bfloat16, device='cuda'),
                    1, 4)
+
+
+def test_reference_qwen_case():
+    """tests/qsa_fp4_check.py as the reference runs it: a 70000-token pool of 2 KV heads x 256 whose per-token
+    magnitudes spread over three decades, quantized with a unit global scale; requests [2, 0, 3] of a random
+    req_to_token [4, 120000] with lengths 50000 / 3000 / 69000 and 2048 / 1500 / 2000 valid top-k positions, gathered
+    compact and page-aligned (2112 columns, zero-filled); then the prefixes of requests [1, 3] (37000 and 64000
+    tokens) packed. Every output bit against the oracle reading the same pool bytes."""
+    heads, dim, rows = 2, 256, 70000
+    gen = torch.Generator(device='cuda').manual_seed(20261023)
+    one = torch.ones(1, dtype=torch.float32, device='cuda')
+    raw = []
+    for _ in range(2):
+        x = torch.randn(rows, heads, dim, generator=gen, device='cuda') * 10 ** (
+            torch.rand(rows, 1, 1, generator=gen, device='cuda') * 3 - 2)
+        pay = torch.empty(rows, heads, dim // 2, dtype=torch.uint8, device='cuda')
+        sf = torch.empty(rows, heads, dim // 16, dtype=torch.uint8, device='cuda')
+        ops.quantize_append(x.to(torch.bfloat16), torch.arange(rows, device='cuda'), one, pay, sf)
+        raw += [pay, sf]
+    raw = (raw[0], raw[2], raw[1], raw[3], one, one)
+    host = tuple(t.cpu().numpy() for t in raw[:4]) + (1.0, 1.0)
+    batch, topk, width = 3, 2048, 120000
+    r2t = torch.randint(0, rows, (4, width), generator=gen, device='cuda', dtype=torch.int32)
+    req = torch.tensor([2, 0, 3], dtype=torch.int64, device='cuda')
+    seq = torch.tensor([50000, 3000, 69000], dtype=torch.int32, device='cuda')
+    idx = torch.full((batch, topk), -1, dtype=torch.int32, device='cuda')
+    counts = (2048, 1500, 2000)
+    for b, n in enumerate(counts):
+        idx[b, :n] = torch.randperm(int(seq[b]), generator=gen, device='cuda')[:n].to(torch.int32)
+    cu_k = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int32, device='cuda')
+    h = lambda t: t.cpu().numpy()
+    for label, cu, zf in (('compact', cu_k, 0),
+                          ('page-aligned', torch.arange(batch + 1, dtype=torch.int32, device='cuda') * 2112, 2112)):
+        cap = int(cu[-1]) if not zf else batch * zf
+        out_k = torch.full((cap, heads, dim), CANARY, dtype=torch.int16, device='cuda').view(torch.bfloat16)
+        out_v = out_k.clone()
+        ops.gather(raw, r2t, req, idx, seq, cu, out_k, out_v, batch, topk, zf)
+        wk = np.full((cap, heads, dim), CANARY, np.uint16)
+        wv = wk.copy()
+        attention.gather_qsa(host, h(r2t), h(req), h(idx), h(seq), h(cu), wk, wv, batch, topk, zf)
+        assert np.array_equal(out_k.view(torch.int16).cpu().numpy().view(np.uint16), wk), label
+        assert np.array_equal(out_v.view(torch.int16).cpu().numpy().view(np.uint16), wv), label
+    p_req = torch.tensor([1, 3], dtype=torch.int64, device='cuda')
+    p_lens = [37000, 64000]
+    p_cu = torch.tensor(np.concatenate([[0], np.cumsum(p_lens)]), dtype=torch.int32, device='cuda')
+    pk, pv = ops.pack(raw, r2t, p_req, p_cu, sum(p_lens), max(p_lens), torch.bfloat16)
+    wk, wv = attention.pack_qsa(host, h(r2t), h(p_req), h(p_cu), sum(p_lens))
+    assert np.array_equal(pk.view(torch.int16).cpu().numpy().view(np.uint16), wk)
+    assert np.array_equal(pv.view(torch.int16).cpu().numpy().view(np.uint16), wv)
