@@ -96,6 +96,44 @@ def cpu_baseline(raw, q, pt, idx, seq, w, scale, seconds):
                       f'softmax attention, one thread, {cpu_model()}, {os.cpu_count()} host cores)'}
 
 
+def timed_sample(stage, run, total, seconds):
+    """A bounded CPU sample on one thread: stage(rows) copies what rows need to the host (untimed), run(data) is the
+    oracle's work on them. One row first, then as many rows (up to `total`) as fit in about `seconds`. Returns
+    (rows timed, seconds)."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    with threadpool_limits(1):
+        one = stage(np.array([0]))
+        t0 = time.perf_counter()
+        run(one)
+        per_row = time.perf_counter() - t0
+        n = int(max(1, min(total, seconds / max(per_row, 1e-6))))
+        data = stage(np.arange(n))
+        t0 = time.perf_counter()
+        run(data)
+        return n, time.perf_counter() - t0
+
+
+def port_record(value, unit, n, total, what, oracle):
+    return {'value': round(value, 6), 'unit': unit, 'cores': 1, 'kind': 'port',
+            'sample': f'{n} of {total} {what} (oracle: {oracle}, one thread, {cpu_model()}, {os.cpu_count()} host '
+                      'cores)'}
+
+
+def compact_rows(device_tensors, slots):
+    """Host copies of the rows `slots` (any shape) of each device tensor (BF16 ones as float32), and slots renumbered
+    into them."""
+    import numpy as np
+    import torch
+    uniq, inv = np.unique(np.asarray(slots), return_inverse=True)
+    sel = torch.from_numpy(uniq.astype(np.int64)).cuda()
+    host = []
+    for t in device_tensors:
+        r = t.index_select(0, sel)
+        host.append((r.float() if r.dtype == torch.bfloat16 else r).cpu().numpy())
+    return host, inv.reshape(np.shape(slots))
+
+
 def measured_traffic(workload, splits, layout):
     """HBM bytes per launch of the decode kernel from the committed rocprofv3 counter summary (FETCH_SIZE and
     WRITE_SIZE, each scaled by the counter's reading for a copy of known size), when it was taken on this exact
@@ -174,9 +212,38 @@ def run_prefill(args, w, ops, workloads, KVPool):
         'us_per_step': round(ms * 1e3, 2), 'gathered_gbs': round(gbs, 1),
         'roofline': {'bound': 'mfma', 'achieved': round(tflops, 2), 'peak': MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
                      'frac': round(tflops / MFMA_PEAK_TFLOPS, 4), 'traffic': None},
-        'cpu_baseline': None,
+        'cpu_baseline': None if args.no_cpu_baseline else prefill_cpu(pool, inp, w, scale, args.cpu_seconds),
     }
     print(json.dumps(record), flush=True)
+
+
+def prefill_cpu(pool, inp, w, scale, seconds):
+    """The oracle's causal sparse attention (gather through the page table, NVFP4 dequant, FP32 softmax) on a sample
+    of the chunk's query rows, after the step (the pool holds the chunk's rows)."""
+    import numpy as np
+    from oracle import attention
+    pt = inp.page_table[0].cpu().numpy()
+    idx, q_pos = inp.indices.cpu().numpy(), inp.q_pos.cpu().numpy()
+    qf = inp.q.float().cpu().numpy()
+
+    def stage(rows):
+        pos = idx[rows]
+        slots = pt[pos // w.page].astype(np.int64) * w.page + pos % w.page
+        (k, v, ksf, vsf), inv = compact_rows(pool.raw[:4], slots)
+        table = np.zeros((1, w.ctx), np.int32)
+        table[0, pos] = inv
+        host = (k, v, ksf, vsf, pool.raw[4].item(), pool.raw[5].item())
+        return rows, host, table
+
+    def run(data):
+        rows, host, table = data
+        attention.sparse_decode(qf[rows], host, table, 1, np.zeros(len(rows), np.int64), idx[rows], None,
+                                np.full(len(rows), w.ctx), scale, query_pos=q_pos[rows], dtype=np.float32)
+
+    n, dt = timed_sample(stage, run, w.chunk, seconds)
+    flops = n * w.q_heads * w.topk * 4 * w.dim
+    return port_record(flops / dt / 1e12, 'TFLOP/s', n, w.chunk, 'query rows of the chunk',
+                       'numpy gather + NVFP4 dequant + FP32 causal softmax attention')
 
 
 def build_latent_pool(w, seed, layout, workloads, LatentPool, chunk=1 << 20):
@@ -255,9 +322,49 @@ def run_mla(args, w, ops, workloads):
         'us_per_step': round(ms * 1e3, 2), 'gathered_gbs': round(gbs, 1),
         'roofline': {'bound': 'mfma', 'achieved': round(tflops, 2), 'peak': MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
                      'frac': round(tflops / MFMA_PEAK_TFLOPS, 4), 'traffic': None},
-        'cpu_baseline': None,
+        'cpu_baseline': None if args.no_cpu_baseline else mla_cpu(pools[0], inp, w, scale, args.cpu_seconds),
     }
     print(json.dumps(record), flush=True)
+
+
+def mla_cpu(cache, inp, w, scale, seconds):
+    """The oracle's sparse MLA (key decoding from the cache bytes, FP32 softmax over the row's keys) on a sample of
+    rows: the NVFP4 latent + rope cache, or the V4 FP8 pages."""
+    import numpy as np
+    import torch
+    from oracle import attention
+    slots = inp.slots.cpu().numpy()
+    qf = inp.q.float().cpu().numpy()
+    v4 = w.fmt == 'fp8_v4'
+    if v4:
+        stride = w.page * 584
+        flat = torch.as_strided(cache, (cache.shape[0] * stride,), (1,))
+
+    def stage(rows):
+        tok = slots[rows]
+        if not v4:
+            (pay, sc, rope), inv = compact_rows((cache.pay, cache.scales, cache.rope), tok)
+            return rows, (pay, sc, rope, np.float32(cache.g.item())), inv
+        uniq, inv = np.unique(tok, return_inverse=True)
+        t = torch.from_numpy(uniq.astype(np.int64)).cuda()
+        base = (t // w.page) * stride
+        row = t % w.page
+        data = flat[(base + row * 576)[:, None] + torch.arange(576, device='cuda')[None, :]]
+        sc = flat[(base + w.page * 576 + row * 8)[:, None] + torch.arange(8, device='cuda')[None, :]]
+        return rows, torch.cat([data, sc], 1).cpu().numpy(), inv.reshape(tok.shape)
+
+    def run(data):
+        rows, cache_h, inv = data
+        if v4:
+            keys = attention.v4_keys(cache_h.reshape(-1), 1, 584, tokens=cache_h.shape[0])
+            attention.sparse_mla_v4(qf[rows], keys, inv, None, None, scale)
+        else:
+            attention.sparse_mla(qf[rows], *cache_h, inv, None, None, scale, dtype=np.float32)
+
+    n, dt = timed_sample(stage, run, w.rows, seconds)
+    flops = w.flops() / w.rows * n
+    what = 'numpy V4 FP8 page decoding + FP64' if v4 else 'numpy NVFP4 latent dequant + FP32'
+    return port_record(flops / dt / 1e12, 'TFLOP/s', n, w.rows, 'rows', what + " softmax attention over the row's keys")
 
 
 def build_block_pool(w, gen, workloads, ops):
@@ -328,9 +435,30 @@ def run_block(args, w, ops, workloads):
         'us_per_layer_step': round(ms * 1e3, 3), 'tokens_per_s': round(w.batch / (ms * 1e-3), 1),
         'roofline': {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None},
-        'cpu_baseline': None,
+        'cpu_baseline': None if args.no_cpu_baseline else block_cpu(pools[0], inp, w, args.cpu_seconds),
     }
     print(json.dumps(record), flush=True)
+
+
+def block_cpu(pool, inp, w, seconds):
+    """The oracle's block-sparse decode (per KV head: the listed blocks' NVFP4 rows dequantized, FP32 softmax) on a
+    sample of the requests of one layer-step."""
+    import numpy as np
+    from oracle import attention
+    host = [t.cpu().numpy() for t in pool]          # k_pay, k_sc, v_pay, v_sc pages
+    r2t, sid = inp.req_to_token.cpu().numpy(), inp.slot_ids.cpu().numpy()
+    idx, seq = inp.topk_idx.cpu().numpy(), inp.seq_lens.cpu().numpy()
+    qf = inp.q.float().cpu().numpy()
+    f32 = lambda q, k, v, valid, sc: attention.softmax_attention(q, k, v, valid, sc, np.float32)
+
+    def run(rows):
+        attention.block_sparse_decode(qf[rows], *host, r2t, sid[rows], idx[:, rows], seq[rows], w.block,
+                                      w.dim ** -0.5, attend=f32)
+
+    n, dt = timed_sample(lambda rows: rows, run, w.batch, seconds)
+    nbytes = w.algorithmic_bytes() / w.batch * n
+    return port_record(nbytes / dt / 1e9, 'GB/s', n, w.batch, 'requests of one layer-step',
+                       'numpy NVFP4 block dequant + FP32 softmax attention per KV head')
 
 
 def run_block_prefill(args, w, ops, workloads):
@@ -408,9 +536,32 @@ def run_block_prefill(args, w, ops, workloads):
                          'frac_hbm': round(copy_gbs / HBM_PEAK_GBS, 4)},
         'roofline': {'bound': 'mfma', 'achieved': round(tflops, 2), 'peak': MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
                      'frac': round(tflops / MFMA_PEAK_TFLOPS, 4), 'traffic': None},
-        'cpu_baseline': None,
+        'cpu_baseline': None if args.no_cpu_baseline else block_prefill_cpu(pools[0], inp, w, args.cpu_seconds),
     }
     print(json.dumps(record), flush=True)
+
+
+def block_prefill_cpu(pool, inp, w, seconds):
+    """The oracle's causal block-sparse prefill (per-token slot lookups, NVFP4 dequant, FP32 softmax) on a sample of
+    the chunk's query rows."""
+    import numpy as np
+    from oracle import attention
+    host = [t.cpu().numpy() for t in pool]
+    r2t = inp.req_to_token.cpu().numpy()
+    idx = inp.topk_idx.cpu().numpy()
+    qf = inp.q.float().cpu().numpy()
+    f32 = lambda q, k, v, valid, sc: attention.softmax_attention(q, k, v, valid, sc, np.float32)
+
+    def run(rows):
+        n = len(rows)
+        one = np.arange(n + 1)
+        attention.block_sparse_prefill(qf[rows], *host, r2t, np.zeros(n, np.int64), idx[:, rows], one, one,
+                                       np.full(n, w.ctx), w.prefix + rows, 1, w.block, w.dim ** -0.5, attend=f32)
+
+    n, dt = timed_sample(lambda rows: rows, run, w.q_len, seconds)
+    flops = w.flops() / w.q_len * n
+    return port_record(flops / dt / 1e12, 'TFLOP/s', n, w.q_len, 'query rows of the chunk',
+                       'numpy per-token slot lookup + NVFP4 dequant + FP32 causal softmax attention')
 
 
 GATHER_WORKLOADS = {
@@ -481,9 +632,52 @@ def run_gather(args, name, ops, workloads, KVPool):
         'us_per_layer_step': round(ms * 1e3, 3), 'bytes_per_step': nbytes,
         'roofline': {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None},
-        'cpu_baseline': None,
+        'cpu_baseline': None if args.no_cpu_baseline else gather_cpu(mode, pools[0], r2t, idx, w, args.cpu_seconds),
     }
     print(json.dumps(record), flush=True)
+
+
+def gather_cpu(mode, raw, r2t, idx, w, seconds):
+    """The oracle's gather (decode rows) or pack (a prefix) into BF16 rows on a sample: requests of the decode
+    workload, or the first positions of the prefix."""
+    import numpy as np
+    from oracle import attention
+    r2t_h = r2t.cpu().numpy()
+    per_row = w.kv_heads * (2 * (w.dim // 2 + w.dim // 16) + 2 * w.dim * 2)   # bytes per (request column, all heads)
+    if mode == 'gather':
+        idx_h = idx.cpu().numpy()
+
+        def stage(rows):
+            pos = idx_h[rows]
+            (k, v, ksf, vsf), inv = compact_rows(raw[:4], r2t_h[rows[:, None], pos])
+            table = np.zeros((len(rows), w.ctx), np.int32)
+            table[np.arange(len(rows))[:, None], pos] = inv
+            return rows, (k, v, ksf, vsf, raw[4].item(), raw[5].item()), table
+
+        def run(data):
+            rows, host, table = data
+            n = len(rows)
+            out = np.zeros((n * w.topk, w.kv_heads, w.dim), np.uint16)
+            attention.gather_qsa(host, table, np.arange(n), idx_h[rows], np.full(n, w.ctx),
+                                 np.arange(n + 1) * w.topk, out, out.copy(), n, w.topk)
+
+        n, dt = timed_sample(stage, run, w.batch, seconds)
+        return port_record(n * w.topk * per_row / dt / 1e9, 'GB/s', n, w.batch, 'requests',
+                           'numpy NVFP4 dequant into BF16 rows')
+    chunk = 512
+
+    def stage(rows):
+        m = len(rows) * chunk
+        (k, v, ksf, vsf), inv = compact_rows(raw[:4], r2t_h[0, :m])
+        return m, (k, v, ksf, vsf, raw[4].item(), raw[5].item()), inv[None, :].astype(np.int32)
+
+    def run(data):
+        m, host, table = data
+        attention.pack_qsa(host, table, np.zeros(1, np.int64), np.array([0, m]), m)
+
+    n, dt = timed_sample(stage, run, w.ctx // chunk, seconds)
+    return port_record(n * chunk * per_row / dt / 1e9, 'GB/s', n * chunk, w.ctx, 'positions of the prefix',
+                       'numpy NVFP4 dequant into BF16 rows')
 
 
 def run_varlen(args, w, ops, workloads):
@@ -538,9 +732,30 @@ def run_varlen(args, w, ops, workloads):
         'us_per_layer_step': round(ms * 1e3, 3),
         'roofline': {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None},
-        'cpu_baseline': None,
+        'cpu_baseline': None if args.no_cpu_baseline else varlen_cpu(q, kv[0], w, scale, args.cpu_seconds),
     }
     print(json.dumps(record), flush=True)
+
+
+def varlen_cpu(q, kv, w, scale, seconds):
+    """The oracle's split-K decode over packed BF16 rows (128-key partials, FP64 merge) on a sample of rows."""
+    import numpy as np
+    from oracle import attention
+    qf = q.float().cpu().numpy()
+
+    def stage(rows):
+        n = len(rows)
+        k, v = (t[:n * w.keys].float().cpu().numpy() for t in kv)
+        return rows, k, v
+
+    def run(data):
+        rows, k, v = data
+        n = len(rows)
+        attention.varlen_decode(qf[rows], k, v, np.arange(n + 1), np.arange(n + 1) * w.keys, scale)
+
+    n, dt = timed_sample(stage, run, w.rows, seconds)
+    return port_record(w.algorithmic_bytes() / w.rows * n / dt / 1e9, 'GB/s', n, w.rows, 'rows',
+                       'numpy split-K softmax attention with FP64 merge')
 
 
 def main():
