@@ -58,6 +58,7 @@ constexpr int kQRow = 32;                // 16-bit values per (chunk, head) row 
                                          // pieces of row r sit at piece ^ ((r >> 1) & 3), which measures free of bank
                                          // conflicts for the b128 reads of 16 rows x 4 pieces
 constexpr int kQAhead = 2;               // chunks of K fragments read ahead of their QK MFMAs
+constexpr int kSlotIters = 11;           // slot list entries per thread: (max keys per split + 32) / 512, rounded up
 template <int F>
 constexpr int kQTile = (kQChunks<F> - kQReg<F>) * kMHeads * kQRow * 2;
 constexpr int kRescaleM = 8;
@@ -266,6 +267,14 @@ __device__ inline void store_vals(const MlaArgs& a, int64_t row, int head, int d
 }
 
 
+// Element index of a split partial in the accumulators' lane order: (row, split, wave of 16 heads, dim-tile pair k,
+// lane) holds 8 values, head 16 wave + lane % 16, dims 32k + 4 (lane / 16) .. +3 then 32k + 16 + 4 (lane / 16) .. +3;
+// heads are padded to whole waves.
+__device__ inline int64_t part_index(const MlaArgs& a, int64_t row, int split, int wave, int k, int lane) {
+  const int waves = (a.heads + 15) >> 4;
+  return ((((row * a.splits + split) * waves + wave) * 16 + k) * 64 + lane) * 8;
+}
+
 template <int F, bool TWO>
 __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
   constexpr int kQC = kQChunks<F>, kQR = kQReg<F>;
@@ -288,32 +297,37 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
   uint16_t* qs = reinterpret_cast<uint16_t*>(lds + 2 * kKTile<F>);
   int32_t* slots = reinterpret_cast<int32_t*>(lds + 2 * kKTile<F> + kQTile<F>);
 
-  // the query's B operands first: dims 32kk + 8j .. +7 of head `head` (a clamped valid head for padding lanes)
+  // 1. the split's key list: columns [t0, t0 + keys_per_split) of list 0 then list 1, as slot entries in LDS. The
+  //    list lengths are uniform scalar loads; every thread's index loads (kSlotIters, 512 apart) issue together and
+  //    before the query's loads, so that waiting for them does not wait for those.
+  const int t0 = split * a.keys_per_split;
+  const int total = (a.steps + 1) * kMSteps;   // one padding step of invalid keys
+  const int n0 = a.len[0] ? min(a.len[0][row], a.topk[0]) : a.topk[0];
+  const int n1 = a.len[1] ? min(a.len[1][row], a.topk[1]) : a.topk[1];
+  int32_t sraw[kSlotIters];
+#pragma unroll
+  for (int u = 0; u < kSlotIters; ++u) {
+    const int i = (int)threadIdx.x + 512 * u;
+    const int col = t0 + i;
+    const int li = col < a.topk[0] ? 0 : 1;
+    const int cc = col - (li ? a.topk[0] : 0);
+    sraw[u] = (i < a.keys_per_split && cc < (li ? n1 : n0)) ? a.idx[li][row * a.idx_stride[li] + cc] : -1;
+  }
+
+  // the query's B operands: dims 32kk + 8j .. +7 of head `head` (a clamped valid head for padding lanes)
   uint4 qraw[kQC];
   {
     const uint16_t* qp = a.q + row * a.q_rs + (int64_t)min(head, a.heads - 1) * a.q_hs;
 #pragma unroll
     for (int kk = 0; kk < kQC; ++kk) qraw[kk] = *reinterpret_cast<const uint4*>(qp + 32 * kk + 8 * j);
   }
-
-  // 1. the split's key list: columns [t0, t0 + keys_per_split) of list 0 then list 1, as slot entries in LDS
-  const int t0 = split * a.keys_per_split;
-  {
-    const int total = (a.steps + 1) * kMSteps;   // one padding step of invalid keys
-    for (int i = threadIdx.x; i < total; i += 512) {
-      const int col = t0 + i;
-      int32_t e = -1;
-      if (i < a.keys_per_split) {
-        const int li = col < a.topk[0] ? 0 : 1;
-        const int cc = col - (li ? a.topk[0] : 0);
-        if (cc < a.topk[li]) {
-          const int n = a.len[li] ? min(a.len[li][row], a.topk[li]) : a.topk[li];
-          const int32_t s = cc < n ? a.idx[li][row * a.idx_stride[li] + cc] : -1;
-          if (s >= 0 && s < a.c[li].slots) e = li ? -s - 2 : s;
-        }
-      }
-      slots[i] = e;
-    }
+#pragma unroll
+  for (int u = 0; u < kSlotIters; ++u) {
+    const int i = (int)threadIdx.x + 512 * u;
+    const int li = t0 + i < a.topk[0] ? 0 : 1;
+    const int32_t sv = sraw[u];
+    const int32_t e = (sv >= 0 && sv < a.c[li].slots) ? (li ? -sv - 2 : sv) : -1;
+    if (i < total) slots[i] = e;
   }
   __syncthreads();
 
@@ -456,39 +470,47 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
     return;
   }
   // 2. the split's output normalized by its own sum (NVFP4: FP16, a convex combination of FP16 latent values; V4:
-  //    FP32) plus its max and sum; a second launch merges the splits
-  if (head_live) {
-    const int64_t ph = ((int64_t)row * a.splits + split) * a.heads + head;
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if constexpr (F == kNvfp4) {
-      uint16_t* pp = static_cast<uint16_t*>(a.part) + ph * kDl;
+  //    FP32) plus its max and sum; a second launch merges the splits. The partials are stored in the accumulators'
+  //    lane order (part_index), so every store of a wave writes one contiguous run.
+  if (16 * wave >= a.heads) return;   // a wave without live heads has no partials (heads pad to whole waves only)
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  const int64_t pbase = part_index(a, row, split, wave, 0, lane);
+  if constexpr (F == kNvfp4) {
+    uint16_t* pp = static_cast<uint16_t*>(a.part) + pbase;
 #pragma unroll
-      for (int dt = 0; dt < 32; ++dt) {
-        const uint2 w = {f32_to_f16_bits(acc[dt][0] * inv) | (f32_to_f16_bits(acc[dt][1] * inv) << 16),
-                         f32_to_f16_bits(acc[dt][2] * inv) | (f32_to_f16_bits(acc[dt][3] * inv) << 16)};
-        *reinterpret_cast<uint2*>(pp + 16 * dt + 4 * j) = w;
-      }
-    } else {
-      float* pp = static_cast<float*>(a.part) + ph * kDl;
-#pragma unroll
-      for (int dt = 0; dt < 32; ++dt) *reinterpret_cast<float4_t*>(pp + 16 * dt + 4 * j) = acc[dt] * inv;
+    for (int k = 0; k < 16; ++k) {
+      const float4_t x = acc[2 * k] * inv, y = acc[2 * k + 1] * inv;
+      *reinterpret_cast<uint4*>(pp + k * 512) =
+          uint4{f32_to_f16_bits(x[0]) | (f32_to_f16_bits(x[1]) << 16), f32_to_f16_bits(x[2]) | (f32_to_f16_bits(x[3]) << 16),
+                f32_to_f16_bits(y[0]) | (f32_to_f16_bits(y[1]) << 16), f32_to_f16_bits(y[2]) | (f32_to_f16_bits(y[3]) << 16)};
     }
-    if (j == 0) *reinterpret_cast<float2*>(a.ml + ph * 2) = float2{m, l_tot};
+  } else {
+    float* pp = static_cast<float*>(a.part) + pbase;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      reinterpret_cast<float4_t*>(pp + k * 512)[0] = acc[2 * k] * inv;
+      reinterpret_cast<float4_t*>(pp + k * 512)[1] = acc[2 * k + 1] * inv;
+    }
   }
+  if (head_live && j == 0)
+    *reinterpret_cast<float2*>(a.ml + (((int64_t)row * a.splits + split) * a.heads + head) * 2) = float2{m, l_tot};
 }
 
-// Split merge: one thread per (row, head, 8 dims); 64 threads cover a head's 512 dims with 16-byte loads.
-// out = sum_s w_s o_s with w_s = 2^(m_s - max m) l_s / (sum_s 2^(m_s - max m) l_s + sink term). The splits are taken
-// four at a time with all their loads issued together and a running maximum across groups, so the usual four splits
-// cost one round trip.
+// Split merge: thread = (row, wave w, dim-tile pair k, lane) of the partials' lane order: head 16w + lane % 16, dims
+// 32k + 4 (lane / 16) .. +3 and 32k + 16 + 4 (lane / 16) .. +3. out = sum_s w_s o_s with w_s = 2^(m_s - max m) l_s /
+// (sum_s 2^(m_s - max m) l_s + sink term). The splits are taken four at a time with all their loads issued together and
+// a running maximum across groups, so the usual four splits cost one round trip; a wave's loads of one split are one
+// contiguous run.
 template <int F>
 __global__ void __launch_bounds__(256) mla_merge_kernel(const MlaArgs a, int rows) {
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t rh = t >> 6;                  // row * heads + head
-  if (rh >= (int64_t)rows * a.heads) return;
-  const int c = (int)(t & 63);
-  const int row = (int)(rh / a.heads), head = (int)(rh % a.heads);
-  const int64_t base = (int64_t)row * a.splits * a.heads + head;   // (row, split 0, head)
+  const int lane = (int)(t & 63), k = (int)((t >> 6) & 15);
+  const int64_t rw = t >> 10;                 // row * waves + w
+  const int waves = (a.heads + 15) >> 4;
+  if (rw >= (int64_t)rows * waves) return;
+  const int row = (int)(rw / waves), w = (int)(rw % waves);
+  const int head = 16 * w + (lane & 15), d0 = 32 * k + 4 * (lane >> 4);
+  if (head >= a.heads) return;
   float m_run = -__builtin_inff(), l_run = 0.0f;
   float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < a.splits; s0 += 4) {
@@ -496,10 +518,11 @@ __global__ void __launch_bounds__(256) mla_merge_kernel(const MlaArgs a, int row
     float x[4][8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {   // past the last split: the last one again, weight 0 below
-      const int64_t ph = base + (int64_t)min(s0 + i, a.splits - 1) * a.heads;
-      ml[i] = *reinterpret_cast<const float2*>(a.ml + ph * 2);
+      const int sp = min(s0 + i, a.splits - 1);
+      ml[i] = *reinterpret_cast<const float2*>(a.ml + (((int64_t)row * a.splits + sp) * a.heads + head) * 2);
+      const int64_t pi = part_index(a, row, sp, w, k, lane);
       if constexpr (F == kNvfp4) {
-        const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.part) + ph * kDl + 8 * c);
+        const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.part) + pi);
         const uint32_t u[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -508,7 +531,7 @@ __global__ void __launch_bounds__(256) mla_merge_kernel(const MlaArgs a, int row
           x[i][2 * e + 1] = (float)h.y;
         }
       } else {
-        const float4_t* v = reinterpret_cast<const float4_t*>(static_cast<const float*>(a.part) + ph * kDl + 8 * c);
+        const float4_t* v = reinterpret_cast<const float4_t*>(static_cast<const float*>(a.part) + pi);
         const float4_t v0 = v[0], v1 = v[1];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -530,10 +553,10 @@ __global__ void __launch_bounds__(256) mla_merge_kernel(const MlaArgs a, int row
     for (int e = 0; e < 8; ++e) o[e] *= alpha;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float w = __builtin_amdgcn_exp2f(ml[i].x - mu) * ml[i].y;
-      l_run += w;
+      const float wt = __builtin_amdgcn_exp2f(ml[i].x - mu) * ml[i].y;
+      l_run += wt;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] += w * x[i][e];
+      for (int e = 0; e < 8; ++e) o[e] += wt * x[i][e];
     }
     m_run = mc;
   }
@@ -543,8 +566,10 @@ __global__ void __launch_bounds__(256) mla_merge_kernel(const MlaArgs a, int row
   const float inv = l_run > 0.0f ? 1.0f / total : 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] *= inv;
-  store_vals(a, row, head, 8 * c, o, 8);
-  if (a.lse && c == 0) a.lse[rh] = l_run > 0.0f ? (mu + __builtin_log2f(l_run)) * kLn2 : -__builtin_inff();
+  store_vals(a, row, head, d0, o, 4);
+  store_vals(a, row, head, d0 + 16, o + 4, 4);
+  if (a.lse && d0 == 0)
+    a.lse[(int64_t)row * a.heads + head] = l_run > 0.0f ? (mu + __builtin_log2f(l_run)) * kLn2 : -__builtin_inff();
 }
 
 int check_cache(const char* what, const xt_mla_cache* c, int64_t* pay_stride, int64_t* sf_stride,
@@ -581,7 +606,8 @@ int check_pages(const char* what, const xt_mla_fp8_cache* c, CacheDev* cd) {
 size_t mla_workspace_bytes(int rows, int heads, int splits, size_t part_elem) {
   if (rows < 0 || heads <= 0 || splits <= 0) return 0;
   if (splits == 1) return 256;
-  return kCounterBytes + (size_t)rows * splits * heads * (kDl * part_elem + 2 * sizeof(float));
+  const size_t padded = (size_t)((heads + 15) / 16) * 16;   // partials in whole waves of 16 heads
+  return kCounterBytes + (size_t)rows * splits * (padded * kDl * part_elem + heads * 2 * sizeof(float));
 }
 
 // Everything but the caches: checks, key lists, split sizing, workspace carving and the launches.
@@ -623,12 +649,13 @@ int mla_launch(const char* what, MlaArgs& a, bool extra, const void* q, int64_t 
     a.steps = 1;
   }
   const size_t lds_bytes = (size_t)2 * kKTile<F> + kQTile<F> + (size_t)(a.steps + 1) * kMSteps * 4;
-  if (lds_bytes > 160 * 1024 - 256)
+  if (lds_bytes > 160 * 1024 - 256 || (a.steps + 1) * kMSteps > 512 * kSlotIters)
     return fail(XT_EUNSUPPORTED, "%s: %d keys per split need %zu bytes of LDS; use more splits", what,
                 a.keys_per_split, lds_bytes);
   char* ws = static_cast<char*>(workspace);
   a.part = ws + kCounterBytes;
-  a.ml = reinterpret_cast<float*>(ws + kCounterBytes + (size_t)rows * splits * heads * kDl * part_elem);
+  a.ml = reinterpret_cast<float*>(ws + kCounterBytes +
+                                  (size_t)rows * splits * ((heads + 15) / 16) * 16 * kDl * part_elem);
   const int64_t n_units = (int64_t)rows * splits;
   if (n_units > 0x7FFFFFFFLL) return fail(XT_EUNSUPPORTED, "%s: %lld workgroups", what, (long long)n_units);
   a.xcd_units = (uint32_t)(n_units / 8);
@@ -650,7 +677,7 @@ int mla_launch(const char* what, MlaArgs& a, bool extra, const void* q, int64_t 
     hipLaunchKernelGGL((mla_kernel<F, false>), dim3((unsigned)n_units), dim3(64 * kMWaves), lds_bytes,
                        reinterpret_cast<hipStream_t>(stream), a);
   if (splits > 1) {
-    const int64_t threads = (int64_t)rows * heads * 64;
+    const int64_t threads = (int64_t)rows * ((heads + 15) / 16) * 16 * 64;   // (row, wave, dim-tile pair, lane)
     hipLaunchKernelGGL(mla_merge_kernel<F>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                        reinterpret_cast<hipStream_t>(stream), a, rows);
   }
