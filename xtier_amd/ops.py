@@ -327,10 +327,12 @@ def fp4_prefill_gqa_share_sparse(q, k_cache, v_cache, sink, req_to_token, slot_i
     bi = torch.searchsorted(cu[1:].contiguous(), r, right=True)
     local = r - cu[bi]
     max_slots = k_pay.shape[0] * block_size_k
-    row_req = torch.remainder(slot_ids.to(torch.int64)[bi], max_slots)
+    # wrapped as the reference wraps it, then kept inside the table (on the device: no synchronization)
+    row_req = torch.clamp(torch.remainder(slot_ids.to(torch.int64)[bi], max_slots), max=req_to_token.shape[0] - 1)
     row_qpos = (prefix_lens.to(torch.int64)[bi] + local).to(torch.int32)
     row_seq = torch.clamp(seq_lens.to(torch.int32)[bi], max=req_to_token.shape[1])   # positions within the table
-    row_idx = (cu_seqblocks_q.to(torch.int64)[bi] + local // block_size_q).to(torch.int32)
+    row_idx = torch.clamp(cu_seqblocks_q.to(torch.int64)[bi] + local // block_size_q,
+                          max=topk_idx.shape[1] - 1).to(torch.int32)   # a list row of topk_idx
     if q.stride(-1) != 1:
         q = q.contiguous()
     if out is None:
