@@ -770,7 +770,8 @@ def main():
     p.add_argument('--layers', type=int, default=16)
     p.add_argument('--splits', type=int, default=None)
     p.add_argument('--layout', default='interleaved', choices=['interleaved', 'split'],
-                   help='pool layout: interleaved (per slot [K pay | K sf | V pay | V sf]) or split (SGLang buffers)')
+                   help='pool layout: interleaved (one 576-B record per slot: per head [K pay | V pay], then per '
+                        'head [K sf | V sf]) or split (SGLang buffers)')
     p.add_argument('--cpu-seconds', type=float, default=10.0)
     p.add_argument('--no-cpu-baseline', action='store_true')
     p.add_argument('--copy-calibration', type=int, default=0, metavar='MIB',

@@ -9,9 +9,11 @@
  *   payload  uint8 [slots, kv_heads, dim / 2]   byte i of a head row = element 2i (bits 0-3), element 2i+1 (bits 4-7)
  *   scales   uint8 [slots, kv_heads, dim / 16]  OCP E4M3, one per 16 elements
  *   global   float [1] on the device            value = (e2m1 * e4m3) * global
- * pay_stride / sf_stride arguments (bytes from one slot to the next; 0 = the packed values heads*dim/2 and heads*dim/16)
- * also admit the interleaved pool of this library: per slot [K payload | K scales | V payload | V scales] in one buffer,
- * so one key's K and V (576 bytes at 4 heads x 128) are contiguous in HBM.
+ * pay_stride / sf_stride (bytes from one slot to the next; 0 = heads * the head stride) and, where an entry point takes
+ * them, pay_head_stride / sf_head_stride (bytes from one KV head's row to the next within a slot; 0 = dim/2, dim/16)
+ * also admit the interleaved pool of this library. Per slot it holds, for each KV head, that head's K payload row then
+ * its V payload row, then for each KV head its K scales then its V scales. One key's K and V are then one contiguous
+ * record (576 bytes at 4 heads x 128), and a head's K and V payload (128 bytes) are adjacent.
  * Slot lookup: page_size 1 -> table is token-granular (SGLang req_to_token, qsa_fp4.py:135);
  *              page_size P > 1 -> table holds page ids, slot = table[pos / P] * P + pos % P.
  */
@@ -58,12 +60,13 @@ int xt_nvfp4_global_scale(const void* src, int64_t n_rows, int heads, int dim, i
  *   on a midpoint taking the smaller one; sign bit when q < 0 and code > 0.
  * saturate = 0: a scale that rounds above 448 becomes E4M3 NaN, as the reference's torch cast (formats.py:124);
  * saturate = 1: it becomes 448 (the satfinite conversion of xtier/arch.py:57-75), so a row that exceeds a fixed
- * global scale never stores NaN. The reference's GPU write path is SGLang's quantizer behind the hook at
- * xtier/packs/qwen4_exp/qsa_fp4.py:202-205 (fused store: xtier/packs/minimax_m3/kv_fp4.py:546-559). */
+ * global scale never stores NaN. Pool strides as above (payload slot and head strides multiples of 8). The reference's
+ * GPU write path is SGLang's quantizer behind the hook at xtier/packs/qwen4_exp/qsa_fp4.py:202-205 (fused store:
+ * xtier/packs/minimax_m3/kv_fp4.py:546-559). */
 int xt_nvfp4_quantize_append(const void* src, int64_t n_rows, int heads, int dim, int64_t src_row_stride,
                              int64_t src_head_stride, const int64_t* slots, const float* g, uint8_t* pay,
-                             uint8_t* scales, int64_t pool_slots, int64_t pay_stride, int64_t sf_stride, int saturate,
-                             xt_stream_t stream);
+                             uint8_t* scales, int64_t pool_slots, int64_t pay_stride, int64_t sf_stride,
+                             int64_t pay_head_stride, int64_t sf_head_stride, int saturate, xt_stream_t stream);
 
 /* --- QSA gather and pack (bit-exact BF16/FP16 rows) -------------------------------------------------------------- */
 
@@ -104,7 +107,8 @@ size_t xt_sparse_decode_workspace_bytes(int rows, int q_heads, int dim, int spli
  * resolved to pool slots through table row row_req[r] (row_req NULL: row r) with the page_size rule above.
  * K/V are dequantized in registers; out[r, h] = sum_k softmax_k(q.k * scale) v_k in the dtype out_dtype, a row
  * without valid keys writing 0. lse (optional, FP32 [rows, q_heads]): natural log-sum-exp of the scaled scores,
- * -inf for an empty row. q_heads must be a multiple of kv_heads with q_heads / kv_heads <= 16; dim = 128.
+ * -inf for an empty row. q_heads must be a multiple of kv_heads with q_heads / kv_heads <= 16; dim = 128. Pool
+ * pointers and strides as above: payload 16-byte and scales 4-byte aligned.
  * splits: key splits per row (1..64); workspace: xt_sparse_decode_workspace_bytes(rows, q_heads, dim, splits) bytes,
  * 256-byte aligned. With splits > 1 it holds a fixed 64 KB region of arrival counters (one per row and KV head group,
  * rows * kv_heads <= 16384) followed by the split partials: zero-filled before its first use, the counters are left
@@ -114,8 +118,8 @@ size_t xt_sparse_decode_workspace_bytes(int rows, int q_heads, int dim, int spli
  * workgroup of each (row, head group) to finish merges the split partials. */
 int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, const uint8_t* k_pay,
                            const uint8_t* v_pay, const uint8_t* k_scales, const uint8_t* v_scales, const float* gk,
-                           const float* gv, int64_t pool_slots, int64_t pay_stride, int64_t sf_stride, int kv_heads,
-                           int q_heads, int dim,
+                           const float* gv, int64_t pool_slots, int64_t pay_stride, int64_t sf_stride,
+                           int64_t pay_head_stride, int64_t sf_head_stride, int kv_heads, int q_heads, int dim,
                            const int32_t* table, int64_t table_stride, int page_size, const int64_t* row_req,
                            const int32_t* indices, int64_t idx_stride, int topk, const int32_t* counts,
                            const int32_t* seq_lens, const int32_t* query_pos, float scale, void* out,

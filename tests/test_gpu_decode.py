@@ -219,14 +219,14 @@ def test_decode_long_context_workload():
 
 
 def test_interleaved_pool_equals_split_pool():
-    """The same bytes in the interleaved layout (one buffer, per slot [K pay | K sf | V pay | V sf]) and in SGLang's
-    four buffers give the same bits."""
+    """The same bytes in the interleaved layout (one buffer; per slot each head's [K row | V row], then each head's
+    [K scales | V scales]) and in SGLang's four buffers give the same bits."""
     pool, pt, idx, q = _small_case(seed=21, batch=4)
     slots = pool.raw[0].shape[0]
     il = KVPool(slots, 4, 128, layout='interleaved', gk=pool.raw[4].clone(), gv=pool.raw[5].clone())
     for dst, src in zip((il.k_pay, il.v_pay, il.k_sf, il.v_sf), pool.raw[:4]):
         dst.copy_(src)
-    assert il.k_pay.stride(0) == 576 and not il.k_pay.is_contiguous()
+    assert il.k_pay.stride()[:2] == (576, 128) and il.v_sf.stride()[:2] == (576, 16) and not il.k_pay.is_contiguous()
     seq = torch.full((4,), 3008, dtype=torch.int32, device='cuda')
     a = ops.sparse_decode(q.cuda(), pool.raw, pt.cuda(), idx.cuda(), seq, 0.09, page_size=64)
     b = ops.sparse_decode(q.cuda(), il.raw, pt.cuda(), idx.cuda(), seq, 0.09, page_size=64)

@@ -102,6 +102,11 @@ def test_pool_append_layouts(layout):
         assert np.array_equal(pay.cpu().numpy()[slots.numpy()], opay)
         assert np.array_equal(sc.cpu().numpy()[slots.numpy()], osc)
     if layout == 'interleaved':
+        # per slot: each head's [K row | V row] (128 bytes), then each head's [K scales | V scales] (16 bytes)
         row = pool.buffer[slots[0]].cpu().numpy()
-        assert np.array_equal(row[:256], pool.k_pay[slots[0]].cpu().numpy().ravel())
-        assert np.array_equal(row[288:544], pool.v_pay[slots[0]].cpu().numpy().ravel())
+        pairs, scales = row[:512].reshape(heads, 128), row[512:].reshape(heads, 16)
+        assert np.array_equal(pairs[:, :64], pool.k_pay[slots[0]].cpu().numpy())
+        assert np.array_equal(pairs[:, 64:], pool.v_pay[slots[0]].cpu().numpy())
+        assert np.array_equal(scales[:, :8], pool.k_sf[slots[0]].cpu().numpy())
+        assert np.array_equal(scales[:, 8:], pool.v_sf[slots[0]].cpu().numpy())
+        assert row.size == 576 and pool.k_pay.stride()[:2] == (576, 128) and pool.k_sf.stride()[:2] == (576, 16)

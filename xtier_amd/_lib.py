@@ -44,13 +44,13 @@ SIGNATURES = {
     'xt_version': (_I, []),
     'xt_last_error': (ctypes.c_char_p, []),
     'xt_nvfp4_global_scale': (_I, [_P, _L, _I, _I, _L, _L, _P, _P, _P]),
-    'xt_nvfp4_quantize_append': (_I, [_P, _L, _I, _I, _L, _L, _P, _P, _P, _P, _L, _L, _L, _I, _P]),
+    'xt_nvfp4_quantize_append': (_I, [_P, _L, _I, _I, _L, _L, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _P]),
     'xt_qsa_gather_nvfp4': (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _P, _L, _P, _P, _L, _P, _P, _P, _P, _I, _I, _I,
                                  _I, _P]),
     'xt_qsa_pack_nvfp4': (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _P, _L, _L, _P, _I, _P, _I, _P, _P, _I, _P]),
     'xt_sparse_decode_workspace_bytes': (_Z, [_I, _I, _I, _I]),
-    'xt_sparse_decode_nvfp4': (_I, [_P, _L, _L, _P, _P, _P, _P, _P, _P, _L, _L, _L, _I, _I, _I, _P, _L, _I, _P, _P,
-                                    _L, _I, _P, _P, _P, _F, _P, _L, _L, _I, _P, _I, _I, _P, _Z, _P]),
+    'xt_sparse_decode_nvfp4': (_I, [_P, _L, _L, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _P, _L, _I, _P,
+                                    _P, _L, _I, _P, _P, _P, _F, _P, _L, _L, _I, _P, _I, _I, _P, _Z, _P]),
     'xt_block_sparse_decode_nvfp4': (_I, [_P, _L, _L, _P, _P, _P, _P, _F, _L, _I, _I, _I, _I, _L, _L, _L, _L, _L, _L,
                                           _P, _L, _I, _P, _P, _L, _L, _I, _P, _F, _P, _L, _L, _I, _P, _I, _I, _P, _Z,
                                           _P]),

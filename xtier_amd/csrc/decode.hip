@@ -577,7 +577,8 @@ extern "C" size_t xt_sparse_decode_workspace_bytes(int rows, int q_heads, int di
 extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride,
                                       const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_scales,
                                       const uint8_t* v_scales, const float* gk, const float* gv, int64_t pool_slots,
-                                      int64_t pay_stride, int64_t sf_stride, int kv_heads, int q_heads, int dim,
+                                      int64_t pay_stride, int64_t sf_stride, int64_t pay_head_stride,
+                                      int64_t sf_head_stride, int kv_heads, int q_heads, int dim,
                                       const int32_t* table, int64_t table_stride,
                                       int page_size, const int64_t* row_req, const int32_t* indices,
                                       int64_t idx_stride, int topk, const int32_t* counts, const int32_t* seq_lens,
@@ -587,14 +588,19 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
   const char* what = "xt_sparse_decode_nvfp4";
   if (dim != kDim) return fail(XT_EUNSUPPORTED, "%s: head size %d (supported: %d)", what, dim, kDim);
   if (kv_heads <= 0) return fail(XT_EINVAL, "%s: kv_heads %d", what, kv_heads);
-  if (pay_stride == 0) pay_stride = (int64_t)kv_heads * (dim / 2);
-  if (sf_stride == 0) sf_stride = (int64_t)kv_heads * (dim / 16);
-  if (pay_stride < (int64_t)kv_heads * (dim / 2) || sf_stride < (int64_t)kv_heads * (dim / 16))
-    return fail(XT_EINVAL, "%s: slot strides %lld / %lld bytes must hold the heads' payload / scales", what,
-                (long long)pay_stride, (long long)sf_stride);
+  if (pay_head_stride == 0) pay_head_stride = dim / 2;
+  if (sf_head_stride == 0) sf_head_stride = dim / 16;
+  if (pay_stride == 0) pay_stride = (int64_t)kv_heads * pay_head_stride;
+  if (sf_stride == 0) sf_stride = (int64_t)kv_heads * sf_head_stride;
+  if (pay_head_stride < dim / 2 || sf_head_stride < dim / 16 ||
+      pay_stride < (int64_t)(kv_heads - 1) * pay_head_stride + dim / 2 ||
+      sf_stride < (int64_t)(kv_heads - 1) * sf_head_stride + dim / 16)
+    return fail(XT_EINVAL, "%s: slot strides %lld / %lld and head strides %lld / %lld bytes must hold the heads' "
+                "payload / scales", what, (long long)pay_stride, (long long)sf_stride, (long long)pay_head_stride,
+                (long long)sf_head_stride);
   if (pool_slots <= 0 || pool_slots > 0x7FFFFFFFLL)
     return fail(XT_EINVAL, "%s: pool_slots %lld outside 1..2^31-1", what, (long long)pool_slots);
-  const Addressing ad{dim / 2, dim / 16, 0, 1, 0, 0, true, nullptr, 0x7FFFFFFF, false, 0.0f, 0.0f};
+  const Addressing ad{pay_head_stride, sf_head_stride, 0, 1, 0, 0, true, nullptr, 0x7FFFFFFF, false, 0.0f, 0.0f};
   return decode_impl(what, q, q_row_stride, q_head_stride, k_pay, v_pay, k_scales, v_scales, gk, gv, pool_slots,
                      pay_stride, sf_stride, kv_heads, q_heads, table, table_stride, page_size, row_req, indices,
                      idx_stride, topk, counts, seq_lens, query_pos, scale, out, out_row_stride, out_head_stride,

@@ -54,7 +54,7 @@ __global__ void quantize_append_kernel(const uint16_t* __restrict__ src, int64_t
                                        int64_t rs, int64_t hs, const int64_t* __restrict__ slots,
                                        const float* __restrict__ gp, uint8_t* __restrict__ pay,
                                        uint8_t* __restrict__ sf, int64_t pool_slots, int64_t pay_stride,
-                                       int64_t sf_stride, int saturate) {
+                                       int64_t sf_stride, int64_t pay_hs, int64_t sf_hs, int saturate) {
   const int blocks = dim / 16;
   const int64_t total = n_rows * heads * blocks;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -98,8 +98,8 @@ __global__ void quantize_append_kernel(const uint16_t* __restrict__ src, int64_t
   uint2 outw;
   outw.x = packed[0];
   outw.y = packed[1];
-  *reinterpret_cast<uint2*>(pay + slot * pay_stride + (int64_t)h * (dim / 2) + blk * 8) = outw;
-  sf[slot * sf_stride + (int64_t)h * (dim / 16) + blk] = (uint8_t)sbyte;
+  *reinterpret_cast<uint2*>(pay + slot * pay_stride + h * pay_hs + blk * 8) = outw;
+  sf[slot * sf_stride + h * sf_hs + blk] = (uint8_t)sbyte;
 }
 
 int check_src(const char* what, const void* src, int64_t n_rows, int heads, int dim, int64_t rs, int64_t hs) {
@@ -139,19 +139,24 @@ extern "C" int xt_nvfp4_global_scale(const void* src, int64_t n_rows, int heads,
 extern "C" int xt_nvfp4_quantize_append(const void* src, int64_t n_rows, int heads, int dim, int64_t src_row_stride,
                                         int64_t src_head_stride, const int64_t* slots, const float* g, uint8_t* pay,
                                         uint8_t* scales, int64_t pool_slots, int64_t pay_stride, int64_t sf_stride,
-                                        int saturate, xt_stream_t stream) {
+                                        int64_t pay_head_stride, int64_t sf_head_stride, int saturate,
+                                        xt_stream_t stream) {
   const char* what = "xt_nvfp4_quantize_append";
   if (int e = check_src(what, src, n_rows, heads, dim, src_row_stride, src_head_stride)) return e;
   if (n_rows == 0) return ok();
   if (slots == nullptr || g == nullptr || pay == nullptr || scales == nullptr || pool_slots <= 0)
     return fail(XT_EINVAL, "%s: slots, g, payload and scales are required (pool_slots %lld)", what,
                 (long long)pool_slots);
-  if (pay_stride == 0) pay_stride = (int64_t)heads * (dim / 2);
-  if (sf_stride == 0) sf_stride = (int64_t)heads * (dim / 16);
-  if (!aligned(pay, 8) || pay_stride % 8 || pay_stride < (int64_t)heads * (dim / 2) ||
-      sf_stride < (int64_t)heads * (dim / 16))
-    return fail(XT_EINVAL, "%s: payload must be 8-byte aligned with a slot stride (%lld) that holds the heads and is a "
-                "multiple of 8; scale slot stride %lld", what, (long long)pay_stride, (long long)sf_stride);
+  if (pay_head_stride == 0) pay_head_stride = dim / 2;
+  if (sf_head_stride == 0) sf_head_stride = dim / 16;
+  if (pay_stride == 0) pay_stride = (int64_t)heads * pay_head_stride;
+  if (sf_stride == 0) sf_stride = (int64_t)heads * sf_head_stride;
+  if (!aligned(pay, 8) || pay_stride % 8 || pay_head_stride % 8 || pay_head_stride < dim / 2 ||
+      sf_head_stride < dim / 16 || pay_stride < (int64_t)(heads - 1) * pay_head_stride + dim / 2 ||
+      sf_stride < (int64_t)(heads - 1) * sf_head_stride + dim / 16)
+    return fail(XT_EINVAL, "%s: payload must be 8-byte aligned with slot and head strides (%lld, %lld) that are "
+                "multiples of 8 and hold the heads' rows; scale strides %lld, %lld", what, (long long)pay_stride,
+                (long long)pay_head_stride, (long long)sf_stride, (long long)sf_head_stride);
   const int64_t total = n_rows * heads * (dim / 16);
   const int64_t blocks = (total + 255) / 256;
   if (blocks > 0x7FFFFFFF) return fail(XT_EUNSUPPORTED, "%s: %lld rows is too many for one launch", what,
@@ -159,6 +164,6 @@ extern "C" int xt_nvfp4_quantize_append(const void* src, int64_t n_rows, int hea
   hipLaunchKernelGGL(quantize_append_kernel, dim3((unsigned)blocks), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t*>(src), n_rows, heads, dim,
                      src_row_stride, src_head_stride, slots, g, pay, scales, pool_slots, pay_stride, sf_stride,
-                     saturate);
+                     pay_head_stride, sf_head_stride, saturate);
   return check_launch(what);
 }

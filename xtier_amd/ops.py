@@ -33,8 +33,8 @@ def _need_cuda(*tensors):
 
 def _check_raw(raw, contiguous=True):
     """The reference's _check (qsa_fp4.py:165-171): packed [m, heads, dim/2] rows with a power-of-2 head size.
-    contiguous=False also admits pools whose slots are strided (the interleaved layout of KVPool): each head row
-    packed, the slot stride the same for K and V."""
+    contiguous=False also admits pools whose slots and heads are strided (the interleaved layout of KVPool): each head
+    row contiguous, the slot and head strides the same for K and V."""
     k, v, k_sf, v_sf, gk, gv = raw
     if k_sf is None:
         raise NotImplementedError('xtier_amd: FP8 pools are not covered; NVFP4 pools only')
@@ -42,8 +42,9 @@ def _check_raw(raw, contiguous=True):
     if contiguous:
         packed = k.is_contiguous() and v.is_contiguous() and k_sf.is_contiguous() and v_sf.is_contiguous()
     else:
-        packed = (all(t.dim() == 3 and t.stride(2) == 1 and t.stride(1) == t.shape[2] for t in (k, v, k_sf, v_sf))
-                  and k.stride(0) == v.stride(0) and k_sf.stride(0) == v_sf.stride(0)
+        packed = (all(t.dim() == 3 and t.stride(2) == 1 and (t.shape[1] == 1 or t.stride(1) >= t.shape[2])
+                      for t in (k, v, k_sf, v_sf))
+                  and k.stride()[:2] == v.stride()[:2] and k_sf.stride()[:2] == v_sf.stride()[:2]
                   and k.shape == v.shape and k_sf.shape == v_sf.shape and k_sf.shape[2] * 8 == k.shape[2])
     if not (packed and dim % 32 == 0 and dim & (dim - 1) == 0):
         raise ValueError(f'xtier qsa_fp4: packed [m, heads, dim / 2] rows with a power-of-2 head size expected, got '
@@ -53,6 +54,11 @@ def _check_raw(raw, contiguous=True):
     _need_cuda(k, v, k_sf, v_sf, gk, gv)
     return (k, v, k_sf, v_sf, gk.float() if gk.dtype != torch.float32 else gk,
             gv.float() if gv.dtype != torch.float32 else gv), k.shape[1], dim
+
+
+def _head_stride(t):
+    """Bytes between the head rows of a pool view [slots, heads, width] (0, the packed default, for one head)."""
+    return t.stride(1) if t.shape[1] > 1 else 0
 
 
 def workspace(device, nbytes):
@@ -112,7 +118,8 @@ def quantize_append(x, slots, g, pay, scales, saturate=True):
         raise ValueError('xtier_amd.quantize_append: uint8 payload / scale views with packed head rows expected')
     _lib.check(_lib.lib().xt_nvfp4_quantize_append(
         _ptr(x), x.shape[0], x.shape[1], x.shape[2], x.stride(0), x.stride(1), _ptr(slots), _ptr(g),
-        _ptr(pay), _ptr(scales), pay.shape[0], pay.stride(0), scales.stride(0), 1 if saturate else 0, _stream(x)),
+        _ptr(pay), _ptr(scales), pay.shape[0], pay.stride(0), scales.stride(0), _head_stride(pay),
+        _head_stride(scales), 1 if saturate else 0, _stream(x)),
         'quantize_append')
 
 
@@ -208,7 +215,7 @@ def sparse_decode(q, raw, table, indices, seq_lens, scale, page_size=1, row_req=
     ws = _decode_ws(q.device, rows, q_heads, dim, splits, ws)
     _lib.check(_lib.lib().xt_sparse_decode_nvfp4(
         _ptr(q), q.stride(0), q.stride(1), *map(_ptr, raw), raw[0].shape[0], raw[0].stride(0), raw[2].stride(0),
-        kv_heads, q_heads, dim, _ptr(table),
+        _head_stride(raw[0]), _head_stride(raw[2]), kv_heads, q_heads, dim, _ptr(table),
         table.stride(0), int(page_size), _ptr(row_req), _ptr(indices), indices.stride(0), topk, _ptr(counts),
         _ptr(seq_lens), _ptr(query_pos), float(scale), _ptr(out), out.stride(0), out.stride(1), _DTYPES[out.dtype],
         _ptr(lse), rows, int(splits), _ptr(ws), ws.numel(), _stream(q)), 'sparse_decode')

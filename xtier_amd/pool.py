@@ -1,13 +1,16 @@
 """A layer's paged NVFP4 KV pool in HBM, in either of two layouts:
 
-- 'interleaved' (this library's layout): one uint8 buffer [slots, 2 * heads * (dim/2 + dim/16)], each slot holding
-  [K payload | K scales | V payload | V scales]. A key's K and V (576 bytes at 4 heads x 128) are contiguous, so a
-  sparse gather reads one burst per key instead of four scattered ones (two payload rows and two 32-byte scale rows).
+- 'interleaved' (this library's layout): one uint8 buffer [slots, 2 * heads * (dim/2 + dim/16)]. Each slot holds, per
+  KV head, the head's K payload row then its V payload row, and after them, per KV head, its K scales then its V
+  scales. A key's K and V (576 bytes at 4 heads x 128) are one contiguous record, so a sparse gather reads one burst
+  per key instead of four scattered ones, and the K and V payload of one head (128 bytes) sit side by side, where one
+  workgroup reads both.
 - 'split': SGLang's NVFP4 pool buffers (xtier/packs/qwen4_exp/qsa_fp4.py:43-58): k, v uint8 [slots, heads, dim/2] and
   k_sf, v_sf uint8 [slots, heads, dim/16], each contiguous.
 
 Either way ``raw`` is the reference's tuple (k_pay, v_pay, k_scales, v_scales, gk, gv), the payload and scale entries
-being strided uint8 views, which every entry point of xtier_amd.ops accepts.
+being uint8 views [slots, heads, width] with strided slots and heads. The decode, prefill and quantize entry points
+of xtier_amd.ops take both layouts; the QSA gather and pack keep the reference's packed-buffer precondition.
 """
 import torch
 
@@ -22,13 +25,11 @@ class KVPool:
         half, blocks = kv_heads * dim // 2, kv_heads * dim // 16
         device = torch.device(device)
         if layout == 'interleaved':
-            width = 2 * (half + blocks)
-            self.buffer = torch.zeros(slots, width, dtype=torch.uint8, device=device)
-            view = lambda off, n, w: self.buffer[:, off:off + n].unflatten(1, (kv_heads, w))
-            self.k_pay = view(0, half, dim // 2)
-            self.k_sf = view(half, blocks, dim // 16)
-            self.v_pay = view(half + blocks, half, dim // 2)
-            self.v_sf = view(2 * half + blocks, blocks, dim // 16)
+            self.buffer = torch.zeros(slots, 2 * (half + blocks), dtype=torch.uint8, device=device)
+            pay = self.buffer[:, :2 * half].unflatten(1, (kv_heads, dim))        # per head [K row | V row]
+            sf = self.buffer[:, 2 * half:].unflatten(1, (kv_heads, dim // 8))    # per head [K scales | V scales]
+            self.k_pay, self.v_pay = pay[:, :, :dim // 2], pay[:, :, dim // 2:]
+            self.k_sf, self.v_sf = sf[:, :, :dim // 16], sf[:, :, dim // 16:]
         elif layout == 'split':
             self.buffer = None
             self.k_pay = torch.zeros(slots, kv_heads, dim // 2, dtype=torch.uint8, device=device)
