@@ -123,6 +123,9 @@ struct WaveCtx {
   int lane, hl, j;
 };
 
+// PS: the K and V scales of a head are 16 contiguous bytes (the interleaved pool): one load serves both, the even lane
+// of each pair taking the K half and the odd lane the V half; compute_step swaps the halves within the pair.
+template <bool PS>
 __device__ inline void load_step(const WaveCtx& w, int step, Step& d) {
   const int base = step * kStep;
 #pragma unroll
@@ -134,8 +137,14 @@ __device__ inline void load_step(const WaveCtx& w, int step, Step& d) {
   }
   const int32_t s = w.slots[base + (w.lane >> 1)];
   const int64_t slot = s < 0 ? 0 : s;
-  d.ks = *reinterpret_cast<const uint32_t*>(w.ksf + slot * w.row_scales + 4 * (w.lane & 1));
-  d.vs = *reinterpret_cast<const uint32_t*>(w.vsf + slot * w.row_scales + 4 * (w.lane & 1));
+  if constexpr (PS) {
+    const uint2 x = *reinterpret_cast<const uint2*>(w.ksf + slot * w.row_scales + 8 * (w.lane & 1));
+    d.ks = x.x;
+    d.vs = x.y;
+  } else {
+    d.ks = *reinterpret_cast<const uint32_t*>(w.ksf + slot * w.row_scales + 4 * (w.lane & 1));
+    d.vs = *reinterpret_cast<const uint32_t*>(w.vsf + slot * w.row_scales + 4 * (w.lane & 1));
+  }
 }
 
 struct SoftmaxState {
@@ -144,6 +153,7 @@ struct SoftmaxState {
   float4_t acc[8];    // O^T of head hl, d = 32j + 8r + i in acc[i][r]
 };
 
+template <bool PS>
 __device__ inline void compute_step(const WaveCtx& w, int step, const Step& d, const half8_t (&qb)[4], float gk,
                                     uint8_t* vtile, SoftmaxState& st) {
   const int lane = w.lane, hl = w.hl, j = w.j;
@@ -151,8 +161,16 @@ __device__ inline void compute_step(const WaveCtx& w, int step, const Step& d, c
   const uint32_t valid =
       (uint32_t)__builtin_amdgcn_ballot_w64(lane < kStep && w.slots[step * kStep + (lane & 31)] >= 0);
   const bool my_scale_valid = (valid >> (lane >> 1)) & 1u;
-  const uint32_t ks = d.ks;
-  const uint32_t vs = my_scale_valid ? d.vs : 0u;   // invalid keys: V scale 0, so V = 0 whatever slot 0 holds
+  // lane 2k + i ends with word i of key k's K scales (ks) and of its V scales (vs)
+  uint32_t ks = d.ks, vs_raw = d.vs;
+  if constexpr (PS) {   // even lane: K words 0, 1; odd lane: V words 0, 1 (quad_perm [1, 0, 3, 2] swaps the pair)
+    const uint32_t o0 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)d.ks, 0xB1, 0xF, 0xF, false);
+    const uint32_t o1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)d.vs, 0xB1, 0xF, 0xF, false);
+    const bool odd = lane & 1;
+    ks = odd ? o1 : d.ks;
+    vs_raw = odd ? d.vs : o0;
+  }
+  const uint32_t vs = my_scale_valid ? vs_raw : 0u;   // invalid keys: V scale 0, so V = 0 whatever slot 0 holds
 
   // V: stage payload and scales in LDS, transposed reads below
   uint8_t* vscale = vtile + kStep * kVRow;
@@ -255,7 +273,7 @@ __device__ inline void store_out(const DecodeArgs& a, int row, int head, int d0,
 }
 
 // HPW: KV heads per workgroup (4 or 1); the workgroup's 8 / HPW key slices of each head merge through LDS.
-template <int P, int HPW>
+template <int P, int HPW, bool PS>
 __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   constexpr int kSlices = kWaves / HPW;
   extern __shared__ __align__(16) uint8_t lds[];
@@ -400,18 +418,18 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
     w.j = j;
     Step buf[P];
 #pragma unroll
-    for (int p = 0; p < P; ++p) load_step(w, p, buf[p]);
+    for (int p = 0; p < P; ++p) load_step<PS>(w, p, buf[p]);
     const float gk = a.gk ? *a.gk : a.gk_val;
     int s0 = 0;
     for (; s0 + P < slice_steps; s0 += P) {
 #pragma unroll
       for (int p = 0; p < P; ++p) {
-        compute_step(w, s0 + p, buf[p], qb, gk, vtile, st);
-        load_step(w, s0 + p + P, buf[p]);
+        compute_step<PS>(w, s0 + p, buf[p], qb, gk, vtile, st);
+        load_step<PS>(w, s0 + p + P, buf[p]);
       }
     }
 #pragma unroll
-    for (int p = 0; p < P; ++p) compute_step(w, s0 + p, buf[p], qb, gk, vtile, st);
+    for (int p = 0; p < P; ++p) compute_step<PS>(w, s0 + p, buf[p], qb, gk, vtile, st);
   }
   // the 4 lanes of a head hold disjoint key subsets of l
   float l_tot = sum4_lanes16(st.l);
@@ -801,11 +819,18 @@ static int decode_impl(const char* what, const void* q, int64_t q_row_stride, in
   const int64_t launched = a.n_units;
   if (launched > 0x7FFFFFFFLL) return fail(XT_EUNSUPPORTED, "%s: %lld workgroups", what, (long long)launched);
 
-  if (hpw == 4)
-    hipLaunchKernelGGL((decode_split_kernel<kPrefetch, 4>), dim3((unsigned)launched), dim3(64 * kWaves), lds_bytes,
-                       reinterpret_cast<hipStream_t>(stream), a);
+  // K and V scales of a head side by side and 8-byte aligned: one load per key serves both
+  const bool ps = v_scales == k_scales + dim / 16 && aligned(k_scales, 8) && sf_stride % 8 == 0 &&
+                  ad.sf_head_stride % 8 == 0;
+  const dim3 grid((unsigned)launched), block(64 * kWaves);
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (hpw == 4 && ps)
+    hipLaunchKernelGGL((decode_split_kernel<kPrefetch, 4, true>), grid, block, lds_bytes, st, a);
+  else if (hpw == 4)
+    hipLaunchKernelGGL((decode_split_kernel<kPrefetch, 4, false>), grid, block, lds_bytes, st, a);
+  else if (ps)
+    hipLaunchKernelGGL((decode_split_kernel<kPrefetch, 1, true>), grid, block, lds_bytes, st, a);
   else
-    hipLaunchKernelGGL((decode_split_kernel<kPrefetch, 1>), dim3((unsigned)launched), dim3(64 * kWaves), lds_bytes,
-                       reinterpret_cast<hipStream_t>(stream), a);
+    hipLaunchKernelGGL((decode_split_kernel<kPrefetch, 1, false>), grid, block, lds_bytes, st, a);
   return check_launch(what);
 }
