@@ -42,7 +42,10 @@ constexpr int kPrefetch = 4;       // steps of loads in flight per wave
 constexpr int kSlotBatch = 4;      // keys per thread whose index / table loads are in flight together
 constexpr float kRescale = 8.0f;   // log2 of the largest P before the running maximum is raised
 constexpr int kPartStride = kDim + 4;   // floats per partial (split, head): 128 accumulators, max, sum, 2 pad
-constexpr int kMergeLds = (kWaves / 2) * 64 * 36 * 4;   // (acc, max, sum) per lane of the 4 waves handing over
+constexpr int kMergeRow = 36;      // floats per lane in the slice merge: 32 accumulators, max, sum, 2 pad
+constexpr int kMergeLds = kWaves * 64 * kMergeRow * 4;   // one region per wave
+constexpr size_t kMaxLds = 160 * 1024 - 256;   // dynamic LDS per workgroup (the rest: static LDS)
+constexpr int kMaxDevices = 64;
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -434,63 +437,66 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   // the 4 lanes of a head hold disjoint key subsets of l
   float l_tot = sum4_lanes16(st.l);
 
-  // 2. tree merge of the slices through LDS: in each round the upper half of the remaining slices hands
-  // (acc, max, sum) to the lower half
-  const bool head_live = active && hl < a.group;
+  // 2. the slices merge through LDS behind one barrier: every wave leaves its (O^T in dim order, max, sum) per lane
+  // in its own region (after the slot list and V tiles, so no wave still reading those is disturbed); then each
+  // thread merges 4 dims of one (KV head, lane) over the slices and normalizes (one split) or writes the partial
+  float* mrg = reinterpret_cast<float*>(lds + a.slot_lds_bytes + kWaves * kWaveLds);
+  {
+    float4_t* mine = reinterpret_cast<float4_t*>(mrg + (wave * 64 + lane) * kMergeRow);
 #pragma unroll
-  for (int width = kSlices / 2; width >= 1; width /= 2) {
-    __syncthreads();
-    if (slice >= width && slice < 2 * width) {
-      float* mg = reinterpret_cast<float*>(lds) + ((slice - width) * HPW + wave % HPW) * 64 * 36 + lane * 36;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) reinterpret_cast<float4_t*>(mg)[i] = st.acc[i];
-      mg[32] = st.m;
-      mg[33] = l_tot;
+    for (int r = 0; r < 4; ++r) {   // dims 32j + 8r .. 32j + 8r + 7
+      mine[2 * r] = float4_t{st.acc[0][r], st.acc[1][r], st.acc[2][r], st.acc[3][r]};
+      mine[2 * r + 1] = float4_t{st.acc[4][r], st.acc[5][r], st.acc[6][r], st.acc[7][r]};
     }
-    __syncthreads();
-    if (slice < width && head_live) {
-      const float* mg = reinterpret_cast<const float*>(lds) + (slice * HPW + wave % HPW) * 64 * 36 + lane * 36;
-      const float m1 = mg[32], l1 = mg[33];
-      const float mx = fmaxf(st.m, m1);
-      const float mu = (mx == -__builtin_inff()) ? 0.0f : mx;
-      const float a0 = __builtin_amdgcn_exp2f(st.m - mu), a1 = __builtin_amdgcn_exp2f(m1 - mu);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) st.acc[i] = st.acc[i] * a0 + reinterpret_cast<const float4_t*>(mg)[i] * a1;
-      l_tot = l_tot * a0 + l1 * a1;
-      st.m = mx;
-    }
+    mine[8] = float4_t{st.m, l_tot, 0.0f, 0.0f};
   }
-  const int head = kvh * a.group + hl;
-  if (a.splits == 1) {   // no partials: normalize and write
-    if (slice != 0 || !head_live) return;
-    const float gv = a.gv ? *a.gv : a.gv_val;
-    const float inv = l_tot > 0.0f ? gv / l_tot : 0.0f;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = st.acc[i][r] * inv;
-      store_out(a, row, head, 32 * j + 8 * r, v, 8);
-    }
-    if (a.lse && j == 0)
-      a.lse[(int64_t)row * a.q_heads + head] =
-          l_tot > 0.0f ? (st.m + __builtin_log2f(l_tot)) * kLn2 : -__builtin_inff();
-    return;
-  }
-  // 3. partials of this row, written through; the last workgroup of (row, KV group) to arrive merges them
+  __syncthreads();
   float* row_part = a.part + (int64_t)row * a.splits * a.q_heads * kPartStride;
   const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-      row_part, (short)0, (int)((int64_t)a.splits * a.q_heads * kPartStride * 4), 0x00020000);
-  if (slice == 0 && head_live) {
-    const int at = ((split * a.q_heads + head) * kPartStride) * 4;
+      row_part, (short)0, a.splits > 1 ? (int)((int64_t)a.splits * a.q_heads * kPartStride * 4) : 0, 0x00020000);
+  const float gv = a.gv ? *a.gv : a.gv_val;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      store_through(pr, at + (32 * j + 8 * r) * 4, float4_t{st.acc[0][r], st.acc[1][r], st.acc[2][r], st.acc[3][r]});
-      store_through(pr, at + (32 * j + 8 * r + 4) * 4,
-                    float4_t{st.acc[4][r], st.acc[5][r], st.acc[6][r], st.acc[7][r]});
+  for (int u = (int)threadIdx.x; u < HPW * 512; u += 512) {
+    const int part = u & 7, ln = (u >> 3) & 63, hw = u >> 9;   // dims 4 part .. +3 of lane ln's 32, KV head hw
+    const int uh = ln & 15, uj = ln >> 4;
+    const int ukvh = kvg * HPW + hw;
+    if (ukvh >= a.kv_heads || uh >= a.group) continue;
+    float ms[kSlices], ls[kSlices];
+    float4_t xs[kSlices];
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int sl = 0; sl < kSlices; ++sl) {
+      const float4_t* src = reinterpret_cast<const float4_t*>(mrg + ((sl * HPW + hw) * 64 + ln) * kMergeRow);
+      xs[sl] = src[part];
+      const float4_t ml = src[8];
+      ms[sl] = ml[0];
+      ls[sl] = ml[1];
+      mx = fmaxf(mx, ms[sl]);
     }
-    if (j == 0) store_through(pr, at + kDim * 4, float4_t{st.m, l_tot, 0.0f, 0.0f});
+    const float mu = (mx == -__builtin_inff()) ? 0.0f : mx;
+    float4_t o = float4_t{0.f, 0.f, 0.f, 0.f};
+    float l = 0.0f;
+#pragma unroll
+    for (int sl = 0; sl < kSlices; ++sl) {
+      const float wgt = __builtin_amdgcn_exp2f(ms[sl] - mu);
+      o += wgt * xs[sl];
+      l += wgt * ls[sl];
+    }
+    const int head = ukvh * a.group + uh, d0 = 32 * uj + 4 * part;
+    if (a.splits == 1) {   // no partials: normalize and write
+      const float inv = l > 0.0f ? gv / l : 0.0f;
+      const float v[4] = {o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
+      store_out(a, row, head, d0, v, 4);
+      if (a.lse && d0 == 0)
+        a.lse[(int64_t)row * a.q_heads + head] = l > 0.0f ? (mx + __builtin_log2f(l)) * kLn2 : -__builtin_inff();
+    } else {               // 3. partials of this row, written through
+      const int at = ((split * a.q_heads + head) * kPartStride) * 4;
+      store_through(pr, at + d0 * 4, o);
+      if (d0 == 0) store_through(pr, at + kDim * 4, float4_t{mx, l, 0.0f, 0.0f});
+    }
   }
+  if (a.splits == 1) return;
+  // the last workgroup of (row, KV group) to arrive merges the partials
   __builtin_amdgcn_s_waitcnt(0);   // this thread's stores have reached memory
   __syncthreads();
   __shared__ int32_t s_last;
@@ -502,7 +508,6 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   // 512 threads, 8 consecutive outputs each: head h0 + o / 128, d0 = o % 128; loads of 8 splits at a time together
   const int h0 = kvg * HPW * a.group;
   const int nh = min(HPW * a.group, a.q_heads - h0);
-  const float gv = a.gv ? *a.gv : a.gv_val;
   for (int o = threadIdx.x * 8; o < nh * kDim; o += blockDim.x * 8) {
     const int hh = h0 + o / kDim, d0 = o % kDim;
     const float* base = row_part + (int64_t)hh * kPartStride;
@@ -712,6 +717,25 @@ extern "C" int xt_block_sparse_prefill_nvfp4(const void* q, int64_t q_row_stride
                      workspace, workspace_bytes, ad, stream);
 }
 
+// One launch of the decode kernel. Dynamic LDS above 64 KB must be allowed per kernel and device; the allowance is
+// raised to the largest size asked for so far.
+template <int HPW, bool PS>
+static int launch_decode(const DecodeArgs& a, dim3 grid, size_t lds_bytes, hipStream_t stream, const char* what) {
+  const void* fn = reinterpret_cast<const void*>(&decode_split_kernel<kPrefetch, HPW, PS>);
+  static size_t allowed[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(XT_ELAUNCH, "%s: no current device below %d", what, kMaxDevices);
+  if (lds_bytes > 64 * 1024 && lds_bytes > allowed[dev]) {
+    const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
+    if (err != hipSuccess)
+      return fail(XT_ELAUNCH, "%s: could not allow %zu bytes of LDS: %s", what, lds_bytes, hipGetErrorString(err));
+    allowed[dev] = lds_bytes;
+  }
+  hipLaunchKernelGGL((decode_split_kernel<kPrefetch, HPW, PS>), grid, dim3(64 * kWaves), lds_bytes, stream, a);
+  return check_launch(what);
+}
+
 static int decode_impl(const char* what, const void* q, int64_t q_row_stride, int64_t q_head_stride,
                        const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_scales, const uint8_t* v_scales,
                        const float* gk, const float* gv, int64_t pool_slots, int64_t pay_stride, int64_t sf_stride,
@@ -756,9 +780,8 @@ static int decode_impl(const char* what, const void* q, int64_t q_row_stride, in
   const int slices = kWaves / hpw;
   const int slice_steps = ((kps / kStep + slices * kPrefetch - 1) / (slices * kPrefetch)) * kPrefetch;
   const int slot_bytes = slices * slice_steps * kStep * (int)sizeof(int32_t);
-  size_t lds_bytes = (size_t)slot_bytes + (size_t)kWaves * kWaveLds;
-  if (lds_bytes < (size_t)kMergeLds) lds_bytes = kMergeLds;
-  if (lds_bytes > 64 * 1024)
+  const size_t lds_bytes = (size_t)slot_bytes + (size_t)kWaves * kWaveLds + kMergeLds;
+  if (lds_bytes > kMaxLds)
     return fail(XT_EUNSUPPORTED, "%s: %d keys per split needs %zu bytes of LDS; use more splits", what, kps,
                 lds_bytes);
 
@@ -822,15 +845,9 @@ static int decode_impl(const char* what, const void* q, int64_t q_row_stride, in
   // K and V scales of a head side by side and 8-byte aligned: one load per key serves both
   const bool ps = v_scales == k_scales + dim / 16 && aligned(k_scales, 8) && sf_stride % 8 == 0 &&
                   ad.sf_head_stride % 8 == 0;
-  const dim3 grid((unsigned)launched), block(64 * kWaves);
+  const dim3 grid((unsigned)launched);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (hpw == 4 && ps)
-    hipLaunchKernelGGL((decode_split_kernel<kPrefetch, 4, true>), grid, block, lds_bytes, st, a);
-  else if (hpw == 4)
-    hipLaunchKernelGGL((decode_split_kernel<kPrefetch, 4, false>), grid, block, lds_bytes, st, a);
-  else if (ps)
-    hipLaunchKernelGGL((decode_split_kernel<kPrefetch, 1, true>), grid, block, lds_bytes, st, a);
-  else
-    hipLaunchKernelGGL((decode_split_kernel<kPrefetch, 1, false>), grid, block, lds_bytes, st, a);
-  return check_launch(what);
+  if (hpw == 4) return ps ? launch_decode<4, true>(a, grid, lds_bytes, st, what)
+                          : launch_decode<4, false>(a, grid, lds_bytes, st, what);
+  return ps ? launch_decode<1, true>(a, grid, lds_bytes, st, what) : launch_decode<1, false>(a, grid, lds_bytes, st, what);
 }
