@@ -1,7 +1,11 @@
-// Library-wide entry points of the C ABI: version and last-error text.
+// Library-wide entry points and host helpers of the C ABI: version, last-error text, launch checks, LDS allowance.
 #include "xt_host.h"
 
 #include <string.h>
+
+#include <map>
+#include <mutex>
+#include <utility>
 
 namespace xt {
 
@@ -24,6 +28,22 @@ int check_launch(const char* what) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(XT_ELAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
   return ok();
+}
+
+int allow_lds(const void* fn, size_t bytes, const char* what) {
+  if (bytes <= 64 * 1024) return XT_OK;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(XT_ELAUNCH, "%s: no current device", what);
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, size_t> allowed;   // (kernel, device) -> bytes allowed so far
+  std::lock_guard<std::mutex> lock(mu);
+  size_t& have = allowed[{fn, dev}];
+  if (bytes <= have) return XT_OK;
+  const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (err != hipSuccess)
+    return fail(XT_ELAUNCH, "%s: could not allow %zu bytes of LDS: %s", what, bytes, hipGetErrorString(err));
+  have = bytes;
+  return XT_OK;
 }
 
 }  // namespace xt

@@ -45,7 +45,6 @@ constexpr int kPartStride = kDim + 4;   // floats per partial (split, head): 128
 constexpr int kMergeRow = 36;      // floats per lane in the slice merge: 32 accumulators, max, sum, 2 pad
 constexpr int kMergeLds = kWaves * 64 * kMergeRow * 4;   // one region per wave
 constexpr size_t kMaxLds = 160 * 1024 - 256;   // dynamic LDS per workgroup (the rest: static LDS)
-constexpr int kMaxDevices = 64;
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -717,21 +716,11 @@ extern "C" int xt_block_sparse_prefill_nvfp4(const void* q, int64_t q_row_stride
                      workspace, workspace_bytes, ad, stream);
 }
 
-// One launch of the decode kernel. Dynamic LDS above 64 KB must be allowed per kernel and device; the allowance is
-// raised to the largest size asked for so far.
+// One launch of the decode kernel.
 template <int HPW, bool PS>
 static int launch_decode(const DecodeArgs& a, dim3 grid, size_t lds_bytes, hipStream_t stream, const char* what) {
-  const void* fn = reinterpret_cast<const void*>(&decode_split_kernel<kPrefetch, HPW, PS>);
-  static size_t allowed[kMaxDevices] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
-    return fail(XT_ELAUNCH, "%s: no current device below %d", what, kMaxDevices);
-  if (lds_bytes > 64 * 1024 && lds_bytes > allowed[dev]) {
-    const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
-    if (err != hipSuccess)
-      return fail(XT_ELAUNCH, "%s: could not allow %zu bytes of LDS: %s", what, lds_bytes, hipGetErrorString(err));
-    allowed[dev] = lds_bytes;
-  }
+  if (int e = allow_lds(reinterpret_cast<const void*>(&decode_split_kernel<kPrefetch, HPW, PS>), lds_bytes, what))
+    return e;
   hipLaunchKernelGGL((decode_split_kernel<kPrefetch, HPW, PS>), grid, dim3(64 * kWaves), lds_bytes, stream, a);
   return check_launch(what);
 }

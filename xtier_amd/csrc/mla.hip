@@ -660,16 +660,9 @@ int mla_launch(const char* what, MlaArgs& a, bool extra, const void* q, int64_t 
   if (n_units > 0x7FFFFFFFLL) return fail(XT_EUNSUPPORTED, "%s: %lld workgroups", what, (long long)n_units);
   a.xcd_units = (uint32_t)(n_units / 8);
   a.xcd_extra = (uint32_t)(n_units % 8);
-  // dynamic LDS above 64 KB must be allowed per kernel; raised to the largest size asked for so far
-  static size_t lds_allowed[2] = {64 * 1024, 64 * 1024};
   const void* fn = extra ? reinterpret_cast<const void*>(&mla_kernel<F, true>)
                          : reinterpret_cast<const void*>(&mla_kernel<F, false>);
-  if (lds_bytes > lds_allowed[extra]) {
-    const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
-    if (err != hipSuccess)
-      return fail(XT_ELAUNCH, "%s: could not allow %zu bytes of LDS: %s", what, lds_bytes, hipGetErrorString(err));
-    lds_allowed[extra] = lds_bytes;
-  }
+  if (int e = allow_lds(fn, lds_bytes, what)) return e;
   if (extra)
     hipLaunchKernelGGL((mla_kernel<F, true>), dim3((unsigned)n_units), dim3(64 * kMWaves), lds_bytes,
                        reinterpret_cast<hipStream_t>(stream), a);

@@ -309,13 +309,7 @@ int launch(const VarlenArgs& a, int64_t units, xt_stream_t stream, const char* w
   const size_t lds_bytes = tiles_bytes > merge_bytes ? tiles_bytes : merge_bytes;
   constexpr int P = D >= 256 ? 1 : 2;
   const void* fn = reinterpret_cast<const void*>(&varlen_kernel<D, P>);
-  static size_t allowed = 64 * 1024;
-  if (lds_bytes > allowed) {
-    const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
-    if (err != hipSuccess)
-      return fail(XT_ELAUNCH, "%s: could not allow %zu bytes of LDS: %s", what, lds_bytes, hipGetErrorString(err));
-    allowed = lds_bytes;
-  }
+  if (int e = allow_lds(fn, lds_bytes, what)) return e;
   hipLaunchKernelGGL((varlen_kernel<D, P>), dim3((unsigned)units), dim3(64 * kVWaves), lds_bytes,
                      reinterpret_cast<hipStream_t>(stream), a);
   return check_launch(what);

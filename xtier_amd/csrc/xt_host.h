@@ -17,6 +17,10 @@ int check_launch(const char* what);
 
 inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+// Dynamic LDS above 64 KB must be allowed per kernel and device. Raises kernel `fn`'s allowance on the current device
+// to `bytes` when a launch asks for more than any before it; thread-safe. XT_OK or XT_ELAUNCH.
+int allow_lds(const void* fn, size_t bytes, const char* what);
+
 // Workspaces of the split kernels (fused decode, sparse MLA) begin with a fixed region of arrival counters, one per
 // (row, head group) of a call: zero before the first call, left zero by every call. Split partials follow it, so calls
 // of any shape, of either kernel, may share one workspace as long as they do not overlap in time.
