@@ -220,53 +220,54 @@ __global__ void __launch_bounds__(512) varlen_kernel(const VarlenArgs a) {
   }
   float l_tot = sum4_lanes16(st.l);
 
-  // slices of a tile merge through LDS (the V tiles' space): slices > 0 hand over (acc, max, sum)
+  // the slices of a tile merge through LDS (the V tiles' space, free after the first barrier): every wave leaves
+  // (O^T, max, sum) per lane, then each thread merges 4 dims of one (tile, head, dim group) over the slices and
+  // normalizes the output (one split) or writes its share of the split partial
+  constexpr int kLane = D / 4 + 4;   // floats per lane: D/4 accumulators, max, sum, 2 pad
+  constexpr int kND = D / 16;
   __syncthreads();
   float* mg = reinterpret_cast<float*>(lds);
-  constexpr int kLane = D / 4 + 2;
-  if (slice > 0) {
-    float* p = mg + (((slice - 1) * a.tiles + tile) * 64 + lane) * kLane;
+  {
+    float4_t* p = reinterpret_cast<float4_t*>(mg + (wave * 64 + lane) * kLane);
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) reinterpret_cast<float4_t*>(p)[dt] = st.acc[dt];
-    p[D / 4] = st.m;
-    p[D / 4 + 1] = l_tot;
+    for (int dt = 0; dt < kND; ++dt) p[dt] = st.acc[dt];
+    p[kND] = float4_t{st.m, l_tot, 0.0f, 0.0f};
   }
   __syncthreads();
-  const bool merger = slice == 0;   // the slice-0 wave of each tile; every wave stays to the last barrier
-  if (merger) {
-    for (int sl = 1; sl < slices; ++sl) {
-      const float* p = mg + (((sl - 1) * a.tiles + tile) * 64 + lane) * kLane;
-      const float m1 = p[D / 4], l1 = p[D / 4 + 1];
-      const float mx = fmaxf(st.m, m1);
-      const float mu = (mx == -__builtin_inff()) ? 0.0f : mx;
-      const float a0 = __builtin_amdgcn_exp2f(st.m - mu), a1 = __builtin_amdgcn_exp2f(m1 - mu);
-#pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt)
-        st.acc[dt] = st.acc[dt] * a0 + reinterpret_cast<const float4_t*>(p)[dt] * a1;
-      l_tot = l_tot * a0 + l1 * a1;
-      st.m = mx;
-    }
-  }
-  if (a.splits == 1) {   // no barrier follows
-    if (!merger || !head_live) return;
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-#pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) {
-      const float v[4] = {st.acc[dt][0] * inv, st.acc[dt][1] * inv, st.acc[dt][2] * inv, st.acc[dt][3] * inv};
-      store_row(a, query, head, 16 * dt + 4 * j, v, 4);
-    }
-    return;
-  }
-  // partials of this (row, split), written through; the last workgroup of (row, KV head) merges them
   float* row_part = a.part + (int64_t)row * a.splits * a.heads * kPart;
   const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-      row_part, (short)0, (int)((int64_t)a.splits * a.heads * kPart * 4), 0x00020000);
-  if (merger && head_live) {
-    const int at = ((split * a.heads + head) * kPart) * 4;
-#pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) store_through(pr, at + (16 * dt + 4 * j) * 4, st.acc[dt]);
-    if (j == 0) store_through(pr, at + D * 4, float4_t{st.m, l_tot, 0.0f, 0.0f});
+      row_part, (short)0, a.splits > 1 ? (int)((int64_t)a.splits * a.heads * kPart * 4) : 0, 0x00020000);
+  // unit u: dims 16 dt + 4 uj .. +3 of head 16 utile + uhl (uj fastest, so consecutive threads write one head row)
+  for (int u = (int)threadIdx.x; u < a.tiles * 64 * kND; u += 64 * kVWaves) {
+    const int uj = u & 3, rest = u >> 2;
+    const int dt = rest % kND, uhl = (rest / kND) & 15, utile = rest / kND / 16;
+    const int ugh = 16 * utile + uhl;
+    if (ugh >= a.group) continue;
+    const int ln = uhl + 16 * uj;
+    float mx = -__builtin_inff(), l = 0.0f;
+    float4_t o = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int sl = 0; sl < slices; ++sl) {   // online merge: rescale what is held when a larger maximum arrives
+      const float4_t* src = reinterpret_cast<const float4_t*>(mg + ((sl * a.tiles + utile) * 64 + ln) * kLane);
+      const float4_t ml = src[kND];
+      const float m_new = fmaxf(mx, ml[0]);
+      const float mu = (m_new == -__builtin_inff()) ? 0.0f : m_new;
+      const float a0 = __builtin_amdgcn_exp2f(mx - mu), a1 = __builtin_amdgcn_exp2f(ml[0] - mu);
+      o = o * a0 + src[dt] * a1;
+      l = l * a0 + ml[1] * a1;
+      mx = m_new;
+    }
+    const int uhead = kvh * a.group + ugh, d0 = 16 * dt + 4 * uj;
+    if (a.splits == 1) {
+      const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+      const float v[4] = {o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
+      store_row(a, query, uhead, d0, v, 4);
+    } else {   // partials of this (row, split), written through; the last workgroup of (row, KV head) merges them
+      const int at = ((split * a.heads + uhead) * kPart) * 4;
+      store_through(pr, at + d0 * 4, o);
+      if (d0 == 0) store_through(pr, at + D * 4, float4_t{mx, l, 0.0f, 0.0f});
+    }
   }
+  if (a.splits == 1) return;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   __shared__ int32_t s_last;
@@ -305,7 +306,7 @@ template <int D>
 int launch(const VarlenArgs& a, int64_t units, xt_stream_t stream, const char* what) {
   constexpr int kRow = 2 * D + 16;
   const size_t tiles_bytes = (size_t)kVWaves * kVStep * kRow;
-  const size_t merge_bytes = (size_t)(kVWaves - 1) * 64 * (D / 4 + 2) * 4;
+  const size_t merge_bytes = (size_t)kVWaves * 64 * (D / 4 + 4) * 4;
   const size_t lds_bytes = tiles_bytes > merge_bytes ? tiles_bytes : merge_bytes;
   constexpr int P = D >= 256 ? 1 : 2;
   const void* fn = reinterpret_cast<const void*>(&varlen_kernel<D, P>);
