@@ -100,10 +100,6 @@ struct Step {
   uint32_t vs;   // V scale bytes, same
 };
 
-// A load through the scalar cache (the constant address space) of memory no launch writes: uniform per-row values.
-__device__ inline int32_t scalar_load(const int32_t* p) {
-  return *(const __attribute__((address_space(4))) int32_t*)(p);
-}
 
 __device__ inline int key_of(int j, int e) { return (e < 4) ? (4 * j + e) : (16 + 4 * j + (e - 4)); }
 
@@ -322,7 +318,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   // constants), so the chain to the first K/V load is two dependent loads: index, then table.
   const int t0 = split * a.keys_per_split;
   const int kmax = max(0, min(a.keys_per_split, a.topk - t0));
-  const int64_t irow = a.idx_rows ? scalar_load(a.idx_rows + row) : row;
+  const int64_t irow = a.idx_rows ? uniform_load(a.idx_rows + row) : row;
   const int32_t* ip = a.indices + irow * a.idx_stride + (int64_t)kvg * a.idx_head_stride;
   const int bmask = (1 << a.block_shift) - 1;
   int32_t pos[kSlotBatch];
@@ -336,10 +332,10 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   // optional arrays are given (a missing one reads the row's length and is ignored), so none waits in a branch
   const int32_t* len_p = a.seq_lens + row;
   const int32_t* req_p = a.row_req ? reinterpret_cast<const int32_t*>(a.row_req + row) : len_p;
-  int32_t len_v = scalar_load(len_p);
-  int32_t cnt_v = scalar_load(a.counts ? a.counts + row : len_p);
-  int32_t qpos_v = scalar_load(a.query_pos ? a.query_pos + row : len_p);
-  int32_t req_lo = scalar_load(req_p), req_hi = scalar_load(a.row_req ? req_p + 1 : len_p);
+  int32_t len_v = uniform_load(len_p);
+  int32_t cnt_v = uniform_load(a.counts ? a.counts + row : len_p);
+  int32_t qpos_v = uniform_load(a.query_pos ? a.query_pos + row : len_p);
+  int32_t req_lo = uniform_load(req_p), req_hi = uniform_load(a.row_req ? req_p + 1 : len_p);
   // every use below follows this asm, so the five loads issue together behind one wait
   asm volatile("" : "+s"(len_v), "+s"(cnt_v), "+s"(qpos_v), "+s"(req_lo), "+s"(req_hi));
   const int count = a.counts ? min(cnt_v, a.topk) : a.topk;

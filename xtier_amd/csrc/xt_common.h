@@ -78,6 +78,10 @@ __device__ inline half2_t fp8x2_to_f16(uint32_t packed) {
 // Maximum and sum of x over lanes l, l ^ 16 and l ^ 32 (the four lanes 16 apart), in VALU permutes: with x as both
 // operands, v_permlane16_swap / v_permlane32_swap hand every lane the pair (x[l], x[l ^ 16]) / (x[l], x[l ^ 32]),
 // in an order that does not matter here (ds_bpermute would take two LDS round trips).
+// A load through the scalar cache (the constant address space) of memory no launch writes: uniform per-row values.
+__device__ inline int32_t uniform_load(const int32_t* p) {
+  return *(const __attribute__((address_space(4))) int32_t*)(p);
+}
 __device__ inline float max4_lanes16(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
@@ -99,6 +103,7 @@ __device__ half2_t fp4x2_to_f16(uint32_t packed);
 template <bool HI>
 __device__ half2_t fp8x2_to_f16(uint32_t packed);
 __device__ float max4_lanes16(float x);
+__device__ int32_t uniform_load(const int32_t* p);
 __device__ float sum4_lanes16(float x);
 #endif
 
