@@ -233,6 +233,34 @@ def test_interleaved_pool_equals_split_pool():
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
+@pytest.mark.parametrize('heads,qh', [(1, 16), (2, 16), (8, 64)])
+def test_interleaved_pool_any_head_count(heads, qh):
+    """KVPool's interleaved layout at 1, 2 and 8 KV heads (head strides of the pairs and of the scales through the
+    ABI, the single-head default, the paired-scale load): quantize-on-append into it gives the split pool's bytes,
+    and the decode gives the split pool's bits, for 1 and 3 key splits."""
+    gen = workloads.generator('cpu', 40 + heads)
+    batch, ctx, page, topk = 3, 1024, 64, 300
+    k = workloads.kv_tensor(batch * ctx, heads, 128, gen, 'cpu').cuda()
+    v = workloads.kv_tensor(batch * ctx, heads, 128, gen, 'cpu').cuda()
+    slots = torch.arange(batch * ctx, device='cuda')
+    pools = {}
+    for layout in ('split', 'interleaved'):
+        pool = KVPool(batch * ctx, heads, 128, layout=layout)
+        pool.set_global_scales(k, v)
+        pool.append(k, v, slots)
+        pools[layout] = pool
+    for a_, b_ in zip(pools['split'].raw[:4], pools['interleaved'].raw[:4]):
+        assert torch.equal(a_, b_)
+    pt = workloads.page_table(batch, ctx, page, gen, 'cpu').cuda()
+    idx = workloads.index_lists(batch, ctx, topk, gen, 'cpu').cuda()
+    q = (torch.randn(batch, qh, 128, generator=gen) * 2).to(torch.bfloat16).cuda()
+    seq = torch.full((batch,), ctx, dtype=torch.int32, device='cuda')
+    for splits in (1, 3):
+        a_ = ops.sparse_decode(q, pools['split'].raw, pt, idx, seq, 0.09, page_size=page, splits=splits)
+        b_ = ops.sparse_decode(q, pools['interleaved'].raw, pt, idx, seq, 0.09, page_size=page, splits=splits)
+        assert torch.equal(a_.view(torch.int16), b_.view(torch.int16)), splits
+
+
 def test_one_workspace_serves_calls_of_any_shape():
     """A workspace left by a call with few rows (its partials written just past the counters) serves a later call
     with more rows and a sparse-MLA call: every result equals the one from a fresh workspace, bit for bit."""
