@@ -34,15 +34,22 @@ int allow_lds(const void* fn, size_t bytes, const char* what) {
   if (bytes <= 64 * 1024) return XT_OK;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(XT_ELAUNCH, "%s: no current device", what);
+  const std::pair<const void*, int> key{fn, dev};
+  // allowances only grow, so what this thread has seen allowed stays allowed: launches after the first take no lock
+  thread_local std::map<std::pair<const void*, int>, size_t> seen;
+  const auto it = seen.find(key);
+  if (it != seen.end() && bytes <= it->second) return XT_OK;
   static std::mutex mu;
   static std::map<std::pair<const void*, int>, size_t> allowed;   // (kernel, device) -> bytes allowed so far
   std::lock_guard<std::mutex> lock(mu);
-  size_t& have = allowed[{fn, dev}];
-  if (bytes <= have) return XT_OK;
-  const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-  if (err != hipSuccess)
-    return fail(XT_ELAUNCH, "%s: could not allow %zu bytes of LDS: %s", what, bytes, hipGetErrorString(err));
-  have = bytes;
+  size_t& have = allowed[key];
+  if (bytes > have) {
+    const hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (err != hipSuccess)
+      return fail(XT_ELAUNCH, "%s: could not allow %zu bytes of LDS: %s", what, bytes, hipGetErrorString(err));
+    have = bytes;
+  }
+  seen[key] = have;
   return XT_OK;
 }
 
