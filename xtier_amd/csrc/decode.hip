@@ -36,6 +36,7 @@ namespace {
 constexpr int kDim = 128;          // head size: 64 payload bytes, 8 scale bytes per head row
 constexpr int kStep = 32;          // keys per step
 constexpr int kWaves = 8;          // wavefronts per workgroup: HPW KV heads x (8 / HPW) key slices
+constexpr int64_t kSmallWaveUnits = 1024;   // from this many workgroup units on, 4-wave workgroups (two per CU)
 constexpr int kVRow = 80;          // LDS bytes per key in the V transpose tile (64 + 16: no bank conflicts)
 constexpr int kWaveLds = kStep * kVRow + kStep * 8;   // V tile + V scale tile per wave
 constexpr int kPrefetch = 4;       // steps of loads in flight per wave
@@ -43,7 +44,8 @@ constexpr int kSlotBatch = 4;      // keys per thread whose index / table loads 
 constexpr float kRescale = 8.0f;   // log2 of the largest P before the running maximum is raised
 constexpr int kPartStride = kDim + 4;   // floats per partial (split, head): 128 accumulators, max, sum, 2 pad
 constexpr int kMergeRow = 36;      // floats per lane in the slice merge: 32 accumulators, max, sum, 2 pad
-constexpr int kMergeLds = kWaves * 64 * kMergeRow * 4;   // one region per wave
+template <int W>
+constexpr int kMergeLds = W * 64 * kMergeRow * 4;   // one region per wave
 constexpr size_t kMaxLds = 160 * 1024 - 256;   // dynamic LDS per workgroup (the rest: static LDS)
 
 struct DecodeArgs {
@@ -271,9 +273,10 @@ __device__ inline void store_out(const DecodeArgs& a, int row, int head, int d0,
 }
 
 // HPW: KV heads per workgroup (4 or 1); the workgroup's 8 / HPW key slices of each head merge through LDS.
-template <int P, int HPW, bool PS>
-__global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
-  constexpr int kSlices = kWaves / HPW;
+template <int P, int HPW, bool PS, int W>
+__global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArgs a) {
+  constexpr int kSlices = W / HPW;
+  constexpr int kThreads = 64 * W;
   extern __shared__ __align__(16) uint8_t lds[];
   // XCD-aware numbering: workgroup g runs on XCD g % 8 (round-robin dispatch); XCD x takes the contiguous unit range
   // starting at x * (n / 8) + min(x, n % 8), so a row's units (its heads and splits) share one L2. A bijection on
@@ -314,7 +317,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
 
   // 1. the split's pool slots (-1: invalid key), shared by the workgroup's waves; each slice owns a whole number of
   // prefetch groups, padded with invalid keys that compute to no-ops (P = 0, V = 0, maximum unchanged). The first
-  // kSlotBatch * 512 index loads go out before the row's count, length and table row are read (they need only launch
+  // kSlotBatch * kThreads index loads go out before the row's count, length and table row are read (they need only launch
   // constants), so the chain to the first K/V load is two dependent loads: index, then table.
   const int t0 = split * a.keys_per_split;
   const int kmax = max(0, min(a.keys_per_split, a.topk - t0));
@@ -324,7 +327,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   int32_t pos[kSlotBatch];
 #pragma unroll
   for (int b = 0; b < kSlotBatch; ++b) {
-    const int i = b * 512 + (int)threadIdx.x, k = t0 + i;
+    const int i = b * kThreads + (int)threadIdx.x, k = t0 + i;
     const int32_t e = (i < kmax) ? ip[k >> a.block_shift] : -1;
     pos[b] = e < 0 ? -1 : (e << a.block_shift) + (k & bmask);
   }
@@ -354,7 +357,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
       int32_t toff[kSlotBatch], ent[kSlotBatch];
 #pragma unroll
       for (int b = 0; b < kSlotBatch; ++b) {
-        const int i = i0 + b * 512 + (int)threadIdx.x;
+        const int i = i0 + b * kThreads + (int)threadIdx.x;
         ok[b] = i < n && pos[b] >= 0 && pos[b] < seqlen && pos[b] <= qpos;
         const int32_t tpos = pos[b] & ~a.lookup_mask;   // block decode: a block's slots follow its first position's
         toff[b] = a.page_shift >= 0 ? (tpos >> a.page_shift) : tpos / a.page_size;
@@ -363,7 +366,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
       for (int b = 0; b < kSlotBatch; ++b) ent[b] = ok[b] ? tp[toff[b]] : -1;
 #pragma unroll
       for (int b = 0; b < kSlotBatch; ++b) {
-        const int i = i0 + b * 512 + (int)threadIdx.x;
+        const int i = i0 + b * kThreads + (int)threadIdx.x;
         int32_t slot = -1;
         if (ok[b] && ent[b] >= 0) {
           const int64_t sl = (int64_t)ent[b] * a.page_size + (pos[b] - toff[b] * a.page_size);
@@ -372,11 +375,11 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
         }
         if (i < total) slots[i] = slot;
       }
-      i0 += kSlotBatch * 512;
+      i0 += kSlotBatch * kThreads;
       if (i0 >= total) break;
 #pragma unroll
-      for (int b = 0; b < kSlotBatch; ++b) {   // splits longer than kSlotBatch * 512 keys
-        const int i = i0 + b * 512 + (int)threadIdx.x, k = t0 + i;
+      for (int b = 0; b < kSlotBatch; ++b) {   // splits longer than kSlotBatch * kThreads keys
+        const int i = i0 + b * kThreads + (int)threadIdx.x, k = t0 + i;
         const int32_t e = (i < kmax) ? ip[k >> a.block_shift] : -1;
         pos[b] = e < 0 ? -1 : (e << a.block_shift) + (k & bmask);
       }
@@ -435,7 +438,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
   // 2. the slices merge through LDS behind one barrier: every wave leaves its (O^T in dim order, max, sum) per lane
   // in its own region (after the slot list and V tiles, so no wave still reading those is disturbed); then each
   // thread merges 4 dims of one (KV head, lane) over the slices and normalizes (one split) or writes the partial
-  float* mrg = reinterpret_cast<float*>(lds + a.slot_lds_bytes + kWaves * kWaveLds);
+  float* mrg = reinterpret_cast<float*>(lds + a.slot_lds_bytes + W * kWaveLds);
   {
     float4_t* mine = reinterpret_cast<float4_t*>(mrg + (wave * 64 + lane) * kMergeRow);
 #pragma unroll
@@ -451,7 +454,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
       row_part, (short)0, a.splits > 1 ? (int)((int64_t)a.splits * a.q_heads * kPartStride * 4) : 0, 0x00020000);
   const float gv = a.gv ? *a.gv : a.gv_val;
 #pragma unroll
-  for (int u = (int)threadIdx.x; u < HPW * 512; u += 512) {
+  for (int u = (int)threadIdx.x; u < HPW * 512; u += kThreads) {
     const int part = u & 7, ln = (u >> 3) & 63, hw = u >> 9;   // dims 4 part .. +3 of lane ln's 32, KV head hw
     const int uh = ln & 15, uj = ln >> 4;
     const int ukvh = kvg * HPW + hw;
@@ -500,7 +503,7 @@ __global__ void __launch_bounds__(512) decode_split_kernel(const DecodeArgs a) {
     s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.splits - 1;
   __syncthreads();
   if (!s_last) return;
-  // 512 threads, 8 consecutive outputs each: head h0 + o / 128, d0 = o % 128; loads of 8 splits at a time together
+  // all threads, 8 consecutive outputs each: head h0 + o / 128, d0 = o % 128; loads of 8 splits at a time together
   const int h0 = kvg * HPW * a.group;
   const int nh = min(HPW * a.group, a.q_heads - h0);
   for (int o = threadIdx.x * 8; o < nh * kDim; o += blockDim.x * 8) {
@@ -713,12 +716,21 @@ extern "C" int xt_block_sparse_prefill_nvfp4(const void* q, int64_t q_row_stride
 }
 
 // One launch of the decode kernel.
-template <int HPW, bool PS>
+template <int HPW, bool PS, int W>
 static int launch_decode(const DecodeArgs& a, dim3 grid, size_t lds_bytes, hipStream_t stream, const char* what) {
-  if (int e = allow_lds(reinterpret_cast<const void*>(&decode_split_kernel<kPrefetch, HPW, PS>), lds_bytes, what))
+  if (int e = allow_lds(reinterpret_cast<const void*>(&decode_split_kernel<kPrefetch, HPW, PS, W>), lds_bytes, what))
     return e;
-  hipLaunchKernelGGL((decode_split_kernel<kPrefetch, HPW, PS>), grid, dim3(64 * kWaves), lds_bytes, stream, a);
+  hipLaunchKernelGGL((decode_split_kernel<kPrefetch, HPW, PS, W>), grid, dim3(64 * W), lds_bytes, stream, a);
   return check_launch(what);
+}
+
+template <int W>
+static int launch_decode(int hpw, bool ps, const DecodeArgs& a, dim3 grid, size_t lds_bytes, hipStream_t stream,
+                         const char* what) {
+  if (hpw == 4) return ps ? launch_decode<4, true, W>(a, grid, lds_bytes, stream, what)
+                          : launch_decode<4, false, W>(a, grid, lds_bytes, stream, what);
+  return ps ? launch_decode<1, true, W>(a, grid, lds_bytes, stream, what)
+            : launch_decode<1, false, W>(a, grid, lds_bytes, stream, what);
 }
 
 static int decode_impl(const char* what, const void* q, int64_t q_row_stride, int64_t q_head_stride,
@@ -762,10 +774,16 @@ static int decode_impl(const char* what, const void* q, int64_t q_row_stride, in
   const int per_split = (topk + splits - 1) / splits;
   const int kps = ((per_split + kStep - 1) / kStep) * kStep;
   const int hpw = ad.idx_head_stride ? 1 : heads_per_workgroup(rows, kv_heads, splits);
-  const int slices = kWaves / hpw;
+  // Waves per workgroup: 8 for one round of workgroups (decode batches), 4 when there are several rounds (prefill
+  // chunks, one row per query): two 4-wave workgroups then share a CU, and one's slot list and merge overlap the
+  // other's gather.
+  const int64_t units = (int64_t)rows * ((kv_heads + hpw - 1) / hpw) * splits;
+  const int waves = units >= kSmallWaveUnits ? 4 : kWaves;
+  const int slices = waves / hpw;
   const int slice_steps = ((kps / kStep + slices * kPrefetch - 1) / (slices * kPrefetch)) * kPrefetch;
   const int slot_bytes = slices * slice_steps * kStep * (int)sizeof(int32_t);
-  const size_t lds_bytes = (size_t)slot_bytes + (size_t)kWaves * kWaveLds + kMergeLds;
+  const size_t lds_bytes =
+      (size_t)slot_bytes + (size_t)waves * kWaveLds + (waves == 4 ? kMergeLds<4> : kMergeLds<kWaves>);
   if (lds_bytes > kMaxLds)
     return fail(XT_EUNSUPPORTED, "%s: %d keys per split needs %zu bytes of LDS; use more splits", what, kps,
                 lds_bytes);
@@ -832,7 +850,6 @@ static int decode_impl(const char* what, const void* q, int64_t q_row_stride, in
                   ad.sf_head_stride % 8 == 0;
   const dim3 grid((unsigned)launched);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (hpw == 4) return ps ? launch_decode<4, true>(a, grid, lds_bytes, st, what)
-                          : launch_decode<4, false>(a, grid, lds_bytes, st, what);
-  return ps ? launch_decode<1, true>(a, grid, lds_bytes, st, what) : launch_decode<1, false>(a, grid, lds_bytes, st, what);
+  return waves == 4 ? launch_decode<4>(hpw, ps, a, grid, lds_bytes, st, what)
+                    : launch_decode<kWaves>(hpw, ps, a, grid, lds_bytes, st, what);
 }
