@@ -36,7 +36,7 @@ namespace {
 constexpr int kDim = 128;          // head size: 64 payload bytes, 8 scale bytes per head row
 constexpr int kStep = 32;          // keys per step
 constexpr int kWaves = 8;          // wavefronts per workgroup: HPW KV heads x (8 / HPW) key slices
-constexpr int64_t kSmallWaveUnits = 1024;   // from this many workgroup units on, 4-wave workgroups (two per CU)
+constexpr int64_t kOneRound = 256;   // 8-wave workgroups that run at once (one per CU of the MI355X); beyond, 4-wave ones
 constexpr int kVRow = 80;          // LDS bytes per key in the V transpose tile (64 + 16: no bank conflicts)
 constexpr int kWaveLds = kStep * kVRow + kStep * 8;   // V tile + V scale tile per wave
 constexpr int kPrefetch = 4;       // steps of loads in flight per wave
@@ -774,11 +774,11 @@ static int decode_impl(const char* what, const void* q, int64_t q_row_stride, in
   const int per_split = (topk + splits - 1) / splits;
   const int kps = ((per_split + kStep - 1) / kStep) * kStep;
   const int hpw = ad.idx_head_stride ? 1 : heads_per_workgroup(rows, kv_heads, splits);
-  // Waves per workgroup: 8 for one round of workgroups (decode batches), 4 when there are several rounds (prefill
-  // chunks, one row per query): two 4-wave workgroups then share a CU, and one's slot list and merge overlap the
-  // other's gather.
+  // Waves per workgroup: 8 when the units fit one round of workgroups (decode batches), else 4 (prefill chunks, one
+  // row per query; odd batch sizes): two 4-wave workgroups then share a CU, and one's slot list and merge overlap the
+  // other's gather, where 8-wave ones would run a second round after the first.
   const int64_t units = (int64_t)rows * ((kv_heads + hpw - 1) / hpw) * splits;
-  const int waves = units >= kSmallWaveUnits ? 4 : kWaves;
+  const int waves = units > kOneRound ? 4 : kWaves;
   const int slices = waves / hpw;
   const int slice_steps = ((kps / kStep + slices * kPrefetch - 1) / (slices * kPrefetch)) * kPrefetch;
   const int slot_bytes = slices * slice_steps * kStep * (int)sizeof(int32_t);
