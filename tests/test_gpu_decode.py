@@ -218,6 +218,19 @@ def test_decode_long_context_workload():
     _check(out, ref, flash, strict=True)
 
 
+@pytest.mark.parametrize('batch,splits', [(96, 1), (40, 3)])
+def test_decode_past_one_round_of_workgroups(batch, splits):
+    """Unit counts beyond one round of 8-wave workgroups (384 and 480 at 4 KV heads) run 4-wave workgroups, two per
+    CU: every row matches the oracle. Outputs here reach magnitude 22, where one BF16 step is 0.125, so the absolute
+    bound applies beyond the BF16 rounding of the reference value (the flash-precision reference errs as much)."""
+    pool, pt, idx, q = _small_case(seed=50 + batch, batch=batch, ctx=1024, topk=400)
+    seq = np.full(batch, 1024, np.int32)
+    out = ops.sparse_decode(q.cuda(), pool.raw, pt.cuda(), idx.cuda(), torch.from_numpy(seq).cuda(), 0.09,
+                            page_size=64, splits=splits)
+    ref, flash, _ = _oracle(pool.raw, bf16_numpy(q), pt.numpy(), 64, np.arange(batch), idx.numpy(), None, seq, 0.09)
+    _check(out, ref, flash)
+
+
 def test_interleaved_pool_equals_split_pool():
     """The same bytes in the interleaved layout (one buffer; per slot each head's [K row | V row], then each head's
     [K scales | V scales]) and in SGLang's four buffers give the same bits."""
