@@ -15,6 +15,11 @@ Pinning (what each function is checked against, in ``tests/``):
   special cases (zero blocks, exact midpoints, negative values rounding to zero).
 - ``attention.*``: float64 softmax computed directly (no online/split form), single-key and empty-row special
   cases, split-K merge against one pass.
+- ``attention.pack_qsa``: torch's own dequantization of the whole pool (float8_e4m3fn scales, the E2M1 table, low
+  nibble first), then indexed; the decode gather with every position listed; a one-byte nibble-order case.
+- ``attention.flash_precision_attention``: a torch FP32 restatement of tests/qsa_decode_check.py:29-45 and a
+  two-key known answer where P rounded to BF16 and P kept in FP32 give different outputs.
+- ``attention.block_sparse_decode`` LSE: torch.logsumexp of the scaled scores over the expanded positions.
 - ``attention.block_sparse_decode`` / ``block_sparse_prefill``: the token-granular ``sparse_decode`` on the expanded
   block lists (with each query's position as the causal limit for the prefill); with every block listed, dense causal
   softmax over the copied context.
