@@ -4,13 +4,14 @@
 
 A step is one layer-step of batched GQA sparse decode: batch 32, 32 query / 4 KV heads, head size 128, context
 32768 per request, top-2048 sorted unique indices per request, NVFP4 paged KV (page 64, shuffled pages) built from
-bf16 N(0,1) with 1% outlier channels x8. The timed region replays a HIP graph of L layer-steps, each on its own
-layer's pool (distinct HBM, as the layers of a decode step), so the gathered rows come from HBM rather than from the
-previous step's cache lines; ms_per_step is the event-timed mean over the K steps.
+bf16 N(0,1) with 1% outlier channels x8. Exactly K layer-steps are timed: HIP graphs of L layer-steps, each on its own
+layer's pool (distinct HBM, as the layers of a decode step, so the gathered rows come from HBM rather than from the
+previous step's cache lines), replayed K // L times, plus one graph of the remaining K mod L steps. ms_per_step is
+the event-timed mean over the K steps; `timing` gives the median and p10 / p90 over the full replays.
 
 Prints one JSON line: value = achieved algorithmic HBM bandwidth (gathered KV payload + scales per step / step
-time), plus the µs per layer-step, the roofline record, and the CPU oracle timed on the host as a reported
-baseline.
+time), plus the µs per layer-step, the roofline record, and the torch CPU restatement timed on the host's cores as a
+reported baseline.
 """
 import argparse
 import json
@@ -42,6 +43,59 @@ def cpu_model():
     return platform.processor() or 'unknown'
 
 
+def cpu_threads():
+    """Host threads for the CPU baseline: every core, capped by OMP_NUM_THREADS where the host sets it (a shared GPU
+    box gives each GPU's jobs a share of its cores)."""
+    n = os.cpu_count() or 1
+    env = os.environ.get('OMP_NUM_THREADS')
+    return max(1, min(n, int(env))) if env and env.isdigit() else n
+
+
+def time_steps(step, layers, steps, warmup):
+    """Times exactly `steps` layer-steps. After `warmup` eager steps, a graph of `layers` layer-steps (layer l on its
+    own pool) is replayed steps // layers times and a graph of the remaining steps once, with HIP events on the
+    launching stream around each replay. Returns (ms per layer-step over the whole timed region, per-layer-step µs of
+    each full replay)."""
+    import torch
+    for i in range(warmup):
+        step(i % layers)
+    torch.cuda.synchronize()
+    full, rest = divmod(steps, layers)
+    graphs = []
+    for n in (layers if full else 0, rest):
+        g = None
+        if n:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for layer in range(n):
+                    step(layer)
+            g.replay()   # the first replay of a graph is not timed
+        graphs.append(g)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(full + 2)]
+    ev[0].record()
+    for i in range(full):
+        graphs[0].replay()
+        ev[i + 1].record()
+    if graphs[1] is not None:
+        graphs[1].replay()
+    ev[-1].record()
+    torch.cuda.synchronize()
+    per = [ev[i].elapsed_time(ev[i + 1]) * 1e3 / layers for i in range(full)]
+    return ev[0].elapsed_time(ev[-1]) / steps, per
+
+
+def spread(per_step_us):
+    """Median and p10 / p90 of the per-layer-step times of the full replays."""
+    import numpy as np
+    if not per_step_us:
+        return None
+    a = np.asarray(per_step_us)
+    return {'median_us': round(float(np.median(a)), 3), 'p10_us': round(float(np.percentile(a, 10)), 3),
+            'p90_us': round(float(np.percentile(a, 90)), 3), 'replays': len(a),
+            'unit': 'µs per layer-step, per graph replay'}
+
+
 def build_layer(w, gen, layout, workloads, KVPool):
     """One layer's pool: K and V drawn as bf16 N(0,1) with 1% outlier channels x8, per-tensor global scales
     amax / 2688, quantized on the GPU into every slot."""
@@ -54,46 +108,39 @@ def build_layer(w, gen, layout, workloads, KVPool):
     return pool.raw
 
 
-def cpu_baseline(raw, q, pt, idx, seq, w, scale, seconds):
-    """The CPU oracle (numpy, one thread) on the same workload: per request gather through the page table, NVFP4
-    dequant, FP32 softmax attention. Timed on a bounded sample of requests and scaled to the layer-step."""
+def cpu_baseline(raw, q, pt, idx, seq, w, scale, runs=20, warm=3):
+    """The torch CPU restatement of the decode (oracle/torch_cpu.py: slots through the page table, NVFP4 dequant of
+    the gathered rows, FP32 softmax attention), batched over the whole layer-step on the host's cores: 3 warm-ups,
+    then the median of 20 runs."""
     import numpy as np
-    from threadpoolctl import threadpool_limits
-
-    from oracle import attention
-
-    pt_h, idx_h, seq_h = pt.cpu().numpy(), idx.cpu().numpy(), seq.cpu().numpy()
-    batch = idx_h.shape[0]
-    slots = (pt_h[np.arange(batch)[:, None], idx_h // w.page].astype(np.int64) * w.page + idx_h % w.page)
-    uniq, inv = np.unique(slots, return_inverse=True)
-    inv = inv.reshape(slots.shape)
     import torch
-    sel = torch.from_numpy(uniq).cuda()
-    host = tuple(t.index_select(0, sel).cpu().numpy() for t in raw[:4]) + (raw[4].item(), raw[5].item())
-    # the compact pool's token table: position -> compact row
-    table = np.zeros((batch, w.ctx), np.int32)
-    table[np.arange(batch)[:, None], idx_h] = inv
-    qf = q.float().cpu().numpy()
 
-    def run(rows):
-        return attention.sparse_decode(qf[rows], host, table, 1, rows, idx_h[rows], None, seq_h[rows], scale,
-                                       dtype=np.float32)
+    from oracle import torch_cpu
 
-    with threadpool_limits(1):
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    pool = tuple(t.cpu() for t in raw[:4]) + (raw[4].item(), raw[5].item())
+    qf, pt_h, idx_h, seq_h = q.float().cpu(), pt.cpu(), idx.cpu(), seq.cpu()
+
+    def run():
+        slots = torch_cpu.slots_of(pt_h, w.page, idx_h, seq_h)
+        return torch_cpu.sparse_decode(qf, pool, slots, scale)
+
+    for _ in range(warm):
+        run()
+    times = []
+    for _ in range(runs):
         t0 = time.perf_counter()
-        run(np.array([0]))
-        per_row = time.perf_counter() - t0
-        n = int(max(1, min(batch, seconds / max(per_row, 1e-6))))
-        rows = np.arange(n)
-        t0 = time.perf_counter()
-        run(rows)
-        dt = time.perf_counter() - t0
-    us_step = dt / n * batch * 1e6
-    sample_bytes = n * w.topk * w.kv_heads * 2 * (w.dim // 2 + w.dim // 16)
-    return {'value': round(sample_bytes / dt / 1e9, 4), 'unit': 'GB/s', 'cores': 1, 'kind': 'port',
-            'us_per_layer_step': round(us_step, 1),
-            'sample': f'{n} of {batch} requests of one layer-step (oracle: numpy gather + NVFP4 dequant + FP32 '
-                      f'softmax attention, one thread, {cpu_model()}, {os.cpu_count()} host cores)'}
+        run()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {'value': round(w.algorithmic_bytes() / med / 1e9, 4), 'unit': 'GB/s', 'cores': threads, 'kind': 'port',
+            'us_per_layer_step': round(med * 1e6, 1), 'p10_us': round(float(np.percentile(times, 10)) * 1e6, 1),
+            'p90_us': round(float(np.percentile(times, 90)) * 1e6, 1),
+            'tokens_per_s': round(w.batch / med, 1),
+            'sample': f'the whole layer-step ({w.batch} requests, full size): torch CPU restatement (page-table slots, '
+                      f'NVFP4 dequant, FP32 softmax attention), {threads} threads of {os.cpu_count()} host cores '
+                      f'({cpu_model()}), {warm} warm-ups, median of {runs}'}
 
 
 def timed_sample(stage, run, total, seconds):
@@ -182,29 +229,15 @@ def run_prefill(args, w, ops, workloads, KVPool):
         ops.sparse_decode(inp.q, pool.raw, inp.page_table, inp.indices, seq, scale, page_size=w.page, row_req=row_req,
                           query_pos=inp.q_pos, out=out, splits=splits, ws=ws)
 
-    for _ in range(max(1, args.warmup)):
-        step()
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step()
-    graph.replay()
-    torch.cuda.synchronize()
     steps = max(1, args.steps)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
-        graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    ms, per = time_steps(lambda layer: step(), 1, steps, max(1, args.warmup))
     tflops = w.flops() / (ms * 1e-3) / 1e12
     gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
     log(f'{w.name}: {ms * 1e3:.1f} us per step, {tflops:.1f} TFLOP/s ({tflops / MFMA_PEAK_TFLOPS:.1%} of '
         f'{MFMA_PEAK_TFLOPS:.0f}), gathered {gbs:.0f} GB/s')
     record = {
         'metric': 'NVFP4-KV sparse prefill attention TFLOP/s (chunk with quantize-on-append)', 'value': round(tflops, 2),
-        'unit': 'TFLOP/s', 'n_gpus': 1, 'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6),
+        'unit': 'TFLOP/s', 'n_gpus': 1, 'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per),
         'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f16', 'data': 'synthetic',
         'config': {'workload': w.name, 'q_heads': w.q_heads, 'kv_heads': w.kv_heads, 'head_dim': w.dim,
                    'context': w.ctx0, 'chunk': w.chunk, 'topk': w.topk, 'recent': w.recent, 'page': w.page,
@@ -289,31 +322,15 @@ def run_mla(args, w, ops, workloads):
     def step(layer):
         ops.sparse_mla(inp.q, pools[layer], inp.slots, None, None, scale, out=out, lse=lse, splits=splits, ws=ws)
 
-    for i in range(max(1, args.warmup)):
-        step(i % layers)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for layer in range(layers):
-            step(layer)
-    graph.replay()
-    torch.cuda.synchronize()
-    replays = max(1, math.ceil(args.steps / layers))
-    steps = replays * layers
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(replays):
-        graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    steps = max(1, args.steps)
+    ms, per = time_steps(step, layers, steps, max(1, args.warmup))
     tflops = w.flops() / (ms * 1e-3) / 1e12
     gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
     log(f'{w.name}: {ms * 1e3:.1f} us per step, {tflops:.1f} TFLOP/s ({tflops / MFMA_PEAK_TFLOPS:.1%} of '
         f'{MFMA_PEAK_TFLOPS:.0f}), {gbs:.0f} GB/s gathered, splits {splits}')
     record = {
         'metric': 'NVFP4 sparse MLA attention TFLOP/s', 'value': round(tflops, 2), 'unit': 'TFLOP/s', 'n_gpus': 1,
-        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'higher_is_better': True,
+        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per), 'higher_is_better': True,
         'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16' if w.fmt == 'fp8_v4' else 'f16', 'data': 'synthetic',
         'config': {'workload': w.name, 'rows': w.rows, 'heads': w.heads, 'latent': w.latent, 'rope': w.rope,
                    'context': w.ctx, 'topk': w.topk, 'causal': w.causal,
@@ -404,30 +421,14 @@ def run_block(args, w, ops, workloads):
         ops.fp4_sparse_decode(inp.q, k_pay, k_sc, v_pay, v_sc, inp.req_to_token, inp.slot_ids, inp.topk_idx,
                               inp.seq_lens, w.block, out=out, splits=splits, ws=ws)
 
-    for i in range(max(1, args.warmup)):
-        step(i % layers)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for layer in range(layers):
-            step(layer)
-    graph.replay()
-    torch.cuda.synchronize()
-    replays = max(1, math.ceil(args.steps / layers))
-    steps = replays * layers
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(replays):
-        graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    steps = max(1, args.steps)
+    ms, per = time_steps(step, layers, steps, max(1, args.warmup))
     gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
     log(f'{w.name}: {ms * 1e3:.2f} us per layer-step, {gbs:.0f} GB/s algorithmic ({gbs / HBM_PEAK_GBS:.1%} of '
         f'{HBM_PEAK_GBS:.0f}), splits {splits}')
     record = {
         'metric': 'NVFP4-KV block-sparse decode HBM GB/s', 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1,
-        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'higher_is_better': True,
+        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per), 'higher_is_better': True,
         'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f16', 'data': 'synthetic',
         'config': {'workload': w.name, 'batch': w.batch, 'q_heads': w.q_heads, 'kv_heads': w.kv_heads,
                    'head_dim': w.dim, 'context': w.ctx, 'topk_blocks': w.topk_blocks, 'block': w.block,
@@ -496,27 +497,9 @@ def run_block_prefill(args, w, ops, workloads):
         for (pay, sc), dst in zip(((k_pay, k_sc), (v_pay, v_sc), ik), copies):
             ops.dequantize_context(pay, sc, inp.req_to_token, inp.slot_ids, inp.seq_lens, rows, out=dst)
 
-    def timed(fn, reps):
-        for i in range(max(1, args.warmup)):
-            fn(i % layers)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for layer in range(layers):
-                fn(layer)
-        graph.replay()
-        torch.cuda.synchronize()
-        n = max(1, math.ceil(reps / layers))
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(n):
-            graph.replay()
-        end.record()
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / (n * layers), n * layers
-
-    ms, steps = timed(step, args.steps)
-    copy_ms, _ = timed(copy, args.steps)
+    steps = max(1, args.steps)
+    ms, per = time_steps(step, layers, steps, max(1, args.warmup))
+    copy_ms, _ = time_steps(copy, layers, steps, max(1, args.warmup))
     tflops = w.flops() / (ms * 1e-3) / 1e12
     gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
     copy_gbs = w.copy_bytes() / (copy_ms * 1e-3) / 1e9
@@ -525,7 +508,7 @@ def run_block_prefill(args, w, ops, workloads):
         f'= {copy_gbs:.0f} GB/s ({copy_gbs / HBM_PEAK_GBS:.1%})')
     record = {
         'metric': 'NVFP4-KV block-sparse prefill TFLOP/s', 'value': round(tflops, 2), 'unit': 'TFLOP/s',
-        'n_gpus': 1, 'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'higher_is_better': True,
+        'n_gpus': 1, 'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per), 'higher_is_better': True,
         'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f16', 'data': 'synthetic',
         'config': {'workload': w.name, 'q_len': w.q_len, 'prefix': w.prefix, 'q_heads': w.q_heads,
                    'kv_heads': w.kv_heads, 'head_dim': w.dim, 'topk_blocks': w.topk_blocks, 'block': w.block,
@@ -600,31 +583,15 @@ def run_gather(args, name, ops, workloads, KVPool):
         else:
             ops.pack(pools[layer], r2t, req, cu, batch * topk, topk, torch.bfloat16)
 
-    for i in range(max(1, args.warmup)):
-        step(i % layers)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for layer in range(layers):
-            step(layer)
-    graph.replay()
-    torch.cuda.synchronize()
-    replays = max(1, math.ceil(args.steps / layers))
-    steps = replays * layers
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(replays):
-        graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    steps = max(1, args.steps)
+    ms, per = time_steps(step, layers, steps, max(1, args.warmup))
     rows = batch * topk * kv_heads
     nbytes = rows * 2 * (dim // 2 + dim // 16) + rows * 2 * dim * 2
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f'{name}: {ms * 1e3:.2f} us per layer-step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of {HBM_PEAK_GBS:.0f})')
     record = {
         'metric': f'NVFP4-KV {mode} into BF16 rows HBM GB/s', 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1,
-        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'higher_is_better': True,
+        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per), 'higher_is_better': True,
         'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic',
         'config': {'workload': name, 'batch': batch, 'kv_heads': kv_heads, 'head_dim': dim, 'context': ctx,
                    'rows_per_request': topk, 'page': page, 'kv_format': 'nvfp4 (SGLang buffers)',
@@ -701,30 +668,14 @@ def run_varlen(args, w, ops, workloads):
     def step(layer):
         ops.varlen_decode(q, kv[layer][0], kv[layer][1], cu_q, cu_k, 1, w.keys, scale, out=out, splits=splits, ws=ws)
 
-    for i in range(max(1, args.warmup)):
-        step(i % layers)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for layer in range(layers):
-            step(layer)
-    graph.replay()
-    torch.cuda.synchronize()
-    replays = max(1, math.ceil(args.steps / layers))
-    steps = replays * layers
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(replays):
-        graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    steps = max(1, args.steps)
+    ms, per = time_steps(step, layers, steps, max(1, args.warmup))
     gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
     log(f'{w.name}: {ms * 1e3:.2f} us per layer-step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of {HBM_PEAK_GBS:.0f}), '
         f'splits {splits}')
     record = {
         'metric': 'BF16 varlen split-K decode HBM GB/s', 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1,
-        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'higher_is_better': True,
+        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per), 'higher_is_better': True,
         'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic',
         'config': {'workload': w.name, 'rows': w.rows, 'q_heads': w.q_heads, 'kv_heads': w.kv_heads,
                    'head_dim': w.dim, 'keys_per_row': w.keys, 'kv_format': 'bf16 packed rows',
@@ -774,6 +725,8 @@ def main():
                         'head [K sf | V sf]) or split (SGLang buffers)')
     p.add_argument('--cpu-seconds', type=float, default=10.0)
     p.add_argument('--no-cpu-baseline', action='store_true')
+    p.add_argument('--no-layout-compare', action='store_true',
+                   help='decode workloads: skip timing the same step on the other pool layout')
     p.add_argument('--copy-calibration', type=int, default=0, metavar='MIB',
                    help='only copy MIB MiB between two device buffers 8 times (the known-size kernel that scales the '
                         'FETCH_SIZE / WRITE_SIZE counters), then exit')
@@ -828,25 +781,8 @@ def main():
     def step(layer):
         ops.sparse_decode(q, layers[layer], pt, idx, seq, scale, page_size=w.page, out=out, splits=splits, ws=ws)
 
-    for i in range(args.warmup):
-        step(i % args.layers)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for layer in range(args.layers):
-            step(layer)
-    graph.replay()
-    torch.cuda.synchronize()
-    replays = max(1, math.ceil(args.steps / args.layers))
-    steps = replays * args.layers
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(replays):
-        graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    steps = max(1, args.steps)
+    ms, per = time_steps(step, args.layers, steps, args.warmup)
     nbytes = w.algorithmic_bytes()
     gbs = nbytes / (ms * 1e-3) / 1e9
     props = torch.cuda.get_device_properties(0)
@@ -854,11 +790,23 @@ def main():
         f'{HBM_PEAK_GBS:.0f}), splits {splits}, {args.layout} pool, {props.multi_processor_count} CUs')
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(layers[0], q, pt, idx, seq, w, scale, args.cpu_seconds)
+        cpu = cpu_baseline(layers[0], q, pt, idx, seq, w, scale)
         log(f'cpu baseline: {cpu}')
+    other = None
+    if not args.no_layout_compare:
+        # the same step on the other pool layout (SGLang's split buffers are what the drop-in hook receives)
+        alt = 'split' if args.layout == 'interleaved' else 'interleaved'
+        del layers
+        torch.cuda.empty_cache()
+        layers = [build_layer(w, gen, alt, workloads, KVPool) for _ in range(args.layers)]
+        ms_alt, per_alt = time_steps(step, args.layers, steps, args.warmup)
+        other = {'pool_layout': alt, 'us_per_layer_step': round(ms_alt * 1e3, 3), 'timing': spread(per_alt),
+                 'achieved_gbs': round(nbytes / (ms_alt * 1e-3) / 1e9, 1),
+                 'frac': round(nbytes / (ms_alt * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f'{alt} pool: {ms_alt * 1e3:.2f} us per layer-step')
     record = {
         'metric': METRIC, 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1, 'steps': steps,
-        'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'higher_is_better': True, 'scaling': 'weak',
+        'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per), 'higher_is_better': True, 'scaling': 'weak',
         'vs_baseline': None, 'dtype': 'f16', 'data': 'synthetic',
         'config': {'workload': w.name, 'batch': w.batch, 'q_heads': w.q_heads, 'kv_heads': w.kv_heads,
                    'head_dim': w.dim, 'context': w.ctx, 'topk': w.topk, 'page': w.page, 'kv_format': 'nvfp4',
@@ -870,6 +818,7 @@ def main():
                      'frac': round(gbs / HBM_PEAK_GBS, 4),
                      'traffic': measured_traffic(w.name, splits, args.layout)},
         'cpu_baseline': cpu,
+        'other_layout': other,
     }
     print(json.dumps(record), flush=True)
 

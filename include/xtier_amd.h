@@ -282,6 +282,14 @@ int xt_sparse_mla_fp8(const void* q, int64_t q_row_stride, int64_t q_head_stride
                       int64_t out_head_stride, int out_dtype, float* lse, int rows, int splits, void* workspace,
                       size_t workspace_bytes, xt_stream_t stream);
 
+/* Self-test, no counterpart in the reference: the known-answer test of the hardware conversions the attention kernels
+ * use (E4M3 -> FP16 from either half of a dword, two E2M1 codes -> FP16 / FP32 from each byte position, E4M3 with a
+ * power-of-2 scale -> BF16), for every byte, written to `out` (xt_selftest_conversions_bytes() bytes, 16-byte
+ * aligned) as laid out in xtier_amd/csrc/selftest.hip. The reference checks its own decodes the same way
+ * (tests/fp4_decode_check.py:67-107, tests/fp8_decode_check.py:28-45). */
+size_t xt_selftest_conversions_bytes(void);
+int xt_selftest_conversions(void* out, xt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -72,5 +72,5 @@ def test_quantize_and_gather_reject_bad_layouts(lib):
     with pytest.raises(ValueError, match='power-of-2 head size'):
         _lib.check(st, 'gather')
     with pytest.raises(NotImplementedError):
-        _lib.check(_decode(lib, dim=64), 'decode')
+        _lib.check(_decode(lib, dim=512), 'decode')
     assert isinstance(lib.xt_last_error(), bytes) and ctypes.sizeof(ctypes.c_void_p) == 8

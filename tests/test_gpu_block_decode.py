@@ -152,7 +152,8 @@ def test_decode_main_hook_equals_direct_call():
     w, inp = _small(13, b=2, ctx=1024, topk=4)
     k_pay, k_sc, v_pay, v_sc = _pool(w, 8, w.batch)
     k_view, v_view = k_pay[:], v_pay[:]
-    k_view._xtier_fp4, v_view._xtier_fp4 = k_sc, v_sc
+    setattr(k_view, minimax.TAG, k_sc)
+    setattr(v_view, minimax.TAG, v_sc)
     got = minimax.decode_main(None, q=inp.q, k_cache=k_view, v_cache=v_view, req_to_token=inp.req_to_token,
                               slot_ids=inp.slot_ids, topk_idx=inp.topk_idx, seq_lens=inp.seq_lens,
                               block_size=w.block, sm_scale=0.1, q_scale=0.5, k_scale=1.0)

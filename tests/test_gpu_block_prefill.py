@@ -138,7 +138,8 @@ def test_prefill_hooks(monkeypatch):
     k_pay, k_sc, v_pay, v_sc = _pages(4, 16)
     ik_pay, ik_sc = _pages(6, 16, heads=1)[:2]
     ik_pay, ik_sc = ik_pay[:, 0], ik_sc[:, 0]
-    k_pay._xtier_fp4, v_pay._xtier_fp4, ik_pay._xtier_fp4 = k_sc, v_sc, ik_sc
+    for view, sc in ((k_pay, k_sc), (v_pay, v_sc), (ik_pay, ik_sc)):
+        setattr(view, minimax.TAG, sc)
     # prefill_main: keyword call -> the NVFP4 prefill
     kw = dict(q=c['q'], k_cache=k_pay, v_cache=v_pay, sink=None, req_to_token=c['r2t'], slot_ids=c['sid'],
               topk_idx=c['ids'], block_size_q=1, block_size_k=BLOCK, cu_seqlens=c['cu'], seq_lens=c['seq'],

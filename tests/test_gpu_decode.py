@@ -44,16 +44,53 @@ def test_decode_workload(name, batch):
     assert np.abs(lse.cpu().numpy() - lse_ref).max() < 2e-3
 
 
-def _small_case(seed=3, batch=6, ctx=3008, heads=4, qh=32, topk=700, page=64):
+def _small_case(seed=3, batch=6, ctx=3008, heads=4, qh=32, topk=700, page=64, dim=128):
     gen = workloads.generator('cpu', seed)
     ctx_p = -(-ctx // page) * page
-    k = workloads.kv_tensor(batch * ctx_p, heads, 128, gen, 'cpu')
-    v = workloads.kv_tensor(batch * ctx_p, heads, 128, gen, 'cpu')
+    k = workloads.kv_tensor(batch * ctx_p, heads, dim, gen, 'cpu')
+    v = workloads.kv_tensor(batch * ctx_p, heads, dim, gen, 'cpu')
     pool = Pool(k, v)
     pt = workloads.page_table(batch, ctx_p, page, gen, 'cpu')
     idx = workloads.index_lists(batch, ctx_p, topk, gen, 'cpu')
-    q = (torch.randn(batch, qh, 128, generator=gen) * 2).to(torch.bfloat16)
+    q = (torch.randn(batch, qh, dim, generator=gen) * 2).to(torch.bfloat16)
     return pool, pt, idx, q
+
+
+@pytest.mark.parametrize('dim,heads,qh,batch,splits', [
+    (64, 2, 16, 6, 1), (64, 4, 32, 40, 4), (64, 1, 8, 5, 3),
+    (256, 2, 24, 6, 1), (256, 2, 24, 6, 5), (256, 4, 32, 80, 4), (256, 1, 4, 3, 2),
+])
+def test_decode_head_sizes(dim, heads, qh, batch, splits):
+    """Head sizes 64 and 256 (the reference's Qwen3.8 QSA shape is 2 KV heads x 256) against the oracle, with -1
+    holes, short rows and key splits; 80 rows x 4 KV heads x 4 splits takes 4 KV heads per workgroup."""
+    pool, pt, idx, q = _small_case(seed=dim + heads * 10 + batch, batch=batch, heads=heads, qh=qh, dim=dim)
+    idx = idx.numpy().copy()
+    idx[0, ::9] = -1
+    seq = np.full(batch, 3008, np.int32)
+    seq[-1] = 1200
+    scale = dim ** -0.5
+    lse = torch.empty(batch, qh, dtype=torch.float32, device='cuda')
+    out = ops.sparse_decode(q.cuda(), pool.raw, pt.cuda(), _dev(idx), _dev(seq), scale, page_size=64, lse=lse,
+                            splits=splits)
+    ref, flash, lse_ref = _oracle(pool.raw, bf16_numpy(q), pt.numpy(), 64, np.arange(batch), idx, None, seq, scale)
+    _check(out, ref, flash)
+    assert np.abs(lse.cpu().numpy() - lse_ref).max() < 2e-3
+
+
+@pytest.mark.parametrize('dim', [64, 256])
+def test_decode_head_sizes_single_key_and_empty_rows(dim):
+    """One valid key gives that V row (bit for bit after BF16 rounding); no valid key gives exact zeros."""
+    pool, pt, idx, q = _small_case(seed=7, batch=3, heads=2, qh=8, dim=dim, topk=64)
+    counts = np.array([0, 1, 64], np.int32)
+    seq = np.full(3, 3008, np.int32)
+    out = ops.sparse_decode(q.cuda(), pool.raw, pt.cuda(), idx.cuda(), _dev(seq), dim ** -0.5, page_size=64,
+                            counts=_dev(counts), splits=2)
+    assert not out[0].any()
+    pos = int(idx[1, 0])
+    slot = int(pt[1, pos // 64]) * 64 + pos % 64
+    v = nvfp4.dequant(pool.v_pay[slot], pool.v_sf[slot], pool.gv)          # [heads, dim]
+    want = torch.from_numpy(np.repeat(v, 4, axis=0)).to(torch.bfloat16)
+    assert torch.equal(out[1].cpu().view(torch.int16), want.view(torch.int16))
 
 
 def test_decode_edge_rows():
@@ -150,16 +187,18 @@ def test_graph_replay_equals_eager():
 
 
 @pytest.mark.parametrize('heads,qh,batch,ctx,topk,splits', [
-    (1, 16, 5, 3008, 700, 3),    # one KV head, group 16: one head per workgroup
-    (2, 32, 4, 3008, 700, 1),
-    (6, 24, 3, 3008, 700, 2),    # KV heads not a multiple of 4
-    (8, 64, 40, 512, 300, 8),    # 4 heads per workgroup, 2 head groups per row
-    (12, 48, 32, 512, 300, 8),   # 4 heads per workgroup, 3 head groups
-    (4, 32, 64, 512, 300, 4),    # 4 heads per workgroup with cross-workgroup partials
+    (1, 16, 5, 3008, 700, 3),    # one KV head, group 16: 8-wave workgroups of 1 KV head x 8 slices
+    (1, 4, 6, 3008, 700, 3),     # group 4: a partial block of 4 heads, so 128-B lines straddle splits and rows
+    (2, 32, 4, 3008, 700, 1),    # 1 KV head x 8 slices, no partials
+    (6, 24, 3, 3008, 700, 2),    # KV heads not a multiple of 4: 1 KV head x 8 slices
+    (8, 64, 40, 512, 300, 8),    # 640 units of 4 KV heads: past one round, 4-wave workgroups of 4 heads x 1 slice
+    (12, 48, 32, 512, 300, 8),   # 768 units of 4 KV heads, 3 head groups per row: 4-wave, 4 heads x 1 slice
+    (4, 32, 64, 512, 300, 4),    # exactly 256 units: 8-wave workgroups of 4 KV heads x 2 slices, with partials
 ])
 def test_decode_head_layouts(heads, qh, batch, ctx, topk, splits):
-    """KV head counts and GQA groups over both workgroup shapes (4 KV heads x 2 key slices for many rows, 1 KV head x
-    8 slices for few) and with or without key splits."""
+    """KV head counts and GQA groups over the workgroup shapes (on 256 CUs: 4 KV heads x 2 slices at one round of
+    workgroups, 4 heads x 1 slice in 4-wave workgroups past it, 1 KV head x 8 slices for few rows), with or without
+    key splits."""
     pool, pt, idx, q = _small_case(seed=heads * 100 + batch, batch=batch, ctx=ctx, heads=heads, qh=qh, topk=topk)
     seq = np.full(batch, ctx, np.int32)
     out = ops.sparse_decode(q.cuda(), pool.raw, pt.cuda(), idx.cuda(), _dev(seq), 0.0884, page_size=64,
@@ -289,3 +328,32 @@ def test_one_workspace_serves_calls_of_any_shape():
                                   ws=ops.new_workspace('cuda', rows, 32, 128, splits))
         assert torch.equal(got.view(torch.int16), fresh.view(torch.int16)), (rows, splits)
     assert not ws[:65536].any()   # the counters are left zero
+
+
+def test_graph_survives_a_grown_workspace():
+    """A graph captured on the cached per-device workspace keeps replaying correctly after a larger eager call has
+    grown that workspace: the old buffer stays allocated (the graph holds its address), so a tensor allocated and
+    filled afterwards is untouched by the replays and every replay equals the eager result."""
+    pool, pt, idx, q = _small_case(seed=41, batch=8)
+    seq = torch.full((8,), 3008, dtype=torch.int32, device='cuda')
+    args = (pool.raw, pt.cuda(), idx.cuda(), seq, 0.0884)
+    qs = q.cuda().clone()
+    out = torch.empty(8, 32, 128, dtype=torch.bfloat16, device='cuda')
+    ops.workspace('cuda', ops.decode_workspace_bytes(8, 32, 128, 4))
+    ops.sparse_decode(qs, *args, page_size=64, out=out, splits=4)   # the cached workspace, warm-up
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.sparse_decode(qs, *args, page_size=64, out=out, splits=4)
+    # an eager call that needs more bytes than the cached workspace holds replaces it
+    before = ops._cached_workspace_bytes(torch.device('cuda'))
+    ops.sparse_decode(qs, *args, page_size=64, splits=48)
+    assert ops._cached_workspace_bytes(torch.device('cuda')) > before
+    torch.cuda.synchronize()
+    canary = torch.full((before // 4 + 4096,), 1234567, dtype=torch.int32, device='cuda')
+    eager = ops.sparse_decode(qs, *args, page_size=64, splits=4, ws=ops.new_workspace('cuda', 8, 32, 128, 4))
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16))
+        assert bool((canary == 1234567).all())

@@ -1,7 +1,9 @@
 """Sparse MLA on the GPU against the FP64 oracle (tests/ds_sparse_mla_check.py:44-67 restated for an NVFP4 latent +
 BF16 rope cache): errors measured as the reference measures them (max |err| / max |ref| < 1e-2, rms err / rms ref <
-4e-3, tests/ds_sparse_mla_check.py:70-75, :160), plus the BF16 absolute bound max 2e-2 / mean 2e-3; rows without keys
-exactly 0 with LSE -inf; two key lists; sink; key splits; graph replay equal to eager."""
+4e-3, tests/ds_sparse_mla_check.py:70-75, :160), plus the absolute bound max 2e-2 / mean 2e-3; rows without keys
+exactly 0 with LSE -inf; two key lists; sink; key splits; graph replay equal to eager; the decode and prefill
+workloads at their full sizes (64 rows at context 131072, a 2048-row causal chunk, top-2048) and latents whose
+per-token magnitudes span three decades (tests/qsa_fp4_check.py:26-34)."""
 import math
 
 import numpy as np
@@ -50,8 +52,7 @@ def _check(out, lse, ref, ref_lse, nonempty=None):
     max_rel = np.abs(d).max() / np.abs(r_s).max()
     rms_rel = np.sqrt((d ** 2).mean()) / np.sqrt((r_s ** 2).mean())
     assert max_rel < 1e-2 and rms_rel < 4e-3, (max_rel, rms_rel)
-    assert np.abs(d).max() <= 2e-2 + np.abs(r_s).max() * 2 ** -8 and np.abs(d).mean() <= 2e-3, \
-        (np.abs(d).max(), np.abs(d).mean())
+    assert np.abs(d).max() <= 2e-2 and np.abs(d).mean() <= 2e-3, (np.abs(d).max(), np.abs(d).mean())
     if lse is not None:
         l_ = lse.reshape(ref_lse.shape).cpu().numpy()
         fin = np.isfinite(ref_lse)
@@ -191,3 +192,60 @@ def test_mla_graph_replay_equals_eager():
         eager, _ = ops.sparse_mla(qs, pool, inp.slots, None, None, 0.05, splits=splits)
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int16), eager.view(torch.int16))
+
+
+def _compact_ref(q, pool, idx, scale):
+    """The oracle on host copies of only the cache rows the lists name (a full-size cache stays on the GPU)."""
+    flat = idx.reshape(-1).long()
+    ok = flat >= 0
+    uniq, inv = torch.unique(flat[ok], return_inverse=True)
+    host = (pool.pay[uniq].cpu().numpy(), pool.scales[uniq].cpu().numpy(), pool.rope[uniq].float().cpu().numpy(),
+            np.float32(pool.g.item()))
+    local = torch.full_like(flat, -1)
+    local[ok] = inv
+    return attention.sparse_mla(q.float().cpu().numpy(), *host, local.reshape(idx.shape).cpu().numpy(), None, None,
+                                scale)
+
+
+def test_mla_decode_workload_full_size():
+    """The decode workload as measured: 64 rows at context 131072 (an 8.4M-token cache), 128 heads, top-2048, default
+    splits; every row against the oracle."""
+    w = workloads.MLA_WORKLOADS['mla_decode_b64']
+    inp = workloads.mla_inputs(w, 20261029, 'cuda')
+    pool = _pool(w, 13)
+    scale = 1 / math.sqrt(576)
+    out, lse = ops.sparse_mla(inp.q[:, None], pool, inp.slots[:, None], None, None, scale)
+    ref, ref_lse = _compact_ref(inp.q, pool, inp.slots, scale)
+    _check(out, lse, ref, ref_lse)
+
+
+def test_mla_prefill_chunk_full_size_sampled_rows():
+    """The prefill workload as measured: a 2048-row causal chunk at the end of a 131072-token context, top-2048 per
+    query (the 128 most recent included); the whole chunk runs, 64 rows spread over it are checked."""
+    w = workloads.MLA_WORKLOADS['mla_prefill_2048']
+    inp = workloads.mla_inputs(w, 20261029, 'cuda')
+    pool = _pool(w, 14)
+    scale = 1 / math.sqrt(576)
+    out, lse = ops.sparse_mla(inp.q, pool, inp.slots, None, None, scale)
+    rows = torch.cat([torch.arange(0, 2048, 33, device='cuda')[:62], torch.tensor([2046, 2047], device='cuda')])
+    ref, ref_lse = _compact_ref(inp.q[rows], pool, inp.slots[rows], scale)
+    _check(out[rows], lse[rows], ref, ref_lse)
+
+
+def test_mla_latent_magnitudes_over_three_decades():
+    """Per-token latent magnitudes 10^U(-2, 1) (the spread of tests/qsa_fp4_check.py:26-34): small tokens' latents
+    come out of (e2m1 * e4m3) * g near the bottom of FP16's normal range, and still meet the bounds."""
+    w = workloads.MlaWorkload('mla_spread', 16, 128, 8192, 2048)
+    inp = workloads.mla_inputs(w, 20261023, 'cuda')
+    gen = workloads.generator('cuda', 77)
+    lat, rope = workloads.mla_cache_rows(w, gen, 'cuda', 0, w.slots)
+    mag = 10 ** torch.empty(w.slots, 1, device='cuda').uniform_(-2, 1, generator=gen)
+    lat = (lat.float() * mag).to(torch.bfloat16)
+    rope = (rope.float() * mag).to(torch.bfloat16)
+    pool = LatentPool(w.slots, w.latent, w.rope, 'cuda')
+    pool.set_global_scale(lat)
+    pool.append(lat, rope, torch.arange(w.slots, device='cuda'), saturate=False)
+    scale = 1 / math.sqrt(576)
+    out, lse = ops.sparse_mla(inp.q, pool, inp.slots, None, None, scale)
+    ref, ref_lse = _compact_ref(inp.q, pool, inp.slots, scale)
+    _check(out, lse, ref, ref_lse)

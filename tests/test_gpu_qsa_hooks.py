@@ -49,8 +49,8 @@ class _Backend:
         return topk_indices
 
 
-def _setup(seed=3, reqs=6, ctx=2048, topk=300, heads=4, qh=32):
-    pool = random_pool(seed, reqs * ctx, heads, 128)
+def _setup(seed=3, reqs=6, ctx=2048, topk=300, heads=4, qh=32, dim=128):
+    pool = random_pool(seed, reqs * ctx, heads, dim)
     gen = workloads.generator('cpu', seed + 1)
     pt = workloads.page_table(reqs, ctx, 64, gen, 'cpu')
     r2t = workloads.token_table(pt, 64)
@@ -58,22 +58,27 @@ def _setup(seed=3, reqs=6, ctx=2048, topk=300, heads=4, qh=32):
     idx[1, ::5] = -1
     seq = torch.full((reqs,), ctx, dtype=torch.int32)
     seq[2] = ctx // 2
-    q = (torch.randn(reqs, qh * 128, generator=gen) * 2).to(torch.bfloat16)
+    q = (torch.randn(reqs, qh * dim, generator=gen) * 2).to(torch.bfloat16)
     return pool, r2t, idx, seq, q
 
 
-def test_paged_attention_fused_matches_oracle():
-    pool, r2t, idx, seq, q = _setup()
+@pytest.mark.parametrize('heads,qh,dim', [
+    (4, 32, 128),
+    (2, 24, 256),   # the reference's Qwen3.8 QSA shape (tests/qsa_fp4_check.py:21, tests/qsa_decode_check.py:54)
+    (2, 16, 64),
+])
+def test_paged_attention_fused_matches_oracle(heads, qh, dim):
+    pool, r2t, idx, seq, q = _setup(heads=heads, qh=qh, dim=dim)
     reqs = q.shape[0]
     rows = torch.tensor([5, 4, 3, 2, 1, 0])        # row r reads request 5 - r
     backend = _Backend(pool.raw, r2t.cuda(), seq[rows].cuda(), rows=rows.cuda())
-    layer = SimpleNamespace(layer_id=1, scaling=1 / math.sqrt(128))
+    layer = SimpleNamespace(layer_id=1, scaling=1 / math.sqrt(dim))
     out = qsa.paged_attention(None, backend, q.cuda(), layer, SimpleNamespace(req_pool_indices=None),
                               idx[rows].cuda())
-    assert out.shape == (reqs, 32 * 128) and out.dtype == torch.bfloat16
-    ref, flash, _ = oracle(pool.raw, bf16_numpy(q).reshape(reqs, 32, 128), r2t.numpy(), 1, rows.numpy(),
-                           idx[rows].numpy(), None, seq[rows].numpy(), 1 / math.sqrt(128))
-    check(out.view(reqs, 32, 128), ref, flash)
+    assert out.shape == (reqs, qh * dim) and out.dtype == torch.bfloat16
+    ref, flash, _ = oracle(pool.raw, bf16_numpy(q).reshape(reqs, qh, dim), r2t.numpy(), 1, rows.numpy(),
+                           idx[rows].numpy(), None, seq[rows].numpy(), 1 / math.sqrt(dim))
+    check(out.view(reqs, qh, dim), ref, flash)
 
 
 def test_extraction_and_pack_inside_forward_extend():
@@ -106,8 +111,9 @@ def test_extraction_and_pack_inside_forward_extend():
     assert torch.equal(seen['pack'][1].view(torch.int16), pv.view(torch.int16))
 
 
-def test_paged_attention_graph_replay_equals_eager():
-    pool, r2t, idx, seq, q = _setup(seed=12)
+@pytest.mark.parametrize('heads,qh,dim', [(4, 32, 128), (2, 24, 256)])
+def test_paged_attention_graph_replay_equals_eager(heads, qh, dim):
+    pool, r2t, idx, seq, q = _setup(seed=12, heads=heads, qh=qh, dim=dim)
     backend = _Backend(pool.raw, r2t.cuda(), seq.cuda())
     layer = SimpleNamespace(layer_id=1, scaling=0.09)
     fb = SimpleNamespace(req_pool_indices=torch.arange(q.shape[0]).cuda())

@@ -20,7 +20,7 @@ def test_falls_through_without_scale_bytes():
 
 def test_unit_scales_and_unsupported_features():
     k = torch.zeros(2, 4, 128, 64, dtype=torch.uint8)
-    k._xtier_fp4 = torch.zeros(2, 4, 128, 8, dtype=torch.uint8)
+    setattr(k, minimax.TAG, torch.zeros(2, 4, 128, 8, dtype=torch.uint8))
     base = dict(q=torch.zeros(1, 16, 128), k_cache=k, v_cache=k)
     with pytest.raises(ValueError):
         minimax.decode_main(_original, **base, k_scale=0.5)
@@ -37,7 +37,7 @@ def test_attach_scales_and_install():
                                                      v_scale_buffer=scs[::-1]),
                            index_k_pool=SimpleNamespace(k_buffer=[], k_scale_buffer=[]), size=7)
     minimax.attach_scales(pool)
-    assert minimax._scales(pays[0]) is scs[0] and minimax._scales(pays[1]) is scs[1]
+    assert minimax.scales_of(pays[0]) is scs[0] and minimax.scales_of(pays[1]) is scs[1]
     seen = []
     registry = SimpleNamespace(register=lambda name, fn, kind: seen.append((name, fn, kind)))
     minimax.install(registry, SimpleNamespace(AROUND='around'))

@@ -34,7 +34,7 @@ def _calls():
     log = []
 
     def original(*args, **kwargs):
-        log.append((args, kwargs, list(qsa._active)))
+        log.append((args, kwargs, list(qsa._stack)))
         return 'original'
     return log, original
 
@@ -74,13 +74,13 @@ def test_forward_extend_activates_layer_and_restores_on_error():
     args, kwargs, active = log[-1]
     assert args == (backend, 'q', 'k', 'v', layer, 'fb', 'extra') and kwargs == {'flag': True}
     assert len(active) == 1 and active[0][4].tolist() == [2.0]
-    assert qsa._active == []
+    assert qsa._stack == []
 
     def failing(*a, **k):
         raise KeyError('x')
     with pytest.raises(KeyError):
         qsa.forward_extend(failing, backend, 'q', 'k', 'v', layer, 'fb')
-    assert qsa._active == []
+    assert qsa._stack == []
     # a non-NVFP4 pool runs original with nothing active
     qsa.forward_extend(original, SimpleNamespace(token_to_kv_pool=_Pool('bf16')), 'q', 'k', 'v', layer, 'fb')
     assert log[-1][2] == []

@@ -3,16 +3,17 @@
 // row a workgroup writes its heads' outputs directly; with several, each workgroup writes one partial result per
 // (row, key split, head), and the last workgroup of a (row, KV head group) to finish merges them.
 //
-// Work decomposition: a workgroup = 8 wavefronts = HPW consecutive KV heads x 8 / HPW key slices of one (query row,
-// key split), HPW = 4 (many rows) or 1 (few rows: more workgroups); each wave owns one (row, KV head, split, slice)
-// and walks its keys in steps of 32. The workgroup computes the split's pool slots once into LDS and merges the
-// slices of each head through LDS (a tree of log2(8 / HPW) rounds). Workgroups are numbered so that all units of a row
-// run on the same XCD (round-robin dispatch puts workgroup g on XCD g % 8): their K/V lines, which hold several
-// heads, and their partials share one L2.
+// Work decomposition: a workgroup = W wavefronts = HPW consecutive KV heads x W / HPW key slices of one (query row,
+// key split). HPW = 4 when the KV heads are a multiple of 4 and that alone fills every CU, else 1 (more workgroups).
+// W = 8 while the workgroups fit one round on the CUs (decode batches), else 4, compiled for two workgroups per CU
+// (prefill chunks, one row per query). Each wave owns one (row, KV head, split, slice) and walks its keys in steps of
+// 32. The workgroup computes the split's pool slots once into LDS and merges the slices of each head through LDS
+// behind one barrier. Workgroups are numbered so that all units of a row run on the same XCD (round-robin dispatch
+// puts workgroup g on XCD g % 8): their K/V lines, which hold several heads, and their partials share one L2.
 //
-// Memory pipeline: per step a wave issues 6 loads (K and V payload as 16-byte row pieces, K and V scales as one dword
-// per lane) and keeps P steps in flight in a register ring. V is transposed for the PV operand through a padded LDS
-// tile; the K scales reach their lanes with one ds_bpermute per 16-key tile.
+// Memory pipeline: per step a wave issues 6 loads (K and V payload as row pieces, K and V scales as dwords) and keeps
+// P steps in flight in a register ring. V is transposed for the PV operand through a padded LDS tile; the K scales
+// reach their lanes with ds_bpermute.
 //
 // Numerics: e2m1 * e4m3 is exact in FP16 (at most 6 significant bits, magnitudes 2^-10 .. 2688), so K and V enter
 // the MFMA exactly without their global scales; the query enters as FP16 of q * scale * log2(e); the K global scale
@@ -20,33 +21,47 @@
 // The running maximum is raised only when a score exceeds it by more than 2^8 (lazy rescale), so P <= 256.
 //
 // Lane layouts (16x16x32 MFMA: A[i][k] = lane i + 16*(k/8), element k%8; B[k][j] = lane j + 16*(k/8), element k%8;
-// C[i][j] = lane j + 16*(i/4), element i%4). With hl = lane % 16 and j = lane / 16:
-//   QK: C = S^T [16 keys x 16 heads]; A = K tile, lane (key hl, payload bytes 16j .. 16j+15 of the head row); MFMA kk
-//       (0..3) contracts dword kk of those 16 bytes, d = 32j + 8kk + e; B = Q^T in the same d order. Lane (hl, j)
-//       ends up with the scores of head hl for keys T(j) = {4j..4j+3, 16+4j..16+4j+3} of the step.
-//   PV: C = O^T [16 rows x 16 heads], row c = payload dword c of the head row; MFMA i (0..7) takes nibble i of every
-//       dword, d = 8c + i. A = V^T, lane (dword hl, keys T(j)); B = P^T, lane (head hl, keys T(j)) in the same order.
-//       Lane (hl, j) ends up with O^T of head hl for d = 32j .. 32j+31.
+// C[i][j] = lane j + 16*(i/4), element i%4). With hl = lane % 16, j = lane / 16 and head size D (64, 128, 256):
+//   QK: C = S^T [16 keys x 16 heads]; A = K tile, lane (key hl, payload bytes (D/8) j .. of the head row); MFMA kk
+//       (0 .. D/32 - 1) contracts dword kk of those bytes, d = (D/4) j + 8kk + e; B = Q^T in the same d order. Lane
+//       (hl, j) ends up with the scores of head hl for keys T(j) = {4j..4j+3, 16+4j..16+4j+3} of the step.
+//   PV: C = O^T [16 rows x 16 heads] per tile t of 16 payload dwords, row c = payload dword 16t + c of the head row;
+//       MFMA i (0..7) takes nibble i of every dword, d = 8 (16t + c) + i. A = V^T, lane (dword hl, keys T(j)); B = P^T,
+//       lane (head hl, keys T(j)) in the same order. Lane (hl, j) ends up with O^T of head hl for
+//       d = 128t + 32j .. 128t + 32j + 31 (D = 64: one tile, lanes j >= 2 empty).
 #include "xt_common.h"
 #include "xt_host.h"
 
 namespace xt {
 namespace {
 
-constexpr int kDim = 128;          // head size: 64 payload bytes, 8 scale bytes per head row
 constexpr int kStep = 32;          // keys per step
-constexpr int kWaves = 8;          // wavefronts per workgroup: HPW KV heads x (8 / HPW) key slices
-constexpr int64_t kOneRound = 256;   // 8-wave workgroups that run at once (one per CU of the MI355X); beyond, 4-wave ones
-constexpr int kVRow = 80;          // LDS bytes per key in the V transpose tile (64 + 16: no bank conflicts)
-constexpr int kWaveLds = kStep * kVRow + kStep * 8;   // V tile + V scale tile per wave
-constexpr int kPrefetch = 4;       // steps of loads in flight per wave
+constexpr int kWaves = 8;          // wavefronts per workgroup while one round of workgroups covers the launch
 constexpr int kSlotBatch = 4;      // keys per thread whose index / table loads are in flight together
 constexpr float kRescale = 8.0f;   // log2 of the largest P before the running maximum is raised
-constexpr int kPartStride = kDim + 4;   // floats per partial (split, head): 128 accumulators, max, sum, 2 pad
-constexpr int kMergeRow = 36;      // floats per lane in the slice merge: 32 accumulators, max, sum, 2 pad
-template <int W>
-constexpr int kMergeLds = W * 64 * kMergeRow * 4;   // one region per wave
 constexpr size_t kMaxLds = 160 * 1024 - 256;   // dynamic LDS per workgroup (the rest: static LDS)
+
+// How a head row of size D (64, 128 or 256) maps onto the lanes and LDS. In the QK layout four lanes (j = 0..3) share
+// a key, lane j holding payload bytes kLaneBytes * j .. of it, i.e. dims d = (D / 4) j + 8 kk + e for its kNK dwords
+// kk; the scales of those dims are kLaneBytes / 8 consecutive bytes. O^T has one row per payload dword (D / 8 rows) in
+// kNT tiles of 16 (D = 64: one tile, rows 8..15 empty).
+template <int D>
+struct Geo {
+  static constexpr int kPay = D / 2;                   // payload bytes of a head row
+  static constexpr int kSf = D / 16;                   // scale bytes of a head row
+  static constexpr int kLaneBytes = D / 8;             // payload bytes per lane and key in the QK layout
+  static constexpr int kNK = D / 32;                   // QK MFMAs per 16-key tile (payload dwords per lane)
+  static constexpr int kNT = D >= 128 ? D / 128 : 1;   // 16-row tiles of O^T
+  static constexpr int kScaleWords = D >= 256 ? 2 : 1; // K (and V) scale dwords per lane and step
+  static constexpr int kVRow = kPay + 16;              // LDS bytes per key in the V transpose tile (80 at D = 128:
+                                                       // no bank conflicts)
+  static constexpr int kWaveLds = kStep * kVRow + kStep * kSf;   // V tile + V scale tile per wave
+  static constexpr int kPartStride = D + 4;            // floats per partial (split, head): accumulators, max, sum, pad
+  static constexpr int kMergeRow = 32 * kNT + 4;       // floats per lane in the slice merge: accumulators, max, sum, pad
+  static constexpr int kPrefetch = D >= 256 ? 1 : 4;   // steps of loads in flight per wave (D = 256: registers)
+  template <int W>
+  static constexpr int kMergeLds = W * 64 * kMergeRow * 4;   // one merge region per wave
+};
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -88,20 +103,57 @@ struct DecodeArgs {
   int64_t o_rs, o_hs;
   int out_dtype;
   float* lse;
-  float* part;                       // [rows, splits, q_heads, kPartStride]: accumulators, max (log2), sum
+  float* part;                       // [rows, splits, q_heads, D + 4]: accumulators, max (log2), sum
   int32_t* counters;                 // [rows * kv_groups] arrivals per (row, KV group); zero between launches
   int64_t n_units;                   // rows * kv_groups * splits workgroups, one per unit
   uint32_t xcd_units;                // n_units / 8
   uint32_t xcd_extra;                // n_units % 8
 };
 
+template <int D>
 struct Step {
-  uint4 kw[2];   // K payload bytes 16j..16j+15 of key 16*tt + hl
-  uint4 vw[2];   // V payload, same keys and bytes
-  uint32_t ks;   // K scale bytes 4*(lane&1) .. +3 of key lane/2
-  uint32_t vs;   // V scale bytes, same
+  uint32_t kw[2][Geo<D>::kNK];     // K payload bytes kLaneBytes * j .. of key 16 * tt + hl
+  uint32_t vw[2][Geo<D>::kNK];     // V payload, same keys and bytes
+  uint32_t ks[Geo<D>::kScaleWords];   // K scale dwords of key scale_key(lane), from dword scale_word(lane)
+  uint32_t vs[Geo<D>::kScaleWords];   // V scale dwords, same
 };
 
+// The key whose scale dwords a lane loads: lanes 2k, 2k + 1 share key k (D >= 128); D = 64 has one dword per key, held
+// by lane k (lanes 32..63 repeat lanes 0..31).
+template <int D>
+__device__ inline int scale_key(int lane) { return D == 64 ? (lane & 31) : (lane >> 1); }
+// The first of the lane's kScaleWords dwords within the key's scale row.
+template <int D>
+__device__ inline int scale_word(int lane) { return D == 64 ? 0 : (lane & 1) * Geo<D>::kScaleWords; }
+
+template <int N>
+__device__ inline void load_words(const uint8_t* p, uint32_t (&w)[N]) {
+  if constexpr (N == 2) {
+    const uint2 x = *reinterpret_cast<const uint2*>(p);
+    w[0] = x.x;
+    w[1] = x.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      const uint4 x = *reinterpret_cast<const uint4*>(p + 4 * i);
+      w[i] = x.x;
+      w[i + 1] = x.y;
+      w[i + 2] = x.z;
+      w[i + 3] = x.w;
+    }
+  }
+}
+
+template <int N>
+__device__ inline void store_words(uint8_t* p, const uint32_t (&w)[N]) {
+  if constexpr (N == 2) {
+    *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 4)
+      *reinterpret_cast<uint4*>(p + 4 * i) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+  }
+}
 
 __device__ inline int key_of(int j, int e) { return (e < 4) ? (4 * j + e) : (16 + 4 * j + (e - 4)); }
 
@@ -123,75 +175,107 @@ struct WaveCtx {
   int lane, hl, j;
 };
 
-// PS: the K and V scales of a head are 16 contiguous bytes (the interleaved pool): one load serves both, the even lane
-// of each pair taking the K half and the odd lane the V half; compute_step swaps the halves within the pair.
-template <bool PS>
-__device__ inline void load_step(const WaveCtx& w, int step, Step& d) {
+// PS (D = 128 only): the K and V scales of a head are 16 contiguous bytes (the interleaved pool): one load serves
+// both, the even lane of each pair taking the K half and the odd lane the V half; compute_step swaps the halves within
+// the pair.
+template <int D, bool PS>
+__device__ inline void load_step(const WaveCtx& w, int step, Step<D>& d) {
+  using G = Geo<D>;
   const int base = step * kStep;
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     const int32_t s = w.slots[base + 16 * tt + w.hl];
     const int64_t slot = s < 0 ? 0 : s;
-    d.kw[tt] = *reinterpret_cast<const uint4*>(w.kp + slot * w.row_bytes + 16 * w.j);
-    d.vw[tt] = *reinterpret_cast<const uint4*>(w.vp + slot * w.row_bytes + 16 * w.j);
+    load_words(w.kp + slot * w.row_bytes + G::kLaneBytes * w.j, d.kw[tt]);
+    load_words(w.vp + slot * w.row_bytes + G::kLaneBytes * w.j, d.vw[tt]);
   }
-  const int32_t s = w.slots[base + (w.lane >> 1)];
+  const int32_t s = w.slots[base + scale_key<D>(w.lane)];
   const int64_t slot = s < 0 ? 0 : s;
   if constexpr (PS) {
     const uint2 x = *reinterpret_cast<const uint2*>(w.ksf + slot * w.row_scales + 8 * (w.lane & 1));
-    d.ks = x.x;
-    d.vs = x.y;
+    d.ks[0] = x.x;
+    d.vs[0] = x.y;
   } else {
-    d.ks = *reinterpret_cast<const uint32_t*>(w.ksf + slot * w.row_scales + 4 * (w.lane & 1));
-    d.vs = *reinterpret_cast<const uint32_t*>(w.vsf + slot * w.row_scales + 4 * (w.lane & 1));
+    const int off = 4 * scale_word<D>(w.lane);
+#pragma unroll
+    for (int i = 0; i < G::kScaleWords; ++i) {
+      d.ks[i] = *reinterpret_cast<const uint32_t*>(w.ksf + slot * w.row_scales + off + 4 * i);
+      d.vs[i] = *reinterpret_cast<const uint32_t*>(w.vsf + slot * w.row_scales + off + 4 * i);
+    }
   }
 }
 
+template <int D>
 struct SoftmaxState {
   float m;            // reference maximum of head hl (log2 domain), identical on the 4 lanes of the head
   float l;            // this lane's share of the sum of 2^(s - m)
-  float4_t acc[8];    // O^T of head hl, d = 32j + 8r + i in acc[i][r]
+  float4_t acc[Geo<D>::kNT][8];   // O^T of head hl: tile t, dims d = 8 (16 t + 4 j + r) + i in acc[t][i][r]
 };
 
-template <bool PS>
-__device__ inline void compute_step(const WaveCtx& w, int step, const Step& d, const half8_t (&qb)[4], float gk,
-                                    uint8_t* vtile, SoftmaxState& st) {
+template <int D, bool PS>
+__device__ inline void compute_step(const WaveCtx& w, int step, const Step<D>& d, const half8_t (&qb)[Geo<D>::kNK],
+                                    float gk, uint8_t* vtile, SoftmaxState<D>& st) {
+  using G = Geo<D>;
   const int lane = w.lane, hl = w.hl, j = w.j;
   // validity of the step's 32 keys (bit t: key t), uniform over the wave
   const uint32_t valid =
       (uint32_t)__builtin_amdgcn_ballot_w64(lane < kStep && w.slots[step * kStep + (lane & 31)] >= 0);
-  const bool my_scale_valid = (valid >> (lane >> 1)) & 1u;
-  // lane 2k + i ends with word i of key k's K scales (ks) and of its V scales (vs)
-  uint32_t ks = d.ks, vs_raw = d.vs;
-  if constexpr (PS) {   // even lane: K words 0, 1; odd lane: V words 0, 1 (quad_perm [1, 0, 3, 2] swaps the pair)
-    const uint32_t o0 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)d.ks, 0xB1, 0xF, 0xF, false);
-    const uint32_t o1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)d.vs, 0xB1, 0xF, 0xF, false);
-    const bool odd = lane & 1;
-    ks = odd ? o1 : d.ks;
-    vs_raw = odd ? d.vs : o0;
+  const bool my_scale_valid = (valid >> scale_key<D>(lane)) & 1u;
+  uint32_t ks[G::kScaleWords], vs[G::kScaleWords];
+#pragma unroll
+  for (int i = 0; i < G::kScaleWords; ++i) {
+    ks[i] = d.ks[i];
+    vs[i] = d.vs[i];
   }
-  const uint32_t vs = my_scale_valid ? vs_raw : 0u;   // invalid keys: V scale 0, so V = 0 whatever slot 0 holds
+  if constexpr (PS) {   // even lane: K words 0, 1; odd lane: V words 0, 1 (quad_perm [1, 0, 3, 2] swaps the pair)
+    const uint32_t o0 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)d.ks[0], 0xB1, 0xF, 0xF, false);
+    const uint32_t o1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)d.vs[0], 0xB1, 0xF, 0xF, false);
+    const bool odd = lane & 1;
+    ks[0] = odd ? o1 : d.ks[0];
+    vs[0] = odd ? d.vs[0] : o0;
+  }
+#pragma unroll
+  for (int i = 0; i < G::kScaleWords; ++i)   // invalid keys: V scale 0, so V = 0 whatever slot 0 holds
+    vs[i] = my_scale_valid ? vs[i] : 0u;
 
   // V: stage payload and scales in LDS, transposed reads below
-  uint8_t* vscale = vtile + kStep * kVRow;
+  uint8_t* vscale = vtile + kStep * G::kVRow;
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt)
-    *reinterpret_cast<uint4*>(vtile + (16 * tt + hl) * kVRow + 16 * j) = d.vw[tt];
-  *reinterpret_cast<uint32_t*>(vscale + (lane >> 1) * 8 + 4 * (lane & 1)) = vs;
+  for (int tt = 0; tt < 2; ++tt) store_words(vtile + (16 * tt + hl) * G::kVRow + G::kLaneBytes * j, d.vw[tt]);
+  if constexpr (D == 64) {
+    if (lane < 32) *reinterpret_cast<uint32_t*>(vscale + lane * 4) = vs[0];
+  } else {
+#pragma unroll
+    for (int i = 0; i < G::kScaleWords; ++i)
+      *reinterpret_cast<uint32_t*>(vscale + scale_key<D>(lane) * G::kSf + 4 * (scale_word<D>(lane) + i)) = vs[i];
+  }
 
-  // QK
+  // QK: lane (hl, j) of tile tt needs the scale bytes of its dims, kLaneBytes / 8 bytes from byte (D / 64) j of key
+  // 16 tt + hl, taken from the lane that loaded them
   float4_t s[2];
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
-    const uint32_t src = (uint32_t)__shfl((int)ks, 2 * (16 * tt + hl) + (j >> 1));
-    const half2_t sc2 = fp8x2_to_f16<false>(src >> (16 * (j & 1)));
-    const half2_t sc_lo = half2_t{sc2.x, sc2.x}, sc_hi = half2_t{sc2.y, sc2.y};
-    const uint32_t kw[4] = {d.kw[tt].x, d.kw[tt].y, d.kw[tt].z, d.kw[tt].w};
+    const int key = 16 * tt + hl;
+    uint32_t chunk;
+    if constexpr (D == 64) {
+      chunk = (uint32_t)__shfl((int)ks[0], key) >> (8 * j);
+    } else if constexpr (D == 128) {
+      chunk = (uint32_t)__shfl((int)ks[0], 2 * key + (j >> 1)) >> (16 * (j & 1));
+    } else {
+      const uint32_t a0 = (uint32_t)__shfl((int)ks[0], 2 * key + (j >> 1));
+      const uint32_t a1 = (uint32_t)__shfl((int)ks[1], 2 * key + (j >> 1));
+      chunk = (j & 1) ? a1 : a0;
+    }
+    const half2_t c01 = fp8x2_to_f16<false>(chunk);
+    const half2_t c23 = D == 256 ? fp8x2_to_f16<true>(chunk) : c01;
     s[tt] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-      s[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant_k(kw[kk], kk < 2 ? sc_lo : sc_hi), qb[kk], s[tt], 0, 0,
+    for (int kk = 0; kk < G::kNK; ++kk) {
+      const int bi = kk >> 1;   // scale block of dword kk within the lane's bytes
+      const _Float16 sc = bi == 0 ? c01.x : bi == 1 ? c01.y : bi == 2 ? c23.x : c23.y;
+      s[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant_k(d.kw[tt][kk], half2_t{sc, sc}), qb[kk], s[tt], 0, 0,
                                                      0);
+    }
   }
   // online softmax of head hl over keys T(j), lazy rescale
   float sv[8];
@@ -207,7 +291,9 @@ __device__ inline void compute_step(const WaveCtx& w, int step, const Step& d, c
     const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
     st.l *= alpha;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) st.acc[i] *= alpha;
+    for (int t = 0; t < G::kNT; ++t)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) st.acc[t][i] *= alpha;
     st.m = m_new;
   }
   const float m_use = (st.m == -__builtin_inff()) ? 0.0f : st.m;
@@ -221,39 +307,45 @@ __device__ inline void compute_step(const WaveCtx& w, int step, const Step& d, c
   st.l += psum;
   const half8_t pb = half8_t{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3],
                              (_Float16)p[4], (_Float16)p[5], (_Float16)p[6], (_Float16)p[7]};
-  // V^T operands: dword hl of keys T(j), and the scale byte of block hl/2 of those keys
-  asm volatile("" ::: "memory");
-  uint32_t vw[8], vb[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int key = key_of(j, e);
-    vw[e] = *reinterpret_cast<const uint32_t*>(vtile + key * kVRow + 4 * hl);
-    vb[e] = vscale[key * 8 + (hl >> 1)];
-  }
-  half8_t av[8];
-#pragma unroll
-  for (int e = 0; e < 8; e += 2) {
-    const uint32_t w0 = vw[e], w1 = vw[e + 1];
-    const uint32_t lo = (w0 & 0x0F0F0F0Fu) | ((w1 & 0x0F0F0F0Fu) << 4);   // byte b: nibble 2b of keys e, e+1
-    const uint32_t hi = ((w0 >> 4) & 0x0F0F0F0Fu) | (w1 & 0xF0F0F0F0u);   // byte b: nibble 2b+1
-    const half2_t sp = fp8x2_to_f16<false>(vb[e] | (vb[e + 1] << 8));
-    half2_t x;
-    x = fp4x2_to_f16<0>(lo) * sp; av[0][e] = x.x; av[0][e + 1] = x.y;
-    x = fp4x2_to_f16<0>(hi) * sp; av[1][e] = x.x; av[1][e + 1] = x.y;
-    x = fp4x2_to_f16<1>(lo) * sp; av[2][e] = x.x; av[2][e + 1] = x.y;
-    x = fp4x2_to_f16<1>(hi) * sp; av[3][e] = x.x; av[3][e + 1] = x.y;
-    x = fp4x2_to_f16<2>(lo) * sp; av[4][e] = x.x; av[4][e + 1] = x.y;
-    x = fp4x2_to_f16<2>(hi) * sp; av[5][e] = x.x; av[5][e + 1] = x.y;
-    x = fp4x2_to_f16<3>(lo) * sp; av[6][e] = x.x; av[6][e + 1] = x.y;
-    x = fp4x2_to_f16<3>(hi) * sp; av[7][e] = x.x; av[7][e + 1] = x.y;
-  }
+  // V^T operands of tile t: payload dword c = 16 t + hl of keys T(j), and the scale byte of block c / 2 of those keys
   asm volatile("" ::: "memory");
 #pragma unroll
-  for (int i = 0; i < 8; ++i) st.acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], pb, st.acc[i], 0, 0, 0);
+  for (int t = 0; t < G::kNT; ++t) {
+    const int c = 16 * t + hl;
+    const bool row_ok = c < D / 8;   // D = 64: O^T rows 8..15 are empty
+    const int cr = row_ok ? c : 0;
+    uint32_t vw[8], vb[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int key = key_of(j, e);
+      vw[e] = row_ok ? *reinterpret_cast<const uint32_t*>(vtile + key * G::kVRow + 4 * cr) : 0u;
+      vb[e] = row_ok ? vscale[key * G::kSf + (cr >> 1)] : 0u;
+    }
+    half8_t av[8];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const uint32_t w0 = vw[e], w1 = vw[e + 1];
+      const uint32_t lo = (w0 & 0x0F0F0F0Fu) | ((w1 & 0x0F0F0F0Fu) << 4);   // byte b: nibble 2b of keys e, e+1
+      const uint32_t hi = ((w0 >> 4) & 0x0F0F0F0Fu) | (w1 & 0xF0F0F0F0u);   // byte b: nibble 2b+1
+      const half2_t sp = fp8x2_to_f16<false>(vb[e] | (vb[e + 1] << 8));
+      half2_t x;
+      x = fp4x2_to_f16<0>(lo) * sp; av[0][e] = x.x; av[0][e + 1] = x.y;
+      x = fp4x2_to_f16<0>(hi) * sp; av[1][e] = x.x; av[1][e + 1] = x.y;
+      x = fp4x2_to_f16<1>(lo) * sp; av[2][e] = x.x; av[2][e + 1] = x.y;
+      x = fp4x2_to_f16<1>(hi) * sp; av[3][e] = x.x; av[3][e + 1] = x.y;
+      x = fp4x2_to_f16<2>(lo) * sp; av[4][e] = x.x; av[4][e + 1] = x.y;
+      x = fp4x2_to_f16<2>(hi) * sp; av[5][e] = x.x; av[5][e + 1] = x.y;
+      x = fp4x2_to_f16<3>(lo) * sp; av[6][e] = x.x; av[6][e + 1] = x.y;
+      x = fp4x2_to_f16<3>(hi) * sp; av[7][e] = x.x; av[7][e + 1] = x.y;
+    }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st.acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], pb, st.acc[t][i], 0, 0, 0);
+  }
 }
 
-// A partial's 16-byte piece, written through to memory (sc1): visible to the merging workgroup on any XCD, whose plain
-// loads cannot hit a stale copy (no workgroup reads these addresses before the merge within a launch).
+// A partial's 16-byte piece, written through to memory (sc1), so that the release of the arrival below has few dirty
+// L2 lines to write back; the ordering itself comes from that release and the last arriver's acquire.
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 __device__ inline void store_through(__amdgpu_buffer_rsrc_t r, int byte_off, float4_t v) {
   const u32x4_t w = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
@@ -272,9 +364,11 @@ __device__ inline void store_out(const DecodeArgs& a, int row, int head, int d0,
   }
 }
 
-// HPW: KV heads per workgroup (4 or 1); the workgroup's 8 / HPW key slices of each head merge through LDS.
-template <int P, int HPW, bool PS, int W>
+// D: head size; HPW: KV heads per workgroup (4 or 1); the workgroup's W / HPW key slices of each head merge through
+// LDS.
+template <int D, int P, int HPW, bool PS, int W>
 __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArgs a) {
+  using G = Geo<D>;
   constexpr int kSlices = W / HPW;
   constexpr int kThreads = 64 * W;
   extern __shared__ __align__(16) uint8_t lds[];
@@ -301,18 +395,18 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
   const bool active = kvh < a.kv_heads;
 
   int32_t* slots = reinterpret_cast<int32_t*>(lds);
-  uint8_t* vtile = lds + a.slot_lds_bytes + wave * kWaveLds;
+  uint8_t* vtile = lds + a.slot_lds_bytes + wave * G::kWaveLds;
 
   // the query's raw words first (loads complete in order); every lane reads a valid address and heads outside the
   // group are zeroed at conversion, so the loads carry no branch
   const int hl = lane & 15, j = lane >> 4;
   const bool q_valid = active && hl < a.group;
-  uint4 qraw[4];
+  uint4 qraw[G::kNK];
   {
     const int head = min(kvh, a.kv_heads - 1) * a.group + min(hl, a.group - 1);
     const uint16_t* qp = a.q + (int64_t)row * a.q_rs + (int64_t)head * a.q_hs;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) qraw[kk] = *reinterpret_cast<const uint4*>(qp + 32 * j + 8 * kk);
+    for (int kk = 0; kk < G::kNK; ++kk) qraw[kk] = *reinterpret_cast<const uint4*>(qp + (D / 4) * j + 8 * kk);
   }
 
   // 1. the split's pool slots (-1: invalid key), shared by the workgroup's waves; each slice owns a whole number of
@@ -388,9 +482,9 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
   __syncthreads();
 
   // B operand of the QK MFMAs: FP16 of q * scale * log2(e); heads beyond the group are zero
-  half8_t qb[4];
+  half8_t qb[G::kNK];
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
+  for (int kk = 0; kk < G::kNK; ++kk) {
     const uint32_t ws[4] = {q_valid ? qraw[kk].x : 0u, q_valid ? qraw[kk].y : 0u, q_valid ? qraw[kk].z : 0u,
                             q_valid ? qraw[kk].w : 0u};
 #pragma unroll
@@ -399,11 +493,13 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
       qb[kk][2 * e + 1] = (_Float16)(bf16_bits_to_f32(ws[e] >> 16) * a.qscale);
     }
   }
-  SoftmaxState st;
+  SoftmaxState<D> st;
   st.m = -__builtin_inff();
   st.l = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) st.acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < G::kNT; ++t)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st.acc[t][i] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   if (active && slice_steps > 0) {
     WaveCtx w;
@@ -417,20 +513,20 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
     w.lane = lane;
     w.hl = hl;
     w.j = j;
-    Step buf[P];
+    Step<D> buf[P];
 #pragma unroll
-    for (int p = 0; p < P; ++p) load_step<PS>(w, p, buf[p]);
+    for (int p = 0; p < P; ++p) load_step<D, PS>(w, p, buf[p]);
     const float gk = a.gk ? *a.gk : a.gk_val;
     int s0 = 0;
     for (; s0 + P < slice_steps; s0 += P) {
 #pragma unroll
       for (int p = 0; p < P; ++p) {
-        compute_step<PS>(w, s0 + p, buf[p], qb, gk, vtile, st);
-        load_step<PS>(w, s0 + p + P, buf[p]);
+        compute_step<D, PS>(w, s0 + p, buf[p], qb, gk, vtile, st);
+        load_step<D, PS>(w, s0 + p + P, buf[p]);
       }
     }
 #pragma unroll
-    for (int p = 0; p < P; ++p) compute_step<PS>(w, s0 + p, buf[p], qb, gk, vtile, st);
+    for (int p = 0; p < P; ++p) compute_step<D, PS>(w, s0 + p, buf[p], qb, gk, vtile, st);
   }
   // the 4 lanes of a head hold disjoint key subsets of l
   float l_tot = sum4_lanes16(st.l);
@@ -438,35 +534,38 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
   // 2. the slices merge through LDS behind one barrier: every wave leaves its (O^T in dim order, max, sum) per lane
   // in its own region (after the slot list and V tiles, so no wave still reading those is disturbed); then each
   // thread merges 4 dims of one (KV head, lane) over the slices and normalizes (one split) or writes the partial
-  float* mrg = reinterpret_cast<float*>(lds + a.slot_lds_bytes + W * kWaveLds);
+  float* mrg = reinterpret_cast<float*>(lds + a.slot_lds_bytes + W * G::kWaveLds);
   {
-    float4_t* mine = reinterpret_cast<float4_t*>(mrg + (wave * 64 + lane) * kMergeRow);
+    float4_t* mine = reinterpret_cast<float4_t*>(mrg + (wave * 64 + lane) * G::kMergeRow);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {   // dims 32j + 8r .. 32j + 8r + 7
-      mine[2 * r] = float4_t{st.acc[0][r], st.acc[1][r], st.acc[2][r], st.acc[3][r]};
-      mine[2 * r + 1] = float4_t{st.acc[4][r], st.acc[5][r], st.acc[6][r], st.acc[7][r]};
-    }
-    mine[8] = float4_t{st.m, l_tot, 0.0f, 0.0f};
+    for (int t = 0; t < G::kNT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {   // dims 8 (16 t + 4 j + r) .. + 7
+        mine[8 * t + 2 * r] = float4_t{st.acc[t][0][r], st.acc[t][1][r], st.acc[t][2][r], st.acc[t][3][r]};
+        mine[8 * t + 2 * r + 1] = float4_t{st.acc[t][4][r], st.acc[t][5][r], st.acc[t][6][r], st.acc[t][7][r]};
+      }
+    mine[8 * G::kNT] = float4_t{st.m, l_tot, 0.0f, 0.0f};
   }
   __syncthreads();
-  float* row_part = a.part + (int64_t)row * a.splits * a.q_heads * kPartStride;
+  float* row_part = a.part + (int64_t)row * a.splits * a.q_heads * G::kPartStride;
   const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-      row_part, (short)0, a.splits > 1 ? (int)((int64_t)a.splits * a.q_heads * kPartStride * 4) : 0, 0x00020000);
+      row_part, (short)0, a.splits > 1 ? (int)((int64_t)a.splits * a.q_heads * G::kPartStride * 4) : 0, 0x00020000);
   const float gv = a.gv ? *a.gv : a.gv_val;
+  constexpr int kParts = 8 * G::kNT;   // 4-dim pieces per lane
 #pragma unroll
-  for (int u = (int)threadIdx.x; u < HPW * 512; u += kThreads) {
-    const int part = u & 7, ln = (u >> 3) & 63, hw = u >> 9;   // dims 4 part .. +3 of lane ln's 32, KV head hw
+  for (int u = (int)threadIdx.x; u < HPW * 64 * kParts; u += kThreads) {
+    const int part = u % kParts, ln = (u / kParts) & 63, hw = u / (kParts * 64);   // piece part of lane ln, KV head hw
     const int uh = ln & 15, uj = ln >> 4;
     const int ukvh = kvg * HPW + hw;
-    if (ukvh >= a.kv_heads || uh >= a.group) continue;
+    if (ukvh >= a.kv_heads || uh >= a.group || (D == 64 && uj >= 2)) continue;
     float ms[kSlices], ls[kSlices];
     float4_t xs[kSlices];
     float mx = -__builtin_inff();
 #pragma unroll
     for (int sl = 0; sl < kSlices; ++sl) {
-      const float4_t* src = reinterpret_cast<const float4_t*>(mrg + ((sl * HPW + hw) * 64 + ln) * kMergeRow);
+      const float4_t* src = reinterpret_cast<const float4_t*>(mrg + ((sl * HPW + hw) * 64 + ln) * G::kMergeRow);
       xs[sl] = src[part];
-      const float4_t ml = src[8];
+      const float4_t ml = src[8 * G::kNT];
       ms[sl] = ml[0];
       ls[sl] = ml[1];
       mx = fmaxf(mx, ms[sl]);
@@ -480,7 +579,7 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
       o += wgt * xs[sl];
       l += wgt * ls[sl];
     }
-    const int head = ukvh * a.group + uh, d0 = 32 * uj + 4 * part;
+    const int head = ukvh * a.group + uh, d0 = 128 * (part >> 3) + 32 * uj + 4 * (part & 7);
     if (a.splits == 1) {   // no partials: normalize and write
       const float inv = l > 0.0f ? gv / l : 0.0f;
       const float v[4] = {o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
@@ -488,9 +587,9 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
       if (a.lse && d0 == 0)
         a.lse[(int64_t)row * a.q_heads + head] = l > 0.0f ? (mx + __builtin_log2f(l)) * kLn2 : -__builtin_inff();
     } else {               // 3. partials of this row, written through
-      const int at = ((split * a.q_heads + head) * kPartStride) * 4;
+      const int at = ((split * a.q_heads + head) * G::kPartStride) * 4;
       store_through(pr, at + d0 * 4, o);
-      if (d0 == 0) store_through(pr, at + kDim * 4, float4_t{mx, l, 0.0f, 0.0f});
+      if (d0 == 0) store_through(pr, at + D * 4, float4_t{mx, l, 0.0f, 0.0f});
     }
   }
   if (a.splits == 1) return;
@@ -499,17 +598,21 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
   __syncthreads();
   __shared__ int32_t s_last;
   int32_t* counter = a.counters + (int64_t)row * a.kv_groups + kvg;
+  // The arrival is an acquire-release read-modify-write at agent scope. Its release half publishes, to every XCD, the
+  // partials all threads of this workgroup stored (each thread waited for its own stores, and the barrier above orders
+  // them before thread 0's release). Its acquire half, in the last workgroup to arrive, orders the loads of the other
+  // workgroups' partials below (after the second barrier) behind their releases.
   if (threadIdx.x == 0)
-    s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.splits - 1;
+    s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == a.splits - 1;
   __syncthreads();
   if (!s_last) return;
-  // all threads, 8 consecutive outputs each: head h0 + o / 128, d0 = o % 128; loads of 8 splits at a time together
+  // all threads, 8 consecutive outputs each: head h0 + o / D, d0 = o % D; loads of 8 splits at a time together
   const int h0 = kvg * HPW * a.group;
   const int nh = min(HPW * a.group, a.q_heads - h0);
-  for (int o = threadIdx.x * 8; o < nh * kDim; o += blockDim.x * 8) {
-    const int hh = h0 + o / kDim, d0 = o % kDim;
-    const float* base = row_part + (int64_t)hh * kPartStride;
-    const int64_t sstride = (int64_t)a.q_heads * kPartStride;
+  for (int o = threadIdx.x * 8; o < nh * D; o += blockDim.x * 8) {
+    const int hh = h0 + o / D, d0 = o % D;
+    const float* base = row_part + (int64_t)hh * G::kPartStride;
+    const int64_t sstride = (int64_t)a.q_heads * G::kPartStride;
     float m_run = -__builtin_inff(), l_run = 0.0f;
     float4_t o0 = float4_t{0.f, 0.f, 0.f, 0.f}, o1 = o0;
     for (int s0 = 0; s0 < a.splits; s0 += 8) {
@@ -517,7 +620,7 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
 #pragma unroll
       for (int i = 0; i < 8; ++i) {   // past the last split: reload the last one, weight 0 below
         const float* pp = base + min(s0 + i, a.splits - 1) * sstride;
-        ml[i] = reinterpret_cast<const float4_t*>(pp + kDim)[0];
+        ml[i] = reinterpret_cast<const float4_t*>(pp + D)[0];
         x0[i] = reinterpret_cast<const float4_t*>(pp + d0)[0];
         x1[i] = reinterpret_cast<const float4_t*>(pp + d0)[1];
       }
@@ -557,10 +660,10 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
 
 using namespace xt;
 
-// Workgroup shape: 4 KV heads x 2 key slices when that alone yields a full launch (256 workgroups), else 1 KV head x 8
-// slices (more, smaller workgroups: a (row, head) merges its 8 slices in LDS instead of through partials).
-static int heads_per_workgroup(int rows, int kv_heads, int splits) {
-  return (kv_heads % 4 == 0 && (int64_t)rows * (kv_heads / 4) * splits >= 256) ? 4 : 1;
+// Workgroup shape: 4 KV heads per workgroup when that alone yields a full launch (one workgroup per CU), else 1 KV
+// head (more, smaller workgroups: a (row, head) merges its slices in LDS instead of through partials).
+static int heads_per_workgroup(int rows, int kv_heads, int splits, int cus) {
+  return (kv_heads % 4 == 0 && (int64_t)rows * (kv_heads / 4) * splits >= cus) ? 4 : 1;
 }
 
 // Pool and index addressing beyond the token-major pool with one shared index list per row.
@@ -580,14 +683,16 @@ struct Addressing {
 static int decode_impl(const char* what, const void* q, int64_t q_row_stride, int64_t q_head_stride,
                        const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_scales, const uint8_t* v_scales,
                        const float* gk, const float* gv, int64_t pool_slots, int64_t pay_stride, int64_t sf_stride,
-                       int kv_heads, int q_heads, const int32_t* table, int64_t table_stride, int page_size,
+                       int kv_heads, int q_heads, int dim, const int32_t* table, int64_t table_stride, int page_size,
                        const int64_t* row_req, const int32_t* indices, int64_t idx_stride, int topk,
                        const int32_t* counts, const int32_t* seq_lens, const int32_t* query_pos, float scale,
                        void* out, int64_t out_row_stride, int64_t out_head_stride, int out_dtype, float* lse, int rows,
                        int splits, void* workspace, size_t workspace_bytes, const Addressing& ad,
                        xt_stream_t stream);
 
-// Workspace: [arrival counters, kCounterBytes][partials [rows, splits, q_heads, kPartStride] FP32]
+// Workspace: [arrival counters, kCounterBytes][partials [rows, splits, q_heads, dim + 4] FP32]
+
+static bool supported_dim(int dim) { return dim == 64 || dim == 128 || dim == 256; }
 
 extern "C" size_t xt_sparse_decode_workspace_bytes(int rows, int q_heads, int dim, int splits) {
   if (rows < 0 || q_heads <= 0 || dim <= 0 || splits <= 0) return 0;
@@ -607,7 +712,7 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
                                       int64_t out_head_stride, int out_dtype, float* lse, int rows, int splits,
                                       void* workspace, size_t workspace_bytes, xt_stream_t stream) {
   const char* what = "xt_sparse_decode_nvfp4";
-  if (dim != kDim) return fail(XT_EUNSUPPORTED, "%s: head size %d (supported: %d)", what, dim, kDim);
+  if (!supported_dim(dim)) return fail(XT_EUNSUPPORTED, "%s: head size %d (supported: 64, 128, 256)", what, dim);
   if (kv_heads <= 0) return fail(XT_EINVAL, "%s: kv_heads %d", what, kv_heads);
   if (pay_head_stride == 0) pay_head_stride = dim / 2;
   if (sf_head_stride == 0) sf_head_stride = dim / 16;
@@ -623,7 +728,7 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
     return fail(XT_EINVAL, "%s: pool_slots %lld outside 1..2^31-1", what, (long long)pool_slots);
   const Addressing ad{pay_head_stride, sf_head_stride, 0, 1, 0, 0, true, nullptr, 0x7FFFFFFF, false, 0.0f, 0.0f};
   return decode_impl(what, q, q_row_stride, q_head_stride, k_pay, v_pay, k_scales, v_scales, gk, gv, pool_slots,
-                     pay_stride, sf_stride, kv_heads, q_heads, table, table_stride, page_size, row_req, indices,
+                     pay_stride, sf_stride, kv_heads, q_heads, dim, table, table_stride, page_size, row_req, indices,
                      idx_stride, topk, counts, seq_lens, query_pos, scale, out, out_row_stride, out_head_stride,
                      out_dtype, lse, rows, splits, workspace, workspace_bytes, ad, stream);
 }
@@ -632,7 +737,7 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
 static int block_pages(const char* what, int64_t pages, int kv_heads, int dim, int block_size, int64_t page_stride,
                        int64_t head_stride, int64_t row_stride, int64_t sf_page_stride, int64_t sf_head_stride,
                        int64_t sf_row_stride, int topk_blocks, int64_t* mul) {
-  if (dim != kDim) return fail(XT_EUNSUPPORTED, "%s: head size %d (supported: %d)", what, dim, kDim);
+  if (!supported_dim(dim)) return fail(XT_EUNSUPPORTED, "%s: head size %d (supported: 64, 128, 256)", what, dim);
   if (block_size <= 0 || (block_size & (block_size - 1)) || block_size > 4096)
     return fail(XT_EINVAL, "%s: block_size %d must be a power of 2 up to 4096", what, block_size);
   if (kv_heads <= 0 || pages <= 0 || topk_blocks < 0)
@@ -679,7 +784,7 @@ extern "C" int xt_block_sparse_decode_nvfp4(const void* q, int64_t q_row_stride,
   const Addressing ad{head_stride, sf_head_stride, shift, mul, idx_head_stride, shift, false, nullptr, max_kv_len, true,
                       kv_scale, kv_scale};
   return decode_impl(what, q, q_row_stride, q_head_stride, k_pay, v_pay, k_scales, v_scales, nullptr, nullptr,
-                     pages * mul, row_stride, sf_row_stride, kv_heads, q_heads, req_to_token, req_stride, 1,
+                     pages * mul, row_stride, sf_row_stride, kv_heads, q_heads, dim, req_to_token, req_stride, 1,
                      slot_ids, topk_idx, idx_row_stride, topk_blocks * block_size, nullptr, seq_lens, nullptr,
                      sm_scale, out, out_row_stride, out_head_stride, out_dtype, lse, rows, splits, workspace,
                      workspace_bytes, ad, stream);
@@ -709,40 +814,52 @@ extern "C" int xt_block_sparse_prefill_nvfp4(const void* q, int64_t q_row_stride
   const Addressing ad{head_stride, sf_head_stride, shift, mul, idx_head_stride, shift, true, row_idx, 0x7FFFFFFF, true,
                       kv_scale, kv_scale};
   return decode_impl(what, q, q_row_stride, q_head_stride, k_pay, v_pay, k_scales, v_scales, nullptr, nullptr,
-                     pages * mul, row_stride, sf_row_stride, kv_heads, q_heads, req_to_token, req_stride, 1,
+                     pages * mul, row_stride, sf_row_stride, kv_heads, q_heads, dim, req_to_token, req_stride, 1,
                      row_req, topk_idx, idx_row_stride, topk_blocks * block_size, nullptr, row_seq_lens,
                      row_query_pos, sm_scale, out, out_row_stride, out_head_stride, out_dtype, lse, rows, splits,
                      workspace, workspace_bytes, ad, stream);
 }
 
 // One launch of the decode kernel.
-template <int HPW, bool PS, int W>
+template <int D, int HPW, bool PS, int W>
 static int launch_decode(const DecodeArgs& a, dim3 grid, size_t lds_bytes, hipStream_t stream, const char* what) {
-  if (int e = allow_lds(reinterpret_cast<const void*>(&decode_split_kernel<kPrefetch, HPW, PS, W>), lds_bytes, what))
+  constexpr int P = Geo<D>::kPrefetch;
+  if (int e = allow_lds(reinterpret_cast<const void*>(&decode_split_kernel<D, P, HPW, PS, W>), lds_bytes, what))
     return e;
-  hipLaunchKernelGGL((decode_split_kernel<kPrefetch, HPW, PS, W>), grid, dim3(64 * W), lds_bytes, stream, a);
+  hipLaunchKernelGGL((decode_split_kernel<D, P, HPW, PS, W>), grid, dim3(64 * W), lds_bytes, stream, a);
   return check_launch(what);
 }
 
-template <int W>
+template <int D, int W>
 static int launch_decode(int hpw, bool ps, const DecodeArgs& a, dim3 grid, size_t lds_bytes, hipStream_t stream,
                          const char* what) {
-  if (hpw == 4) return ps ? launch_decode<4, true, W>(a, grid, lds_bytes, stream, what)
-                          : launch_decode<4, false, W>(a, grid, lds_bytes, stream, what);
-  return ps ? launch_decode<1, true, W>(a, grid, lds_bytes, stream, what)
-            : launch_decode<1, false, W>(a, grid, lds_bytes, stream, what);
+  if constexpr (D == 128) {   // paired K/V scales: the interleaved pool at head size 128
+    if (ps) return hpw == 4 ? launch_decode<D, 4, true, W>(a, grid, lds_bytes, stream, what)
+                            : launch_decode<D, 1, true, W>(a, grid, lds_bytes, stream, what);
+  }
+  return hpw == 4 ? launch_decode<D, 4, false, W>(a, grid, lds_bytes, stream, what)
+                  : launch_decode<D, 1, false, W>(a, grid, lds_bytes, stream, what);
 }
+
+// LDS bytes of a launch: the slot list, one V tile per wave and one merge region per wave.
+template <int D>
+static size_t decode_lds(int slot_bytes, int waves) {
+  return (size_t)slot_bytes + (size_t)waves * Geo<D>::kWaveLds +
+         (waves == 4 ? Geo<D>::template kMergeLds<4> : Geo<D>::template kMergeLds<kWaves>);
+}
+
+static int prefetch_of(int dim) { return dim == 64 ? Geo<64>::kPrefetch : dim == 128 ? Geo<128>::kPrefetch
+                                                                                     : Geo<256>::kPrefetch; }
 
 static int decode_impl(const char* what, const void* q, int64_t q_row_stride, int64_t q_head_stride,
                        const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_scales, const uint8_t* v_scales,
                        const float* gk, const float* gv, int64_t pool_slots, int64_t pay_stride, int64_t sf_stride,
-                       int kv_heads, int q_heads, const int32_t* table, int64_t table_stride, int page_size,
+                       int kv_heads, int q_heads, int dim, const int32_t* table, int64_t table_stride, int page_size,
                        const int64_t* row_req, const int32_t* indices, int64_t idx_stride, int topk,
                        const int32_t* counts, const int32_t* seq_lens, const int32_t* query_pos, float scale,
                        void* out, int64_t out_row_stride, int64_t out_head_stride, int out_dtype, float* lse, int rows,
                        int splits, void* workspace, size_t workspace_bytes, const Addressing& ad,
                        xt_stream_t stream) {
-  const int dim = kDim;
   if (kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads != 0)
     return fail(XT_EINVAL, "%s: q_heads %d must be a positive multiple of kv_heads %d", what, q_heads, kv_heads);
   const int group = q_heads / kv_heads;
@@ -773,17 +890,21 @@ static int decode_impl(const char* what, const void* q, int64_t q_row_stride, in
   if (!aligned(workspace, 256)) return fail(XT_EINVAL, "%s: workspace must be 256-byte aligned", what);
   const int per_split = (topk + splits - 1) / splits;
   const int kps = ((per_split + kStep - 1) / kStep) * kStep;
-  const int hpw = ad.idx_head_stride ? 1 : heads_per_workgroup(rows, kv_heads, splits);
-  // Waves per workgroup: 8 when the units fit one round of workgroups (decode batches), else 4 (prefill chunks, one
-  // row per query; odd batch sizes): two 4-wave workgroups then share a CU, and one's slot list and merge overlap the
-  // other's gather, where 8-wave ones would run a second round after the first.
+  const int cus = device_cus();
+  const int hpw = ad.idx_head_stride ? 1 : heads_per_workgroup(rows, kv_heads, splits, cus);
+  // Waves per workgroup: 8 when the units fit one round of workgroups, one per CU (decode batches), else 4 (prefill
+  // chunks, one row per query; odd batch sizes): two 4-wave workgroups then share a CU, and one's slot list and merge
+  // overlap the other's gather, where 8-wave ones would run a second round after the first.
+  // Head size 256 always runs 4-wave workgroups: eight waves' merge regions would not fit in LDS.
   const int64_t units = (int64_t)rows * ((kv_heads + hpw - 1) / hpw) * splits;
-  const int waves = units > kOneRound ? 4 : kWaves;
+  const int waves = (units > cus || dim == 256) ? 4 : kWaves;
   const int slices = waves / hpw;
-  const int slice_steps = ((kps / kStep + slices * kPrefetch - 1) / (slices * kPrefetch)) * kPrefetch;
+  const int pf = prefetch_of(dim);
+  const int slice_steps = ((kps / kStep + slices * pf - 1) / (slices * pf)) * pf;
   const int slot_bytes = slices * slice_steps * kStep * (int)sizeof(int32_t);
-  const size_t lds_bytes =
-      (size_t)slot_bytes + (size_t)waves * kWaveLds + (waves == 4 ? kMergeLds<4> : kMergeLds<kWaves>);
+  const size_t lds_bytes = dim == 64    ? decode_lds<64>(slot_bytes, waves)
+                           : dim == 128 ? decode_lds<128>(slot_bytes, waves)
+                                        : decode_lds<256>(slot_bytes, waves);
   if (lds_bytes > kMaxLds)
     return fail(XT_EUNSUPPORTED, "%s: %d keys per split needs %zu bytes of LDS; use more splits", what, kps,
                 lds_bytes);
@@ -845,11 +966,15 @@ static int decode_impl(const char* what, const void* q, int64_t q_row_stride, in
   const int64_t launched = a.n_units;
   if (launched > 0x7FFFFFFFLL) return fail(XT_EUNSUPPORTED, "%s: %lld workgroups", what, (long long)launched);
 
-  // K and V scales of a head side by side and 8-byte aligned: one load per key serves both
-  const bool ps = v_scales == k_scales + dim / 16 && aligned(k_scales, 8) && sf_stride % 8 == 0 &&
+  // K and V scales of a head side by side and 8-byte aligned (head size 128): one load per key serves both
+  const bool ps = dim == 128 && v_scales == k_scales + dim / 16 && aligned(k_scales, 8) && sf_stride % 8 == 0 &&
                   ad.sf_head_stride % 8 == 0;
   const dim3 grid((unsigned)launched);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  return waves == 4 ? launch_decode<4>(hpw, ps, a, grid, lds_bytes, st, what)
-                    : launch_decode<kWaves>(hpw, ps, a, grid, lds_bytes, st, what);
+  if (dim == 64)
+    return waves == 4 ? launch_decode<64, 4>(hpw, ps, a, grid, lds_bytes, st, what)
+                      : launch_decode<64, kWaves>(hpw, ps, a, grid, lds_bytes, st, what);
+  if (dim == 256) return launch_decode<256, 4>(hpw, ps, a, grid, lds_bytes, st, what);
+  return waves == 4 ? launch_decode<128, 4>(hpw, ps, a, grid, lds_bytes, st, what)
+                    : launch_decode<128, kWaves>(hpw, ps, a, grid, lds_bytes, st, what);
 }

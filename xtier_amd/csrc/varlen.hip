@@ -149,7 +149,7 @@ __device__ inline void store_row(const VarlenArgs& a, int64_t query, int head, i
 }
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-// 16 bytes written through to L2 (sc1): the merging workgroup may run on another XCD
+// 16 bytes written through (sc1): the arrival's release then has few dirty L2 lines to write back
 __device__ inline void store_through(__amdgpu_buffer_rsrc_t r, int byte_off, float4_t v) {
   const u32x4_t w = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
   __builtin_amdgcn_raw_buffer_store_b128(w, r, byte_off, 0, 16);
@@ -272,8 +272,12 @@ __global__ void __launch_bounds__(512) varlen_kernel(const VarlenArgs a) {
   __syncthreads();
   __shared__ int32_t s_last;
   int32_t* counter = a.counters + (int64_t)row * a.kv_heads + kvh;
+  // The arrival is an acquire-release read-modify-write at agent scope. Its release half publishes, to every XCD, the
+  // partials all threads of this workgroup stored (each thread waited for its own stores, and the barrier above orders
+  // them before thread 0's release). Its acquire half, in the last workgroup to arrive, orders the loads of the other
+  // workgroups' partials below (after the second barrier) behind their releases.
   if (threadIdx.x == 0)
-    s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.splits - 1;
+    s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == a.splits - 1;
   __syncthreads();
   if (!s_last) return;
   // merge: 512 threads over the group's heads x D outputs, 8 consecutive dims each

@@ -21,6 +21,9 @@ inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 // to `bytes` when a launch asks for more than any before it; thread-safe. XT_OK or XT_ELAUNCH.
 int allow_lds(const void* fn, size_t bytes, const char* what);
 
+// Compute units of the current device (256 on an MI355X), read once per device; 256 if the query fails.
+int device_cus();
+
 // Workspaces of the split kernels (fused decode, sparse MLA) begin with a fixed region of arrival counters, one per
 // (row, head group) of a call: zero before the first call, left zero by every call. Split partials follow it, so calls
 // of any shape, of either kernel, may share one workspace as long as they do not overlap in time.

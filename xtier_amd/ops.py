@@ -7,6 +7,7 @@ xtier/backend/formats.py). Tensors are torch tensors on the GPU; every call runs
 """
 import ctypes
 import math
+import warnings
 
 import torch
 
@@ -15,6 +16,7 @@ from . import _lib
 LOG2E = 1.4426950408889634
 _DTYPES = {torch.bfloat16: _lib.XT_DTYPE_BF16, torch.float16: _lib.XT_DTYPE_F16}
 _workspaces = {}   # device index -> uint8 tensor, grown on demand (never during a graph capture)
+_retired = []      # workspaces a larger one replaced: kept alive, since graphs captured earlier hold their addresses
 
 
 def _ptr(t):
@@ -72,6 +74,9 @@ def workspace(device, nbytes):
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError(f'xtier_amd: the decode workspace must hold {nbytes} bytes before a graph capture; '
                                'call xtier_amd.ops.workspace(device, nbytes) first')
+        if buf is not None:
+            # never freed: a graph captured with it replays into these bytes (its arrival counters must stay zero)
+            _retired.append(buf)
         buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
         _workspaces[idx] = buf
     return buf
@@ -171,14 +176,29 @@ def pack(raw, req_to_token, req_indices, cu_k, total_k, max_k, output_dtype):
 
 # --- fused sparse attention ---------------------------------------------------------------------------------------
 
+_cu_counts = {}
+
+
+def device_cus(device=None):
+    """Compute units of the current (or given) GPU, 256 on an MI355X; 256 when no GPU is visible."""
+    if not torch.cuda.is_available():
+        return 256
+    idx = torch.cuda.current_device() if device is None else torch.device(device).index
+    idx = torch.cuda.current_device() if idx is None else idx
+    n = _cu_counts.get(idx)
+    if n is None:
+        n = _cu_counts[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return n
+
+
 def default_splits(rows, kv_heads, topk):
-    """Key splits per row: about 256 workgroups of one KV head (one per CU), at least 256 keys per split, and at most
-    8192 keys per split (the slot list lives in LDS). Measured on MI355X: batch 32 x 4 KV heads, top-2048 -> 2;
+    """Key splits per row: about one workgroup of one KV head per CU, at least 256 keys per split, and at most 8192
+    keys per split (the slot list lives in LDS). Measured on MI355X (256 CUs): batch 32 x 4 KV heads, top-2048 -> 2;
     batch 4 x 4 KV heads, top-2048 -> 8; 4096 prefill rows -> 1."""
     if topk <= 0:
         return 1
     units = max(1, rows * kv_heads)
-    splits = max(1, min(math.ceil(256 / units), topk // 256, 64))
+    splits = max(1, min(math.ceil(device_cus() / units), topk // 256, 64))
     return max(splits, min(64, math.ceil(topk / 8192)))
 
 
@@ -222,12 +242,27 @@ def sparse_decode(q, raw, table, indices, seq_lens, scale, page_size=1, row_req=
     return out
 
 
+def _narrowed(what, splits, fewer, need):
+    """A capture that must run with fewer key splits than the shape wants says so once per shape: it is slower."""
+    key = (what, splits, fewer, need)
+    if key not in _warned:
+        _warned.add(key)
+        warnings.warn(f'xtier_amd.{what}: inside a graph capture the cached workspace holds less than the {need} bytes '
+                      f'{splits} key splits need, so the call runs {fewer}, which is slower; call '
+                      f'xtier_amd.ops.workspace(device, {need}) before capturing, or pass ws=', RuntimeWarning,
+                      stacklevel=3)
+    return fewer
+
+
+_warned = set()
+
+
 def _capture_splits(device, rows, q_heads, dim, splits, ws):
     """``splits``, or 1 inside a graph capture whose cached workspace is too small (one key split needs no partials,
-    so no workspace has to grow inside the capture)."""
-    if (ws is None and torch.cuda.is_current_stream_capturing()
-            and _cached_workspace_bytes(device) < decode_workspace_bytes(rows, q_heads, dim, splits)):
-        return 1
+    so no workspace has to grow inside the capture), with a warning."""
+    need = decode_workspace_bytes(rows, q_heads, dim, splits)
+    if splits > 1 and ws is None and torch.cuda.is_current_stream_capturing() and _cached_workspace_bytes(device) < need:
+        return _narrowed('sparse_decode', splits, 1, need)
     return splits
 
 
@@ -416,9 +451,10 @@ def varlen_decode(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_
     max_k = max(int(max_seqlen_k), 1)
     if splits is None:
         splits = default_splits(rows, kv_heads, max_k)
-        if (ws is None and torch.cuda.is_current_stream_capturing()
-                and _cached_workspace_bytes(q.device) < varlen_workspace_bytes(rows, heads, dim, splits)):
-            splits = 1
+        need = varlen_workspace_bytes(rows, heads, dim, splits)
+        if (splits > 1 and ws is None and torch.cuda.is_current_stream_capturing()
+                and _cached_workspace_bytes(q.device) < need):
+            splits = _narrowed('varlen_decode', splits, 1, need)
     need = varlen_workspace_bytes(rows, heads, dim, splits)
     if ws is None:
         ws = (workspace(q.device, need) if _cached_workspace_bytes(q.device) >= need
@@ -481,10 +517,10 @@ def _mla_keys(indices, lengths, rows):
 
 
 def default_mla_splits(rows, topk, v4=False):
-    """Key splits per row for sparse MLA: about 256 workgroups (one per CU) and at least 256 keys per split, and at
-    least enough that a split's slot list fits in LDS beside the key and query tiles."""
+    """Key splits per row for sparse MLA: about one workgroup per CU and at least 256 keys per split, and at least
+    enough that a split's slot list fits in LDS beside the key and query tiles."""
     fit = math.ceil(topk / _lib.lib().xt_sparse_mla_max_split_keys(int(v4)))
-    return min(64, max(1, min(math.ceil(256 / max(1, rows)), max(1, topk // 256), 64), fit))
+    return min(64, max(1, min(math.ceil(device_cus() / max(1, rows)), max(1, topk // 256), 64), fit))
 
 
 def mla_workspace_bytes(rows, heads, splits, v4=False):
@@ -545,9 +581,10 @@ def sparse_mla(q, k_cache, indices, topk_length, attn_sink, softmax_scale, extra
     if splits is None:
         splits = default_mla_splits(rows, topk_all, v4)
         fewest = default_mla_splits(1 << 20, topk_all, v4)   # the LDS bound alone
-        if ws is None and torch.cuda.is_current_stream_capturing() and rows and \
-                _cached_workspace_bytes(q.device) < mla_workspace_bytes(rows, heads, splits, v4):
-            splits = fewest
+        need = mla_workspace_bytes(rows, heads, splits, v4)
+        if ws is None and torch.cuda.is_current_stream_capturing() and rows and splits > fewest and \
+                _cached_workspace_bytes(q.device) < need:
+            splits = _narrowed('sparse_mla', splits, fewest, need)
     need = mla_workspace_bytes(rows, heads, splits, v4)
     if ws is None:
         ws = (workspace(q.device, need) if _cached_workspace_bytes(q.device) >= need
