@@ -107,7 +107,7 @@ size_t xt_sparse_decode_workspace_bytes(int rows, int q_heads, int dim, int spli
  * resolved to pool slots through table row row_req[r] (row_req NULL: row r) with the page_size rule above.
  * K/V are dequantized in registers; out[r, h] = sum_k softmax_k(q.k * scale) v_k in the dtype out_dtype, a row
  * without valid keys writing 0. lse (optional, FP32 [rows, q_heads]): natural log-sum-exp of the scaled scores,
- * -inf for an empty row. q_heads must be a multiple of kv_heads with q_heads / kv_heads <= 16; dim = 128. Pool
+ * -inf for an empty row. q_heads must be a multiple of kv_heads with q_heads / kv_heads <= 16; dim 64, 128 or 256. Pool
  * pointers and strides as above: payload 16-byte and scales 4-byte aligned.
  * splits: key splits per row (1..64); workspace: xt_sparse_decode_workspace_bytes(rows, q_heads, dim, splits) bytes,
  * 256-byte aligned. With splits > 1 it holds a fixed 64 KB region of arrival counters (one per row and KV head group,
@@ -138,7 +138,7 @@ int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_s
  * page row, as the reference assumes; a block that starts mid-page continues on the next page here, where the
  * reference reads past the page). out[b, h'] = sum softmax(q.k * sm_scale * kv_scale) v * kv_scale over the query
  * heads h' of KV head h (natural exp, kv_fp4.py:100-113), 0 for a row without keys; lse (optional) as above.
- * Requirements: dim 128, q_heads / kv_heads <= 16, block_size a power of 2, page_stride / row_stride ==
+ * Requirements: dim 64, 128 or 256, q_heads / kv_heads <= 16, block_size a power of 2, page_stride / row_stride ==
  * sf_page_stride / sf_row_stride >= block_size. splits and workspace as xt_sparse_decode_nvfp4 (workgroups hold one
  * KV head, so the arrival counters need rows * kv_heads <= 16384 when splits > 1). */
 int xt_block_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, const uint8_t* k_pay,
