@@ -105,10 +105,12 @@ def test_mla_two_lists_empty_and_single_key_rows():
     ref, ref_lse = _ref(inp.q, pool, idx, lengths, sink, scale, extra=(pool2, idx2, len2))
     o = out[:, 0].float().cpu()
     assert torch.equal(o[0], torch.zeros_like(o[0])) and torch.isneginf(lse[0]).all()
-    rows = np.arange(w.rows) >= 1
+    rows = np.arange(w.rows) >= 2
     _check(out[:, 0], lse[:, :, 0], ref, ref_lse, nonempty=rows)
-    # one key: p = 1 -> out = latent * 1 / (1 + exp(sink - s)); without the sink term the value itself (checked by
-    # the oracle comparison above, within the FP16 rounding of the dequantized latent)
+    # one key: p = 1, so out = latent / (1 + exp(sink - s)), a raw latent value up to ~30 in size (outlier channels):
+    # within the FP16 rounding of the dequantized latent and the BF16 rounding of the output, relative to the value
+    d = np.abs(o[1].numpy().astype(np.float64) - ref[1])
+    assert np.all(d <= np.abs(ref[1]) * (2.0 ** -8 + 2.0 ** -10) + 1e-6), d.max()
 
 
 @pytest.mark.parametrize('heads', [64, 16])
@@ -232,14 +234,18 @@ def test_mla_prefill_chunk_full_size_sampled_rows():
     _check(out[rows], lse[rows], ref, ref_lse)
 
 
-def test_mla_latent_magnitudes_over_three_decades():
-    """Per-token latent magnitudes 10^U(-2, 1) (the spread of tests/qsa_fp4_check.py:26-34): small tokens' latents
-    come out of (e2m1 * e4m3) * g near the bottom of FP16's normal range, and still meet the bounds."""
+@pytest.mark.parametrize('top', [10.0, 1e-3])
+def test_mla_latent_magnitudes_over_three_decades(top):
+    """Per-token latent and rope magnitudes spread over three decades, 10^U(-3, 0) * top: top 10 is the spread of
+    tests/qsa_fp4_check.py:26-34; top 1e-3 makes g = amax / 2688 small enough that the small tokens' (e2m1 * e4m3) * g
+    falls below FP16's normal range. Outputs then span the data's own scale, so they are held to the reference test's
+    scale-free measures (max |err| / max |ref| < 1e-2, rms err / rms ref < 4e-3, tests/ds_sparse_mla_check.py:70-75)
+    and the LSE to 2e-3."""
     w = workloads.MlaWorkload('mla_spread', 16, 128, 8192, 2048)
     inp = workloads.mla_inputs(w, 20261023, 'cuda')
     gen = workloads.generator('cuda', 77)
     lat, rope = workloads.mla_cache_rows(w, gen, 'cuda', 0, w.slots)
-    mag = 10 ** torch.empty(w.slots, 1, device='cuda').uniform_(-2, 1, generator=gen)
+    mag = top * 10 ** torch.empty(w.slots, 1, device='cuda').uniform_(-3, 0, generator=gen)
     lat = (lat.float() * mag).to(torch.bfloat16)
     rope = (rope.float() * mag).to(torch.bfloat16)
     pool = LatentPool(w.slots, w.latent, w.rope, 'cuda')
@@ -248,4 +254,9 @@ def test_mla_latent_magnitudes_over_three_decades():
     scale = 1 / math.sqrt(576)
     out, lse = ops.sparse_mla(inp.q, pool, inp.slots, None, None, scale)
     ref, ref_lse = _compact_ref(inp.q, pool, inp.slots, scale)
-    _check(out, lse, ref, ref_lse)
+    d = out.float().cpu().numpy().astype(np.float64) - ref
+    max_rel = np.abs(d).max() / np.abs(ref).max()
+    rms_rel = np.sqrt((d ** 2).mean()) / np.sqrt((ref ** 2).mean())
+    assert max_rel < 1e-2 and rms_rel < 4e-3, (max_rel, rms_rel)
+    # scores here reach ~15: the FP16 rounding of the scaled query (2^-11 relative) moves the LSE in proportion
+    assert np.all(np.abs(lse.cpu().numpy() - ref_lse) <= 2e-3 + 2.0 ** -10 * np.abs(ref_lse))

@@ -13,7 +13,7 @@ __constant__ uint32_t kV4Exps[3] = {120, 127, 134};
 // One workgroup of 256 threads, thread b = byte b. Output (uint16 units):
 //   [0, 256)        fp8x2_to_f16<false>(b).x           (E4M3 byte in the low half)
 //   [256, 512)      fp8x2_to_f16<true>(b << 16).x      (E4M3 byte in the high half)
-//   [512, 2560)     fp4x2_to_f16<SEL>(b << 8 SEL), SEL = 0..3: 2 values each, low nibble first
+//   [512, 2560)     fp4x2_to_f16<SEL>(b << 8 SEL), SEL = 0..3: the result dword of each (element 0 first)
 //   [2560, 3328)    cvt_scalef32_pk_bf16_fp8(b, 2^(e - 127)) for the three exponents above
 // then FP32 (two uint16 units each) at [3328, 3328 + 2 * 2048): fp4x2_to_f32<SEL>(b << 8 SEL), SEL = 0..3.
 __global__ __launch_bounds__(256) void conversions_kernel(uint16_t* out) {
@@ -22,11 +22,9 @@ __global__ __launch_bounds__(256) void conversions_kernel(uint16_t* out) {
   out[256 + b] = __builtin_bit_cast(uint16_t, fp8x2_to_f16<true>(b << 16).x);
   const half2_t h[4] = {fp4x2_to_f16<0>(b), fp4x2_to_f16<1>(b << 8), fp4x2_to_f16<2>(b << 16),
                         fp4x2_to_f16<3>(b << 24)};
+  uint32_t* pairs = reinterpret_cast<uint32_t*>(out + 512);   // each pair stored as the dword the conversion wrote
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    out[512 + s * 512 + 2 * b] = __builtin_bit_cast(uint16_t, h[s].x);
-    out[512 + s * 512 + 2 * b + 1] = __builtin_bit_cast(uint16_t, h[s].y);
-  }
+  for (int s = 0; s < 4; ++s) pairs[s * 256 + b] = __builtin_bit_cast(uint32_t, h[s]);
 #pragma unroll
   for (int e = 0; e < 3; ++e) {
     typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -37,10 +35,7 @@ __global__ __launch_bounds__(256) void conversions_kernel(uint16_t* out) {
   const float2_t v[4] = {fp4x2_to_f32<0>(b), fp4x2_to_f32<1>(b << 8), fp4x2_to_f32<2>(b << 16),
                          fp4x2_to_f32<3>(b << 24)};
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    f[s * 512 + 2 * b] = v[s].x;
-    f[s * 512 + 2 * b + 1] = v[s].y;
-  }
+  for (int s = 0; s < 4; ++s) reinterpret_cast<float2_t*>(f)[s * 256 + b] = v[s];
 }
 
 }  // namespace

@@ -211,7 +211,8 @@ def sparse_decode(q, raw, table, indices, seq_lens, scale, page_size=1, row_req=
     """Fused NVFP4 sparse attention, one query per row: q [rows, q_heads, dim] BF16 attends to the valid positions of
     indices [rows, topk] (int32; valid: column < counts[r], 0 <= pos < seq_lens[r], pos <= query_pos[r] when given),
     resolved through ``table`` (token-granular req_to_token for page_size 1, else a page table) row row_req[r].
-    Returns out [rows, q_heads, dim] (BF16 unless ``out`` is given); lse [rows, q_heads] FP32 is filled if given."""
+    Returns out [rows, q_heads, dim] (BF16 unless ``out`` is given); lse [rows, q_heads] FP32 is filled if given.
+    ws: a workspace tensor, or None (the per-device cached one)."""
     raw, kv_heads, dim = _check_raw(raw, contiguous=False)
     rows, q_heads, qdim = q.shape
     if qdim != dim:
@@ -230,15 +231,16 @@ def sparse_decode(q, raw, table, indices, seq_lens, scale, page_size=1, row_req=
         row_req = row_req.to(torch.int64)
     seq_lens, counts, query_pos = (None if t is None else (t if t.dtype == torch.int32 else t.to(torch.int32))
                                    for t in (seq_lens, counts, query_pos))
+    args = (_ptr(q), q.stride(0), q.stride(1), *map(_ptr, raw), raw[0].shape[0], raw[0].stride(0), raw[2].stride(0),
+            _head_stride(raw[0]), _head_stride(raw[2]), kv_heads, q_heads, dim, _ptr(table), table.stride(0),
+            int(page_size), _ptr(row_req), _ptr(indices), indices.stride(0), topk, _ptr(counts), _ptr(seq_lens),
+            _ptr(query_pos), float(scale), _ptr(out), out.stride(0), out.stride(1), _DTYPES[out.dtype], _ptr(lse),
+            rows)
     if splits is None:
         splits = _capture_splits(q.device, rows, q_heads, dim, default_splits(rows, kv_heads, topk), ws)
     ws = _decode_ws(q.device, rows, q_heads, dim, splits, ws)
-    _lib.check(_lib.lib().xt_sparse_decode_nvfp4(
-        _ptr(q), q.stride(0), q.stride(1), *map(_ptr, raw), raw[0].shape[0], raw[0].stride(0), raw[2].stride(0),
-        _head_stride(raw[0]), _head_stride(raw[2]), kv_heads, q_heads, dim, _ptr(table),
-        table.stride(0), int(page_size), _ptr(row_req), _ptr(indices), indices.stride(0), topk, _ptr(counts),
-        _ptr(seq_lens), _ptr(query_pos), float(scale), _ptr(out), out.stride(0), out.stride(1), _DTYPES[out.dtype],
-        _ptr(lse), rows, int(splits), _ptr(ws), ws.numel(), _stream(q)), 'sparse_decode')
+    _lib.check(_lib.lib().xt_sparse_decode_nvfp4(*args, int(splits), _ptr(ws), ws.numel(), _stream(q)),
+               'sparse_decode')
     return out
 
 
