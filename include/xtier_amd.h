@@ -126,6 +126,23 @@ int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_s
                            int64_t out_row_stride, int64_t out_head_stride, int out_dtype, float* lse, int rows,
                            int splits, void* workspace, size_t workspace_bytes, xt_stream_t stream);
 
+/* No counterpart in the reference: xt_sparse_decode_nvfp4 for callers that cannot allocate device memory (code under
+ * graph capture that must not grow a memory pool, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments and results without the workspace: it uses a fixed 8 MiB array in the library's device memory, one per
+ * GPU, held until the process ends (64 KB of arrival counters, then the split partials), and calls no allocator. A
+ * call whose xt_sparse_decode_workspace_bytes(rows, q_heads, dim, splits) exceeds 8 MiB fails with XT_EWORKSPACE.
+ * Every call on one GPU shares that GPU's array: calls that overlap in time on one GPU race (as two calls sharing a
+ * workspace would). The first call on a device looks the array up and zeroes its counters on `stream`. */
+int xt_sparse_decode_nvfp4_static(const void* q, int64_t q_row_stride, int64_t q_head_stride, const uint8_t* k_pay,
+                                  const uint8_t* v_pay, const uint8_t* k_scales, const uint8_t* v_scales,
+                                  const float* gk, const float* gv, int64_t pool_slots, int64_t pay_stride,
+                                  int64_t sf_stride, int64_t pay_head_stride, int64_t sf_head_stride, int kv_heads,
+                                  int q_heads, int dim, const int32_t* table, int64_t table_stride, int page_size,
+                                  const int64_t* row_req, const int32_t* indices, int64_t idx_stride, int topk,
+                                  const int32_t* counts, const int32_t* seq_lens, const int32_t* query_pos,
+                                  float scale, void* out, int64_t out_row_stride, int64_t out_head_stride,
+                                  int out_dtype, float* lse, int rows, int splits, xt_stream_t stream);
+
 /* Block-sparse NVFP4 decode over head-major pages (the MiniMax cache layout; replaces
  * xtier/packs/minimax_m3/kv_fp4.py:119-153, fp4_sparse_decode, behind the hook _decode_main :579-590).
  * Pool: page p, KV head h, row t (t < block_size) holds payload at k_pay + p * page_stride + h * head_stride +

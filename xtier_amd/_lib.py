@@ -51,6 +51,8 @@ SIGNATURES = {
     'xt_sparse_decode_workspace_bytes': (_Z, [_I, _I, _I, _I]),
     'xt_sparse_decode_nvfp4': (_I, [_P, _L, _L, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _P, _L, _I, _P,
                                     _P, _L, _I, _P, _P, _P, _F, _P, _L, _L, _I, _P, _I, _I, _P, _Z, _P]),
+    'xt_sparse_decode_nvfp4_static': (_I, [_P, _L, _L, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _P, _L,
+                                           _I, _P, _P, _L, _I, _P, _P, _P, _F, _P, _L, _L, _I, _P, _I, _I, _P]),
     'xt_block_sparse_decode_nvfp4': (_I, [_P, _L, _L, _P, _P, _P, _P, _F, _L, _I, _I, _I, _I, _L, _L, _L, _L, _L, _L,
                                           _P, _L, _I, _P, _P, _L, _L, _I, _P, _F, _P, _L, _L, _I, _P, _I, _I, _P, _Z,
                                           _P]),

@@ -32,6 +32,8 @@
 #include "xt_common.h"
 #include "xt_host.h"
 
+#include <mutex>
+
 namespace xt {
 namespace {
 
@@ -738,6 +740,76 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
                      pay_stride, sf_stride, kv_heads, q_heads, dim, table, table_stride, page_size, row_req, indices,
                      idx_stride, topk, counts, seq_lens, query_pos, scale, out, out_row_stride, out_head_stride,
                      out_dtype, lse, rows, splits, workspace, workspace_bytes, ad, stream);
+}
+
+// --- the variant that allocates nothing ------------------------------------------------------------------------------
+// Callers that cannot allocate device memory (work under graph capture, tight serving loops, harnesses that forbid
+// hipMalloc) run the sparse decode with a workspace that is a fixed array of the library's own device memory: one
+// `scratch` array per GPU, loaded with the code object and held until the process ends. The array's name is a host-side
+// stand-in; its device address, looked up once per device, is what kernels receive.
+constexpr size_t kScratchBytes = 8u << 20;   // arrival counters (64 KB) + split partials
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::once_flag g_scratch_once[kScratchDevices];
+void* g_scratch[kScratchDevices];             // device address of each GPU's array (NULL: lookup failed)
+hipError_t g_scratch_error[kScratchDevices];
+
+__global__ void zero_counters(uint32_t* p, int words) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < words; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+}  // namespace
+
+// The current device's scratch address. The first call on a device looks it up with that device current and zeroes
+// the counter region with a kernel on `stream` (the decode kernels leave the counters zero after every call, and device
+// globals start zeroed, so later calls need no clearing).
+static int device_scratch(const char* what, hipStream_t stream, void** ptr) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices)
+    return fail(XT_ELAUNCH, "%s: no current device (or device index >= %d)", what, kScratchDevices);
+  std::call_once(g_scratch_once[dev], [&] {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess) {
+      hipLaunchKernelGGL(zero_counters, dim3(16), dim3(256), 0, stream, static_cast<uint32_t*>(p),
+                         (int)(kCounterBytes / 4));
+      e = hipGetLastError();
+    }
+    g_scratch_error[dev] = e;
+    g_scratch[dev] = e == hipSuccess ? p : nullptr;
+  });
+  if (!g_scratch[dev])
+    return fail(XT_ELAUNCH, "%s: the device scratch array is not available on device %d: %s", what, dev,
+                hipGetErrorString(g_scratch_error[dev]));
+  *ptr = g_scratch[dev];
+  return XT_OK;
+}
+
+extern "C" int xt_sparse_decode_nvfp4_static(const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                                             const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t* k_scales,
+                                             const uint8_t* v_scales, const float* gk, const float* gv,
+                                             int64_t pool_slots, int64_t pay_stride, int64_t sf_stride,
+                                             int64_t pay_head_stride, int64_t sf_head_stride, int kv_heads,
+                                             int q_heads, int dim, const int32_t* table, int64_t table_stride,
+                                             int page_size, const int64_t* row_req, const int32_t* indices,
+                                             int64_t idx_stride, int topk, const int32_t* counts,
+                                             const int32_t* seq_lens, const int32_t* query_pos, float scale,
+                                             void* out, int64_t out_row_stride, int64_t out_head_stride,
+                                             int out_dtype, float* lse, int rows, int splits, xt_stream_t stream) {
+  const char* what = "xt_sparse_decode_nvfp4_static";
+  const size_t need = xt_sparse_decode_workspace_bytes(rows, q_heads, dim, splits);
+  if (need > kScratchBytes)
+    return fail(XT_EWORKSPACE, "%s: %d rows x %d heads x %d splits need %zu bytes of workspace, more than the %zu of "
+                "the static array; use fewer splits or xt_sparse_decode_nvfp4 with a workspace", what, rows, q_heads,
+                splits, need, kScratchBytes);
+  void* ws = nullptr;
+  if (int e = device_scratch(what, reinterpret_cast<hipStream_t>(stream), &ws)) return e;
+  return xt_sparse_decode_nvfp4(q, q_row_stride, q_head_stride, k_pay, v_pay, k_scales, v_scales, gk, gv, pool_slots,
+                                pay_stride, sf_stride, pay_head_stride, sf_head_stride, kv_heads, q_heads, dim, table,
+                                table_stride, page_size, row_req, indices, idx_stride, topk, counts, seq_lens,
+                                query_pos, scale, out, out_row_stride, out_head_stride, out_dtype, lse, rows, splits, ws,
+                                kScratchBytes, stream);
 }
 
 // The head-major page checks shared by the block decode and the block prefill; fills the page-row remap.

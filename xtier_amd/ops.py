@@ -212,7 +212,8 @@ def sparse_decode(q, raw, table, indices, seq_lens, scale, page_size=1, row_req=
     indices [rows, topk] (int32; valid: column < counts[r], 0 <= pos < seq_lens[r], pos <= query_pos[r] when given),
     resolved through ``table`` (token-granular req_to_token for page_size 1, else a page table) row row_req[r].
     Returns out [rows, q_heads, dim] (BF16 unless ``out`` is given); lse [rows, q_heads] FP32 is filled if given.
-    ws: a workspace tensor, or None (the per-device cached one)."""
+    ws: a workspace tensor, None (the per-device cached one), or 'static': the library's fixed per-GPU array
+    (xt_sparse_decode_nvfp4_static; with ``out`` given the call allocates nothing)."""
     raw, kv_heads, dim = _check_raw(raw, contiguous=False)
     rows, q_heads, qdim = q.shape
     if qdim != dim:
@@ -236,6 +237,11 @@ def sparse_decode(q, raw, table, indices, seq_lens, scale, page_size=1, row_req=
             int(page_size), _ptr(row_req), _ptr(indices), indices.stride(0), topk, _ptr(counts), _ptr(seq_lens),
             _ptr(query_pos), float(scale), _ptr(out), out.stride(0), out.stride(1), _DTYPES[out.dtype], _ptr(lse),
             rows)
+    if isinstance(ws, str) and ws == 'static':
+        # the library's own per-GPU scratch array: nothing is allocated for this call
+        splits = default_splits(rows, kv_heads, topk) if splits is None else splits
+        _lib.check(_lib.lib().xt_sparse_decode_nvfp4_static(*args, int(splits), _stream(q)), 'sparse_decode')
+        return out
     if splits is None:
         splits = _capture_splits(q.device, rows, q_heads, dim, default_splits(rows, kv_heads, topk), ws)
     ws = _decode_ws(q.device, rows, q_heads, dim, splits, ws)
