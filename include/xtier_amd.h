@@ -68,6 +68,33 @@ int xt_nvfp4_quantize_append(const void* src, int64_t n_rows, int heads, int dim
                              uint8_t* scales, int64_t pool_slots, int64_t pay_stride, int64_t sf_stride,
                              int64_t pay_head_stride, int64_t sf_head_stride, int saturate, xt_stream_t stream);
 
+/* One tensor of a KV append (xt_nvfp4_store_kv): src BF16 [n_rows, heads, dim] (element strides; dim a multiple of 16,
+ * 16-byte aligned rows) written to the pool at each row's slot s, the slot's page p = s / page_size and row
+ * t = s % page_size: head h's payload at pay + p * pay_page_stride + t * pay_row_stride + h * pay_head_stride
+ * (dim / 2 bytes) and its E4M3 scales at scales + p * sf_page_stride + t * sf_row_stride + h * sf_head_stride
+ * (dim / 16 bytes), quantized with the device global scale *g as xt_nvfp4_quantize_append does. g == NULL stores the
+ * BF16 values as they are (dim * 2 bytes at the payload address; scales unused): the rope rows of a latent cache.
+ * Token-major pools: page_size 1 and the slot stride as the page stride. All strides in bytes. */
+typedef struct {
+  const void* src;
+  int64_t src_row_stride, src_head_stride;
+  int heads, dim;
+  const float* g;
+  uint8_t* pay;
+  uint8_t* scales;
+  int64_t pay_page_stride, pay_row_stride, pay_head_stride;
+  int64_t sf_page_stride, sf_row_stride, sf_head_stride;
+} xt_kv_store;
+
+/* The fused KV-write epilogue: the n_stores (1..4) tensors of one append (K and V, plus the MiniMax index K or a latent
+ * cache's rope rows) quantized and written at the same slots[n_rows] (int64; negative or >= pool_slots: skipped) in ONE
+ * launch, bytes identical to one xt_nvfp4_quantize_append per tensor. page_size: rows per page, a power of 2 (1 for
+ * token-major pools). Replaces SGLang's fused quantize + store that the MiniMax pack enables
+ * (xtier/packs/minimax_m3/kv_fp4.py:546-559, nvfp4_store_kv_index as tests/minimax_kv_fp4_check.py:152-175 calls it)
+ * and the per-buffer quantize of the QSA hook (xtier/packs/qwen4_exp/qsa_fp4.py:202-205). */
+int xt_nvfp4_store_kv(const xt_kv_store* stores, int n_stores, int64_t n_rows, const int64_t* slots,
+                      int64_t pool_slots, int page_size, int saturate, xt_stream_t stream);
+
 /* --- QSA gather and pack (bit-exact BF16/FP16 rows) -------------------------------------------------------------- */
 
 /* QSA decode/verify gather (xtier/packs/qwen4_exp/qsa_fp4.py:119-143, :174-180; hook extraction :223-228):
@@ -90,6 +117,26 @@ int xt_qsa_pack_nvfp4(const uint8_t* k_pay, const uint8_t* v_pay, const uint8_t*
                       const float* gk, const float* gv, int64_t pool_slots, int heads, int dim,
                       const int32_t* req_to_token, int64_t sr0, int64_t sr1, const int64_t* req_indices, int batch,
                       const int32_t* cu_k, int max_k, void* out_k, void* out_v, int out_dtype, xt_stream_t stream);
+
+/* The QSA gather and prefix pack on an FP8 (E4M3) pool (the FP8 branch of qsa_fp4.py:104-116 and :160-162, checked by
+ * tests/qsa_fp8_check.py): k / v are E4M3 bytes [pool_slots, heads, dim] with no block or global scale, and each value
+ * is its plain E4M3 value (exact in BF16 and FP16). Arguments and layouts otherwise as xt_qsa_gather_nvfp4 /
+ * xt_qsa_pack_nvfp4; K and V 8-byte aligned. */
+int xt_qsa_gather_fp8(const uint8_t* k, const uint8_t* v, int64_t pool_slots, int heads, int dim,
+                      const int32_t* req_to_token, int64_t req_stride, const int64_t* req_indices,
+                      const int32_t* indices, int64_t idx_stride, const int32_t* seq_lens, const int32_t* cu_k,
+                      void* out_k, void* out_v, int out_dtype, int batch, int topk, int zero_fill_cols,
+                      xt_stream_t stream);
+int xt_qsa_pack_fp8(const uint8_t* k, const uint8_t* v, int64_t pool_slots, int heads, int dim,
+                    const int32_t* req_to_token, int64_t sr0, int64_t sr1, const int64_t* req_indices, int batch,
+                    const int32_t* cu_k, int max_k, void* out_k, void* out_v, int out_dtype, xt_stream_t stream);
+
+/* The packed-row layout of a decode gather (SGLang's qwen_sparse_fa2_cu_seqlens_triton as qsa_fp4.py:255-256 calls
+ * it): valid_counts[b] = the number of indices[b, :topk] (row stride idx_stride) with 0 <= index < seq_lens[b], and
+ * cu_seqlens_k [batch + 1] their running sum from 0. As in the reference, a row's valid indices are expected to come
+ * first (top-k lists padded with -1 at the end). One workgroup on `stream`. */
+int xt_qsa_valid_counts(const int32_t* seq_lens, const int32_t* indices, int64_t idx_stride, int batch, int topk,
+                        int32_t* valid_counts, int32_t* cu_seqlens_k, xt_stream_t stream);
 
 /* --- fused sparse attention over the NVFP4 pool ------------------------------------------------------------------ */
 

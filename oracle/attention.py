@@ -29,11 +29,13 @@ def slots_of(table, table_row, positions, page_size):
 
 def gather_qsa(raw, req_to_token, req_indices, indices, seq_lens, cu_k, out_k, out_v, batch, topk, zero_fill_cols=0):
     """qsa_fp4.py:119-143 and :174-180 in numpy. raw = (k_pay u8 [m, H, D/2], v_pay, k_sf u8 [m, H, D/16], v_sf,
-    gk, gv); out_k/out_v are uint16 arrays of BF16 bits [rows, H, D], written in place where the reference stores.
+    gk, gv), or an FP8 pool's (k u8 [m, H, D], v, None, None, None, None); out_k/out_v are uint16 arrays of BF16 bits
+    [rows, H, D], written in place where the reference stores.
     Rows are (e2m1 * e4m3) * g in FP32 rounded to BF16; zero-fill mode writes zeros for the invalid columns below
     zero_fill_cols."""
     k_pay, v_pay, k_sf, v_sf, gk, gv = raw
     heads = k_pay.shape[1]
+    rows_of = _row_reader(raw)
     num_cols = zero_fill_cols if zero_fill_cols > 0 else topk
     span = -(-num_cols // 16) * 16
     indices = np.asarray(indices)
@@ -47,27 +49,44 @@ def gather_qsa(raw, req_to_token, req_indices, indices, seq_lens, cu_k, out_k, o
         valid = (cols < valid_count) & (pos >= 0) & (pos < length)
         store = (cols < zero_fill_cols) if zero_fill_cols > 0 else valid
         slots = np.where(valid, np.asarray(req_to_token)[req, np.where(valid, pos, 0)], 0).astype(np.int64)
-        for pay, sf, g, out in ((k_pay, k_sf, gk, out_k), (v_pay, v_sf, gv, out_v)):
-            p = np.where(valid[:, None, None], pay[slots], 0).astype(np.uint8)
-            s = np.where(valid[:, None, None], sf[slots], 0).astype(np.uint8)
-            rows = nvfp4.bf16_bits(nvfp4.dequant(p, s, g))
+        for side, out in ((0, out_k), (1, out_v)):
+            rows = rows_of(side, slots)
+            rows[~valid] = 0
             dst = start + cols[store]
             out[dst] = rows[store]
     return out_k, out_v
 
 
+def _row_reader(raw):
+    """rows(side, slots) -> BF16 bits [n, H, D] of K (side 0) or V (side 1) at pool slots: NVFP4 (e2m1 * e4m3) * g
+    (qsa_fp4.py:94-101), or, for an FP8 pool (raw = (k, v, None, None, None, None)), the E4M3 value of each byte
+    (qsa_fp4.py:104-116), NaN bytes giving the quiet NaN 0x7FC0."""
+    k_pay, v_pay, k_sf, v_sf, gk, gv = raw
+    if k_sf is None:
+        def rows(side, slots):
+            vals = nvfp4.e4m3_decode((k_pay, v_pay)[side][slots])
+            bits = nvfp4.bf16_bits(vals)
+            bits[np.isnan(vals)] = 0x7FC0
+            return bits
+        return rows
+    return lambda side, slots: nvfp4.bf16_bits(nvfp4.dequant(((k_pay, v_pay)[side])[slots],
+                                                             ((k_sf, v_sf)[side])[slots], (gk, gv)[side]))
+
+
 def pack_qsa(raw, req_to_token, req_indices, cu_k, total_k, heads_dim=None):
     """qsa_fp4.py:146-162 and :183-192: request b's first cu_k[b+1]-cu_k[b] positions, in order, as BF16 bits rows
-    [total_k, H, D] (rows not covered stay 0 here; the reference leaves them unwritten)."""
-    k_pay, v_pay, k_sf, v_sf, gk, gv = raw
-    heads, half = k_pay.shape[1], k_pay.shape[2]
-    out_k = np.zeros((total_k, heads, half * 2), dtype=np.uint16)
+    [total_k, H, D] (rows not covered stay 0 here; the reference leaves them unwritten); NVFP4 or FP8 pools."""
+    k_pay = raw[0]
+    heads = k_pay.shape[1]
+    dim = k_pay.shape[2] if raw[2] is None else k_pay.shape[2] * 2
+    rows_of = _row_reader(raw)
+    out_k = np.zeros((total_k, heads, dim), dtype=np.uint16)
     out_v = np.zeros_like(out_k)
     for b in range(len(req_indices)):
         start, end = int(cu_k[b]), int(cu_k[b + 1])
         slots = np.asarray(req_to_token)[int(req_indices[b]), :end - start].astype(np.int64)
-        out_k[start:end] = nvfp4.bf16_bits(nvfp4.dequant(k_pay[slots], k_sf[slots], gk))
-        out_v[start:end] = nvfp4.bf16_bits(nvfp4.dequant(v_pay[slots], v_sf[slots], gv))
+        out_k[start:end] = rows_of(0, slots)
+        out_v[start:end] = rows_of(1, slots)
     return out_k, out_v
 
 

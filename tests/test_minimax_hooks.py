@@ -43,7 +43,8 @@ def test_attach_scales_and_install():
     minimax.install(registry, SimpleNamespace(AROUND='around'))
     assert seen == [(f'{minimax.OPS}.flash_decode_with_gqa_share_sparse', minimax.decode_main, 'around'),
                     (f'{minimax.OPS}.flash_prefill_with_gqa_share_sparse', minimax.prefill_main, 'around'),
-                    (f'{minimax.OPS}.minimax_sparse_prefill', minimax.sparse_prefill, 'around')]
+                    (f'{minimax.OPS}.minimax_sparse_prefill', minimax.sparse_prefill, 'around'),
+                    (minimax.STORE, minimax.store_kv_index, 'around')]
     # caches without scale bytes fall through
     assert minimax.prefill_main(_original, k_cache=torch.zeros(1))[0] == 'original'
     got = minimax.sparse_prefill(_original, *range(16), flag=1)
@@ -63,3 +64,17 @@ def test_deepseek_hook_falls_through_and_installs():
     registry = SimpleNamespace(register=lambda name, fn, kind: seen.append((name, fn, kind)))
     deepseek.install(registry, SimpleNamespace(AROUND='around'))
     assert [s[1] for s in seen] == [deepseek.flash_mla_with_kvcache, deepseek.no_sparse_prefill]
+
+
+def test_enable_fused_store_conditions(monkeypatch):
+    def pool(head_dim=128, index_dim=128, pages=(128, 128), scales=(1.0, 1.0), on=False):
+        main = SimpleNamespace(head_dim=head_dim, page_size=pages[0], global_scale=torch.tensor([scales[0]]))
+        index = SimpleNamespace(INDEX_HEAD_DIM=index_dim, page_size=pages[1], global_scale=torch.tensor([scales[1]]))
+        return SimpleNamespace(main_pool=main, index_k_pool=index, use_nvfp4_fused_quantize_store=on)
+    p = pool()
+    assert minimax.enable_fused_store(p) and p.use_nvfp4_fused_quantize_store
+    for bad in (pool(index_dim=64), pool(pages=(128, 64)), pool(scales=(1.0, 0.5))):
+        assert not minimax.enable_fused_store(bad) and not bad.use_nvfp4_fused_quantize_store
+    monkeypatch.setenv('XTIER_MINIMAX_FP4_FUSED_STORE', '0')
+    off = pool()
+    assert not minimax.enable_fused_store(off) and not off.use_nvfp4_fused_quantize_store

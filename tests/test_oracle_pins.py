@@ -171,3 +171,39 @@ def test_block_decode_lse_is_torch_logsumexp_of_the_expanded_keys():
             np.testing.assert_allclose(lse[r, h * group:(h + 1) * group], want, rtol=0, atol=1e-10)
     fin = lse[np.isfinite(lse)]
     assert fin.size and np.all(np.abs(fin) < 50)   # the scores are not saturated: the log of the sum matters
+
+
+# --- FP8 pools ------------------------------------------------------------------------------------------------------
+
+def test_fp8_gather_and_pack_equal_torch_decode_then_index():
+    """qsa_fp4.py:104-116: on an FP8 pool every value is its E4M3 value; checked against torch's float8_e4m3fn ->
+    bfloat16 of the whole pool, then indexed (NaN bytes compared as NaN, as tests/qsa_fp8_check.py compares them)."""
+    rng = np.random.default_rng(15)
+    slots, heads, dim = 400, 2, 64
+    k8 = rng.integers(0, 256, (slots, heads, dim), dtype=np.uint8)
+    v8 = rng.integers(0, 256, (slots, heads, dim), dtype=np.uint8)
+    raw = (k8, v8, None, None, None, None)
+    full = lambda a: torch.from_numpy(a).view(torch.float8_e4m3fn).to(torch.bfloat16).float().numpy()
+    kf, vf = full(k8), full(v8)
+    r2t = np.stack([rng.permutation(slots)[:300] for _ in range(2)]).astype(np.int32)
+    req, lens = np.array([1, 0]), [300, 77]
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    pk, pv = attention.pack_qsa(raw, r2t, req, cu, int(cu[-1]))
+    for b, n in enumerate(lens):
+        sl = r2t[req[b], :n]
+        np.testing.assert_array_equal(nvfp4.bf16_to_f32(pk[cu[b]:cu[b + 1]]), kf[sl])
+        np.testing.assert_array_equal(nvfp4.bf16_to_f32(pv[cu[b]:cu[b + 1]]), vf[sl])
+    idx = np.full((2, 80), -1, np.int32)
+    idx[0, :60] = rng.permutation(300)[:60]
+    idx[1, :50] = rng.permutation(77)[:50]
+    seq = np.array([300, 40], np.int32)
+    cnt = [60, int((idx[1, :50] < 40).sum())]
+    idx[1, :50] = np.concatenate([np.sort(idx[1, :50][idx[1, :50] < 40]), np.sort(idx[1, :50][idx[1, :50] >= 40])])
+    cu2 = np.array([0, 60, 60 + cnt[1]])
+    gk_ = np.zeros((cu2[-1], heads, dim), np.uint16)
+    gv_ = gk_.copy()
+    attention.gather_qsa(raw, r2t, req, idx, seq, cu2, gk_, gv_, 2, 80)
+    for b in range(2):
+        sl = r2t[req[b], idx[b, :cnt[b]]]
+        np.testing.assert_array_equal(nvfp4.bf16_to_f32(gk_[cu2[b]:cu2[b + 1]]), kf[sl])
+        np.testing.assert_array_equal(nvfp4.bf16_to_f32(gv_[cu2[b]:cu2[b + 1]]), vf[sl])

@@ -112,3 +112,20 @@ def test_resolve_returns_the_varlen_decode():
     assert qsa.resolve(lambda: 'original') is ops.varlen_decode
     with pytest.raises(NotImplementedError):
         ops.varlen_decode(torch.zeros(2, 4, 64), None, None, torch.zeros(3), torch.zeros(3), 2, 8, 0.1)
+
+
+def test_raw_buffers_fp8_pool_returns_the_bytes_without_scales():
+    class Fp8Pool:
+        dtype = torch.float8_e4m3fn
+
+        def __init__(self):
+            self.k = torch.zeros(8, 2, 128, dtype=torch.float8_e4m3fn)
+            self.v = torch.ones(8, 2, 128).to(torch.float8_e4m3fn)
+
+        def get_key_buffer(self, layer_id):
+            return self.k
+
+        def get_value_buffer(self, layer_id):
+            return self.v
+    raw = qsa.raw_buffers(Fp8Pool(), SimpleNamespace(layer_id=0))
+    assert raw[0].dtype == torch.uint8 and raw[1][0, 0, 0].item() == 0x38 and raw[2:] == (None,) * 4

@@ -22,6 +22,13 @@ _Z = ctypes.c_size_t
 
 
 
+class KvStore(ctypes.Structure):
+    """xt_kv_store: one tensor of a fused KV append (strides of the source in elements, of the pool in bytes)."""
+    _fields_ = [('src', _P), ('src_row_stride', _L), ('src_head_stride', _L), ('heads', _I), ('dim', _I),
+                ('g', _P), ('pay', _P), ('scales', _P), ('pay_page_stride', _L), ('pay_row_stride', _L),
+                ('pay_head_stride', _L), ('sf_page_stride', _L), ('sf_row_stride', _L), ('sf_head_stride', _L)]
+
+
 class MlaCache(ctypes.Structure):
     """xt_mla_cache: one NVFP4 latent + BF16 rope cache (strides in bytes, 0 = packed)."""
     _fields_ = [('pay', _P), ('scales', _P), ('rope', _P), ('g', _P), ('slots', _L), ('pay_stride', _L),
@@ -39,15 +46,20 @@ class MlaFp8Cache(ctypes.Structure):
 
 
 _CP, _KP, _FP = ctypes.POINTER(MlaCache), ctypes.POINTER(MlaKeys), ctypes.POINTER(MlaFp8Cache)
+_SP = ctypes.POINTER(KvStore)
 
 SIGNATURES = {
     'xt_version': (_I, []),
     'xt_last_error': (ctypes.c_char_p, []),
     'xt_nvfp4_global_scale': (_I, [_P, _L, _I, _I, _L, _L, _P, _P, _P]),
     'xt_nvfp4_quantize_append': (_I, [_P, _L, _I, _I, _L, _L, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _P]),
+    'xt_nvfp4_store_kv': (_I, [_SP, _I, _L, _P, _L, _I, _I, _P]),
     'xt_qsa_gather_nvfp4': (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _P, _L, _P, _P, _L, _P, _P, _P, _P, _I, _I, _I,
                                  _I, _P]),
     'xt_qsa_pack_nvfp4': (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _P, _L, _L, _P, _I, _P, _I, _P, _P, _I, _P]),
+    'xt_qsa_gather_fp8': (_I, [_P, _P, _L, _I, _I, _P, _L, _P, _P, _L, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    'xt_qsa_pack_fp8': (_I, [_P, _P, _L, _I, _I, _P, _L, _L, _P, _I, _P, _I, _P, _P, _I, _P]),
+    'xt_qsa_valid_counts': (_I, [_P, _P, _L, _I, _I, _P, _P, _P]),
     'xt_sparse_decode_workspace_bytes': (_Z, [_I, _I, _I, _I]),
     'xt_sparse_decode_nvfp4': (_I, [_P, _L, _L, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _I, _P, _L, _I, _P,
                                     _P, _L, _I, _P, _P, _P, _F, _P, _L, _L, _I, _P, _I, _I, _P, _Z, _P]),

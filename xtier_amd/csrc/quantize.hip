@@ -49,6 +49,86 @@ __global__ void global_scale_kernel(const uint32_t* __restrict__ ws, float* __re
   }
 }
 
+// The E2M1 code of q = x / d as formats.py:124-127 computes it, without the division. For a midpoint m of the code
+// table, fl(|x| / d) > m holds exactly when |x| / d > m + ulp(m) / 2 (every midpoint has an even last mantissa bit, so
+// the tie rounds down to m), i.e. when |x| > t_m * d. That product (25 by 24 significant bits) is exact in FP64, and
+// an FP32 |x| exceeds a real T exactly when it exceeds T rounded toward -inf to FP32. So the seven thresholds of a
+// block are formed once, and each value takes seven FP32 compares. d must be positive and finite.
+struct Thresholds {
+  float t[7];
+};
+
+__device__ inline Thresholds block_thresholds(float d) {
+  // m + ulp(m) / 2 for m = 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5 (ulp(m) = 2^(e - 23), e the exponent of m)
+  constexpr double kMid[7] = {0.25 + 0x1p-26, 0.75 + 0x1p-25, 1.25 + 0x1p-24, 1.75 + 0x1p-24, 2.5 + 0x1p-23,
+                              3.5 + 0x1p-23, 5.0 + 0x1p-22};
+  Thresholds th;
+#pragma unroll
+  for (int i = 0; i < 7; ++i) th.t[i] = __double2float_rd(kMid[i] * (double)d);
+  return th;
+}
+
+// Non-negative floats order as their bit patterns, so |x| > t holds exactly when bits(t) - bits(|x|) is negative
+// (both below 2^31; a NaN |x| exceeds every threshold and codes 7, as the reference's bucketize gives it). The code
+// is found by a three-level search over the seven thresholds, each level's threshold picked with a bitfield select
+// under the masks of the levels above. The sign bit goes with a code above 0 when x < 0 (not for a NaN).
+__device__ inline int32_t above(uint32_t t, uint32_t a) { return (int32_t)(t - a) >> 31; }   // -1 if a > t, else 0
+
+__device__ inline uint32_t e2m1_code(float x, const Thresholds& th) {
+  const uint32_t bits = __float_as_uint(x), a = bits & 0x7FFFFFFFu;
+  const uint32_t t[7] = {__float_as_uint(th.t[0]), __float_as_uint(th.t[1]), __float_as_uint(th.t[2]),
+                         __float_as_uint(th.t[3]), __float_as_uint(th.t[4]), __float_as_uint(th.t[5]),
+                         __float_as_uint(th.t[6])};
+  const uint32_t m4 = above(t[3], a);
+  const uint32_t m2 = above((m4 & t[5]) | (~m4 & t[1]), a);
+  const uint32_t hi = (m2 & t[6]) | (~m2 & t[4]), lo = (m2 & t[2]) | (~m2 & t[0]);
+  const uint32_t m1 = above((m4 & hi) | (~m4 & lo), a);
+  const uint32_t code = (m4 & 4u) | (m2 & 2u) | (m1 & 1u);
+  const bool negative = (int32_t)bits < 0 && a <= 0x7F800000u;
+  return code | (negative && code ? 8u : 0u);
+}
+
+// The division form, for a block whose d is not finite (a NaN or infinite global scale).
+__device__ inline uint32_t e2m1_code_div(float x, float d) {
+  const float q = x / d;
+  const float a_ = __builtin_fabsf(q);
+  uint32_t code = (uint32_t)(a_ > 0.25f) + (uint32_t)(a_ > 0.75f) + (uint32_t)(a_ > 1.25f) + (uint32_t)(a_ > 1.75f) +
+                  (uint32_t)(a_ > 2.5f) + (uint32_t)(a_ > 3.5f) + (uint32_t)(a_ > 5.0f);
+  if (q != q) code = 7u;
+  if (q < 0.0f && code > 0u) code |= 8u;
+  return code;
+}
+
+// 16 BF16 values (eight dwords) -> eight payload bytes (two dwords) and the E4M3 scale byte, with global scale g.
+__device__ inline void quantize_block(const uint32_t (&w)[8], float g, bool saturate, uint32_t (&packed)[2],
+                                      uint32_t& sbyte) {
+  uint32_t amax_bits = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    amax_bits = max(amax_bits, w[k] & 0x7FFFu);
+    amax_bits = max(amax_bits, (w[k] >> 16) & 0x7FFFu);
+  }
+  const float bamax = bf16_bits_to_f32(amax_bits);
+  sbyte = e4m3_encode(bamax / (6.0f * g), saturate);
+  float d = e4m3_decode(sbyte) * g;
+  d = (d < 1e-30f) ? 1e-30f : d;
+  packed[0] = packed[1] = 0u;
+  if (__builtin_isfinite(d)) {
+    const Thresholds th = block_thresholds(d);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float x = bf16_bits_to_f32(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu);
+      packed[e >> 3] |= e2m1_code(x, th) << (4 * (e & 7));
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float x = bf16_bits_to_f32(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu);
+      packed[e >> 3] |= e2m1_code_div(x, d) << (4 * (e & 7));
+    }
+  }
+}
+
 // One thread per 16-element block: read 32 bytes of BF16, write 8 bytes of payload and one scale byte.
 __global__ void quantize_append_kernel(const uint16_t* __restrict__ src, int64_t n_rows, int heads, int dim,
                                        int64_t rs, int64_t hs, const int64_t* __restrict__ slots,
@@ -69,37 +149,80 @@ __global__ void quantize_append_kernel(const uint16_t* __restrict__ src, int64_t
   const uint4 a = reinterpret_cast<const uint4*>(p)[0];
   const uint4 b = reinterpret_cast<const uint4*>(p)[1];
   const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  float x[16];
-  uint32_t amax_bits = 0;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    x[2 * k] = bf16_bits_to_f32(w[k] & 0xFFFFu);
-    x[2 * k + 1] = bf16_bits_to_f32(w[k] >> 16);
-    amax_bits = max(amax_bits, w[k] & 0x7FFFu);
-    amax_bits = max(amax_bits, (w[k] >> 16) & 0x7FFFu);
-  }
-  const float g = *gp;
-  const float six_g = 6.0f * g;
-  const float bamax = bf16_bits_to_f32(amax_bits);
-  const uint32_t sbyte = e4m3_encode(bamax / six_g, saturate != 0);
-  float denom = e4m3_decode(sbyte) * g;
-  denom = (denom < 1e-30f) ? 1e-30f : denom;
-  uint32_t packed[2] = {0u, 0u};
-#pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const float q = x[e] / denom;
-    const float a_ = __builtin_fabsf(q);
-    uint32_t code = (uint32_t)(a_ > 0.25f) + (uint32_t)(a_ > 0.75f) + (uint32_t)(a_ > 1.25f) +
-                    (uint32_t)(a_ > 1.75f) + (uint32_t)(a_ > 2.5f) + (uint32_t)(a_ > 3.5f) + (uint32_t)(a_ > 5.0f);
-    if (q != q) code = 7u;
-    if (q < 0.0f && code > 0u) code |= 8u;
-    packed[e >> 3] |= code << (4 * (e & 7));
-  }
+  uint32_t packed[2], sbyte;
+  quantize_block(w, *gp, saturate != 0, packed, sbyte);
   uint2 outw;
   outw.x = packed[0];
   outw.y = packed[1];
   *reinterpret_cast<uint2*>(pay + slot * pay_stride + h * pay_hs + blk * 8) = outw;
   sf[slot * sf_stride + h * sf_hs + blk] = (uint8_t)sbyte;
+}
+
+// One launch writes every tensor of a KV append into its pool at the rows' slots: grid row k (blockIdx.y) is store k,
+// so its descriptor is uniform over the workgroup (scalar loads); within a store, units of 16 values (row r, head h,
+// block b) are numbered row by row, so consecutive threads read consecutive 32-byte pieces of a row and write its
+// consecutive payload pieces and scale bytes. A store with g == NULL copies its BF16 values.
+constexpr int kMaxStores = 4;
+struct StoreArgs {
+  xt_kv_store st[kMaxStores];
+  int n_stores;
+  int64_t n_rows;
+  const int64_t* slots;
+  int64_t pool_slots;
+  int page_shift;                        // log2(rows per page); 0: token-major
+  int saturate;
+};
+
+constexpr int kStoreUnits = 2;   // units per thread, their loads all in flight before the first use
+
+__global__ __launch_bounds__(256) void store_kv_kernel(const StoreArgs a) {
+  const xt_kv_store& st = a.st[blockIdx.y];
+  const uint32_t blocks = (uint32_t)st.dim / 16u, heads = (uint32_t)st.heads;
+  const int64_t units = a.n_rows * st.heads * blocks;
+  // unit i of this thread: (blockIdx.x * kStoreUnits + i) * 256 + threadIdx.x (< 2^31, checked on the host), so each
+  // of the thread's loads is one of 256 consecutive pieces
+  uint32_t u[kStoreUnits];
+  int64_t slot[kStoreUnits];
+  uint4 lo[kStoreUnits], hi[kStoreUnits];
+#pragma unroll
+  for (int i = 0; i < kStoreUnits; ++i) {
+    u[i] = (blockIdx.x * kStoreUnits + i) * 256u + threadIdx.x;
+    const bool in = (int64_t)u[i] < units;
+    const uint32_t uu = in ? u[i] : 0u;
+    const uint32_t b = uu % blocks, rh = uu / blocks, h = rh % heads;
+    const int64_t r = rh / heads;
+    slot[i] = in ? a.slots[r] : -1;
+    const uint16_t* src = static_cast<const uint16_t*>(st.src) + r * st.src_row_stride + h * st.src_head_stride + 16 * b;
+    lo[i] = reinterpret_cast<const uint4*>(src)[0];
+    hi[i] = reinterpret_cast<const uint4*>(src)[1];
+  }
+  // the global scale (written by an earlier launch, so a scalar load) joins them; the empty asm takes every load
+  // before the slot tests, so none is sunk below a test
+  int32_t gbits = st.g ? uniform_load(reinterpret_cast<const int32_t*>(st.g)) : 0;
+#pragma unroll
+  for (int i = 0; i < kStoreUnits; ++i)
+    asm volatile("" : "+v"(slot[i]), "+v"(lo[i].x), "+v"(lo[i].y), "+v"(lo[i].z), "+v"(lo[i].w), "+v"(hi[i].x),
+                 "+v"(hi[i].y), "+v"(hi[i].z), "+v"(hi[i].w));
+  asm volatile("" : "+s"(gbits));
+  const float g = __int_as_float(gbits);
+#pragma unroll
+  for (int i = 0; i < kStoreUnits; ++i) {
+    if (slot[i] < 0 || slot[i] >= a.pool_slots) continue;
+    const uint32_t b = u[i] % blocks, rh = u[i] / blocks, h = rh % heads;
+    const int64_t page = slot[i] >> a.page_shift, prow = slot[i] & ((1ll << a.page_shift) - 1);
+    uint8_t* pay = st.pay + page * st.pay_page_stride + prow * st.pay_row_stride + (int64_t)h * st.pay_head_stride;
+    if (st.g == nullptr) {   // a plain copy of the BF16 values
+      reinterpret_cast<uint4*>(pay + 32 * b)[0] = lo[i];
+      reinterpret_cast<uint4*>(pay + 32 * b)[1] = hi[i];
+      continue;
+    }
+    const uint32_t w[8] = {lo[i].x, lo[i].y, lo[i].z, lo[i].w, hi[i].x, hi[i].y, hi[i].z, hi[i].w};
+    uint32_t packed[2], sbyte;
+    quantize_block(w, g, a.saturate != 0, packed, sbyte);
+    *reinterpret_cast<uint2*>(pay + 8 * b) = make_uint2(packed[0], packed[1]);
+    st.scales[page * st.sf_page_stride + prow * st.sf_row_stride + (int64_t)h * st.sf_head_stride + b] =
+        (uint8_t)sbyte;
+  }
 }
 
 int check_src(const char* what, const void* src, int64_t n_rows, int heads, int dim, int64_t rs, int64_t hs) {
@@ -165,5 +288,54 @@ extern "C" int xt_nvfp4_quantize_append(const void* src, int64_t n_rows, int hea
                      reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t*>(src), n_rows, heads, dim,
                      src_row_stride, src_head_stride, slots, g, pay, scales, pool_slots, pay_stride, sf_stride,
                      pay_head_stride, sf_head_stride, saturate);
+  return check_launch(what);
+}
+
+extern "C" int xt_nvfp4_store_kv(const xt_kv_store* stores, int n_stores, int64_t n_rows, const int64_t* slots,
+                                 int64_t pool_slots, int page_size, int saturate, xt_stream_t stream) {
+  const char* what = "xt_nvfp4_store_kv";
+  if (!stores || n_stores < 1 || n_stores > kMaxStores)
+    return fail(XT_EINVAL, "%s: 1 to %d stores expected, got %d", what, kMaxStores, n_stores);
+  if (n_rows < 0 || page_size <= 0 || (page_size & (page_size - 1)) || pool_slots <= 0)
+    return fail(XT_EINVAL, "%s: n_rows %lld, page_size %d (a power of 2), pool_slots %lld", what, (long long)n_rows,
+                page_size, (long long)pool_slots);
+  if (n_rows == 0) return ok();
+  if (!slots) return fail(XT_EINVAL, "%s: slots is null", what);
+  StoreArgs a;
+  a.n_stores = n_stores;
+  a.n_rows = n_rows;
+  a.slots = slots;
+  a.pool_slots = pool_slots;
+  a.page_shift = __builtin_ctz((unsigned)page_size);
+  a.saturate = saturate;
+  int64_t most = 0;   // units of the largest store
+  for (int k = 0; k < kMaxStores; ++k) {
+    if (k >= n_stores) {
+      a.st[k] = stores[0];
+      continue;
+    }
+    const xt_kv_store& st = stores[k];
+    if (int e = check_src(what, st.src, n_rows, st.heads, st.dim, st.src_row_stride, st.src_head_stride)) return e;
+    const bool copy = st.g == nullptr;
+    const int64_t row_bytes = copy ? 2 * st.dim : st.dim / 2;
+    if (!st.pay || (!copy && !st.scales))
+      return fail(XT_EINVAL, "%s: store %d: a payload%s pointer is required", what, k, copy ? "" : " and a scale");
+    if (!aligned(st.pay, copy ? 16 : 8) || st.pay_page_stride % 8 || st.pay_row_stride % 8 || st.pay_head_stride % 8 ||
+        (copy && (st.pay_page_stride % 16 || st.pay_row_stride % 16 || st.pay_head_stride % 16)))
+      return fail(XT_EINVAL, "%s: store %d: payload address and strides must be multiples of %d bytes", what, k,
+                  copy ? 16 : 8);
+    if (st.pay_page_stride < 0 || st.pay_row_stride < 0 || st.pay_head_stride < 0 || st.sf_page_stride < 0 ||
+        st.sf_row_stride < 0 || st.sf_head_stride < 0 ||
+        (st.heads > 1 && st.pay_head_stride < row_bytes) ||
+        (!copy && st.heads > 1 && st.sf_head_stride < st.dim / 16))
+      return fail(XT_EINVAL, "%s: store %d: strides must be non-negative and keep the heads' rows apart", what, k);
+    a.st[k] = st;
+    most = std::max<int64_t>(most, n_rows * st.heads * (st.dim / 16));
+  }
+  if (most > 0x7FFFF000LL) return fail(XT_EUNSUPPORTED, "%s: %lld rows is too many for one launch", what,
+                                       (long long)n_rows);
+  const int64_t blocks = (most + 256 * kStoreUnits - 1) / (256 * kStoreUnits);
+  hipLaunchKernelGGL(store_kv_kernel, dim3((unsigned)blocks, (unsigned)n_stores), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), a);
   return check_launch(what);
 }

@@ -9,6 +9,9 @@ here, any other call goes to ``original`` untouched.
 What an NVFP4 call must satisfy: the pool is written with outer scales of 1, so a ``k_scale`` / ``v_scale`` other than
 1 is a ValueError; these kernels have no attention sink and no HiSparse slot lists (NotImplementedError).
 
+The KV store: ``enable_fused_store`` (kv_fp4.py:546-559) turns on the pool's fused store, and the hook on SGLang's
+``nvfp4_store_kv_index`` runs it as one launch of this library's store (main K, V and index K).
+
 The prefill entry: while BF16 copies of every request's context (main K, V and index K) fit in
 ``XTIER_MINIMAX_FP4_PREFILL_GB`` GiB (default 1.5), ``dequantize_context`` makes them and ``original`` runs SGLang's
 BF16 kernels on the copies through a request-local token table; beyond that ``original`` gets the NVFP4 views and
@@ -117,12 +120,42 @@ def sparse_prefill(original, q, k_cache, v_cache, sink, idx_q, idx_k_cache, idx_
                     cu_seqlens, seq_lens, prefix_lens, max_seqlen_q, max_seqlen_k, *args, **kwargs)
 
 
-HOOKS = (('flash_decode_with_gqa_share_sparse', decode_main),
-         ('flash_prefill_with_gqa_share_sparse', prefill_main),
-         ('minimax_sparse_prefill', sparse_prefill))
+STORE = 'sglang.kernels.ops.kvcache.nvfp4_store_kv_index.nvfp4_store_kv_index'
+
+
+def store_kv_index(original, k, v, ik, kpay, ksc, vpay, vsc, ipay, isc, loc, global_scale, page_size=PAGE,
+                   **kwargs):
+    """AROUND SGLang's fused MiniMax NVFP4 store (called as tests/minimax_kv_fp4_check.py:173 calls it): main K, V
+    and index K quantized into their head-major pages in one launch of this library's store, ``original`` for
+    anything else (CPU tensors, extra options)."""
+    if kwargs or not (torch.is_tensor(k) and k.is_cuda):
+        return original(k, v, ik, kpay, ksc, vpay, vsc, ipay, isc, loc, global_scale, page_size=page_size, **kwargs)
+    ops.nvfp4_store_kv_index(k, v, ik, kpay, ksc, vpay, vsc, ipay, isc, loc, global_scale, page_size=page_size)
+
+
+def enable_fused_store(pool):
+    """kv_fp4.py:546-559: the pool writes K, V and the index K through the one-launch store (the hook above) instead
+    of quantizing each buffer and scattering it. Taken when not disabled (XTIER_MINIMAX_FP4_FUSED_STORE=0), not
+    already on, and the main and index pools share head size, page size and global scale. Returns whether it is on."""
+    main, index = pool.main_pool, pool.index_k_pool
+    if os.environ.get('XTIER_MINIMAX_FP4_FUSED_STORE', '1') == '0':
+        return bool(pool.use_nvfp4_fused_quantize_store)
+    compatible = (main.head_dim == index.INDEX_HEAD_DIM and main.page_size == index.page_size
+                  and torch.equal(main.global_scale, index.global_scale))
+    if compatible and not pool.use_nvfp4_fused_quantize_store:
+        pool.use_nvfp4_fused_quantize_store = True
+        logger.info('xtier_amd: MiniMax NVFP4 KV store through the one-launch K / V / index K store')
+    return bool(pool.use_nvfp4_fused_quantize_store)
+
+
+HOOKS = ((f'{OPS}.flash_decode_with_gqa_share_sparse', decode_main),
+         (f'{OPS}.flash_prefill_with_gqa_share_sparse', prefill_main),
+         (f'{OPS}.minimax_sparse_prefill', sparse_prefill),
+         (STORE, store_kv_index))
 
 
 def install(registry, hook_type):
-    """Registers every hook of HOOKS AROUND its op of SGLang's generic MiniMax path (kv_fp4.py:632-638)."""
+    """Registers every hook of HOOKS AROUND its target: SGLang's generic MiniMax sparse ops (kv_fp4.py:632-638) and
+    its fused NVFP4 store."""
     for target, hook in HOOKS:
-        registry.register(f'{OPS}.{target}', hook, hook_type.AROUND)
+        registry.register(target, hook, hook_type.AROUND)

@@ -33,13 +33,32 @@ def _need_cuda(*tensors):
             raise ValueError('xtier_amd: GPU tensors expected')
 
 
+def _check_fp8_raw(raw):
+    """An FP8 pool's raw tuple (k, v, None, None, None, None) (qsa_fp4.py:43-58, :165-171): E4M3 bytes [m, heads,
+    dim] with a power-of-2 head size, contiguous."""
+    k, v = raw[0], raw[1]
+    dim = k.shape[2]
+    if not (k.is_contiguous() and v.is_contiguous() and k.shape == v.shape and dim % 32 == 0
+            and dim & (dim - 1) == 0):
+        raise ValueError(f'xtier qsa_fp4: packed [m, heads, dim] FP8 rows with a power-of-2 head size expected, got '
+                         f'{tuple(k.shape)}')
+    k, v = (t if t.dtype == torch.uint8 else t.view(torch.uint8) for t in (k, v))
+    _need_cuda(k, v)
+    return (k, v, None, None, None, None), k.shape[1], dim
+
+
+def is_fp8_raw(raw):
+    """True for an FP8 pool's raw tuple (no block scales)."""
+    return raw[2] is None
+
+
 def _check_raw(raw, contiguous=True):
     """The reference's _check (qsa_fp4.py:165-171): packed [m, heads, dim/2] rows with a power-of-2 head size.
     contiguous=False also admits pools whose slots and heads are strided (the interleaved layout of KVPool): each head
     row contiguous, the slot and head strides the same for K and V."""
     k, v, k_sf, v_sf, gk, gv = raw
     if k_sf is None:
-        raise NotImplementedError('xtier_amd: FP8 pools are not covered; NVFP4 pools only')
+        raise NotImplementedError('xtier_amd: the fused attention reads NVFP4 pools; an FP8 pool takes the gather')
     dim = k.shape[2] * 2
     if contiguous:
         packed = k.is_contiguous() and v.is_contiguous() and k_sf.is_contiguous() and v_sf.is_contiguous()
@@ -128,6 +147,71 @@ def quantize_append(x, slots, g, pay, scales, saturate=True):
         'quantize_append')
 
 
+def _pool_strides(view, heads, page_size):
+    """(page, row, head) byte strides and rows per page of one tensor's pool view: token-major [slots, heads, width]
+    or [slots, width] (page_size 1); head-major pages [pages, heads, page, width]; one-head pages [pages, page, width]
+    (page_size > 1)."""
+    es = view.element_size()
+    if view.dim() == 4:
+        return view.stride(0) * es, view.stride(2) * es, view.stride(1) * es, view.shape[2]
+    if page_size > 1 and view.dim() == 3:
+        return view.stride(0) * es, view.stride(1) * es, 0, view.shape[1]
+    return view.stride(0) * es, 0, (view.stride(1) * es if view.dim() == 3 and heads > 1 else 0), 1
+
+
+def store_kv(stores, slots, page_size=1, saturate=True):
+    """The fused KV-write epilogue: every store of ``stores`` written at ``slots`` [n] (int64; negative: skipped) in
+    one launch. A store is (x, g, pay, scales): x BF16 [n, heads, dim] (or [n, dim]); g the device global scale
+    [1] and pay / scales the pool's uint8 payload / scale views (token-major [slots, heads, width] with page_size 1,
+    head-major pages [pages, heads, page, width], or one-head pages [pages, page, width]); or g None for a plain BF16
+    copy into pay (the rope rows of a latent cache), scales None. Bytes equal one quantize_append per store."""
+    if not 1 <= len(stores) <= 4:
+        raise ValueError('xtier_amd.store_kv: 1 to 4 stores')
+    descs, keep = [], []
+    n = None
+    pool_slots = None
+    for x, g, pay, sc in stores:
+        x3 = x if x.dim() == 3 else x.unsqueeze(1)
+        if x3.dtype != torch.bfloat16 or x3.stride(-1) != 1:
+            raise ValueError(f'xtier_amd.store_kv: BF16 rows with a contiguous last dim expected, got {x.dtype}')
+        _need_cuda(x3, g, pay, sc, slots)
+        n = x3.shape[0] if n is None else n
+        if x3.shape[0] != n:
+            raise ValueError('xtier_amd.store_kv: every store takes the same rows')
+        heads, dim = x3.shape[1], x3.shape[2]
+        pp, pr, ph, page = _pool_strides(pay, heads, page_size)
+        sp = sr = sh = 0
+        if g is not None:
+            if pay.dtype != torch.uint8 or sc.dtype != torch.uint8:
+                pay, sc = pay.view(torch.uint8), sc.view(torch.uint8)
+            sp, sr, sh, _ = _pool_strides(sc, heads, page_size)
+            g = g if g.dtype == torch.float32 else g.float()
+        if page != page_size:
+            raise ValueError(f'xtier_amd.store_kv: pages of {page} rows, page_size {page_size}')
+        slots_here = pay.shape[0] * page
+        pool_slots = slots_here if pool_slots is None else min(pool_slots, slots_here)
+        descs.append(_lib.KvStore(_ptr(x3), x3.stride(0), x3.stride(1), heads, dim, _ptr(g), _ptr(pay), _ptr(sc),
+                                  pp, pr, ph, sp, sr, sh))
+        keep.append((x3, g, pay, sc))
+    if slots.dtype != torch.int64:
+        slots = slots.to(torch.int64)
+    slots = slots.contiguous()
+    arr = (_lib.KvStore * len(descs))(*descs)
+    _lib.check(_lib.lib().xt_nvfp4_store_kv(arr, len(descs), n, _ptr(slots), pool_slots, int(page_size),
+                                            1 if saturate else 0, _stream(slots)), 'store_kv')
+
+
+def nvfp4_store_kv_index(k, v, ik, kpay, ksc, vpay, vsc, ipay, isc, loc, global_scale, page_size=128):
+    """SGLang's fused MiniMax NVFP4 store as tests/minimax_kv_fp4_check.py:152-175 calls it (enabled by the pack at
+    xtier/packs/minimax_m3/kv_fp4.py:546-559): main K and V [n, heads, dim] and index K [n, dim] quantized with the
+    pool's global scale into head-major pages (kpay / vpay [pages, heads, page_size, dim/2], ksc / vsc [.., dim/16];
+    ipay / isc [pages, page_size, dim/2 | dim/16]) at token slots loc [n], in one launch. The E4M3 conversion
+    saturates (a scale byte is never NaN), as a store into a serving cache must."""
+    g = global_scale if torch.is_tensor(global_scale) else torch.tensor([float(global_scale)], device=k.device)
+    g = g.reshape(1)
+    store_kv([(k, g, kpay, ksc), (v, g, vpay, vsc), (ik, g, ipay, isc)], loc, page_size=page_size)
+
+
 def nvfp4_encode(x, saturate=False):
     """formats.py:114-128 on the GPU for a BF16 tensor [slots, heads, dim] (or [rows, dim]): (payload u8
     [..., dim/2], scale bytes u8 [..., dim/16], g f32 [1])."""
@@ -147,31 +231,60 @@ def nvfp4_encode(x, saturate=False):
 
 def gather(raw, req_to_token, req_indices, indices, seq_lens, cu_k, out_k, out_v, batch, topk, zero_fill_cols=0):
     """qsa_fp4.gather (qsa_fp4.py:174-180): the decode/verify rows of ``indices`` dequantized into out_k / out_v
-    (compact, or page-aligned and zero-filled up to zero_fill_cols)."""
-    raw, heads, dim = _check_raw(raw)
+    (compact, or page-aligned and zero-filled up to zero_fill_cols), from an NVFP4 pool or an FP8 one
+    (raw = (k, v, None, None, None, None))."""
+    fp8 = is_fp8_raw(raw)
+    raw, heads, dim = _check_fp8_raw(raw) if fp8 else _check_raw(raw)
     if out_k.dtype not in _DTYPES or not out_k.is_contiguous() or not out_v.is_contiguous():
         raise ValueError('xtier_amd.gather: contiguous BF16/FP16 outputs expected')
     _need_cuda(req_to_token, req_indices, indices, seq_lens, cu_k, out_k, out_v)
     req_indices = req_indices.to(torch.int64) if req_indices.dtype != torch.int64 else req_indices
-    _lib.check(_lib.lib().xt_qsa_gather_nvfp4(
-        *map(_ptr, raw), raw[0].shape[0], heads, dim, _ptr(req_to_token), req_to_token.stride(0),
-        _ptr(req_indices.contiguous()), _ptr(indices), indices.stride(0), _ptr(seq_lens), _ptr(cu_k), _ptr(out_k),
-        _ptr(out_v), _DTYPES[out_k.dtype], int(batch), int(topk), int(zero_fill_cols), _stream(out_k)), 'gather')
+    tail = (_ptr(req_to_token), req_to_token.stride(0), _ptr(req_indices.contiguous()), _ptr(indices),
+            indices.stride(0), _ptr(seq_lens), _ptr(cu_k), _ptr(out_k), _ptr(out_v), _DTYPES[out_k.dtype], int(batch),
+            int(topk), int(zero_fill_cols), _stream(out_k))
+    if fp8:
+        st = _lib.lib().xt_qsa_gather_fp8(_ptr(raw[0]), _ptr(raw[1]), raw[0].shape[0], heads, dim, *tail)
+    else:
+        st = _lib.lib().xt_qsa_gather_nvfp4(*map(_ptr, raw), raw[0].shape[0], heads, dim, *tail)
+    _lib.check(st, 'gather')
 
 
 def pack(raw, req_to_token, req_indices, cu_k, total_k, max_k, output_dtype):
-    """qsa_fp4.pack (qsa_fp4.py:183-192): whole prefixes as (packed_k, packed_v) [total_k, heads, dim]."""
-    raw, heads, dim = _check_raw(raw)
+    """qsa_fp4.pack (qsa_fp4.py:183-192): whole prefixes as (packed_k, packed_v) [total_k, heads, dim], from an NVFP4
+    or an FP8 pool."""
+    fp8 = is_fp8_raw(raw)
+    raw, heads, dim = _check_fp8_raw(raw) if fp8 else _check_raw(raw)
     device = raw[0].device
     packed_k = torch.empty((total_k, heads, dim), dtype=output_dtype, device=device)
     packed_v = torch.empty((total_k, heads, dim), dtype=output_dtype, device=device)
     batch = req_indices.numel()
     req_indices = req_indices.to(torch.int64).contiguous()
-    _lib.check(_lib.lib().xt_qsa_pack_nvfp4(
-        *map(_ptr, raw), raw[0].shape[0], heads, dim, _ptr(req_to_token), req_to_token.stride(0),
-        req_to_token.stride(1), _ptr(req_indices), batch, _ptr(cu_k), int(max_k), _ptr(packed_k), _ptr(packed_v),
-        _DTYPES[output_dtype], _stream(packed_k)), 'pack')
+    tail = (_ptr(req_to_token), req_to_token.stride(0), req_to_token.stride(1), _ptr(req_indices), batch, _ptr(cu_k),
+            int(max_k), _ptr(packed_k), _ptr(packed_v), _DTYPES[output_dtype], _stream(packed_k))
+    if fp8:
+        st = _lib.lib().xt_qsa_pack_fp8(_ptr(raw[0]), _ptr(raw[1]), raw[0].shape[0], heads, dim, *tail)
+    else:
+        st = _lib.lib().xt_qsa_pack_nvfp4(*map(_ptr, raw), raw[0].shape[0], heads, dim, *tail)
+    _lib.check(st, 'pack')
     return packed_k, packed_v
+
+
+def valid_counts(seq_lens, indices, valid=None, cu_seqlens_k=None):
+    """(valid_counts [batch] int32, cu_seqlens_k [batch + 1] int32) of top-k lists indices [batch, topk]: the number of
+    entries with 0 <= index < seq_lens[b] and their running sum (SGLang's qwen_sparse_fa2_cu_seqlens_triton as
+    qsa_fp4.py:255-256 uses it; valid entries first, -1 padding after)."""
+    batch, topk = indices.shape
+    _need_cuda(seq_lens, indices)
+    indices = indices if indices.dtype == torch.int32 and indices.stride(1) == 1 else \
+        indices.to(torch.int32).contiguous()
+    seq_lens = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
+    if valid is None:
+        valid = torch.empty(batch, dtype=torch.int32, device=indices.device)
+    if cu_seqlens_k is None:
+        cu_seqlens_k = torch.empty(batch + 1, dtype=torch.int32, device=indices.device)
+    _lib.check(_lib.lib().xt_qsa_valid_counts(_ptr(seq_lens), _ptr(indices), indices.stride(0), batch, topk,
+                                              _ptr(valid), _ptr(cu_seqlens_k), _stream(indices)), 'valid_counts')
+    return valid, cu_seqlens_k
 
 
 # --- fused sparse attention ---------------------------------------------------------------------------------------

@@ -55,9 +55,9 @@ class KVPool:
         ops.global_scale(v, out=self.gv)
 
     def append(self, k, v, slots, saturate=True):
-        """NVFP4 quantize-on-append of K and V rows [n, kv_heads, dim] (BF16) at pool slots [n]."""
-        ops.quantize_append(k, slots, self.gk, self.k_pay, self.k_sf, saturate=saturate)
-        ops.quantize_append(v, slots, self.gv, self.v_pay, self.v_sf, saturate=saturate)
+        """NVFP4 quantize-on-append of K and V rows [n, kv_heads, dim] (BF16) at pool slots [n], in one launch."""
+        ops.store_kv([(k, self.gk, self.k_pay, self.k_sf), (v, self.gv, self.v_pay, self.v_sf)], slots,
+                     saturate=saturate)
 
 
 class LatentPool:
@@ -95,7 +95,7 @@ class LatentPool:
         self.g = ops.global_scale(latent.reshape(latent.shape[0], 1, -1))
 
     def append(self, latent, rope, slots, saturate=True):
-        """Quantize BF16 latent rows [n, latent_dim] with the pool's g into `slots` and copy their rope rows."""
-        ops.quantize_append(latent.reshape(latent.shape[0], 1, -1), slots, self.g, self.pay.unsqueeze(1),
-                            self.scales.unsqueeze(1), saturate=saturate)
-        self.rope.index_copy_(0, slots, rope.to(torch.bfloat16))
+        """Quantize BF16 latent rows [n, latent_dim] with the pool's g into `slots` and copy their rope rows, in one
+        launch."""
+        ops.store_kv([(latent, self.g, self.pay, self.scales), (rope.to(torch.bfloat16), None, self.rope, None)], slots,
+                     saturate=saturate)
