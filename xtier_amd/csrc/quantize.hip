@@ -99,15 +99,37 @@ __device__ inline uint32_t e2m1_code_div(float x, float d) {
   return code;
 }
 
+// Two E2M1 codes at once from one dword of two BF16 values. Every source value is a BF16, and a BF16 value exceeds a
+// real T exactly when it exceeds T rounded toward -inf to BF16, so the thresholds are taken as BF16 bit patterns
+// (the FP32 ones truncated: rounding down twice is rounding down once) and the search of e2m1_code runs on both 16-bit
+// halves with packed 16-bit integer arithmetic. Returns the byte of the two codes (first value in the low nibble).
+typedef short short2v __attribute__((ext_vector_type(2)));
+__device__ inline short2v pk_above(short2v t, short2v a) {   // per half: -1 where a > t, else 0
+  return (t - a) >> (short)15;
+}
+__device__ inline uint32_t as_u32(short2v v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ inline short2v as_s2(uint32_t v) { return __builtin_bit_cast(short2v, v); }
+
+__device__ inline uint32_t e2m1_pair(uint32_t w, const uint32_t (&t2)[7]) {
+  const short2v a = as_s2(w & 0x7FFF7FFFu);
+  const uint32_t m4 = as_u32(pk_above(as_s2(t2[3]), a));
+  const uint32_t m2 = as_u32(pk_above(as_s2((m4 & t2[5]) | (~m4 & t2[1])), a));
+  const uint32_t hi = (m2 & t2[6]) | (~m2 & t2[4]), lo = (m2 & t2[2]) | (~m2 & t2[0]);
+  const uint32_t m1 = as_u32(pk_above(as_s2((m4 & hi) | (~m4 & lo)), a));
+  const uint32_t code = (m4 & 0x00040004u) | (m2 & 0x00020002u) | (m1 & 0x00010001u);
+  // the sign with a code above 0 when the value is negative and not a NaN (a NaN half exceeds 0x7F80)
+  const uint32_t nan = as_u32(pk_above(as_s2(0x7F807F80u), a));
+  const uint32_t sign = (w >> 12) & 0x00080008u & ~nan & (m4 | m2 | m1);
+  const uint32_t c = code | sign;
+  return (c & 0xFu) | ((c >> 12) & 0xF0u);
+}
+
 // 16 BF16 values (eight dwords) -> eight payload bytes (two dwords) and the E4M3 scale byte, with global scale g.
 __device__ inline void quantize_block(const uint32_t (&w)[8], float g, bool saturate, uint32_t (&packed)[2],
                                       uint32_t& sbyte) {
   uint32_t amax_bits = 0;
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    amax_bits = max(amax_bits, w[k] & 0x7FFFu);
-    amax_bits = max(amax_bits, (w[k] >> 16) & 0x7FFFu);
-  }
+  for (int k = 0; k < 8; ++k) amax_bits = max(amax_bits, max(w[k] & 0x7FFFu, (w[k] >> 16) & 0x7FFFu));
   const float bamax = bf16_bits_to_f32(amax_bits);
   sbyte = e4m3_encode(bamax / (6.0f * g), saturate);
   float d = e4m3_decode(sbyte) * g;
@@ -115,11 +137,14 @@ __device__ inline void quantize_block(const uint32_t (&w)[8], float g, bool satu
   packed[0] = packed[1] = 0u;
   if (__builtin_isfinite(d)) {
     const Thresholds th = block_thresholds(d);
+    uint32_t t2[7];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const float x = bf16_bits_to_f32(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu);
-      packed[e >> 3] |= e2m1_code(x, th) << (4 * (e & 7));
+    for (int i = 0; i < 7; ++i) {
+      const uint32_t tb = __float_as_uint(th.t[i]) >> 16;   // toward -inf to BF16 (positive: truncation)
+      t2[i] = tb | (tb << 16);
     }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) packed[k >> 2] |= e2m1_pair(w[k], t2) << (8 * (k & 3));
   } else {
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
@@ -165,6 +190,8 @@ __global__ void quantize_append_kernel(const uint16_t* __restrict__ src, int64_t
 constexpr int kMaxStores = 4;
 struct StoreArgs {
   xt_kv_store st[kMaxStores];
+  uint64_t head_magic[kMaxStores];       // ceil(2^40 / heads): n / heads = (n * magic) >> 40 for every n < 2^31
+  int block_shift[kMaxStores];           // log2(dim / 16)
   int n_stores;
   int64_t n_rows;
   const int64_t* slots;
@@ -173,26 +200,29 @@ struct StoreArgs {
   int saturate;
 };
 
-constexpr int kStoreUnits = 2;   // units per thread, their loads all in flight before the first use
+constexpr int kStoreUnits = 2;   // 16-value units per thread, their loads all in flight before the first use
 
+// Unit i of a thread is (blockIdx.x * kStoreUnits + i) * 256 + threadIdx.x: one 16-value block (32 source bytes, 8
+// payload bytes, a scale byte), consecutive threads taking consecutive blocks of a row.
 __global__ __launch_bounds__(256) void store_kv_kernel(const StoreArgs a) {
   const xt_kv_store& st = a.st[blockIdx.y];
-  const uint32_t blocks = (uint32_t)st.dim / 16u, heads = (uint32_t)st.heads;
-  const int64_t units = a.n_rows * st.heads * blocks;
-  // unit i of this thread: (blockIdx.x * kStoreUnits + i) * 256 + threadIdx.x (< 2^31, checked on the host), so each
-  // of the thread's loads is one of 256 consecutive pieces
+  const int bs = a.block_shift[blockIdx.y];
+  const uint64_t magic = a.head_magic[blockIdx.y];
+  const uint32_t heads = (uint32_t)st.heads;
+  const int64_t units = (a.n_rows * st.heads) << bs;
   uint32_t u[kStoreUnits];
   int64_t slot[kStoreUnits];
   uint4 lo[kStoreUnits], hi[kStoreUnits];
 #pragma unroll
   for (int i = 0; i < kStoreUnits; ++i) {
-    u[i] = (blockIdx.x * kStoreUnits + i) * 256u + threadIdx.x;
+    u[i] = (blockIdx.x * kStoreUnits + i) * 256u + threadIdx.x;   // < 2^31, checked on the host
     const bool in = (int64_t)u[i] < units;
     const uint32_t uu = in ? u[i] : 0u;
-    const uint32_t b = uu % blocks, rh = uu / blocks, h = rh % heads;
-    const int64_t r = rh / heads;
+    const uint32_t b = uu & ((1u << bs) - 1), rh = uu >> bs;
+    const uint32_t r = (uint32_t)(((uint64_t)rh * magic) >> 40), h = rh - r * heads;
     slot[i] = in ? a.slots[r] : -1;
-    const uint16_t* src = static_cast<const uint16_t*>(st.src) + r * st.src_row_stride + h * st.src_head_stride + 16 * b;
+    const uint16_t* src =
+        static_cast<const uint16_t*>(st.src) + (int64_t)r * st.src_row_stride + (int64_t)h * st.src_head_stride + 16 * b;
     lo[i] = reinterpret_cast<const uint4*>(src)[0];
     hi[i] = reinterpret_cast<const uint4*>(src)[1];
   }
@@ -208,7 +238,8 @@ __global__ __launch_bounds__(256) void store_kv_kernel(const StoreArgs a) {
 #pragma unroll
   for (int i = 0; i < kStoreUnits; ++i) {
     if (slot[i] < 0 || slot[i] >= a.pool_slots) continue;
-    const uint32_t b = u[i] % blocks, rh = u[i] / blocks, h = rh % heads;
+    const uint32_t b = u[i] & ((1u << bs) - 1), rh = u[i] >> bs;
+    const uint32_t h = rh - (uint32_t)(((uint64_t)rh * magic) >> 40) * heads;
     const int64_t page = slot[i] >> a.page_shift, prow = slot[i] & ((1ll << a.page_shift) - 1);
     uint8_t* pay = st.pay + page * st.pay_page_stride + prow * st.pay_row_stride + (int64_t)h * st.pay_head_stride;
     if (st.g == nullptr) {   // a plain copy of the BF16 values
@@ -308,14 +339,19 @@ extern "C" int xt_nvfp4_store_kv(const xt_kv_store* stores, int n_stores, int64_
   a.pool_slots = pool_slots;
   a.page_shift = __builtin_ctz((unsigned)page_size);
   a.saturate = saturate;
-  int64_t most = 0;   // units of the largest store
+  int64_t most = 0;   // 16-value units of the largest store
   for (int k = 0; k < kMaxStores; ++k) {
     if (k >= n_stores) {
       a.st[k] = stores[0];
+      a.head_magic[k] = 1ull << 40;
+      a.block_shift[k] = 0;
       continue;
     }
     const xt_kv_store& st = stores[k];
     if (int e = check_src(what, st.src, n_rows, st.heads, st.dim, st.src_row_stride, st.src_head_stride)) return e;
+    if ((st.dim / 16) & (st.dim / 16 - 1) || st.heads > 512)
+      return fail(XT_EINVAL, "%s: store %d: dim %d (dim / 16 must be a power of 2), heads %d (at most 512)", what, k,
+                  st.dim, st.heads);
     const bool copy = st.g == nullptr;
     const int64_t row_bytes = copy ? 2 * st.dim : st.dim / 2;
     if (!st.pay || (!copy && !st.scales))
@@ -330,6 +366,8 @@ extern "C" int xt_nvfp4_store_kv(const xt_kv_store* stores, int n_stores, int64_
         (!copy && st.heads > 1 && st.sf_head_stride < st.dim / 16))
       return fail(XT_EINVAL, "%s: store %d: strides must be non-negative and keep the heads' rows apart", what, k);
     a.st[k] = st;
+    a.head_magic[k] = ((1ull << 40) + (uint64_t)st.heads - 1) / (uint64_t)st.heads;
+    a.block_shift[k] = __builtin_ctz((unsigned)(st.dim / 16));
     most = std::max<int64_t>(most, n_rows * st.heads * (st.dim / 16));
   }
   if (most > 0x7FFFF000LL) return fail(XT_EUNSUPPORTED, "%s: %lld rows is too many for one launch", what,
