@@ -709,6 +709,69 @@ def varlen_cpu(q, kv, w, scale, seconds):
                        'numpy split-K softmax attention with FP64 merge')
 
 
+CEILING_WORKLOADS = ('mfma_ceiling', 'gather_ceiling_b32')
+
+
+def run_ceiling(args, name, ops, workloads):
+    """The ceilings the roofline fractions are read against (xt_ceiling_mfma / xt_ceiling_gather): the sustained dense
+    MFMA rate, and the batch-32 decode's exact gather (batch 32, context 32768, top-2048, pages of 64, 576-byte
+    interleaved records, 16 rotated pools) with no dequantization or math."""
+    import torch
+    torch.cuda.set_device(0)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    steps = max(1, args.steps)
+    if name == 'mfma_ceiling':
+        blocks, iters = 4 * cus, 2000
+
+        def step(_):
+            ops.ceiling_mfma(iters, blocks)
+
+        ms, per = time_steps(step, 1, steps, max(1, args.warmup))
+        check = ops.ceiling_mfma(iters, blocks)
+        assert bool((check == 64.0 * iters).all()), 'xt_ceiling_mfma returned wrong sums'
+        flops = blocks * 4 * iters * 4 * 32 * 32 * 16 * 2
+        tflops = flops / (ms * 1e-3) / 1e12
+        log(f'mfma ceiling: {tflops:.0f} TFLOP/s ({tflops / MFMA_PEAK_TFLOPS:.1%} of {MFMA_PEAK_TFLOPS:.0f})')
+        record = {'metric': 'sustained dense FP16 MFMA TFLOP/s', 'value': round(tflops, 1), 'unit': 'TFLOP/s',
+                  'n_gpus': 1, 'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6),
+                  'timing': spread(per), 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
+                  'dtype': 'f16', 'data': 'synthetic',
+                  'config': {'workload': name, 'workgroups': blocks, 'mfma_per_wave': iters * 4,
+                             'instruction': 'v_mfma_f32_32x32x16_f16'},
+                  'roofline': {'bound': 'mfma', 'achieved': round(tflops, 1), 'peak': MFMA_PEAK_TFLOPS,
+                               'unit': 'TFLOP/s', 'frac': round(tflops / MFMA_PEAK_TFLOPS, 4), 'traffic': None},
+                  'cpu_baseline': None}
+        print(json.dumps(record), flush=True)
+        return
+    w = workloads.WORKLOADS['gqa_decode_b32']
+    gen = workloads.generator('cuda', 20261029)
+    pools = [torch.randint(0, 256, (w.slots, 576), dtype=torch.uint8, device='cuda', generator=gen)
+             for _ in range(args.layers)]
+    pt = workloads.page_table(w.batch, w.ctx, w.page, gen, 'cuda')
+    idx = workloads.index_lists(w.batch, w.ctx, w.topk, gen, 'cuda', w.index_mode)
+    sink = torch.empty(int(ops._lib.lib().xt_ceiling_gather_sink_words(w.batch, w.topk)), dtype=torch.int32,
+                       device='cuda')
+
+    def step(layer):
+        ops.ceiling_gather(pools[layer], pt, idx, w.page, sink=sink)
+
+    ms, per = time_steps(step, args.layers, steps, max(1, args.warmup))
+    nbytes = w.batch * w.topk * 576
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f'gather ceiling: {ms * 1e3:.2f} us per layer-step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of '
+        f'{HBM_PEAK_GBS:.0f})')
+    record = {'metric': 'decode gather pattern alone, GB/s', 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1,
+              'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per),
+              'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'u8', 'data': 'synthetic',
+              'config': {'workload': name, 'batch': w.batch, 'context': w.ctx, 'topk': w.topk, 'page': w.page,
+                         'record_bytes': 576, 'layers_rotated': args.layers},
+              'us_per_layer_step': round(ms * 1e3, 3),
+              'roofline': {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+                           'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None},
+              'cpu_baseline': None}
+    print(json.dumps(record), flush=True)
+
+
 def main():
     p = argparse.ArgumentParser()
     p.add_argument('--gpus', type=int, default=1)
@@ -717,7 +780,8 @@ def main():
     p.add_argument('--workload', default='gqa_decode_b32',
                    help='gqa_decode_b32 (default), cpu_ref_decode, long_ctx_decode_b4, gqa_prefill_chunk4096, '
                         'minimax_decode_b32, minimax_prefill_chunk4096, qsa_varlen_b32, qsa_gather_b32, qsa_pack_ctx65536, '
-                        'mla_decode_b64, mla_prefill_2048 or mla_v4_decode_b64')
+                        'mla_decode_b64, mla_prefill_2048, mla_v4_decode_b64, or the ceilings mfma_ceiling and '
+                        'gather_ceiling_b32')
     p.add_argument('--layers', type=int, default=16)
     p.add_argument('--splits', type=int, default=None)
     p.add_argument('--layout', default='interleaved', choices=['interleaved', 'split'],
@@ -750,6 +814,8 @@ def main():
     from xtier_amd import ops, workloads
     from xtier_amd.pool import KVPool
 
+    if args.workload in CEILING_WORKLOADS:
+        return run_ceiling(args, args.workload, ops, workloads)
     if args.workload in workloads.VARLEN_WORKLOADS:
         return run_varlen(args, workloads.VARLEN_WORKLOADS[args.workload], ops, workloads)
     if args.workload in workloads.BLOCK_WORKLOADS:

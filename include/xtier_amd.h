@@ -354,6 +354,20 @@ int xt_sparse_mla_fp8(const void* q, int64_t q_row_stride, int64_t q_head_stride
 size_t xt_selftest_conversions_bytes(void);
 int xt_selftest_conversions(void* out, xt_stream_t stream);
 
+/* Ceilings, no counterpart in the reference: what this GPU sustains on the two resources the attention kernels are
+ * bound by, for reading their roofline fractions.
+ * xt_ceiling_mfma: `blocks` workgroups of 4 wavefronts, each running `iters` x 4 independent v_mfma_f32_32x32x16_f16
+ * from registers (32768 flops each); out[blocks * 256] receives 64 * iters per thread (a result check).
+ * xt_ceiling_gather: the fused decode's HBM access pattern alone: for each row of `batch` and each of its `topk`
+ * positions (indices int32 [batch, topk]), the slot page_table[row, pos / page_size] * page_size + pos % page_size and
+ * the whole `record_bytes`-byte record of it in `pool` (pool_records records), folded by XOR into one word per thread
+ * of sink (xt_ceiling_gather_sink_words(batch, topk) words). Invalid positions, table entries and slots are skipped. */
+int xt_ceiling_mfma(float* out, int iters, int blocks, xt_stream_t stream);
+int xt_ceiling_gather(const void* pool, int64_t record_bytes, int64_t pool_records, const int32_t* page_table,
+                      int64_t pt_stride, int page_size, int pt_width, const int32_t* indices, int batch, int topk,
+                      uint32_t* sink, xt_stream_t stream);
+size_t xt_ceiling_gather_sink_words(int batch, int topk);
+
 #ifdef __cplusplus
 }
 #endif

@@ -113,8 +113,10 @@ def test_mla_two_lists_empty_and_single_key_rows():
     assert np.all(d <= np.abs(ref[1]) * (2.0 ** -8 + 2.0 ** -10) + 1e-6), d.max()
 
 
-@pytest.mark.parametrize('heads', [64, 16])
+@pytest.mark.parametrize('heads', [100, 72, 64, 16])
 def test_mla_fewer_heads(heads):
+    """Head counts on both sides of the 64-head boundary between the two kernel forms, including waves of 32 heads
+    that are partly or wholly padding."""
     w, inp = _case(31, rows=3, heads=heads)
     pool = _pool(w, 9)
     out, lse = ops.sparse_mla(inp.q, pool, inp.slots, None, None, 0.05)

@@ -725,3 +725,30 @@ def sparse_mla(q, k_cache, indices, topk_length, attn_sink, softmax_scale, extra
             int(splits), _ptr(ws), ws.numel(), _stream(q))
     _lib.check(status, 'sparse_mla')
     return (out.unsqueeze(1), lse.unsqueeze(-1)) if shape4 else (out, lse)
+
+
+def ceiling_mfma(iters, blocks, device='cuda'):
+    """The sustained MFMA rate alone (xt_ceiling_mfma): `blocks` x 4 wavefronts x `iters` x 4 independent
+    v_mfma_f32_32x32x16_f16 (32768 flops each). Returns the per-thread check values, 64 * iters each."""
+    out = torch.empty(int(blocks) * 256, dtype=torch.float32, device=device)
+    _lib.check(_lib.lib().xt_ceiling_mfma(_ptr(out), int(iters), int(blocks), _stream(out)), 'ceiling_mfma')
+    return out
+
+
+def ceiling_gather(pool, page_table, indices, page_size, sink=None):
+    """The fused decode's HBM access pattern alone (xt_ceiling_gather): pool uint8 [records, record_bytes] (one slot
+    record per row, e.g. the interleaved KV pool's 576-byte records), page_table int32 [batch, pages], indices int32
+    [batch, topk] positions. Every listed record is read whole and folded by XOR into one word per thread of the
+    returned sink."""
+    if pool.dtype != torch.uint8 or pool.dim() != 2 or not pool.is_contiguous():
+        raise ValueError('xtier_amd.ceiling_gather: pool must be contiguous uint8 [records, record_bytes]')
+    page_table, indices = page_table.int().contiguous(), indices.int().contiguous()
+    batch, topk = indices.shape
+    words = int(_lib.lib().xt_ceiling_gather_sink_words(batch, topk))
+    if sink is None or sink.numel() < words:
+        sink = torch.empty(max(1, words), dtype=torch.int32, device=pool.device)
+    status = _lib.lib().xt_ceiling_gather(_ptr(pool), pool.shape[1], pool.shape[0], _ptr(page_table),
+                                          page_table.stride(0), int(page_size), page_table.shape[1], _ptr(indices),
+                                          batch, topk, _ptr(sink), _stream(pool))
+    _lib.check(status, 'ceiling_gather')
+    return sink
