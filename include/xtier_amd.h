@@ -346,6 +346,46 @@ int xt_sparse_mla_fp8(const void* q, int64_t q_row_stride, int64_t q_head_stride
                       int64_t out_head_stride, int out_dtype, float* lse, int rows, int splits, void* workspace,
                       size_t workspace_bytes, xt_stream_t stream);
 
+/* --- Top-k producers: the indexer logits and the selection of each query's keys ----------------------------- */
+
+/* Replaces qsa_prefill.qsa_mqa_prefill (xtier/packs/qwen4_exp/qsa_prefill.py:77-102, the kernel at :22-74 and the
+ * mask SGLang applies after it): logits[r, n] = sum_h ReLU(q[r, h, :] . k[n, :]) / score_scale for start[r] <= n <
+ * end[r], -inf elsewhere; FP32 [rows, ld] (columns 0 .. keys - 1 written). q [rows, heads, dim] and k [keys, dim]
+ * (key row stride in elements) are BF16 or FP16 (dtype), products exact and summed in FP32; heads a power of 2 up to
+ * 32, dim 64, 128 or 256; score_scale > 0 (the reference's default is sqrt(dim), applied by the caller). */
+int xt_qsa_indexer_logits(const void* q, int64_t q_row_stride, int64_t q_head_stride, int rows, int heads, int dim,
+                          const void* k, int64_t k_row_stride, int keys, const int32_t* starts, const int32_t* ends,
+                          float score_scale, int dtype, float* logits, int64_t ld, xt_stream_t stream);
+
+/* Replaces indexer_torch.fp8_mqa_logits (xtier/packs/glm5_next/indexer_torch.py:28-45, DeepGEMM's fp8_mqa_logits):
+ * logits[q, n] = sum_h w[q, h] ReLU(q[q, h, :] . k[n, :]) * k_scale[n] for ks[q] <= n < ke[q] (ks / ke may be
+ * NULL: all keys), else 0 (clean_logits 0) or -inf; FP32 [num_q, ld], columns 0 .. num_kv - 1 written. q [num_q,
+ * heads, dim] and k [num_kv, dim] (k_row_stride bytes per key) are FP8 E4M3, products exact in FP32 and summed in
+ * FP32; heads a multiple of 32 up to 128, dim 64, 128 or 256. */
+int xt_dsa_mqa_logits(const void* q, int64_t q_row_stride, int64_t q_head_stride, int num_q, int heads, int dim,
+                      const void* k, int64_t k_row_stride, const float* k_scale, int num_kv, const float* weights,
+                      int64_t w_row_stride, const int32_t* ks, const int32_t* ke, int clean_logits, float* logits,
+                      int64_t ld, xt_stream_t stream);
+
+/* Replaces indexer_torch.fp8_paged_mqa_logits (indexer_torch.py:48-72, DeepGEMM's fp8_paged_mqa_logits; one query
+ * per row): key t of row b is row t % block of page block_table[b, t / block] of the paged cache (num_pages pages
+ * of page_bytes: block x dim E4M3 values, then block FP32 scales); logits [batch, ld] FP32, columns 0 .. max_seq_len
+ * - 1 written, positions at or past context_lens[b], past the table or on a page past the cache 0 / -inf as for
+ * xt_dsa_mqa_logits; a negative table entry reads page 0, as the reference's clamp does. */
+int xt_dsa_paged_mqa_logits(const void* q, int64_t q_row_stride, int64_t q_head_stride, int batch, int heads, int dim,
+                            const void* kvcache, int64_t num_pages, int64_t page_bytes, int block,
+                            const int32_t* block_table,
+                            int64_t bt_stride, int bt_width, const int32_t* context_lens, const float* weights,
+                            int64_t w_row_stride, int max_seq_len, int clean_logits, float* logits, int64_t ld,
+                            xt_stream_t stream);
+
+/* The selection that turns logits into the index lists the attention entry points read (the int32 [batch, topk],
+ * -1 padded format the reference's top-k producers hand to them, e.g. qsa_fp4.py:122 topk_indices): for each row of
+ * x (FP32 [rows, ld], columns 0 .. cols - 1) the positions of the topk largest finite values in ascending order, ties
+ * toward the lower position, -1 after the last (a row with fewer finite values than topk). out int32 [rows, out_ld]. */
+int xt_topk_rows(const float* x, int64_t ld, int rows, int cols, int topk, int32_t* out, int64_t out_ld,
+                 xt_stream_t stream);
+
 /* Self-test, no counterpart in the reference: the known-answer test of the hardware conversions the attention kernels
  * use (E4M3 -> FP16 from either half of a dword, two E2M1 codes -> FP16 / FP32 from each byte position, E4M3 with a
  * power-of-2 scale -> BF16), for every byte, written to `out` (xt_selftest_conversions_bytes() bytes, 16-byte

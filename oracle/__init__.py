@@ -26,4 +26,11 @@ Pinning (what each function is checked against, in ``tests/``):
 - ``attention.dequantize_context``: the NVFP4 dequantizer on each position's slot bytes.
 - ``attention.sparse_mla`` / ``sparse_mla_v4`` / ``v4_keys``: float64 reference with sink and LSE, as
   tests/ds_sparse_mla_check.py:44-67; V4 page decoding against the exact keys of its packing rule.
+- ``topk.topk_rows``: brute force over (value, position) pairs with ties, masks, NaN and +inf; hand-worked ties.
+- ``topk.qsa_indexer_logits``: a torch head loop in float64 and a hand-worked case where ReLU after the head sum
+  would change the answer.
+- ``topk.dsa_mqa_logits``: the reference's einsum formula (indexer_torch.py:28-45) in torch float64 and a scalar loop
+  over one element.
+- ``topk.dsa_paged_mqa_logits``: equal to ``dsa_mqa_logits`` on the keys gathered page by page.
+- ``topk.minimax_block_scores_*``: parity unpinned until their own tests (below) land.
 """

@@ -82,6 +82,16 @@ SIGNATURES = {
     'xt_selftest_conversions_bytes': (_Z, []),
     'xt_selftest_conversions': (_I, [_P, _P]),
     'xt_ceiling_mfma': (_I, [_P, ctypes.c_int, ctypes.c_int, _P]),
+    'xt_qsa_indexer_logits': (_I, [_P, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P,
+                                   ctypes.c_int64, ctypes.c_int, _P, _P, ctypes.c_float, ctypes.c_int, _P,
+                                   ctypes.c_int64, _P]),
+    'xt_dsa_mqa_logits': (_I, [_P, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P,
+                               ctypes.c_int64, _P, ctypes.c_int, _P, ctypes.c_int64, _P, _P, ctypes.c_int, _P,
+                               ctypes.c_int64, _P]),
+    'xt_dsa_paged_mqa_logits': (_I, [_P, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P,
+                                     ctypes.c_int64, ctypes.c_int64, ctypes.c_int, _P, ctypes.c_int64, ctypes.c_int, _P, _P,
+                                     ctypes.c_int64, ctypes.c_int, ctypes.c_int, _P, ctypes.c_int64, _P]),
+    'xt_topk_rows': (_I, [_P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, ctypes.c_int64, _P]),
     'xt_ceiling_gather': (_I, [_P, ctypes.c_int64, ctypes.c_int64, _P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, _P,
                                ctypes.c_int, ctypes.c_int, _P, _P]),
     'xt_ceiling_gather_sink_words': (_Z, [ctypes.c_int, ctypes.c_int]),

@@ -1,0 +1,516 @@
+// The step before the sparse attention: the indexer logits that score every key for each query, and the top-k
+// selection that turns them into the int32 [rows, topk] position lists the attention kernels read.
+//
+//   QSA indexer logits (BF16 / FP16 q and k): logits[r, n] = sum_h ReLU(q[r, h] . k[n]) / score_scale, -inf outside
+//     the row's [start, end). v_mfma_f32_32x32x16_{bf16,f16}: A = 32 keys x 16 dims, B = 16 dims x (32 / H rows x H
+//     heads); ReLU and the head sum on the accumulators (H lanes apart within a row of 16 lanes).
+//   DSA logits (FP8 E4M3 q and k, an FP32 scale per key, FP32 head weights): logits[q, n] = sum_h w[q, h] ReLU(q_h .
+//     k_n) * k_scale[n], outside [ks, ke) 0 or -inf. v_mfma_f32_32x32x16_f16 on the E4M3 values converted exactly to
+//     FP16, with the heads as rows (A = 32 heads x 16 dims of one query, B = 16 dims x 32 keys): a lane then holds 16
+//     heads of one key, so the weighted head sum is 16 FMAs in the lane and one exchange with the lane 32 apart. (The
+//     FP8 MFMA rounds inside its 16-product sum, to about 2^-16 of the sum of magnitudes; the FP16 one sums the exact
+//     products to FP32 accuracy.) Keys come from a flat array or, for decode, from
+//     the paged cache (page = block x D E4M3 values, then block FP32 scales) through the block table.
+//   Top-k rows: per row the positions of the topk largest finite values, ascending (ties toward the lower position),
+//     -1 padded. One workgroup per row: a three-pass radix select (11, 11, 10 bits of an order-preserving key) finds
+//     the topk-th largest key T and how many keys equal to T are taken; one pass in position order writes the
+//     positions, each 1024-position chunk placed by a block-wide prefix count.
+#include "xt_common.h"
+#include "xt_host.h"
+
+namespace xt {
+namespace {
+
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef short short8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+// ---------------------------------------------------------------------------------------------------------------
+// Block-wide prefix counts (1024 threads = 16 wavefronts).
+
+__device__ inline uint32_t wave_exclusive_count(bool flag, uint32_t& wave_total) {
+  const uint64_t bits = __builtin_amdgcn_ballot_w64(flag);
+  wave_total = (uint32_t)__builtin_popcountll(bits);
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(bits >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bits, 0u));
+}
+
+// Exclusive prefix of `flag` over the workgroup in thread order, and the total; `scratch` holds 16 words. Two barriers.
+__device__ inline uint32_t block_exclusive_count(bool flag, uint32_t* scratch, uint32_t& total) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  uint32_t wt;
+  const uint32_t in_wave = wave_exclusive_count(flag, wt);
+  if (lane == 0) scratch[wave] = wt;
+  __syncthreads();
+  uint32_t before = 0, sum = 0;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) {
+    const uint32_t c = scratch[w];
+    before += w < wave ? c : 0u;
+    sum += c;
+  }
+  __syncthreads();   // scratch is reused by the next call
+  total = sum;
+  return before + in_wave;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Top-k rows
+
+__device__ inline bool finite_f32(float f) { return (__float_as_uint(f) & 0x7F800000u) != 0x7F800000u; }
+// Order-preserving key: a larger float has a larger key.
+__device__ inline uint32_t order_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+constexpr int kTopkThreads = 1024;
+
+__global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float* x, int64_t ld, int cols, int topk,
+                                                                   int32_t* out, int64_t out_ld) {
+  __shared__ uint32_t hist[2048];
+  __shared__ uint32_t scratch[16];
+  __shared__ uint32_t sel[2];   // the chosen digit's bucket, the rank left inside it
+  const int tid = threadIdx.x;
+  const float* xr = x + (int64_t)blockIdx.x * ld;
+  int32_t* o = out + (int64_t)blockIdx.x * out_ld;
+
+  uint32_t prefix = 0, pmask = 0, remaining = 0, k = 0;
+  for (int pass = 0; pass < 3; ++pass) {
+    const int shift = pass == 0 ? 21 : pass == 1 ? 10 : 0;
+    const uint32_t dmask = pass == 2 ? 0x3FFu : 0x7FFu;
+    for (int i = tid; i < 2048; i += kTopkThreads) hist[i] = 0;
+    __syncthreads();
+    for (int c = tid; c < cols; c += kTopkThreads) {
+      const float f = xr[c];
+      const uint32_t key = order_key(f);
+      if (finite_f32(f) && (key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & dmask], 1u);
+    }
+    __syncthreads();
+    // thread t owns buckets 2047 - 2t and 2046 - 2t (from the top); the exclusive prefix of their counts in thread
+    // order is the number of keys in higher buckets
+    const uint32_t hi = 2047 - 2 * tid, lo = hi - 1;
+    const uint32_t chi = hist[hi], clo = hist[lo];
+    // a block prefix sum of the pair counts (counts up to 2^31: the same wave / block structure with sums)
+    const int wave = tid >> 6, lane = tid & 63;
+    uint32_t v = chi + clo, incl = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t y = (uint32_t)__shfl_up((int)incl, d);
+      if (lane >= d) incl += y;
+    }
+    if (lane == 63) scratch[wave] = incl;
+    __syncthreads();
+    uint32_t above = incl - v, all = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+      const uint32_t c = scratch[w];
+      above += w < wave ? c : 0u;
+      all += c;
+    }
+    if (pass == 0) {
+      k = min((uint32_t)topk, all);   // the finite keys bound how many can be taken
+      remaining = k;
+    }
+    if (k != 0) {
+      if (above < remaining && remaining <= above + chi) {
+        sel[0] = hi;
+        sel[1] = remaining - above;
+      } else if (above + chi < remaining && remaining <= above + chi + clo) {
+        sel[0] = lo;
+        sel[1] = remaining - above - chi;
+      }
+    }
+    __syncthreads();
+    if (k == 0) break;
+    prefix |= sel[0] << shift;
+    pmask |= dmask << shift;
+    remaining = sel[1];
+    __syncthreads();   // sel and scratch are rewritten by the next pass
+  }
+  // positions in order: keys above T, then the first `remaining` keys equal to T
+  uint32_t placed = 0, eq_seen = 0;
+  for (int base = 0; k != 0 && base < cols && placed < k; base += kTopkThreads) {
+    const int c = base + tid;
+    const float f = c < cols ? xr[c] : -__builtin_inff();
+    const bool fin = finite_f32(f);
+    const uint32_t key = order_key(f);
+    const bool eq = fin && key == prefix;
+    uint32_t n_eq, n_take;
+    const uint32_t eq_before = eq_seen + block_exclusive_count(eq, scratch, n_eq);
+    const bool take = fin && (key > prefix || (eq && eq_before < remaining));
+    const uint32_t at = placed + block_exclusive_count(take, scratch, n_take);
+    if (take) o[at] = c;
+    placed += n_take;
+    eq_seen += n_eq;
+  }
+  for (int i = (int)k + tid; i < topk; i += kTopkThreads) o[i] = -1;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// QSA indexer logits
+
+template <bool BF>
+__device__ inline float16_t mfma_qk(short8_t a, short8_t b, float16_t c) {
+  if constexpr (BF)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c,
+                                                  0, 0, 0);
+}
+
+struct QsaArgs {
+  const uint16_t* q;
+  int64_t q_rs, q_hs;
+  const uint16_t* k;
+  int64_t k_rs;
+  const int32_t* starts;
+  const int32_t* ends;
+  float score_scale;
+  float* logits;
+  int64_t ld;
+  int rows, keys;
+  int keys_per_wg;
+  int vec_store;             // logits rows are 16-byte aligned: stores of 4 floats
+};
+
+constexpr int kQsaWaves = 4;
+
+// Workgroup = (block of 32 / H rows, keys_per_wg keys); wave w takes every 4th 32-key block of them. Lane layouts
+// (32x32x16): A = keys, lane (key l % 32, dims 16kk + 8 (l / 32) .. +7) read straight from k; B = queries, lane
+// (column j = l % 32: row j / H, head j % H; same dims) kept in registers; C = S^T, lane (column j, keys
+// 8 (r / 4) + 4 (l / 32) + r % 4).
+template <int H, int NK, bool BF>
+__global__ __launch_bounds__(64 * kQsaWaves) void qsa_logits_kernel(const QsaArgs a) {
+  constexpr int kRows = 32 / H;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
+  const int r0 = blockIdx.x * kRows;
+  const int my_row = r0 + j / H, head = j % H;
+  const bool row_ok = my_row < a.rows;
+  // the rows' key range: a 32-key block outside every row's [start, end) is written as -inf without the product
+  int lo = 0x7FFFFFFF, hi = 0;
+  for (int r = 0; r < kRows; ++r) {
+    if (r0 + r < a.rows) {
+      lo = min(lo, max(0, a.starts[r0 + r]));
+      hi = max(hi, min(a.keys, a.ends[r0 + r]));
+    }
+  }
+  const int start = row_ok ? a.starts[my_row] : 0, end = row_ok ? a.ends[my_row] : 0;
+  short8_t qb[NK];
+  {
+    const uint16_t* qp = a.q + (int64_t)(row_ok ? my_row : 0) * a.q_rs + (int64_t)head * a.q_hs + 8 * h;
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) {
+      const uint4 w = row_ok ? *reinterpret_cast<const uint4*>(qp + 16 * kk) : uint4{0u, 0u, 0u, 0u};
+      qb[kk] = __builtin_bit_cast(short8_t, w);
+    }
+  }
+  const int k_begin = blockIdx.y * a.keys_per_wg, k_end = min(a.keys, k_begin + a.keys_per_wg);
+  for (int kb = k_begin + 32 * wave; kb < k_end; kb += 32 * kQsaWaves) {
+    float v[16];
+    if (kb + 32 <= lo || kb >= hi) {   // uniform: no row of the block takes these keys
+#pragma unroll
+      for (int r = 0; r < 16; ++r) v[r] = -__builtin_inff();
+    } else {
+      const int key = min(kb + j, a.keys - 1);
+      const uint16_t* kp = a.k + (int64_t)key * a.k_rs + 8 * h;
+      float16_t s = {};
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk) {
+        const short8_t kf = __builtin_bit_cast(short8_t, *reinterpret_cast<const uint4*>(kp + 16 * kk));
+        s = mfma_qk<BF>(kf, qb[kk], s);
+      }
+      // ReLU, then the sum over the H heads of a row (H consecutive lanes), in the order lane ^ 1, ^ 2, ...
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = fmaxf(s[r], 0.0f);
+        if constexpr (H >= 2) x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
+        if constexpr (H >= 4) x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
+        if constexpr (H >= 8) x += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), (4 << 10) | 0x1F));
+        if constexpr (H >= 16) x += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), (8 << 10) | 0x1F));
+        if constexpr (H >= 32) x += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), (16 << 10) | 0x1F));
+        const int key = kb + 8 * (r >> 2) + 4 * h + (r & 3);
+        v[r] = (key >= start && key < end) ? x / a.score_scale : -__builtin_inff();
+      }
+    }
+    // the lane of head 0 of each row writes its 16 keys: 4 runs of 4 consecutive keys
+    if (row_ok && head == 0) {
+      float* op = a.logits + (int64_t)my_row * a.ld;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int key = kb + 8 * g + 4 * h;
+        if (key + 4 <= a.keys && a.vec_store) {
+          *reinterpret_cast<float4_t*>(op + key) = float4_t{v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (key + e < a.keys) op[key + e] = v[4 * g + e];
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// DSA logits (FP8)
+
+struct DsaArgs {
+  const uint8_t* q;          // [num_q, heads, D] E4M3
+  int64_t q_rs, q_hs;
+  const uint8_t* k;          // flat: [num_kv, D] E4M3 with k_rs bytes per key; paged: the page buffer
+  int64_t k_rs;
+  const float* k_scale;      // flat: [num_kv]
+  int64_t page_bytes;        // paged: bytes from one page to the next (block x (D + 4))
+  int64_t num_pages;         // paged: pages in the cache (table entries past it read as no key)
+  int block;                 // paged: keys per page (0: flat keys)
+  const int32_t* block_table;
+  int64_t bt_stride;
+  int bt_width;
+  const float* w;            // [num_q, heads]
+  int64_t w_rs;
+  const int32_t* ks;         // flat: [num_q] (inclusive) start, or NULL
+  const int32_t* ke;         // flat: end (exclusive); paged: context length per row
+  int clean;
+  float* logits;
+  int64_t ld;
+  int num_q, num_kv, heads;
+  int keys_per_wg;
+  int out_cols;              // columns written per row (paged: max_seq_len)
+};
+
+constexpr int kDsaWaves = 4;
+
+// Workgroup = (4 query rows, one per wavefront, keys_per_wg keys); the wavefronts walk the same 32-key blocks, so a
+// block's key bytes are fetched once for the four rows. Per block and 32-head group, S = Q . K^T on 32x32x16 FP16
+// MFMAs of the converted E4M3 values (A = Q: lane (head l % 32, dims 16kk + 8 (l / 32) .. +7); B = K^T: lane (key
+// l % 32, same dims); C: lane (key column l % 32, heads 8 (r / 4) + 4 (l / 32) + r % 4)).
+template <int NK>
+__global__ __launch_bounds__(64 * kDsaWaves) void dsa_logits_kernel(const DsaArgs a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
+  const int qrow = blockIdx.x * kDsaWaves + wave;
+  if (qrow >= a.num_q) return;   // no barrier below
+  const int groups = a.heads / 32;
+  const int k_begin = blockIdx.y * a.keys_per_wg, k_end = min(a.out_cols, k_begin + a.keys_per_wg);
+  const bool paged = a.block > 0;
+  const int lim_lo = (!paged && a.ks) ? a.ks[qrow] : 0;
+  const int lim_hi = paged ? a.ke[qrow] : (a.ke ? a.ke[qrow] : a.num_kv);
+  const float fill = a.clean ? -__builtin_inff() : 0.0f;
+  for (int kb = k_begin; kb < k_end; kb += 32) {
+    const int key = kb + j;
+    bool live = key >= lim_lo && key < lim_hi && key < (paged ? a.bt_width * a.block : a.num_kv);
+    int32_t page = 0;
+    if (paged) {
+      // a negative entry reads page 0, as the reference's clamp does (indexer_torch.py:61); an entry past the cache
+      // reads as no key
+      page = live ? max(a.block_table[(int64_t)qrow * a.bt_stride + key / a.block], 0) : 0;
+      live = live && page < a.num_pages;
+      page = live ? page : 0;
+    }
+    float total = 0.0f;
+    if (__builtin_amdgcn_ballot_w64(live)) {
+      // this lane's key row and scale
+      const uint8_t* kp;
+      float ksc;
+      if (paged) {
+        const int kk = live ? key : 0;
+        const uint8_t* pg = a.k + (int64_t)page * a.page_bytes;
+        kp = pg + (int64_t)(kk % a.block) * (16 * NK);
+        ksc = *reinterpret_cast<const float*>(pg + (int64_t)a.block * (16 * NK) + 4 * (kk % a.block));
+      } else {
+        const int kk = live ? key : 0;
+        kp = a.k + (int64_t)kk * a.k_rs;
+        ksc = a.k_scale[kk];
+      }
+      uint64_t kf[NK];
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk) kf[kk] = *reinterpret_cast<const uint64_t*>(kp + 16 * kk + 8 * h);
+      float acc = 0.0f;
+      for (int g = 0; g < groups; ++g) {
+        const uint8_t* qp = a.q + (int64_t)qrow * a.q_rs + (int64_t)(32 * g + j) * a.q_hs + 8 * h;
+        float16_t s = {};
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk)
+          s = __builtin_amdgcn_mfma_f32_32x32x16_f16(fp8x8_to_f16(*reinterpret_cast<const uint64_t*>(qp + 16 * kk)),
+                                                     fp8x8_to_f16(kf[kk]), s, 0, 0, 0);
+        const float* wp = a.w + (int64_t)qrow * a.w_rs + 32 * g + 4 * h;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc += fmaxf(s[r], 0.0f) * wp[8 * (r >> 2) + (r & 3)];
+      }
+      // the other 16 heads of each group are in the lane 32 apart
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc), __float_as_uint(acc), false, false);
+      total = (__uint_as_float(sw[0]) + __uint_as_float(sw[1])) * ksc;
+    }
+    if (h == 0 && key < k_end) a.logits[(int64_t)qrow * a.ld + key] = live ? total : fill;
+  }
+}
+
+}  // namespace
+}  // namespace xt
+
+using namespace xt;
+
+extern "C" int xt_topk_rows(const float* x, int64_t ld, int rows, int cols, int topk, int32_t* out, int64_t out_ld,
+                            xt_stream_t stream) {
+  const char* what = "xt_topk_rows";
+  if (rows < 0 || cols < 0 || topk < 0) return fail(XT_EINVAL, "%s: negative size", what);
+  if (rows == 0 || topk == 0) return ok();
+  if (!x || !out) return fail(XT_EINVAL, "%s: a required pointer is null", what);
+  if (ld < cols || out_ld < topk) return fail(XT_EINVAL, "%s: row strides shorter than the rows", what);
+  hipLaunchKernelGGL(topk_rows_kernel, dim3((unsigned)rows), dim3(kTopkThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), x, ld, cols, topk, out, out_ld);
+  return check_launch(what);
+}
+
+template <int H>
+static int qsa_launch(int nk, bool bf, const QsaArgs& a, dim3 grid, hipStream_t st) {
+#define XT_QSA(NK)                                                                                                    \
+  if (nk == NK) {                                                                                                    \
+    if (bf)                                                                                                          \
+      hipLaunchKernelGGL((qsa_logits_kernel<H, NK, true>), grid, dim3(64 * kQsaWaves), 0, st, a);                   \
+    else                                                                                                             \
+      hipLaunchKernelGGL((qsa_logits_kernel<H, NK, false>), grid, dim3(64 * kQsaWaves), 0, st, a);                  \
+    return XT_OK;                                                                                                    \
+  }
+  XT_QSA(4)
+  XT_QSA(8)
+  XT_QSA(16)
+#undef XT_QSA
+  return XT_EUNSUPPORTED;
+}
+
+extern "C" int xt_qsa_indexer_logits(const void* q, int64_t q_row_stride, int64_t q_head_stride, int rows, int heads,
+                                     int dim, const void* k, int64_t k_row_stride, int keys, const int32_t* starts,
+                                     const int32_t* ends, float score_scale, int dtype, float* logits, int64_t ld,
+                                     xt_stream_t stream) {
+  const char* what = "xt_qsa_indexer_logits";
+  if (rows < 0 || keys < 0) return fail(XT_EINVAL, "%s: negative size", what);
+  if (rows == 0 || keys == 0) return ok();
+  if (!q || !k || !starts || !ends || !logits) return fail(XT_EINVAL, "%s: a required pointer is null", what);
+  if (heads != 1 && heads != 2 && heads != 4 && heads != 8 && heads != 16 && heads != 32)
+    return fail(XT_EUNSUPPORTED, "%s: %d heads (supported: powers of 2 up to 32)", what, heads);
+  if (dim != 64 && dim != 128 && dim != 256) return fail(XT_EUNSUPPORTED, "%s: head size %d (64, 128, 256)", what, dim);
+  if (dtype != XT_DTYPE_BF16 && dtype != XT_DTYPE_F16) return fail(XT_EINVAL, "%s: q / k must be BF16 or FP16", what);
+  if (!aligned(q, 16) || !aligned(k, 16) || q_row_stride % 8 || q_head_stride % 8 || k_row_stride % 8 ||
+      ld < keys || !(score_scale > 0.0f))
+    return fail(XT_EINVAL, "%s: rows must be 16-byte aligned, ld >= keys, score_scale > 0", what);
+  QsaArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_rs = q_row_stride;
+  a.q_hs = q_head_stride;
+  a.k = static_cast<const uint16_t*>(k);
+  a.k_rs = k_row_stride;
+  a.starts = starts;
+  a.ends = ends;
+  a.score_scale = score_scale;
+  a.logits = logits;
+  a.ld = ld;
+  a.rows = rows;
+  a.keys = keys;
+  a.keys_per_wg = 2048;
+  a.vec_store = (ld % 4 == 0) && aligned(logits, 16);
+  const int rows_per_wg = 32 / heads;
+  const dim3 grid((unsigned)((rows + rows_per_wg - 1) / rows_per_wg), (unsigned)((keys + 2047) / 2048));
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const bool bf = dtype == XT_DTYPE_BF16;
+  const int nk = dim / 16;
+  int e = XT_EUNSUPPORTED;
+  switch (heads) {
+    case 1: e = qsa_launch<1>(nk, bf, a, grid, st); break;
+    case 2: e = qsa_launch<2>(nk, bf, a, grid, st); break;
+    case 4: e = qsa_launch<4>(nk, bf, a, grid, st); break;
+    case 8: e = qsa_launch<8>(nk, bf, a, grid, st); break;
+    case 16: e = qsa_launch<16>(nk, bf, a, grid, st); break;
+    case 32: e = qsa_launch<32>(nk, bf, a, grid, st); break;
+  }
+  if (e != XT_OK) return fail(e, "%s: no kernel for %d heads x %d", what, heads, dim);
+  return check_launch(what);
+}
+
+static int dsa_common(const char* what, DsaArgs& a, int dim, xt_stream_t stream) {
+  if (a.heads % 32 || a.heads <= 0 || a.heads > 128)
+    return fail(XT_EUNSUPPORTED, "%s: %d heads (supported: 32, 64, 96, 128)", what, a.heads);
+  if (dim != 64 && dim != 128 && dim != 256) return fail(XT_EUNSUPPORTED, "%s: head size %d (64, 128, 256)", what, dim);
+  if (!aligned(a.q, 8) || a.q_rs % 8 || a.q_hs % 8 || !aligned(a.w, 4) || a.ld < a.out_cols)
+    return fail(XT_EINVAL, "%s: q rows must be 8-byte aligned and ld >= the columns written", what);
+  a.keys_per_wg = 4096;
+  const dim3 grid((unsigned)((a.num_q + kDsaWaves - 1) / kDsaWaves), (unsigned)((a.out_cols + 4095) / 4096));
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  switch (dim / 16) {
+    case 4: hipLaunchKernelGGL(dsa_logits_kernel<4>, grid, dim3(64 * kDsaWaves), 0, st, a); break;
+    case 8: hipLaunchKernelGGL(dsa_logits_kernel<8>, grid, dim3(64 * kDsaWaves), 0, st, a); break;
+    default: hipLaunchKernelGGL(dsa_logits_kernel<16>, grid, dim3(64 * kDsaWaves), 0, st, a); break;
+  }
+  return check_launch(what);
+}
+
+extern "C" int xt_dsa_mqa_logits(const void* q, int64_t q_row_stride, int64_t q_head_stride, int num_q, int heads,
+                                 int dim, const void* k, int64_t k_row_stride, const float* k_scale, int num_kv,
+                                 const float* weights, int64_t w_row_stride, const int32_t* ks, const int32_t* ke,
+                                 int clean_logits, float* logits, int64_t ld, xt_stream_t stream) {
+  const char* what = "xt_dsa_mqa_logits";
+  if (num_q < 0 || num_kv < 0) return fail(XT_EINVAL, "%s: negative size", what);
+  if (num_q == 0 || num_kv == 0) return ok();
+  if (!q || !k || !k_scale || !weights || !logits) return fail(XT_EINVAL, "%s: a required pointer is null", what);
+  if (!aligned(k, 8) || k_row_stride % 8 || k_row_stride < dim)
+    return fail(XT_EINVAL, "%s: key rows must be 8-byte aligned", what);
+  DsaArgs a = {};
+  a.q = static_cast<const uint8_t*>(q);
+  a.q_rs = q_row_stride;
+  a.q_hs = q_head_stride;
+  a.k = static_cast<const uint8_t*>(k);
+  a.k_rs = k_row_stride;
+  a.k_scale = k_scale;
+  a.block = 0;
+  a.w = weights;
+  a.w_rs = w_row_stride;
+  a.ks = ks;
+  a.ke = ke;
+  a.clean = clean_logits;
+  a.logits = logits;
+  a.ld = ld;
+  a.num_q = num_q;
+  a.num_kv = num_kv;
+  a.heads = heads;
+  a.out_cols = num_kv;
+  return dsa_common(what, a, dim, stream);
+}
+
+extern "C" int xt_dsa_paged_mqa_logits(const void* q, int64_t q_row_stride, int64_t q_head_stride, int batch,
+                                       int heads, int dim, const void* kvcache, int64_t num_pages, int64_t page_bytes,
+                                       int block,
+                                       const int32_t* block_table, int64_t bt_stride, int bt_width,
+                                       const int32_t* context_lens, const float* weights, int64_t w_row_stride,
+                                       int max_seq_len, int clean_logits, float* logits, int64_t ld,
+                                       xt_stream_t stream) {
+  const char* what = "xt_dsa_paged_mqa_logits";
+  if (batch < 0 || max_seq_len < 0) return fail(XT_EINVAL, "%s: negative size", what);
+  if (batch == 0 || max_seq_len == 0) return ok();
+  if (!q || !kvcache || !block_table || !context_lens || !weights || !logits)
+    return fail(XT_EINVAL, "%s: a required pointer is null", what);
+  if (block <= 0 || num_pages <= 0 || page_bytes < (int64_t)block * (dim + 4) || page_bytes % 8 ||
+      !aligned(kvcache, 8) || bt_width <= 0 || bt_stride < bt_width)
+    return fail(XT_EINVAL, "%s: pages of %d keys need %d bytes each (8-byte aligned)", what, block, block * (dim + 4));
+  DsaArgs a = {};
+  a.q = static_cast<const uint8_t*>(q);
+  a.q_rs = q_row_stride;
+  a.q_hs = q_head_stride;
+  a.k = static_cast<const uint8_t*>(kvcache);
+  a.page_bytes = page_bytes;
+  a.num_pages = num_pages;
+  a.block = block;
+  a.block_table = block_table;
+  a.bt_stride = bt_stride;
+  a.bt_width = bt_width;
+  a.w = weights;
+  a.w_rs = w_row_stride;
+  a.ks = nullptr;
+  a.ke = context_lens;
+  a.clean = clean_logits;
+  a.logits = logits;
+  a.ld = ld;
+  a.num_q = batch;
+  a.num_kv = bt_width * block;
+  a.heads = heads;
+  a.out_cols = max_seq_len;
+  return dsa_common(what, a, dim, stream);
+}

@@ -75,13 +75,19 @@ template <bool HI>
 __device__ inline half2_t fp8x2_to_f16(uint32_t packed) {
   return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(packed, 1.0f, HI);
 }
-// Maximum and sum of x over lanes l, l ^ 16 and l ^ 32 (the four lanes 16 apart), in VALU permutes: with x as both
-// operands, v_permlane16_swap / v_permlane32_swap hand every lane the pair (x[l], x[l ^ 16]) / (x[l], x[l ^ 32]),
-// in an order that does not matter here (ds_bpermute would take two LDS round trips).
+// Eight E4M3 bytes (low byte first) -> eight exact FP16 values in the same order.
+__device__ inline half8_t fp8x8_to_f16(uint64_t v) {
+  const half2_t a = fp8x2_to_f16<false>((uint32_t)v), b = fp8x2_to_f16<true>((uint32_t)v);
+  const half2_t c = fp8x2_to_f16<false>((uint32_t)(v >> 32)), d = fp8x2_to_f16<true>((uint32_t)(v >> 32));
+  return half8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
 // A load through the scalar cache (the constant address space) of memory no launch writes: uniform per-row values.
 __device__ inline int32_t uniform_load(const int32_t* p) {
   return *(const __attribute__((address_space(4))) int32_t*)(p);
 }
+// Maximum and sum of x over lanes l, l ^ 16 and l ^ 32 (the four lanes 16 apart), in VALU permutes: with x as both
+// operands, v_permlane16_swap / v_permlane32_swap hand every lane the pair (x[l], x[l ^ 16]) / (x[l], x[l ^ 32]),
+// in an order that does not matter here (ds_bpermute would take two LDS round trips).
 __device__ inline float max4_lanes16(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
@@ -102,6 +108,7 @@ template <int SEL>
 __device__ half2_t fp4x2_to_f16(uint32_t packed);
 template <bool HI>
 __device__ half2_t fp8x2_to_f16(uint32_t packed);
+__device__ half8_t fp8x8_to_f16(uint64_t v);
 __device__ float max4_lanes16(float x);
 __device__ int32_t uniform_load(const int32_t* p);
 __device__ float sum4_lanes16(float x);

@@ -752,3 +752,101 @@ def ceiling_gather(pool, page_table, indices, page_size, sink=None):
                                           batch, topk, _ptr(sink), _stream(pool))
     _lib.check(status, 'ceiling_gather')
     return sink
+
+
+def topk_rows(x, topk, out=None):
+    """xt_topk_rows: x FP32 [rows, cols] (unit column stride) -> int32 [rows, topk]: per row the positions of the topk
+    largest finite values, ascending, ties toward the lower position, -1 padded."""
+    if x.dtype != torch.float32 or x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError('xtier_amd.topk_rows: x must be float32 [rows, cols] with contiguous rows')
+    rows, cols = x.shape
+    if out is None:
+        out = torch.empty((rows, topk), dtype=torch.int32, device=x.device)
+    elif out.dtype != torch.int32 or out.shape != (rows, topk) or out.stride(1) != 1:
+        raise ValueError('xtier_amd.topk_rows: out must be int32 [rows, topk] with contiguous rows')
+    _lib.check(_lib.lib().xt_topk_rows(_ptr(x), x.stride(0), rows, cols, int(topk), _ptr(out), out.stride(0),
+                                       _stream(x)), 'topk_rows')
+    return out
+
+
+def qsa_indexer_logits(q, k, row_starts, row_ends, score_scale=None):
+    """The QSA indexer logits (qsa_prefill.py:77-102, with SGLang's mask): q [rows, heads, dim] and k [keys, 1, dim]
+    (or [keys, dim]) BF16 / FP16, row_starts / row_ends [rows] -> FP32 [rows, keys]: sum_h ReLU(q . k) / score_scale
+    (default sqrt(dim)) inside [start, end), -inf outside."""
+    if k.dim() == 3:
+        k = k[:, 0]
+    rows, heads, dim = q.shape
+    keys = k.shape[0]
+    if q.dtype not in _DTYPES or k.dtype != q.dtype:
+        raise ValueError('xtier_amd.qsa_indexer_logits: q and k must both be BF16 or both FP16')
+    if q.stride(-1) != 1 or k.stride(-1) != 1:
+        raise ValueError('xtier_amd.qsa_indexer_logits: q and k need a contiguous last dimension')
+    starts = row_starts.to(device=q.device, dtype=torch.int32).contiguous()
+    ends = row_ends.to(device=q.device, dtype=torch.int32).contiguous()
+    logits = torch.empty((rows, keys), dtype=torch.float32, device=q.device)
+    scale = float(score_scale or math.sqrt(dim))
+    status = _lib.lib().xt_qsa_indexer_logits(_ptr(q), q.stride(0), q.stride(1), rows, heads, dim, _ptr(k), k.stride(0),
+                                              keys, _ptr(starts), _ptr(ends), scale, _DTYPES[q.dtype], _ptr(logits),
+                                              logits.stride(0), _stream(q))
+    _lib.check(status, 'qsa_indexer_logits')
+    return logits
+
+
+def _fp8(t, what):
+    if t.dtype == torch.float8_e4m3fn:
+        return t
+    if t.dtype == torch.uint8:
+        return t.view(torch.float8_e4m3fn)
+    raise ValueError(f'xtier_amd.{what}: FP8 E4M3 tensors expected, not {t.dtype}')
+
+
+def dsa_mqa_logits(q_fp8, kv, weights, ks, ke, clean_logits=False, max_seqlen_k=0):
+    """fp8_mqa_logits (indexer_torch.py:28-45): q [num_q, heads, dim] E4M3, kv = (k [num_kv, dim] E4M3, k_scale
+    [num_kv] FP32), weights [num_q, heads], ks / ke [num_q] -> FP32 [num_q, num_kv], a view of rows padded to a
+    multiple of 4 columns (the stride SGLang's top-k expects): sum_h w ReLU(q_h . k) * k_scale inside [ks, ke), 0
+    (or -inf when clean_logits) elsewhere."""
+    k_fp8, k_scale = kv
+    q_fp8, k_fp8 = _fp8(q_fp8, 'dsa_mqa_logits'), _fp8(k_fp8, 'dsa_mqa_logits')
+    num_q, heads, dim = q_fp8.shape
+    num_kv = k_fp8.shape[0]
+    k2 = k_fp8.reshape(num_kv, dim)
+    if q_fp8.stride(-1) != 1 or k2.stride(-1) != 1:
+        raise ValueError('xtier_amd.dsa_mqa_logits: q and k need a contiguous last dimension')
+    w = weights.float().contiguous()
+    sc = k_scale.reshape(num_kv).float().contiguous()
+    storage = torch.zeros(num_q, (num_kv + 3) // 4 * 4, dtype=torch.float32, device=q_fp8.device)
+    ks32 = ks.to(device=q_fp8.device, dtype=torch.int32).contiguous()
+    ke32 = ke.to(device=q_fp8.device, dtype=torch.int32).contiguous()
+    status = _lib.lib().xt_dsa_mqa_logits(_ptr(q_fp8), q_fp8.stride(0), q_fp8.stride(1), num_q, heads, dim, _ptr(k2),
+                                          k2.stride(0), _ptr(sc), num_kv, _ptr(w), w.stride(0), _ptr(ks32), _ptr(ke32),
+                                          int(bool(clean_logits)), _ptr(storage), storage.stride(0), _stream(q_fp8))
+    _lib.check(status, 'dsa_mqa_logits')
+    return storage[:, :num_kv]
+
+
+def dsa_paged_mqa_logits(q_fp8, kvcache_fp8, weights, context_lens, block_table, schedule_metadata, max_seq_len,
+                         clean_logits=False, indices=None):
+    """fp8_paged_mqa_logits (indexer_torch.py:48-72): q [batch, 1, heads, dim] E4M3, the paged cache [pages, block, 1,
+    dim + 4] bytes (block x dim E4M3 values, then block FP32 scales per page), weights [batch, heads], context_lens
+    [batch] (or [batch, 1]), block_table [batch, pages] -> FP32 [batch, max_seq_len]."""
+    if indices is not None:
+        raise NotImplementedError('xtier_amd.dsa_paged_mqa_logits: no index tensor is taken')
+    if context_lens.dim() == 2:
+        if context_lens.shape[1] != 1:
+            raise NotImplementedError('xtier_amd.dsa_paged_mqa_logits: one query per row (next_n 1)')
+        context_lens = context_lens[:, 0]
+    q = _fp8(q_fp8, 'dsa_paged_mqa_logits')
+    batch, _, heads, dim = q.shape
+    block = kvcache_fp8.shape[1]
+    cache = kvcache_fp8.view(torch.uint8) if kvcache_fp8.dtype != torch.uint8 else kvcache_fp8
+    page_bytes = cache.stride(0) * cache.element_size()
+    w = weights.float().contiguous()
+    lens = context_lens.to(device=q.device, dtype=torch.int32).contiguous()
+    table = block_table.to(device=q.device, dtype=torch.int32).contiguous()
+    out = torch.empty((batch, int(max_seq_len)), dtype=torch.float32, device=q.device)
+    status = _lib.lib().xt_dsa_paged_mqa_logits(_ptr(q), q.stride(0), q.stride(2), batch, heads, dim, _ptr(cache),
+                                                cache.shape[0], page_bytes, block, _ptr(table), table.stride(0), table.shape[1],
+                                                _ptr(lens), _ptr(w), w.stride(0), int(max_seq_len),
+                                                int(bool(clean_logits)), _ptr(out), out.stride(0), _stream(q))
+    _lib.check(status, 'dsa_paged_mqa_logits')
+    return out
