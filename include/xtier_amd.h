@@ -386,6 +386,44 @@ int xt_dsa_paged_mqa_logits(const void* q, int64_t q_row_stride, int64_t q_head_
 int xt_topk_rows(const float* x, int64_t ld, int rows, int cols, int topk, int32_t* out, int64_t out_ld,
                  xt_stream_t stream);
 
+/* MiniMax index block scores over the NVFP4 index pool (payload [pages, 128, dim/2], E4M3 scale bytes [pages, 128,
+ * dim/16], byte strides of a page and a slot row; max_slots = pages * 128; slot s is page s / 128, row s % 128, and
+ * slots and slot_ids wrap as (s + max_slots) % max_slots). The score of position p for head h is (q_h . k_p) *
+ * score_factor, score_factor = (sm_scale * 1.4426950409) * k_scale in FP32; q BF16 / FP16 (q_dtype XT_DTYPE_*),
+ * products exact and summed in FP32; dim 64, 128 or 256; block_size a multiple of 32 up to 256. req_to_token [reqs,
+ * r2t_stride], seq_lens / slot_ids (and prefix_lens / cu_seqlens) are int32, or int64 where bit 0 (req_to_token),
+ * 1 (seq_lens), 2 (slot_ids), 3 (prefix_lens), 4 (cu_seqlens) of index_int64 is set. Scores are written in
+ * score_dtype (0 FP32, 1 BF16, 2 FP16) at the given element strides; entries not named below are left as they are.
+ *
+ * Replaces _fp4_decode_score_kernel (xtier/packs/minimax_m3/kv_fp4.py:168-222, launched in SGLang's
+ * flash_decode_with_topk_idx through the shim at :225-244): scores[h, b, blk] for every head and block blk <
+ * ceil(seq_lens[b] / block_size): the maximum (lse 0) or log2 of the sum of exp2 (lse 1; NaN -> -inf) of the block's
+ * scores below seq_len; then 1e29 for the last local_blocks blocks, else 1e30 for the first init_blocks. A request
+ * with at most skip_topk blocks (skip_topk >= 0) gets nothing. max_blocks_hint (any positive value is correct)
+ * sizes the grid. */
+int xt_minimax_decode_scores(const void* q, int64_t q_batch_stride, int64_t q_head_stride, int batch, int heads,
+                             int dim, int q_dtype, const void* index_payload, int64_t pay_page_stride,
+                             int64_t pay_slot_stride, const void* index_scales, int64_t sc_page_stride,
+                             int64_t sc_slot_stride, int64_t max_slots, const void* req_to_token, int64_t r2t_stride,
+                             const void* seq_lens, const void* slot_ids, int index_int64, int block_size,
+                             float score_factor, int init_blocks, int local_blocks, int skip_topk, int lse,
+                             void* scores, int score_dtype, int64_t s_head_stride, int64_t s_batch_stride,
+                             int64_t s_block_stride, int max_blocks_hint, xt_stream_t stream);
+
+/* Replaces _fp4_index_score_kernel (kv_fp4.py:407-446, launched in SGLang's flash_prefill_with_topk_index through
+ * the shim at :449-472): q [total_q, heads, dim]; for query row t of request b (token cu_seqlens[b] + t, position
+ * prefix_lens[b] + t) and every head, scores[h, cu_seqlens[b] + t, blk] = the maximum of the scores of the block's
+ * positions at or before the row's position and below seq_len (-inf when none), for blk < ceil(min(seq_len,
+ * prefix_len + 64 (t / 64 + 1)) / block_size). max_q_len bounds every request's query count. */
+int xt_minimax_prefill_scores(const void* q, int64_t q_token_stride, int64_t q_head_stride, int batch, int heads,
+                              int dim, int q_dtype, int max_q_len, const void* index_payload, int64_t pay_page_stride,
+                              int64_t pay_slot_stride, const void* index_scales, int64_t sc_page_stride,
+                              int64_t sc_slot_stride, int64_t max_slots, const void* req_to_token, int64_t r2t_stride,
+                              const void* cu_seqlens, const void* seq_lens, const void* prefix_lens,
+                              const void* slot_ids, int index_int64, int block_size, float score_factor, void* scores,
+                              int score_dtype, int64_t s_head_stride, int64_t s_token_stride, int64_t s_block_stride,
+                              xt_stream_t stream);
+
 /* Self-test, no counterpart in the reference: the known-answer test of the hardware conversions the attention kernels
  * use (E4M3 -> FP16 from either half of a dword, two E2M1 codes -> FP16 / FP32 from each byte position, E4M3 with a
  * power-of-2 scale -> BF16), for every byte, written to `out` (xt_selftest_conversions_bytes() bytes, 16-byte

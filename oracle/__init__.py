@@ -32,5 +32,8 @@ Pinning (what each function is checked against, in ``tests/``):
 - ``topk.dsa_mqa_logits``: the reference's einsum formula (indexer_torch.py:28-45) in torch float64 and a scalar loop
   over one element.
 - ``topk.dsa_paged_mqa_logits``: equal to ``dsa_mqa_logits`` on the keys gathered page by page.
-- ``topk.minimax_block_scores_*``: parity unpinned until their own tests (below) land.
+- ``topk.minimax_block_scores_decode`` / ``_prefill``: per-block brute force over keys read through the 16-entry
+  E2M1 table (not the dequantizer), torch.logsumexp for the LSE score, the forced init / local blocks with their
+  precedence, the skip of requests with at most topk blocks, a negative slot against its wrapped value, and the
+  64-row tile that bounds the blocks a prefill row gets.
 """

@@ -80,24 +80,37 @@ def dsa_paged_mqa_logits(q, kvcache, weights, context_lens, block_table, max_seq
 
 
 def _index_keys(pay, sf, slots):
-    """NVFP4 index-key rows of the given slots (pay [pages, 128, d/2], sf [pages, 128, d/16]) as float64 [n, d]."""
+    """NVFP4 index-key rows of the given slots (pay [pages, 128, d/2], sf [pages, 128, d/16]) as float64 [n, d]; slots
+    wrap modulo the pool's slot count, as (slot + max_slots) % max_slots does (kv_fp4.py:190, :209, :437)."""
     pay = np.asarray(pay, np.uint8).reshape(-1, pay.shape[-1])
     sf = np.asarray(sf, np.uint8).reshape(-1, sf.shape[-1])
+    slots = (np.asarray(slots, np.int64) + len(pay)) % len(pay)
     return nvfp4.dequant(pay[slots], sf[slots], 1.0).astype(np.float64)
 
 
+def _score_scale(sm_scale, k_scale):
+    """The FP32 factor of the scores: (sm_scale * 1.4426950409) * k_scale, as the kernels form it (kv_fp4.py:181,
+    :208; :417, :441)."""
+    return float(np.float32(np.float32(sm_scale) * np.float32(1.4426950409)) * np.float32(k_scale))
+
+
 def minimax_block_scores_decode(q, pay, sf, req_to_token, slot_ids, seq_lens, block_size, sm_scale, k_scale,
-                                init_blocks, local_blocks, score_type='max'):
-    """q [batch, heads, d] -> float64 scores [heads, batch, max_blocks] (log2 domain; unused entries nan)."""
+                                init_blocks, local_blocks, score_type='max', topk=None):
+    """q [batch, heads, d] -> float64 scores [heads, batch, max_blocks] (log2 domain; unused entries nan). With
+    ``topk`` (SKIP_TRIVIAL_TOPK_SCORE, kv_fp4.py:186-188) a request with at most topk blocks gets no scores."""
     q = np.asarray(q, np.float64)
     batch, heads, d = q.shape
     max_blocks = int(max(-(-int(s) // block_size) for s in seq_lens)) if batch else 0
     out = np.full((heads, batch, max_blocks), np.nan)
-    c = sm_scale * 1.4426950409 * k_scale
+    c = _score_scale(sm_scale, k_scale)
+    r2t = np.asarray(req_to_token)
+    slots = len(np.asarray(pay).reshape(-1, pay.shape[-1]))
     for b in range(batch):
         n = int(seq_lens[b])
         nb = -(-n // block_size)
-        toks = np.asarray(req_to_token)[int(slot_ids[b]), :n]
+        if topk is not None and nb <= topk:
+            continue
+        toks = r2t[(int(slot_ids[b]) + slots) % slots, :n]
         keys = _index_keys(pay, sf, toks)
         sc = q[b] @ keys.T * c                                   # [heads, n]
         local_start = max(0, nb - local_blocks)
@@ -105,6 +118,7 @@ def minimax_block_scores_decode(q, pay, sf, req_to_token, slot_ids, seq_lens, bl
             seg = sc[:, blk * block_size:min(n, (blk + 1) * block_size)]
             m = seg.max(1)
             val = m if score_type == 'max' else m + np.log2(np.exp2(seg - m[:, None]).sum(1))
+            val = np.where(np.isnan(val), -np.inf, val)
             if local_start <= blk < nb:
                 val = np.full(heads, 1e29)
             elif blk < init_blocks:
@@ -119,13 +133,14 @@ def minimax_block_scores_prefill(q, pay, sf, req_to_token, slot_ids, cu_seqlens,
     position within its block_q tile's range, nan outside the tile's range)."""
     q = np.asarray(q, np.float64)
     total, heads, d = q.shape
-    c = sm_scale * 1.4426950409 * k_scale
+    c = _score_scale(sm_scale, k_scale)
     max_blocks = int(max(-(-int(s) // block_size) for s in seq_lens))
     out = np.full((heads, total, max_blocks), np.nan)
+    slots = len(np.asarray(pay).reshape(-1, pay.shape[-1]))
     for b in range(len(seq_lens)):
         s0, s1 = int(cu_seqlens[b]), int(cu_seqlens[b + 1])
         n, pre = int(seq_lens[b]), int(prefix_lens[b])
-        toks = np.asarray(req_to_token)[int(slot_ids[b]), :n]
+        toks = np.asarray(req_to_token)[(int(slot_ids[b]) + slots) % slots, :n]
         keys = _index_keys(pay, sf, toks)
         for t in range(s1 - s0):
             tile = t // block_q

@@ -41,7 +41,9 @@ def test_attach_scales_and_install():
     seen = []
     registry = SimpleNamespace(register=lambda name, fn, kind: seen.append((name, fn, kind)))
     minimax.install(registry, SimpleNamespace(AROUND='around'))
-    assert seen == [(f'{minimax.OPS}.flash_decode_with_gqa_share_sparse', minimax.decode_main, 'around'),
+    assert seen == [(f'{minimax.OPS}.flash_decode_with_topk_idx', minimax.decode_topk, 'around'),
+                    (f'{minimax.OPS}.flash_decode_with_gqa_share_sparse', minimax.decode_main, 'around'),
+                    (f'{minimax.OPS}.flash_prefill_with_topk_index', minimax.prefill_topk, 'around'),
                     (f'{minimax.OPS}.flash_prefill_with_gqa_share_sparse', minimax.prefill_main, 'around'),
                     (f'{minimax.OPS}.minimax_sparse_prefill', minimax.sparse_prefill, 'around'),
                     (minimax.STORE, minimax.store_kv_index, 'around')]
@@ -78,3 +80,70 @@ def test_enable_fused_store_conditions(monkeypatch):
     monkeypatch.setenv('XTIER_MINIMAX_FP4_FUSED_STORE', '0')
     off = pool()
     assert not minimax.enable_fused_store(off) and not off.use_nvfp4_fused_quantize_store
+
+
+def _fake_sglang(kernel_name, launch_args, launch_kwargs, grid):
+    """A stand-in for the SGLang module whose score kernel the top-k hooks replace: its entry launches
+    ``kernel_name`` of its own module with the given arguments and returns what it saw."""
+    import sys
+    import types
+    mod = types.ModuleType('xt_fake_sglang_topk')
+
+    class Real:
+        def __getitem__(self, g):
+            raise AssertionError('the real score kernel ran')
+    setattr(mod, kernel_name, Real())
+
+    def run(q, k_cache, **kwargs):
+        getattr(mod, kernel_name)[grid](q, k_cache, *launch_args, **launch_kwargs)
+        return 'topk', k_cache.shape, kwargs
+    run.__module__ = mod.__name__
+    sys.modules[mod.__name__] = mod
+    return mod, run
+
+
+def test_decode_topk_hook_routes_the_score_launch(monkeypatch):
+    seen = {}
+    monkeypatch.setattr(minimax.ops, 'minimax_decode_scores', lambda *a, **k: seen.update(args=a, kw=k))
+    pay = torch.zeros(3, 128, 64, dtype=torch.uint8)
+    sc = torch.zeros(3, 128, 8, dtype=torch.uint8)
+    setattr(pay, minimax.TAG, sc)
+    q = torch.zeros(2, 8, 128, dtype=torch.bfloat16)
+    r2t, score, seq, sid = torch.zeros(2, 9), torch.zeros(8, 2, 4), torch.zeros(2), torch.zeros(2)
+    # the launch arguments of SGLang's _decode_score_kernel, as the reference's shim takes them (kv_fp4.py:233-236)
+    args = (r2t, score, seq, sid, 999, 2, 4, 128, 64, 16, 0.1, 1.0, 0, 1, 1024, 128, 1, 0, 0, 0, 9, 8, 4, 1)
+    mod, run = _fake_sglang('_decode_score_kernel', args, dict(NUM_KV_CHUNKS=2, SCORE_TYPE='lse',
+                                                               SKIP_TRIVIAL_TOPK_SCORE=True), (4, 2))
+    kept = mod._decode_score_kernel
+    got = minimax.decode_topk(run, q=q, k_cache=pay, disable_index_value=True, sink=None, topk=16)
+    assert got[0] == 'topk' and got[1] == (384, 1, 128) and got[2] == dict(disable_index_value=True, sink=None,
+                                                                              topk=16)
+    assert mod._decode_score_kernel is kept                        # restored after the call
+    a, k = seen['args'], seen['kw']
+    assert a[:4] == (q, pay, sc, r2t) and a[4] is score and a[7:13] == (64, 0.1, 1.0, 0, 1, 'lse')
+    assert k == dict(skip_topk=16, heads=2 * 4, batch=2, q_strides=(1024, 128, 1), r2t_stride=9,
+                     score_strides=(8, 4, 1))
+    with pytest.raises(NotImplementedError):
+        minimax.decode_topk(run, q=q, k_cache=pay, disable_index_value=False)
+    assert minimax.decode_topk(_original, q=q, k_cache=torch.zeros(1))[0] == 'original'
+
+
+def test_prefill_topk_hook_routes_the_score_launch(monkeypatch):
+    seen = {}
+    monkeypatch.setattr(minimax.ops, 'minimax_prefill_scores', lambda *a, **k: seen.update(args=a, kw=k))
+    pay = torch.zeros(3, 128, 64, dtype=torch.uint8)
+    sc = torch.zeros(3, 128, 8, dtype=torch.uint8)
+    setattr(pay, minimax.TAG, sc)
+    q = torch.zeros(70, 4, 128, dtype=torch.bfloat16)
+    score, r2t, cu, seq, pre, sid = (torch.zeros(1) for _ in range(6))
+    # SGLang's _flash_attn_fwd_with_block_score_kernel arguments (kv_fp4.py:459-462), the score strides and the
+    # req_to_token stride last
+    args = (None, None, score, r2t, cu, seq, pre, sid, 999, 4, 4, 128, 128, 64, 0.2, 1.0, 1.0, None, None, 512, 128,
+            1, 'x', 'y', 300, 75, 1, 77)
+    mod, run = _fake_sglang('_flash_attn_fwd_with_block_score_kernel', (None,) + args,
+                            dict(SCORE_TYPE='max', DISABLE_INDEX_VALUE=True), lambda meta: (2, 4))
+    got = minimax.prefill_topk(run, q=q, k_cache=pay, disable_index_value=True)
+    assert got[0] == 'topk'
+    a, k = seen['args'], seen['kw']
+    assert a[:5] == (q, pay, sc, r2t, score) and a[5:12] == (cu, seq, pre, sid, 64, 0.2, 1.0)
+    assert k == dict(max_q_len=128, heads=4, q_strides=(512, 128, 1), r2t_stride=77, score_strides=(300, 75, 1))

@@ -92,6 +92,10 @@ SIGNATURES = {
                                      ctypes.c_int64, ctypes.c_int64, ctypes.c_int, _P, ctypes.c_int64, ctypes.c_int, _P, _P,
                                      ctypes.c_int64, ctypes.c_int, ctypes.c_int, _P, ctypes.c_int64, _P]),
     'xt_topk_rows': (_I, [_P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, ctypes.c_int64, _P]),
+    'xt_minimax_decode_scores': (_I, [_P, _L, _L, _I, _I, _I, _I, _P, _L, _L, _P, _L, _L, _L, _P, _L, _P, _P, _I, _I,
+                                      ctypes.c_float, _I, _I, _I, _I, _P, _I, _L, _L, _L, _I, _P]),
+    'xt_minimax_prefill_scores': (_I, [_P, _L, _L, _I, _I, _I, _I, _I, _P, _L, _L, _P, _L, _L, _L, _P, _L, _P, _P, _P,
+                                       _P, _I, _I, ctypes.c_float, _P, _I, _L, _L, _L, _P]),
     'xt_ceiling_gather': (_I, [_P, ctypes.c_int64, ctypes.c_int64, _P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, _P,
                                ctypes.c_int, ctypes.c_int, _P, _P]),
     'xt_ceiling_gather_sink_words': (_Z, [ctypes.c_int, ctypes.c_int]),

@@ -20,6 +20,7 @@ the prefill-op hook below serves it.
 import logging
 import math
 import os
+import sys
 
 import torch
 
@@ -90,6 +91,100 @@ def prefill_main(original, *args, **kwargs):
     return ops.fp4_prefill_gqa_share_sparse(**kwargs, k_sc=k_sc, v_sc=scales_of(kwargs['v_cache']))
 
 
+class _DecodeScores:
+    """Takes the place of SGLang's _decode_score_kernel for one flash_decode_with_topk_idx call: ``kernel[grid](...)``
+    with that kernel's launch arguments (the argument list the shim of kv_fp4.py:225-244 receives) runs
+    xt_minimax_decode_scores on the NVFP4 index pool. The BF16 cache SGLang was handed is a shape-only stand-in."""
+
+    def __init__(self, pay, sc):
+        self.pay, self.sc = pay, sc
+
+    def __getitem__(self, grid):
+        def launch(q, _k, req_to_token, score, seq_lens, slot_ids, _max_slots, batch_size, gqa_group_size, _head_dim,
+                   block_size, topk, sm_scale, k_scale, init_blocks, local_blocks, sq0, sq1, sq2, _sk0, _sk1, _sk2,
+                   sr0, ss0, ss1, ss2, NUM_KV_CHUNKS=1, SCORE_TYPE='max', SKIP_TRIVIAL_TOPK_SCORE=False,
+                   IS_FP8=False, **_):
+            if IS_FP8:
+                raise NotImplementedError('xtier_amd.minimax: the NVFP4 index scores read no FP8 index cache')
+            g = grid({'NUM_KV_CHUNKS': NUM_KV_CHUNKS}) if callable(grid) else grid
+            ops.minimax_decode_scores(q, self.pay, self.sc, req_to_token, score, seq_lens, slot_ids, block_size,
+                                      sm_scale, k_scale, init_blocks, local_blocks, SCORE_TYPE,
+                                      skip_topk=topk if SKIP_TRIVIAL_TOPK_SCORE else None,
+                                      heads=g[1] * gqa_group_size, batch=batch_size, q_strides=(sq0, sq1, sq2),
+                                      r2t_stride=sr0, score_strides=(ss0, ss1, ss2))
+        return launch
+
+
+class _PrefillScores:
+    """Takes the place of SGLang's _flash_attn_fwd_with_block_score_kernel for one flash_prefill_with_topk_index call
+    (score only: no index value, no sink, no output; the argument list of the shim at kv_fp4.py:449-472): runs
+    xt_minimax_prefill_scores on the NVFP4 index pool, 64 query rows per grid row as that kernel's grid counts."""
+
+    BLOCK_Q = 64
+
+    def __init__(self, pay, sc):
+        self.pay, self.sc = pay, sc
+
+    def __getitem__(self, grid):
+        def launch(q, _k, _v, sink, o, score, req_to_token, cu_seqlens, seq_lens, prefix_lens, slot_ids, _max_slots,
+                   num_heads, _gqa_group_size, _qk_head_dim, _v_head_dim, block_size_k, sm_scale, k_scale, _v_scale,
+                   _gumbel, _one, sq0, sq1, sq2, *rest, SCORE_TYPE='max', DISABLE_INDEX_VALUE=True, IS_FP8=False,
+                   **_):
+            if IS_FP8 or not DISABLE_INDEX_VALUE or SCORE_TYPE != 'max' or sink is not None or o is not None:
+                raise NotImplementedError('xtier_amd.minimax: the NVFP4 prefill index scores compute the max score '
+                                          'only (no index value, sink or FP8 index cache)')
+            ss0, ss1, ss2, sr0 = rest[-4:]
+            g = grid({'BLOCK_SIZE_Q': self.BLOCK_Q}) if callable(grid) else grid
+            ops.minimax_prefill_scores(q, self.pay, self.sc, req_to_token, score, cu_seqlens, seq_lens, prefix_lens,
+                                       slot_ids, block_size_k, sm_scale, k_scale, max_q_len=g[0] * self.BLOCK_Q,
+                                       heads=num_heads, q_strides=(sq0, sq1, sq2), r2t_stride=sr0,
+                                       score_strides=(ss0, ss1, ss2))
+        return launch
+
+
+def _run_with_scores(run, kernel_name, scores, q, pay, kwargs):
+    """Calls SGLang's ``run`` (its own chunking, score buffer and top-k) with ``kernel_name`` of its module replaced by
+    ``scores`` for the call, and a shape-only BF16 stand-in of the index cache [slots, 1, dim]."""
+    module = sys.modules[run.__module__]
+    stand_in = torch.empty((1, 1, 1), dtype=q.dtype, device=q.device).expand(pay.shape[0] * pay.shape[1], 1,
+                                                                                pay.shape[2] * 2)
+    kept = getattr(module, kernel_name)
+    setattr(module, kernel_name, scores)
+    try:
+        return run(q=q, k_cache=stand_in, **kwargs)
+    finally:
+        setattr(module, kernel_name, kept)
+
+
+def _index_call(kwargs, what):
+    if not kwargs.get('disable_index_value') or kwargs.get('sink') is not None:
+        raise NotImplementedError(f'xtier_amd.minimax: {what} on the NVFP4 index cache computes scores only '
+                                  '(disable_index_value, no sink)')
+    q, pay = kwargs.pop('q'), kwargs.pop('k_cache')
+    return q, pay
+
+
+def decode_topk(original, *args, **kwargs):
+    """AROUND flash_decode_with_topk_idx (kv_fp4.py:572-576, :247-265): on a tagged index cache, SGLang's own call
+    with the index scores from xt_minimax_decode_scores; ``original`` untouched otherwise."""
+    sc = scales_of(kwargs.get('k_cache'))
+    if sc is None:
+        return original(*args, **kwargs)
+    q, pay = _index_call(kwargs, 'flash_decode_with_topk_idx')
+    return _run_with_scores(original, '_decode_score_kernel', _DecodeScores(pay, sc), q, pay, kwargs)
+
+
+def prefill_topk(original, *args, **kwargs):
+    """AROUND flash_prefill_with_topk_index (kv_fp4.py:593-598, :475-494): as ``decode_topk``, with the prefill
+    scores from xt_minimax_prefill_scores."""
+    sc = scales_of(kwargs.get('k_cache'))
+    if sc is None:
+        return original(*args, **kwargs)
+    q, pay = _index_call(kwargs, 'flash_prefill_with_topk_index')
+    return _run_with_scores(original, '_flash_attn_fwd_with_block_score_kernel', _PrefillScores(pay, sc), q, pay,
+                            kwargs)
+
+
 def _copy_rows(k_cache, idx_k_cache, idx_v_cache, slot_ids, max_seqlen_k, kwargs):
     """Rows per request of the BF16 context copies, or None when the call stays on the NVFP4 views: an untagged
     cache, a separate index V cache or a loc_mapping (forms the copy does not cover), or copies over the budget."""
@@ -148,7 +243,9 @@ def enable_fused_store(pool):
     return bool(pool.use_nvfp4_fused_quantize_store)
 
 
-HOOKS = ((f'{OPS}.flash_decode_with_gqa_share_sparse', decode_main),
+HOOKS = ((f'{OPS}.flash_decode_with_topk_idx', decode_topk),
+         (f'{OPS}.flash_decode_with_gqa_share_sparse', decode_main),
+         (f'{OPS}.flash_prefill_with_topk_index', prefill_topk),
          (f'{OPS}.flash_prefill_with_gqa_share_sparse', prefill_main),
          (f'{OPS}.minimax_sparse_prefill', sparse_prefill),
          (STORE, store_kv_index))

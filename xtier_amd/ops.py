@@ -850,3 +850,100 @@ def dsa_paged_mqa_logits(q_fp8, kvcache_fp8, weights, context_lens, block_table,
                                                 int(bool(clean_logits)), _ptr(out), out.stride(0), _stream(q))
     _lib.check(status, 'dsa_paged_mqa_logits')
     return out
+
+
+_SCORE_DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+
+def _f32(x):
+    return ctypes.c_float(float(x)).value
+
+
+def minimax_score_factor(sm_scale, k_scale):
+    """The FP32 factor of the MiniMax index scores, formed as the reference's kernels form it:
+    (sm_scale * 1.4426950409) * k_scale, each product rounded to FP32 (kv_fp4.py:181, :208)."""
+    return _f32(_f32(_f32(sm_scale) * _f32(1.4426950409)) * _f32(k_scale))
+
+
+def _index_bits(*arrays):
+    """The index_int64 mask of the block-score entry points: bit i set when array i is int64 (else int32)."""
+    bits = 0
+    for i, t in enumerate(arrays):
+        if t is None:
+            continue
+        if t.dtype == torch.int64:
+            bits |= 1 << i
+        elif t.dtype != torch.int32:
+            raise ValueError(f'xtier_amd.minimax scores: index arrays are int32 or int64, got {t.dtype}')
+    return bits
+
+
+def _index_pool(pay, sc, what):
+    """The MiniMax index pool views: payload [pages, 128, dim/2] and scale bytes [pages, 128, dim/16], unit stride
+    within a slot row."""
+    sc = sc.view(torch.uint8) if sc.dtype != torch.uint8 else sc
+    pay = pay.view(torch.uint8) if pay.dtype != torch.uint8 else pay
+    if (pay.dim() != 3 or sc.dim() != 3 or pay.shape[:2] != sc.shape[:2] or pay.shape[1] != 128
+            or pay.stride(2) != 1 or sc.stride(2) != 1 or sc.shape[2] * 8 != pay.shape[2]):
+        raise ValueError(f'xtier_amd.{what}: index pool views [pages, 128, dim/2] and [pages, 128, dim/16] expected, '
+                         f'got {tuple(pay.shape)} and {tuple(sc.shape)}')
+    _need_cuda(pay, sc)
+    return pay, sc
+
+
+def minimax_decode_scores(q, idx_pay, idx_sc, req_to_token, score, seq_lens, slot_ids, block_size, sm_scale, k_scale,
+                          init_blocks, local_blocks, score_type='max', skip_topk=None, heads=None, batch=None,
+                          q_strides=None, r2t_stride=None, score_strides=None):
+    """The MiniMax decode index scores (_fp4_decode_score_kernel, kv_fp4.py:168-222) into ``score``
+    [heads, batch, blocks] (FP32 / BF16 / FP16): q [batch, heads, dim] BF16 / FP16 against the NVFP4 index pool.
+    Strides default to the tensors' own; ``skip_topk``: requests with at most that many blocks get no scores."""
+    pay, sc = _index_pool(idx_pay, idx_sc, 'minimax_decode_scores')
+    if q.dtype not in _DTYPES or score.dtype not in _SCORE_DTYPES:
+        raise ValueError('xtier_amd.minimax_decode_scores: BF16 / FP16 queries and FP32 / BF16 / FP16 scores')
+    if score_type not in ('max', 'lse'):
+        raise ValueError(f'xtier_amd.minimax_decode_scores: score_type {score_type!r} (max or lse)')
+    _need_cuda(q, req_to_token, score, seq_lens, slot_ids)
+    batch = q.shape[0] if batch is None else int(batch)
+    dim = q.shape[2]
+    heads = q.shape[1] if heads is None else int(heads)
+    sq = q_strides or q.stride()
+    if sq[2] != 1:
+        raise ValueError('xtier_amd.minimax_decode_scores: the query head dimension must be contiguous')
+    ss = score_strides or score.stride()
+    hint = -(-req_to_token.shape[1] // int(block_size))
+    status = _lib.lib().xt_minimax_decode_scores(
+        _ptr(q), sq[0], sq[1], batch, heads, dim, _DTYPES[q.dtype], _ptr(pay), pay.stride(0), pay.stride(1), _ptr(sc),
+        sc.stride(0), sc.stride(1), pay.shape[0] * 128, _ptr(req_to_token),
+        req_to_token.stride(0) if r2t_stride is None else r2t_stride, _ptr(seq_lens), _ptr(slot_ids),
+        _index_bits(req_to_token, seq_lens, slot_ids), int(block_size), minimax_score_factor(sm_scale, k_scale),
+        int(init_blocks), int(local_blocks), -1 if skip_topk is None else int(skip_topk), int(score_type == 'lse'),
+        _ptr(score), _SCORE_DTYPES[score.dtype], ss[0], ss[1], ss[2], hint, _stream(q))
+    _lib.check(status, 'minimax_decode_scores')
+    return score
+
+
+def minimax_prefill_scores(q, idx_pay, idx_sc, req_to_token, score, cu_seqlens, seq_lens, prefix_lens, slot_ids,
+                           block_size, sm_scale, k_scale, max_q_len, heads=None, q_strides=None, r2t_stride=None,
+                           score_strides=None):
+    """The MiniMax prefill index scores (_fp4_index_score_kernel, kv_fp4.py:407-446) into ``score``
+    [heads, total_q, blocks]: q [total_q, heads, dim] BF16 / FP16; causal, each row's blocks bounded by its 64-row
+    tile. ``max_q_len`` bounds every request's query count."""
+    pay, sc = _index_pool(idx_pay, idx_sc, 'minimax_prefill_scores')
+    if q.dtype not in _DTYPES or score.dtype not in _SCORE_DTYPES:
+        raise ValueError('xtier_amd.minimax_prefill_scores: BF16 / FP16 queries and FP32 / BF16 / FP16 scores')
+    _need_cuda(q, req_to_token, score, cu_seqlens, seq_lens, prefix_lens, slot_ids)
+    dim = q.shape[2]
+    heads = q.shape[1] if heads is None else int(heads)
+    sq = q_strides or q.stride()
+    if sq[2] != 1:
+        raise ValueError('xtier_amd.minimax_prefill_scores: the query head dimension must be contiguous')
+    ss = score_strides or score.stride()
+    status = _lib.lib().xt_minimax_prefill_scores(
+        _ptr(q), sq[0], sq[1], cu_seqlens.shape[0] - 1, heads, dim, _DTYPES[q.dtype], int(max_q_len), _ptr(pay),
+        pay.stride(0), pay.stride(1), _ptr(sc), sc.stride(0), sc.stride(1), pay.shape[0] * 128, _ptr(req_to_token),
+        req_to_token.stride(0) if r2t_stride is None else r2t_stride, _ptr(cu_seqlens), _ptr(seq_lens),
+        _ptr(prefix_lens), _ptr(slot_ids), _index_bits(req_to_token, seq_lens, slot_ids, prefix_lens, cu_seqlens),
+        int(block_size), minimax_score_factor(sm_scale, k_scale), _ptr(score), _SCORE_DTYPES[score.dtype], ss[0],
+        ss[1], ss[2], _stream(q))
+    _lib.check(status, 'minimax_prefill_scores')
+    return score
