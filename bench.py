@@ -709,6 +709,202 @@ def varlen_cpu(q, kv, w, scale, seconds):
                        'numpy split-K softmax attention with FP64 merge')
 
 
+INDEXER_WORKLOADS = {
+    # QSA indexer prefill logits deep in a 380K prompt: 352 rows x 95088 compressed keys, 4 heads x 128, BF16 (the
+    # first case of the reference's tests/qsa_prefill_check.py:25-53; 2.40 -> 0.61 ms on an RTX PRO 5000,
+    # docs/reports/2026-10-23-prefill.md:48-53)
+    'qsa_logits_352x95088': dict(kind='qsa', rows=352, heads=4, dim=128, prefix=380000, ratio=4),
+    # DSA indexer prefill logits: 4096 queries x 16384 keys, 32 heads x 128, FP8 E4M3 with FP32 key scales and head
+    # weights (the shapes of the reference's tests/glm_indexer_torch_check.py:27-43, at prefill size)
+    'dsa_logits_4096x16384': dict(kind='dsa', num_q=4096, heads=32, dim=128, num_kv=16384),
+    # top-2048 selection over the QSA case's logits (352 rows x 95088 columns)
+    'topk_352x95088_k2048': dict(kind='topk', rows=352, cols=95088, topk=2048),
+    # MiniMax decode index scores: batch 32, context 32768, 4 index heads x 128 over the NVFP4 index pool, blocks of
+    # 128 (the shapes of tests/minimax_kv_fp4_check.py:29, :81-108 at batch 32)
+    'minimax_decode_scores_b32': dict(kind='mm_decode', batch=32, ctx=32768, heads=4, dim=128, block=128),
+    # MiniMax prefill index scores: one 8192-token prompt, 4 index heads x 128, blocks of 128
+    'minimax_prefill_scores_8k': dict(kind='mm_prefill', ext=8192, heads=4, dim=128, block=128),
+}
+
+
+def run_indexer(args, name, ops):
+    """The top-k producers: the QSA and DSA indexer logits, the top-k selection and the MiniMax index block scores,
+    each timed over exactly K launches (HIP graphs), against the bound its algorithmic bytes or flops set."""
+    import numpy as np
+    import torch
+
+    from oracle import topk as ref
+
+    torch.cuda.set_device(0)
+    cfg = INDEXER_WORKLOADS[name]
+    kind = cfg['kind']
+    gen = torch.Generator(device='cuda').manual_seed(20261023)
+    seconds = float(os.environ.get('XT_CPU_SAMPLE_S', '10'))
+
+    def bf16(*shape, std=1.0):
+        return (torch.randn(*shape, device='cuda', generator=gen) * std).bfloat16()
+
+    if kind == 'qsa':
+        rows, heads, dim = cfg['rows'], cfg['heads'], cfg['dim']
+        keys = (cfg['prefix'] + rows) // cfg['ratio']
+        q, k = bf16(rows, heads, dim), bf16(keys, 1, dim)
+        starts = torch.zeros(rows, dtype=torch.int32, device='cuda')
+        ends = ((torch.arange(cfg['prefix'], cfg['prefix'] + rows, device='cuda') + 1) // cfg['ratio']).int()
+        out = torch.empty(rows, keys, device='cuda')
+        lib = ops._lib.lib()
+
+        def step(_):
+            ops._lib.check(lib.xt_qsa_indexer_logits(q.data_ptr(), q.stride(0), q.stride(1), rows, heads, dim,
+                                                     k.data_ptr(), k.stride(0), keys, starts.data_ptr(),
+                                                     ends.data_ptr(), math.sqrt(dim), ops._lib.XT_DTYPE_BF16,
+                                                     out.data_ptr(), out.stride(0),
+                                                     torch.cuda.current_stream().cuda_stream), 'qsa')
+        nbytes = q.numel() * 2 + k.numel() * 2 + rows * keys * 4 + rows * 8
+        flops = 2 * rows * heads * keys * dim
+        conf = {'rows': rows, 'keys': keys, 'heads': heads, 'dim': dim, 'dtype': 'bf16'}
+        qh, kh, eh = q.float().cpu().numpy(), k[:, 0].float().cpu().numpy(), ends.cpu().numpy()
+
+        def cpu(n):
+            ref.qsa_indexer_logits(qh[:n], kh, np.zeros(n, np.int64), eh[:n])
+        cpu_total, cpu_unit = rows, 'rows'
+    elif kind == 'dsa':
+        nq, heads, dim, nkv = cfg['num_q'], cfg['heads'], cfg['dim'], cfg['num_kv']
+        q = (torch.randn(nq, heads, dim, device='cuda', generator=gen) * 2).to(torch.float8_e4m3fn)
+        k = (torch.randn(nkv, dim, device='cuda', generator=gen) * 2).to(torch.float8_e4m3fn)
+        ksc = torch.rand(nkv, device='cuda', generator=gen) + 0.5
+        w = torch.randn(nq, heads, device='cuda', generator=gen)
+        ks = torch.zeros(nq, dtype=torch.int32, device='cuda')
+        ke = torch.full((nq,), nkv, dtype=torch.int32, device='cuda')
+
+        def step(_):
+            ops.dsa_mqa_logits(q, (k, ksc), w, ks, ke)
+        ld = (nkv + 3) // 4 * 4
+        nbytes = q.numel() + k.numel() + nkv * 4 + w.numel() * 4 + nq * ld * 4
+        flops = 2 * nq * heads * nkv * dim
+        conf = {'num_q': nq, 'num_kv': nkv, 'heads': heads, 'dim': dim, 'dtype': 'e4m3'}
+        qh, kh, kch, wh = q.float().cpu().numpy(), k.float().cpu().numpy(), ksc.cpu().numpy(), w.cpu().numpy()
+
+        def cpu(n):
+            ref.dsa_mqa_logits(qh[:n], kh, kch, wh[:n], np.zeros(n, np.int64), np.full(n, nkv))
+        cpu_total, cpu_unit = nq, 'queries'
+    elif kind == 'topk':
+        rows, cols, kk = cfg['rows'], cfg['cols'], cfg['topk']
+        x = torch.randn(rows, cols, device='cuda', generator=gen)
+        out = torch.empty(rows, kk, dtype=torch.int32, device='cuda')
+
+        def step(_):
+            ops.topk_rows(x, kk, out=out)
+        nbytes = rows * cols * 4 + rows * kk * 4
+        flops = 0
+        conf = {'rows': rows, 'cols': cols, 'topk': kk, 'dtype': 'f32'}
+        xh = x.cpu().numpy()
+
+        def cpu(n):
+            ref.topk_rows(xh[:n], kk)
+        cpu_total, cpu_unit = rows, 'rows'
+    else:
+        page = 128
+        heads, dim, bs = cfg['heads'], cfg['dim'], cfg['block']
+        if kind == 'mm_decode':
+            batch, ctx = cfg['batch'], cfg['ctx']
+            lens, pre, ext = [ctx] * batch, [0] * batch, None
+        else:
+            batch, ext = 1, [cfg['ext']]
+            lens, pre = ext, [0]
+        blocks = [-(-n // page) for n in lens]
+        pages = sum(blocks) + 1
+        perm = torch.randperm(pages - 1, device='cuda', generator=gen) + 1
+        width = max(blocks) * page
+        r2t = torch.zeros(batch, width, dtype=torch.int32, device='cuda')
+        off = 0
+        for r, n in enumerate(blocks):
+            pg = perm[off:off + n].int()
+            r2t[r, :n * page] = (pg[:, None] * page + torch.arange(page, device='cuda', dtype=torch.int32)).view(-1)
+            off += n
+        pay = torch.randint(0, 256, (pages, page, dim // 2), device='cuda', generator=gen, dtype=torch.uint8)
+        sc = torch.randint(0x28, 0x40, (pages, page, dim // 16), device='cuda', generator=gen, dtype=torch.uint8)
+        seq = torch.tensor(lens, dtype=torch.int32, device='cuda')
+        sid = torch.arange(batch, dtype=torch.int32, device='cuda')
+        nblk = -(-max(lens) // bs)
+        if kind == 'mm_decode':
+            q = bf16(batch, heads, dim)
+            score = torch.empty(heads, batch, nblk, device='cuda')
+
+            def step(_):
+                ops.minimax_decode_scores(q, pay, sc, r2t, score, seq, sid, bs, dim ** -0.5, 1.0, 0, 1)
+            keys = sum(lens)
+            nbytes = keys * (dim // 2 + dim // 16 + 4) + q.numel() * 2 + score.numel() * 4
+            flops = 2 * keys * heads * dim
+            conf = {'batch': batch, 'context': ctx, 'heads': heads, 'dim': dim, 'block': bs, 'dtype': 'bf16'}
+
+            def cpu(n):
+                ref.minimax_block_scores_decode(qh[:n], payh, sch, r2th, np.arange(n), lens[:n], bs, dim ** -0.5,
+                                                1.0, 0, 1)
+            cpu_total, cpu_unit = batch, 'requests'
+        else:
+            total = ext[0]
+            q = bf16(total, heads, dim)
+            score = torch.empty(heads, total, nblk, device='cuda')
+            cu = torch.tensor([0, total], dtype=torch.int32, device='cuda')
+            pre_t = torch.zeros(1, dtype=torch.int32, device='cuda')
+
+            def step(_):
+                ops.minimax_prefill_scores(q, pay, sc, r2t, score, cu, seq, pre_t, sid, bs, dim ** -0.5, 1.0, total)
+            # the keys each row's 64-row tile visits, every head
+            visited = sum(min(total, 64 * (t // 64 + 1)) for t in range(total))
+            nbytes = total * heads * dim * 2 + sum(lens) * (dim // 2 + dim // 16 + 4) + total * heads * nblk * 4
+            flops = 2 * visited * heads * dim
+            conf = {'prompt': total, 'heads': heads, 'dim': dim, 'block': bs, 'dtype': 'bf16'}
+
+            def cpu(n):
+                # the prompt's last n rows (prefix total - n), each against its causal keys
+                ref.minimax_block_scores_prefill(qh[total - n:], payh, sch, r2th, [0], [0, n], [total], [total - n],
+                                                 bs, dim ** -0.5, 1.0)
+
+            def cpu_work(n):
+                # keys visited by the last n rows, as a fraction of the whole prompt's
+                return sum(min(total, total - n + 64 * (t // 64 + 1)) for t in range(n)) / visited
+            cpu_total, cpu_unit = total, 'prompt rows (the last ones, scaled by the keys they visit)'
+        qh, payh, sch, r2th = q.float().cpu().numpy(), pay.cpu().numpy(), sc.cpu().numpy(), r2t.cpu().numpy()
+    steps = max(1, args.steps)
+    ms, per = time_steps(step, 1, steps, max(1, args.warmup))
+    t = ms * 1e-3
+    gbs, tflops = nbytes / t / 1e9, flops / t / 1e12
+    t_hbm, t_mfma = nbytes / (HBM_PEAK_GBS * 1e9), flops / (MFMA_PEAK_TFLOPS * 1e12)
+    bound = 'mfma' if t_mfma > t_hbm else 'hbm'
+    if bound == 'mfma':
+        roof = {'bound': 'mfma', 'achieved': round(tflops, 1), 'peak': MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
+                'frac': round(tflops / MFMA_PEAK_TFLOPS, 4), 'traffic': None}
+    else:
+        roof = {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+                'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None}
+    log(f'{name}: {ms * 1e3:.1f} us per launch, {gbs:.0f} GB/s, {tflops:.1f} TFLOP/s ({bound}-bound, '
+        f'{roof["frac"]:.1%} of peak)')
+    # CPU baseline: the oracle on a bounded prefix of the rows, one thread
+    from threadpoolctl import threadpool_limits
+    with threadpool_limits(1):
+        t0 = time.perf_counter()
+        cpu(1)
+        one = time.perf_counter() - t0
+        n = int(max(1, min(cpu_total, seconds / max(one, 1e-6))))
+        t0 = time.perf_counter()
+        cpu(n)
+        dt = time.perf_counter() - t0
+    frac = cpu_work(n) if kind == 'mm_prefill' else n / cpu_total
+    cpu_ms = dt / frac * 1e3
+    record = {'metric': f'{name} µs per launch', 'value': round(ms * 1e3, 3), 'unit': 'µs', 'n_gpus': 1,
+              'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per),
+              'higher_is_better': False, 'scaling': 'weak', 'vs_baseline': None, 'dtype': conf.pop('dtype'),
+              'data': 'synthetic', 'config': dict(workload=name, **conf),
+              'algorithmic_bytes': nbytes, 'algorithmic_flops': flops,
+              'roofline': roof,
+              'cpu_baseline': {'value': round(cpu_ms * 1e3, 1), 'unit': 'µs per launch (extrapolated)', 'cores': 1,
+                               'kind': 'port',
+                               'sample': f'{n} of {cpu_total} {cpu_unit}: the numpy oracle (oracle/topk.py) on one '
+                                         f'thread of {cpu_model()}, scaled to the whole launch'}}
+    print(json.dumps(record), flush=True)
+
+
 CEILING_WORKLOADS = ('mfma_ceiling', 'gather_ceiling_b32')
 
 
@@ -780,7 +976,9 @@ def main():
     p.add_argument('--workload', default='gqa_decode_b32',
                    help='gqa_decode_b32 (default), cpu_ref_decode, long_ctx_decode_b4, gqa_prefill_chunk4096, '
                         'minimax_decode_b32, minimax_prefill_chunk4096, qsa_varlen_b32, qsa_gather_b32, qsa_pack_ctx65536, '
-                        'mla_decode_b64, mla_prefill_2048, mla_v4_decode_b64, or the ceilings mfma_ceiling and '
+                        'mla_decode_b64, mla_prefill_2048, mla_v4_decode_b64, the top-k producers '
+                        'qsa_logits_352x95088, dsa_logits_4096x16384, topk_352x95088_k2048, '
+                        'minimax_decode_scores_b32, minimax_prefill_scores_8k, or the ceilings mfma_ceiling and '
                         'gather_ceiling_b32')
     p.add_argument('--layers', type=int, default=16)
     p.add_argument('--splits', type=int, default=None)
@@ -816,6 +1014,8 @@ def main():
 
     if args.workload in CEILING_WORKLOADS:
         return run_ceiling(args, args.workload, ops, workloads)
+    if args.workload in INDEXER_WORKLOADS:
+        return run_indexer(args, args.workload, ops)
     if args.workload in workloads.VARLEN_WORKLOADS:
         return run_varlen(args, workloads.VARLEN_WORKLOADS[args.workload], ops, workloads)
     if args.workload in workloads.BLOCK_WORKLOADS:

@@ -31,8 +31,10 @@ def qsa_indexer_logits(q, k, starts, ends, score_scale=None):
     k = np.asarray(k, np.float64)
     rows, heads, dim = q.shape
     scale = score_scale or math.sqrt(dim)
-    s = np.einsum('rhd,nd->rnh', q, k)
-    logits = np.maximum(s, 0.0).sum(-1) / scale
+    logits = np.zeros((rows, k.shape[0]))
+    for h in range(heads):                      # one head's [rows, keys] products at a time
+        logits += np.maximum(q[:, h] @ k.T, 0.0)
+    logits /= scale
     cols = np.arange(k.shape[0])[None, :]
     keep = (cols >= np.asarray(starts)[:, None]) & (cols < np.asarray(ends)[:, None])
     return np.where(keep, logits, -np.inf)

@@ -67,6 +67,28 @@ def test_qsa_indexer_logits(rows, heads, dim, keys, dtype):
     assert (err <= bound).all(), float((err / bound).max())
 
 
+@pytest.mark.parametrize('rows,prefix', [(352, 380000), (1000, 100000), (64, 8192), (4096, 30000), (37, 500000)])
+def test_qsa_indexer_logits_reference_cases(rows, prefix):
+    """The cases of tests/qsa_prefill_check.py:25-53: 4 heads x 128, compressed keys (ratio 4) up to the last row, each
+    row's range [0, (pos + 1) / 4)."""
+    g = torch.Generator().manual_seed(20261023 + rows)
+    keys = (prefix + rows) // 4
+    q = torch.randn(rows, 4, 128, generator=g).bfloat16()
+    k = torch.randn(keys, 1, 128, generator=g).bfloat16()
+    starts = torch.zeros(rows, dtype=torch.int32)
+    ends = ((torch.arange(prefix, prefix + rows) + 1) // 4).to(torch.int32)
+    got = ops.qsa_indexer_logits(q.cuda(), k.cuda(), starts.cuda(), ends.cuda()).cpu().numpy()
+    qn, kn = q.float().numpy().astype(np.float64), k[:, 0].float().numpy().astype(np.float64)
+    want = ref.qsa_indexer_logits(qn, kn, starts.numpy(), ends.numpy())
+    fin = np.isfinite(want)
+    assert np.array_equal(np.isinf(got), ~fin) and not np.isnan(got).any()
+    a = np.zeros(want.shape)
+    for h in range(4):
+        a += np.abs(qn[:, h]) @ np.abs(kn).T
+    bound = (130 + 4 + 2) * 2.0 ** -24 * a / math.sqrt(128) + np.abs(want) * 2.0 ** -24
+    assert (np.abs(got.astype(np.float64)[fin] - want[fin]) <= bound[fin]).all()
+
+
 def test_qsa_prefill_hook():
     calls = []
     original = lambda *a: calls.append(a) or 'original'
