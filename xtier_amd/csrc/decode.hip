@@ -420,23 +420,30 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
   const int64_t irow = a.idx_rows ? uniform_load(a.idx_rows + row) : row;
   const int32_t* ip = a.indices + irow * a.idx_stride + (int64_t)kvg * a.idx_head_stride;
   const int bmask = (1 << a.block_shift) - 1;
+  // Loads that are not needed read a valid stand-in address (the row's length) instead of sitting in a branch:
+  // a branch around a load compiles to a wait right after it, which would serialize the batch.
+  const int32_t* len_p = a.seq_lens + row;
   int32_t pos[kSlotBatch];
 #pragma unroll
   for (int b = 0; b < kSlotBatch; ++b) {
     const int i = b * kThreads + (int)threadIdx.x, k = t0 + i;
-    const int32_t e = (i < kmax) ? ip[k >> a.block_shift] : -1;
+    const int32_t e0 = *((i < kmax) ? ip + (k >> a.block_shift) : len_p);
+    const int32_t e = (i < kmax) ? e0 : -1;
     pos[b] = e < 0 ? -1 : (e << a.block_shift) + (k & bmask);
   }
-  // the row's count, length, causal limit and table row: scalar loads from addresses valid whether or not the
-  // optional arrays are given (a missing one reads the row's length and is ignored), so none waits in a branch
-  const int32_t* len_p = a.seq_lens + row;
+  // the row's count, length, causal limit and table row, and the global scales: scalar loads from addresses valid
+  // whether or not the optional arrays are given (a missing one reads the row's length and is ignored), so none waits
+  // in a branch. The scales are read here, not next to their first use: a vector load issued after the K/V loads
+  // would make the first softmax step wait for all of them.
   const int32_t* req_p = a.row_req ? reinterpret_cast<const int32_t*>(a.row_req + row) : len_p;
   int32_t len_v = uniform_load(len_p);
   int32_t cnt_v = uniform_load(a.counts ? a.counts + row : len_p);
   int32_t qpos_v = uniform_load(a.query_pos ? a.query_pos + row : len_p);
   int32_t req_lo = uniform_load(req_p), req_hi = uniform_load(a.row_req ? req_p + 1 : len_p);
-  // every use below follows this asm, so the five loads issue together behind one wait
-  asm volatile("" : "+s"(len_v), "+s"(cnt_v), "+s"(qpos_v), "+s"(req_lo), "+s"(req_hi));
+  float gk_v = a.gk ? uniform_load_f32(a.gk) : a.gk_val;
+  float gv_v = a.gv ? uniform_load_f32(a.gv) : a.gv_val;
+  // every use below follows this asm, so the seven loads issue together behind one wait
+  asm volatile("" : "+s"(len_v), "+s"(cnt_v), "+s"(qpos_v), "+s"(req_lo), "+s"(req_hi), "+s"(gk_v), "+s"(gv_v));
   const int count = a.counts ? min(cnt_v, a.topk) : a.topk;
   const int n = max(0, min(t0 + a.keys_per_split, count) - t0);
   const int slice_steps = (((n + kStep - 1) / kStep + kSlices * P - 1) / (kSlices * P)) * P;
@@ -459,7 +466,10 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
         toff[b] = a.page_shift >= 0 ? (tpos >> a.page_shift) : tpos / a.page_size;
       }
 #pragma unroll
-      for (int b = 0; b < kSlotBatch; ++b) ent[b] = ok[b] ? tp[toff[b]] : -1;
+      for (int b = 0; b < kSlotBatch; ++b) {
+        const int32_t t = *(ok[b] ? tp + toff[b] : len_p);
+        ent[b] = ok[b] ? t : -1;
+      }
 #pragma unroll
       for (int b = 0; b < kSlotBatch; ++b) {
         const int i = i0 + b * kThreads + (int)threadIdx.x;
@@ -476,7 +486,8 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
 #pragma unroll
       for (int b = 0; b < kSlotBatch; ++b) {   // splits longer than kSlotBatch * kThreads keys
         const int i = i0 + b * kThreads + (int)threadIdx.x, k = t0 + i;
-        const int32_t e = (i < kmax) ? ip[k >> a.block_shift] : -1;
+        const int32_t e0 = *((i < kmax) ? ip + (k >> a.block_shift) : len_p);
+        const int32_t e = (i < kmax) ? e0 : -1;
         pos[b] = e < 0 ? -1 : (e << a.block_shift) + (k & bmask);
       }
     }
@@ -518,7 +529,7 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
     Step<D> buf[P];
 #pragma unroll
     for (int p = 0; p < P; ++p) load_step<D, PS>(w, p, buf[p]);
-    const float gk = a.gk ? *a.gk : a.gk_val;
+    const float gk = gk_v;
     int s0 = 0;
     for (; s0 + P < slice_steps; s0 += P) {
 #pragma unroll
@@ -552,7 +563,7 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
   float* row_part = a.part + (int64_t)row * a.splits * a.q_heads * G::kPartStride;
   const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
       row_part, (short)0, a.splits > 1 ? (int)((int64_t)a.splits * a.q_heads * G::kPartStride * 4) : 0, 0x00020000);
-  const float gv = a.gv ? *a.gv : a.gv_val;
+  const float gv = gv_v;
   constexpr int kParts = 8 * G::kNT;   // 4-dim pieces per lane
 #pragma unroll
   for (int u = (int)threadIdx.x; u < HPW * 64 * kParts; u += kThreads) {

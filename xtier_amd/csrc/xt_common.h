@@ -85,6 +85,9 @@ __device__ inline half8_t fp8x8_to_f16(uint64_t v) {
 __device__ inline int32_t uniform_load(const int32_t* p) {
   return *(const __attribute__((address_space(4))) int32_t*)(p);
 }
+__device__ inline float uniform_load_f32(const float* p) {
+  return *(const __attribute__((address_space(4))) float*)(p);
+}
 // Maximum and sum of x over lanes l, l ^ 16 and l ^ 32 (the four lanes 16 apart), in VALU permutes: with x as both
 // operands, v_permlane16_swap / v_permlane32_swap hand every lane the pair (x[l], x[l ^ 16]) / (x[l], x[l ^ 32]),
 // in an order that does not matter here (ds_bpermute would take two LDS round trips).
@@ -111,6 +114,7 @@ __device__ half2_t fp8x2_to_f16(uint32_t packed);
 __device__ half8_t fp8x8_to_f16(uint64_t v);
 __device__ float max4_lanes16(float x);
 __device__ int32_t uniform_load(const int32_t* p);
+__device__ float uniform_load_f32(const float* p);
 __device__ float sum4_lanes16(float x);
 #endif
 
