@@ -905,7 +905,7 @@ def run_indexer(args, name, ops):
     print(json.dumps(record), flush=True)
 
 
-CEILING_WORKLOADS = ('mfma_ceiling', 'gather_ceiling_b32')
+CEILING_WORKLOADS = ('mfma_ceiling', 'gather_ceiling_b32', 'gather_pieces_ceiling_b32')
 
 
 def run_ceiling(args, name, ops, workloads):
@@ -945,22 +945,31 @@ def run_ceiling(args, name, ops, workloads):
              for _ in range(args.layers)]
     pt = workloads.page_table(w.batch, w.ctx, w.page, gen, 'cuda')
     idx = workloads.index_lists(w.batch, w.ctx, w.topk, gen, 'cuda', w.index_mode)
-    sink = torch.empty(int(ops._lib.lib().xt_ceiling_gather_sink_words(w.batch, w.topk)), dtype=torch.int32,
-                       device='cuda')
+    pieces = name == 'gather_pieces_ceiling_b32'
+    splits = args.splits or 2
+    words = (w.batch * 4 * splits * 512 if pieces else
+             int(ops._lib.lib().xt_ceiling_gather_sink_words(w.batch, w.topk)))
+    sink = torch.empty(words, dtype=torch.int32, device='cuda')
 
     def step(layer):
-        ops.ceiling_gather(pools[layer], pt, idx, w.page, sink=sink)
+        if pieces:
+            ops.ceiling_gather_pieces(pools[layer], pt, idx, w.page, splits, sink=sink)
+        else:
+            ops.ceiling_gather(pools[layer], pt, idx, w.page, sink=sink)
 
     ms, per = time_steps(step, args.layers, steps, max(1, args.warmup))
     nbytes = w.batch * w.topk * 576
     gbs = nbytes / (ms * 1e-3) / 1e9
-    log(f'gather ceiling: {ms * 1e3:.2f} us per layer-step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of '
+    log(f'{name}: {ms * 1e3:.2f} us per layer-step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of '
         f'{HBM_PEAK_GBS:.0f})')
-    record = {'metric': 'decode gather pattern alone, GB/s', 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1,
+    what = ('decode gather pattern alone, per-head pieces as the decode reads them' if pieces else
+            'decode gather pattern alone, whole records')
+    record = {'metric': f'{what}, GB/s', 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1,
               'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per),
               'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'u8', 'data': 'synthetic',
               'config': {'workload': name, 'batch': w.batch, 'context': w.ctx, 'topk': w.topk, 'page': w.page,
-                         'record_bytes': 576, 'layers_rotated': args.layers},
+                         'record_bytes': 576, 'layers_rotated': args.layers,
+                         **({'splits': splits, 'kv_heads_per_workgroup': 1} if pieces else {})},
               'us_per_layer_step': round(ms * 1e3, 3),
               'roofline': {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                            'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None},
@@ -978,8 +987,8 @@ def main():
                         'minimax_decode_b32, minimax_prefill_chunk4096, qsa_varlen_b32, qsa_gather_b32, qsa_pack_ctx65536, '
                         'mla_decode_b64, mla_prefill_2048, mla_v4_decode_b64, the top-k producers '
                         'qsa_logits_352x95088, dsa_logits_4096x16384, topk_352x95088_k2048, '
-                        'minimax_decode_scores_b32, minimax_prefill_scores_8k, or the ceilings mfma_ceiling and '
-                        'gather_ceiling_b32')
+                        'minimax_decode_scores_b32, minimax_prefill_scores_8k, or the ceilings mfma_ceiling, '
+                        'gather_ceiling_b32 and gather_pieces_ceiling_b32')
     p.add_argument('--layers', type=int, default=16)
     p.add_argument('--splits', type=int, default=None)
     p.add_argument('--layout', default='interleaved', choices=['interleaved', 'split'],

@@ -445,6 +445,15 @@ int xt_ceiling_gather(const void* pool, int64_t record_bytes, int64_t pool_recor
                       int64_t pt_stride, int page_size, int pt_width, const int32_t* indices, int batch, int topk,
                       uint32_t* sink, xt_stream_t stream);
 size_t xt_ceiling_gather_sink_words(int batch, int topk);
+/* xt_ceiling_gather_pieces: the same records read the way the fused decode reads them from the interleaved pool
+ * (576-byte records of 4 KV heads x D = 128): one workgroup per (row, KV head, key split) numbered as the decode
+ * numbers its units, each reading its head's 128 payload bytes and 16 scale bytes of every key of the split, in steps of
+ * 32 keys per wavefront with four steps in flight. topk / splits must be a multiple of 256 up to 2048. sink receives
+ * batch * 4 * splits * 512 words; the XOR of the 512 words of workgroup g is the XOR of the head pieces of its unit's
+ * valid keys (unit of g: x * (n / 8) + min(x, n % 8) + g / 8 with x = g % 8, n = the number of workgroups). */
+int xt_ceiling_gather_pieces(const void* pool, int64_t pool_records, const int32_t* page_table, int64_t pt_stride,
+                             int page_size, int pt_width, const int32_t* indices, int batch, int topk, int kv_heads,
+                             int splits, uint32_t* sink, xt_stream_t stream);
 
 #ifdef __cplusplus
 }

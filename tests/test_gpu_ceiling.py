@@ -39,3 +39,36 @@ def test_gather_ceiling_reads_exactly_the_listed_records(topk, record):
                 continue
             want ^= np.bitwise_xor.reduce(words[t[r, pos // page] * page + pos % page])
         assert got[r] == want, r
+
+
+@pytest.mark.parametrize('topk,splits', [(512, 2), (2048, 2), (1024, 4), (256, 1)])
+def test_gather_pieces_reads_each_units_head_pieces(topk, splits):
+    """Workgroup g's words XOR to the XOR of its unit's head pieces (128 payload + 16 scale bytes) over the valid keys
+    of its split, the unit numbered as the decode numbers them."""
+    batch, ctx, page = 3, 4096, 64
+    records = batch * ctx + 64
+    gen = workloads.generator('cuda', topk + splits)
+    pool = torch.randint(0, 256, (records, 576), dtype=torch.uint8, device='cuda', generator=gen)
+    pt = workloads.page_table(batch, ctx, page, gen, 'cuda')
+    idx = workloads.index_lists(batch, ctx, topk, gen, 'cuda')
+    idx[0, 3] = -1
+    idx[1, 7] = ctx + 9 * page
+    pt[2, int(idx[2, 0]) // page] = -1
+    sink = ops.ceiling_gather_pieces(pool, pt, idx, page, splits)
+    n = batch * 4 * splits
+    got = np.bitwise_xor.reduce(sink.cpu().numpy().astype(np.uint32).reshape(n, 512), axis=1)
+    words = pool.cpu().numpy().view(np.uint32)          # [records, 144]
+    p, t = idx.cpu().numpy(), pt.cpu().numpy()
+    kps = topk // splits
+    for g in range(n):
+        x = g % 8
+        u = x * (n // 8) + min(x, n % 8) + g // 8
+        split, head, row = u % splits, (u // splits) % 4, u // splits // 4
+        want = np.uint32(0)
+        for pos in p[row, split * kps:(split + 1) * kps]:
+            if pos < 0 or pos // page >= t.shape[1] or t[row, pos // page] < 0:
+                continue
+            w = words[t[row, pos // page] * page + pos % page]
+            want ^= np.bitwise_xor.reduce(w[32 * head:32 * head + 32]) ^ np.bitwise_xor.reduce(
+                w[128 + 4 * head:128 + 4 * head + 4])
+        assert got[g] == want, g

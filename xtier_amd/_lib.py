@@ -99,6 +99,7 @@ SIGNATURES = {
     'xt_ceiling_gather': (_I, [_P, ctypes.c_int64, ctypes.c_int64, _P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, _P,
                                ctypes.c_int, ctypes.c_int, _P, _P]),
     'xt_ceiling_gather_sink_words': (_Z, [ctypes.c_int, ctypes.c_int]),
+    'xt_ceiling_gather_pieces': (_I, [_P, _L, _P, _L, _I, _I, _P, _I, _I, _I, _I, _P, _P]),
     'xt_sparse_mla_fp8': (_I, [_P, _L, _L, _I, _FP, _KP, _FP, _KP, _P, _F, _P, _L, _L, _I, _P, _I, _I, _P, _Z, _P]),
     'xt_sparse_mla_nvfp4': (_I, [_P, _L, _L, _I, _I, _I, _CP, _KP, _CP, _KP, _P, _F, _P, _L, _L, _I, _P, _I, _I, _P,
                                  _Z, _P]),

@@ -3,8 +3,10 @@
 //   MFMA: v_mfma_f32_32x32x16_f16 back to back from registers, four independent accumulators per wavefront, several
 //         wavefronts per SIMD (a launch of 4 workgroups of 4 wavefronts per CU; one wavefront alone does not keep the
 //         matrix core busy).
-//   Gather: the fused decode's exact HBM access pattern, whole slot records at page-table positions of per-row index
-//           lists, with no dequantization or math: the bytes arrive and are folded into one word per thread.
+//   Gather: the fused decode's HBM access pattern, slot records at page-table positions of per-row index lists, with
+//           no dequantization or math: the bytes arrive and are folded into one word per thread. Two forms: whole
+//           records per workgroup, and the decode's own decomposition (one KV head's pieces of each record per
+//           workgroup, key splits, slices of 8 wavefronts, four steps of loads in flight).
 #include "xt_common.h"
 #include "xt_host.h"
 
@@ -82,6 +84,77 @@ __global__ __launch_bounds__(512) void gather_ceiling_kernel(const uint8_t* pool
   sink[(int64_t)blockIdx.x * 512 + threadIdx.x] = acc;
 }
 
+// The decode's own decomposition on the interleaved pool (576-byte records: per KV head h, K payload 64 B and V payload
+// 64 B at 128 h, then per head 8 + 8 scale bytes at 512 + 16 h; 4 KV heads of D = 128). Workgroup = unit (row, KV
+// head, key split), numbered as the decode numbers them (XCD x takes a contiguous unit range, so a row's heads and
+// splits share one L2); its keys_per_split slots are resolved into LDS; wave w takes keys w * per_wave .. as steps of
+// 32: lane (hl, j) reads 16 B of K and of V of keys hl and 16 + hl at byte 16 j of the head's pieces, and each lane
+// pair the 16 scale bytes of key lane / 2, four steps in flight. Invalid keys read slot 0 and count as zero.
+constexpr int kPieceMaxKeys = 2048;   // keys per split
+
+__global__ __launch_bounds__(512) void gather_pieces_kernel(const uint8_t* pool, int64_t pool_records,
+                                                            const int32_t* page_table, int64_t pt_stride,
+                                                            int page_size, int pt_width, const int32_t* indices,
+                                                            int topk, int kv_heads, int splits, uint32_t* sink) {
+  __shared__ int32_t slots[kPieceMaxKeys];
+  const uint32_t g = blockIdx.x, xcd = g & 7u, units = gridDim.x;
+  const uint32_t u = xcd * (units / 8) + min(xcd, units % 8) + (g >> 3);
+  const int split = (int)(u % (uint32_t)splits), head = (int)((u / splits) % (uint32_t)kv_heads);
+  const int row = (int)(u / splits / kv_heads);
+  const int kps = topk / splits, t0 = split * kps;
+  for (int i = threadIdx.x; i < kps; i += 512) {
+    const int32_t pos = indices[(int64_t)row * topk + t0 + i];
+    int32_t slot = -1;
+    if (pos >= 0 && pos / page_size < pt_width) {
+      const int32_t ent = page_table[(int64_t)row * pt_stride + pos / page_size];
+      const int64_t v = (int64_t)ent * page_size + pos % page_size;
+      if (ent >= 0 && v < pool_records) slot = (int32_t)v;
+    }
+    slots[i] = slot;
+  }
+  __syncthreads();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane & 15, j = lane >> 4;
+  const int per_wave = kps / 8, steps = per_wave / 32;
+  const int32_t* ws = slots + wave * per_wave;
+  const uint8_t* hp = pool + 128 * head + 16 * j;
+  const uint8_t* sp = pool + 512 + 16 * head + 8 * (lane & 1);
+  uint4 kv[4][4];
+  uint2 sc[4];
+  bool ok[4][3];
+  auto load = [&](int st, int b) {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int32_t s = ws[32 * st + 16 * tt + hl];
+      ok[b][tt] = s >= 0;
+      const int64_t off = (int64_t)(s < 0 ? 0 : s) * 576;
+      kv[b][2 * tt] = *reinterpret_cast<const uint4*>(hp + off);
+      kv[b][2 * tt + 1] = *reinterpret_cast<const uint4*>(hp + off + 64);
+    }
+    const int32_t s = ws[32 * st + (lane >> 1)];
+    ok[b][2] = s >= 0;
+    sc[b] = *reinterpret_cast<const uint2*>(sp + (int64_t)(s < 0 ? 0 : s) * 576);
+  };
+  uint32_t acc = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+    if (b < steps) load(b, b);
+  for (int s0 = 0; s0 < steps; s0 += 4) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      if (s0 + b < steps) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t x = kv[b][q].x ^ kv[b][q].y ^ kv[b][q].z ^ kv[b][q].w;
+          acc ^= ok[b][q >> 1] ? x : 0u;
+        }
+        acc ^= ok[b][2] ? (sc[b].x ^ sc[b].y) : 0u;
+        if (s0 + b + 4 < steps) load(s0 + b + 4, b);
+      }
+    }
+  }
+  sink[(int64_t)g * 512 + threadIdx.x] = acc;
+}
+
 }  // namespace
 }  // namespace xt
 
@@ -124,4 +197,24 @@ extern "C" int xt_ceiling_gather(const void* pool, int64_t record_bytes, int64_t
 extern "C" size_t xt_ceiling_gather_sink_words(int batch, int topk) {
   if (batch <= 0 || topk <= 0) return 0;
   return (size_t)batch * ((topk + kGatherKeys - 1) / kGatherKeys) * 512;
+}
+
+extern "C" int xt_ceiling_gather_pieces(const void* pool, int64_t pool_records, const int32_t* page_table,
+                                        int64_t pt_stride, int page_size, int pt_width, const int32_t* indices,
+                                        int batch, int topk, int kv_heads, int splits, uint32_t* sink,
+                                        xt_stream_t stream) {
+  const char* what = "xt_ceiling_gather_pieces";
+  if (batch < 0 || topk < 0 || kv_heads != 4 || splits < 1) return fail(XT_EINVAL, "%s: bad sizes", what);
+  if (batch == 0 || topk == 0) return ok();
+  if (!pool || !page_table || !indices || !sink) return fail(XT_EINVAL, "%s: a required pointer is null", what);
+  const int kps = topk / splits;
+  if (topk % splits || kps > kPieceMaxKeys || kps % 256)
+    return fail(XT_EINVAL, "%s: keys per split %d must divide topk and be a multiple of 256 up to %d", what, kps,
+                kPieceMaxKeys);
+  if (!aligned(pool, 16) || pool_records <= 0 || page_size <= 0 || pt_width <= 0 || pt_stride < pt_width)
+    return fail(XT_EINVAL, "%s: bad pool or page table", what);
+  hipLaunchKernelGGL(gather_pieces_kernel, dim3((unsigned)(batch * kv_heads * splits)), dim3(512), 0,
+                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint8_t*>(pool), pool_records,
+                     page_table, pt_stride, page_size, pt_width, indices, topk, kv_heads, splits, sink);
+  return check_launch(what);
 }

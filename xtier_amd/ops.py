@@ -754,6 +754,24 @@ def ceiling_gather(pool, page_table, indices, page_size, sink=None):
     return sink
 
 
+def ceiling_gather_pieces(pool, page_table, indices, page_size, splits=2, sink=None):
+    """The fused decode's own gather decomposition alone (xt_ceiling_gather_pieces) on the interleaved pool's 576-byte
+    records (4 KV heads x D = 128): one workgroup per (row, KV head, key split) reading its head's pieces of every
+    key. Returns the sink (512 words per workgroup)."""
+    if pool.dtype != torch.uint8 or pool.dim() != 2 or pool.shape[1] != 576 or not pool.is_contiguous():
+        raise ValueError('xtier_amd.ceiling_gather_pieces: pool must be contiguous uint8 [records, 576]')
+    page_table, indices = page_table.int().contiguous(), indices.int().contiguous()
+    batch, topk = indices.shape
+    words = batch * 4 * splits * 512
+    if sink is None or sink.numel() < words:
+        sink = torch.empty(words, dtype=torch.int32, device=pool.device)
+    status = _lib.lib().xt_ceiling_gather_pieces(_ptr(pool), pool.shape[0], _ptr(page_table), page_table.stride(0),
+                                                 int(page_size), page_table.shape[1], _ptr(indices), batch, topk, 4,
+                                                 int(splits), _ptr(sink), _stream(pool))
+    _lib.check(status, 'ceiling_gather_pieces')
+    return sink
+
+
 def topk_rows(x, topk, out=None):
     """xt_topk_rows: x FP32 [rows, cols] (unit column stride) -> int32 [rows, topk]: per row the positions of the topk
     largest finite values, ascending, ties toward the lower position, -1 padded."""
