@@ -66,6 +66,8 @@ struct ScoreArgs {
   int init_blocks, local_blocks;
   int skip_topk;              // decode: a request with at most this many blocks gets no scores (-1: none skipped)
   int lse;                    // decode: log2-sum-exp2 instead of the maximum
+  int chunks;                 // prefill: block ranges per row tile (grid x = row tiles * chunks)
+  int chunk_blocks;           // prefill: blocks per range
 };
 
 __device__ inline void store_score(const ScoreArgs& a, int64_t at, float v) {
@@ -202,8 +204,9 @@ __global__ __launch_bounds__(64 * kScoreWaves) void decode_scores_kernel(const S
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Prefill: grid (x, request b, head group of HPW heads); workgroup x covers query rows [R x, R x + R) of request b,
-// R = 256 / HPW. Column j of wavefront w's column group g is (row (32 / HPW)(2 w + g) + j / HPW, head j % HPW).
+// Prefill: grid (row tile x block range, request b, head group of HPW heads); a workgroup covers R = 256 / HPW query
+// rows of request b and one range of chunk_blocks blocks (the per-block results are independent, so ranges split a
+// long prompt's work over many workgroups). Column j of wavefront w's column group g is (row (32 / HPW)(2 w + g) + j / HPW, head j % HPW).
 // Key chunks of S = min(block_size, 128) positions are staged as 16-bit values in LDS by the whole workgroup (once
 // for its 256 columns), then each wavefront runs its two column groups over them. Chunks wholly at or below every
 // row's position skip the causal test and scale once after the maximum (c > 0: the maximum commutes with the
@@ -222,7 +225,8 @@ __global__ __launch_bounds__(64 * kScoreWaves) void prefill_scores_kernel(const 
   const int b = blockIdx.y;
   const int64_t q0 = load_index(a.cu_seqlens, b, a.wide & kWideCu);
   const int64_t q_len = load_index(a.cu_seqlens, b + 1, a.wide & kWideCu) - q0;
-  const int64_t row0 = (int64_t)(gridDim.x - 1 - blockIdx.x) * R;   // the longest rows first
+  const int tiles = (int)gridDim.x / a.chunks, chunk = (int)blockIdx.x % a.chunks;
+  const int64_t row0 = (int64_t)(tiles - 1 - (int)blockIdx.x / a.chunks) * R;   // the longest rows first
   if (row0 >= q_len) return;   // uniform over the workgroup: before every barrier
   const int64_t seq = load_index(a.seq_lens, b, a.wide & kWideSeq);
   const int64_t pre = load_index(a.prefix_lens, b, a.wide & kWidePrefix);
@@ -248,11 +252,13 @@ __global__ __launch_bounds__(64 * kScoreWaves) void prefill_scores_kernel(const 
   // the workgroup's block count: that of its last live row (block counts grow with the row)
   const int64_t last = min(q_len, row0 + R) - 1;
   const int64_t wg_blocks = (min(seq, pre + 64 * (last / 64 + 1)) + bs - 1) / bs;
+  const int64_t blk_lo = (int64_t)chunk * a.chunk_blocks, blk_hi = min(wg_blocks, blk_lo + a.chunk_blocks);
+  if (blk_lo >= wg_blocks) return;   // uniform: before every barrier
   const int64_t first_pos = pre + row0;       // every row of the workgroup sees keys at or below this
   const bool wide_r2t = a.wide & kWideR2t;
   const int S = bs < kStageKeys ? bs : kStageKeys;
   const int chunks16 = S * NK;                // 16-value pieces per stage
-  for (int64_t blk = 0; blk < wg_blocks; ++blk) {
+  for (int64_t blk = blk_lo; blk < blk_hi; ++blk) {
     float m[2] = {-__builtin_inff(), -__builtin_inff()};    // scaled maxima of masked chunks
     float mr[2] = {-__builtin_inff(), -__builtin_inff()};   // raw maxima of unmasked chunks
     for (int sub = 0; sub < bs; sub += S) {
@@ -455,7 +461,15 @@ extern "C" int xt_minimax_prefill_scores(const void* q, int64_t q_token_stride, 
   a.c = score_factor;
   const int hpw = heads >= 4 ? 4 : heads >= 2 ? 2 : 1;   // heads per workgroup: 256 / hpw rows each
   const int rows = 256 / hpw;
-  const dim3 grid((unsigned)((max_q_len + rows - 1) / rows), (unsigned)batch, (unsigned)((heads + hpw - 1) / hpw));
+  // block ranges: the request's blocks are at most ceil(r2t_stride / block_size) (its positions index a row of
+  // req_to_token); ranges of at least 8 blocks, at most 64 ranges
+  const int64_t max_blocks = (r2t_stride + block_size - 1) / block_size;
+  const int64_t want_chunks = (max_blocks + 7) / 8;
+  a.chunks = want_chunks < 1 ? 1 : want_chunks > 64 ? 64 : (int)want_chunks;
+  a.chunk_blocks = max_blocks > 0 ? (int)((max_blocks + a.chunks - 1) / a.chunks) : 0x7FFFFFFF;
+  const int64_t tiles = (max_q_len + rows - 1) / rows;
+  if (tiles * a.chunks > 0x7FFFFFFF) return fail(XT_EUNSUPPORTED, "%s: %lld query tiles", what, (long long)tiles);
+  const dim3 grid((unsigned)(tiles * a.chunks), (unsigned)batch, (unsigned)((heads + hpw - 1) / hpw));
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const bool bf = q_dtype == XT_DTYPE_BF16;
   switch (dim) {

@@ -3,7 +3,8 @@
 //
 //   QSA indexer logits (BF16 / FP16 q and k): logits[r, n] = sum_h ReLU(q[r, h] . k[n]) / score_scale, -inf outside
 //     the row's [start, end). v_mfma_f32_32x32x16_{bf16,f16}: A = 32 keys x 16 dims, B = 16 dims x (32 / H rows x H
-//     heads); ReLU and the head sum on the accumulators (H lanes apart within a row of 16 lanes).
+//     heads); ReLU and the head sum on the accumulators (H lanes apart within a row of 16 lanes); the division as a
+//     multiplication by 1 / score_scale.
 //   DSA logits (FP8 E4M3 q and k, an FP32 scale per key, FP32 head weights): logits[q, n] = sum_h w[q, h] ReLU(q_h .
 //     k_n) * k_scale[n], outside [ks, ke) 0 or -inf. v_mfma_f32_32x32x16_f16 on the E4M3 values converted exactly to
 //     FP16, with the heads as rows (A = 32 heads x 16 dims of one query, B = 16 dims x 32 keys): a lane then holds 16
@@ -146,6 +147,137 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float* x,
   for (int i = (int)k + tid; i < topk; i += kTopkThreads) o[i] = -1;
 }
 
+// Rows of at most 4 * kTopkRegThreads * kTopkChunks columns (16-byte aligned rows): the row is read once into
+// registers as order keys (a non-finite value as key 0, which no finite value has), and the three radix passes and
+// the ordered write run on them. Chunk i of thread t holds columns 4 (kTopkRegThreads i + t) .. + 3. The write needs
+// one block scan per chunk row: with `remaining` of the keys equal to T taken in column order, the keys taken before a
+// column are the keys above T before it plus min(keys equal to T before it, remaining).
+constexpr int kTopkRegThreads = 512;
+constexpr int kTopkChunks = 48;
+
+template <int NW>
+__device__ inline uint32_t block_exclusive_sum(uint32_t v, uint32_t* scratch, uint32_t& total) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  uint32_t incl = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t y = (uint32_t)__shfl_up((int)incl, d);
+    if (lane >= d) incl += y;
+  }
+  if (lane == 63) scratch[wave] = incl;
+  __syncthreads();
+  uint32_t before = incl - v, sum = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const uint32_t c = scratch[w];
+    before += w < wave ? c : 0u;
+    sum += c;
+  }
+  __syncthreads();   // scratch is reused by the next call
+  total = sum;
+  return before;
+}
+
+__global__ __launch_bounds__(kTopkRegThreads) void topk_rows_reg_kernel(const float* x, int64_t ld, int cols,
+                                                                          int topk, int32_t* out, int64_t out_ld) {
+  constexpr int NW = kTopkRegThreads / 64, NB = 2048 / kTopkRegThreads;   // waves; buckets per thread
+  __shared__ uint32_t hist[2048];
+  __shared__ uint32_t scratch[NW];
+  __shared__ uint32_t sel[2];
+  const int tid = threadIdx.x;
+  const float* xr = x + (int64_t)blockIdx.x * ld;
+  int32_t* o = out + (int64_t)blockIdx.x * out_ld;
+  uint32_t key[kTopkChunks][4];
+#pragma unroll
+  for (int i = 0; i < kTopkChunks; ++i) {
+    const int c = 4 * (kTopkRegThreads * i + tid);
+    float f[4];
+    if (4 * kTopkRegThreads * (i + 1) <= cols) {   // uniform: the whole chunk row is inside the row
+      const float4_t v = *reinterpret_cast<const float4_t*>(xr + c);
+      f[0] = v[0]; f[1] = v[1]; f[2] = v[2]; f[3] = v[3];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float y = xr[min(c + e, cols - 1)];   // an address inside the row, used only where c + e < cols
+        f[e] = c + e < cols ? y : __builtin_inff();
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) key[i][e] = finite_f32(f[e]) ? order_key(f[e]) : 0u;
+  }
+  uint32_t prefix = 0, pmask = 0, remaining = 0, k = 0;
+  for (int pass = 0; pass < 3; ++pass) {
+    const int shift = pass == 0 ? 21 : pass == 1 ? 10 : 0;
+    const uint32_t dmask = pass == 2 ? 0x3FFu : 0x7FFu;
+    for (int i = tid; i < 2048; i += kTopkRegThreads) hist[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kTopkChunks; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (key[i][e] != 0u && (key[i][e] & pmask) == prefix) atomicAdd(&hist[(key[i][e] >> shift) & dmask], 1u);
+    __syncthreads();
+    // thread t owns buckets 2047 - NB t down to 2048 - NB (t + 1); the exclusive prefix of their counts in thread
+    // order is the number of keys in higher buckets
+    uint32_t cnt[NB], sum = 0;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      cnt[b] = hist[2047 - NB * tid - b];
+      sum += cnt[b];
+    }
+    uint32_t all;
+    uint32_t above = block_exclusive_sum<NW>(sum, scratch, all);
+    if (pass == 0) {
+      k = min((uint32_t)topk, all);
+      remaining = k;
+    }
+    if (k != 0) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        if (above < remaining && remaining <= above + cnt[b]) {
+          sel[0] = 2047 - NB * tid - b;
+          sel[1] = remaining - above;
+        }
+        above += cnt[b];
+      }
+    }
+    __syncthreads();
+    if (k == 0) break;
+    prefix |= sel[0] << shift;
+    pmask |= dmask << shift;
+    remaining = sel[1];
+    __syncthreads();   // sel is rewritten by the next pass
+  }
+  // T = prefix: columns in order, the keys above T and the first `remaining` keys equal to T
+  uint32_t gt_seen = 0, eq_seen = 0;
+  if (k != 0) {
+#pragma unroll
+    for (int i = 0; i < kTopkChunks; ++i) {
+      uint32_t ngt = 0, neq = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ngt += key[i][e] > prefix ? 1u : 0u;
+        neq += (key[i][e] != 0u && key[i][e] == prefix) ? 1u : 0u;
+      }
+      // counts up to 4 * kTopkRegThreads per chunk row: (above, equal) packed in one word
+      uint32_t tot;
+      const uint32_t before = block_exclusive_sum<NW>(ngt | (neq << 16), scratch, tot);
+      uint32_t gt_b = gt_seen + (before & 0xFFFFu), eq_b = eq_seen + (before >> 16);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t kv = key[i][e];
+        const bool gt = kv > prefix, eq = kv != 0u && kv == prefix;
+        if (gt || (eq && eq_b < remaining)) o[gt_b + min(eq_b, remaining)] = 4 * (kTopkRegThreads * i + tid) + e;
+        gt_b += gt ? 1u : 0u;
+        eq_b += eq ? 1u : 0u;
+      }
+      gt_seen += tot & 0xFFFFu;
+      eq_seen += tot >> 16;
+    }
+  }
+  for (int i = (int)k + tid; i < topk; i += kTopkRegThreads) o[i] = -1;
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // QSA indexer logits
 
@@ -176,75 +308,95 @@ struct QsaArgs {
 
 constexpr int kQsaWaves = 4;
 
-// Workgroup = (block of 32 / H rows, keys_per_wg keys); wave w takes every 4th 32-key block of them. Lane layouts
-// (32x32x16): A = keys, lane (key l % 32, dims 16kk + 8 (l / 32) .. +7) read straight from k; B = queries, lane
-// (column j = l % 32: row j / H, head j % H; same dims) kept in registers; C = S^T, lane (column j, keys
-// 8 (r / 4) + 4 (l / 32) + r % 4).
+// Workgroup = (4 wavefronts x 2 column groups of 32 / H rows, keys_per_wg keys): every wavefront sweeps the whole key
+// range for its own 2 x 32 / H rows, so the four wavefronts read the same K blocks (from L1 after the first) and each
+// K block leaves L2 once per 8 x 32 / H rows. Lane layouts (32x32x16): A = keys, lane (key l % 32, dims
+// 16kk + 8 (l / 32) .. +7) read straight from k; B = queries, lane (column j = l % 32: row j / H, head j % H; same
+// dims) kept in registers, one set per column group; C = S^T, lane (column j, keys 8 (r / 4) + 4 (l / 32) + r % 4).
+constexpr int kQsaGroups = 2;   // column groups per wavefront
+
 template <int H, int NK, bool BF>
 __global__ __launch_bounds__(64 * kQsaWaves) void qsa_logits_kernel(const QsaArgs a) {
-  constexpr int kRows = 32 / H;
+  constexpr int kRowsG = 32 / H, kRowsW = kQsaGroups * kRowsG;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
-  const int r0 = blockIdx.x * kRows;
-  const int my_row = r0 + j / H, head = j % H;
-  const bool row_ok = my_row < a.rows;
-  // the rows' key range: a 32-key block outside every row's [start, end) is written as -inf without the product
-  int lo = 0x7FFFFFFF, hi = 0;
-  for (int r = 0; r < kRows; ++r) {
-    if (r0 + r < a.rows) {
-      lo = min(lo, max(0, a.starts[r0 + r]));
-      hi = max(hi, min(a.keys, a.ends[r0 + r]));
-    }
-  }
-  const int start = row_ok ? a.starts[my_row] : 0, end = row_ok ? a.ends[my_row] : 0;
-  short8_t qb[NK];
-  {
-    const uint16_t* qp = a.q + (int64_t)(row_ok ? my_row : 0) * a.q_rs + (int64_t)head * a.q_hs + 8 * h;
+  const int rw = (blockIdx.x * kQsaWaves + wave) * kRowsW;   // this wavefront's first row
+  const int head = j % H;
+  int my_row[kQsaGroups], start[kQsaGroups], end[kQsaGroups];
+  bool row_ok[kQsaGroups];
+  short8_t qb[kQsaGroups][NK];
+#pragma unroll
+  for (int g = 0; g < kQsaGroups; ++g) {
+    my_row[g] = rw + g * kRowsG + j / H;
+    row_ok[g] = my_row[g] < a.rows;
+    start[g] = row_ok[g] ? a.starts[my_row[g]] : 0;
+    end[g] = row_ok[g] ? a.ends[my_row[g]] : 0;
+    const uint16_t* qp = a.q + (int64_t)(row_ok[g] ? my_row[g] : 0) * a.q_rs + (int64_t)head * a.q_hs + 8 * h;
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
-      const uint4 w = row_ok ? *reinterpret_cast<const uint4*>(qp + 16 * kk) : uint4{0u, 0u, 0u, 0u};
-      qb[kk] = __builtin_bit_cast(short8_t, w);
+      const uint4 w = row_ok[g] ? *reinterpret_cast<const uint4*>(qp + 16 * kk) : uint4{0u, 0u, 0u, 0u};
+      qb[g][kk] = __builtin_bit_cast(short8_t, w);
     }
   }
+  // the wavefront's key range: a 32-key block outside every one of its rows' [start, end) is written as -inf
+  // without the product
+  int lo = 0x7FFFFFFF, hi = 0;
+  for (int r = 0; r < kRowsW; ++r) {
+    if (rw + r < a.rows) {
+      lo = min(lo, max(0, a.starts[rw + r]));
+      hi = max(hi, min(a.keys, a.ends[rw + r]));
+    }
+  }
+  // x / score_scale as x * (1 / score_scale): one more rounding, at most 2^-24 relative
+  const float inv = 1.0f / a.score_scale;
   const int k_begin = blockIdx.y * a.keys_per_wg, k_end = min(a.keys, k_begin + a.keys_per_wg);
-  for (int kb = k_begin + 32 * wave; kb < k_end; kb += 32 * kQsaWaves) {
-    float v[16];
-    if (kb + 32 <= lo || kb >= hi) {   // uniform: no row of the block takes these keys
+  for (int kb = k_begin; kb < k_end; kb += 32) {
+    float v[kQsaGroups][16];
+    if (kb + 32 <= lo || kb >= hi) {   // uniform over the wavefront
 #pragma unroll
-      for (int r = 0; r < 16; ++r) v[r] = -__builtin_inff();
+      for (int g = 0; g < kQsaGroups; ++g)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v[g][r] = -__builtin_inff();
     } else {
       const int key = min(kb + j, a.keys - 1);
       const uint16_t* kp = a.k + (int64_t)key * a.k_rs + 8 * h;
-      float16_t s = {};
+      short8_t kf[NK];
 #pragma unroll
-      for (int kk = 0; kk < NK; ++kk) {
-        const short8_t kf = __builtin_bit_cast(short8_t, *reinterpret_cast<const uint4*>(kp + 16 * kk));
-        s = mfma_qk<BF>(kf, qb[kk], s);
-      }
-      // ReLU, then the sum over the H heads of a row (H consecutive lanes), in the order lane ^ 1, ^ 2, ...
+      for (int kk = 0; kk < NK; ++kk) kf[kk] = __builtin_bit_cast(short8_t, *reinterpret_cast<const uint4*>(kp + 16 * kk));
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = fmaxf(s[r], 0.0f);
-        if constexpr (H >= 2) x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
-        if constexpr (H >= 4) x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
-        if constexpr (H >= 8) x += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), (4 << 10) | 0x1F));
-        if constexpr (H >= 16) x += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), (8 << 10) | 0x1F));
-        if constexpr (H >= 32) x += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), (16 << 10) | 0x1F));
-        const int key = kb + 8 * (r >> 2) + 4 * h + (r & 3);
-        v[r] = (key >= start && key < end) ? x / a.score_scale : -__builtin_inff();
+      for (int g = 0; g < kQsaGroups; ++g) {
+        float16_t s = {};
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk) s = mfma_qk<BF>(kf[kk], qb[g][kk], s);
+        // ReLU, then the sum over the H heads of a row (H consecutive lanes), in the order lane ^ 1, ^ 2, ...
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float x = fmaxf(s[r], 0.0f);
+          if constexpr (H >= 2) x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
+          if constexpr (H >= 4) x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
+          if constexpr (H >= 8) x += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), (4 << 10) | 0x1F));
+          if constexpr (H >= 16) x += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), (8 << 10) | 0x1F));
+          if constexpr (H >= 32) x += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), (16 << 10) | 0x1F));
+          const int kr = kb + 8 * (r >> 2) + 4 * h + (r & 3);
+          v[g][r] = (kr >= start[g] && kr < end[g]) ? x * inv : -__builtin_inff();
+        }
       }
     }
     // the lane of head 0 of each row writes its 16 keys: 4 runs of 4 consecutive keys
-    if (row_ok && head == 0) {
-      float* op = a.logits + (int64_t)my_row * a.ld;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int key = kb + 8 * g + 4 * h;
-        if (key + 4 <= a.keys && a.vec_store) {
-          *reinterpret_cast<float4_t*>(op + key) = float4_t{v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
-        } else {
+    for (int g = 0; g < kQsaGroups; ++g) {
+      if (row_ok[g] && head == 0) {
+        float* op = a.logits + (int64_t)my_row[g] * a.ld;
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (key + e < a.keys) op[key + e] = v[4 * g + e];
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int key = kb + 8 * q4 + 4 * h;
+          if (key + 4 <= a.keys && a.vec_store) {
+            *reinterpret_cast<float4_t*>(op + key) =
+                float4_t{v[g][4 * q4], v[g][4 * q4 + 1], v[g][4 * q4 + 2], v[g][4 * q4 + 3]};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (key + e < a.keys) op[key + e] = v[g][4 * q4 + e];
+          }
         }
       }
     }
@@ -344,6 +496,93 @@ __global__ __launch_bounds__(64 * kDsaWaves) void dsa_logits_kernel(const DsaArg
   }
 }
 
+// Flat keys, heads x dim within registers (G head groups of 32, G * NK <= 16): the four rows of a workgroup read the
+// same keys, so the workgroup stages them once per 128 keys in LDS (E4M3 bytes, double-buffered, one barrier per
+// stage), each wavefront keeps its row's query (as FP16) and head weights in registers for the whole key range, and
+// converts each 32-key block's K once for all its head groups.
+constexpr int kDsaStageKeys = 128;
+
+template <int NK, int G>
+__global__ __launch_bounds__(64 * kDsaWaves) void dsa_flat_kernel(const DsaArgs a) {
+  constexpr int D = 16 * NK, ROW = D + 16;                 // LDS bytes per key (16 of padding)
+  constexpr int PIECES = kDsaStageKeys * D / 16;           // 16-byte pieces per stage
+  constexpr int PER_THREAD = PIECES / (64 * kDsaWaves);
+  __shared__ __align__(16) uint8_t kt[2][kDsaStageKeys * ROW];
+  __shared__ float kst[2][kDsaStageKeys];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5, tid = threadIdx.x;
+  const int qrow = blockIdx.x * kDsaWaves + wave;
+  const bool row_ok = qrow < a.num_q;   // every thread takes every barrier below
+  const int k_begin = blockIdx.y * a.keys_per_wg, k_end = min(a.num_kv, k_begin + a.keys_per_wg);
+  const int lim_lo = (row_ok && a.ks) ? a.ks[qrow] : 0;
+  const int lim_hi = row_ok ? (a.ke ? a.ke[qrow] : a.num_kv) : 0;
+  const float fill = a.clean ? -__builtin_inff() : 0.0f;
+  // this row's query (A operand: head 32 g + j, dims 16 kk + 8 h .. + 7) and weights (C rows of lane half h)
+  half8_t qf[G][NK];
+  float wv[G][16];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const uint8_t* qp = a.q + (int64_t)(row_ok ? qrow : 0) * a.q_rs + (int64_t)(32 * g + j) * a.q_hs + 8 * h;
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk)
+      qf[g][kk] = fp8x8_to_f16(row_ok ? *reinterpret_cast<const uint64_t*>(qp + 16 * kk) : 0ull);
+    const float* wp = a.w + (int64_t)(row_ok ? qrow : 0) * a.w_rs + 32 * g + 4 * h;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) wv[g][r] = row_ok ? wp[8 * (r >> 2) + (r & 3)] : 0.0f;
+  }
+  uint4 reg[PER_THREAD];
+  float sreg = 0.0f;
+  auto load_stage = [&](int k0) {   // keys past the end read the last key (never written out)
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int c = tid + 64 * kDsaWaves * i, key = min(k0 + c / (D / 16), a.num_kv - 1);
+      reg[i] = *reinterpret_cast<const uint4*>(a.k + (int64_t)key * a.k_rs + 16 * (c % (D / 16)));
+    }
+    if (tid < kDsaStageKeys) sreg = a.k_scale[min(k0 + tid, a.num_kv - 1)];
+  };
+  auto store_stage = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int c = tid + 64 * kDsaWaves * i;
+      *reinterpret_cast<uint4*>(&kt[buf][(c / (D / 16)) * ROW + 16 * (c % (D / 16))]) = reg[i];
+    }
+    if (tid < kDsaStageKeys) kst[buf][tid] = sreg;
+  };
+  const int stages = k_end > k_begin ? (k_end - k_begin + kDsaStageKeys - 1) / kDsaStageKeys : 0;
+  if (stages > 0) {
+    load_stage(k_begin);
+    store_stage(0);
+  }
+  __syncthreads();
+  for (int st = 0; st < stages; ++st) {
+    const int k0 = k_begin + st * kDsaStageKeys, buf = st & 1;
+    if (st + 1 < stages) load_stage(k0 + kDsaStageKeys);   // in flight during this stage's MFMAs
+#pragma unroll 1
+    for (int t = 0; t < kDsaStageKeys / 32; ++t) {
+      const uint8_t* kr = &kt[buf][(32 * t + j) * ROW + 8 * h];
+      half8_t kv[NK];
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk) kv[kk] = fp8x8_to_f16(*reinterpret_cast<const uint64_t*>(kr + 16 * kk));
+      float acc = 0.0f;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float16_t sc = {};
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk) sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(qf[g][kk], kv[kk], sc, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc += fmaxf(sc[r], 0.0f) * wv[g][r];
+      }
+      // the other 16 heads of each group are in the lane 32 apart
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc), __float_as_uint(acc), false, false);
+      const float total = (__uint_as_float(sw[0]) + __uint_as_float(sw[1])) * kst[buf][32 * t + j];
+      const int key = k0 + 32 * t + j;
+      const bool live = key >= lim_lo && key < lim_hi;
+      if (row_ok && h == 0 && key < k_end) a.logits[(int64_t)qrow * a.ld + key] = live ? total : fill;
+    }
+    if (st + 1 < stages) store_stage(buf ^ 1);   // its readers finished the stage before the last barrier
+    __syncthreads();
+  }
+}
+
 }  // namespace
 }  // namespace xt
 
@@ -356,8 +595,12 @@ extern "C" int xt_topk_rows(const float* x, int64_t ld, int rows, int cols, int 
   if (rows == 0 || topk == 0) return ok();
   if (!x || !out) return fail(XT_EINVAL, "%s: a required pointer is null", what);
   if (ld < cols || out_ld < topk) return fail(XT_EINVAL, "%s: row strides shorter than the rows", what);
-  hipLaunchKernelGGL(topk_rows_kernel, dim3((unsigned)rows), dim3(kTopkThreads), 0,
-                     reinterpret_cast<hipStream_t>(stream), x, ld, cols, topk, out, out_ld);
+  if (cols <= 4 * kTopkRegThreads * kTopkChunks && ld % 4 == 0 && aligned(x, 16))
+    hipLaunchKernelGGL(topk_rows_reg_kernel, dim3((unsigned)rows), dim3(kTopkRegThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), x, ld, cols, topk, out, out_ld);
+  else
+    hipLaunchKernelGGL(topk_rows_kernel, dim3((unsigned)rows), dim3(kTopkThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), x, ld, cols, topk, out, out_ld);
   return check_launch(what);
 }
 
@@ -406,10 +649,10 @@ extern "C" int xt_qsa_indexer_logits(const void* q, int64_t q_row_stride, int64_
   a.ld = ld;
   a.rows = rows;
   a.keys = keys;
-  a.keys_per_wg = 2048;
+  a.keys_per_wg = 1024;
   a.vec_store = (ld % 4 == 0) && aligned(logits, 16);
-  const int rows_per_wg = 32 / heads;
-  const dim3 grid((unsigned)((rows + rows_per_wg - 1) / rows_per_wg), (unsigned)((keys + 2047) / 2048));
+  const int rows_per_wg = kQsaWaves * kQsaGroups * (32 / heads);
+  const dim3 grid((unsigned)((rows + rows_per_wg - 1) / rows_per_wg), (unsigned)((keys + 1023) / 1024));
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const bool bf = dtype == XT_DTYPE_BF16;
   const int nk = dim / 16;
@@ -435,6 +678,17 @@ static int dsa_common(const char* what, DsaArgs& a, int dim, xt_stream_t stream)
   a.keys_per_wg = 4096;
   const dim3 grid((unsigned)((a.num_q + kDsaWaves - 1) / kDsaWaves), (unsigned)((a.out_cols + 4095) / 4096));
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int nk = dim / 16, groups = a.heads / 32;
+  if (a.block == 0 && groups * nk <= 16 && aligned(a.k, 16) && a.k_rs % 16 == 0) {
+#define XT_DSA_FLAT(NK, G)                                                                                           \
+  if (nk == NK && groups == G) {                                                                                     \
+    hipLaunchKernelGGL((dsa_flat_kernel<NK, G>), grid, dim3(64 * kDsaWaves), 0, st, a);                             \
+    return check_launch(what);                                                                                       \
+  }
+    XT_DSA_FLAT(4, 1) XT_DSA_FLAT(4, 2) XT_DSA_FLAT(4, 3) XT_DSA_FLAT(4, 4) XT_DSA_FLAT(8, 1) XT_DSA_FLAT(8, 2)
+    XT_DSA_FLAT(16, 1)
+#undef XT_DSA_FLAT
+  }
   switch (dim / 16) {
     case 4: hipLaunchKernelGGL(dsa_logits_kernel<4>, grid, dim3(64 * kDsaWaves), 0, st, a); break;
     case 8: hipLaunchKernelGGL(dsa_logits_kernel<8>, grid, dim3(64 * kDsaWaves), 0, st, a); break;
