@@ -349,6 +349,66 @@ __global__ __launch_bounds__(64 * kQsaWaves) void qsa_logits_kernel(const QsaArg
   // x / score_scale as x * (1 / score_scale): one more rounding, at most 2^-24 relative
   const float inv = 1.0f / a.score_scale;
   const int k_begin = blockIdx.y * a.keys_per_wg, k_end = min(a.keys, k_begin + a.keys_per_wg);
+  if constexpr (H <= 4) {
+    // Queries as rows: S = Q . K^T with A = the query columns above, B = K; C lane (key kb + j, column-group rows
+    // i = 8 (r / 4) + 4 h + r % 4: row i / H, head i % H). A row's H heads are H consecutive r of one lane, so the
+    // head sum stays in the lane, and lane j writes key kb + j of 16 / H rows (each row: 32 consecutive keys across
+    // the lanes).
+    constexpr int kOut = 16 / H;
+    int orow[kQsaGroups][kOut], ost[kQsaGroups][kOut], oen[kQsaGroups][kOut];
+    int max_start = 0, min_end = 0x7FFFFFFF;
+#pragma unroll
+    for (int g = 0; g < kQsaGroups; ++g)
+#pragma unroll
+      for (int o = 0; o < kOut; ++o) {
+        const int r = o * H;
+        orow[g][o] = rw + g * kRowsG + (8 * (r >> 2) + 4 * h + (r & 3)) / H;
+        const bool ok = orow[g][o] < a.rows;
+        ost[g][o] = ok ? a.starts[orow[g][o]] : 0;
+        oen[g][o] = ok ? a.ends[orow[g][o]] : 0;
+        if (ok) {
+          max_start = max(max_start, ost[g][o]);
+          min_end = min(min_end, oen[g][o]);
+        }
+      }
+    // over the wavefront: a block inside every row's range needs no per-key test
+    for (int d = 1; d < 64; d <<= 1) {
+      max_start = max(max_start, __shfl_xor(max_start, d));
+      min_end = min(min_end, __shfl_xor(min_end, d));
+    }
+    for (int kb = k_begin; kb < k_end; kb += 32) {
+      const int key = kb + j;
+      if (kb + 32 <= lo || kb >= hi) {   // uniform over the wavefront
+#pragma unroll
+        for (int g = 0; g < kQsaGroups; ++g)
+#pragma unroll
+          for (int o = 0; o < kOut; ++o)
+            if (orow[g][o] < a.rows && key < a.keys) a.logits[(int64_t)orow[g][o] * a.ld + key] = -__builtin_inff();
+        continue;
+      }
+      const bool inside = kb >= max_start && kb + 32 <= min_end;
+      const uint16_t* kp = a.k + (int64_t)min(key, a.keys - 1) * a.k_rs + 8 * h;
+      short8_t kf[NK];
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk) kf[kk] = __builtin_bit_cast(short8_t, *reinterpret_cast<const uint4*>(kp + 16 * kk));
+#pragma unroll
+      for (int g = 0; g < kQsaGroups; ++g) {
+        float16_t sc = {};
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk) sc = mfma_qk<BF>(qb[g][kk], kf[kk], sc);
+#pragma unroll
+        for (int o = 0; o < kOut; ++o) {
+          float x = fmaxf(sc[o * H], 0.0f);
+#pragma unroll
+          for (int e = 1; e < H; ++e) x += fmaxf(sc[o * H + e], 0.0f);
+          const bool in_range = inside || (key >= ost[g][o] && key < oen[g][o]);
+          if (orow[g][o] < a.rows && key < a.keys)
+            a.logits[(int64_t)orow[g][o] * a.ld + key] = in_range ? x * inv : -__builtin_inff();
+        }
+      }
+    }
+    return;
+  }
   for (int kb = k_begin; kb < k_end; kb += 32) {
     float v[kQsaGroups][16];
     if (kb + 32 <= lo || kb >= hi) {   // uniform over the wavefront
@@ -504,10 +564,12 @@ constexpr int kDsaStageKeys = 128;
 
 template <int NK, int G>
 __global__ __launch_bounds__(64 * kDsaWaves) void dsa_flat_kernel(const DsaArgs a) {
-  constexpr int D = 16 * NK, ROW = D + 16;                 // LDS bytes per key (16 of padding)
+  // LDS bytes per key: D + 8, so the 32 keys a half-wavefront reads sit on 32 distinct bank pairs ((D + 8) / 4 is
+  // twice an odd number)
+  constexpr int D = 16 * NK, ROW = D + 8;
   constexpr int PIECES = kDsaStageKeys * D / 16;           // 16-byte pieces per stage
   constexpr int PER_THREAD = PIECES / (64 * kDsaWaves);
-  __shared__ __align__(16) uint8_t kt[2][kDsaStageKeys * ROW];
+  __shared__ __align__(16) uint8_t kt[2][kDsaStageKeys * ROW];   // ROW * 128 is a multiple of 16
   __shared__ float kst[2][kDsaStageKeys];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5, tid = threadIdx.x;
   const int qrow = blockIdx.x * kDsaWaves + wave;
@@ -543,7 +605,9 @@ __global__ __launch_bounds__(64 * kDsaWaves) void dsa_flat_kernel(const DsaArgs 
 #pragma unroll
     for (int i = 0; i < PER_THREAD; ++i) {
       const int c = tid + 64 * kDsaWaves * i;
-      *reinterpret_cast<uint4*>(&kt[buf][(c / (D / 16)) * ROW + 16 * (c % (D / 16))]) = reg[i];
+      uint2* dst = reinterpret_cast<uint2*>(&kt[buf][(c / (D / 16)) * ROW + 16 * (c % (D / 16))]);
+      dst[0] = uint2{reg[i].x, reg[i].y};   // 8-byte aligned rows: two 8-byte stores
+      dst[1] = uint2{reg[i].z, reg[i].w};
     }
     if (tid < kDsaStageKeys) kst[buf][tid] = sreg;
   };
