@@ -168,7 +168,7 @@ __device__ inline half8_t dequant_k(uint32_t w, half2_t sc) {
 }
 
 struct WaveCtx {
-  const uint8_t* kp;    // this head's payload column
+  const uint8_t* kp;    // this head's payload column (uniform over the wave)
   const uint8_t* vp;
   const uint8_t* ksf;   // this head's scale column
   const uint8_t* vsf;
@@ -177,32 +177,40 @@ struct WaveCtx {
   int lane, hl, j;
 };
 
+// The byte offset of a slot's row plus a lane offset. O32: every slot is below 2^24 and every row offset below 2^32
+// (checked on the host), so one 24-bit multiply-add gives it and the load takes the uniform column address plus a
+// 32-bit offset; otherwise 64-bit arithmetic.
+template <bool O32>
+__device__ inline const uint8_t* row_at(const uint8_t* col, int32_t slot, int64_t stride, uint32_t lane_off) {
+  const uint32_t s = slot < 0 ? 0u : (uint32_t)slot;
+  if constexpr (O32) return col + (__umul24(s, (uint32_t)stride) + lane_off);
+  else return col + (int64_t)s * stride + lane_off;
+}
+
 // PS (D = 128 only): the K and V scales of a head are 16 contiguous bytes (the interleaved pool): one load serves
 // both, the even lane of each pair taking the K half and the odd lane the V half; compute_step swaps the halves within
 // the pair.
-template <int D, bool PS>
+template <int D, bool PS, bool O32>
 __device__ inline void load_step(const WaveCtx& w, int step, Step<D>& d) {
   using G = Geo<D>;
   const int base = step * kStep;
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     const int32_t s = w.slots[base + 16 * tt + w.hl];
-    const int64_t slot = s < 0 ? 0 : s;
-    load_words(w.kp + slot * w.row_bytes + G::kLaneBytes * w.j, d.kw[tt]);
-    load_words(w.vp + slot * w.row_bytes + G::kLaneBytes * w.j, d.vw[tt]);
+    load_words(row_at<O32>(w.kp, s, w.row_bytes, G::kLaneBytes * w.j), d.kw[tt]);
+    load_words(row_at<O32>(w.vp, s, w.row_bytes, G::kLaneBytes * w.j), d.vw[tt]);
   }
   const int32_t s = w.slots[base + scale_key<D>(w.lane)];
-  const int64_t slot = s < 0 ? 0 : s;
   if constexpr (PS) {
-    const uint2 x = *reinterpret_cast<const uint2*>(w.ksf + slot * w.row_scales + 8 * (w.lane & 1));
+    const uint2 x = *reinterpret_cast<const uint2*>(row_at<O32>(w.ksf, s, w.row_scales, 8 * (w.lane & 1)));
     d.ks[0] = x.x;
     d.vs[0] = x.y;
   } else {
-    const int off = 4 * scale_word<D>(w.lane);
+    const uint32_t off = 4 * scale_word<D>(w.lane);
 #pragma unroll
     for (int i = 0; i < G::kScaleWords; ++i) {
-      d.ks[i] = *reinterpret_cast<const uint32_t*>(w.ksf + slot * w.row_scales + off + 4 * i);
-      d.vs[i] = *reinterpret_cast<const uint32_t*>(w.vsf + slot * w.row_scales + off + 4 * i);
+      d.ks[i] = *reinterpret_cast<const uint32_t*>(row_at<O32>(w.ksf, s, w.row_scales, off + 4 * i));
+      d.vs[i] = *reinterpret_cast<const uint32_t*>(row_at<O32>(w.vsf, s, w.row_scales, off + 4 * i));
     }
   }
 }
@@ -279,14 +287,20 @@ __device__ inline void compute_step(const WaveCtx& w, int step, const Step<D>& d
                                                      0);
     }
   }
-  // online softmax of head hl over keys T(j), lazy rescale
+  // online softmax of head hl over keys T(j), lazy rescale. The K global scale gk is positive (the kernel moves a
+  // negative one's sign into the query and raises magnitudes below FLT_MIN to it), so a masked score (-inf) gives
+  // P = 0. Only a step with invalid keys (a slice's tail, causal limits) masks scores, a branch uniform over the wave.
+  // The maximum reads the products (ordinary VALU results), never the MFMA accumulators themselves: inline asm gets
+  // no MFMA read-after-write wait states from the compiler.
+  const bool full = valid == 0xFFFFFFFFu;
   float sv[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float x = s[e >> 2][e & 3] * gk;
-    sv[e] = ((valid >> key_of(j, e)) & 1u) ? x : -__builtin_inff();
+  for (int e = 0; e < 8; ++e) sv[e] = s[e >> 2][e & 3] * gk;
+  if (!full) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sv[e] = ((valid >> key_of(j, e)) & 1u) ? sv[e] : -__builtin_inff();
   }
-  float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+  float mt = max3_raw(max3_raw(sv[0], sv[1], sv[2]), max3_raw(sv[3], sv[4], sv[5]), max2_raw(sv[6], sv[7]));
   mt = max4_lanes16(mt);
   if (__builtin_amdgcn_ballot_w64(mt > st.m + kRescale)) {   // rare after the first steps
     const float m_new = (mt > st.m + kRescale) ? mt : st.m;
@@ -300,13 +314,9 @@ __device__ inline void compute_step(const WaveCtx& w, int step, const Step<D>& d
   }
   const float m_use = (st.m == -__builtin_inff()) ? 0.0f : st.m;
   float p[8];
-  float psum = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    p[e] = __builtin_amdgcn_exp2f(sv[e] - m_use);
-    psum += p[e];
-  }
-  st.l += psum;
+  for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(sv[e] - m_use);
+  st.l += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
   const half8_t pb = half8_t{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3],
                              (_Float16)p[4], (_Float16)p[5], (_Float16)p[6], (_Float16)p[7]};
   // V^T operands of tile t: payload dword c = 16 t + hl of keys T(j), and the scale byte of block c / 2 of those keys
@@ -368,7 +378,7 @@ __device__ inline void store_out(const DecodeArgs& a, int row, int head, int d0,
 
 // D: head size; HPW: KV heads per workgroup (4 or 1); the workgroup's W / HPW key slices of each head merge through
 // LDS.
-template <int D, int P, int HPW, bool PS, int W>
+template <int D, int P, int HPW, bool PS, int W, bool O32>
 __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArgs a) {
   using G = Geo<D>;
   constexpr int kSlices = W / HPW;
@@ -391,7 +401,7 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
   const int split = (int)(u % splits_u);
   const int kvg = (int)((u / splits_u) % groups_u);
   const int row = (int)(u / splits_u / groups_u);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int kvh = kvg * HPW + (wave % HPW);
   const int slice = wave / HPW;
   const bool active = kvh < a.kv_heads;
@@ -494,7 +504,12 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
   }
   __syncthreads();
 
-  // B operand of the QK MFMAs: FP16 of q * scale * log2(e); heads beyond the group are zero
+  // B operand of the QK MFMAs: FP16 of q * scale * log2(e); heads beyond the group are zero. A negative K global scale
+  // moves its sign into the query, and a magnitude below FLT_MIN (zero included) is raised to it, so the softmax works
+  // with gk > 0 (a NaN stays NaN); at that size the scaled scores round to 0 either way.
+  const float gk_abs = __builtin_fabsf(gk_v);
+  const float gk = gk_abs < 1.17549435e-38f ? 1.17549435e-38f : gk_abs;
+  const float qs = gk_v < 0.0f ? -a.qscale : a.qscale;
   half8_t qb[G::kNK];
 #pragma unroll
   for (int kk = 0; kk < G::kNK; ++kk) {
@@ -502,8 +517,8 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
                             q_valid ? qraw[kk].w : 0u};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      qb[kk][2 * e] = (_Float16)(bf16_bits_to_f32(ws[e] & 0xFFFFu) * a.qscale);
-      qb[kk][2 * e + 1] = (_Float16)(bf16_bits_to_f32(ws[e] >> 16) * a.qscale);
+      qb[kk][2 * e] = (_Float16)(bf16_bits_to_f32(ws[e] & 0xFFFFu) * qs);
+      qb[kk][2 * e + 1] = (_Float16)(bf16_bits_to_f32(ws[e] >> 16) * qs);
     }
   }
   SoftmaxState<D> st;
@@ -528,14 +543,13 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
     w.j = j;
     Step<D> buf[P];
 #pragma unroll
-    for (int p = 0; p < P; ++p) load_step<D, PS>(w, p, buf[p]);
-    const float gk = gk_v;
+    for (int p = 0; p < P; ++p) load_step<D, PS, O32>(w, p, buf[p]);
     int s0 = 0;
     for (; s0 + P < slice_steps; s0 += P) {
 #pragma unroll
       for (int p = 0; p < P; ++p) {
         compute_step<D, PS>(w, s0 + p, buf[p], qb, gk, vtile, st);
-        load_step<D, PS>(w, s0 + p + P, buf[p]);
+        load_step<D, PS, O32>(w, s0 + p + P, buf[p]);
       }
     }
 #pragma unroll
@@ -911,24 +925,31 @@ extern "C" int xt_block_sparse_prefill_nvfp4(const void* q, int64_t q_row_stride
 }
 
 // One launch of the decode kernel.
-template <int D, int HPW, bool PS, int W>
+template <int D, int HPW, bool PS, int W, bool O32>
 static int launch_decode(const DecodeArgs& a, dim3 grid, size_t lds_bytes, hipStream_t stream, const char* what) {
   constexpr int P = Geo<D>::kPrefetch;
-  if (int e = allow_lds(reinterpret_cast<const void*>(&decode_split_kernel<D, P, HPW, PS, W>), lds_bytes, what))
+  if (int e = allow_lds(reinterpret_cast<const void*>(&decode_split_kernel<D, P, HPW, PS, W, O32>), lds_bytes, what))
     return e;
-  hipLaunchKernelGGL((decode_split_kernel<D, P, HPW, PS, W>), grid, dim3(64 * W), lds_bytes, stream, a);
+  hipLaunchKernelGGL((decode_split_kernel<D, P, HPW, PS, W, O32>), grid, dim3(64 * W), lds_bytes, stream, a);
   return check_launch(what);
 }
 
-template <int D, int W>
-static int launch_decode(int hpw, bool ps, const DecodeArgs& a, dim3 grid, size_t lds_bytes, hipStream_t stream,
+template <int D, int HPW, bool PS, int W>
+static int launch_decode(bool o32, const DecodeArgs& a, dim3 grid, size_t lds_bytes, hipStream_t stream,
                          const char* what) {
+  return o32 ? launch_decode<D, HPW, PS, W, true>(a, grid, lds_bytes, stream, what)
+             : launch_decode<D, HPW, PS, W, false>(a, grid, lds_bytes, stream, what);
+}
+
+template <int D, int W>
+static int launch_decode(int hpw, bool ps, bool o32, const DecodeArgs& a, dim3 grid, size_t lds_bytes,
+                         hipStream_t stream, const char* what) {
   if constexpr (D == 128) {   // paired K/V scales: the interleaved pool at head size 128
-    if (ps) return hpw == 4 ? launch_decode<D, 4, true, W>(a, grid, lds_bytes, stream, what)
-                            : launch_decode<D, 1, true, W>(a, grid, lds_bytes, stream, what);
+    if (ps) return hpw == 4 ? launch_decode<D, 4, true, W>(o32, a, grid, lds_bytes, stream, what)
+                            : launch_decode<D, 1, true, W>(o32, a, grid, lds_bytes, stream, what);
   }
-  return hpw == 4 ? launch_decode<D, 4, false, W>(a, grid, lds_bytes, stream, what)
-                  : launch_decode<D, 1, false, W>(a, grid, lds_bytes, stream, what);
+  return hpw == 4 ? launch_decode<D, 4, false, W>(o32, a, grid, lds_bytes, stream, what)
+                  : launch_decode<D, 1, false, W>(o32, a, grid, lds_bytes, stream, what);
 }
 
 // LDS bytes of a launch: the slot list, one V tile per wave and one merge region per wave.
@@ -1059,12 +1080,17 @@ static int decode_impl(const char* what, const void* q, int64_t q_row_stride, in
   // K and V scales of a head side by side and 8-byte aligned (head size 128): one load per key serves both
   const bool ps = dim == 128 && v_scales == k_scales + dim / 16 && aligned(k_scales, 8) && sf_stride % 8 == 0 &&
                   ad.sf_head_stride % 8 == 0;
+  // 32-bit row offsets: slots below 2^24 (one 24-bit multiply) and every slot's row, plus the lane offsets within it,
+  // below 2^32 bytes from the head's column
+  const bool o32 = pool_slots <= (1LL << 24) && pay_stride < (1LL << 24) && sf_stride < (1LL << 24) &&
+                   (pool_slots - 1) * pay_stride + dim / 2 < (1LL << 32) &&
+                   (pool_slots - 1) * sf_stride + dim / 16 < (1LL << 32);
   const dim3 grid((unsigned)launched);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (dim == 64)
-    return waves == 4 ? launch_decode<64, 4>(hpw, ps, a, grid, lds_bytes, st, what)
-                      : launch_decode<64, kWaves>(hpw, ps, a, grid, lds_bytes, st, what);
-  if (dim == 256) return launch_decode<256, 4>(hpw, ps, a, grid, lds_bytes, st, what);
-  return waves == 4 ? launch_decode<128, 4>(hpw, ps, a, grid, lds_bytes, st, what)
-                    : launch_decode<128, kWaves>(hpw, ps, a, grid, lds_bytes, st, what);
+    return waves == 4 ? launch_decode<64, 4>(hpw, ps, o32, a, grid, lds_bytes, st, what)
+                      : launch_decode<64, kWaves>(hpw, ps, o32, a, grid, lds_bytes, st, what);
+  if (dim == 256) return launch_decode<256, 4>(hpw, ps, o32, a, grid, lds_bytes, st, what);
+  return waves == 4 ? launch_decode<128, 4>(hpw, ps, o32, a, grid, lds_bytes, st, what)
+                    : launch_decode<128, kWaves>(hpw, ps, o32, a, grid, lds_bytes, st, what);
 }

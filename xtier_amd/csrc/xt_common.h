@@ -88,14 +88,28 @@ __device__ inline int32_t uniform_load(const int32_t* p) {
 __device__ inline float uniform_load_f32(const float* p) {
   return *(const __attribute__((address_space(4))) float*)(p);
 }
+// Maxima of scores as single instructions. fmaxf first quiets each operand (v_max_f32 x, x) wherever the compiler
+// cannot prove it already canonical (results of permutes, values merged from branches); attention scores are never
+// signalling NaNs, so these skip that step. The operands must be results of ordinary VALU instructions: the compiler
+// inserts no wait states in front of inline asm, so an MFMA accumulator read here could still be in flight.
+__device__ inline float max2_raw(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ inline float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
 // Maximum and sum of x over lanes l, l ^ 16 and l ^ 32 (the four lanes 16 apart), in VALU permutes: with x as both
 // operands, v_permlane16_swap / v_permlane32_swap hand every lane the pair (x[l], x[l ^ 16]) / (x[l], x[l ^ 32]),
 // in an order that does not matter here (ds_bpermute would take two LDS round trips).
 __device__ inline float max4_lanes16(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const float y = max2_raw(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return max2_raw(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ inline float sum4_lanes16(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -112,6 +126,8 @@ __device__ half2_t fp4x2_to_f16(uint32_t packed);
 template <bool HI>
 __device__ half2_t fp8x2_to_f16(uint32_t packed);
 __device__ half8_t fp8x8_to_f16(uint64_t v);
+__device__ float max2_raw(float a, float b);
+__device__ float max3_raw(float a, float b, float c);
 __device__ float max4_lanes16(float x);
 __device__ int32_t uniform_load(const int32_t* p);
 __device__ float uniform_load_f32(const float* p);
