@@ -51,44 +51,60 @@ __global__ void global_scale_kernel(const uint32_t* __restrict__ ws, float* __re
 
 // The E2M1 code of q = x / d as formats.py:124-127 computes it, without the division. For a midpoint m of the code
 // table, fl(|x| / d) > m holds exactly when |x| / d > m + ulp(m) / 2 (every midpoint has an even last mantissa bit, so
-// the tie rounds down to m), i.e. when |x| > t_m * d. That product (25 by 24 significant bits) is exact in FP64, and
-// an FP32 |x| exceeds a real T exactly when it exceeds T rounded toward -inf to FP32. So the seven thresholds of a
-// block are formed once, and each value takes seven FP32 compares. d must be positive and finite.
-struct Thresholds {
-  float t[7];
-};
-
-__device__ inline Thresholds block_thresholds(float d) {
+// the tie rounds down to m), i.e. when |x| > t_m * d. That product (25 by 24 significant bits) is exact in FP64, and a
+// BF16 |x| exceeds a real T exactly when it exceeds T rounded toward -inf to BF16. So the seven thresholds of a block
+// are formed once as BF16 bit patterns: the FP64 product truncated to BF16 precision (rounding a positive value
+// toward -inf), capped at the largest finite BF16. d must be positive and finite (d >= 1e-30 keeps every product a
+// normal BF16 magnitude).
+__device__ inline void block_thresholds(float d, uint32_t (&t2)[7]) {
   // m + ulp(m) / 2 for m = 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5 (ulp(m) = 2^(e - 23), e the exponent of m)
   constexpr double kMid[7] = {0.25 + 0x1p-26, 0.75 + 0x1p-25, 1.25 + 0x1p-24, 1.75 + 0x1p-24, 2.5 + 0x1p-23,
                               3.5 + 0x1p-23, 5.0 + 0x1p-22};
-  Thresholds th;
+  const double dd = (double)d;
 #pragma unroll
-  for (int i = 0; i < 7; ++i) th.t[i] = __double2float_rd(kMid[i] * (double)d);
-  return th;
+  for (int i = 0; i < 7; ++i) {
+    const uint32_t hi = (uint32_t)((uint64_t)__double_as_longlong(kMid[i] * dd) >> 32);
+    // FP64 high word: exponent (bias 1023) in bits 20-30 and the top 20 mantissa bits; BF16: exponent (bias 127)
+    // in bits 7-14 and the top 7 mantissa bits
+    const uint32_t tb = min((hi >> 13) - ((1023u - 127u) << 7), 0x7F7Fu);
+    t2[i] = tb | (tb << 16);
+  }
 }
 
-// Non-negative floats order as their bit patterns, so |x| > t holds exactly when bits(t) - bits(|x|) is negative
-// (both below 2^31; a NaN |x| exceeds every threshold and codes 7, as the reference's bucketize gives it). The code
-// is found by a three-level search over the seven thresholds, each level's threshold picked with a bitfield select
-// under the masks of the levels above. The sign bit goes with a code above 0 when x < 0 (not for a NaN).
-__device__ inline int32_t above(uint32_t t, uint32_t a) { return (int32_t)(t - a) >> 31; }   // -1 if a > t, else 0
+// Per 16-bit half: 0xFFFF where the half, as a signed integer, is negative, else 0. Written as inline asm so that the
+// compiler keeps the masks as data for single-instruction bitfield selects (it would otherwise rebuild each select
+// as two per-half compares and selects and a permute). The operand must be an ordinary VALU result.
+__device__ inline uint32_t pk_neg_mask(uint32_t x) {
+  uint32_t r;
+  asm("v_pk_ashrrev_i16 %0, 15, %1 op_sel_hi:[0,1]" : "=v"(r) : "v"(x));   // the constant 15 for both halves
+  return r;
+}
+typedef short short2v __attribute__((ext_vector_type(2)));
+typedef unsigned short ushort2v __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t pk_sub16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(short2v, a) - __builtin_bit_cast(short2v, b));
+}
+__device__ inline uint32_t select_bits(uint32_t m, uint32_t a, uint32_t b) { return (m & a) | (~m & b); }
 
-__device__ inline uint32_t e2m1_code(float x, const Thresholds& th) {
-  const uint32_t bits = __float_as_uint(x), a = bits & 0x7FFFFFFFu;
-  const uint32_t t[7] = {__float_as_uint(th.t[0]), __float_as_uint(th.t[1]), __float_as_uint(th.t[2]),
-                         __float_as_uint(th.t[3]), __float_as_uint(th.t[4]), __float_as_uint(th.t[5]),
-                         __float_as_uint(th.t[6])};
-  const uint32_t m4 = above(t[3], a);
-  const uint32_t m2 = above((m4 & t[5]) | (~m4 & t[1]), a);
-  const uint32_t hi = (m2 & t[6]) | (~m2 & t[4]), lo = (m2 & t[2]) | (~m2 & t[0]);
-  const uint32_t m1 = above((m4 & hi) | (~m4 & lo), a);
-  const uint32_t code = (m4 & 4u) | (m2 & 2u) | (m1 & 1u);
-  const bool negative = (int32_t)bits < 0 && a <= 0x7F800000u;
-  return code | (negative && code ? 8u : 0u);
+// Two E2M1 codes at once from one dword of two BF16 values, with the thresholds of block_thresholds. Non-negative
+// BF16 values order as their bit patterns, so |x| > T holds exactly when bits(T) - bits(|x|) is negative (both below
+// 2^15); the code is a three-level search over the seven thresholds on both 16-bit halves at once, each level's
+// threshold picked by a bitfield select under the masks of the levels above. The sign bit goes with a code above 0
+// when x < 0. No value is a NaN here: a NaN anywhere in a block makes its scale, hence d, a NaN, and such a block
+// takes the division form. An infinite value exceeds every (finite) threshold and codes 7. Returns the byte of the two
+// codes (first value in the low nibble).
+__device__ inline uint32_t e2m1_pair(uint32_t w, const uint32_t (&t2)[7]) {
+  const uint32_t a = w & 0x7FFF7FFFu;
+  const uint32_t m4 = pk_neg_mask(pk_sub16(t2[3], a));
+  const uint32_t m2 = pk_neg_mask(pk_sub16(select_bits(m4, t2[5], t2[1]), a));
+  const uint32_t t1 = select_bits(m4, select_bits(m2, t2[6], t2[4]), select_bits(m2, t2[2], t2[0]));
+  const uint32_t m1 = pk_neg_mask(pk_sub16(t1, a));
+  const uint32_t code = (m4 & 0x00040004u) | (m2 & 0x00020002u) | (m1 & 0x00010001u);
+  const uint32_t c = code | ((w >> 12) & 0x00080008u & (m4 | m2 | m1));
+  return (c & 0xFu) | ((c >> 12) & 0xF0u);
 }
 
-// The division form, for a block whose d is not finite (a NaN or infinite global scale).
+// The division form, for a block whose d is not finite (a NaN or infinite global scale, or a NaN in the block).
 __device__ inline uint32_t e2m1_code_div(float x, float d) {
   const float q = x / d;
   const float a_ = __builtin_fabsf(q);
@@ -99,50 +115,23 @@ __device__ inline uint32_t e2m1_code_div(float x, float d) {
   return code;
 }
 
-// Two E2M1 codes at once from one dword of two BF16 values. Every source value is a BF16, and a BF16 value exceeds a
-// real T exactly when it exceeds T rounded toward -inf to BF16, so the thresholds are taken as BF16 bit patterns
-// (the FP32 ones truncated: rounding down twice is rounding down once) and the search of e2m1_code runs on both 16-bit
-// halves with packed 16-bit integer arithmetic. Returns the byte of the two codes (first value in the low nibble).
-typedef short short2v __attribute__((ext_vector_type(2)));
-__device__ inline short2v pk_above(short2v t, short2v a) {   // per half: -1 where a > t, else 0
-  return (t - a) >> (short)15;
-}
-__device__ inline uint32_t as_u32(short2v v) { return __builtin_bit_cast(uint32_t, v); }
-__device__ inline short2v as_s2(uint32_t v) { return __builtin_bit_cast(short2v, v); }
-
-__device__ inline uint32_t e2m1_pair(uint32_t w, const uint32_t (&t2)[7]) {
-  const short2v a = as_s2(w & 0x7FFF7FFFu);
-  const uint32_t m4 = as_u32(pk_above(as_s2(t2[3]), a));
-  const uint32_t m2 = as_u32(pk_above(as_s2((m4 & t2[5]) | (~m4 & t2[1])), a));
-  const uint32_t hi = (m2 & t2[6]) | (~m2 & t2[4]), lo = (m2 & t2[2]) | (~m2 & t2[0]);
-  const uint32_t m1 = as_u32(pk_above(as_s2((m4 & hi) | (~m4 & lo)), a));
-  const uint32_t code = (m4 & 0x00040004u) | (m2 & 0x00020002u) | (m1 & 0x00010001u);
-  // the sign with a code above 0 when the value is negative and not a NaN (a NaN half exceeds 0x7F80)
-  const uint32_t nan = as_u32(pk_above(as_s2(0x7F807F80u), a));
-  const uint32_t sign = (w >> 12) & 0x00080008u & ~nan & (m4 | m2 | m1);
-  const uint32_t c = code | sign;
-  return (c & 0xFu) | ((c >> 12) & 0xF0u);
-}
-
 // 16 BF16 values (eight dwords) -> eight payload bytes (two dwords) and the E4M3 scale byte, with global scale g.
+// The block maximum is a packed 16-bit maximum of the magnitudes' bit patterns (a NaN's exceeds every finite one's, so
+// a NaN wins as in torch's amax); the scale byte's value comes from the hardware E4M3 -> FP16 conversion (exact for
+// every byte, NaN for 0x7F / 0xFF).
 __device__ inline void quantize_block(const uint32_t (&w)[8], float g, bool saturate, uint32_t (&packed)[2],
                                       uint32_t& sbyte) {
-  uint32_t amax_bits = 0;
+  ushort2v mx = {0, 0};
 #pragma unroll
-  for (int k = 0; k < 8; ++k) amax_bits = max(amax_bits, max(w[k] & 0x7FFFu, (w[k] >> 16) & 0x7FFFu));
-  const float bamax = bf16_bits_to_f32(amax_bits);
+  for (int k = 0; k < 8; ++k) mx = __builtin_elementwise_max(mx, __builtin_bit_cast(ushort2v, w[k] & 0x7FFF7FFFu));
+  const float bamax = bf16_bits_to_f32(max((uint32_t)mx.x, (uint32_t)mx.y));
   sbyte = e4m3_encode(bamax / (6.0f * g), saturate);
-  float d = e4m3_decode(sbyte) * g;
+  float d = (float)fp8x2_to_f16<false>(sbyte).x * g;
   d = (d < 1e-30f) ? 1e-30f : d;
   packed[0] = packed[1] = 0u;
   if (__builtin_isfinite(d)) {
-    const Thresholds th = block_thresholds(d);
     uint32_t t2[7];
-#pragma unroll
-    for (int i = 0; i < 7; ++i) {
-      const uint32_t tb = __float_as_uint(th.t[i]) >> 16;   // toward -inf to BF16 (positive: truncation)
-      t2[i] = tb | (tb << 16);
-    }
+    block_thresholds(d, t2);
 #pragma unroll
     for (int k = 0; k < 8; ++k) packed[k >> 2] |= e2m1_pair(w[k], t2) << (8 * (k & 3));
   } else {
@@ -200,7 +189,10 @@ struct StoreArgs {
   int saturate;
 };
 
-constexpr int kStoreUnits = 2;   // 16-value units per thread, their loads all in flight before the first use
+// 16-value units per thread, their loads all in flight before the first use. One: the block arithmetic (about 270
+// VALU instructions per unit) is the larger cost, so more waves in flight beat more loads per wave (a 4096-row K + V
+// append: 4.6 us at one unit per thread, 5.0 at two, 6.0 at four, graph-replayed).
+constexpr int kStoreUnits = 1;
 
 // Unit i of a thread is (blockIdx.x * kStoreUnits + i) * 256 + threadIdx.x: one 16-value block (32 source bytes, 8
 // payload bytes, a scale byte), consecutive threads taking consecutive blocks of a row.
