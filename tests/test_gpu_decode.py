@@ -127,6 +127,26 @@ def test_decode_edge_rows():
     assert np.array_equal(o[1].view(torch.int16).numpy().view(np.uint16), want)
 
 
+def test_decode_lengths_past_the_table_width():
+    """Positions at or past a table row's pitch (table_stride * page_size) are skipped keys even when seq_lens reaches
+    beyond: the table is a contiguous [batch, 30] view into a longer buffer whose next entries (the next row, and after
+    the last row a tail) are valid page ids, so a read past a row would pick up real keys and change the output."""
+    pool, pt, idx, q = _small_case(seed=11)
+    batch, width = idx.shape[0], 30
+    buf = torch.zeros(batch * width + 64, dtype=torch.int32)
+    buf[:batch * width] = pt[:, :width].reshape(-1)
+    buf[batch * width:] = pt[0, :64] if pt.shape[1] >= 64 else pt[0, torch.arange(64) % pt.shape[1]]
+    table = buf.cuda()[:batch * width].view(batch, width)
+    assert table.stride(0) == width
+    seq = np.full(batch, 3008, np.int32)                     # past the 30 * 64 = 1920 positions the table holds
+    scale = 0.0884
+    out = ops.sparse_decode(q.cuda(), pool.raw, table, idx.cuda(), _dev(seq), scale, page_size=64, splits=2)
+    clamped = np.full(batch, width * 64, np.int32)
+    ref, flash, _ = _oracle(pool.raw, bf16_numpy(q), pt[:, :width].numpy(), 64, np.arange(batch), idx.numpy(), None,
+                            clamped, scale)
+    _check(out, ref, flash)
+
+
 @pytest.mark.parametrize('splits', [1, 2, 7, 22, 64])
 def test_decode_splits(splits):
     pool, pt, idx, q = _small_case(seed=splits)

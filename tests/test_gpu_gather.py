@@ -50,6 +50,30 @@ def test_gather_compact_and_zero_fill(heads, dim, slots, dtype):
         assert np.array_equal(out_v.view(torch.int16).cpu().numpy().view(np.uint16), wv), label
 
 
+def test_gather_lengths_past_the_table_width():
+    """Positions at or past a req_to_token row's pitch are invalid even when seq_lens reaches beyond: the table is a
+    contiguous [rows, width] view into a longer buffer of valid slots, so a read past a row would gather real rows."""
+    heads, dim, slots = 4, 128, 9000
+    pool = random_pool(7, slots, heads, dim)
+    rng = np.random.default_rng(5)
+    batch, topk, width = 2, 512, 3000
+    r2t, req, seq, idx = _requests(rng, slots, batch, topk, width, [512, 512], [5000, 5000])   # positions < 5000
+    buf = torch.from_numpy(rng.integers(0, slots, (batch + 1) * width + 4096).astype(np.int32))
+    buf[:(batch + 1) * width] = torch.from_numpy(r2t.reshape(-1))
+    table = buf.cuda()[:(batch + 1) * width].view(batch + 1, width)
+    counts = np.array([512, 512], np.int32)
+    cu = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    dev = lambda a: torch.from_numpy(a).cuda()
+    out_k = torch.full((int(cu[-1]), heads, dim), CANARY, dtype=torch.int16).view(torch.bfloat16).cuda()
+    out_v = out_k.clone()
+    ops.gather(pool.raw, table, dev(req), dev(idx), dev(seq), dev(cu), out_k, out_v, batch, topk, 0)
+    wk = np.full((int(cu[-1]), heads, dim), CANARY, np.uint16)
+    wv = wk.copy()
+    attention.gather_qsa(pool.host, r2t, req, idx, np.minimum(seq, width), cu, wk, wv, batch, topk, 0)
+    assert np.array_equal(out_k.view(torch.int16).cpu().numpy().view(np.uint16), wk)
+    assert np.array_equal(out_v.view(torch.int16).cpu().numpy().view(np.uint16), wv)
+
+
 def _gather_f32(raw, r2t, req, idx, seq, cu, batch, topk, zf, wk, wv):
     """FP16 variant of the oracle gather: the reference rounds the same FP32 values to the output dtype."""
     from oracle import nvfp4

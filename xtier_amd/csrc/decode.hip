@@ -760,7 +760,10 @@ extern "C" int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64
                 (long long)sf_head_stride);
   if (pool_slots <= 0 || pool_slots > 0x7FFFFFFFLL)
     return fail(XT_EINVAL, "%s: pool_slots %lld outside 1..2^31-1", what, (long long)pool_slots);
-  const Addressing ad{pay_head_stride, sf_head_stride, 0, 1, 0, 0, true, nullptr, 0x7FFFFFFF, false, 0.0f, 0.0f};
+  // positions past a table row's pitch are skipped keys, whatever the row's length says (no read past the row)
+  const int max_len =
+      table_stride > 0 ? (int)std::min<int64_t>(0x7FFFFFFF, table_stride * (int64_t)std::max(page_size, 1)) : 0x7FFFFFFF;
+  const Addressing ad{pay_head_stride, sf_head_stride, 0, 1, 0, 0, true, nullptr, max_len, false, 0.0f, 0.0f};
   return decode_impl(what, q, q_row_stride, q_head_stride, k_pay, v_pay, k_scales, v_scales, gk, gv, pool_slots,
                      pay_stride, sf_stride, kv_heads, q_heads, dim, table, table_stride, page_size, row_req, indices,
                      idx_stride, topk, counts, seq_lens, query_pos, scale, out, out_row_stride, out_head_stride,

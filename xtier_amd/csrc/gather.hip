@@ -47,7 +47,8 @@ constexpr int kPieces = 4;
 
 // Decode gather (qsa_fp4.py:119-143): request b = blockIdx.y; its output is a run of 8-value pieces (column c, head h,
 // piece) in output order, so every store of a wave writes 1 KiB of consecutive rows. Column c < num_cols is valid when
-// c < cu_k[b+1] - cu_k[b], its position indices[b, c] (c < topk) lies in [0, seq_lens[b]) and the slot
+// c < cu_k[b+1] - cu_k[b], its position indices[b, c] (c < topk) lies in [0, seq_lens[b]) (and below the table's row
+// pitch) and the slot
 // req_to_token[req_indices[b], pos] in [0, pool_slots); valid columns are dequantized into rows cu_k[b] + c, invalid
 // ones are zeros when zero_fill (columns up to num_cols) and skipped otherwise.
 template <bool FP8>
@@ -61,7 +62,8 @@ __global__ __launch_bounds__(256) void qsa_gather_kernel(
   const int b = blockIdx.y;
   const int32_t start = cu_k[b];
   const int32_t valid_count = cu_k[b + 1] - start;
-  const int32_t length = seq_lens[b];
+  // positions past the table row's pitch are invalid, whatever seq_lens says (no read past the row)
+  const int32_t length = req_stride > 0 ? (int32_t)min((int64_t)seq_lens[b], req_stride) : seq_lens[b];
   const int32_t* tp = req_to_token + req_indices[b] * req_stride;
   const int pieces = 1 << piece_shift;
   const int items = num_cols * heads * pieces;
