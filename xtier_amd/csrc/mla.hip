@@ -500,17 +500,21 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
 // 32k + 4 (lane / 16) .. +3 and 32k + 16 + 4 (lane / 16) .. +3. out = sum_s w_s o_s with w_s = 2^(m_s - max m) l_s /
 // (sum_s 2^(m_s - max m) l_s + sink term). The splits are taken four at a time with all their loads issued together and
 // a running maximum across groups, so the usual four splits cost one round trip; a wave's loads of one split are one
-// contiguous run.
+// contiguous run. A workgroup (256 threads: row, w, four consecutive k) holds 16 heads x 128 dims of output; it
+// stages them in LDS and writes each head's 256 bytes as 16 consecutive 16-byte pieces (written straight from the
+// lane order, every store instruction would scatter 64 pieces of 4 bytes over 16 head rows).
 template <int F>
 __global__ void __launch_bounds__(256) mla_merge_kernel(const MlaArgs a, int rows) {
-  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int lane = (int)(t & 63), k = (int)((t >> 6) & 15);
-  const int64_t rw = t >> 10;                 // row * waves + w
+  __shared__ __align__(16) uint16_t tile[16][128];
+  const int lane = (int)(threadIdx.x & 63), kl = (int)(threadIdx.x >> 6);
+  const int64_t rw = blockIdx.x >> 2;         // row * waves + w
+  const int k0 = 4 * (int)(blockIdx.x & 3), k = k0 + kl;
   const int waves = (a.heads + 15) >> 4;
-  if (rw >= (int64_t)rows * waves) return;
+  if (rw >= (int64_t)rows * waves) return;    // uniform over the workgroup
   const int row = (int)(rw / waves), w = (int)(rw % waves);
-  const int head = 16 * w + (lane & 15), d0 = 32 * k + 4 * (lane >> 4);
-  if (head >= a.heads) return;
+  const int hl = lane & 15, head = 16 * w + hl, d0 = 32 * k + 4 * (lane >> 4);
+  const bool live = head < a.heads;
+  const int hc = live ? head : a.heads - 1;   // padding heads read a live head's partials and write nothing
   float m_run = -__builtin_inff(), l_run = 0.0f;
   float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < a.splits; s0 += 4) {
@@ -519,7 +523,7 @@ __global__ void __launch_bounds__(256) mla_merge_kernel(const MlaArgs a, int row
 #pragma unroll
     for (int i = 0; i < 4; ++i) {   // past the last split: the last one again, weight 0 below
       const int sp = min(s0 + i, a.splits - 1);
-      ml[i] = *reinterpret_cast<const float2*>(a.ml + (((int64_t)row * a.splits + sp) * a.heads + head) * 2);
+      ml[i] = *reinterpret_cast<const float2*>(a.ml + (((int64_t)row * a.splits + sp) * a.heads + hc) * 2);
       const int64_t pi = part_index(a, row, sp, w, k, lane);
       if constexpr (F == kNvfp4) {
         const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.part) + pi);
@@ -562,14 +566,26 @@ __global__ void __launch_bounds__(256) mla_merge_kernel(const MlaArgs a, int row
   }
   const float mu = (m_run == -__builtin_inff()) ? 0.0f : m_run;
   float total = l_run;
-  if (a.sink) total += __builtin_amdgcn_exp2f(a.sink[head] * kLog2e - mu);
+  if (a.sink) total += __builtin_amdgcn_exp2f(a.sink[hc] * kLog2e - mu);
   const float inv = l_run > 0.0f ? 1.0f / total : 0.0f;
+  uint32_t pk[4];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] *= inv;
-  store_vals(a, row, head, d0, o, 4);
-  store_vals(a, row, head, d0 + 16, o + 4, 4);
-  if (a.lse && d0 == 0)
+  for (int e = 0; e < 4; ++e) {
+    const float v0 = o[2 * e] * inv, v1 = o[2 * e + 1] * inv;
+    pk[e] = a.out_dtype == XT_DTYPE_BF16 ? (f32_to_bf16_bits(v0) | (f32_to_bf16_bits(v1) << 16))
+                                         : (f32_to_f16_bits(v0) | (f32_to_f16_bits(v1) << 16));
+  }
+  const int c0 = d0 - 32 * k0;   // this thread's dims within the workgroup's 128: c0 .. c0+3 and c0+16 .. c0+19
+  *reinterpret_cast<uint2*>(&tile[hl][c0]) = make_uint2(pk[0], pk[1]);
+  *reinterpret_cast<uint2*>(&tile[hl][c0 + 16]) = make_uint2(pk[2], pk[3]);
+  if (live && a.lse && d0 == 0)
     a.lse[(int64_t)row * a.heads + head] = l_run > 0.0f ? (mu + __builtin_log2f(l_run)) * kLn2 : -__builtin_inff();
+  __syncthreads();
+  // thread u: head 16 w + u / 16, dims 32 k0 + 8 (u % 16) .. +7
+  const int sh = (int)threadIdx.x >> 4, sc = (int)threadIdx.x & 15;
+  if (16 * w + sh < a.heads)
+    *reinterpret_cast<uint4*>(a.out + (int64_t)row * a.o_rs + (int64_t)(16 * w + sh) * a.o_hs + 32 * k0 + 8 * sc) =
+        *reinterpret_cast<const uint4*>(&tile[sh][8 * sc]);
 }
 
 int check_cache(const char* what, const xt_mla_cache* c, int64_t* pay_stride, int64_t* sf_stride,
