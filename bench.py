@@ -660,7 +660,7 @@ def run_varlen(args, w, ops, workloads):
     q = torch.randn(w.rows, w.q_heads, w.dim, generator=gen, device='cuda').to(torch.bfloat16)
     cu_q = torch.arange(w.rows + 1, dtype=torch.int32, device='cuda')
     cu_k = cu_q * w.keys
-    splits = args.splits or ops.default_splits(w.rows, w.kv_heads, w.keys)
+    splits = args.splits or ops.varlen_splits(w.rows, w.kv_heads, w.q_heads // w.kv_heads, w.keys)
     ws = torch.zeros(ops.varlen_workspace_bytes(w.rows, w.q_heads, w.dim, splits), dtype=torch.uint8, device='cuda')
     out = torch.empty_like(q)
     scale = w.dim ** -0.5

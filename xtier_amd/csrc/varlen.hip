@@ -3,9 +3,13 @@
 // scores in FP32 scaled by softmax_scale * log2(e), exp2, P rounded to BF16 for the PV product, FP32 sums and
 // accumulators; key splits merged in FP32 by the last workgroup of a (row, KV head) to finish, in the same launch.
 //
-// Work decomposition: a workgroup = 8 wavefronts = T head tiles (16 query heads each, T = ceil(group / 16)) x 8 / T
-// key slices of one (row, KV head, key split). A wave walks its slice in steps of 32 keys; the slices of a tile merge
-// through LDS. Workgroups are numbered so that a row's units run on one XCD (workgroup g runs on XCD g % 8).
+// Work decomposition: a workgroup = 8 wavefronts = HPW consecutive KV heads x T head tiles (16 query heads each,
+// T = ceil(group / 16)) x 8 / (HPW T) key slices of one (row, KV head group, key split). A wave walks its slice in
+// steps of 32 keys; the slices of a (KV head, tile) merge through LDS. With HPW = 4 the waves of a slice read the same
+// keys' rows of every KV head at once, so the workgroup streams whole key rows ([keys, KV heads, D] packed); one KV
+// head per workgroup reads its 2D-byte pieces at the key stride, which streamed at 39 % of HBM peak against 64 % for
+// whole rows (batch 32, 4 KV heads, 2048 keys per row, loads alone). Workgroups are numbered so that a row's units run
+// on one XCD (workgroup g runs on XCD g % 8).
 //
 // Lane layouts (16x16x32 MFMA, hl = lane % 16, j = lane / 16):
 //   QK: A = K tile, lane (key hl, dims (D/4) j + 8 kk .. +7 for MFMA kk); B = Q^T, lane (head hl, same dims);
@@ -36,13 +40,14 @@ struct VarlenArgs {
   const int32_t* cu_q;
   const int32_t* cu_k;
   int heads, kv_heads, group, tiles;
+  int hpw, kv_groups;                // KV heads per workgroup, workgroups per (row, split)
   float qscale;                      // softmax scale * log2(e)
   int splits, keys_per_split;        // keys_per_split: a multiple of kVStep
   uint16_t* out;
   int64_t o_rs, o_hs;
   int out_dtype;
   float* part;                       // [rows, splits, heads, D + 4]: accumulators, max (log2), sum
-  int32_t* counters;                 // [rows * kv_heads]
+  int32_t* counters;                 // [rows * kv_groups]
   uint32_t xcd_units, xcd_extra;
 };
 
@@ -163,13 +168,16 @@ __global__ void __launch_bounds__(512) varlen_kernel(const VarlenArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
   const uint32_t g = blockIdx.x, xcd = g & 7u;
   const uint32_t u = xcd * a.xcd_units + min(xcd, a.xcd_extra) + (g >> 3);
-  const uint32_t splits_u = (uint32_t)a.splits, kvh_u = (uint32_t)a.kv_heads;
+  const uint32_t splits_u = (uint32_t)a.splits, groups_u = (uint32_t)a.kv_groups;
   const int split = (int)(u % splits_u);
-  const int kvh = (int)((u / splits_u) % kvh_u);
-  const int row = (int)(u / splits_u / kvh_u);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int kvg = (int)((u / splits_u) % groups_u);
+  const int row = (int)(u / splits_u / groups_u);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int hl = lane & 15, j = lane >> 4;
-  const int tile = wave % a.tiles, slice = wave / a.tiles, slices = kVWaves / a.tiles;
+  // wave = (slice * T + tile) * HPW + KV head within the group
+  const int hw = wave % a.hpw, tile = (wave / a.hpw) % a.tiles, slice = wave / (a.hpw * a.tiles);
+  const int slices = kVWaves / (a.hpw * a.tiles);
+  const int kvh = kvg * a.hpw + hw;
   const int gh = 16 * tile + hl;                 // head within the KV head's group
   const bool head_live = gh < a.group;
   const int head = kvh * a.group + min(gh, a.group - 1);
@@ -237,17 +245,20 @@ __global__ void __launch_bounds__(512) varlen_kernel(const VarlenArgs a) {
   float* row_part = a.part + (int64_t)row * a.splits * a.heads * kPart;
   const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
       row_part, (short)0, a.splits > 1 ? (int)((int64_t)a.splits * a.heads * kPart * 4) : 0, 0x00020000);
-  // unit u: dims 16 dt + 4 uj .. +3 of head 16 utile + uhl (uj fastest, so consecutive threads write one head row)
-  for (int u = (int)threadIdx.x; u < a.tiles * 64 * kND; u += 64 * kVWaves) {
+  // unit u: dims 16 dt + 4 uj .. +3 of head 16 utile + uhl of KV head uhw (uj fastest, so consecutive threads write
+  // one head row)
+  for (int u = (int)threadIdx.x; u < a.hpw * a.tiles * 64 * kND; u += 64 * kVWaves) {
     const int uj = u & 3, rest = u >> 2;
-    const int dt = rest % kND, uhl = (rest / kND) & 15, utile = rest / kND / 16;
+    const int dt = rest % kND, uhl = (rest / kND) & 15, ut = rest / kND / 16;
+    const int utile = ut % a.tiles, uhw = ut / a.tiles;
     const int ugh = 16 * utile + uhl;
     if (ugh >= a.group) continue;
     const int ln = uhl + 16 * uj;
     float mx = -__builtin_inff(), l = 0.0f;
     float4_t o = float4_t{0.f, 0.f, 0.f, 0.f};
     for (int sl = 0; sl < slices; ++sl) {   // online merge: rescale what is held when a larger maximum arrives
-      const float4_t* src = reinterpret_cast<const float4_t*>(mg + ((sl * a.tiles + utile) * 64 + ln) * kLane);
+      const int sw = (sl * a.tiles + utile) * a.hpw + uhw;   // the wave of slice sl of this (KV head, tile)
+      const float4_t* src = reinterpret_cast<const float4_t*>(mg + (sw * 64 + ln) * kLane);
       const float4_t ml = src[kND];
       const float m_new = fmaxf(mx, ml[0]);
       const float mu = (m_new == -__builtin_inff()) ? 0.0f : m_new;
@@ -256,7 +267,7 @@ __global__ void __launch_bounds__(512) varlen_kernel(const VarlenArgs a) {
       l = l * a0 + ml[1] * a1;
       mx = m_new;
     }
-    const int uhead = kvh * a.group + ugh, d0 = 16 * dt + 4 * uj;
+    const int uhead = (kvg * a.hpw + uhw) * a.group + ugh, d0 = 16 * dt + 4 * uj;
     if (a.splits == 1) {
       const float inv = l > 0.0f ? 1.0f / l : 0.0f;
       const float v[4] = {o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
@@ -271,7 +282,7 @@ __global__ void __launch_bounds__(512) varlen_kernel(const VarlenArgs a) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   __shared__ int32_t s_last;
-  int32_t* counter = a.counters + (int64_t)row * a.kv_heads + kvh;
+  int32_t* counter = a.counters + (int64_t)row * a.kv_groups + kvg;
   // The arrival, in the HIP memory model at agent scope: a release fence, then the count (a relaxed read-modify-write,
   // part of the counter's release sequence), then, in the workgroup that arrives last, an acquire fence. The release
   // publishes to every XCD the partials all threads of this workgroup stored (each thread waited for its own stores,
@@ -287,25 +298,47 @@ __global__ void __launch_bounds__(512) varlen_kernel(const VarlenArgs a) {
   }
   __syncthreads();
   if (!s_last) return;
-  // merge: 512 threads over the group's heads x D outputs, 8 consecutive dims each
+  // merge: 512 threads over the KV head group's query heads x D outputs, 8 consecutive dims each; the splits are
+  // taken 8 at a time with all their loads issued together (one round trip for up to 8 splits) and an online rescale
+  // across groups
   const int nthreads = 64 * kVWaves;
   const int64_t sstride = (int64_t)a.heads * kPart;
-  for (int o = threadIdx.x * 8; o < a.group * D; o += nthreads * 8) {
-    const int hh = kvh * a.group + o / D, d0 = o % D;
+  for (int o = threadIdx.x * 8; o < a.hpw * a.group * D; o += nthreads * 8) {
+    const int hh = kvg * a.hpw * a.group + o / D, d0 = o % D;
     const float* base = row_part + (int64_t)hh * kPart;
-    float mx = -__builtin_inff();
-    for (int sp = 0; sp < a.splits; ++sp) mx = fmaxf(mx, base[sp * sstride + D]);
-    const float mu = (mx == -__builtin_inff()) ? 0.0f : mx;
-    float total = 0.0f;
+    float m_run = -__builtin_inff(), l_run = 0.0f;
     float4_t o0 = float4_t{0.f, 0.f, 0.f, 0.f}, o1 = o0;
-    for (int sp = 0; sp < a.splits; ++sp) {
-      const float* pp = base + sp * sstride;
-      const float w = __builtin_amdgcn_exp2f(pp[D] - mu);
-      total += w * pp[D + 1];
-      o0 += w * reinterpret_cast<const float4_t*>(pp + d0)[0];
-      o1 += w * reinterpret_cast<const float4_t*>(pp + d0)[1];
+    for (int s0 = 0; s0 < a.splits; s0 += 8) {
+      float2 ml[8];
+      float4_t x0[8], x1[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {   // past the last split: the last one again, weight 0 below
+        const float* pp = base + min(s0 + i, a.splits - 1) * sstride;
+        ml[i] = *reinterpret_cast<const float2*>(pp + D);
+        x0[i] = reinterpret_cast<const float4_t*>(pp + d0)[0];
+        x1[i] = reinterpret_cast<const float4_t*>(pp + d0)[1];
+      }
+      float mc = m_run;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (s0 + i >= a.splits) ml[i].x = -__builtin_inff();
+        mc = fmaxf(mc, ml[i].x);
+      }
+      const float mu = (mc == -__builtin_inff()) ? 0.0f : mc;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - mu);
+      l_run *= alpha;
+      o0 *= alpha;
+      o1 *= alpha;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float w = __builtin_amdgcn_exp2f(ml[i].x - mu);
+        l_run += w * ml[i].y;
+        o0 += w * x0[i];
+        o1 += w * x1[i];
+      }
+      m_run = mc;
     }
-    const float inv = total > 0.0f ? 1.0f / total : 0.0f;
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
     const float v[8] = {o0[0] * inv, o0[1] * inv, o0[2] * inv, o0[3] * inv,
                         o1[0] * inv, o1[1] * inv, o1[2] * inv, o1[3] * inv};
     store_row(a, query, hh, d0, v, 8);
@@ -367,9 +400,14 @@ extern "C" int xt_varlen_decode_bf16(const void* q, int64_t q_row_stride, int64_
       out_row_stride % 8 || out_head_stride % 8)
     return fail(XT_EINVAL, "%s: q / k / v / out rows must be 16-byte aligned (strides in elements: multiples of 8)",
                 what);
-  if (splits > 1 && (int64_t)rows * kv_heads > kCounterSlots)
-    return fail(XT_EUNSUPPORTED, "%s: %d rows x %d KV heads with key splits exceed %d arrival counters; use splits 1",
-                what, rows, kv_heads, kCounterSlots);
+  // KV heads per workgroup: 4 (or 2) whole-row heads when that many workgroups still fill every CU, else 1
+  const int cus = device_cus();
+  int hpw = 1;
+  for (int h : {4, 2})
+    if (hpw == 1 && kv_heads % h == 0 && h * tiles <= kVWaves && (int64_t)rows * (kv_heads / h) * splits >= cus) hpw = h;
+  if (splits > 1 && (int64_t)rows * (kv_heads / hpw) > kCounterSlots)
+    return fail(XT_EUNSUPPORTED, "%s: %d rows x %d KV head groups with key splits exceed %d arrival counters; use "
+                "splits 1", what, rows, kv_heads / hpw, kCounterSlots);
   const size_t need = xt_varlen_decode_workspace_bytes(rows, heads, dim, splits);
   if (workspace_bytes < need)
     return fail(XT_EWORKSPACE, "%s: workspace %zu bytes < %zu needed", what, workspace_bytes, need);
@@ -390,6 +428,8 @@ extern "C" int xt_varlen_decode_bf16(const void* q, int64_t q_row_stride, int64_
   a.kv_heads = kv_heads;
   a.group = group;
   a.tiles = tiles;
+  a.hpw = hpw;
+  a.kv_groups = kv_heads / hpw;
   a.qscale = softmax_scale * kLog2e;
   a.splits = splits;
   const int per_split = (max_seqlen_k + splits - 1) / splits;
@@ -401,7 +441,7 @@ extern "C" int xt_varlen_decode_bf16(const void* q, int64_t q_row_stride, int64_
   a.out_dtype = out_dtype;
   a.counters = static_cast<int32_t*>(workspace);
   a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
-  const int64_t units = (int64_t)rows * kv_heads * splits;
+  const int64_t units = (int64_t)rows * a.kv_groups * splits;
   if (units > 0x7FFFFFFFLL) return fail(XT_EUNSUPPORTED, "%s: %lld workgroups", what, (long long)units);
   a.xcd_units = (uint32_t)(units / 8);
   a.xcd_extra = (uint32_t)(units % 8);

@@ -315,6 +315,20 @@ def default_splits(rows, kv_heads, topk):
     return max(splits, min(64, math.ceil(topk / 8192)))
 
 
+def varlen_splits(rows, kv_heads, group, max_k):
+    """Key splits for varlen_decode: the fewest that fill every CU with workgroups of 4 (else 2) KV heads, which then
+    stream whole packed key rows, as long as every split keeps at least 128 keys; else default_splits (one KV head per
+    workgroup). Measured on MI355X (256 CUs): batch 32 x 4 KV heads, 2048 keys -> 8 splits of 4 KV heads."""
+    tiles = -(-group // 16)
+    cap = min(64, max(1, max_k // 128))
+    for h in (4, 2):
+        if kv_heads % h == 0 and h * tiles <= 8:
+            s = math.ceil(device_cus() / max(1, rows * (kv_heads // h)))
+            if s <= cap:
+                return max(s, min(64, math.ceil(max_k / 8192)))
+    return default_splits(rows, kv_heads, max_k)
+
+
 def decode_workspace_bytes(rows, q_heads, dim, splits):
     return int(_lib.lib().xt_sparse_decode_workspace_bytes(rows, q_heads, dim, splits))
 
@@ -571,7 +585,7 @@ def varlen_decode(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_
     cu_q, cu_k = (t if t.dtype == torch.int32 else t.to(torch.int32) for t in (cu_seqlens_q, cu_seqlens_k))
     max_k = max(int(max_seqlen_k), 1)
     if splits is None:
-        splits = default_splits(rows, kv_heads, max_k)
+        splits = varlen_splits(rows, kv_heads, heads // kv_heads, max_k)
         need = varlen_workspace_bytes(rows, heads, dim, splits)
         if (splits > 1 and ws is None and torch.cuda.is_current_stream_capturing()
                 and _cached_workspace_bytes(q.device) < need):
