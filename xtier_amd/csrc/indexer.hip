@@ -19,6 +19,9 @@
 #include "xt_common.h"
 #include "xt_host.h"
 
+#include <algorithm>
+#include <atomic>
+
 namespace xt {
 namespace {
 
@@ -668,14 +671,39 @@ extern "C" int xt_topk_rows(const float* x, int64_t ld, int rows, int cols, int 
   return check_launch(what);
 }
 
+// Workgroups of one instantiation that fit a CU at once (its register use sets it), read once per process.
+template <int H, int NK, bool BF>
+static int qsa_per_cu() {
+  static std::atomic<int> cached{0};
+  int n = cached.load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, qsa_logits_kernel<H, NK, BF>, 64 * kQsaWaves, 0) !=
+            hipSuccess || n <= 0)
+      n = 1;
+    cached.store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// The grid: row tiles x key chunks, the chunks sized so that the workgroups fit one round on the CUs (a second round
+// of a few workgroups would take as long as the first: 558 workgroups at 512 per round measured 116 us).
+template <int H, int NK, bool BF>
+static void qsa_go(QsaArgs a, int row_tiles, hipStream_t st) {
+  const int64_t slots = (int64_t)device_cus() * qsa_per_cu<H, NK, BF>();
+  const int64_t chunks = std::max<int64_t>(1, slots / row_tiles);
+  a.keys_per_wg = (int)std::max<int64_t>(32, ((a.keys + chunks - 1) / chunks + 31) / 32 * 32);
+  const dim3 grid((unsigned)row_tiles, (unsigned)((a.keys + a.keys_per_wg - 1) / a.keys_per_wg));
+  hipLaunchKernelGGL((qsa_logits_kernel<H, NK, BF>), grid, dim3(64 * kQsaWaves), 0, st, a);
+}
+
 template <int H>
-static int qsa_launch(int nk, bool bf, const QsaArgs& a, dim3 grid, hipStream_t st) {
+static int qsa_launch(int nk, bool bf, const QsaArgs& a, int row_tiles, hipStream_t st) {
 #define XT_QSA(NK)                                                                                                    \
   if (nk == NK) {                                                                                                    \
     if (bf)                                                                                                          \
-      hipLaunchKernelGGL((qsa_logits_kernel<H, NK, true>), grid, dim3(64 * kQsaWaves), 0, st, a);                   \
+      qsa_go<H, NK, true>(a, row_tiles, st);                                                                         \
     else                                                                                                             \
-      hipLaunchKernelGGL((qsa_logits_kernel<H, NK, false>), grid, dim3(64 * kQsaWaves), 0, st, a);                  \
+      qsa_go<H, NK, false>(a, row_tiles, st);                                                                        \
     return XT_OK;                                                                                                    \
   }
   XT_QSA(4)
@@ -713,21 +741,21 @@ extern "C" int xt_qsa_indexer_logits(const void* q, int64_t q_row_stride, int64_
   a.ld = ld;
   a.rows = rows;
   a.keys = keys;
-  a.keys_per_wg = 1024;
+  a.keys_per_wg = 1024;   // set with the grid in qsa_go
   a.vec_store = (ld % 4 == 0) && aligned(logits, 16);
   const int rows_per_wg = kQsaWaves * kQsaGroups * (32 / heads);
-  const dim3 grid((unsigned)((rows + rows_per_wg - 1) / rows_per_wg), (unsigned)((keys + 1023) / 1024));
+  const int row_tiles = (rows + rows_per_wg - 1) / rows_per_wg;
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const bool bf = dtype == XT_DTYPE_BF16;
   const int nk = dim / 16;
   int e = XT_EUNSUPPORTED;
   switch (heads) {
-    case 1: e = qsa_launch<1>(nk, bf, a, grid, st); break;
-    case 2: e = qsa_launch<2>(nk, bf, a, grid, st); break;
-    case 4: e = qsa_launch<4>(nk, bf, a, grid, st); break;
-    case 8: e = qsa_launch<8>(nk, bf, a, grid, st); break;
-    case 16: e = qsa_launch<16>(nk, bf, a, grid, st); break;
-    case 32: e = qsa_launch<32>(nk, bf, a, grid, st); break;
+    case 1: e = qsa_launch<1>(nk, bf, a, row_tiles, st); break;
+    case 2: e = qsa_launch<2>(nk, bf, a, row_tiles, st); break;
+    case 4: e = qsa_launch<4>(nk, bf, a, row_tiles, st); break;
+    case 8: e = qsa_launch<8>(nk, bf, a, row_tiles, st); break;
+    case 16: e = qsa_launch<16>(nk, bf, a, row_tiles, st); break;
+    case 32: e = qsa_launch<32>(nk, bf, a, row_tiles, st); break;
   }
   if (e != XT_OK) return fail(e, "%s: no kernel for %d heads x %d", what, heads, dim);
   return check_launch(what);
