@@ -16,13 +16,15 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize('cols,k', [(1, 1), (100, 64), (5000, 2048), (100000, 2048), (70000, 4096)])
 def test_topk_rows_bit_for_bit(cols, k):
     g = torch.Generator().manual_seed(cols + k)
-    x = torch.randn(6, cols, generator=g)
+    x = torch.randn(7, cols, generator=g)
     x[0] = torch.round(x[0] * 4) / 4                      # heavy ties
     x[1, : cols // 2] = -math.inf                        # masked half
     x[2] = -math.inf                                     # nothing finite
     if cols > 3:
         x[3, 1], x[3, 2] = math.nan, math.inf            # not finite: never taken
     x[4] = 1.0                                           # all equal: the lowest positions
+    zero = torch.where(torch.rand(cols, generator=g) < 0.5, -0.0, 0.0)
+    x[6] = torch.where(torch.arange(cols) % 7 == 3, x[6].abs() + 0.5, zero)   # -0 and +0 tie below the positives
     xg = x.cuda()
     got = ops.topk_rows(xg, k).cpu().numpy()
     want = ref.topk_rows(x.numpy(), k)

@@ -13,9 +13,12 @@
 //     products to FP32 accuracy.) Keys come from a flat array or, for decode, from
 //     the paged cache (page = block x D E4M3 values, then block FP32 scales) through the block table.
 //   Top-k rows: per row the positions of the topk largest finite values, ascending (ties toward the lower position),
-//     -1 padded. One workgroup per row: a three-pass radix select (11, 11, 10 bits of an order-preserving key) finds
-//     the topk-th largest key T and how many keys equal to T are taken; one pass in position order writes the
-//     positions, each 1024-position chunk placed by a block-wide prefix count.
+//     -1 padded. One workgroup per row: a three-pass radix select over an order-preserving key finds the topk-th
+//     largest key T and how many keys equal to T are taken. Rows up to 98304 columns live in registers: the first
+//     pass (13 bits) leaves a small candidate bucket whose keys go to LDS for the other two passes, and bitmaps of the
+//     taken columns are turned into positions with one block scan. Longer rows are streamed three times (11, 11, 10
+//     bits), and one pass in position order writes the positions, each 1024-position chunk placed by a block-wide
+//     prefix count.
 #include "xt_common.h"
 #include "xt_host.h"
 
@@ -61,10 +64,10 @@ __device__ inline uint32_t block_exclusive_count(bool flag, uint32_t* scratch, u
 // Top-k rows
 
 __device__ inline bool finite_f32(float f) { return (__float_as_uint(f) & 0x7F800000u) != 0x7F800000u; }
-// Order-preserving key: a larger float has a larger key.
+// Order-preserving key: a larger float has a larger key, and -0 has the key of +0 (they compare equal, so they tie).
 __device__ inline uint32_t order_key(float f) {
   const uint32_t u = __float_as_uint(f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return u == 0x80000000u ? 0x80000000u : (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
 constexpr int kTopkThreads = 1024;
@@ -150,13 +153,24 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float* x,
   for (int i = (int)k + tid; i < topk; i += kTopkThreads) o[i] = -1;
 }
 
-// Rows of at most 4 * kTopkRegThreads * kTopkChunks columns (16-byte aligned rows): the row is read once into
-// registers as order keys (a non-finite value as key 0, which no finite value has), and the three radix passes and
-// the ordered write run on them. Chunk i of thread t holds columns 4 (kTopkRegThreads i + t) .. + 3. The write needs
-// one block scan per chunk row: with `remaining` of the keys equal to T taken in column order, the keys taken before a
-// column are the keys above T before it plus min(keys equal to T before it, remaining).
+// Rows of at most kTopkRegCols columns (16-byte aligned rows): the row is read once into registers as order keys (a
+// non-finite value as key 0, which no finite value has; the smallest finite key is 0x00800000). Chunk i of thread t
+// holds columns 4 (kTopkRegThreads i + t) .. + 3.
+//   1. A histogram of the top 13 bits finds the bucket b0 that holds the topk-th largest key.
+//   2. One pass over the registers classifies every key: a bucket above b0 is taken (bit e of byte
+//      kTopkRegThreads i + t of the taken map, so byte j covers columns 4 j .. 4 j + 3), a key in b0 is a candidate,
+//      appended with its column to its wavefront's list in LDS.
+//   3. Two histograms over the candidates (bits 18..9, then 8..0) find the topk-th largest key T and how many keys
+//      equal to T are taken; the candidates above T join the taken map, those equal to T go to the tie map. When a
+//      wavefront's list overflows, the two histograms run over the registers instead and the maps are rewritten
+//      against T.
+//   4. Thread t turns bytes 48 t .. 48 t + 47 of both maps (columns 192 t .. 192 t + 191) into positions in column
+//      order: one block scan places them, and a key equal to T is written only while fewer than `remaining` of them
+//      come before it.
 constexpr int kTopkRegThreads = 512;
 constexpr int kTopkChunks = 48;
+constexpr int kTopkRegCols = 4 * kTopkRegThreads * kTopkChunks;   // 98304
+constexpr int kTopkCandPerWave = 512;   // 8 lists of keys and 8 of columns fill the 32 KB histogram
 
 template <int NW>
 __device__ inline uint32_t block_exclusive_sum(uint32_t v, uint32_t* scratch, uint32_t& total) {
@@ -181,13 +195,58 @@ __device__ inline uint32_t block_exclusive_sum(uint32_t v, uint32_t* scratch, ui
   return before;
 }
 
+// The bucket of histogram h (NBK buckets) that holds the remaining-th largest key, and how many keys of that bucket
+// are then taken. Thread t owns buckets NBK - 1 - NB t down to NBK - NB (t + 1); the exclusive prefix of their counts
+// in thread order is the number of keys in higher buckets. With first_topk >= 0, remaining starts as min(first_topk,
+// keys counted), returned in k. remaining is 0 afterwards when there is nothing to take (the bucket is then
+// meaningless).
+template <int NBK>
+__device__ inline uint32_t pick_bucket(const uint32_t* h, uint32_t& remaining, uint32_t* scratch, uint32_t* sel,
+                                       int first_topk = -1, uint32_t* k = nullptr) {
+  constexpr int NB = NBK / kTopkRegThreads, NW = kTopkRegThreads / 64;
+  const int top = NBK - 1 - NB * (int)threadIdx.x;
+  uint32_t cnt[NB], sum = 0;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    cnt[b] = h[top - b];
+    sum += cnt[b];
+  }
+  uint32_t all;
+  uint32_t above = block_exclusive_sum<NW>(sum, scratch, all);
+  if (first_topk >= 0) {
+    remaining = min((uint32_t)first_topk, all);
+    *k = remaining;
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    if (above < remaining && remaining <= above + cnt[b]) {
+      sel[0] = top - b;
+      sel[1] = remaining - above;
+    }
+    above += cnt[b];
+  }
+  __syncthreads();
+  const uint32_t bucket = sel[0];
+  remaining = remaining == 0 ? 0u : sel[1];
+  __syncthreads();   // sel is rewritten by the next call
+  return bucket;
+}
+
+// Sets the bit of column `col` in a byte map (byte col / 4, bit col % 4) with a word-wide LDS atomic.
+__device__ inline void map_set(uint32_t* map, uint32_t col) {
+  const uint32_t byte = col >> 2;
+  atomicOr(&map[byte >> 2], 1u << (8u * (byte & 3u) + (col & 3u)));
+}
+
 __global__ __launch_bounds__(kTopkRegThreads) void topk_rows_reg_kernel(const float* x, int64_t ld, int cols,
                                                                           int topk, int32_t* out, int64_t out_ld) {
-  constexpr int NW = kTopkRegThreads / 64, NB = 2048 / kTopkRegThreads;   // waves; buckets per thread
-  __shared__ uint32_t hist[2048];
-  __shared__ uint32_t scratch[NW];
-  __shared__ uint32_t sel[2];
-  const int tid = threadIdx.x;
+  constexpr int NW = kTopkRegThreads / 64;
+  constexpr int MAPW = kTopkRegCols / 16;   // words per map
+  __shared__ __align__(16) uint32_t hist[8192];   // the 13-bit histogram, then the candidate lists
+  __shared__ uint32_t hist2[1024];
+  __shared__ __align__(16) uint32_t gtmap[MAPW], eqmap[MAPW];
+  __shared__ uint32_t scratch[NW], sel[2], wcount[NW];
+  const int tid = threadIdx.x, wave = tid >> 6;
   const float* xr = x + (int64_t)blockIdx.x * ld;
   int32_t* o = out + (int64_t)blockIdx.x * out_ld;
   uint32_t key[kTopkChunks][4];
@@ -208,74 +267,149 @@ __global__ __launch_bounds__(kTopkRegThreads) void topk_rows_reg_kernel(const fl
 #pragma unroll
     for (int e = 0; e < 4; ++e) key[i][e] = finite_f32(f[e]) ? order_key(f[e]) : 0u;
   }
-  uint32_t prefix = 0, pmask = 0, remaining = 0, k = 0;
-  for (int pass = 0; pass < 3; ++pass) {
-    const int shift = pass == 0 ? 21 : pass == 1 ? 10 : 0;
-    const uint32_t dmask = pass == 2 ? 0x3FFu : 0x7FFu;
-    for (int i = tid; i < 2048; i += kTopkRegThreads) hist[i] = 0;
+
+  // 1. the top 13 bits
+#pragma unroll
+  for (int j = 0; j < 4; ++j) reinterpret_cast<uint4*>(hist)[tid + kTopkRegThreads * j] = uint4{0, 0, 0, 0};
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kTopkChunks; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (key[i][e] != 0u) atomicAdd(&hist[key[i][e] >> 19], 1u);
+  __syncthreads();
+  uint32_t remaining = 0, k = 0;
+  const uint32_t b0 = pick_bucket<8192>(hist, remaining, scratch, sel, topk, &k);
+  if (k == 0) {   // uniform: no finite value
+    for (int i = tid; i < topk; i += kTopkRegThreads) o[i] = -1;
+    return;
+  }
+
+  // 2. classify: buckets above b0 taken, b0 appended to the wavefront's candidate list (the count stays uniform)
+  uint32_t* cand_key = hist + wave * kTopkCandPerWave;
+  uint32_t* cand_col = hist + (NW + wave) * kTopkCandPerWave;
+  uint8_t* gtb = reinterpret_cast<uint8_t*>(gtmap);
+  uint32_t wc = 0;
+#pragma unroll
+  for (int i = 0; i < kTopkChunks; ++i) {
+    uint32_t nib = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t d = key[i][e] >> 19;
+      nib |= d > b0 ? 1u << e : 0u;
+      const bool c = d == b0;
+      const uint64_t m = __builtin_amdgcn_ballot_w64(c);
+      if (m != 0) {
+        const uint32_t pos =
+            wc + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        if (c && pos < (uint32_t)kTopkCandPerWave) {
+          cand_key[pos] = key[i][e];
+          cand_col[pos] = (uint32_t)(4 * (kTopkRegThreads * i + tid) + e);
+        }
+        wc += (uint32_t)__builtin_popcountll(m);
+      }
+    }
+    gtb[kTopkRegThreads * i + tid] = (uint8_t)nib;
+  }
+#pragma unroll
+  for (int j = 0; j < MAPW / 4 / kTopkRegThreads; ++j)
+    reinterpret_cast<uint4*>(eqmap)[tid + kTopkRegThreads * j] = uint4{0, 0, 0, 0};
+  if ((tid & 63) == 0) wcount[wave] = wc;
+  __syncthreads();
+  bool fits = true;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) fits = fits && wcount[w] <= (uint32_t)kTopkCandPerWave;
+
+  // 3. bits 18..9 and 8..0 of the keys in b0
+  uint32_t t_key;
+  if (fits) {   // uniform
+    const int n = (int)wc;
+    for (int j = tid; j < 1024; j += kTopkRegThreads) hist2[j] = 0;
+    __syncthreads();
+    for (int j = tid & 63; j < n; j += 64) atomicAdd(&hist2[(cand_key[j] >> 9) & 1023u], 1u);
+    __syncthreads();
+    const uint32_t b1 = pick_bucket<1024>(hist2, remaining, scratch, sel);
+    for (int j = tid; j < 512; j += kTopkRegThreads) hist2[j] = 0;
+    __syncthreads();
+    const uint32_t hi1 = (b0 << 10) | b1;
+    for (int j = tid & 63; j < n; j += 64)
+      if ((cand_key[j] >> 9) == hi1) atomicAdd(&hist2[cand_key[j] & 511u], 1u);
+    __syncthreads();
+    const uint32_t b2 = pick_bucket<512>(hist2, remaining, scratch, sel);
+    t_key = (hi1 << 9) | b2;
+    for (int j = tid & 63; j < n; j += 64) {
+      const uint32_t c = cand_key[j];
+      if (c > t_key) map_set(gtmap, cand_col[j]);
+      else if (c == t_key) map_set(eqmap, cand_col[j]);
+    }
+  } else {
+    for (int j = tid; j < 1024; j += kTopkRegThreads) hist2[j] = 0;
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kTopkChunks; ++i)
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (key[i][e] != 0u && (key[i][e] & pmask) == prefix) atomicAdd(&hist[(key[i][e] >> shift) & dmask], 1u);
+        if ((key[i][e] >> 19) == b0) atomicAdd(&hist2[(key[i][e] >> 9) & 1023u], 1u);
     __syncthreads();
-    // thread t owns buckets 2047 - NB t down to 2048 - NB (t + 1); the exclusive prefix of their counts in thread
-    // order is the number of keys in higher buckets
-    uint32_t cnt[NB], sum = 0;
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      cnt[b] = hist[2047 - NB * tid - b];
-      sum += cnt[b];
-    }
-    uint32_t all;
-    uint32_t above = block_exclusive_sum<NW>(sum, scratch, all);
-    if (pass == 0) {
-      k = min((uint32_t)topk, all);
-      remaining = k;
-    }
-    if (k != 0) {
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        if (above < remaining && remaining <= above + cnt[b]) {
-          sel[0] = 2047 - NB * tid - b;
-          sel[1] = remaining - above;
-        }
-        above += cnt[b];
-      }
-    }
+    const uint32_t b1 = pick_bucket<1024>(hist2, remaining, scratch, sel);
+    for (int j = tid; j < 512; j += kTopkRegThreads) hist2[j] = 0;
     __syncthreads();
-    if (k == 0) break;
-    prefix |= sel[0] << shift;
-    pmask |= dmask << shift;
-    remaining = sel[1];
-    __syncthreads();   // sel is rewritten by the next pass
-  }
-  // T = prefix: columns in order, the keys above T and the first `remaining` keys equal to T
-  uint32_t gt_seen = 0, eq_seen = 0;
-  if (k != 0) {
+    const uint32_t hi1 = (b0 << 10) | b1;
+#pragma unroll
+    for (int i = 0; i < kTopkChunks; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if ((key[i][e] >> 9) == hi1) atomicAdd(&hist2[key[i][e] & 511u], 1u);
+    __syncthreads();
+    const uint32_t b2 = pick_bucket<512>(hist2, remaining, scratch, sel);
+    t_key = (hi1 << 9) | b2;
+    uint8_t* eqb = reinterpret_cast<uint8_t*>(eqmap);
 #pragma unroll
     for (int i = 0; i < kTopkChunks; ++i) {
-      uint32_t ngt = 0, neq = 0;
+      uint32_t gn = 0, en = 0;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        ngt += key[i][e] > prefix ? 1u : 0u;
-        neq += (key[i][e] != 0u && key[i][e] == prefix) ? 1u : 0u;
+        gn |= key[i][e] > t_key ? 1u << e : 0u;
+        en |= key[i][e] == t_key ? 1u << e : 0u;
       }
-      // counts up to 4 * kTopkRegThreads per chunk row: (above, equal) packed in one word
-      uint32_t tot;
-      const uint32_t before = block_exclusive_sum<NW>(ngt | (neq << 16), scratch, tot);
-      uint32_t gt_b = gt_seen + (before & 0xFFFFu), eq_b = eq_seen + (before >> 16);
+      gtb[kTopkRegThreads * i + tid] = (uint8_t)gn;
+      eqb[kTopkRegThreads * i + tid] = (uint8_t)en;
+    }
+  }
+  __syncthreads();
+
+  // 4. positions in column order
+  constexpr int TW = MAPW / kTopkRegThreads;   // 12 words of each map per thread
+  uint32_t gw[TW], ew[TW], ng = 0, ne = 0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t kv = key[i][e];
-        const bool gt = kv > prefix, eq = kv != 0u && kv == prefix;
-        if (gt || (eq && eq_b < remaining)) o[gt_b + min(eq_b, remaining)] = 4 * (kTopkRegThreads * i + tid) + e;
-        gt_b += gt ? 1u : 0u;
-        eq_b += eq ? 1u : 0u;
+  for (int j = 0; j < TW / 4; ++j) {
+    const uint4 g = reinterpret_cast<const uint4*>(gtmap)[TW / 4 * tid + j];
+    const uint4 q = reinterpret_cast<const uint4*>(eqmap)[TW / 4 * tid + j];
+    gw[4 * j] = g.x; gw[4 * j + 1] = g.y; gw[4 * j + 2] = g.z; gw[4 * j + 3] = g.w;
+    ew[4 * j] = q.x; ew[4 * j + 1] = q.y; ew[4 * j + 2] = q.z; ew[4 * j + 3] = q.w;
+  }
+#pragma unroll
+  for (int j = 0; j < TW; ++j) {
+    ng += (uint32_t)__builtin_popcount(gw[j]);
+    ne += (uint32_t)__builtin_popcount(ew[j]);
+  }
+  uint32_t tot;
+  uint32_t gt_b = block_exclusive_sum<NW>(ng, scratch, tot);
+  uint32_t eq_b = block_exclusive_sum<NW>(ne, scratch, tot);
+#pragma unroll
+  for (int j = 0; j < TW; ++j) {
+    uint32_t m = gw[j] | ew[j];
+    while (m != 0u) {
+      const uint32_t b = (uint32_t)__builtin_ctz(m);
+      m &= m - 1u;
+      const int col = 4 * (4 * (TW * tid + j) + (int)(b >> 3)) + (int)(b & 7u);
+      if ((gw[j] >> b) & 1u) {
+        o[gt_b + min(eq_b, remaining)] = col;
+        ++gt_b;
+      } else {
+        if (eq_b < remaining) o[gt_b + eq_b] = col;
+        ++eq_b;
       }
-      gt_seen += tot & 0xFFFFu;
-      eq_seen += tot >> 16;
     }
   }
   for (int i = (int)k + tid; i < topk; i += kTopkRegThreads) o[i] = -1;
