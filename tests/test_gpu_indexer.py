@@ -31,6 +31,24 @@ def test_topk_rows_bit_for_bit(cols, k):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize('cols,k', [(96256, 2048), (70000, 512)])
+def test_topk_rows_values_placed_by_position(cols, k):
+    """Rows whose largest values sit at positions picked by the row's layout (one element of every other
+    2048-position block, its complement, one lane of every 64, one position in 97): the selection must not depend
+    on where in the row the large values are."""
+    g = torch.Generator().manual_seed(cols)
+    pos = torch.arange(cols)
+    chunk, lane, elem = pos // 2048, (pos // 4) % 512, pos % 4
+    picked = (chunk % 2 == 0) & (elem == (chunk // 2) % 4)
+    x = torch.randn(4, cols, generator=g)
+    x[0] = torch.where(picked, x[0], x[0] + 10)           # large values everywhere but the picked positions
+    x[1] = torch.where(picked, x[1] + 10, x[1])           # large values only at the picked positions
+    x[2] = torch.where(lane % 64 == 5, x[2] + 10, x[2])   # the large values all in one lane of every wavefront
+    x[3] = torch.where(pos % 97 == 0, x[3], -math.inf)    # about cols / 97 finite values, fewer than k
+    got = ops.topk_rows(x.cuda(), k).cpu().numpy()
+    assert np.array_equal(got, ref.topk_rows(x.numpy(), k))
+
+
 def test_topk_rows_strided_rows_and_out():
     x = torch.randn(5, 3000, device='cuda')
     out = torch.full((5, 100), 7, dtype=torch.int32, device='cuda')
