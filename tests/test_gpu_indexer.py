@@ -13,7 +13,7 @@ from xtier_amd import glm, ops, qsa
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize('cols,k', [(1, 1), (100, 64), (5000, 2048), (100000, 2048), (70000, 4096)])
+@pytest.mark.parametrize('cols,k', [(1, 1), (100, 64), (5000, 2048), (4999, 1000), (100000, 2048), (70000, 4096)])
 def test_topk_rows_bit_for_bit(cols, k):
     g = torch.Generator().manual_seed(cols + k)
     x = torch.randn(7, cols, generator=g)
@@ -47,6 +47,11 @@ def test_topk_rows_values_placed_by_position(cols, k):
     x[3] = torch.where(pos % 97 == 0, x[3], -math.inf)    # about cols / 97 finite values, fewer than k
     got = ops.topk_rows(x.cuda(), k).cpu().numpy()
     assert np.array_equal(got, ref.topk_rows(x.numpy(), k))
+
+
+def test_topk_rows_empty_rows():
+    x = torch.randn(3, 8, device='cuda')[:, :0]          # rows of no column: nothing is read, every entry is -1
+    assert np.array_equal(ops.topk_rows(x, 5).cpu().numpy(), np.full((3, 5), -1, np.int32))
 
 
 def test_topk_rows_strided_rows_and_out():

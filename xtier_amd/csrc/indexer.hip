@@ -156,7 +156,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float* x,
 // Rows of at most kTopkRegCols columns (16-byte aligned rows): the row is read once into registers as order keys (a
 // non-finite value as key 0, which no finite value has; the smallest finite key is 0x00800000). Chunk i of thread t
 // holds columns 4 (kTopkRegThreads i + t) .. + 3.
-//   1. A histogram of the top 13 bits finds the bucket b0 that holds the topk-th largest key.
+//   1. A histogram of the top 13 bits finds the bucket b0 that holds the topk-th largest key (counted as the row
+//      arrives when the loads need no branches).
 //   2. One pass over the registers classifies every key: a bucket above b0 is taken (bit e of byte
 //      kTopkRegThreads i + t of the taken map, so byte j covers columns 4 j .. 4 j + 3), a key in b0 is a candidate,
 //      appended with its column to its wavefront's list in LDS.
@@ -238,6 +239,11 @@ __device__ inline void map_set(uint32_t* map, uint32_t col) {
   atomicOr(&map[byte >> 2], 1u << (8u * (byte & 3u) + (col & 3u)));
 }
 
+// ALIGNED4: cols % 4 == 0, so every chunk row loads as float4 from an address clamped into the row (columns past the
+// end are masked when converted) and the loads have no branches, which lets the histogram of the first chunk rows run
+// while the later ones are still in flight. Otherwise the last chunk rows load per element behind uniform branches,
+// and the histogram starts after the whole row has arrived.
+template <bool ALIGNED4>
 __global__ __launch_bounds__(kTopkRegThreads) void topk_rows_reg_kernel(const float* x, int64_t ld, int cols,
                                                                           int topk, int32_t* out, int64_t out_ld) {
   constexpr int NW = kTopkRegThreads / 64;
@@ -249,34 +255,42 @@ __global__ __launch_bounds__(kTopkRegThreads) void topk_rows_reg_kernel(const fl
   const int tid = threadIdx.x, wave = tid >> 6;
   const float* xr = x + (int64_t)blockIdx.x * ld;
   int32_t* o = out + (int64_t)blockIdx.x * out_ld;
-  uint32_t key[kTopkChunks][4];
-#pragma unroll
-  for (int i = 0; i < kTopkChunks; ++i) {
-    const int c = 4 * (kTopkRegThreads * i + tid);
-    float f[4];
-    if (4 * kTopkRegThreads * (i + 1) <= cols) {   // uniform: the whole chunk row is inside the row
-      const float4_t v = *reinterpret_cast<const float4_t*>(xr + c);
-      f[0] = v[0]; f[1] = v[1]; f[2] = v[2]; f[3] = v[3];
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float y = xr[min(c + e, cols - 1)];   // an address inside the row, used only where c + e < cols
-        f[e] = c + e < cols ? y : __builtin_inff();
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) key[i][e] = finite_f32(f[e]) ? order_key(f[e]) : 0u;
-  }
-
-  // 1. the top 13 bits
+  // 1. the top 13 bits, counted as the row arrives: each chunk row's atomics run while the later chunk rows' loads
+  // are still in flight, so the histogram's LDS time hides under the HBM stream
 #pragma unroll
   for (int j = 0; j < 4; ++j) reinterpret_cast<uint4*>(hist)[tid + kTopkRegThreads * j] = uint4{0, 0, 0, 0};
   __syncthreads();
+  // chunk row i is loaded in step i and converted and counted in step i + kTopkAhead, so kTopkAhead chunk rows of
+  // loads stay in flight while the histogram's atomics run
+  constexpr int kTopkAhead = 4;
+  uint32_t key[kTopkChunks][4];
 #pragma unroll
-  for (int i = 0; i < kTopkChunks; ++i)
+  for (int step = 0; step < kTopkChunks + kTopkAhead; ++step) {
+    if (step < kTopkChunks) {
+      const int i = step, c = 4 * (kTopkRegThreads * i + tid);
+      if (ALIGNED4) {
+        const float4_t v = *reinterpret_cast<const float4_t*>(xr + min(c, cols - 4));
+        key[i][0] = __float_as_uint(v[0]); key[i][1] = __float_as_uint(v[1]);
+        key[i][2] = __float_as_uint(v[2]); key[i][3] = __float_as_uint(v[3]);
+      } else if (4 * kTopkRegThreads * (i + 1) <= cols) {   // uniform: the whole chunk row is inside the row
+        const float4_t v = *reinterpret_cast<const float4_t*>(xr + c);
+        key[i][0] = __float_as_uint(v[0]); key[i][1] = __float_as_uint(v[1]);
+        key[i][2] = __float_as_uint(v[2]); key[i][3] = __float_as_uint(v[3]);
+      } else {   // an address inside the row; columns past the end are masked when converted
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (key[i][e] != 0u) atomicAdd(&hist[key[i][e] >> 19], 1u);
+        for (int e = 0; e < 4; ++e) key[i][e] = __float_as_uint(xr[min(c + e, cols - 1)]);
+      }
+    }
+    if (step >= kTopkAhead) {
+      const int i = step - kTopkAhead;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float f = __uint_as_float(key[i][e]);
+        key[i][e] = finite_f32(f) && 4 * (kTopkRegThreads * i + tid) + e < cols ? order_key(f) : 0u;
+        if (key[i][e] != 0u) atomicAdd(&hist[key[i][e] >> 19], 1u);
+      }
+    }
+  }
   __syncthreads();
   uint32_t remaining = 0, k = 0;
   const uint32_t b0 = pick_bucket<8192>(hist, remaining, scratch, sel, topk, &k);
@@ -794,10 +808,16 @@ extern "C" int xt_topk_rows(const float* x, int64_t ld, int rows, int cols, int 
   const char* what = "xt_topk_rows";
   if (rows < 0 || cols < 0 || topk < 0) return fail(XT_EINVAL, "%s: negative size", what);
   if (rows == 0 || topk == 0) return ok();
-  if (!x || !out) return fail(XT_EINVAL, "%s: a required pointer is null", what);
+  if (!out || (!x && cols > 0)) return fail(XT_EINVAL, "%s: a required pointer is null", what);
   if (ld < cols || out_ld < topk) return fail(XT_EINVAL, "%s: row strides shorter than the rows", what);
-  if (cols <= 4 * kTopkRegThreads * kTopkChunks && ld % 4 == 0 && aligned(x, 16))
-    hipLaunchKernelGGL(topk_rows_reg_kernel, dim3((unsigned)rows), dim3(kTopkRegThreads), 0,
+  // the register-resident rows read at column 0 (and at cols - 4 when cols % 4 == 0); empty rows stream, reading
+  // nothing, and come out all -1
+  const bool in_registers = cols > 0 && cols <= 4 * kTopkRegThreads * kTopkChunks && ld % 4 == 0 && aligned(x, 16);
+  if (in_registers && cols % 4 == 0)
+    hipLaunchKernelGGL(topk_rows_reg_kernel<true>, dim3((unsigned)rows), dim3(kTopkRegThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), x, ld, cols, topk, out, out_ld);
+  else if (in_registers)
+    hipLaunchKernelGGL(topk_rows_reg_kernel<false>, dim3((unsigned)rows), dim3(kTopkRegThreads), 0,
                        reinterpret_cast<hipStream_t>(stream), x, ld, cols, topk, out, out_ld);
   else
     hipLaunchKernelGGL(topk_rows_kernel, dim3((unsigned)rows), dim3(kTopkThreads), 0,
