@@ -266,7 +266,7 @@ __global__ __launch_bounds__(kTopkRegThreads) void topk_rows_reg_kernel(const fl
   __syncthreads();
   // chunk row i is loaded in step i and converted and counted in step i + kTopkAhead, so kTopkAhead chunk rows of
   // loads stay in flight while the histogram's atomics run
-  constexpr int kTopkAhead = 4;
+  constexpr int kTopkAhead = 2;
   uint32_t key[kTopkChunks][4];
 #pragma unroll
   for (int step = 0; step < kTopkChunks + kTopkAhead; ++step) {
