@@ -382,7 +382,9 @@ int xt_dsa_paged_mqa_logits(const void* q, int64_t q_row_stride, int64_t q_head_
 /* The selection that turns logits into the index lists the attention entry points read (the int32 [batch, topk],
  * -1 padded format the reference's top-k producers hand to them, e.g. qsa_fp4.py:122 topk_indices): for each row of
  * x (FP32 [rows, ld], columns 0 .. cols - 1) the positions of the topk largest finite values in ascending order, ties
- * toward the lower position, -1 after the last (a row with fewer finite values than topk). out int32 [rows, out_ld]. */
+ * toward the lower position (-0 and +0 tie), -1 after the last (a row with fewer finite values than topk). out int32
+ * [rows, out_ld]. Only columns 0 .. cols - 1 of a row are read; with cols == 0 nothing is read (x may be null) and
+ * every entry is -1. */
 int xt_topk_rows(const float* x, int64_t ld, int rows, int cols, int topk, int32_t* out, int64_t out_ld,
                  xt_stream_t stream);
 
