@@ -60,7 +60,8 @@ struct Geo {
   static constexpr int kWaveLds = kStep * kVRow + kStep * kSf;   // V tile + V scale tile per wave
   static constexpr int kPartStride = D + 4;            // floats per partial (split, head): accumulators, max, sum, pad
   static constexpr int kMergeRow = 32 * kNT + 4;       // floats per lane in the slice merge: accumulators, max, sum, pad
-  static constexpr int kPrefetch = D >= 256 ? 1 : 4;   // steps of loads in flight per wave (D = 256: registers)
+  static constexpr int kPrefetch = D >= 256 ? 1 : 2;   // steps of loads in flight per wave (D = 256: registers;
+                                                       // batch-32 decode: 2 steps 19.1 us, 4 steps 20.1 us)
   template <int W>
   static constexpr int kMergeLds = W * 64 * kMergeRow * 4;   // one merge region per wave
 };
@@ -356,14 +357,6 @@ __device__ inline void compute_step(const WaveCtx& w, int step, const Step<D>& d
   }
 }
 
-// A partial's 16-byte piece, written through to memory (sc1), so that the release of the arrival below has few dirty
-// L2 lines to write back; the ordering itself comes from that release and the last arriver's acquire.
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-__device__ inline void store_through(__amdgpu_buffer_rsrc_t r, int byte_off, float4_t v) {
-  const u32x4_t w = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
-  __builtin_amdgcn_raw_buffer_store_b128(w, r, byte_off, 0, 16);
-}
-
 __device__ inline void store_out(const DecodeArgs& a, int row, int head, int d0, const float* v, int n) {
   uint16_t* o = a.out + (int64_t)row * a.o_rs + (int64_t)head * a.o_hs + d0;
   for (int e = 0; e < n; e += 2) {
@@ -615,48 +608,30 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
         a.lse[(int64_t)row * a.q_heads + head] = l > 0.0f ? (mx + __builtin_log2f(l)) * kLn2 : -__builtin_inff();
     } else {               // 3. partials of this row, written through
       const int at = ((split * a.q_heads + head) * G::kPartStride) * 4;
-      store_through(pr, at + d0 * 4, o);
-      if (d0 == 0) store_through(pr, at + D * 4, float4_t{mx, l, 0.0f, 0.0f});
+      store_partial(pr, at + d0 * 4, o);
+      if (d0 == 0) store_partial(pr, at + D * 4, float4_t{mx, l, 0.0f, 0.0f});
     }
   }
   if (a.splits == 1) return;
-  // the last workgroup of (row, KV group) to arrive merges the partials
-  __builtin_amdgcn_s_waitcnt(0);   // this thread's stores have reached memory
-  __syncthreads();
-  __shared__ int32_t s_last;
+  // the last workgroup of (row, KV group) to arrive merges the partials (the split arrival of xt_common.h)
+  __shared__ int s_last;
   int32_t* counter = a.counters + (int64_t)row * a.kv_groups + kvg;
-  // The arrival, in the HIP memory model at agent scope: a release fence, then the count (a relaxed read-modify-write,
-  // part of the counter's release sequence), then, in the workgroup that arrives last, an acquire fence. The release
-  // publishes to every XCD the partials all threads of this workgroup stored (each thread waited for its own stores,
-  // and the barrier above orders them before thread 0's fence); the last arriver's acquire orders its loads of the
-  // other workgroups' partials below (after the second barrier) behind their releases. Only the last arriver pays for
-  // the acquire (batch-32 decode: an acquire-release count in every workgroup added 2.3 us to the call over an
-  // unordered count, this form 1.5 us).
-  if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    const bool last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.splits - 1;
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    s_last = last;
-  }
-  __syncthreads();
-  if (!s_last) return;
+  if (!arrive_last(counter, a.splits, &s_last)) return;
   // all threads, 8 consecutive outputs each: head h0 + o / D, d0 = o % D; loads of 8 splits at a time together
   const int h0 = kvg * HPW * a.group;
   const int nh = min(HPW * a.group, a.q_heads - h0);
   for (int o = threadIdx.x * 8; o < nh * D; o += blockDim.x * 8) {
     const int hh = h0 + o / D, d0 = o % D;
-    const float* base = row_part + (int64_t)hh * G::kPartStride;
-    const int64_t sstride = (int64_t)a.q_heads * G::kPartStride;
     float m_run = -__builtin_inff(), l_run = 0.0f;
     float4_t o0 = float4_t{0.f, 0.f, 0.f, 0.f}, o1 = o0;
     for (int s0 = 0; s0 < a.splits; s0 += 8) {
       float4_t ml[8], x0[8], x1[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {   // past the last split: reload the last one, weight 0 below
-        const float* pp = base + min(s0 + i, a.splits - 1) * sstride;
-        ml[i] = reinterpret_cast<const float4_t*>(pp + D)[0];
-        x0[i] = reinterpret_cast<const float4_t*>(pp + d0)[0];
-        x1[i] = reinterpret_cast<const float4_t*>(pp + d0)[1];
+        const int at = (min(s0 + i, a.splits - 1) * a.q_heads + hh) * G::kPartStride * 4;
+        ml[i] = load_partial(pr, at + D * 4);
+        x0[i] = load_partial(pr, at + d0 * 4);
+        x1[i] = load_partial(pr, at + d0 * 4 + 16);
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i)
@@ -686,7 +661,7 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
       a.lse[(int64_t)row * a.q_heads + hh] =
           l_run > 0.0f ? (m_run + __builtin_log2f(l_run)) * kLn2 : -__builtin_inff();
   }
-  if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  reset_counter(counter);
 }
 
 }  // namespace

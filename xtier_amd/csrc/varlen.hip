@@ -153,13 +153,6 @@ __device__ inline void store_row(const VarlenArgs& a, int64_t query, int head, i
   }
 }
 
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-// 16 bytes written through (sc1): the arrival's release then has few dirty L2 lines to write back
-__device__ inline void store_through(__amdgpu_buffer_rsrc_t r, int byte_off, float4_t v) {
-  const u32x4_t w = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
-  __builtin_amdgcn_raw_buffer_store_b128(w, r, byte_off, 0, 16);
-}
-
 template <int D, int P>
 __global__ void __launch_bounds__(512) varlen_kernel(const VarlenArgs a) {
   constexpr int kRow = 2 * D + 16;
@@ -274,38 +267,21 @@ __global__ void __launch_bounds__(512) varlen_kernel(const VarlenArgs a) {
       store_row(a, query, uhead, d0, v, 4);
     } else {   // partials of this (row, split), written through; the last workgroup of (row, KV head) merges them
       const int at = ((split * a.heads + uhead) * kPart) * 4;
-      store_through(pr, at + d0 * 4, o);
-      if (d0 == 0) store_through(pr, at + D * 4, float4_t{mx, l, 0.0f, 0.0f});
+      store_partial(pr, at + d0 * 4, o);
+      if (d0 == 0) store_partial(pr, at + D * 4, float4_t{mx, l, 0.0f, 0.0f});
     }
   }
   if (a.splits == 1) return;
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  __shared__ int32_t s_last;
+  // the last workgroup of (row, KV head group) to arrive merges the partials (the split arrival of xt_common.h)
+  __shared__ int s_last;
   int32_t* counter = a.counters + (int64_t)row * a.kv_groups + kvg;
-  // The arrival, in the HIP memory model at agent scope: a release fence, then the count (a relaxed read-modify-write,
-  // part of the counter's release sequence), then, in the workgroup that arrives last, an acquire fence. The release
-  // publishes to every XCD the partials all threads of this workgroup stored (each thread waited for its own stores,
-  // and the barrier above orders them before thread 0's fence); the last arriver's acquire orders its loads of the
-  // other workgroups' partials below (after the second barrier) behind their releases. Only the last arriver pays for
-  // the acquire (batch-32 decode: an acquire-release count in every workgroup added 2.3 us to the call over an
-  // unordered count, this form 1.5 us).
-  if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    const bool last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.splits - 1;
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    s_last = last;
-  }
-  __syncthreads();
-  if (!s_last) return;
+  if (!arrive_last(counter, a.splits, &s_last)) return;
   // merge: 512 threads over the KV head group's query heads x D outputs, 8 consecutive dims each; the splits are
   // taken 8 at a time with all their loads issued together (one round trip for up to 8 splits) and an online rescale
   // across groups
   const int nthreads = 64 * kVWaves;
-  const int64_t sstride = (int64_t)a.heads * kPart;
   for (int o = threadIdx.x * 8; o < a.hpw * a.group * D; o += nthreads * 8) {
     const int hh = kvg * a.hpw * a.group + o / D, d0 = o % D;
-    const float* base = row_part + (int64_t)hh * kPart;
     float m_run = -__builtin_inff(), l_run = 0.0f;
     float4_t o0 = float4_t{0.f, 0.f, 0.f, 0.f}, o1 = o0;
     for (int s0 = 0; s0 < a.splits; s0 += 8) {
@@ -313,10 +289,11 @@ __global__ void __launch_bounds__(512) varlen_kernel(const VarlenArgs a) {
       float4_t x0[8], x1[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {   // past the last split: the last one again, weight 0 below
-        const float* pp = base + min(s0 + i, a.splits - 1) * sstride;
-        ml[i] = *reinterpret_cast<const float2*>(pp + D);
-        x0[i] = reinterpret_cast<const float4_t*>(pp + d0)[0];
-        x1[i] = reinterpret_cast<const float4_t*>(pp + d0)[1];
+        const int at = (min(s0 + i, a.splits - 1) * a.heads + hh) * kPart * 4;
+        const float4_t m4 = load_partial(pr, at + D * 4);
+        ml[i] = make_float2(m4[0], m4[1]);
+        x0[i] = load_partial(pr, at + d0 * 4);
+        x1[i] = load_partial(pr, at + d0 * 4 + 16);
       }
       float mc = m_run;
 #pragma unroll
@@ -343,7 +320,7 @@ __global__ void __launch_bounds__(512) varlen_kernel(const VarlenArgs a) {
                         o1[0] * inv, o1[1] * inv, o1[2] * inv, o1[3] * inv};
     store_row(a, query, hh, d0, v, 8);
   }
-  if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  reset_counter(counter);
 }
 
 template <int D>

@@ -117,8 +117,46 @@ __device__ inline float sum4_lanes16(float x) {
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
+// Split arrival: the workgroups of one output (key splits of a row) leave partial results in a workspace and count
+// their arrivals; the last to arrive merges. The protocol keeps every access to the shared partials coherent by
+// itself, so no fence has to write back or invalidate a whole L2 (an agent-scope release fence is a buffer_wbl2 and
+// an acquire a buffer_inv; on the batch-32 decode's 256 workgroups the two cost 2.4 us per launch):
+//   1. every thread stores its pieces of the partial with sc1 (written through to memory, the coherence point of all
+//      XCDs; the bits of an agent-scope atomic store), then waits for their completion (s_waitcnt vmcnt(0));
+//   2. a workgroup barrier, then thread 0 counts the arrival with a system-scope atomic add (sc1: performed at memory,
+//      coherent whichever XCD the workgroups ran on); it is issued after every store of the workgroup completed;
+//   3. the workgroup that sees the count reach splits - 1 passes a second barrier and reads the partials with sc0 sc1
+//      (missing L1 and any L2 copy, so the reads come from memory), issued after the count returned.
+// Every partial a last arriver reads was therefore complete in memory before its count, and the count is what the
+// last arriver waited for. The last arriver resets the counter (a system-scope store) for the next call.
+typedef uint32_t xt_u32x4_t __attribute__((ext_vector_type(4)));
+__device__ inline void store_partial(__amdgpu_buffer_rsrc_t r, int byte_off, float4_t v) {
+  const xt_u32x4_t w = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+  __builtin_amdgcn_raw_buffer_store_b128(w, r, byte_off, 0, 16 /* sc1 */);
+}
+__device__ inline float4_t load_partial(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  const xt_u32x4_t w = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 17 /* sc0 sc1 */);
+  return float4_t{__uint_as_float(w[0]), __uint_as_float(w[1]), __uint_as_float(w[2]), __uint_as_float(w[3])};
+}
+// Called by every thread after its partial stores. True in every thread of the workgroup that arrived last among
+// `splits`. `flag` is a __shared__ int of the caller.
+__device__ inline bool arrive_last(int32_t* counter, int splits, int* flag) {
+  __builtin_amdgcn_s_waitcnt(0);   // this thread's partial stores are complete
+  __syncthreads();
+  if (threadIdx.x == 0)
+    *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == splits - 1;
+  __syncthreads();
+  return *flag;
+}
+__device__ inline void reset_counter(int32_t* counter) {
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 #else
 // The host pass parses device code without the gfx950 builtins; these declarations are never code-generated.
+__device__ void store_partial(__amdgpu_buffer_rsrc_t r, int byte_off, float4_t v);
+__device__ float4_t load_partial(__amdgpu_buffer_rsrc_t r, int byte_off);
+__device__ bool arrive_last(int32_t* counter, int splits, int* flag);
+__device__ void reset_counter(int32_t* counter);
 template <int SEL>
 __device__ float2_t fp4x2_to_f32(uint32_t packed);
 template <int SEL>
