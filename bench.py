@@ -33,6 +33,26 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def emit(record):
+    """Prints the record as one JSON line, with the GPU it ran on: name, architecture, compute units and the shader
+    clock read right after the timed region (xt_clock_probe)."""
+    import torch
+
+    from xtier_amd import ops
+    props = torch.cuda.get_device_properties(0)
+    try:
+        mhz = ops.clock_mhz()
+    except Exception as e:  # noqa: BLE001 - the record is printed without the clock rather than not at all
+        log(f'clock probe failed: {e}')
+        mhz = None
+    record['device'] = {'name': props.name, 'arch': getattr(props, 'gcnArchName', None),
+                        'compute_units': props.multi_processor_count,
+                        'shader_clock_mhz': None if mhz is None else round(mhz, 1),
+                        'clock_read': 'core clock ticks over 100 MHz ticks while one wavefront runs, after the timed '
+                                      'region'}
+    print(json.dumps(record), flush=True)
+
+
 def cpu_model():
     try:
         for line in open('/proc/cpuinfo'):
@@ -52,17 +72,19 @@ def cpu_threads():
 
 
 def time_steps(step, layers, steps, warmup):
-    """Times exactly `steps` layer-steps. After `warmup` eager steps, a graph of `layers` layer-steps (layer l on its
-    own pool) is replayed steps // layers times and a graph of the remaining steps once, with HIP events on the
-    launching stream around each replay. Returns (ms per layer-step over the whole timed region, per-layer-step µs of
-    each full replay)."""
+    """Times exactly `steps` layer-steps. After `warmup` eager steps, a graph of g layer-steps (layer l on its own
+    pool, g = min(layers, steps // 5), so that at least five full replays are timed) is replayed steps // g times and a
+    graph of the remaining steps once, with HIP events on the launching stream around each replay. Returns (ms per
+    layer-step over the whole timed region, per-layer-step µs of each full replay, g: the pools the timed region
+    rotates)."""
     import torch
+    g_len = max(1, min(layers, steps // 5 if steps >= 5 else steps))
     for i in range(warmup):
-        step(i % layers)
+        step(i % g_len)
     torch.cuda.synchronize()
-    full, rest = divmod(steps, layers)
+    full, rest = divmod(steps, g_len)
     graphs = []
-    for n in (layers if full else 0, rest):
+    for n in (g_len if full else 0, rest):
         g = None
         if n:
             g = torch.cuda.CUDAGraph()
@@ -81,11 +103,11 @@ def time_steps(step, layers, steps, warmup):
         graphs[1].replay()
     ev[-1].record()
     torch.cuda.synchronize()
-    per = [ev[i].elapsed_time(ev[i + 1]) * 1e3 / layers for i in range(full)]
-    return ev[0].elapsed_time(ev[-1]) / steps, per
+    per = [ev[i].elapsed_time(ev[i + 1]) * 1e3 / g_len for i in range(full)]
+    return ev[0].elapsed_time(ev[-1]) / steps, per, g_len
 
 
-def spread(per_step_us):
+def spread(per_step_us, launches_per_replay):
     """Median and p10 / p90 of the per-layer-step times of the full replays."""
     import numpy as np
     if not per_step_us:
@@ -93,7 +115,7 @@ def spread(per_step_us):
     a = np.asarray(per_step_us)
     return {'median_us': round(float(np.median(a)), 3), 'p10_us': round(float(np.percentile(a, 10)), 3),
             'p90_us': round(float(np.percentile(a, 90)), 3), 'replays': len(a),
-            'unit': 'µs per layer-step, per graph replay'}
+            'launches_per_replay': launches_per_replay, 'unit': 'µs per layer-step, per graph replay'}
 
 
 def build_layer(w, gen, layout, workloads, KVPool):
@@ -230,14 +252,14 @@ def run_prefill(args, w, ops, workloads, KVPool):
                           query_pos=inp.q_pos, out=out, splits=splits, ws=ws)
 
     steps = max(1, args.steps)
-    ms, per = time_steps(lambda layer: step(), 1, steps, max(1, args.warmup))
+    ms, per, rot = time_steps(lambda layer: step(), 1, steps, max(1, args.warmup))
     tflops = w.flops() / (ms * 1e-3) / 1e12
     gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
     log(f'{w.name}: {ms * 1e3:.1f} us per step, {tflops:.1f} TFLOP/s ({tflops / MFMA_PEAK_TFLOPS:.1%} of '
         f'{MFMA_PEAK_TFLOPS:.0f}), gathered {gbs:.0f} GB/s')
     record = {
         'metric': 'NVFP4-KV sparse prefill attention TFLOP/s (chunk with quantize-on-append)', 'value': round(tflops, 2),
-        'unit': 'TFLOP/s', 'n_gpus': 1, 'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per),
+        'unit': 'TFLOP/s', 'n_gpus': 1, 'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per, rot),
         'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f16', 'data': 'synthetic',
         'config': {'workload': w.name, 'q_heads': w.q_heads, 'kv_heads': w.kv_heads, 'head_dim': w.dim,
                    'context': w.ctx0, 'chunk': w.chunk, 'topk': w.topk, 'recent': w.recent, 'page': w.page,
@@ -247,7 +269,7 @@ def run_prefill(args, w, ops, workloads, KVPool):
                      'frac': round(tflops / MFMA_PEAK_TFLOPS, 4), 'traffic': None},
         'cpu_baseline': None if args.no_cpu_baseline else prefill_cpu(pool, inp, w, scale, args.cpu_seconds),
     }
-    print(json.dumps(record), flush=True)
+    emit(record)
 
 
 def prefill_cpu(pool, inp, w, scale, seconds):
@@ -323,25 +345,25 @@ def run_mla(args, w, ops, workloads):
         ops.sparse_mla(inp.q, pools[layer], inp.slots, None, None, scale, out=out, lse=lse, splits=splits, ws=ws)
 
     steps = max(1, args.steps)
-    ms, per = time_steps(step, layers, steps, max(1, args.warmup))
+    ms, per, rot = time_steps(step, layers, steps, max(1, args.warmup))
     tflops = w.flops() / (ms * 1e-3) / 1e12
     gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
     log(f'{w.name}: {ms * 1e3:.1f} us per step, {tflops:.1f} TFLOP/s ({tflops / MFMA_PEAK_TFLOPS:.1%} of '
         f'{MFMA_PEAK_TFLOPS:.0f}), {gbs:.0f} GB/s gathered, splits {splits}')
     record = {
         'metric': 'NVFP4 sparse MLA attention TFLOP/s', 'value': round(tflops, 2), 'unit': 'TFLOP/s', 'n_gpus': 1,
-        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per), 'higher_is_better': True,
+        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per, rot), 'higher_is_better': True,
         'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16' if w.fmt == 'fp8_v4' else 'f16', 'data': 'synthetic',
         'config': {'workload': w.name, 'rows': w.rows, 'heads': w.heads, 'latent': w.latent, 'rope': w.rope,
                    'context': w.ctx, 'topk': w.topk, 'causal': w.causal,
                    'kv_format': 'fp8 v4 pages' if w.fmt == 'fp8_v4' else 'nvfp4 latent + bf16 rope',
-                   'layers_rotated': layers, 'splits': splits, 'cache_layout': args.layout},
+                   'layers_rotated': rot, 'splits': splits, 'cache_layout': args.layout},
         'us_per_step': round(ms * 1e3, 2), 'gathered_gbs': round(gbs, 1),
         'roofline': {'bound': 'mfma', 'achieved': round(tflops, 2), 'peak': MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
                      'frac': round(tflops / MFMA_PEAK_TFLOPS, 4), 'traffic': None},
         'cpu_baseline': None if args.no_cpu_baseline else mla_cpu(pools[0], inp, w, scale, args.cpu_seconds),
     }
-    print(json.dumps(record), flush=True)
+    emit(record)
 
 
 def mla_cpu(cache, inp, w, scale, seconds):
@@ -422,23 +444,23 @@ def run_block(args, w, ops, workloads):
                               inp.seq_lens, w.block, out=out, splits=splits, ws=ws)
 
     steps = max(1, args.steps)
-    ms, per = time_steps(step, layers, steps, max(1, args.warmup))
+    ms, per, rot = time_steps(step, layers, steps, max(1, args.warmup))
     gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
     log(f'{w.name}: {ms * 1e3:.2f} us per layer-step, {gbs:.0f} GB/s algorithmic ({gbs / HBM_PEAK_GBS:.1%} of '
         f'{HBM_PEAK_GBS:.0f}), splits {splits}')
     record = {
         'metric': 'NVFP4-KV block-sparse decode HBM GB/s', 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1,
-        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per), 'higher_is_better': True,
+        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per, rot), 'higher_is_better': True,
         'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f16', 'data': 'synthetic',
         'config': {'workload': w.name, 'batch': w.batch, 'q_heads': w.q_heads, 'kv_heads': w.kv_heads,
                    'head_dim': w.dim, 'context': w.ctx, 'topk_blocks': w.topk_blocks, 'block': w.block,
-                   'kv_format': 'nvfp4 head-major pages', 'layers_rotated': layers, 'splits': splits},
+                   'kv_format': 'nvfp4 head-major pages', 'layers_rotated': rot, 'splits': splits},
         'us_per_layer_step': round(ms * 1e3, 3), 'tokens_per_s': round(w.batch / (ms * 1e-3), 1),
         'roofline': {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None},
         'cpu_baseline': None if args.no_cpu_baseline else block_cpu(pools[0], inp, w, args.cpu_seconds),
     }
-    print(json.dumps(record), flush=True)
+    emit(record)
 
 
 def block_cpu(pool, inp, w, seconds):
@@ -498,8 +520,8 @@ def run_block_prefill(args, w, ops, workloads):
             ops.dequantize_context(pay, sc, inp.req_to_token, inp.slot_ids, inp.seq_lens, rows, out=dst)
 
     steps = max(1, args.steps)
-    ms, per = time_steps(step, layers, steps, max(1, args.warmup))
-    copy_ms, _ = time_steps(copy, layers, steps, max(1, args.warmup))
+    ms, per, rot = time_steps(step, layers, steps, max(1, args.warmup))
+    copy_ms, _, _ = time_steps(copy, layers, steps, max(1, args.warmup))
     tflops = w.flops() / (ms * 1e-3) / 1e12
     gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
     copy_gbs = w.copy_bytes() / (copy_ms * 1e-3) / 1e9
@@ -508,11 +530,11 @@ def run_block_prefill(args, w, ops, workloads):
         f'= {copy_gbs:.0f} GB/s ({copy_gbs / HBM_PEAK_GBS:.1%})')
     record = {
         'metric': 'NVFP4-KV block-sparse prefill TFLOP/s', 'value': round(tflops, 2), 'unit': 'TFLOP/s',
-        'n_gpus': 1, 'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per), 'higher_is_better': True,
+        'n_gpus': 1, 'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per, rot), 'higher_is_better': True,
         'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f16', 'data': 'synthetic',
         'config': {'workload': w.name, 'q_len': w.q_len, 'prefix': w.prefix, 'q_heads': w.q_heads,
                    'kv_heads': w.kv_heads, 'head_dim': w.dim, 'topk_blocks': w.topk_blocks, 'block': w.block,
-                   'block_size_q': 1, 'kv_format': 'nvfp4 head-major pages', 'layers_rotated': layers,
+                   'block_size_q': 1, 'kv_format': 'nvfp4 head-major pages', 'layers_rotated': rot,
                    'splits': splits},
         'us_per_chunk': round(ms * 1e3, 2), 'listed_kv_gbs': round(gbs, 1),
         'context_copy': {'us': round(copy_ms * 1e3, 2), 'bytes': w.copy_bytes(), 'gbs': round(copy_gbs, 1),
@@ -521,7 +543,7 @@ def run_block_prefill(args, w, ops, workloads):
                      'frac': round(tflops / MFMA_PEAK_TFLOPS, 4), 'traffic': None},
         'cpu_baseline': None if args.no_cpu_baseline else block_prefill_cpu(pools[0], inp, w, args.cpu_seconds),
     }
-    print(json.dumps(record), flush=True)
+    emit(record)
 
 
 def block_prefill_cpu(pool, inp, w, seconds):
@@ -584,24 +606,24 @@ def run_gather(args, name, ops, workloads, KVPool):
             ops.pack(pools[layer], r2t, req, cu, batch * topk, topk, torch.bfloat16)
 
     steps = max(1, args.steps)
-    ms, per = time_steps(step, layers, steps, max(1, args.warmup))
+    ms, per, rot = time_steps(step, layers, steps, max(1, args.warmup))
     rows = batch * topk * kv_heads
     nbytes = rows * 2 * (dim // 2 + dim // 16) + rows * 2 * dim * 2
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f'{name}: {ms * 1e3:.2f} us per layer-step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of {HBM_PEAK_GBS:.0f})')
     record = {
         'metric': f'NVFP4-KV {mode} into BF16 rows HBM GB/s', 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1,
-        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per), 'higher_is_better': True,
+        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per, rot), 'higher_is_better': True,
         'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic',
         'config': {'workload': name, 'batch': batch, 'kv_heads': kv_heads, 'head_dim': dim, 'context': ctx,
                    'rows_per_request': topk, 'page': page, 'kv_format': 'nvfp4 (SGLang buffers)',
-                   'layers_rotated': layers},
+                   'layers_rotated': rot},
         'us_per_layer_step': round(ms * 1e3, 3), 'bytes_per_step': nbytes,
         'roofline': {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None},
         'cpu_baseline': None if args.no_cpu_baseline else gather_cpu(mode, pools[0], r2t, idx, w, args.cpu_seconds),
     }
-    print(json.dumps(record), flush=True)
+    emit(record)
 
 
 def gather_cpu(mode, raw, r2t, idx, w, seconds):
@@ -669,23 +691,23 @@ def run_varlen(args, w, ops, workloads):
         ops.varlen_decode(q, kv[layer][0], kv[layer][1], cu_q, cu_k, 1, w.keys, scale, out=out, splits=splits, ws=ws)
 
     steps = max(1, args.steps)
-    ms, per = time_steps(step, layers, steps, max(1, args.warmup))
+    ms, per, rot = time_steps(step, layers, steps, max(1, args.warmup))
     gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
     log(f'{w.name}: {ms * 1e3:.2f} us per layer-step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of {HBM_PEAK_GBS:.0f}), '
         f'splits {splits}')
     record = {
         'metric': 'BF16 varlen split-K decode HBM GB/s', 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1,
-        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per), 'higher_is_better': True,
+        'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per, rot), 'higher_is_better': True,
         'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic',
         'config': {'workload': w.name, 'rows': w.rows, 'q_heads': w.q_heads, 'kv_heads': w.kv_heads,
                    'head_dim': w.dim, 'keys_per_row': w.keys, 'kv_format': 'bf16 packed rows',
-                   'layers_rotated': layers, 'splits': splits},
+                   'layers_rotated': rot, 'splits': splits},
         'us_per_layer_step': round(ms * 1e3, 3),
         'roofline': {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None},
         'cpu_baseline': None if args.no_cpu_baseline else varlen_cpu(q, kv[0], w, scale, args.cpu_seconds),
     }
-    print(json.dumps(record), flush=True)
+    emit(record)
 
 
 def varlen_cpu(q, kv, w, scale, seconds):
@@ -748,14 +770,18 @@ def run_indexer(args, name, ops):
         rows, heads, dim = cfg['rows'], cfg['heads'], cfg['dim']
         keys = (cfg['prefix'] + rows) // cfg['ratio']
         q, k = bf16(rows, heads, dim), bf16(keys, 1, dim)
+        # one key buffer per launch of a graph replay (8 x 24 MB, with the 134 MB of logits written between two reads
+        # of one of them), so the keys come from HBM, not from the 256 MB MALL
+        kcopies = [k] + [k.clone() for _ in range(7)]
         starts = torch.zeros(rows, dtype=torch.int32, device='cuda')
         ends = ((torch.arange(cfg['prefix'], cfg['prefix'] + rows, device='cuda') + 1) // cfg['ratio']).int()
         out = torch.empty(rows, keys, device='cuda')
         lib = ops._lib.lib()
 
-        def step(_):
+        def step(layer):
+            kl = kcopies[layer % len(kcopies)]
             ops._lib.check(lib.xt_qsa_indexer_logits(q.data_ptr(), q.stride(0), q.stride(1), rows, heads, dim,
-                                                     k.data_ptr(), k.stride(0), keys, starts.data_ptr(),
+                                                     kl.data_ptr(), kl.stride(0), keys, starts.data_ptr(),
                                                      ends.data_ptr(), math.sqrt(dim), ops._lib.XT_DTYPE_BF16,
                                                      out.data_ptr(), out.stride(0),
                                                      torch.cuda.current_stream().cuda_stream), 'qsa')
@@ -790,10 +816,13 @@ def run_indexer(args, name, ops):
     elif kind == 'topk':
         rows, cols, kk = cfg['rows'], cfg['cols'], cfg['topk']
         x = torch.randn(rows, cols, device='cuda', generator=gen)
+        # three inputs of 134 MB in turn: two others (268 MB, more than the 256 MB MALL) are read between two reads of
+        # one, so each launch reads its input from HBM
+        xs = [x] + [torch.randn(rows, cols, device='cuda', generator=gen) for _ in range(2)]
         out = torch.empty(rows, kk, dtype=torch.int32, device='cuda')
 
-        def step(_):
-            ops.topk_rows(x, kk, out=out)
+        def step(layer):
+            ops.topk_rows(xs[layer % len(xs)], kk, out=out)
         nbytes = rows * cols * 4 + rows * kk * 4
         flops = 0
         conf = {'rows': rows, 'cols': cols, 'topk': kk, 'dtype': 'f32'}
@@ -872,10 +901,10 @@ def run_indexer(args, name, ops):
                 return sum(min(total, total - n + 64 * (t // 64 + 1)) for t in range(n)) / visited
             cpu_total, cpu_unit = total, 'prompt rows (the last ones, scaled by the keys they visit)'
         qh, payh, sch, r2th = q.float().cpu().numpy(), pay.cpu().numpy(), sc.cpu().numpy(), r2t.cpu().numpy()
-    # 8 launches per graph replay (a replay of one short launch would time the graph launch), the same inputs
-    # except for the decode scores' rotated pools
+    # 8 launches per graph replay (a replay of one short launch would time the graph launch); the HBM-bound ones rotate
+    # their inputs (QSA keys, top-k rows, decode-score pools) so that no launch reads its input from the MALL
     steps = max(1, args.steps)
-    ms, per = time_steps(step, 8, steps, max(1, args.warmup))
+    ms, per, rot = time_steps(step, 8, steps, max(1, args.warmup))
     t = ms * 1e-3
     gbs, tflops = nbytes / t / 1e9, flops / t / 1e12
     t_hbm, t_mfma = nbytes / (HBM_PEAK_GBS * 1e9), flops / (MFMA_PEAK_TFLOPS * 1e12)
@@ -901,7 +930,7 @@ def run_indexer(args, name, ops):
     frac = cpu_work(n) if kind == 'mm_prefill' else n / cpu_total
     cpu_ms = dt / frac * 1e3
     record = {'metric': f'{name} µs per launch', 'value': round(ms * 1e3, 3), 'unit': 'µs', 'n_gpus': 1,
-              'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per),
+              'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per, rot),
               'higher_is_better': False, 'scaling': 'weak', 'vs_baseline': None, 'dtype': conf.pop('dtype'),
               'data': 'synthetic', 'config': dict(workload=name, **conf),
               'algorithmic_bytes': nbytes, 'algorithmic_flops': flops,
@@ -910,7 +939,7 @@ def run_indexer(args, name, ops):
                                'kind': 'port',
                                'sample': f'{n} of {cpu_total} {cpu_unit}: the numpy oracle (oracle/topk.py) on one '
                                          f'thread of {cpu_model()}, scaled to the whole launch'}}
-    print(json.dumps(record), flush=True)
+    emit(record)
 
 
 CEILING_WORKLOADS = ('mfma_ceiling', 'gather_ceiling_b32', 'gather_pieces_ceiling_b32')
@@ -930,7 +959,7 @@ def run_ceiling(args, name, ops, workloads):
         def step(_):
             ops.ceiling_mfma(iters, blocks)
 
-        ms, per = time_steps(step, 1, steps, max(1, args.warmup))
+        ms, per, rot = time_steps(step, 1, steps, max(1, args.warmup))
         check = ops.ceiling_mfma(iters, blocks)
         assert bool((check == 64.0 * iters).all()), 'xt_ceiling_mfma returned wrong sums'
         flops = blocks * 4 * iters * 4 * 32 * 32 * 16 * 2
@@ -938,14 +967,14 @@ def run_ceiling(args, name, ops, workloads):
         log(f'mfma ceiling: {tflops:.0f} TFLOP/s ({tflops / MFMA_PEAK_TFLOPS:.1%} of {MFMA_PEAK_TFLOPS:.0f})')
         record = {'metric': 'sustained dense FP16 MFMA TFLOP/s', 'value': round(tflops, 1), 'unit': 'TFLOP/s',
                   'n_gpus': 1, 'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6),
-                  'timing': spread(per), 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
+                  'timing': spread(per, rot), 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
                   'dtype': 'f16', 'data': 'synthetic',
                   'config': {'workload': name, 'workgroups': blocks, 'mfma_per_wave': iters * 4,
                              'instruction': 'v_mfma_f32_32x32x16_f16'},
                   'roofline': {'bound': 'mfma', 'achieved': round(tflops, 1), 'peak': MFMA_PEAK_TFLOPS,
                                'unit': 'TFLOP/s', 'frac': round(tflops / MFMA_PEAK_TFLOPS, 4), 'traffic': None},
                   'cpu_baseline': None}
-        print(json.dumps(record), flush=True)
+        emit(record)
         return
     w = workloads.WORKLOADS['gqa_decode_b32']
     gen = workloads.generator('cuda', 20261029)
@@ -965,7 +994,7 @@ def run_ceiling(args, name, ops, workloads):
         else:
             ops.ceiling_gather(pools[layer], pt, idx, w.page, sink=sink)
 
-    ms, per = time_steps(step, args.layers, steps, max(1, args.warmup))
+    ms, per, rot = time_steps(step, args.layers, steps, max(1, args.warmup))
     nbytes = w.batch * w.topk * 576
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f'{name}: {ms * 1e3:.2f} us per layer-step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of '
@@ -973,16 +1002,16 @@ def run_ceiling(args, name, ops, workloads):
     what = ('decode gather pattern alone, per-head pieces as the decode reads them' if pieces else
             'decode gather pattern alone, whole records')
     record = {'metric': f'{what}, GB/s', 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1,
-              'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per),
+              'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per, rot),
               'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'u8', 'data': 'synthetic',
               'config': {'workload': name, 'batch': w.batch, 'context': w.ctx, 'topk': w.topk, 'page': w.page,
-                         'record_bytes': 576, 'layers_rotated': args.layers,
+                         'record_bytes': 576, 'layers_rotated': rot,
                          **({'splits': splits, 'kv_heads_per_workgroup': 1} if pieces else {})},
               'us_per_layer_step': round(ms * 1e3, 3),
               'roofline': {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                            'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None},
               'cpu_baseline': None}
-    print(json.dumps(record), flush=True)
+    emit(record)
 
 
 def main():
@@ -1065,7 +1094,7 @@ def main():
         ops.sparse_decode(q, layers[layer], pt, idx, seq, scale, page_size=w.page, out=out, splits=splits, ws=ws)
 
     steps = max(1, args.steps)
-    ms, per = time_steps(step, args.layers, steps, args.warmup)
+    ms, per, rot = time_steps(step, args.layers, steps, args.warmup)
     nbytes = w.algorithmic_bytes()
     gbs = nbytes / (ms * 1e-3) / 1e9
     props = torch.cuda.get_device_properties(0)
@@ -1082,28 +1111,32 @@ def main():
         del layers
         torch.cuda.empty_cache()
         layers = [build_layer(w, gen, alt, workloads, KVPool) for _ in range(args.layers)]
-        ms_alt, per_alt = time_steps(step, args.layers, steps, args.warmup)
-        other = {'pool_layout': alt, 'us_per_layer_step': round(ms_alt * 1e3, 3), 'timing': spread(per_alt),
+        ms_alt, per_alt, rot_alt = time_steps(step, args.layers, steps, args.warmup)
+        other = {'pool_layout': alt, 'us_per_layer_step': round(ms_alt * 1e3, 3), 'timing': spread(per_alt, rot_alt),
                  'achieved_gbs': round(nbytes / (ms_alt * 1e-3) / 1e9, 1),
                  'frac': round(nbytes / (ms_alt * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         log(f'{alt} pool: {ms_alt * 1e3:.2f} us per layer-step')
+    traffic = measured_traffic(w.name, splits, args.layout)
     record = {
         'metric': METRIC, 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1, 'steps': steps,
-        'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per), 'higher_is_better': True, 'scaling': 'weak',
+        'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per, rot), 'higher_is_better': True, 'scaling': 'weak',
         'vs_baseline': None, 'dtype': 'f16', 'data': 'synthetic',
         'config': {'workload': w.name, 'batch': w.batch, 'q_heads': w.q_heads, 'kv_heads': w.kv_heads,
                    'head_dim': w.dim, 'context': w.ctx, 'topk': w.topk, 'page': w.page, 'kv_format': 'nvfp4',
-                   'layers_rotated': args.layers, 'splits': splits, 'pool_layout': args.layout},
+                   'layers_rotated': rot, 'splits': splits, 'pool_layout': args.layout},
         'us_per_layer_step': round(ms * 1e3, 3),
         'tokens_per_s': round(w.batch / (ms * 1e-3), 1),
         'hbm_frac': round(gbs / HBM_PEAK_GBS, 4),
         'roofline': {'bound': 'hbm', 'achieved': round(gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-                     'frac': round(gbs / HBM_PEAK_GBS, 4),
-                     'traffic': measured_traffic(w.name, splits, args.layout)},
+                     'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': traffic,
+                     'traffic_source': None if traffic is None else
+                     f'profiles/decode_split_{w.name}_hbm_traffic.txt: rocprofv3 FETCH_SIZE and WRITE_SIZE of this '
+                     'workload, split count and pool layout (one counter per run, scaled by a copy of known size), '
+                     'committed with the kernel build; not measured in this run'},
         'cpu_baseline': cpu,
         'other_layout': other,
     }
-    print(json.dumps(record), flush=True)
+    emit(record)
 
 
 if __name__ == '__main__':

@@ -456,6 +456,11 @@ size_t xt_ceiling_gather_sink_words(int batch, int topk);
 int xt_ceiling_gather_pieces(const void* pool, int64_t pool_records, const int32_t* page_table, int64_t pt_stride,
                              int page_size, int pt_width, const int32_t* indices, int batch, int topk, int kv_heads,
                              int splits, uint32_t* sink, xt_stream_t stream);
+/* xt_clock_probe: the shader clock, read the way the benchmarks record it beside their rates (no counterpart in the
+ * reference): one wavefront runs `iters` dependent FMAs between two reads of the core clock counter (s_memtime) and
+ * of the constant 100 MHz clock (s_memrealtime); out[0] = core clock ticks, out[1] = 100 MHz ticks, out[2] = a check
+ * word (uint64_t[3], device memory). MHz = 100 * out[0] / out[1]. */
+int xt_clock_probe(uint64_t* out, int iters, xt_stream_t stream);
 
 #ifdef __cplusplus
 }

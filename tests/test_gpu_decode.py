@@ -257,7 +257,7 @@ def test_decode_full_gqa_workload(splits):
 
 def test_decode_long_context_workload():
     """Batch 4 at context 524288 (a 2M-slot pool, 1.2 GB of NVFP4 K/V, far beyond the MALL), top-2048 with half the
-    keys in the last 4096 positions, the default key splits: every row against the oracle."""
+    keys in the last 4096 positions, at the default key splits and at 8 and 16: every row against the oracle."""
     w = workloads.WORKLOADS['long_ctx_decode_b4']
     gen = workloads.generator('cuda', 20261106)
     k = workloads.kv_tensor(w.slots, w.kv_heads, w.dim, gen, 'cuda')
@@ -272,11 +272,12 @@ def test_decode_long_context_workload():
     idx = workloads.index_lists(w.batch, w.ctx, w.topk, gen, 'cuda', w.index_mode)
     seq = torch.full((w.batch,), w.ctx, dtype=torch.int32, device='cuda')
     scale = 1 / math.sqrt(w.dim)
-    assert ops.default_splits(w.batch, w.kv_heads, w.topk) == 8
-    out = ops.sparse_decode(q, raw, pt, idx, seq, scale, page_size=w.page)
+    assert ops.default_splits(w.batch, w.kv_heads, w.topk) == 4
     ref, flash, _ = _oracle(raw, bf16_numpy(q), pt.cpu().numpy(), w.page, np.arange(w.batch), idx.cpu().numpy(),
                             None, seq.cpu().numpy(), scale)
-    _check(out, ref, flash, strict=True)
+    for splits in (None, 8, 16):   # the default, and the split counts a caller may still ask for
+        out = ops.sparse_decode(q, raw, pt, idx, seq, scale, page_size=w.page, splits=splits)
+        _check(out, ref, flash, strict=True)
 
 
 @pytest.mark.parametrize('batch,splits', [(96, 1), (40, 3)])

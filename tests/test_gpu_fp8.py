@@ -133,3 +133,64 @@ def test_paged_attention_on_fp8_pool_through_the_hook():
         ref[b] = attention.softmax_attention(qf[b], kf[sl], vf[sl], ones, layer.scaling)
         flash[b] = attention.flash_precision_attention(qf[b], kf[sl], vf[sl], ones, layer.scaling)
     check(out.view(reqs, qh, DIM), ref, flash)
+
+
+class _Fa2Scratch:
+    """SGLang's _get_fa2_scratch: one BF16 K and V buffer per backend, reallocated only when a request outgrows it."""
+
+    def __init__(self):
+        self.k = self.v = None
+
+    def __call__(self, capacity, heads, dim, dtype, device):
+        if self.k is None or self.k.shape[0] < capacity:
+            self.k = torch.empty(capacity, heads, dim, dtype=dtype, device=device)
+            self.v = torch.empty_like(self.k)
+        return self.k[:capacity], self.v[:capacity]
+
+
+def test_paged_attention_on_fp8_pool_graph_replay_equals_eager():
+    """Under a CUDA graph the FP8 path takes the metadata's fa2 buffers and asks the scratch for the graph's capacity
+    (_cuda_graph_max_tokens * topk), as qsa_fp4.py:250-258 does: a capture of fewer rows than that capacity, replayed
+    with new queries and with eager calls of other sizes in between, matches the eager result bit for bit each time."""
+    k8, v8 = _pool(20261031, -2.0, 0.0)
+    k8, v8 = k8[:40000].contiguous().cuda(), v8[:40000].contiguous().cuda()
+    gen = torch.Generator().manual_seed(7)
+    reqs, ctx, topk, qh, max_tokens = 4, 6000, 512, 24, 8
+    r2t = torch.randperm(40000, generator=gen)[:reqs * ctx].view(reqs, ctx).to(torch.int32).cuda()
+    seq = torch.tensor([6000, 5000, 300, 4000], dtype=torch.int32).cuda()
+    idx = torch.full((reqs, topk), -1, dtype=torch.int32)
+    for b in range(reqs):
+        n = min(topk, int(seq[b])) - (b == 3) * 100
+        idx[b, :n] = torch.sort(torch.randperm(int(seq[b]), generator=gen)[:n]).values.to(torch.int32)
+    idx = idx.cuda()
+    graph_md = SimpleNamespace(row_req_pool_indices=None, sequence_lengths=seq, is_cuda_graph=True,
+                               fa2_valid_counts=torch.zeros(max_tokens, dtype=torch.int32, device='cuda'),
+                               fa2_cu_seqlens_k=torch.zeros(max_tokens + 1, dtype=torch.int32, device='cuda'),
+                               fa2_cu_seqlens_q=torch.arange(max_tokens + 1, dtype=torch.int32, device='cuda'))
+    eager_md = SimpleNamespace(row_req_pool_indices=None, sequence_lengths=seq, is_cuda_graph=False)
+    state = {'md': eager_md}
+    scratch = _Fa2Scratch()
+    backend = SimpleNamespace(token_to_kv_pool=_Fp8Pool(k8, v8), req_to_token_pool=SimpleNamespace(req_to_token=r2t),
+                              _resolve_metadata=lambda fb: state['md'], _expand_block_indices=lambda ti, md: ti,
+                              _get_fa2_scratch=scratch, _cuda_graph_max_tokens=max_tokens)
+    layer = SimpleNamespace(layer_id=0, scaling=1 / math.sqrt(DIM))
+    fb = SimpleNamespace(req_pool_indices=torch.arange(reqs).cuda())
+    qs = torch.randn(reqs, qh * DIM, generator=gen).to(torch.bfloat16).cuda()
+    qsa.paged_attention(None, backend, qs, layer, fb, idx)      # eager first: workspaces exist before the capture
+    state['md'] = graph_md
+    qsa.paged_attention(None, backend, qs, layer, fb, idx)      # the graph capacity's scratch, before the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = qsa.paged_attention(None, backend, qs, layer, fb, idx)
+    assert scratch.k.shape[0] == max_tokens * topk
+    for i in range(3):
+        qs.copy_((torch.randn(qs.shape, generator=gen) * (1 + i)).to(torch.bfloat16).cuda())
+        graph.replay()
+        torch.cuda.synchronize()
+        state['md'] = eager_md
+        qsa.paged_attention(None, backend, qs[:2], layer, fb, idx[:2])   # an eager call of another size in between
+        eager = qsa.paged_attention(None, backend, qs, layer, fb, idx)
+        torch.cuda.synchronize()
+        state['md'] = graph_md
+        assert torch.equal(captured.view(torch.int16), eager.view(torch.int16)), i

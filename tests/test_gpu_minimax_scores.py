@@ -162,6 +162,30 @@ def test_prefill_scores(prefix, ext, dim, bs, heads, q_dtype):
             assert (err <= (bound + 2.0 ** -23 * np.abs(want[:, row, :nb]))[f]).all(), (r, t)
 
 
+@pytest.mark.parametrize('bs', [96, 160, 192, 224])
+def test_block_sizes_not_powers_of_two_are_refused(bs):
+    """Block sizes must be 32, 64, 128 or 256 (the reference's tl.arange(0, block_size) takes powers of two): the
+    prefill stages keys 128 at a time and masks them by causality and length only, so any other multiple of 32 would
+    let the next block's keys into a block's maximum. Both score entry points refuse them before launching."""
+    g = torch.Generator().manual_seed(bs)
+    seq_lens = [600]
+    r2t, pages = _mapping(seq_lens, g)
+    pay, sc = _pool(pages, 128, g)
+    q = (torch.randn(300, 2, 128, generator=g) * 0.3).to(torch.bfloat16).cuda()
+    nb = -(-600 // bs)
+    score = torch.full((2, 300, nb), 7.0, device='cuda')
+    i32 = lambda v: torch.tensor(v, dtype=torch.int32).cuda()
+    with pytest.raises(NotImplementedError, match='block size'):
+        ops.minimax_prefill_scores(q, pay.cuda(), sc.cuda(), r2t.cuda(), score, i32([0, 300]), i32(seq_lens),
+                                   i32([300]), i32([0]), bs, 128 ** -0.5, 1.0, 300)
+    assert bool((score == 7.0).all())   # nothing written
+    dscore = torch.full((2, 1, nb), 7.0, device='cuda')
+    with pytest.raises(NotImplementedError, match='block size'):
+        ops.minimax_decode_scores(q[:1], pay.cuda(), sc.cuda(), r2t.cuda(), dscore, i32(seq_lens), i32([0]), bs,
+                                  128 ** -0.5, 1.0, 0, 0)
+    assert bool((dscore == 7.0).all())
+
+
 class _SglangDecodeStandIn:
     """What SGLang's flash_decode_with_topk_idx does around its score kernel, reduced to the launch (its argument list
     as the reference's shim receives it, kv_fp4.py:233-236) and a top-k over the score buffer."""

@@ -330,8 +330,10 @@ int score_common(const char* what, ScoreArgs& a, int dim, int q_dtype, const voi
   if (q_dtype != XT_DTYPE_BF16 && q_dtype != XT_DTYPE_F16) return fail(XT_EUNSUPPORTED, "%s: queries must be BF16 or FP16", what);
   if (score_dtype < 0 || score_dtype > 2) return fail(XT_EINVAL, "%s: score dtype %d (0 FP32, 1 BF16, 2 FP16)", what,
                                                       score_dtype);
-  if (a.block_size < 32 || a.block_size > 256 || a.block_size % 32)
-    return fail(XT_EUNSUPPORTED, "%s: block size %d (32, 64, ..., 256)", what, a.block_size);
+  // powers of two only, as the reference's tl.arange(0, block_size) requires: the prefill stages 128 keys at a time
+  // and masks keys by causality and length, not by the block's end
+  if (a.block_size != 32 && a.block_size != 64 && a.block_size != 128 && a.block_size != 256)
+    return fail(XT_EUNSUPPORTED, "%s: block size %d (32, 64, 128 or 256)", what, a.block_size);
   if (a.max_slots < kPoolRows || a.max_slots % kPoolRows)
     return fail(XT_EINVAL, "%s: the index pool holds %lld slots (whole pages of 128)", what, (long long)a.max_slots);
   if (!aligned(pay, 16) || pay_ps % 16 || pay_rs % 16 || pay_rs < dim / 2 || !aligned(sc, 8) || sc_rs < dim / 16 ||

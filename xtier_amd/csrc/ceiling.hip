@@ -155,10 +155,31 @@ __global__ __launch_bounds__(512) void gather_pieces_kernel(const uint8_t* pool,
   sink[(int64_t)g * 512 + threadIdx.x] = acc;
 }
 
+// One wavefront: `iters` dependent FMAs between two reads of the core clock counter and the 100 MHz constant clock.
+__global__ __launch_bounds__(64) void clock_probe_kernel(uint64_t* out, int iters) {
+  const uint64_t c0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  float x = (float)threadIdx.x;
+  for (int i = 0; i < iters; ++i) x = __builtin_fmaf(x, 0.999999f, 1.0f);
+  asm volatile("" : "+v"(x));
+  const uint64_t c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0) {
+    out[0] = c1 - c0;
+    out[1] = r1 - r0;
+    out[2] = __float_as_uint(x);
+  }
+}
+
 }  // namespace
 }  // namespace xt
 
 using namespace xt;
+
+extern "C" int xt_clock_probe(uint64_t* out, int iters, xt_stream_t stream) {
+  const char* what = "xt_clock_probe";
+  if (!out || iters <= 0 || iters > (1 << 24)) return fail(XT_EINVAL, "%s: out must be given, iters in 1..2^24", what);
+  hipLaunchKernelGGL(clock_probe_kernel, dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), out, iters);
+  return check_launch(what);
+}
 
 extern "C" int xt_ceiling_mfma(float* out, int iters, int blocks, xt_stream_t stream) {
   const char* what = "xt_ceiling_mfma";

@@ -305,13 +305,16 @@ def device_cus(device=None):
 
 
 def default_splits(rows, kv_heads, topk):
-    """Key splits per row: about one workgroup of one KV head per CU, at least 256 keys per split, and at most 8192
-    keys per split (the slot list lives in LDS). Measured on MI355X (256 CUs): batch 32 x 4 KV heads, top-2048 -> 2;
-    batch 4 x 4 KV heads, top-2048 -> 8; 4096 prefill rows -> 1."""
+    """Key splits per row: about one workgroup of one KV head per CU, at least 512 keys per split (two steps of two
+    loads in flight for each of a workgroup's 8 wavefronts), and at most 8192 keys per split (the slot list lives in
+    LDS). Small launches are latency-bound and every split adds to the merge, so the floor of 512 keys wins over
+    filling the CUs. Measured on MI355X (256 CUs), per layer-step: batch 32 x 4 KV heads, top-2048: 2 splits 19.1 us;
+    batch 4 x 4 KV heads, top-2048: 1 / 2 / 4 / 8 / 16 splits 16.3 / 14.0 / 12.1 / 12.6 / 15.0 us; 1 row x 1 KV
+    head, top-512: 1 / 2 splits 8.4 / 10.4 us; 4096 prefill rows -> 1."""
     if topk <= 0:
         return 1
     units = max(1, rows * kv_heads)
-    splits = max(1, min(math.ceil(device_cus() / units), topk // 256, 64))
+    splits = max(1, min(math.ceil(device_cus() / units), topk // 512, 64))
     return max(splits, min(64, math.ceil(topk / 8192)))
 
 
@@ -739,6 +742,14 @@ def sparse_mla(q, k_cache, indices, topk_length, attn_sink, softmax_scale, extra
             int(splits), _ptr(ws), ws.numel(), _stream(q))
     _lib.check(status, 'sparse_mla')
     return (out.unsqueeze(1), lse.unsqueeze(-1)) if shape4 else (out, lse)
+
+
+def clock_mhz(device='cuda', iters=200000):
+    """The shader clock in MHz while one wavefront runs (xt_clock_probe: core clock ticks over 100 MHz ticks)."""
+    out = torch.zeros(3, dtype=torch.int64, device=device)
+    _lib.check(_lib.lib().xt_clock_probe(_ptr(out), int(iters), _stream(out)), 'clock_probe')
+    core, real, _ = out.tolist()
+    return 100.0 * core / real if real > 0 else None
 
 
 def ceiling_mfma(iters, blocks, device='cuda'):
