@@ -41,7 +41,8 @@ def test_attach_scales_and_install():
     seen = []
     registry = SimpleNamespace(register=lambda name, fn, kind: seen.append((name, fn, kind)))
     minimax.install(registry, SimpleNamespace(AROUND='around'))
-    assert seen == [(f'{minimax.OPS}.flash_decode_with_topk_idx', minimax.decode_topk, 'around'),
+    assert seen == [(minimax.KV_POOL, minimax.kv_pool, 'around'),
+                    (f'{minimax.OPS}.flash_decode_with_topk_idx', minimax.decode_topk, 'around'),
                     (f'{minimax.OPS}.flash_decode_with_gqa_share_sparse', minimax.decode_main, 'around'),
                     (f'{minimax.OPS}.flash_prefill_with_topk_index', minimax.prefill_topk, 'around'),
                     (f'{minimax.OPS}.flash_prefill_with_gqa_share_sparse', minimax.prefill_main, 'around'),
@@ -147,3 +148,50 @@ def test_prefill_topk_hook_routes_the_score_launch(monkeypatch):
     a, k = seen['args'], seen['kw']
     assert a[:5] == (q, pay, sc, r2t, score) and a[5:12] == (cu, seq, pre, sid, 64, 0.2, 1.0)
     assert k == dict(max_q_len=128, heads=4, q_strides=(512, 128, 1), r2t_stride=77, score_strides=(300, 75, 1))
+
+
+def _msa_pool(nvfp4=True, same_scale=True):
+    pays = [torch.zeros(1), torch.zeros(1)]
+    scs = [torch.ones(1), torch.ones(1)]
+    main = SimpleNamespace(k_buffer=pays, k_scale_buffer=scs, v_buffer=pays[::-1], v_scale_buffer=scs[::-1],
+                           head_dim=128, page_size=128, global_scale=torch.ones(1), is_minimax_m3_nvfp4_main=nvfp4)
+    index = SimpleNamespace(k_buffer=[torch.zeros(1)], k_scale_buffer=[torch.ones(1)], INDEX_HEAD_DIM=128,
+                            page_size=128, global_scale=torch.ones(1) * (1.0 if same_scale else 2.0))
+    return SimpleNamespace(main_pool=main, index_k_pool=index, use_nvfp4_fused_quantize_store=False, size=256)
+
+
+def test_kv_pool_hook_tags_nvfp4_pools_and_turns_on_the_fused_store(monkeypatch):
+    """AROUND _build_minimax_sparse_kv_pool (minimax_m3/__init__.py:93-100): an NVFP4 MSA-v1 pool comes back with its
+    payload views tagged and the one-launch store on; the builder's arguments pass through unchanged."""
+    monkeypatch.delenv('XTIER_MINIMAX_FP4_FUSED_STORE', raising=False)
+    pool = _msa_pool()
+    calls = []
+
+    def build(*args, **kwargs):
+        calls.append((args, kwargs))
+        return pool
+    assert minimax.kv_pool(build, 'cfg', dtype='nvfp4') is pool
+    assert calls == [(('cfg',), {'dtype': 'nvfp4'})]
+    assert minimax.scales_of(pool.main_pool.k_buffer[0]) is pool.main_pool.k_scale_buffer[0]
+    assert minimax.scales_of(pool.index_k_pool.k_buffer[0]) is pool.index_k_pool.k_scale_buffer[0]
+    assert pool.use_nvfp4_fused_quantize_store
+    # the pools' global scales differ: tagged, but the stores stay SGLang's
+    other = _msa_pool(same_scale=False)
+    minimax.kv_pool(lambda: other)
+    assert minimax.scales_of(other.main_pool.k_buffer[0]) is not None and not other.use_nvfp4_fused_quantize_store
+
+
+def test_kv_pool_hook_leaves_other_pools_alone():
+    for pool in (_msa_pool(nvfp4=False), SimpleNamespace(size=3)):
+        assert minimax.kv_pool(lambda p=pool: p) is pool
+    plain = _msa_pool(nvfp4=False)
+    minimax.kv_pool(lambda: plain)
+    assert minimax.scales_of(plain.main_pool.k_buffer[0]) is None and not plain.use_nvfp4_fused_quantize_store
+
+
+def test_install_off_switch(monkeypatch):
+    """XTIER_MINIMAX_KV_FP4=0 (minimax_m3/__init__.py:176-181) registers neither the pool hook nor the op hooks."""
+    monkeypatch.setenv('XTIER_MINIMAX_KV_FP4', '0')
+    seen = []
+    minimax.install(SimpleNamespace(register=lambda *a: seen.append(a)), SimpleNamespace(AROUND='around'))
+    assert seen == []

@@ -129,3 +129,45 @@ def test_raw_buffers_fp8_pool_returns_the_bytes_without_scales():
             return self.v
     raw = qsa.raw_buffers(Fp8Pool(), SimpleNamespace(layer_id=0))
     assert raw[0].dtype == torch.uint8 and raw[1][0, 0, 0].item() == 0x38 and raw[2:] == (None,) * 4
+
+
+class _Registry:
+    def __init__(self):
+        self.seen = []
+
+    def register(self, target, fn, kind):
+        self.seen.append((target, fn, kind))
+
+
+_KINDS = SimpleNamespace(AROUND='around', AFTER='after')
+
+
+def test_install_registers_the_reference_targets():
+    """Default switches: the indexer logits, the six NVFP4 hooks and the varlen resolver, on the targets and with the
+    kinds of qwen4_exp/__init__.py:58-71."""
+    reg = _Registry()
+    qsa.install(reg, _KINDS)
+    assert reg.seen == [
+        (qsa.QSA_PREFILL, qsa.qsa_mqa_prefill, 'around'),
+        (f'{qsa.QSA_BACKEND}.forward_extend', qsa.forward_extend, 'around'),
+        (f'{qsa.QSA_BACKEND}._forward_paged_attention', qsa.paged_attention, 'around'),
+        (f'{qsa.SPARSE_ATTN}.pack_qsa_prefill_kv', qsa.pack_qsa_prefill_kv, 'around'),
+        (f'{qsa.SPARSE_ATTN}.qwen_sparse_kv_extraction_compact_triton', qsa.extraction, 'around'),
+        (f'{qsa.KV_FP4}.NVFP4KVCacheMethod.create_buffers', qsa.create_buffers, 'after'),
+        (f'{qsa.KV_FP4_UTIL}.NVFP4KVQuantizeUtil.quantize', qsa.quantize, 'around'),
+        (f'{qsa.QSA_MODULE}._resolve_flash_attn_varlen_func', qsa.resolve, 'around')]
+    assert qsa.QSA_BACKEND == 'sglang.srt.layers.attention.qwen_sparse_attn_backend.QwenSparseAttnBackend'
+
+
+@pytest.mark.parametrize('env,present', [({'XTIER_QSA_FP4': '0'}, {qsa.qsa_mqa_prefill, qsa.resolve}),
+                                         ({'XTIER_QSA_KEYS_PER_CTA': '0'},
+                                          {qsa.forward_extend, qsa.paged_attention, qsa.pack_qsa_prefill_kv,
+                                           qsa.extraction, qsa.create_buffers, qsa.quantize, qsa.resolve}),
+                                         ({'XTIER_QSA_FP4': '0', 'XTIER_QSA_KEYS_PER_CTA': '0'}, {qsa.resolve})])
+def test_install_switches(monkeypatch, env, present):
+    """XTIER_QSA_FP4=0 leaves out the NVFP4 hooks, XTIER_QSA_KEYS_PER_CTA=0 the indexer logits; the resolver stays."""
+    for name, value in env.items():
+        monkeypatch.setenv(name, value)
+    reg = _Registry()
+    qsa.install(reg, _KINDS)
+    assert {fn for _, fn, _ in reg.seen} == present

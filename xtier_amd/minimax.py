@@ -12,6 +12,10 @@ What an NVFP4 call must satisfy: the pool is written with outer scales of 1, so 
 The KV store: ``enable_fused_store`` (kv_fp4.py:546-559) turns on the pool's fused store, and the hook on SGLang's
 ``nvfp4_store_kv_index`` runs it as one launch of this library's store (main K, V and index K).
 
+The pool: ``kv_pool``, AROUND SGLang's builder of the MiniMax sparse KV pool (minimax_m3/__init__.py:93-100), calls
+both on an NVFP4 main pool as it is built. ``install`` registers it and the op hooks unless XTIER_MINIMAX_KV_FP4=0
+(minimax_m3/__init__.py:176-181), the reference's switch for the NVFP4 KV cache.
+
 The prefill entry: while BF16 copies of every request's context (main K, V and index K) fit in
 ``XTIER_MINIMAX_FP4_PREFILL_GB`` GiB (default 1.5), ``dequantize_context`` makes them and ``original`` runs SGLang's
 BF16 kernels on the copies through a request-local token table; beyond that ``original`` gets the NVFP4 views and
@@ -28,6 +32,7 @@ from . import ops
 
 logger = logging.getLogger(__name__)
 OPS = 'sglang.srt.layers.attention.minimax_sparse_ops.minimax_sparse'
+KV_POOL = 'sglang.srt.mem_cache.kv_cache_configurator.KVCacheConfigurator._build_minimax_sparse_kv_pool'
 PAGE = 128                    # tokens per page of the MSA-v1 pool
 TAG = '_xt_nvfp4_scales'      # attribute of a payload view that holds its scale-byte view
 PREFILL_GB = float(os.environ.get('XTIER_MINIMAX_FP4_PREFILL_GB', '1.5'))
@@ -251,8 +256,28 @@ HOOKS = ((f'{OPS}.flash_decode_with_topk_idx', decode_topk),
          (STORE, store_kv_index))
 
 
+def kv_pool(original, *args, **kwargs):
+    """AROUND KVCacheConfigurator._build_minimax_sparse_kv_pool (minimax_m3/__init__.py:93-100): the pool as SGLang
+    builds it; when its main pool is the NVFP4 MSA-v1 pool, its payload views are tagged with their scale views
+    (attach_scales) and its stores go through the one-launch store (enable_fused_store). Any other pool is returned
+    untouched."""
+    pool = original(*args, **kwargs)
+    if getattr(getattr(pool, 'main_pool', None), 'is_minimax_m3_nvfp4_main', False):
+        attach_scales(pool)
+        enable_fused_store(pool)
+    return pool
+
+
+def kv_fp4_enabled():
+    """The reference's switch for the NVFP4 KV cache (minimax_m3/__init__.py:67-68): on unless XTIER_MINIMAX_KV_FP4=0."""
+    return os.environ.get('XTIER_MINIMAX_KV_FP4', '1') != '0'
+
+
 def install(registry, hook_type):
-    """Registers every hook of HOOKS AROUND its target: SGLang's generic MiniMax sparse ops (kv_fp4.py:632-638) and
-    its fused NVFP4 store."""
+    """Unless XTIER_MINIMAX_KV_FP4=0 (minimax_m3/__init__.py:176-181): the pool hook, then every hook of HOOKS AROUND
+    its target (SGLang's generic MiniMax sparse ops, kv_fp4.py:632-638, and its fused NVFP4 store)."""
+    if not kv_fp4_enabled():
+        return
+    registry.register(KV_POOL, kv_pool, hook_type.AROUND)
     for target, hook in HOOKS:
         registry.register(target, hook, hook_type.AROUND)
