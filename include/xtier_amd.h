@@ -153,7 +153,8 @@ size_t xt_sparse_decode_workspace_bytes(int rows, int q_heads, int dim, int spli
  *   not NULL (causal prefill);
  * resolved to pool slots through table row row_req[r] (row_req NULL: row r) with the page_size rule above.
  * K/V are dequantized in registers; out[r, h] = sum_k softmax_k(q.k * scale) v_k in the dtype out_dtype, a row
- * without valid keys writing 0. lse (optional, FP32 [rows, q_heads]): natural log-sum-exp of the scaled scores,
+ * without valid keys writing 0. Any finite BF16 query is taken exactly: each head's query enters the FP16 MFMA as
+ * q * 2^-e, with 2^e from the head's largest magnitude, and scale * log2(e) * 2^e multiplies the FP32 scores. lse (optional, FP32 [rows, q_heads]): natural log-sum-exp of the scaled scores,
  * -inf for an empty row. q_heads must be a multiple of kv_heads with q_heads / kv_heads <= 16; dim 64, 128 or 256. Pool
  * pointers and strides as above: payload 16-byte and scales 4-byte aligned.
  * splits: key splits per row (1..64); workspace: xt_sparse_decode_workspace_bytes(rows, q_heads, dim, splits) bytes,
@@ -305,7 +306,9 @@ size_t xt_sparse_mla_workspace_bytes(int rows, int heads, int splits);
  *   out[r, h] = sum_k exp(s_k - m) v_k / (sum_k exp(s_k - m) + exp(sink[h] - m)),  s_k = scale * q[r, h] . key_k,
  * written in out_dtype to out (BF16/FP16 [rows, heads, latent_dim], strides in elements); sink NULL: no sink term.
  * lse (optional FP32 [rows, heads]): natural log of sum_k exp(s_k) over the keys only (sparse_mla.py:73-85); a row
- * without valid keys writes zeros and lse -inf. latent_dim 512, rope_dim 64, heads <= 128 are supported.
+ * without valid keys writes zeros and lse -inf. latent_dim 512, rope_dim 64, heads <= 128 are supported. The FP16
+ * operands are exact: e2m1 * e4m3 latents and each head's query as q * 2^-e (2^e from its largest magnitude, so any
+ * finite BF16 query fits); g multiplies the latent part of the FP32 scores and the probabilities of the values.
  * splits: key splits per row (1..64); with splits > 1 a second launch on `stream` merges the split partials.
  * workspace: xt_sparse_mla_workspace_bytes bytes, 256-byte aligned; its first 64 KB are left untouched (the counter
  * region of the decode entry points), so one zero-filled workspace may serve decode and MLA calls of any shape, one at

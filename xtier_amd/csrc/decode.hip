@@ -225,7 +225,7 @@ struct SoftmaxState {
 
 template <int D, bool PS>
 __device__ inline void compute_step(const WaveCtx& w, int step, const Step<D>& d, const half8_t (&qb)[Geo<D>::kNK],
-                                    float gk, uint8_t* vtile, SoftmaxState<D>& st) {
+                                    float smul, uint8_t* vtile, SoftmaxState<D>& st) {
   using G = Geo<D>;
   const int lane = w.lane, hl = w.hl, j = w.j;
   // validity of the step's 32 keys (bit t: key t), uniform over the wave
@@ -288,15 +288,15 @@ __device__ inline void compute_step(const WaveCtx& w, int step, const Step<D>& d
                                                      0);
     }
   }
-  // online softmax of head hl over keys T(j), lazy rescale. The K global scale gk is positive (the kernel moves a
-  // negative one's sign into the query and raises magnitudes below FLT_MIN to it), so a masked score (-inf) gives
-  // P = 0. Only a step with invalid keys (a slice's tail, causal limits) masks scores, a branch uniform over the wave.
+  // online softmax of head hl over keys T(j), lazy rescale. The scores' multiplier smul (this lane's head's: K global
+  // scale, softmax scale, log2(e) and the query's power of two) is positive, so a masked score (-inf) gives P = 0.
+  // Only a step with invalid keys (a slice's tail, causal limits) masks scores, a branch uniform over the wave.
   // The maximum reads the products (ordinary VALU results), never the MFMA accumulators themselves: inline asm gets
   // no MFMA read-after-write wait states from the compiler.
   const bool full = valid == 0xFFFFFFFFu;
   float sv[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) sv[e] = s[e >> 2][e & 3] * gk;
+  for (int e = 0; e < 8; ++e) sv[e] = s[e >> 2][e & 3] * smul;
   if (!full) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) sv[e] = ((valid >> key_of(j, e)) & 1u) ? sv[e] : -__builtin_inff();
@@ -497,23 +497,6 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
   }
   __syncthreads();
 
-  // B operand of the QK MFMAs: FP16 of q * scale * log2(e); heads beyond the group are zero. A negative K global scale
-  // moves its sign into the query, and a magnitude below FLT_MIN (zero included) is raised to it, so the softmax works
-  // with gk > 0 (a NaN stays NaN); at that size the scaled scores round to 0 either way.
-  const float gk_abs = __builtin_fabsf(gk_v);
-  const float gk = gk_abs < 1.17549435e-38f ? 1.17549435e-38f : gk_abs;
-  const float qs = gk_v < 0.0f ? -a.qscale : a.qscale;
-  half8_t qb[G::kNK];
-#pragma unroll
-  for (int kk = 0; kk < G::kNK; ++kk) {
-    const uint32_t ws[4] = {q_valid ? qraw[kk].x : 0u, q_valid ? qraw[kk].y : 0u, q_valid ? qraw[kk].z : 0u,
-                            q_valid ? qraw[kk].w : 0u};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      qb[kk][2 * e] = (_Float16)(bf16_bits_to_f32(ws[e] & 0xFFFFu) * qs);
-      qb[kk][2 * e + 1] = (_Float16)(bf16_bits_to_f32(ws[e] >> 16) * qs);
-    }
-  }
   SoftmaxState<D> st;
   st.m = -__builtin_inff();
   st.l = 0.0f;
@@ -537,16 +520,47 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
     Step<D> buf[P];
 #pragma unroll
     for (int p = 0; p < P; ++p) load_step<D, PS, O32>(w, p, buf[p]);
+    // the query's operands, prepared while the first steps' loads are in flight. B operand of the QK MFMAs: FP16 of
+    // q * 2^-e, exact, with 2^e per head from its largest magnitude
+    // (pow2_query_scale); heads beyond the group are zero. The FP32 scores are multiplied by smul = |gk| * scale *
+    // log2(e) * 2^e, this lane's head's. A negative K global scale moves its sign into the query, and a magnitude below
+    // FLT_MIN (zero included) is raised to it, so the softmax works with smul > 0 for a positive softmax scale (a NaN
+    // stays NaN); at that size the scaled scores round to 0 either way.
+    const float gk_abs = __builtin_fabsf(gk_v);
+    const float gk = gk_abs < 1.17549435e-38f ? 1.17549435e-38f : gk_abs;
+    float qmax = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < G::kNK; ++kk) {
+      const uint32_t ws[4] = {qraw[kk].x, qraw[kk].y, qraw[kk].z, qraw[kk].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        qmax = fmaxf(qmax, fmaxf(__builtin_fabsf(bf16_bits_to_f32(ws[e] & 0xFFFFu)),
+                                 __builtin_fabsf(bf16_bits_to_f32(ws[e] >> 16))));
+    }
+    const float2_t p2 = pow2_query_scale(max4_lanes16(qmax));   // the head's maximum over its four lanes
+    const float qs = gk_v < 0.0f ? -p2[0] : p2[0];
+    const float smul = gk * a.qscale * p2[1];
+    half8_t qb[G::kNK];
+#pragma unroll
+    for (int kk = 0; kk < G::kNK; ++kk) {
+      const uint32_t ws[4] = {q_valid ? qraw[kk].x : 0u, q_valid ? qraw[kk].y : 0u, q_valid ? qraw[kk].z : 0u,
+                              q_valid ? qraw[kk].w : 0u};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qb[kk][2 * e] = (_Float16)(bf16_bits_to_f32(ws[e] & 0xFFFFu) * qs);
+        qb[kk][2 * e + 1] = (_Float16)(bf16_bits_to_f32(ws[e] >> 16) * qs);
+      }
+    }
     int s0 = 0;
     for (; s0 + P < slice_steps; s0 += P) {
 #pragma unroll
       for (int p = 0; p < P; ++p) {
-        compute_step<D, PS>(w, s0 + p, buf[p], qb, gk, vtile, st);
+        compute_step<D, PS>(w, s0 + p, buf[p], qb, smul, vtile, st);
         load_step<D, PS, O32>(w, s0 + p + P, buf[p]);
       }
     }
 #pragma unroll
-    for (int p = 0; p < P; ++p) compute_step<D, PS>(w, s0 + p, buf[p], qb, gk, vtile, st);
+    for (int p = 0; p < P; ++p) compute_step<D, PS>(w, s0 + p, buf[p], qb, smul, vtile, st);
   }
   // the 4 lanes of a head hold disjoint key subsets of l
   float l_tot = sum4_lanes16(st.l);

@@ -1,6 +1,7 @@
 // Sparse MLA: 128 query heads share one key per token. Two cache formats:
 //   NVFP4 latent (kNvfp4): key = [latent (512, NVFP4 with E4M3 block scales and a global scale) | rope (64, BF16)],
-//     576 wide, value = the latent; operands FP16, q pre-scaled by scale * log2(e);
+//     576 wide, value = the latent; operands FP16: the query as q * 2^-e per head (exact), the key tile as e2m1 * e4m3
+//     (exact), the global scale applied to the FP32 latent scores and folded into P;
 //   DeepSeek V4 FP8 pages (kFp8V4, sparse_mla.py:38-59): key = [448 E4M3 values x UE8M0 scale per 64 | 64 BF16 rope],
 //     512 wide, value = the key; operands BF16 as in the reference, the scale applied to the FP32 scores.
 // q.k and p.v on MFMA (v_mfma_f32_16x16x32_f16 / _bf16), online softmax in the exp2 domain, an optional per-head sink
@@ -22,8 +23,9 @@
 //   PV: A = V^T, lane (dim hl of a 16-dim tile, keys T(j) = {4j..4j+3, 16+4j..16+4j+3}); B = P^T, lane (head hl, keys
 //       T(j)); C = O^T, lane (head hl, dims 4j .. 4j+3 of the tile).
 //
-// Numerics: NVFP4: FP16((e2m1 * e4m3) * g) rounds the dequantized latent once (11 significant bits); the rope is exact
-// in FP16 within its range; P is FP16. V4: e4m3 * 2^(e - 127) is exact in BF16 (4 significant bits) for scales from
+// Numerics: NVFP4: e2m1 * e4m3 is exact in FP16 (at most 6 significant bits), and so is the query scaled by a power of
+// two; the latent and rope parts of a score accumulate apart, and score = (latent . q * g + rope . q) * scale *
+// log2(e) * 2^e in FP32 (g of the key's cache); P is FP16 of p * g for the values, the sum takes p. V4: e4m3 * 2^(e - 127) is exact in BF16 (4 significant bits) for scales from
 // 2^-126; a zero scale byte (2^-127) reads as 0; P is BF16. The running maximum is raised lazily (P <= 256); sums are
 // FP32.
 #include "xt_common.h"
@@ -199,8 +201,7 @@ __device__ inline void load_raw(const MlaArgs& a, const int32_t* slots, int step
 // P * V stays finite whatever slot 0 holds); an NVFP4 key's rope is left as read: its score is masked by a select,
 // never multiplied.
 template <int F, bool TWO>
-__device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step, const Raw<F>& r, float g0, float g1,
-                               uint16_t* kt) {
+__device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step, const Raw<F>& r, uint16_t* kt) {
   const int t = threadIdx.x, kq = t >> 6, c = t & 63;
   int32_t ent[4];
   step_entries(slots, step, kq, ent);
@@ -228,10 +229,7 @@ __device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step,
   } else {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int32_t e = ent[i];
-    const float g = (TWO && e <= -2) ? g1 : g0;
-    const float sg = entry_valid(e) ? (float)fp8x2_to_f16<false>(r.sc[i]).x * g : 0.0f;
-    const _Float16 h = (_Float16)sg;
+    const _Float16 h = entry_valid(ent[i]) ? fp8x2_to_f16<false>(r.sc[i]).x : (_Float16)0.0f;
     const half2_t s2 = half2_t{h, h};
     const half2_t p0 = fp4x2_to_f16<0>(r.pay[i]) * s2, p1 = fp4x2_to_f16<1>(r.pay[i]) * s2;
     const half2_t p2 = fp4x2_to_f16<2>(r.pay[i]) * s2, p3 = fp4x2_to_f16<3>(r.pay[i]) * s2;
@@ -331,8 +329,25 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
   }
   __syncthreads();
 
-  // B operands of q.k, chunks 0..kQR-1 in registers, the rest in LDS: NVFP4, FP16 of q * scale * log2(e); V4, q
+  // B operands of q.k, chunks 0..kQR-1 in registers, the rest in LDS: NVFP4, FP16 of q * 2^-e, exact, with 2^e per
+  // head from its largest magnitude (pow2_query_scale), and scale * log2(e) * 2^e applied to the FP32 scores; V4, q
   // as given (BF16), the scale applied to the FP32 scores
+  float smul = a.qscale;
+  float qdown = 1.0f;
+  if constexpr (F == kNvfp4) {
+    float qmax = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < kQC; ++kk) {
+      const uint32_t ws[4] = {qraw[kk].x, qraw[kk].y, qraw[kk].z, qraw[kk].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        qmax = fmaxf(qmax, fmaxf(__builtin_fabsf(bf16_bits_to_f32(ws[e] & 0xFFFFu)),
+                                 __builtin_fabsf(bf16_bits_to_f32(ws[e] >> 16))));
+    }
+    const float2_t p2 = pow2_query_scale(max4_lanes16(qmax));   // the head's maximum over its four lanes
+    qdown = p2[0];
+    smul = a.qscale * p2[1];
+  }
   short8_t qb[kQR];
 #pragma unroll
   for (int kk = 0; kk < kQC; ++kk) {
@@ -342,8 +357,8 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
       half8_t hh;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        hh[2 * e] = head_live ? (_Float16)(bf16_bits_to_f32(ws[e] & 0xFFFFu) * a.qscale) : (_Float16)0.0f;
-        hh[2 * e + 1] = head_live ? (_Float16)(bf16_bits_to_f32(ws[e] >> 16) * a.qscale) : (_Float16)0.0f;
+        hh[2 * e] = head_live ? (_Float16)(bf16_bits_to_f32(ws[e] & 0xFFFFu) * qdown) : (_Float16)0.0f;
+        hh[2 * e + 1] = head_live ? (_Float16)(bf16_bits_to_f32(ws[e] >> 16) * qdown) : (_Float16)0.0f;
       }
       h = __builtin_bit_cast(short8_t, hh);
     } else {
@@ -367,7 +382,7 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
 
   Raw<F> raw;
   load_raw<F, TWO>(a, slots, 0, raw);
-  dequant<F, TWO>(a, slots, 0, raw, g0, g1, ktiles);
+  dequant<F, TWO>(a, slots, 0, raw, ktiles);
   if (a.steps > 1) load_raw<F, TWO>(a, slots, 1, raw);
   __syncthreads();
   for (int step = 0; step < a.steps; ++step) {
@@ -375,13 +390,25 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
     // the next step's keys into the other tile (its readers finished before the previous barrier; after the last step
     // it is the padding step, all zeros, never read), then the raw records of the step after (the last one again at
     // the end): no branch, so the compiler can interleave this VALU work with the MFMAs below
-    dequant<F, TWO>(a, slots, step + 1, raw, g0, g1, ktiles + ((step + 1) & 1) * (kKTile<F> / 2));
+    dequant<F, TWO>(a, slots, step + 1, raw, ktiles + ((step + 1) & 1) * (kKTile<F> / 2));
     load_raw<F, TWO>(a, slots, min(step + 2, a.steps - 1), raw);
     const uint32_t valid = (uint32_t)__builtin_amdgcn_ballot_w64(lane < kMSteps &&
                                                                   entry_valid(slots[step * kMSteps + (lane & 31)]));
     // S^T for the two 16-key tiles, one MFMA chain each. The K fragments (and LDS-resident query chunks) of chunk
     // kk + kQAhead are read while the MFMAs of chunk kk run; scheduling barriers keep that order, so an MFMA does not
     // wait for a read issued just before it.
+    // this lane's keys T(j) as bits 0..7: keys 4j .. 4j+3, then 16+4j .. 16+4j+3
+    const uint32_t vmask = ((valid >> (4 * j)) & 0xFu) | (((valid >> (16 + 4 * j)) & 0xFu) << 4);
+    // NVFP4: the global scale of each of those keys (of its cache; two caches may differ). Chunks below kLatC are the
+    // latent's: once they are summed, the accumulators are multiplied by the key's global scale, and the rope chunks
+    // (no global scale) add onto them.
+    constexpr int kLatC = F == kNvfp4 ? kDl / 32 : kQC;
+    uint32_t l1 = 0u;   // bit e: key e of T(j) is cache 1's
+    if constexpr (F == kNvfp4 && TWO) {
+      const uint32_t b =
+          (uint32_t)__builtin_amdgcn_ballot_w64(lane < kMSteps && slots[step * kMSteps + (lane & 31)] <= -2);
+      l1 = ((b >> (4 * j)) & 0xFu) | (((b >> (16 + 4 * j)) & 0xFu) << 4);
+    }
     float4_t s[2] = {float4_t{0.f, 0.f, 0.f, 0.f}, float4_t{0.f, 0.f, 0.f, 0.f}};
     short8_t kf[kQC][2], qf[kQC];
     auto read_chunk = [&](int kk) {
@@ -398,20 +425,18 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
     for (int kk = 0; kk < kQC; ++kk) {
       if (kk + kQAhead < kQC) read_chunk(kk + kQAhead);
       __builtin_amdgcn_sched_barrier(0);
+      if (kk == kLatC) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s[e >> 2][e & 3] *= ((l1 >> e) & 1u) ? g1 : g0;
+      }
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) s[tt] = mfma16<F>(kf[kk][tt], qf[kk], s[tt]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    if constexpr (F == kFp8V4) {
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) s[tt] *= a.qscale;
-    }
-    // online softmax of head hl over keys T(j), lazy rescale
-    // this lane's keys T(j) as bits 0..7: keys 4j .. 4j+3, then 16+4j .. 16+4j+3
-    const uint32_t vmask = ((valid >> (4 * j)) & 0xFu) | (((valid >> (16 + 4 * j)) & 0xFu) << 4);
     float sv[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sv[e] = ((vmask >> e) & 1u) ? s[e >> 2][e & 3] : -__builtin_inff();
+    for (int e = 0; e < 8; ++e) sv[e] = ((vmask >> e) & 1u) ? s[e >> 2][e & 3] * smul : -__builtin_inff();
+    // online softmax of head hl over keys T(j), lazy rescale
     float mt = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
     mt = max4_lanes16(mt);
     if (__builtin_amdgcn_ballot_w64(mt > m + kRescaleM)) {
@@ -430,7 +455,7 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
       const float p = __builtin_amdgcn_exp2f(sv[e] - m_use);
       psum += p;
       if constexpr (F == kNvfp4)
-        pb[e] = __builtin_bit_cast(short, (_Float16)p);
+        pb[e] = __builtin_bit_cast(short, (_Float16)(p * (((l1 >> e) & 1u) ? g1 : g0)));
       else
         pb[e] = __builtin_bit_cast(short, (__bf16)p);
     }

@@ -117,6 +117,16 @@ __device__ inline float sum4_lanes16(float x) {
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
+// The power of two 2^e that brings a head's largest query magnitude `qmax` into [2^10, 2^11): the query enters FP16
+// MFMA operands as q * 2^-e, exactly (BF16's 8 significant bits fit FP16's 11, and the head's values sit in FP16's
+// normal range), and 2^e multiplies the FP32 scores. Zero, subnormal, infinite or NaN maxima give e = 0; e is kept
+// in [-100, 100]. Returns {2^-e, 2^e}.
+__device__ inline float2_t pow2_query_scale(float qmax) {
+  const int biased = (int)(__float_as_uint(qmax) >> 23) & 0xFF;
+  int e = (biased == 0 || biased == 255) ? 0 : biased - 127 - 10;
+  e = e < -100 ? -100 : e > 100 ? 100 : e;
+  return float2_t{__uint_as_float((uint32_t)(127 - e) << 23), __uint_as_float((uint32_t)(127 + e) << 23)};
+}
 // Split arrival: the workgroups of one output (key splits of a row) leave partial results in a workspace and count
 // their arrivals; the last to arrive merges. The protocol keeps every access to the shared partials coherent by
 // itself, so no fence has to write back or invalidate a whole L2 (an agent-scope release fence is a buffer_wbl2 and
@@ -153,6 +163,7 @@ __device__ inline void reset_counter(int32_t* counter) {
 }
 #else
 // The host pass parses device code without the gfx950 builtins; these declarations are never code-generated.
+__device__ float2_t pow2_query_scale(float qmax);
 __device__ void store_partial(__amdgpu_buffer_rsrc_t r, int byte_off, float4_t v);
 __device__ float4_t load_partial(__amdgpu_buffer_rsrc_t r, int byte_off);
 __device__ bool arrive_last(int32_t* counter, int splits, int* flag);
