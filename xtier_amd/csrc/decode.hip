@@ -370,9 +370,11 @@ __device__ inline void store_out(const DecodeArgs& a, int row, int head, int d0,
 }
 
 // D: head size; HPW: KV heads per workgroup (4 or 1); the workgroup's W / HPW key slices of each head merge through
-// LDS.
+// LDS. Two waves per SIMD (one 8-wave or two 4-wave workgroups per CU); three for the 4-wave workgroups of 4 KV heads
+// (prefill chunks: one slice per head, no LDS merge region, so three workgroups fit a CU's LDS; 168 VGPRs, the few
+// values spilled are held across the main loop only: the batch-4096 prefill chunk 622 -> 599 us).
 template <int D, int P, int HPW, bool PS, int W, bool O32>
-__global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArgs a) {
+__global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4) ? 3 : 2) decode_split_kernel(const DecodeArgs a) {
   using G = Geo<D>;
   constexpr int kSlices = W / HPW;
   constexpr int kThreads = 64 * W;
@@ -564,6 +566,31 @@ __global__ void __launch_bounds__(64 * W, 2) decode_split_kernel(const DecodeArg
   }
   // the 4 lanes of a head hold disjoint key subsets of l
   float l_tot = sum4_lanes16(st.l);
+
+  // One slice per head and one key split (4 KV heads per 4-wave workgroup: prefill chunks): the wave's state is its
+  // head's result; it normalizes and writes it from registers (acc[t][0..7][r] are dims 128 t + 32 j + 8 r .. + 7),
+  // with no LDS merge, and the launch reserves no merge region.
+  if constexpr (kSlices == 1) {
+    if (a.splits == 1) {
+      if (active && hl < a.group && (D != 64 || j < 2)) {
+        const float inv = l_tot > 0.0f ? gv_v / l_tot : 0.0f;
+        const int head = kvh * a.group + hl;
+#pragma unroll
+        for (int t = 0; t < G::kNT; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = st.acc[t][i][r] * inv;
+            store_out(a, row, head, 128 * t + 32 * j + 8 * r, v, 8);
+          }
+        if (a.lse && j == 0)
+          a.lse[(int64_t)row * a.q_heads + head] =
+              l_tot > 0.0f ? (st.m + __builtin_log2f(l_tot)) * kLn2 : -__builtin_inff();
+      }
+      return;
+    }
+  }
 
   // 2. the slices merge through LDS behind one barrier: every wave leaves its (O^T in dim order, max, sum) per lane
   // in its own region (after the slot list and V tiles, so no wave still reading those is disturbed); then each
@@ -944,11 +971,12 @@ static int launch_decode(int hpw, bool ps, bool o32, const DecodeArgs& a, dim3 g
                   : launch_decode<D, 1, false, W>(o32, a, grid, lds_bytes, stream, what);
 }
 
-// LDS bytes of a launch: the slot list, one V tile per wave and one merge region per wave.
+// LDS bytes of a launch: the slot list, one V tile per wave and, unless each head has one slice and one split (the
+// waves then write their heads' outputs from registers), one merge region per wave.
 template <int D>
-static size_t decode_lds(int slot_bytes, int waves) {
+static size_t decode_lds(int slot_bytes, int waves, bool direct) {
   return (size_t)slot_bytes + (size_t)waves * Geo<D>::kWaveLds +
-         (waves == 4 ? Geo<D>::template kMergeLds<4> : Geo<D>::template kMergeLds<kWaves>);
+         (direct ? 0 : waves == 4 ? Geo<D>::template kMergeLds<4> : Geo<D>::template kMergeLds<kWaves>);
 }
 
 static int prefetch_of(int dim) { return dim == 64 ? Geo<64>::kPrefetch : dim == 128 ? Geo<128>::kPrefetch
@@ -1005,9 +1033,10 @@ static int decode_impl(const char* what, const void* q, int64_t q_row_stride, in
   const int pf = prefetch_of(dim);
   const int slice_steps = ((kps / kStep + slices * pf - 1) / (slices * pf)) * pf;
   const int slot_bytes = slices * slice_steps * kStep * (int)sizeof(int32_t);
-  const size_t lds_bytes = dim == 64    ? decode_lds<64>(slot_bytes, waves)
-                           : dim == 128 ? decode_lds<128>(slot_bytes, waves)
-                                        : decode_lds<256>(slot_bytes, waves);
+  const bool direct = slices == 1 && splits == 1;
+  const size_t lds_bytes = dim == 64    ? decode_lds<64>(slot_bytes, waves, direct)
+                           : dim == 128 ? decode_lds<128>(slot_bytes, waves, direct)
+                                        : decode_lds<256>(slot_bytes, waves, direct);
   if (lds_bytes > kMaxLds)
     return fail(XT_EUNSUPPORTED, "%s: %d keys per split needs %zu bytes of LDS; use more splits", what, kps,
                 lds_bytes);
