@@ -184,7 +184,7 @@ struct WaveCtx {
 template <bool O32>
 __device__ inline const uint8_t* row_at(const uint8_t* col, int32_t slot, int64_t stride, uint32_t lane_off) {
   const uint32_t s = slot < 0 ? 0u : (uint32_t)slot;
-  if constexpr (O32) return col + (__umul24(s, (uint32_t)stride) + lane_off);
+  if constexpr (O32) return col + ((uint32_t)__umul24(s, (uint32_t)stride) + lane_off);   // __umul24 is signed
   else return col + (int64_t)s * stride + lane_off;
 }
 

@@ -1,7 +1,8 @@
 // Sparse MLA: 128 query heads share one key per token. Two cache formats:
 //   NVFP4 latent (kNvfp4): key = [latent (512, NVFP4 with E4M3 block scales and a global scale) | rope (64, BF16)],
 //     576 wide, value = the latent; operands FP16: the query as q * 2^-e per head (exact), the key tile as e2m1 * e4m3
-//     (exact), the global scale applied to the FP32 latent scores and folded into P;
+//     (exact), the global scale applied to the FP32 latent scores and to the values (through P with two caches, on
+//     the normalized output with one);
 //   DeepSeek V4 FP8 pages (kFp8V4, sparse_mla.py:38-59): key = [448 E4M3 values x UE8M0 scale per 64 | 64 BF16 rope],
 //     512 wide, value = the key; operands BF16 as in the reference, the scale applied to the FP32 scores.
 // q.k and p.v on MFMA (v_mfma_f32_16x16x32_f16 / _bf16), online softmax in the exp2 domain, an optional per-head sink
@@ -25,7 +26,7 @@
 //
 // Numerics: NVFP4: e2m1 * e4m3 is exact in FP16 (at most 6 significant bits), and so is the query scaled by a power of
 // two; the latent and rope parts of a score accumulate apart, and score = (latent . q * g + rope . q) * scale *
-// log2(e) * 2^e in FP32 (g of the key's cache); P is FP16 of p * g for the values, the sum takes p. V4: e4m3 * 2^(e - 127) is exact in BF16 (4 significant bits) for scales from
+// log2(e) * 2^e in FP32 (g of the key's cache); P is FP16 of p (of p * g with two caches), the sum takes p. V4: e4m3 * 2^(e - 127) is exact in BF16 (4 significant bits) for scales from
 // 2^-126; a zero scale byte (2^-127) reads as 0; P is BF16. The running maximum is raised lazily (P <= 256); sums are
 // FP32.
 #include "xt_common.h"
@@ -95,6 +96,8 @@ struct MlaArgs {
                                      // normalized by its own sum
   float* ml;                         // [rows, splits, heads, 2]: the split's running max (log2 domain) and sum
   uint32_t xcd_units, xcd_extra;
+  int o32;                           // NVFP4: every cache has fewer than 2^24 slots and all its rows within 2^32
+                                     // bytes, so record offsets are one 24-bit multiply-add (else 64-bit arithmetic)
 };
 
 typedef short short8_t __attribute__((ext_vector_type(8)));
@@ -181,6 +184,23 @@ __device__ inline void load_raw(const MlaArgs& a, const int32_t* slots, int step
     }
     return;
   } else {
+  if (a.o32) {   // uniform over the launch; unsigned 32-bit offsets (HIP's __umul24 returns a signed int)
+    const uint32_t cu = (uint32_t)c;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t s;
+      const CacheDev& cd = cache_of<TWO>(a, ent[i], s);
+      r.pay[i] = *reinterpret_cast<const uint32_t*>(cd.pay + ((uint32_t)__umul24(s, cd.pay_stride) + 4u * cu));
+      r.sc[i] = cd.sf[(uint32_t)__umul24(s, cd.sf_stride) + (cu >> 1)];
+    }
+    if (t < 256) {
+      uint32_t s;
+      const CacheDev& cd = cache_of<TWO>(a, slots[step * kMSteps + (t >> 3)], s);
+      r.rope = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(cd.rope) +
+                                               ((uint32_t)__umul24(s, cd.rope_stride) + 16u * ((uint32_t)t & 7u)));
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     uint32_t s;
@@ -455,7 +475,7 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
       const float p = __builtin_amdgcn_exp2f(sv[e] - m_use);
       psum += p;
       if constexpr (F == kNvfp4)
-        pb[e] = __builtin_bit_cast(short, (_Float16)(p * (((l1 >> e) & 1u) ? g1 : g0)));
+        pb[e] = __builtin_bit_cast(short, (_Float16)(TWO ? p * (((l1 >> e) & 1u) ? g1 : g0) : p));
       else
         pb[e] = __builtin_bit_cast(short, (__bf16)p);
     }
@@ -484,7 +504,7 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
     const float m_use = (m == -__builtin_inff()) ? 0.0f : m;
     float total = l_tot;
     if (a.sink) total += __builtin_amdgcn_exp2f(a.sink[head] * kLog2e - m_use);
-    const float inv = l_tot > 0.0f ? 1.0f / total : 0.0f;
+    const float inv = l_tot > 0.0f ? (TWO ? 1.0f : g0) / total : 0.0f;   // one cache: its g, once
 #pragma unroll
     for (int dt = 0; dt < 32; ++dt) {
       const float v[4] = {acc[dt][0] * inv, acc[dt][1] * inv, acc[dt][2] * inv, acc[dt][3] * inv};
@@ -498,7 +518,7 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
   //    FP32) plus its max and sum; a second launch merges the splits. The partials are stored in the accumulators'
   //    lane order (part_index), so every store of a wave writes one contiguous run.
   if (16 * wave >= a.heads) return;   // a wave without live heads has no partials (heads pad to whole waves only)
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  const float inv = l_tot > 0.0f ? (TWO ? 1.0f : g0) / l_tot : 0.0f;   // one cache: its g, once
   const int64_t pbase = part_index(a, row, split, wave, 0, lane);
   if constexpr (F == kNvfp4) {
     uint16_t* pp = static_cast<uint16_t*>(a.part) + pbase;
@@ -791,6 +811,11 @@ extern "C" int xt_sparse_mla_nvfp4(const void* q, int64_t q_row_stride, int64_t 
   } else {
     a.c[1] = a.c[0];
   }
+  auto fits32 = [](const CacheDev& c) {
+    return c.slots < (1 << 24) && (uint64_t)c.slots * c.pay_stride <= 0xFFFFFFFFull &&
+           (uint64_t)c.slots * c.sf_stride <= 0xFFFFFFFFull && (uint64_t)c.slots * c.rope_stride <= 0xFFFFFFFFull;
+  };
+  a.o32 = fits32(a.c[0]) && fits32(a.c[1]);
   return mla_launch<kNvfp4>(what, a, extra, q, q_row_stride, q_head_stride, heads, keys, extra_keys, sink, scale, out,
                             out_row_stride, out_head_stride, out_dtype, lse, rows, splits, workspace,
                             workspace_bytes, stream);
@@ -809,6 +834,7 @@ extern "C" int xt_sparse_mla_fp8(const void* q, int64_t q_row_stride, int64_t q_
   if (st != XT_OK || done) return st;
   const bool extra = extra_cache && extra_keys && extra_keys->indices && extra_keys->topk > 0;
   MlaArgs a;
+  a.o32 = 0;
   st = check_pages(what, cache, &a.c[0]);
   if (st != XT_OK) return st;
   if (extra) {
