@@ -261,6 +261,42 @@ def test_mla_prefill_chunk_full_size_sampled_rows():
     _check(out[rows], lse[rows], ref, ref_lse)
 
 
+def _scaled_pool(w, seed, mag, slots, layout='interleaved'):
+    gen = workloads.generator('cuda', seed)
+    lat, rope = workloads.mla_cache_rows(w, gen, 'cuda', 0, slots)
+    lat, rope = (lat.float() * mag).to(torch.bfloat16), (rope.float() * mag).to(torch.bfloat16)
+    pool = LatentPool(slots, w.latent, w.rope, 'cuda', layout=layout)
+    pool.set_global_scale(lat)
+    pool.append(lat, rope, torch.arange(slots, device='cuda'), saturate=False)
+    return pool
+
+
+@pytest.mark.parametrize('splits', [1, 2])
+@pytest.mark.parametrize('mag0,mag1', [(1e-3, 1e-3), (1e-3, 10.0), (10.0, 3e-2)])
+def test_mla_two_caches_of_different_scales(mag0, mag1, splits):
+    """Two key lists over caches whose latents differ in size (global scales g0, g1 from ~4e-6 to ~0.1): P enters
+    the value MFMA as FP16(p * g / max(g0, g1)), so neither a small g (P * g below FP16's normal range) nor a large
+    one (P * g beyond FP16's range) costs precision; held to the reference's scale-free measures and the LSE to
+    2e-3."""
+    w, inp = _case(41, rows=6)
+    pool = _scaled_pool(w, 8, mag0, w.slots)
+    pool2 = _scaled_pool(w, 9, mag1, 2048, layout='split')
+    gen = torch.Generator(device='cuda').manual_seed(6)
+    idx2 = torch.randint(0, 2048, (w.rows, 96), generator=gen, device='cuda', dtype=torch.int32)
+    len2 = torch.full((w.rows,), 96, dtype=torch.int32, device='cuda')
+    scale = 1 / math.sqrt(576)
+    out, lse = ops.sparse_mla(inp.q[:, None], pool, inp.slots[:, None], None, None, scale, extra_k_cache=pool2,
+                              extra_indices=idx2[:, None], extra_topk_length=len2, splits=splits)
+    ref, ref_lse = _ref(inp.q, pool, inp.slots, None, None, scale, extra=(pool2, idx2, len2))
+    d = out[:, 0].float().cpu().numpy().astype(np.float64) - ref
+    assert np.isfinite(d).all()
+    max_rel = np.abs(d).max() / np.abs(ref).max()
+    rms_rel = np.sqrt((d ** 2).mean()) / np.sqrt((ref ** 2).mean())
+    assert max_rel < 1e-2 and rms_rel < 4e-3, (max_rel, rms_rel)
+    got = lse[:, :, 0].cpu().numpy()
+    assert np.all(np.abs(got - ref_lse) <= 2e-3 + 2.0 ** -20 * np.abs(ref_lse))
+
+
 @pytest.mark.parametrize('top', [10.0, 1e-3])
 def test_mla_latent_magnitudes_over_three_decades(top):
     """Per-token latent and rope magnitudes spread over three decades, 10^U(-3, 0) * top: top 10 is the spread of

@@ -372,9 +372,11 @@ __device__ inline void store_out(const DecodeArgs& a, int row, int head, int d0,
 // D: head size; HPW: KV heads per workgroup (4 or 1); the workgroup's W / HPW key slices of each head merge through
 // LDS. Two waves per SIMD (one 8-wave or two 4-wave workgroups per CU); three for the 4-wave workgroups of 4 KV heads
 // (prefill chunks: one slice per head, no LDS merge region, so three workgroups fit a CU's LDS; 168 VGPRs, the few
-// values spilled are held across the main loop only: the batch-4096 prefill chunk 622 -> 599 us).
+// values spilled are held across the main loop only: the batch-4096 prefill chunk 622 -> 599 us). Head size 256
+// stays at two: its accumulators alone would spill ~100 registers at 168.
 template <int D, int P, int HPW, bool PS, int W, bool O32>
-__global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4) ? 3 : 2) decode_split_kernel(const DecodeArgs a) {
+__global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 : 2)
+    decode_split_kernel(const DecodeArgs a) {
   using G = Geo<D>;
   constexpr int kSlices = W / HPW;
   constexpr int kThreads = 64 * W;

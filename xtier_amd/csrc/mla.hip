@@ -1,13 +1,14 @@
 // Sparse MLA: 128 query heads share one key per token. Two cache formats:
 //   NVFP4 latent (kNvfp4): key = [latent (512, NVFP4 with E4M3 block scales and a global scale) | rope (64, BF16)],
 //     576 wide, value = the latent; operands FP16: the query as q * 2^-e per head (exact), the key tile as e2m1 * e4m3
-//     (exact), the global scale applied to the FP32 latent scores and to the values (through P with two caches, on
-//     the normalized output with one);
+//     (exact), the global scale applied to the FP32 latent scores and to the values on the normalized output (with
+//     two caches, P carries each key's g relative to the larger of the two);
 //   DeepSeek V4 FP8 pages (kFp8V4, sparse_mla.py:38-59): key = [448 E4M3 values x UE8M0 scale per 64 | 64 BF16 rope],
 //     512 wide, value = the key; operands BF16 as in the reference, the scale applied to the FP32 scores.
 // q.k and p.v on MFMA (v_mfma_f32_16x16x32_f16 / _bf16), online softmax in the exp2 domain, an optional per-head sink
 // in the denominator. With key splits, each (row, split) writes its output normalized by its own sum (FP16 for the
-// NVFP4 latent, whose values are FP16; FP32 for V4) with its max and sum, and a second, wide launch merges the splits:
+// NVFP4 latent: a convex combination of the cache's values, so within its largest magnitude 2688 g, which FP16 holds
+// for latents below 65504; FP32 for V4) with its max and sum, and a second, wide launch merges the splits:
 // one merging workgroup per row would read a row's partials at one CU's bandwidth.
 //
 // Work decomposition: a workgroup = 8 wavefronts x 16 heads = 128 heads of one (query row, key split), so every key is
@@ -26,9 +27,10 @@
 //
 // Numerics: NVFP4: e2m1 * e4m3 is exact in FP16 (at most 6 significant bits), and so is the query scaled by a power of
 // two; the latent and rope parts of a score accumulate apart, and score = (latent . q * g + rope . q) * scale *
-// log2(e) * 2^e in FP32 (g of the key's cache); P is FP16 of p (of p * g with two caches), the sum takes p. V4: e4m3 * 2^(e - 127) is exact in BF16 (4 significant bits) for scales from
-// 2^-126; a zero scale byte (2^-127) reads as 0; P is BF16. The running maximum is raised lazily (P <= 256); sums are
-// FP32.
+// log2(e) * 2^e in FP32 (g of the key's cache); P is FP16 of p (of p * g / max(g0, g1) with two caches), the sum takes
+// p, and the normalization multiplies by g (by max(g0, g1)). V4: e4m3 * 2^(e - 127) is exact in BF16 (4 significant
+// bits) for scales from 2^-126; a zero scale byte (2^-127) reads as 0; P is BF16. The running maximum is raised lazily
+// (P <= 256); sums are FP32.
 #include "xt_common.h"
 #include "xt_host.h"
 
@@ -389,10 +391,15 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
     else
       *reinterpret_cast<short8_t*>(qs + ((kk - kQR) * kMHeads + 16 * wave + hl) * kQRow + 8 * (j ^ ((hl >> 1) & 3))) = h;
   }
-  float g0 = 1.0f, g1 = 1.0f;   // NVFP4 global scales (V4 has none)
+  // NVFP4 global scales (V4 has none): g0 / g1 scale the latent scores; with two caches P carries g / max(g0, g1)
+  // (at most 1, so P <= 256 stays in FP16's range whatever the scales) and the normalization multiplies by the max.
+  // (1 / max is uniform: readfirstlane keeps it in a scalar register, and P's select reuses the scores' g0 / g1).
+  float g0 = 1.0f, g1 = 1.0f, ginv = 1.0f;
   if constexpr (F == kNvfp4) {
     g0 = *a.c[0].g;
     g1 = TWO ? *a.c[1].g : g0;
+    const float gm = fmaxf(g0, g1);
+    if (TWO && gm > 0.0f) ginv = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(1.0f / gm)));
   }
 
   float m = -__builtin_inff(), l = 0.0f;
@@ -475,7 +482,7 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
       const float p = __builtin_amdgcn_exp2f(sv[e] - m_use);
       psum += p;
       if constexpr (F == kNvfp4)
-        pb[e] = __builtin_bit_cast(short, (_Float16)(TWO ? p * (((l1 >> e) & 1u) ? g1 : g0) : p));
+        pb[e] = __builtin_bit_cast(short, (_Float16)(TWO ? p * ginv * (((l1 >> e) & 1u) ? g1 : g0) : p));
       else
         pb[e] = __builtin_bit_cast(short, (__bf16)p);
     }
@@ -504,7 +511,7 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
     const float m_use = (m == -__builtin_inff()) ? 0.0f : m;
     float total = l_tot;
     if (a.sink) total += __builtin_amdgcn_exp2f(a.sink[head] * kLog2e - m_use);
-    const float inv = l_tot > 0.0f ? (TWO ? 1.0f : g0) / total : 0.0f;   // one cache: its g, once
+    const float inv = l_tot > 0.0f ? (TWO ? fmaxf(g0, g1) : g0) / total : 0.0f;
 #pragma unroll
     for (int dt = 0; dt < 32; ++dt) {
       const float v[4] = {acc[dt][0] * inv, acc[dt][1] * inv, acc[dt][2] * inv, acc[dt][3] * inv};
@@ -514,11 +521,11 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
       a.lse[row * a.heads + head] = l_tot > 0.0f ? (m + __builtin_log2f(l_tot)) * kLn2 : -__builtin_inff();
     return;
   }
-  // 2. the split's output normalized by its own sum (NVFP4: FP16, a convex combination of FP16 latent values; V4:
+  // 2. the split's output normalized by its own sum (NVFP4: FP16, a convex combination of latent values; V4:
   //    FP32) plus its max and sum; a second launch merges the splits. The partials are stored in the accumulators'
   //    lane order (part_index), so every store of a wave writes one contiguous run.
   if (16 * wave >= a.heads) return;   // a wave without live heads has no partials (heads pad to whole waves only)
-  const float inv = l_tot > 0.0f ? (TWO ? 1.0f : g0) / l_tot : 0.0f;   // one cache: its g, once
+  const float inv = l_tot > 0.0f ? (TWO ? fmaxf(g0, g1) : g0) / l_tot : 0.0f;
   const int64_t pbase = part_index(a, row, split, wave, 0, lane);
   if constexpr (F == kNvfp4) {
     uint16_t* pp = static_cast<uint16_t*>(a.part) + pbase;

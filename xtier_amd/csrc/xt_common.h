@@ -118,8 +118,9 @@ __device__ inline float sum4_lanes16(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 // The power of two 2^e that brings a head's largest query magnitude `qmax` into [2^10, 2^11): the query enters FP16
-// MFMA operands as q * 2^-e, exactly (BF16's 8 significant bits fit FP16's 11, and the head's values sit in FP16's
-// normal range), and 2^e multiplies the FP32 scores. Zero, subnormal, infinite or NaN maxima give e = 0; e is kept
+// MFMA operands as q * 2^-e, exactly for every element down to 2^-24 of qmax (BF16's 8 significant bits fit FP16's
+// 11 within its normal range; smaller elements weigh less than that in any score), and 2^e multiplies the FP32
+// scores. Zero, subnormal, infinite or NaN maxima give e = 0; e is kept
 // in [-100, 100]. Returns {2^-e, 2^e}.
 __device__ inline float2_t pow2_query_scale(float qmax) {
   const int biased = (int)(__float_as_uint(qmax) >> 23) & 0xFF;

@@ -744,7 +744,7 @@ def sparse_mla(q, k_cache, indices, topk_length, attn_sink, softmax_scale, extra
     return (out.unsqueeze(1), lse.unsqueeze(-1)) if shape4 else (out, lse)
 
 
-def clock_mhz(device='cuda', iters=200000):
+def clock_mhz(device='cuda', iters=20000):
     """The shader clock in MHz while one wavefront runs (xt_clock_probe: core clock ticks over 100 MHz ticks)."""
     out = torch.zeros(3, dtype=torch.int64, device=device)
     _lib.check(_lib.lib().xt_clock_probe(_ptr(out), int(iters), _stream(out)), 'clock_probe')
