@@ -432,7 +432,7 @@ def run_block(args, w, ops, workloads):
     layers = max(1, min(args.layers, 8))
     pools = [build_block_pool(w, gen, workloads, ops) for _ in range(layers)]
     inp = workloads.block_decode_inputs(w, 20261104, 'cuda')
-    splits = args.splits or ops.default_splits(w.batch, w.kv_heads, w.keys)
+    splits = args.splits or ops.default_splits(w.batch, w.kv_heads, w.keys, False)
     ws = ops.new_workspace('cuda', w.batch, w.q_heads, w.dim, splits)
     out = torch.empty(w.batch, w.q_heads, w.dim, dtype=torch.bfloat16, device='cuda')
     torch.cuda.synchronize()
@@ -499,7 +499,7 @@ def run_block_prefill(args, w, ops, workloads):
                           ops)[:2]
     ik = [t[:, 0] for t in ik]
     inp = workloads.block_prefill_inputs(w, 20261202, 'cuda')
-    splits = args.splits or ops.default_splits(w.q_len, w.kv_heads, w.topk_blocks * w.block)
+    splits = args.splits or ops.default_splits(w.q_len, w.kv_heads, w.topk_blocks * w.block, False)
     ws = ops.new_workspace('cuda', w.q_len, w.q_heads, w.dim, splits)
     out = torch.empty_like(inp.q)
     rows = -(-w.ctx // 128) * 128

@@ -58,11 +58,12 @@ def _small_case(seed=3, batch=6, ctx=3008, heads=4, qh=32, topk=700, page=64, di
 
 @pytest.mark.parametrize('dim,heads,qh,batch,splits', [
     (64, 2, 16, 6, 1), (64, 4, 32, 40, 4), (64, 1, 8, 5, 3),
-    (256, 2, 24, 6, 1), (256, 2, 24, 6, 5), (256, 4, 32, 80, 4), (256, 1, 4, 3, 2),
+    (256, 2, 24, 6, 1), (256, 2, 24, 6, 5), (256, 4, 32, 80, 4), (256, 1, 4, 3, 2), (256, 2, 16, 128, 2),
 ])
 def test_decode_head_sizes(dim, heads, qh, batch, splits):
     """Head sizes 64 and 256 (the reference's Qwen3.8 QSA shape is 2 KV heads x 256) against the oracle, with -1
-    holes, short rows and key splits; 80 rows x 4 KV heads x 4 splits takes 4 KV heads per workgroup."""
+    holes, short rows and key splits; 80 rows x 4 KV heads x 4 splits takes 4 KV heads per workgroup, 40 rows x 4 KV
+    heads x 4 splits (head size 64) and 128 rows x 2 KV heads x 2 splits (head size 256) take 2."""
     pool, pt, idx, q = _small_case(seed=dim + heads * 10 + batch, batch=batch, heads=heads, qh=qh, dim=dim)
     idx = idx.numpy().copy()
     idx[0, ::9] = -1
@@ -314,6 +315,30 @@ def test_decode_past_one_round_of_workgroups(batch, splits):
                             page_size=64, splits=splits)
     ref, flash, _ = _oracle(pool.raw, bf16_numpy(q), pt.numpy(), 64, np.arange(batch), idx.numpy(), None, seq, 0.09)
     _check(out, ref, flash)
+
+
+@pytest.mark.parametrize('splits', [4, 5])
+def test_decode_two_kv_heads_per_workgroup(splits):
+    """32 rows x 4 KV heads with 4 or 5 key splits fill the CUs with workgroups of 2 KV heads (8 waves at 256
+    workgroups, 4 at 320): every row against the oracle on SGLang's split pool, and the interleaved pool's bits equal
+    to the split pool's."""
+    pool, pt, idx, q = _small_case(seed=50 + splits, batch=32)
+    idx = idx.numpy().copy()
+    idx[3, ::5] = -1
+    seq = np.full(32, 3008, np.int32)
+    seq[7] = 900
+    scale = 128 ** -0.5
+    lse = torch.empty(32, 32, dtype=torch.float32, device='cuda')
+    out = ops.sparse_decode(q.cuda(), pool.raw, pt.cuda(), _dev(idx), _dev(seq), scale, page_size=64, lse=lse,
+                            splits=splits)
+    ref, flash, lse_ref = _oracle(pool.raw, bf16_numpy(q), pt.numpy(), 64, np.arange(32), idx, None, seq, scale)
+    _check(out, ref, flash)
+    assert np.abs(lse.cpu().numpy() - lse_ref).max() < 2e-3
+    il = KVPool(pool.raw[0].shape[0], 4, 128, layout='interleaved', gk=pool.raw[4].clone(), gv=pool.raw[5].clone())
+    for dst, src in zip((il.k_pay, il.v_pay, il.k_sf, il.v_sf), pool.raw[:4]):
+        dst.copy_(src)
+    out2 = ops.sparse_decode(q.cuda(), il.raw, pt.cuda(), _dev(idx), _dev(seq), scale, page_size=64, splits=splits)
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
 
 
 def test_interleaved_pool_equals_split_pool():

@@ -4,7 +4,8 @@
 // (row, key split, head), and the last workgroup of a (row, KV head group) to finish merges them.
 //
 // Work decomposition: a workgroup = W wavefronts = HPW consecutive KV heads x W / HPW key slices of one (query row,
-// key split). HPW = 4 when the KV heads are a multiple of 4 and that alone fills every CU, else 1 (more workgroups).
+// key split). HPW = 4 when the KV heads are a multiple of 4 and that alone fills every CU, else 2 when a multiple of 2
+// fills them, else 1 (more workgroups).
 // W = 8 while the workgroups fit one round on the CUs (decode batches), else 4, compiled for two workgroups per CU
 // (prefill chunks, one row per query). Each wave owns one (row, KV head, split, slice) and walks its keys in steps of
 // 32. The workgroup computes the split's pool slots once into LDS and merges the slices of each head through LDS
@@ -369,7 +370,7 @@ __device__ inline void store_out(const DecodeArgs& a, int row, int head, int d0,
   }
 }
 
-// D: head size; HPW: KV heads per workgroup (4 or 1); the workgroup's W / HPW key slices of each head merge through
+// D: head size; HPW: KV heads per workgroup (4, 2 or 1); the workgroup's W / HPW key slices of each head merge through
 // LDS. Two waves per SIMD (one 8-wave or two 4-wave workgroups per CU); three for the 4-wave workgroups of 4 KV heads
 // (prefill chunks: one slice per head, no LDS merge region, so three workgroups fit a CU's LDS; 168 VGPRs, the few
 // values spilled are held across the main loop only: the batch-4096 prefill chunk 622 -> 599 us). Head size 256
@@ -714,8 +715,14 @@ using namespace xt;
 
 // Workgroup shape: 4 KV heads per workgroup when that alone yields a full launch (one workgroup per CU), else 1 KV
 // head (more, smaller workgroups: a (row, head) merges its slices in LDS instead of through partials).
+// KV heads per workgroup: 4 when that alone fills every CU, else 2 when that does, else 1 (more, smaller workgroups).
+// A pair of heads reads each key's K and V payload pieces of both heads together (whole 128-byte lines on SGLang's
+// split pool). Measured, batch 32 x 4 KV heads, top-2048: 2 heads x 4 splits 18.7 us (split pool 20.8 us) against
+// 1 head x 2 splits 19.1 us (21.8 us).
 static int heads_per_workgroup(int rows, int kv_heads, int splits, int cus) {
-  return (kv_heads % 4 == 0 && (int64_t)rows * (kv_heads / 4) * splits >= cus) ? 4 : 1;
+  if (kv_heads % 4 == 0 && (int64_t)rows * (kv_heads / 4) * splits >= cus) return 4;
+  if (kv_heads % 2 == 0 && (int64_t)rows * (kv_heads / 2) * splits >= cus) return 2;
+  return 1;
 }
 
 // Pool and index addressing beyond the token-major pool with one shared index list per row.
@@ -966,11 +973,13 @@ template <int D, int W>
 static int launch_decode(int hpw, bool ps, bool o32, const DecodeArgs& a, dim3 grid, size_t lds_bytes,
                          hipStream_t stream, const char* what) {
   if constexpr (D == 128) {   // paired K/V scales: the interleaved pool at head size 128
-    if (ps) return hpw == 4 ? launch_decode<D, 4, true, W>(o32, a, grid, lds_bytes, stream, what)
-                            : launch_decode<D, 1, true, W>(o32, a, grid, lds_bytes, stream, what);
+    if (ps) return hpw == 4   ? launch_decode<D, 4, true, W>(o32, a, grid, lds_bytes, stream, what)
+                   : hpw == 2 ? launch_decode<D, 2, true, W>(o32, a, grid, lds_bytes, stream, what)
+                              : launch_decode<D, 1, true, W>(o32, a, grid, lds_bytes, stream, what);
   }
-  return hpw == 4 ? launch_decode<D, 4, false, W>(o32, a, grid, lds_bytes, stream, what)
-                  : launch_decode<D, 1, false, W>(o32, a, grid, lds_bytes, stream, what);
+  return hpw == 4   ? launch_decode<D, 4, false, W>(o32, a, grid, lds_bytes, stream, what)
+         : hpw == 2 ? launch_decode<D, 2, false, W>(o32, a, grid, lds_bytes, stream, what)
+                    : launch_decode<D, 1, false, W>(o32, a, grid, lds_bytes, stream, what);
 }
 
 // LDS bytes of a launch: the slot list, one V tile per wave and, unless each head has one slice and one split (the

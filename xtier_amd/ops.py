@@ -304,18 +304,24 @@ def device_cus(device=None):
     return n
 
 
-def default_splits(rows, kv_heads, topk):
-    """Key splits per row: about one workgroup of one KV head per CU, at least 512 keys per split (two steps of two
-    loads in flight for each of a workgroup's 8 wavefronts), and at most 8192 keys per split (the slot list lives in
-    LDS). Small launches are latency-bound and every split adds to the merge, so the floor of 512 keys wins over
-    filling the CUs. Measured on MI355X (256 CUs), per layer-step: batch 32 x 4 KV heads, top-2048: 2 splits 19.1 us;
+def default_splits(rows, kv_heads, topk, pair_heads=True):
+    """Key splits per row: about one workgroup per CU, at least 512 keys per split (two steps of two loads in flight
+    for each of a workgroup's 8 wavefronts), and at most 8192 keys per split (the slot list lives in LDS). With an
+    even number of KV heads shared by every head's index list (`pair_heads`), workgroups of 2 KV heads are preferred
+    when 2 or more such splits fill the CUs; else workgroups of 1 KV head. Small launches are latency-bound and every
+    split adds to the merge, so the floor of 512 keys wins over filling the CUs. Measured on MI355X (256 CUs), per
+    layer-step: batch 32 x 4 KV heads, top-2048: 2 KV heads x 4 splits 18.7 us, 1 KV head x 2 splits 19.1 us;
     batch 4 x 4 KV heads, top-2048: 1 / 2 / 4 / 8 / 16 splits 16.3 / 14.0 / 12.1 / 12.6 / 15.0 us; 1 row x 1 KV
     head, top-512: 1 / 2 splits 8.4 / 10.4 us; 4096 prefill rows -> 1."""
     if topk <= 0:
         return 1
+    cap, floor = min(topk // 512, 64), min(64, math.ceil(topk / 8192))
+    if pair_heads and kv_heads % 2 == 0 and rows > 0:
+        s = math.ceil(device_cus() / (rows * (kv_heads // 2)))
+        if 2 <= s <= cap:
+            return max(s, floor)
     units = max(1, rows * kv_heads)
-    splits = max(1, min(math.ceil(device_cus() / units), topk // 512, 64))
-    return max(splits, min(64, math.ceil(topk / 8192)))
+    return max(max(1, min(math.ceil(device_cus() / units), cap)), floor)
 
 
 def varlen_splits(rows, kv_heads, group, max_k):
@@ -329,7 +335,7 @@ def varlen_splits(rows, kv_heads, group, max_k):
             s = math.ceil(device_cus() / max(1, rows * (kv_heads // h)))
             if s <= cap:
                 return max(s, min(64, math.ceil(max_k / 8192)))
-    return default_splits(rows, kv_heads, max_k)
+    return default_splits(rows, kv_heads, max_k, False)
 
 
 def decode_workspace_bytes(rows, q_heads, dim, splits):
@@ -449,7 +455,7 @@ def fp4_sparse_decode(q, k_pay, k_sc, v_pay, v_sc, req_to_token, slot_ids, topk_
     seq_lens = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
     topk = topk_idx.shape[2]
     if splits is None:
-        splits = _capture_splits(q.device, b, qh, d, default_splits(b, kh, topk * block_size), ws)
+        splits = _capture_splits(q.device, b, qh, d, default_splits(b, kh, topk * block_size, False), ws)
     ws = _decode_ws(q.device, b, qh, d, splits, ws)
     _lib.check(_lib.lib().xt_block_sparse_decode_nvfp4(
         _ptr(q), q.stride(0), q.stride(1), _ptr(k_pay), _ptr(v_pay), _ptr(k_sc), _ptr(v_sc), float(kv_scale),
@@ -524,7 +530,8 @@ def fp4_prefill_gqa_share_sparse(q, k_cache, v_cache, sink, req_to_token, slot_i
     q16 = q if q.dtype == torch.bfloat16 else q.to(torch.bfloat16)
     topk = topk_idx.shape[2]
     if splits is None:
-        splits = _capture_splits(dev, total_q, qh, d, default_splits(total_q, kh, topk * block_size_k), ws)
+        splits = _capture_splits(dev, total_q, qh, d, default_splits(total_q, kh, topk * block_size_k, False),
+                                 ws)
     ws = _decode_ws(dev, total_q, qh, d, splits, ws)
     _lib.check(_lib.lib().xt_block_sparse_prefill_nvfp4(
         _ptr(q16), q16.stride(0), q16.stride(1), _ptr(k_pay), _ptr(v_pay), _ptr(k_sc8), _ptr(v_sc8), float(kv_scale),
