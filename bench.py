@@ -942,7 +942,53 @@ def run_indexer(args, name, ops):
     emit(record)
 
 
-CEILING_WORKLOADS = ('mfma_ceiling', 'gather_ceiling_b32', 'gather_pieces_ceiling_b32')
+CEILING_WORKLOADS = ('mfma_ceiling', 'gather_ceiling_b32', 'gather_pieces_ceiling_b32', 'launch_ceiling',
+                     'split_merge_ceiling')
+
+
+def run_launch_ceilings(args, name, ops, cus):
+    """The floors under the short kernels: an empty launch of one workgroup per CU (xt_ceiling_launch), and the
+    decode kernels' split arrival alone (xt_ceiling_split_merge) on the batch-32 decode's grid: one workgroup per CU,
+    each writing its partial (32 rows x 2 splits x 8 heads x 132 floats = 4224 bytes per workgroup at 2 splits),
+    counting its arrival, the last of each row reloading and merging; the fenced form and 4 / 8 splits beside it.
+    16 launches per graph replay; microseconds per launch, lower is better."""
+    import torch
+    steps, warm = max(1, args.steps), max(1, args.warmup)
+    if name == 'launch_ceiling':
+        ms, per, rot = time_steps(lambda _: ops.ceiling_launch(cus), 16, steps, warm)
+        log(f'launch ceiling: {ms * 1e3:.2f} us per empty launch of {cus} workgroups x 512 threads')
+        config = {'workload': name, 'workgroups': cus, 'threads': 512}
+        metric, variants = 'empty kernel launch in a graph, us per launch', None
+    else:
+        part = torch.zeros(cus * 16896, dtype=torch.uint8, device='cuda')
+        counters = torch.zeros(1024, dtype=torch.int32, device='cuda')
+        out = torch.zeros(cus * 512, dtype=torch.int32, device='cuda')
+        variants = []
+        for splits, nbytes, fenced in ((2, 4224, False), (2, 4224, True), (4, 8448, False), (8, 16896, False),
+                                       (8, 16896, True)):
+            def step(_, splits=splits, nbytes=nbytes, fenced=fenced):
+                ops.ceiling_split_merge(part, counters, out, splits, nbytes, cus, fenced)
+            vms, vper, rot = time_steps(step, 16, steps, warm)
+            torch.cuda.synchronize()
+            cols = [range(t * 16, nbytes, 8192) for t in range(512)]
+            want = torch.tensor([(splits * sum(o + 1 for o in c)) & 0xFFFFFFFF for c in cols], dtype=torch.int64)
+            got = out[:cus // splits * 512].view(cus // splits, 512).cpu().long() & 0xFFFFFFFF
+            assert bool((got == want).all()), f'xt_ceiling_split_merge returned wrong sums ({splits} splits)'
+            assert int(counters.abs().sum()) == 0, 'xt_ceiling_split_merge left arrival counters set'
+            variants.append({'splits': splits, 'bytes_per_workgroup': nbytes, 'fenced': fenced,
+                             'us_per_launch': round(vms * 1e3, 3), 'timing': spread(vper, rot)})
+            log(f'split merge: {splits} splits of {nbytes} B{" fenced" if fenced else ""}: {vms * 1e3:.2f} us per launch')
+            if len(variants) == 1:
+                ms, per = vms, vper
+        config = {'workload': name, 'workgroups': cus, 'threads': 512, 'splits': 2, 'bytes_per_workgroup': 4224}
+        metric = 'split arrival and merge alone (write-through, system-scope count, reload), us per launch'
+    record = {'metric': metric, 'value': round(ms * 1e3, 3), 'unit': 'us', 'n_gpus': 1, 'steps': steps,
+              'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per, rot),
+              'higher_is_better': False, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'u32',
+              'data': 'synthetic', 'config': config, 'roofline': None, 'cpu_baseline': None}
+    if variants:
+        record['variants'] = variants
+    emit(record)
 
 
 def run_ceiling(args, name, ops, workloads):
@@ -953,6 +999,8 @@ def run_ceiling(args, name, ops, workloads):
     torch.cuda.set_device(0)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     steps = max(1, args.steps)
+    if name in ('launch_ceiling', 'split_merge_ceiling'):
+        return run_launch_ceilings(args, name, ops, cus)
     if name == 'mfma_ceiling':
         blocks, iters = 4 * cus, 2000
 
@@ -1025,7 +1073,7 @@ def main():
                         'mla_decode_b64, mla_prefill_2048, mla_v4_decode_b64, the top-k producers '
                         'qsa_logits_352x95088, dsa_logits_4096x16384, topk_352x95088_k2048, '
                         'minimax_decode_scores_b32, minimax_prefill_scores_8k, or the ceilings mfma_ceiling, '
-                        'gather_ceiling_b32 and gather_pieces_ceiling_b32')
+                        'gather_ceiling_b32, gather_pieces_ceiling_b32, launch_ceiling and split_merge_ceiling')
     p.add_argument('--layers', type=int, default=16)
     p.add_argument('--splits', type=int, default=None)
     p.add_argument('--layout', default='interleaved', choices=['interleaved', 'split'],

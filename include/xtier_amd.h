@@ -459,6 +459,19 @@ size_t xt_ceiling_gather_sink_words(int batch, int topk);
 int xt_ceiling_gather_pieces(const void* pool, int64_t pool_records, const int32_t* page_table, int64_t pt_stride,
                              int page_size, int pt_width, const int32_t* indices, int batch, int topk, int kv_heads,
                              int splits, uint32_t* sink, xt_stream_t stream);
+/* xt_ceiling_launch: an empty kernel of `blocks` workgroups of 512 threads: the cost of a launch with no work in it,
+ * the floor under every short kernel of this library (no counterpart in the reference). */
+int xt_ceiling_launch(int blocks, xt_stream_t stream);
+/* xt_ceiling_split_merge: the split arrival of the decode kernels on its own (no counterpart in the reference): groups
+ * of `splits` (2, 4 or 8) consecutive workgroups of 512 threads out of `blocks` (a multiple of splits); each writes
+ * `bytes` (a multiple of 16) of partial into part (blocks * bytes, 16-byte aligned) as 16-byte words {offset, 1, 2, 3},
+ * counts its arrival in counters[group] (int32, zero before the call and again after it), and the last of its group
+ * reloads the group's partials and writes out[group * 512 + t] = splits * (sum of thread t's word offsets + their
+ * number). fenced = 0: the protocol the kernels use (write-through stores, a system-scope count, cache-bypassing
+ * reloads); fenced = 1: plain stores and loads with an agent-scope release fence before every count and an acquire
+ * fence in the last arriver. */
+int xt_ceiling_split_merge(void* part, int bytes, int32_t* counters, uint32_t* out, int splits, int blocks, int fenced,
+                           xt_stream_t stream);
 /* xt_clock_probe: the shader clock, read the way the benchmarks record it beside their rates (no counterpart in the
  * reference): one wavefront runs `iters` dependent FMAs between two reads of the core clock counter (s_memtime) and
  * of the constant 100 MHz clock (s_memrealtime); out[0] = core clock ticks, out[1] = 100 MHz ticks, out[2] = a check

@@ -74,3 +74,13 @@ def test_quantize_and_gather_reject_bad_layouts(lib):
     with pytest.raises(NotImplementedError):
         _lib.check(_decode(lib, dim=512), 'decode')
     assert isinstance(lib.xt_last_error(), bytes) and ctypes.sizeof(ctypes.c_void_p) == 8
+
+
+def test_ceilings_reject_bad_arguments_on_host(lib):
+    assert lib.xt_ceiling_launch(0, None) == _lib.XT_EINVAL
+    merge = lib.xt_ceiling_split_merge
+    assert merge(1 << 20, 4224, 1 << 20, 1 << 20, 3, 255, 0, None) == _lib.XT_EINVAL      # splits 2, 4 or 8
+    assert merge(1 << 20, 4224, 1 << 20, 1 << 20, 2, 255, 0, None) == _lib.XT_EINVAL      # blocks % splits
+    assert merge(1 << 20, 4220, 1 << 20, 1 << 20, 2, 256, 0, None) == _lib.XT_EINVAL      # bytes % 16
+    assert merge(None, 4224, 1 << 20, 1 << 20, 2, 256, 0, None) == _lib.XT_EINVAL
+    assert merge((1 << 20) + 8, 4224, 1 << 20, 1 << 20, 2, 256, 0, None) == _lib.XT_EINVAL   # part alignment

@@ -1,6 +1,7 @@
 """The ceiling kernels the roofline fractions are read against (include/xtier_amd.h xt_ceiling_*): the MFMA loop's
-sums, and that the gather reads exactly the listed records (per-row XOR of every valid record's words, skipped
-positions, table entries and slots included)."""
+sums, that the gather reads exactly the listed records (per-row XOR of every valid record's words, skipped
+positions, table entries and slots included), and that the split-arrival probe merges every group's partials and
+leaves its counters at zero, in both of its forms, on two calls in a row."""
 import numpy as np
 import pytest
 import torch
@@ -72,3 +73,23 @@ def test_gather_pieces_reads_each_units_head_pieces(topk, splits):
             want ^= np.bitwise_xor.reduce(w[32 * head:32 * head + 32]) ^ np.bitwise_xor.reduce(
                 w[128 + 4 * head:128 + 4 * head + 4])
         assert got[g] == want, g
+
+
+@pytest.mark.parametrize('splits,nbytes,fenced', [(2, 4224, False), (2, 4224, True), (4, 8448, False),
+                                                  (8, 16896, False), (8, 16896, True)])
+def test_split_merge_probe_merges_every_group(splits, nbytes, fenced):
+    """The last arriver of each group of `splits` workgroups sums the group's partials (words {offset, 1, 2, 3}):
+    thread t gets splits * sum(offset + 1) over its 16-byte words; the counters are zero again after each call."""
+    blocks = 64 * splits
+    part = torch.zeros(blocks * nbytes, dtype=torch.uint8, device='cuda')
+    counters = torch.zeros(blocks // splits, dtype=torch.int32, device='cuda')
+    out = torch.full((blocks // splits * 512,), -1, dtype=torch.int32, device='cuda')
+    want = np.array([(splits * sum(o + 1 for o in range(t * 16, nbytes, 8192))) & 0xFFFFFFFF for t in range(512)])
+    for _ in range(2):
+        ops.ceiling_split_merge(part, counters, out, splits, nbytes, blocks, fenced)
+        torch.cuda.synchronize()
+        got = out.view(-1, 512).cpu().numpy().astype(np.int64) & 0xFFFFFFFF
+        assert (got == want[None, :]).all()
+        assert int(counters.abs().sum()) == 0
+    ops.ceiling_launch(256)
+    torch.cuda.synchronize()

@@ -7,6 +7,9 @@
 //           no dequantization or math: the bytes arrive and are folded into one word per thread. Two forms: whole
 //           records per workgroup, and the decode's own decomposition (one KV head's pieces of each record per
 //           workgroup, key splits, slices of 8 wavefronts, four steps of loads in flight).
+//   Launch: an empty kernel, the floor under every short kernel; and the split arrival of the decode kernels on its
+//           own (partials written through, the count, the last arriver's reload and merge), with the fenced form
+//           beside it.
 #include "xt_common.h"
 #include "xt_host.h"
 
@@ -155,6 +158,71 @@ __global__ __launch_bounds__(512) void gather_pieces_kernel(const uint8_t* pool,
   sink[(int64_t)g * 512 + threadIdx.x] = acc;
 }
 
+// An empty kernel: what a launch costs with no work in it (dispatch, wave launch, completion).
+__global__ __launch_bounds__(512) void launch_ceiling_kernel() {}
+
+// The split arrival of the decode kernels on its own, with their helpers (store_partial, arrive_last, load_partial):
+// groups of S consecutive workgroups of 512 threads; each writes `bytes` of partial (16-byte words {offset, 1, 2, 3})
+// written through, counts its arrival, and the last of its group reloads the group's S partials and sums them into
+// one word per thread: out[group * 512 + t] = S * (sum of its word offsets + its word count). FENCED: the form with
+// plain stores, an agent-scope release fence before every count and an acquire fence in the last arriver, then plain
+// loads (the fences write back / invalidate the L2 instead of bypassing it per access).
+template <int S, bool FENCED>
+__global__ __launch_bounds__(512) void split_merge_kernel(uint8_t* part, int bytes, int32_t* counters, uint32_t* out) {
+  const int grp = blockIdx.x / S;
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(part + (int64_t)grp * S * bytes, (short)0, S * bytes, 0x00020000);
+  const int mine = (blockIdx.x % S) * bytes;
+  for (int o = threadIdx.x * 16; o < bytes; o += 512 * 16) {
+    const float4_t v = {__uint_as_float((uint32_t)o), __uint_as_float(1u), __uint_as_float(2u), __uint_as_float(3u)};
+    if (FENCED)
+      __builtin_amdgcn_raw_buffer_store_b128(
+          xt_u32x4_t{(uint32_t)o, 1u, 2u, 3u}, r, mine + o, 0, 0);
+    else
+      store_partial(r, mine + o, v);
+  }
+  __shared__ int flag;
+  bool last;
+  if (FENCED) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      flag = __hip_atomic_fetch_add(counters + grp, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+      if (flag) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    __syncthreads();
+    last = flag;
+  } else {
+    last = arrive_last(counters + grp, S, &flag);
+  }
+  if (!last) return;
+  uint32_t sum0 = 0, sum1 = 0;
+  for (int o = threadIdx.x * 16; o < bytes; o += 512 * 16) {
+    xt_u32x4_t w[S];
+#pragma unroll
+    for (int k = 0; k < S; ++k) {
+      if (FENCED) {
+        w[k] = __builtin_amdgcn_raw_buffer_load_b128(r, k * bytes + o, 0, 0);
+      } else {
+        const float4_t f = load_partial(r, k * bytes + o);
+        w[k] = xt_u32x4_t{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3])};
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < S; ++k) {
+      sum0 += w[k][0];
+      sum1 += w[k][1];
+    }
+  }
+  out[grp * 512 + threadIdx.x] = sum0 + sum1;
+  if (FENCED) {
+    if (threadIdx.x == 0) __hip_atomic_store(counters + grp, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    reset_counter(counters + grp);
+  }
+}
+
 // One wavefront: `iters` dependent FMAs between two reads of the core clock counter and the 100 MHz constant clock.
 __global__ __launch_bounds__(64) void clock_probe_kernel(uint64_t* out, int iters) {
   const uint64_t c0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
@@ -178,6 +246,39 @@ extern "C" int xt_clock_probe(uint64_t* out, int iters, xt_stream_t stream) {
   const char* what = "xt_clock_probe";
   if (!out || iters <= 0 || iters > (1 << 24)) return fail(XT_EINVAL, "%s: out must be given, iters in 1..2^24", what);
   hipLaunchKernelGGL(clock_probe_kernel, dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), out, iters);
+  return check_launch(what);
+}
+
+extern "C" int xt_ceiling_launch(int blocks, xt_stream_t stream) {
+  const char* what = "xt_ceiling_launch";
+  if (blocks <= 0 || blocks > (1 << 20)) return fail(XT_EINVAL, "%s: blocks in 1..2^20", what);
+  hipLaunchKernelGGL(launch_ceiling_kernel, dim3((unsigned)blocks), dim3(512), 0, reinterpret_cast<hipStream_t>(stream));
+  return check_launch(what);
+}
+
+template <int S>
+static void launch_split_merge(int fenced, uint8_t* p, int bytes, int32_t* counters, uint32_t* out, int blocks,
+                               hipStream_t st) {
+  if (fenced)
+    hipLaunchKernelGGL((split_merge_kernel<S, true>), dim3((unsigned)blocks), dim3(512), 0, st, p, bytes, counters, out);
+  else
+    hipLaunchKernelGGL((split_merge_kernel<S, false>), dim3((unsigned)blocks), dim3(512), 0, st, p, bytes, counters,
+                       out);
+}
+
+extern "C" int xt_ceiling_split_merge(void* part, int bytes, int32_t* counters, uint32_t* out, int splits, int blocks,
+                                      int fenced, xt_stream_t stream) {
+  const char* what = "xt_ceiling_split_merge";
+  if (!part || !counters || !out) return fail(XT_EINVAL, "%s: a required pointer is null", what);
+  if ((splits != 2 && splits != 4 && splits != 8) || blocks <= 0 || blocks % splits || blocks > (1 << 16))
+    return fail(XT_EINVAL, "%s: splits 2, 4 or 8; blocks a multiple of splits up to 2^16", what);
+  if (bytes <= 0 || bytes % 16 || (int64_t)bytes * splits > (1 << 24) || !aligned(part, 16) || !aligned(counters, 4))
+    return fail(XT_EINVAL, "%s: bytes a multiple of 16 with bytes * splits up to 2^24; 16-byte aligned part", what);
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  uint8_t* p = static_cast<uint8_t*>(part);
+  if (splits == 2) launch_split_merge<2>(fenced, p, bytes, counters, out, blocks, st);
+  else if (splits == 4) launch_split_merge<4>(fenced, p, bytes, counters, out, blocks, st);
+  else launch_split_merge<8>(fenced, p, bytes, counters, out, blocks, st);
   return check_launch(what);
 }
 

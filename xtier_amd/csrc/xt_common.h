@@ -16,6 +16,7 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef short short2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t xt_u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -140,7 +141,6 @@ __device__ inline float2_t pow2_query_scale(float qmax) {
 //      (missing L1 and any L2 copy, so the reads come from memory), issued after the count returned.
 // Every partial a last arriver reads was therefore complete in memory before its count, and the count is what the
 // last arriver waited for. The last arriver resets the counter (a system-scope store) for the next call.
-typedef uint32_t xt_u32x4_t __attribute__((ext_vector_type(4)));
 __device__ inline void store_partial(__amdgpu_buffer_rsrc_t r, int byte_off, float4_t v) {
   const xt_u32x4_t w = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
   __builtin_amdgcn_raw_buffer_store_b128(w, r, byte_off, 0, 16 /* sc1 */);

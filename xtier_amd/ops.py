@@ -804,6 +804,24 @@ def ceiling_gather_pieces(pool, page_table, indices, page_size, splits=2, sink=N
     return sink
 
 
+def ceiling_launch(blocks=256, device='cuda'):
+    """An empty kernel of `blocks` workgroups of 512 threads (xt_ceiling_launch): the cost of a launch alone."""
+    dev = torch.device(device)
+    _lib.check(_lib.lib().xt_ceiling_launch(int(blocks), torch.cuda.current_stream(dev).cuda_stream),
+               'ceiling_launch')
+
+
+def ceiling_split_merge(part, counters, out, splits, bytes_per_split, blocks, fenced=False):
+    """The decode kernels' split arrival alone (xt_ceiling_split_merge): part uint8 >= blocks * bytes_per_split,
+    counters int32 >= blocks / splits (zero before and after), out int32 >= blocks / splits * 512 (the merged sums)."""
+    if part.numel() < blocks * bytes_per_split or counters.numel() < blocks // max(1, splits) or \
+            out.numel() < blocks // max(1, splits) * 512:
+        raise ValueError('xtier_amd.ceiling_split_merge: buffers too small')
+    _lib.check(_lib.lib().xt_ceiling_split_merge(_ptr(part), int(bytes_per_split), _ptr(counters), _ptr(out),
+                                                 int(splits), int(blocks), int(bool(fenced)), _stream(part)),
+               'ceiling_split_merge')
+
+
 def topk_rows(x, topk, out=None):
     """xt_topk_rows: x FP32 [rows, cols] (unit column stride) -> int32 [rows, topk]: per row the positions of the topk
     largest finite values, ascending, ties toward the lower position, -1 padded."""
