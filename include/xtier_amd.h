@@ -161,9 +161,9 @@ size_t xt_sparse_decode_workspace_bytes(int rows, int q_heads, int dim, int spli
  * 256-byte aligned. With splits > 1 it holds a fixed 64 KB region of arrival counters (one per row and KV head group,
  * rows * kv_heads <= 16384) followed by the split partials: zero-filled before its first use, the counters are left
  * zero by every call, so calls of any shape (and sparse MLA calls) may share one workspace; calls that overlap in time
- * need separate workspaces. One launch on `stream`; a workgroup
- * handles 4 KV heads (many rows) or 1 KV head (few rows) of one (row, key split), and with splits > 1 the last
- * workgroup of each (row, head group) to finish merges the split partials. */
+ * need separate workspaces. One launch on `stream`; a workgroup handles 4 KV heads of one (row, key split) when
+ * rows * kv_heads / 4 * splits fills every CU, else 2 when rows * kv_heads / 2 * splits does, else 1, and with
+ * splits > 1 the last workgroup of each (row, head group) to finish merges the split partials. */
 int xt_sparse_decode_nvfp4(const void* q, int64_t q_row_stride, int64_t q_head_stride, const uint8_t* k_pay,
                            const uint8_t* v_pay, const uint8_t* k_scales, const uint8_t* v_scales, const float* gk,
                            const float* gv, int64_t pool_slots, int64_t pay_stride, int64_t sf_stride,
