@@ -713,8 +713,6 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
 
 using namespace xt;
 
-// Workgroup shape: 4 KV heads per workgroup when that alone yields a full launch (one workgroup per CU), else 1 KV
-// head (more, smaller workgroups: a (row, head) merges its slices in LDS instead of through partials).
 // KV heads per workgroup: 4 when that alone fills every CU, else 2 when that does, else 1 (more, smaller workgroups).
 // A pair of heads reads each key's K and V payload pieces of both heads together (whole 128-byte lines on SGLang's
 // split pool). Measured, batch 32 x 4 KV heads, top-2048: 2 heads x 4 splits 18.7 us (split pool 20.8 us) against
