@@ -308,8 +308,10 @@ size_t xt_sparse_mla_workspace_bytes(int rows, int heads, int splits);
  * lse (optional FP32 [rows, heads]): natural log of sum_k exp(s_k) over the keys only (sparse_mla.py:73-85); a row
  * without valid keys writes zeros and lse -inf. latent_dim 512, rope_dim 64, heads <= 128 are supported. The FP16
  * operands are exact: e2m1 * e4m3 latents and each head's query as q * 2^-e (2^e from its largest magnitude, so any
- * finite BF16 query fits); g multiplies the latent part of the FP32 scores and the probabilities of the values.
- * splits: key splits per row (1..64); with splits > 1 a second launch on `stream` merges the split partials.
+ * finite BF16 query fits); g multiplies the latent part of the FP32 scores and the normalized output (with two
+ * caches the probabilities carry each key's g relative to the larger of the two).
+ * splits: key splits per row (1..64); with splits > 1 a second launch on `stream` merges the split partials, which
+ * are FP16 outputs normalized per split: latents must stay below 65504 in magnitude (FP16's range) there.
  * workspace: xt_sparse_mla_workspace_bytes bytes, 256-byte aligned; its first 64 KB are left untouched (the counter
  * region of the decode entry points), so one zero-filled workspace may serve decode and MLA calls of any shape, one at
  * a time. */
