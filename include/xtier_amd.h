@@ -310,8 +310,8 @@ size_t xt_sparse_mla_workspace_bytes(int rows, int heads, int splits);
  * operands are exact: e2m1 * e4m3 latents and each head's query as q * 2^-e (2^e from its largest magnitude, so any
  * finite BF16 query fits); g multiplies the latent part of the FP32 scores and the normalized output (with two
  * caches the probabilities carry each key's g relative to the larger of the two).
- * splits: key splits per row (1..64); with splits > 1 a second launch on `stream` merges the split partials, which
- * are FP16 outputs normalized per split: latents must stay below 65504 in magnitude (FP16's range) there.
+ * splits: key splits per row (1..64); with splits > 1 a second launch on `stream` merges the split partials (FP16
+ * outputs normalized per split before the global scale, so within FP16's range for any g).
  * workspace: xt_sparse_mla_workspace_bytes bytes, 256-byte aligned; its first 64 KB are left untouched (the counter
  * region of the decode entry points), so one zero-filled workspace may serve decode and MLA calls of any shape, one at
  * a time. */

@@ -7,8 +7,8 @@
 //     512 wide, value = the key; operands BF16 as in the reference, the scale applied to the FP32 scores.
 // q.k and p.v on MFMA (v_mfma_f32_16x16x32_f16 / _bf16), online softmax in the exp2 domain, an optional per-head sink
 // in the denominator. With key splits, each (row, split) writes its output normalized by its own sum (FP16 for the
-// NVFP4 latent: a convex combination of the cache's values, so within its largest magnitude 2688 g, which FP16 holds
-// for latents below 65504; FP32 for V4) with its max and sum, and a second, wide launch merges the splits:
+// NVFP4 latent, before the global scale: a convex combination of e2m1 * e4m3 values, at most 2688 in magnitude; FP32
+// for V4) with its max and sum, and a second, wide launch merges the splits and applies the global scale:
 // one merging workgroup per row would read a row's partials at one CU's bandwidth.
 //
 // Work decomposition: a workgroup = 8 wavefronts x 16 heads = 128 heads of one (query row, key split), so every key is
@@ -521,11 +521,11 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
       a.lse[row * a.heads + head] = l_tot > 0.0f ? (m + __builtin_log2f(l_tot)) * kLn2 : -__builtin_inff();
     return;
   }
-  // 2. the split's output normalized by its own sum (NVFP4: FP16, a convex combination of latent values; V4:
-  //    FP32) plus its max and sum; a second launch merges the splits. The partials are stored in the accumulators'
+  // 2. the split's output normalized by its own sum (NVFP4: FP16, a convex combination of e2m1 * e4m3 values, so at
+  //    most 2688 in magnitude whatever g; V4: FP32) plus its max and sum; a second launch merges the splits. The partials are stored in the accumulators'
   //    lane order (part_index), so every store of a wave writes one contiguous run.
   if (16 * wave >= a.heads) return;   // a wave without live heads has no partials (heads pad to whole waves only)
-  const float inv = l_tot > 0.0f ? (TWO ? fmaxf(g0, g1) : g0) / l_tot : 0.0f;
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;   // NVFP4: without g (the merge applies it)
   const int64_t pbase = part_index(a, row, split, wave, 0, lane);
   if constexpr (F == kNvfp4) {
     uint16_t* pp = static_cast<uint16_t*>(a.part) + pbase;
@@ -619,7 +619,9 @@ __global__ void __launch_bounds__(256) mla_merge_kernel(const MlaArgs a, int row
   const float mu = (m_run == -__builtin_inff()) ? 0.0f : m_run;
   float total = l_run;
   if (a.sink) total += __builtin_amdgcn_exp2f(a.sink[hc] * kLog2e - mu);
-  const float inv = l_run > 0.0f ? 1.0f / total : 0.0f;
+  // NVFP4: the partials are without g; it is max(g0, g1) (c[1] is c[0] with one cache), as in the one-split output
+  const float gout = F == kNvfp4 ? fmaxf(*a.c[0].g, *a.c[1].g) : 1.0f;
+  const float inv = l_run > 0.0f ? gout / total : 0.0f;
   uint32_t pk[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
