@@ -108,6 +108,25 @@ def test_mla_query_magnitudes(mag):
     assert (np.abs(got - ref_lse) <= 2e-3 + 1e-6 * np.abs(ref_lse)).all()
 
 
+def test_mla_rope_beyond_fp16_range():
+    """Rope values of ~1e5 (beyond FP16's range; BF16 holds them) against a rope query scaled by 1e-5: the rope
+    chunks run the BF16 MFMA on the cache's own BF16 values, so the scores stay finite and exact in their products."""
+    w, inp = _case(13, rows=4)
+    gen = workloads.generator('cuda', 6)
+    lat, rope = workloads.mla_cache_rows(w, gen, 'cuda', 0, w.slots)
+    rope = (rope.float() * 1e5).to(torch.bfloat16)
+    pool = LatentPool(w.slots, w.latent, w.rope, 'cuda')
+    pool.set_global_scale(lat)
+    pool.append(lat, rope, torch.arange(w.slots, device='cuda'), saturate=False)
+    q = inp.q.float()
+    q[:, :, w.latent:] *= 1e-5
+    q = q.to(torch.bfloat16)
+    scale = 1 / math.sqrt(576)
+    out, lse = ops.sparse_mla(q[:, None], pool, inp.slots[:, None], None, None, scale, splits=2)
+    ref, ref_lse = _ref(q, pool, inp.slots, None, None, scale)
+    _check(out, lse, ref, ref_lse, bf16_slack=True)
+
+
 def test_mla_two_lists_empty_and_single_key_rows():
     """A window list in one cache followed by compressed keys in another (sparse_mla.py:109-118); row 0 has no valid
     key in either list (zeros, LSE -inf), row 1 a single key (its latent, rounded once to FP16 then BF16)."""

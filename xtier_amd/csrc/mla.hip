@@ -1,8 +1,9 @@
 // Sparse MLA: 128 query heads share one key per token. Two cache formats:
 //   NVFP4 latent (kNvfp4): key = [latent (512, NVFP4 with E4M3 block scales and a global scale) | rope (64, BF16)],
-//     576 wide, value = the latent; operands FP16: the query as q * 2^-e per head (exact), the key tile as e2m1 * e4m3
-//     (exact), the global scale applied to the FP32 latent scores and to the values on the normalized output (with
-//     two caches, P carries each key's g relative to the larger of the two);
+//     576 wide, value = the latent; operands FP16 for the latent (the query as q * 2^-e per head, the key tile as
+//     e2m1 * e4m3, both exact) and BF16 for the rope (the cache's values and q * 2^-e, exact), the global scale
+//     applied to the FP32 latent scores and to the values on the normalized output (with two caches, P carries each
+//     key's g relative to the larger of the two);
 //   DeepSeek V4 FP8 pages (kFp8V4, sparse_mla.py:38-59): key = [448 E4M3 values x UE8M0 scale per 64 | 64 BF16 rope],
 //     512 wide, value = the key; operands BF16 as in the reference, the scale applied to the FP32 scores.
 // q.k and p.v on MFMA (v_mfma_f32_16x16x32_f16 / _bf16), online softmax in the exp2 domain, an optional per-head sink
@@ -26,7 +27,8 @@
 //       T(j)); C = O^T, lane (head hl, dims 4j .. 4j+3 of the tile).
 //
 // Numerics: NVFP4: e2m1 * e4m3 is exact in FP16 (at most 6 significant bits), and so is the query scaled by a power of
-// two; the latent and rope parts of a score accumulate apart, and score = (latent . q * g + rope . q) * scale *
+// two; the rope chunks multiply BF16 values (the cache's rope and q * 2^-e) exactly in the BF16 MFMA; the latent and
+// rope parts of a score accumulate apart, and score = (latent . q * g + rope . q) * scale *
 // log2(e) * 2^e in FP32 (g of the key's cache); P is FP16 of p (of p * g / max(g0, g1) with two caches), the sum takes
 // p, and the normalization multiplies by g (by max(g0, g1)). V4: e4m3 * 2^(e - 127) is exact in BF16 (4 significant
 // bits) for scales from 2^-126; a zero scale byte (2^-127) reads as 0; P is BF16. The running maximum is raised lazily
@@ -59,6 +61,9 @@ template <int F>
 constexpr int kQChunks = kDk<F> / 32;    // 32-dim chunks of a query row
 template <int F>
 constexpr int kQReg = F == kNvfp4 ? 9 : 7;     // chunks kept in registers; the others live in LDS
+template <int F>
+constexpr int kLatChunks = F == kNvfp4 ? kDl / 32 : kQChunks<F>;   // NVFP4: chunks of the latent (FP16 MFMA); the
+                                                                   // rope chunks after them run BF16
 constexpr int kQRow = 32;                // 16-bit values per (chunk, head) row of the LDS query block; the four 16-byte
                                          // pieces of row r sit at piece ^ ((r >> 1) & 3), which measures free of bank
                                          // conflicts for the b128 reads of 16 rows x 4 pieces
@@ -258,19 +263,8 @@ __device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step,
     *reinterpret_cast<half8_t*>(kt + (4 * kq + i) * kKRow<F> + 8 * c) =
         half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
   }
-  if (t < 256) {
-    const int key = t >> 3, p = t & 7;
-    const uint32_t w[4] = {r.rope.x, r.rope.y, r.rope.z, r.rope.w};
-    half8_t hv;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {   // BF16 -> FP16 is exact in range, so round-toward-zero packing is exact
-      const half2_t pr = __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(w[e] << 16),
-                                                                                __uint_as_float(w[e] & 0xFFFF0000u)));
-      hv[2 * e] = pr.x;
-      hv[2 * e + 1] = pr.y;
-    }
-    *reinterpret_cast<half8_t*>(kt + key * kKRow<F> + kDl + 8 * p) = hv;
-  }
+  if (t < 256)   // the rope stays BF16: its chunks run the BF16 MFMA, with no range or precision loss
+    *reinterpret_cast<uint4*>(kt + (t >> 3) * kKRow<F> + kDl + 8 * (t & 7)) = r.rope;
   }
 }
 
@@ -297,7 +291,7 @@ __device__ inline int64_t part_index(const MlaArgs& a, int64_t row, int split, i
 
 template <int F, bool TWO>
 __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
-  constexpr int kQC = kQChunks<F>, kQR = kQReg<F>;
+  constexpr int kQC = kQChunks<F>, kQR = kQReg<F>, kLatC = kLatChunks<F>;
   extern __shared__ __align__(16) uint8_t lds[];
   asm volatile("" ::"s"(a.xcd_units), "s"(a.xcd_extra), "s"(a.splits), "s"(a.keys_per_split), "s"(a.topk[0]),
                "s"(a.topk[1]), "s"(a.idx[0]), "s"(a.idx[1]), "s"(a.idx_stride[0]), "s"(a.idx_stride[1]),
@@ -374,7 +368,16 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
 #pragma unroll
   for (int kk = 0; kk < kQC; ++kk) {
     short8_t h;
-    if constexpr (F == kNvfp4) {
+    if (F == kNvfp4 && kk >= kLatC) {   // rope chunks: BF16 of q * 2^-e, exact (a power of two), for the BF16 MFMA
+      const uint32_t ws[4] = {qraw[kk].x, qraw[kk].y, qraw[kk].z, qraw[kk].w};
+      uint32_t b[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        b[e] = head_live ? ((__float_as_uint(bf16_bits_to_f32(ws[e] & 0xFFFFu) * qdown) >> 16) |
+                            (__float_as_uint(bf16_bits_to_f32(ws[e] >> 16) * qdown) & 0xFFFF0000u))
+                         : 0u;
+      h = __builtin_bit_cast(short8_t, uint4{b[0], b[1], b[2], b[3]});
+    } else if constexpr (F == kNvfp4) {
       const uint32_t ws[4] = {qraw[kk].x, qraw[kk].y, qraw[kk].z, qraw[kk].w};
       half8_t hh;
 #pragma unroll
@@ -429,7 +432,6 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
     // NVFP4: the global scale of each of those keys (of its cache; two caches may differ). Chunks below kLatC are the
     // latent's: once they are summed, the accumulators are multiplied by the key's global scale, and the rope chunks
     // (no global scale) add onto them.
-    constexpr int kLatC = F == kNvfp4 ? kDl / 32 : kQC;
     uint32_t l1 = 0u;   // bit e: key e of T(j) is cache 1's
     if constexpr (F == kNvfp4 && TWO) {
       const uint32_t b =
@@ -457,7 +459,8 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
         for (int e = 0; e < 8; ++e) s[e >> 2][e & 3] *= ((l1 >> e) & 1u) ? g1 : g0;
       }
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) s[tt] = mfma16<F>(kf[kk][tt], qf[kk], s[tt]);
+      for (int tt = 0; tt < 2; ++tt)
+        s[tt] = kk >= kLatC ? mfma16<kFp8V4>(kf[kk][tt], qf[kk], s[tt]) : mfma16<F>(kf[kk][tt], qf[kk], s[tt]);
       __builtin_amdgcn_sched_barrier(0);
     }
     float sv[8];
