@@ -616,8 +616,19 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
       row_part, (short)0, a.splits > 1 ? (int)((int64_t)a.splits * a.q_heads * G::kPartStride * 4) : 0, 0x00020000);
   const float gv = gv_v;
   constexpr int kParts = 8 * G::kNT;   // 4-dim pieces per lane
+  constexpr int kUnits = (HPW * 64 * kParts + kThreads - 1) / kThreads;   // pieces per thread
+  // with key splits and at most two pieces per thread, each thread keeps its pieces' merged (output, max, sum) for
+  // the split merge below (with more, the registers would spill: the merge reloads its own split too)
+  constexpr bool kKeep = kUnits <= 2;
+  float4_t keep_o[kUnits];
+  float keep_m[kUnits], keep_l[kUnits];
 #pragma unroll
-  for (int u = (int)threadIdx.x; u < HPW * 64 * kParts; u += kThreads) {
+  for (int k = 0; k < kUnits; ++k) {
+    const int u = (int)threadIdx.x + k * kThreads;
+    keep_m[k] = -__builtin_inff();
+    keep_l[k] = 0.0f;
+    keep_o[k] = float4_t{0.f, 0.f, 0.f, 0.f};
+    if (u >= HPW * 64 * kParts) continue;
     const int part = u % kParts, ln = (u / kParts) & 63, hw = u / (kParts * 64);   // piece part of lane ln, KV head hw
     const int uh = ln & 15, uj = ln >> 4;
     const int ukvh = kvg * HPW + hw;
@@ -654,56 +665,95 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
       const int at = ((split * a.q_heads + head) * G::kPartStride) * 4;
       store_partial(pr, at + d0 * 4, o);
       if (d0 == 0) store_partial(pr, at + D * 4, float4_t{mx, l, 0.0f, 0.0f});
+      if constexpr (kKeep) {
+        keep_m[k] = mx;
+        keep_l[k] = l;
+        keep_o[k] = o;
+      }
     }
   }
   if (a.splits == 1) return;
-  // the last workgroup of (row, KV group) to arrive merges the partials (the split arrival of xt_common.h)
+  // the last workgroup of (row, KV group) to arrive merges the partials (the split arrival of xt_common.h): each
+  // thread merges the same pieces it wrote, in split order whichever workgroup arrives last (so the result does not
+  // depend on the order of arrival), its own split's from registers and the others' loaded, four splits at a time
+  // with their loads issued together (its own split and splits past the last read nothing: an offset past the buffer
+  // reads zeros)
   __shared__ int s_last;
   int32_t* counter = a.counters + (int64_t)row * a.kv_groups + kvg;
   if (!arrive_last(counter, a.splits, &s_last)) return;
-  // all threads, 8 consecutive outputs each: head h0 + o / D, d0 = o % D; loads of 8 splits at a time together
-  const int h0 = kvg * HPW * a.group;
-  const int nh = min(HPW * a.group, a.q_heads - h0);
-  for (int o = threadIdx.x * 8; o < nh * D; o += blockDim.x * 8) {
-    const int hh = h0 + o / D, d0 = o % D;
-    float m_run = -__builtin_inff(), l_run = 0.0f;
-    float4_t o0 = float4_t{0.f, 0.f, 0.f, 0.f}, o1 = o0;
-    for (int s0 = 0; s0 < a.splits; s0 += 8) {
-      float4_t ml[8], x0[8], x1[8];
+  int heads_k[kUnits], d0s[kUnits];
+  bool live_k[kUnits];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {   // past the last split: reload the last one, weight 0 below
-        const int at = (min(s0 + i, a.splits - 1) * a.q_heads + hh) * G::kPartStride * 4;
-        ml[i] = load_partial(pr, at + D * 4);
-        x0[i] = load_partial(pr, at + d0 * 4);
-        x1[i] = load_partial(pr, at + d0 * 4 + 16);
-      }
+  for (int k = 0; k < kUnits; ++k) {
+    const int u = (int)threadIdx.x + k * kThreads;
+    const int part = u % kParts, ln = (u / kParts) & 63, hw = u / (kParts * 64);
+    const int uh = ln & 15, uj = ln >> 4;
+    const int ukvh = kvg * HPW + hw;
+    live_k[k] = u < HPW * 64 * kParts && ukvh < a.kv_heads && uh < a.group && !(D == 64 && uj >= 2);
+    heads_k[k] = min(ukvh, a.kv_heads - 1) * a.group + min(uh, a.group - 1);
+    d0s[k] = 128 * (part >> 3) + 32 * uj + 4 * (part & 7);
+  }
+  // up to two pieces at a time: their loads of four splits (16 x 16 bytes) go out together
+  constexpr int kBatch = kUnits < 2 ? kUnits : 2;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if (s0 + i >= a.splits) ml[i][0] = -__builtin_inff();
-      float mc = m_run;
+  for (int kb = 0; kb < kUnits; kb += kBatch) {
+    float m_run[kBatch], l_run[kBatch];
+    float4_t o[kBatch];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) mc = fmaxf(mc, ml[i][0]);
-      const float mu = (mc == -__builtin_inff()) ? 0.0f : mc;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - mu);
-      l_run *= alpha;
-      o0 *= alpha;
-      o1 *= alpha;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float wgt = __builtin_amdgcn_exp2f(ml[i][0] - mu);
-        l_run += wgt * ml[i][1];
-        o0 += wgt * x0[i];
-        o1 += wgt * x1[i];
-      }
-      m_run = mc;
+    for (int b = 0; b < kBatch; ++b) {
+      m_run[b] = -__builtin_inff();
+      l_run[b] = 0.0f;
+      o[b] = float4_t{0.f, 0.f, 0.f, 0.f};
     }
-    const float inv = l_run > 0.0f ? gv / l_run : 0.0f;
-    const float v[8] = {o0[0] * inv, o0[1] * inv, o0[2] * inv, o0[3] * inv,
-                        o1[0] * inv, o1[1] * inv, o1[2] * inv, o1[3] * inv};
-    store_out(a, row, hh, d0, v, 8);
-    if (a.lse && d0 == 0)
-      a.lse[(int64_t)row * a.q_heads + hh] =
-          l_run > 0.0f ? (m_run + __builtin_log2f(l_run)) * kLn2 : -__builtin_inff();
+    for (int s0 = 0; s0 < a.splits; s0 += 4) {
+      float4_t ml[kBatch][4], x[kBatch][4];
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool other = live_k[kb + b] && s0 + i < a.splits && (!kKeep || s0 + i != split);
+          const int at = other ? ((s0 + i) * a.q_heads + heads_k[kb + b]) * G::kPartStride * 4 : 0x7FFF0000;
+          ml[b][i] = load_partial(pr, at + D * 4);
+          x[b][i] = load_partial(pr, at + d0s[kb + b] * 4);
+        }
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        float mc = m_run[b];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (kKeep && s0 + i == split) {
+            ml[b][i][0] = keep_m[kb + b];
+            ml[b][i][1] = keep_l[kb + b];
+            x[b][i] = keep_o[kb + b];
+          } else if (s0 + i >= a.splits) {
+            ml[b][i][0] = -__builtin_inff();
+          }
+          mc = fmaxf(mc, ml[b][i][0]);
+        }
+        const float mu = (mc == -__builtin_inff()) ? 0.0f : mc;
+        const float alpha = __builtin_amdgcn_exp2f(m_run[b] - mu);
+        l_run[b] *= alpha;
+        o[b] *= alpha;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float wgt = __builtin_amdgcn_exp2f(ml[b][i][0] - mu);
+          l_run[b] += wgt * ml[b][i][1];
+          o[b] += wgt * x[b][i];
+        }
+        m_run[b] = mc;
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int k = kb + b;
+      if (!live_k[k]) continue;
+      const float inv = l_run[b] > 0.0f ? gv / l_run[b] : 0.0f;
+      const float v[4] = {o[b][0] * inv, o[b][1] * inv, o[b][2] * inv, o[b][3] * inv};
+      store_out(a, row, heads_k[k], d0s[k], v, 4);
+      if (a.lse && d0s[k] == 0)
+        a.lse[(int64_t)row * a.q_heads + heads_k[k]] =
+            l_run[b] > 0.0f ? (m_run[b] + __builtin_log2f(l_run[b])) * kLn2 : -__builtin_inff();
+    }
   }
   reset_counter(counter);
 }
