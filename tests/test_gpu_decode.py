@@ -320,24 +320,33 @@ def test_decode_past_one_round_of_workgroups(batch, splits):
 @pytest.mark.parametrize('splits', [4, 5])
 def test_decode_two_kv_heads_per_workgroup(splits):
     """32 rows x 4 KV heads with 4 or 5 key splits fill the CUs with workgroups of 2 KV heads (8 waves at 256
-    workgroups, 4 at 320): every row against the oracle on SGLang's split pool, and the interleaved pool's bits equal
-    to the split pool's."""
+    workgroups, 4 at 320), with -1 holes, a short row, a short and an empty key list and a causal limit: every row
+    against the oracle on SGLang's split pool, and the interleaved pool's bits equal to the split pool's."""
     pool, pt, idx, q = _small_case(seed=50 + splits, batch=32)
     idx = idx.numpy().copy()
     idx[3, ::5] = -1
     seq = np.full(32, 3008, np.int32)
     seq[7] = 900
+    counts = np.full(32, idx.shape[1], np.int32)
+    counts[11] = 150                      # a short list: its last splits hold no key
+    counts[12] = 0                        # no key at all: zeros, LSE -inf
+    qpos = np.full(32, 1 << 30, np.int32)
+    qpos[13] = 1200                       # a causal limit
     scale = 128 ** -0.5
     lse = torch.empty(32, 32, dtype=torch.float32, device='cuda')
     out = ops.sparse_decode(q.cuda(), pool.raw, pt.cuda(), _dev(idx), _dev(seq), scale, page_size=64, lse=lse,
-                            splits=splits)
-    ref, flash, lse_ref = _oracle(pool.raw, bf16_numpy(q), pt.numpy(), 64, np.arange(32), idx, None, seq, scale)
-    _check(out, ref, flash)
-    assert np.abs(lse.cpu().numpy() - lse_ref).max() < 2e-3
+                            counts=_dev(counts), query_pos=_dev(qpos), splits=splits)
+    ref, flash, lse_ref = _oracle(pool.raw, bf16_numpy(q), pt.numpy(), 64, np.arange(32), idx, counts, seq, scale,
+                                  qpos)
+    live = np.arange(32) != 12
+    _check(out, ref, flash, nonempty=live)
+    assert not out[12].any() and torch.isneginf(lse[12]).all()
+    assert np.abs(lse.cpu().numpy()[live] - lse_ref[live]).max() < 2e-3
     il = KVPool(pool.raw[0].shape[0], 4, 128, layout='interleaved', gk=pool.raw[4].clone(), gv=pool.raw[5].clone())
     for dst, src in zip((il.k_pay, il.v_pay, il.k_sf, il.v_sf), pool.raw[:4]):
         dst.copy_(src)
-    out2 = ops.sparse_decode(q.cuda(), il.raw, pt.cuda(), _dev(idx), _dev(seq), scale, page_size=64, splits=splits)
+    out2 = ops.sparse_decode(q.cuda(), il.raw, pt.cuda(), _dev(idx), _dev(seq), scale, page_size=64,
+                             counts=_dev(counts), query_pos=_dev(qpos), splits=splits)
     assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
 
 
