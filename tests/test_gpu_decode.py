@@ -350,6 +350,37 @@ def test_decode_two_kv_heads_per_workgroup(splits):
     assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
 
 
+@pytest.mark.parametrize('splits', [4, 5])
+def test_decode_nan_scales_stay_in_their_head(splits):
+    """A NaN E4M3 scale byte (0x7F / 0xFF) in a live key's row reaches exactly the outputs the oracle makes NaN: a K
+    scale the whole of its KV head's query heads, a V scale the 16 dims of its block in those heads, in every row
+    that reads the key. With 4 splits one wave covers the two KV heads of a pair (its zero blocks must not carry the
+    NaN to the other head), with 5 one wave per KV head; on both pool layouts."""
+    pool, pt, idx, q = _small_case(seed=71, batch=32)
+    idx = idx.numpy()
+    seq = np.full(32, 3008, np.int32)
+    table = pt.numpy()
+    slot = lambda r, c: int(attention.slots_of(table, r, idx[r, c:c + 1], 64)[0])
+    k_sf, v_sf = pool.raw[2], pool.raw[3]      # [slots, 4 heads, 8 blocks]
+    k_sf[slot(5, 17), 1, 3] = 0x7F             # K scale, KV head 1: query heads 8..15 of the rows reading it
+    v_sf[slot(9, 300), 2, 5] = 0xFF            # V scale, KV head 2, dims 80..95 of query heads 16..23
+    k_sf[slot(20, 611), 0, 0] = 0xFF           # K scale, KV head 0 (a pair's first head), the last split
+    scale = 128 ** -0.5
+    out = ops.sparse_decode(q.cuda(), pool.raw, pt.cuda(), _dev(idx), _dev(seq), scale, page_size=64, splits=splits)
+    ref, flash, _ = _oracle(pool.raw, bf16_numpy(q), table, 64, np.arange(32), idx, None, seq, scale)
+    got = out.float().cpu().numpy()
+    nan = np.isnan(ref)
+    assert nan[5, 8:16].all() and nan[9, 16:24, 80:96].all() and not nan[9, 16:24, :80].any() and nan[20, :8].all()
+    assert np.array_equal(np.isnan(got), nan)
+    _check(torch.nan_to_num(out.float(), nan=0.0), np.where(nan, 0.0, ref), np.where(nan, 0.0, flash),
+           nonempty=~nan)
+    il = KVPool(pool.raw[0].shape[0], 4, 128, layout='interleaved', gk=pool.raw[4].clone(), gv=pool.raw[5].clone())
+    for dst, src in zip((il.k_pay, il.v_pay, il.k_sf, il.v_sf), pool.raw[:4]):
+        dst.copy_(src)
+    out2 = ops.sparse_decode(q.cuda(), il.raw, pt.cuda(), _dev(idx), _dev(seq), scale, page_size=64, splits=splits)
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+
+
 def test_interleaved_pool_equals_split_pool():
     """The same bytes in the interleaved layout (one buffer; per slot each head's [K row | V row], then each head's
     [K scales | V scales]) and in SGLang's four buffers give the same bits."""

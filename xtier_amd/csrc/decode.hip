@@ -8,7 +8,10 @@
 // fills them, else 1 (more workgroups).
 // W = 8 while the workgroups fit one round on the CUs (decode batches), else 4, compiled for two workgroups per CU
 // (prefill chunks, one row per query). Each wave owns one (row, KV head, split, slice) and walks its keys in steps of
-// 32. The workgroup computes the split's pool slots once into LDS and merges the slices of each head through LDS
+// 32; with 2 KV heads and 8 waves per workgroup at head size 128 and GQA groups up to 8 (the batch-32 decode), each
+// wave instead owns both heads of the pair (paired waves, steps of 16 keys: one contiguous run of the pair's payload
+// per key and wave, every MFMA column a query head). The workgroup computes the split's pool slots once into LDS and
+// merges the slices of each head through LDS
 // behind one barrier. Workgroups are numbered so that all units of a row run on the same XCD (round-robin dispatch
 // puts workgroup g on XCD g % 8): their K/V lines, which hold several heads, and their partials share one L2.
 //
@@ -34,6 +37,7 @@
 #include "xt_host.h"
 
 #include <mutex>
+#include <type_traits>
 
 namespace xt {
 namespace {
@@ -174,6 +178,10 @@ struct WaveCtx {
   const uint8_t* vp;
   const uint8_t* ksf;   // this head's scale column
   const uint8_t* vsf;
+  const uint8_t* kp2;   // paired waves: the second head's payload and K scale columns
+  const uint8_t* vp2;
+  const uint8_t* ksf2;
+  uint32_t vs_off;      // paired waves: this lane's V scale dword within the first head's scale column
   int64_t row_bytes, row_scales;
   const int32_t* slots;  // this wave's slot list in LDS (-1: invalid)
   int lane, hl, j;
@@ -217,12 +225,51 @@ __device__ inline void load_step(const WaveCtx& w, int step, Step<D>& d) {
   }
 }
 
+// Paired waves (head size 128, GQA group <= 8): one wave covers the two KV heads of a pair in steps of 16 keys, the
+// group of head h in MFMA columns 8h .. 8h + 7, so every column is a query head. QK contracts the 256 dims of both
+// heads (MFMAs 0-3 head 0's, 4-7 head 1's) against a block-diagonal Q^T (head 0's columns zero in head 1's dims and
+// the other way round); PV contracts 32 (head, key) pairs, rows 0-15 of the V tile head 0's keys and 16-31 head 1's,
+// against a block-diagonal P^T. A key's payload of the two heads is one 256-byte run of the interleaved pool (one
+// 128-byte line per K or V on SGLang's split pool), read by one wave.
+constexpr int kPairStep = 16;      // keys per step of a paired wave
+struct PairStep {
+  uint32_t kw[2][4];   // K payload bytes 16 j .. 16 j + 15 of key hl, head h of the pair
+  uint32_t vw[2][4];   // V payload, same
+  uint32_t ks[2];      // K scale dword j / 2 of key hl, head h: the scale bytes 2 j, 2 j + 1 of this lane's dims
+  uint32_t vs;         // V scale dword j % 2 of key hl, head j / 2
+};
+
+template <bool O32>
+__device__ inline void load_step_pair(const WaveCtx& w, int step, PairStep& d) {
+  const int32_t s = w.slots[step * kPairStep + w.hl];
+  const uint32_t po = 16u * (uint32_t)w.j;
+  load_words(row_at<O32>(w.kp, s, w.row_bytes, po), d.kw[0]);
+  load_words(row_at<O32>(w.kp2, s, w.row_bytes, po), d.kw[1]);
+  load_words(row_at<O32>(w.vp, s, w.row_bytes, po), d.vw[0]);
+  load_words(row_at<O32>(w.vp2, s, w.row_bytes, po), d.vw[1]);
+  const uint32_t so = 4u * (uint32_t)(w.j >> 1);
+  d.ks[0] = *reinterpret_cast<const uint32_t*>(row_at<O32>(w.ksf, s, w.row_scales, so));
+  d.ks[1] = *reinterpret_cast<const uint32_t*>(row_at<O32>(w.ksf2, s, w.row_scales, so));
+  d.vs = *reinterpret_cast<const uint32_t*>(row_at<O32>(w.vsf, s, w.row_scales, w.vs_off));
+}
+
+// Bit 7 of byte b set where byte b of x is an E4M3 NaN (0x7F / 0xFF).
+__device__ inline uint32_t e4m3_nan_bytes(uint32_t x) { return ((x & 0x7F7F7F7Fu) + 0x01010101u) & 0x80808080u; }
+// 16-bit mask of the keys (lanes hl, hl + 16, hl + 32, hl + 48 -> bit hl) where the predicate holds in any lane.
+__device__ inline uint32_t key_mask16(bool pred) {
+  const uint64_t b = __builtin_amdgcn_ballot_w64(pred);
+  return (uint32_t)((b | (b >> 16) | (b >> 32) | (b >> 48)) & 0xFFFFu);
+}
+
 template <int D>
 struct SoftmaxState {
   float m;            // reference maximum of head hl (log2 domain), identical on the 4 lanes of the head
   float l;            // this lane's share of the sum of 2^(s - m)
   float4_t acc[Geo<D>::kNT][8];   // O^T of head hl: tile t, dims d = 8 (16 t + 4 j + r) + i in acc[t][i][r]
 };
+
+template <int D>
+__device__ inline void pv_step(int hl, int j, const half8_t& pb, const uint8_t* vtile, SoftmaxState<D>& st);
 
 template <int D, bool PS>
 __device__ inline void compute_step(const WaveCtx& w, int step, const Step<D>& d, const half8_t (&qb)[Geo<D>::kNK],
@@ -321,6 +368,15 @@ __device__ inline void compute_step(const WaveCtx& w, int step, const Step<D>& d
   st.l += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
   const half8_t pb = half8_t{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3],
                              (_Float16)p[4], (_Float16)p[5], (_Float16)p[6], (_Float16)p[7]};
+  pv_step<D>(hl, j, pb, vtile, st);
+}
+
+// O^T += V^T . P^T over the V tile of the step: rows key_of(j, e) (a 32-key step's keys; paired waves: head 0's 16
+// keys, then head 1's), payload at vtile, scale bytes after kStep rows.
+template <int D>
+__device__ inline void pv_step(int hl, int j, const half8_t& pb, const uint8_t* vtile, SoftmaxState<D>& st) {
+  using G = Geo<D>;
+  const uint8_t* vscale = vtile + kStep * G::kVRow;
   // V^T operands of tile t: payload dword c = 16 t + hl of keys T(j), and the scale byte of block c / 2 of those keys
   asm volatile("" ::: "memory");
 #pragma unroll
@@ -358,6 +414,99 @@ __device__ inline void compute_step(const WaveCtx& w, int step, const Step<D>& d
   }
 }
 
+// One 16-key step of a paired wave (head size 128). Lane (hl, j) loaded key hl's pieces of both heads; it ends up with
+// the scores of column hl (head hl / 8 of the pair) for keys 4 j .. 4 j + 3. qb[kk]: the block-diagonal Q^T, zero
+// where the column's head does not own MFMA kk's dims.
+// A NaN scale byte of a valid key must reach only its own head's outputs, as separate heads would: the zero blocks of
+// Q^T and P^T multiply the other head's values, and 0 * NaN is NaN. A step holding one (a ballot, uniform over the
+// wave) therefore takes the NaN bytes out of the operands and puts NaN where separate heads would have it: into the
+// scores of the (key, head) pairs of a K scale, into the outputs of the (head, 16-dim block) pairs of a V scale.
+__device__ inline void compute_step_pair(const WaveCtx& w, int step, const PairStep& d, const half8_t (&qb)[8],
+                                         float smul, uint8_t* vtile, SoftmaxState<128>& st) {
+  using G = Geo<128>;
+  const int lane = w.lane, hl = w.hl, j = w.j;
+  const uint32_t valid = key_mask16(lane < kPairStep && w.slots[step * kPairStep + hl] >= 0);
+  const bool key_ok = (valid >> hl) & 1u;
+  uint32_t ks0 = d.ks[0], ks1 = d.ks[1];
+  uint32_t vs = key_ok ? d.vs : 0u;   // invalid keys: V scale 0, so V = 0 whatever slot 0 holds
+  uint32_t nan_k0 = 0u, nan_k1 = 0u;  // per head: keys with a NaN K scale byte
+  uint32_t nan_vb = 0u;               // blocks (bit b: dims 16 b ..) of column hl's head with a NaN V scale byte
+  bool nan_v = false;
+  if (__builtin_amdgcn_ballot_w64(key_ok && (e4m3_nan_bytes(ks0) | e4m3_nan_bytes(ks1) | e4m3_nan_bytes(vs)))) {
+    const uint32_t n0 = e4m3_nan_bytes(ks0), n1 = e4m3_nan_bytes(ks1), nv = e4m3_nan_bytes(vs);
+    nan_k0 = key_mask16(key_ok && n0);
+    nan_k1 = key_mask16(key_ok && n1);
+    // lane (key, j) holds V scale bytes 4 (j % 2) .. + 3 of head j / 2, i.e. blocks 4 (j % 2) + b
+    uint32_t m0 = 0u, m1 = 0u;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint64_t bal = __builtin_amdgcn_ballot_w64((nv >> (8 * b + 7)) & 1u);
+      m0 |= (((bal & 0xFFFFull) != 0) << b) | ((((bal >> 16) & 0xFFFFull) != 0) << (4 + b));
+      m1 |= ((((bal >> 32) & 0xFFFFull) != 0) << b) | ((((bal >> 48) & 0xFFFFull) != 0) << (4 + b));
+    }
+    nan_vb = hl < 8 ? m0 : m1;
+    nan_v = (m0 | m1) != 0u;
+    ks0 &= ~((n0 >> 7) * 0xFFu);   // NaN bytes -> 0 (bit 7 of a byte times 0xFF: that byte all ones)
+    ks1 &= ~((n1 >> 7) * 0xFFu);
+    vs &= ~((nv >> 7) * 0xFFu);
+  }
+
+  // V: payload rows 16 h + key, then the scale rows in the same order
+  store_words(vtile + hl * G::kVRow + 16 * j, d.vw[0]);
+  store_words(vtile + (16 + hl) * G::kVRow + 16 * j, d.vw[1]);
+  *reinterpret_cast<uint32_t*>(vtile + kStep * G::kVRow + (16 * (j >> 1) + hl) * G::kSf + 4 * (j & 1)) = vs;
+
+  // QK: dword kk of the lane's 16 payload bytes holds dims 32 j + 8 kk .., scale byte 2 j + kk / 2 of the head row
+  float4_t s = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const half2_t c01 = fp8x2_to_f16<false>((h ? ks1 : ks0) >> (16 * (j & 1)));
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const _Float16 sc = kk < 2 ? c01.x : c01.y;
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant_k(d.kw[h][kk], half2_t{sc, sc}), qb[4 * h + kk], s, 0, 0, 0);
+    }
+  }
+  float sv[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) sv[e] = s[e] * smul;
+  if (valid != 0xFFFFu) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sv[e] = ((valid >> (4 * j + e)) & 1u) ? sv[e] : -__builtin_inff();
+  }
+  if (nan_k0 | nan_k1) {
+    const uint32_t nk = hl < 8 ? nan_k0 : nan_k1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sv[e] = ((nk >> (4 * j + e)) & 1u) ? __builtin_nanf("") : sv[e];
+  }
+  float mt = max2_raw(max2_raw(sv[0], sv[1]), max2_raw(sv[2], sv[3]));
+  mt = max4_lanes16(mt);
+  if (__builtin_amdgcn_ballot_w64(mt > st.m + kRescale)) {   // rare after the first steps
+    const float m_new = (mt > st.m + kRescale) ? mt : st.m;
+    const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+    st.l *= alpha;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st.acc[0][i] *= alpha;
+    st.m = m_new;
+  }
+  const float m_use = (st.m == -__builtin_inff()) ? 0.0f : st.m;
+  float p[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(sv[e] - m_use);
+  st.l += (p[0] + p[1]) + (p[2] + p[3]);
+  const _Float16 z = (_Float16)0.0f;
+  const half8_t pb = hl < 8 ? half8_t{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3], z, z, z, z}
+                            : half8_t{z, z, z, z, (_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
+  pv_step<128>(hl, j, pb, vtile, st);
+  if (nan_v) {   // acc[0][i][r] holds dims 8 (4 j + r) + i: block (4 j + r) / 2
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if ((nan_vb >> ((4 * j + r) >> 1)) & 1u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) st.acc[0][i][r] = __builtin_nanf("");
+  }
+}
+
 __device__ inline void store_out(const DecodeArgs& a, int row, int head, int d0, const float* v, int n) {
   uint16_t* o = a.out + (int64_t)row * a.o_rs + (int64_t)head * a.o_hs + d0;
   for (int e = 0; e < n; e += 2) {
@@ -375,12 +524,16 @@ __device__ inline void store_out(const DecodeArgs& a, int row, int head, int d0,
 // (prefill chunks: one slice per head, no LDS merge region, so three workgroups fit a CU's LDS; 168 VGPRs, the few
 // values spilled are held across the main loop only: the batch-4096 prefill chunk 622 -> 599 us). Head size 256
 // stays at two: its accumulators alone would spill ~100 registers at 168.
-template <int D, int P, int HPW, bool PS, int W, bool O32>
+template <int D, int P, int HPW, bool PS, int W, bool O32, bool PR>
 __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 : 2)
     decode_split_kernel(const DecodeArgs a) {
   using G = Geo<D>;
-  constexpr int kSlices = W / HPW;
+  static_assert(!PR || (D == 128 && HPW % 2 == 0), "paired waves: head size 128, whole pairs of KV heads");
+  constexpr int kWaveHeads = PR ? 2 : 1;            // KV heads per wave
+  constexpr int kHeadSets = HPW / kWaveHeads;       // distinct wave head sets per workgroup
+  constexpr int kSlices = W / kHeadSets;
   constexpr int kThreads = 64 * W;
+  constexpr int KS = PR ? kPairStep : kStep;        // keys per step
   extern __shared__ __align__(16) uint8_t lds[];
   // XCD-aware numbering: workgroup g runs on XCD g % 8 (round-robin dispatch); XCD x takes the contiguous unit range
   // starting at x * (n / 8) + min(x, n % 8), so a row's units (its heads and splits) share one L2. A bijection on
@@ -400,8 +553,8 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
   const int kvg = (int)((u / splits_u) % groups_u);
   const int row = (int)(u / splits_u / groups_u);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int kvh = kvg * HPW + (wave % HPW);
-  const int slice = wave / HPW;
+  const int kvh = kvg * HPW + kWaveHeads * (wave % kHeadSets);   // the wave's (first) KV head
+  const int slice = wave / kHeadSets;
   const bool active = kvh < a.kv_heads;
 
   int32_t* slots = reinterpret_cast<int32_t*>(lds);
@@ -410,10 +563,13 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
   // the query's raw words first (loads complete in order); every lane reads a valid address and heads outside the
   // group are zeroed at conversion, so the loads carry no branch
   const int hl = lane & 15, j = lane >> 4;
-  const bool q_valid = active && hl < a.group;
+  // column hl: a query head of the wave's KV head, or (paired waves) of KV head hl / 8 of its pair
+  const int col_kvh = PR ? kvh + (hl >> 3) : kvh;
+  const int col_qh = PR ? (hl & 7) : hl;
+  const bool q_valid = col_kvh < a.kv_heads && col_qh < a.group;
   uint4 qraw[G::kNK];
   {
-    const int head = min(kvh, a.kv_heads - 1) * a.group + min(hl, a.group - 1);
+    const int head = min(col_kvh, a.kv_heads - 1) * a.group + min(col_qh, a.group - 1);
     const uint16_t* qp = a.q + (int64_t)row * a.q_rs + (int64_t)head * a.q_hs;
 #pragma unroll
     for (int kk = 0; kk < G::kNK; ++kk) qraw[kk] = *reinterpret_cast<const uint4*>(qp + (D / 4) * j + 8 * kk);
@@ -454,13 +610,13 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
   asm volatile("" : "+s"(len_v), "+s"(cnt_v), "+s"(qpos_v), "+s"(req_lo), "+s"(req_hi), "+s"(gk_v), "+s"(gv_v));
   const int count = a.counts ? min(cnt_v, a.topk) : a.topk;
   const int n = max(0, min(t0 + a.keys_per_split, count) - t0);
-  const int slice_steps = (((n + kStep - 1) / kStep + kSlices * P - 1) / (kSlices * P)) * P;
+  const int slice_steps = (((n + KS - 1) / KS + kSlices * P - 1) / (kSlices * P)) * P;
   {
     const int32_t seqlen = min(len_v, a.max_len);
     const int32_t qpos = a.query_pos ? qpos_v : 0x7FFFFFFF;
     const int64_t trow = a.row_req ? (int64_t)(((uint64_t)(uint32_t)req_hi << 32) | (uint32_t)req_lo) : row;
     const int32_t* tp = a.table + trow * a.table_stride;
-    const int total = kSlices * slice_steps * kStep;
+    const int total = kSlices * slice_steps * KS;
     for (int i0 = 0;;) {
       // validity and table offsets of all kSlotBatch keys first, then their table loads back to back (a use of an
       // index between two table loads would wait for the earlier table load too)
@@ -518,13 +674,22 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
     w.vp = a.v_pay + (int64_t)kvh * a.pay_head_stride;
     w.ksf = a.k_sf + (int64_t)kvh * a.sf_head_stride;
     w.vsf = a.v_sf + (int64_t)kvh * a.sf_head_stride;
-    w.slots = slots + slice * slice_steps * kStep;
+    w.kp2 = w.kp + a.pay_head_stride;
+    w.vp2 = w.vp + a.pay_head_stride;
+    w.ksf2 = w.ksf + a.sf_head_stride;
+    w.vs_off = 4u * (uint32_t)(j & 1) + (uint32_t)(j >> 1) * (uint32_t)a.sf_head_stride;
+    w.slots = slots + slice * slice_steps * KS;
     w.lane = lane;
     w.hl = hl;
     w.j = j;
-    Step<D> buf[P];
+    using StepT = typename std::conditional<PR, PairStep, Step<D>>::type;
+    StepT buf[P];
+    auto load = [&](int step, StepT& d) {
+      if constexpr (PR) load_step_pair<O32>(w, step, d);
+      else load_step<D, PS, O32>(w, step, d);
+    };
 #pragma unroll
-    for (int p = 0; p < P; ++p) load_step<D, PS, O32>(w, p, buf[p]);
+    for (int p = 0; p < P; ++p) load(p, buf[p]);
     // the query's operands, prepared while the first steps' loads are in flight. B operand of the QK MFMAs: FP16 of
     // q * 2^-e, exact, with 2^e per head from its largest magnitude
     // (pow2_query_scale); heads beyond the group are zero. The FP32 scores are multiplied by smul = |gk| * scale *
@@ -545,27 +710,42 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
     const float2_t p2 = pow2_query_scale(max4_lanes16(qmax));   // the head's maximum over its four lanes
     const float qs = gk_v < 0.0f ? -p2[0] : p2[0];
     const float smul = gk * a.qscale * p2[1];
-    half8_t qb[G::kNK];
+    // paired waves: MFMA kk < 4 contracts head 0's dims, kk >= 4 head 1's; a column's operand is zero in the other
+    // head's dims (block-diagonal Q^T)
+    constexpr int kQB = PR ? 2 * G::kNK : G::kNK;
+    half8_t qb[kQB];
 #pragma unroll
     for (int kk = 0; kk < G::kNK; ++kk) {
       const uint32_t ws[4] = {q_valid ? qraw[kk].x : 0u, q_valid ? qraw[kk].y : 0u, q_valid ? qraw[kk].z : 0u,
                               q_valid ? qraw[kk].w : 0u};
+      half8_t h;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        qb[kk][2 * e] = (_Float16)(bf16_bits_to_f32(ws[e] & 0xFFFFu) * qs);
-        qb[kk][2 * e + 1] = (_Float16)(bf16_bits_to_f32(ws[e] >> 16) * qs);
+        h[2 * e] = (_Float16)(bf16_bits_to_f32(ws[e] & 0xFFFFu) * qs);
+        h[2 * e + 1] = (_Float16)(bf16_bits_to_f32(ws[e] >> 16) * qs);
+      }
+      if constexpr (PR) {
+        const half8_t zero = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+        qb[kk] = hl < 8 ? h : zero;
+        qb[(G::kNK + kk) % kQB] = hl < 8 ? zero : h;
+      } else {
+        qb[kk] = h;
       }
     }
+    auto compute = [&](int step, const StepT& d) {
+      if constexpr (PR) compute_step_pair(w, step, d, qb, smul, vtile, st);
+      else compute_step<D, PS>(w, step, d, qb, smul, vtile, st);
+    };
     int s0 = 0;
     for (; s0 + P < slice_steps; s0 += P) {
 #pragma unroll
       for (int p = 0; p < P; ++p) {
-        compute_step<D, PS>(w, s0 + p, buf[p], qb, smul, vtile, st);
-        load_step<D, PS, O32>(w, s0 + p + P, buf[p]);
+        compute(s0 + p, buf[p]);
+        load(s0 + p + P, buf[p]);
       }
     }
 #pragma unroll
-    for (int p = 0; p < P; ++p) compute_step<D, PS>(w, s0 + p, buf[p], qb, smul, vtile, st);
+    for (int p = 0; p < P; ++p) compute(s0 + p, buf[p]);
   }
   // the 4 lanes of a head hold disjoint key subsets of l
   float l_tot = sum4_lanes16(st.l);
@@ -575,9 +755,9 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
   // with no LDS merge, and the launch reserves no merge region.
   if constexpr (kSlices == 1) {
     if (a.splits == 1) {
-      if (active && hl < a.group && (D != 64 || j < 2)) {
+      if (active && q_valid && (D != 64 || j < 2)) {
         const float inv = l_tot > 0.0f ? gv_v / l_tot : 0.0f;
-        const int head = kvh * a.group + hl;
+        const int head = col_kvh * a.group + col_qh;
 #pragma unroll
         for (int t = 0; t < G::kNT; ++t)
 #pragma unroll
@@ -616,7 +796,10 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
       row_part, (short)0, a.splits > 1 ? (int)((int64_t)a.splits * a.q_heads * G::kPartStride * 4) : 0, 0x00020000);
   const float gv = gv_v;
   constexpr int kParts = 8 * G::kNT;   // 4-dim pieces per lane
-  constexpr int kUnits = (HPW * 64 * kParts + kThreads - 1) / kThreads;   // pieces per thread
+  constexpr int kUnits = (kHeadSets * 64 * kParts + kThreads - 1) / kThreads;   // pieces per thread
+  // the KV head and query head of column uh of the wave head set hw (paired waves: head uh / 8 of the pair)
+  auto unit_kvh = [&](int hw, int uh) { return kvg * HPW + kWaveHeads * hw + (PR ? (uh >> 3) : 0); };
+  auto unit_qh = [&](int uh) { return PR ? (uh & 7) : uh; };
   // with key splits and at most two pieces per thread, each thread keeps its pieces' merged (output, max, sum) for
   // the split merge below (with more, the registers would spill: the merge reloads its own split too)
   constexpr bool kKeep = kUnits <= 2;
@@ -628,17 +811,18 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
     keep_m[k] = -__builtin_inff();
     keep_l[k] = 0.0f;
     keep_o[k] = float4_t{0.f, 0.f, 0.f, 0.f};
-    if (u >= HPW * 64 * kParts) continue;
-    const int part = u % kParts, ln = (u / kParts) & 63, hw = u / (kParts * 64);   // piece part of lane ln, KV head hw
+    if (u >= kHeadSets * 64 * kParts) continue;
+    const int part = u % kParts, ln = (u / kParts) & 63, hw = u / (kParts * 64);   // piece part of lane ln, head set hw
     const int uh = ln & 15, uj = ln >> 4;
-    const int ukvh = kvg * HPW + hw;
-    if (ukvh >= a.kv_heads || uh >= a.group || (D == 64 && uj >= 2)) continue;
+    const int ukvh = unit_kvh(hw, uh), uqh = unit_qh(uh);
+    if (ukvh >= a.kv_heads || uqh >= a.group || (D == 64 && uj >= 2)) continue;
     float ms[kSlices], ls[kSlices];
     float4_t xs[kSlices];
     float mx = -__builtin_inff();
 #pragma unroll
     for (int sl = 0; sl < kSlices; ++sl) {
-      const float4_t* src = reinterpret_cast<const float4_t*>(mrg + ((sl * HPW + hw) * 64 + ln) * G::kMergeRow);
+      const float4_t* src =
+          reinterpret_cast<const float4_t*>(mrg + ((sl * kHeadSets + hw) * 64 + ln) * G::kMergeRow);
       xs[sl] = src[part];
       const float4_t ml = src[8 * G::kNT];
       ms[sl] = ml[0];
@@ -654,7 +838,7 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
       o += wgt * xs[sl];
       l += wgt * ls[sl];
     }
-    const int head = ukvh * a.group + uh, d0 = 128 * (part >> 3) + 32 * uj + 4 * (part & 7);
+    const int head = ukvh * a.group + uqh, d0 = 128 * (part >> 3) + 32 * uj + 4 * (part & 7);
     if (a.splits == 1) {   // no partials: normalize and write
       const float inv = l > 0.0f ? gv / l : 0.0f;
       const float v[4] = {o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
@@ -688,9 +872,9 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
     const int u = (int)threadIdx.x + k * kThreads;
     const int part = u % kParts, ln = (u / kParts) & 63, hw = u / (kParts * 64);
     const int uh = ln & 15, uj = ln >> 4;
-    const int ukvh = kvg * HPW + hw;
-    live_k[k] = u < HPW * 64 * kParts && ukvh < a.kv_heads && uh < a.group && !(D == 64 && uj >= 2);
-    heads_k[k] = min(ukvh, a.kv_heads - 1) * a.group + min(uh, a.group - 1);
+    const int ukvh = unit_kvh(hw, uh), uqh = unit_qh(uh);
+    live_k[k] = u < kHeadSets * 64 * kParts && ukvh < a.kv_heads && uqh < a.group && !(D == 64 && uj >= 2);
+    heads_k[k] = min(ukvh, a.kv_heads - 1) * a.group + min(uqh, a.group - 1);
     d0s[k] = 128 * (part >> 3) + 32 * uj + 4 * (part & 7);
   }
   // up to two pieces at a time: their loads of four splits (16 x 16 bytes) go out together
@@ -1001,25 +1185,29 @@ extern "C" int xt_block_sparse_prefill_nvfp4(const void* q, int64_t q_row_stride
 }
 
 // One launch of the decode kernel.
-template <int D, int HPW, bool PS, int W, bool O32>
+template <int D, int HPW, bool PS, int W, bool O32, bool PR>
 static int launch_decode(const DecodeArgs& a, dim3 grid, size_t lds_bytes, hipStream_t stream, const char* what) {
   constexpr int P = Geo<D>::kPrefetch;
-  if (int e = allow_lds(reinterpret_cast<const void*>(&decode_split_kernel<D, P, HPW, PS, W, O32>), lds_bytes, what))
+  if (int e = allow_lds(reinterpret_cast<const void*>(&decode_split_kernel<D, P, HPW, PS, W, O32, PR>), lds_bytes,
+                        what))
     return e;
-  hipLaunchKernelGGL((decode_split_kernel<D, P, HPW, PS, W, O32>), grid, dim3(64 * W), lds_bytes, stream, a);
+  hipLaunchKernelGGL((decode_split_kernel<D, P, HPW, PS, W, O32, PR>), grid, dim3(64 * W), lds_bytes, stream, a);
   return check_launch(what);
 }
 
-template <int D, int HPW, bool PS, int W>
+template <int D, int HPW, bool PS, int W, bool PR = false>
 static int launch_decode(bool o32, const DecodeArgs& a, dim3 grid, size_t lds_bytes, hipStream_t stream,
                          const char* what) {
-  return o32 ? launch_decode<D, HPW, PS, W, true>(a, grid, lds_bytes, stream, what)
-             : launch_decode<D, HPW, PS, W, false>(a, grid, lds_bytes, stream, what);
+  return o32 ? launch_decode<D, HPW, PS, W, true, PR>(a, grid, lds_bytes, stream, what)
+             : launch_decode<D, HPW, PS, W, false, PR>(a, grid, lds_bytes, stream, what);
 }
 
 template <int D, int W>
-static int launch_decode(int hpw, bool ps, bool o32, const DecodeArgs& a, dim3 grid, size_t lds_bytes,
+static int launch_decode(int hpw, bool ps, bool pr, bool o32, const DecodeArgs& a, dim3 grid, size_t lds_bytes,
                          hipStream_t stream, const char* what) {
+  if constexpr (D == 128 && W == kWaves) {   // paired waves: 2 KV heads per workgroup, 8 key slices
+    if (pr) return launch_decode<D, 2, false, W, true>(o32, a, grid, lds_bytes, stream, what);
+  }
   if constexpr (D == 128) {   // paired K/V scales: the interleaved pool at head size 128
     if (ps) return hpw == 4   ? launch_decode<D, 4, true, W>(o32, a, grid, lds_bytes, stream, what)
                    : hpw == 2 ? launch_decode<D, 2, true, W>(o32, a, grid, lds_bytes, stream, what)
@@ -1088,10 +1276,17 @@ static int decode_impl(const char* what, const void* q, int64_t q_row_stride, in
   // Head size 256 always runs 4-wave workgroups: eight waves' merge regions would not fit in LDS.
   const int64_t units = (int64_t)rows * ((kv_heads + hpw - 1) / hpw) * splits;
   const int waves = (units > cus || dim == 256) ? 4 : kWaves;
-  const int slices = waves / hpw;
+  // Paired waves (each wave both KV heads of a pair, steps of 16 keys) for workgroups of 2 KV heads at head size 128
+  // and GQA groups up to 8 with one index list for all heads: a key's payload of the pair is one contiguous run per
+  // wave instead of one piece per wave and head.
+  // (Prefill chunks keep one wave per KV head: the paired waves' second query operand costs 16 registers, which
+  // spills at their three waves per SIMD; at two waves per SIMD the batch-4096 chunk measured 664 against 598 us.)
+  const bool pr = dim == 128 && group <= 8 && !ad.idx_head_stride && hpw == 2 && waves == kWaves;
+  const int slices = pr ? waves : waves / hpw;
+  const int step_keys = pr ? kPairStep : kStep;
   const int pf = prefetch_of(dim);
-  const int slice_steps = ((kps / kStep + slices * pf - 1) / (slices * pf)) * pf;
-  const int slot_bytes = slices * slice_steps * kStep * (int)sizeof(int32_t);
+  const int slice_steps = ((kps / step_keys + slices * pf - 1) / (slices * pf)) * pf;
+  const int slot_bytes = slices * slice_steps * step_keys * (int)sizeof(int32_t);
   const bool direct = slices == 1 && splits == 1;
   const size_t lds_bytes = dim == 64    ? decode_lds<64>(slot_bytes, waves, direct)
                            : dim == 128 ? decode_lds<128>(slot_bytes, waves, direct)
@@ -1164,13 +1359,14 @@ static int decode_impl(const char* what, const void* q, int64_t q_row_stride, in
   // below 2^32 bytes from the head's column
   const bool o32 = pool_slots <= (1LL << 24) && pay_stride < (1LL << 24) && sf_stride < (1LL << 24) &&
                    (pool_slots - 1) * pay_stride + dim / 2 < (1LL << 32) &&
-                   (pool_slots - 1) * sf_stride + dim / 16 < (1LL << 32);
+                   (pool_slots - 1) * sf_stride + dim / 16 < (1LL << 32) &&
+                   (!pr || (pool_slots - 1) * sf_stride + ad.sf_head_stride + dim / 16 < (1LL << 32));
   const dim3 grid((unsigned)launched);
   const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (dim == 64)
-    return waves == 4 ? launch_decode<64, 4>(hpw, ps, o32, a, grid, lds_bytes, st, what)
-                      : launch_decode<64, kWaves>(hpw, ps, o32, a, grid, lds_bytes, st, what);
-  if (dim == 256) return launch_decode<256, 4>(hpw, ps, o32, a, grid, lds_bytes, st, what);
-  return waves == 4 ? launch_decode<128, 4>(hpw, ps, o32, a, grid, lds_bytes, st, what)
-                    : launch_decode<128, kWaves>(hpw, ps, o32, a, grid, lds_bytes, st, what);
+    return waves == 4 ? launch_decode<64, 4>(hpw, ps, false, o32, a, grid, lds_bytes, st, what)
+                      : launch_decode<64, kWaves>(hpw, ps, false, o32, a, grid, lds_bytes, st, what);
+  if (dim == 256) return launch_decode<256, 4>(hpw, ps, false, o32, a, grid, lds_bytes, st, what);
+  return waves == 4 ? launch_decode<128, 4>(hpw, ps, false, o32, a, grid, lds_bytes, st, what)
+                    : launch_decode<128, kWaves>(hpw, ps, pr, o32, a, grid, lds_bytes, st, what);
 }
