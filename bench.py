@@ -107,6 +107,34 @@ def time_steps(step, layers, steps, warmup):
     return ev[0].elapsed_time(ev[-1]) / steps, per, g_len
 
 
+def timeline_summary(stamps, waves, phases):
+    """Phase times of one decode launch from its per-wave stamps (100 MHz ticks, rows g * waves + w): per phase the
+    p10 / p50 / p90 / max over the waves that reached it, in µs from the earliest wave's entry; and the spread of the
+    main loop's end within a workgroup (its last wave minus its first)."""
+    import numpy as np
+    st = np.asarray(stamps, dtype=np.int64)
+    st = st[: (st.shape[0] // waves) * waves].reshape(-1, waves, len(phases))
+    st = st[(st[:, :, 0] > 0).all(1)]
+    t0 = st[:, :, 0].min()
+    out = {'unit': 'µs from the first wave entry of the launch (100 MHz clock)', 'phases': {}}
+    for i, name in enumerate(phases):
+        col = st[:, :, i].ravel()
+        col = col[col > 0]
+        if col.size == 0:
+            continue
+        rel = (col - t0) / 100.0
+        out['phases'][name] = {'waves': int(col.size), 'p10': round(float(np.percentile(rel, 10)), 2),
+                               'p50': round(float(np.percentile(rel, 50)), 2),
+                               'p90': round(float(np.percentile(rel, 90)), 2), 'max': round(float(rel.max()), 2)}
+    loop = st[:, :, 3]
+    ok = (loop > 0).all(1)
+    if ok.any():
+        d = (loop[ok].max(1) - loop[ok].min(1)) / 100.0
+        out['main_loop_done_spread_within_workgroup'] = {'p50': round(float(np.percentile(d, 50)), 2),
+                                                         'p90': round(float(np.percentile(d, 90)), 2)}
+    return out
+
+
 def spread(per_step_us, launches_per_replay):
     """Median and p10 / p90 of the per-layer-step times of the full replays."""
     import numpy as np
@@ -1083,6 +1111,9 @@ def main():
     p.add_argument('--no-cpu-baseline', action='store_true')
     p.add_argument('--no-layout-compare', action='store_true',
                    help='decode workloads: skip timing the same step on the other pool layout')
+    p.add_argument('--timeline', action='store_true',
+                   help='decode workloads: after the timed region, one more launch with the per-wave timeline '
+                        '(xt_decode_timeline) and its phase times in the record')
     p.add_argument('--copy-calibration', type=int, default=0, metavar='MIB',
                    help='only copy MIB MiB between two device buffers 8 times (the known-size kernel that scales the '
                         'FETCH_SIZE / WRITE_SIZE counters), then exit')
@@ -1148,6 +1179,18 @@ def main():
     props = torch.cuda.get_device_properties(0)
     log(f'{w.name}: {ms * 1e3:.2f} us per layer-step, {gbs:.0f} GB/s algorithmic ({gbs / HBM_PEAK_GBS:.1%} of '
         f'{HBM_PEAK_GBS:.0f}), splits {splits}, {args.layout} pool, {props.multi_processor_count} CUs')
+    timeline = None
+    if args.timeline:
+        # one launch on the pool used half a rotation ago (its records are out of the MALL by now, as in the timed
+        # region)
+        hpw, waves, units = ops.decode_shape(w.batch, w.kv_heads, splits, w.dim)
+        torch.cuda.synchronize()
+        with ops.decode_timeline(units * waves) as tl:
+            step(rot // 2)
+        timeline = timeline_summary(tl.stamps, waves, ops.TIMELINE_PHASES)
+        timeline['shape'] = {'kv_heads_per_workgroup': hpw, 'waves_per_workgroup': waves, 'workgroups': units,
+                             'pool_layout': args.layout}
+        log('timeline: ' + json.dumps(timeline))
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(layers[0], q, pt, idx, seq, w, scale)
@@ -1184,6 +1227,8 @@ def main():
         'cpu_baseline': cpu,
         'other_layout': other,
     }
+    if timeline is not None:
+        record['timeline'] = timeline
     emit(record)
 
 

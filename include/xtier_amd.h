@@ -479,6 +479,15 @@ int xt_ceiling_split_merge(void* part, int bytes, int32_t* counters, uint32_t* o
  * of the constant 100 MHz clock (s_memrealtime); out[0] = core clock ticks, out[1] = 100 MHz ticks, out[2] = a check
  * word (uint64_t[3], device memory). MHz = 100 * out[0] / out[1]. */
 int xt_clock_probe(uint64_t* out, int iters, xt_stream_t stream);
+/* xt_decode_timeline: a per-wave timeline of the fused decode (no counterpart in the reference; for measurement).
+ * With `stamps` (device memory, 8-byte aligned, `bytes` long) set, every later launch of the decode kernel
+ * (xt_sparse_decode_nvfp4, its _static variant, the block decode and prefill) makes the first lane of each wavefront w
+ * of workgroup g write 8 readings of the 100 MHz constant clock (s_memrealtime) to stamps[(g * waves + w) * 8 + i]:
+ * i = 0 entry, 1 the split's slot list in LDS, 2 the first key step computed, 3 the main loop done, 4 the slices merged
+ * in LDS, 5 the partials (or, with one split, the outputs) issued, 6 the arrival counted, 7 the last arriver's split
+ * merge done; phases a wave does not reach read 0. Workgroups past bytes / (waves * 64) write nothing; waves is 8 for
+ * decode batches that fit one round of workgroups, else 4. A process-wide setting; NULL turns it off (the default). */
+int xt_decode_timeline(uint64_t* stamps, size_t bytes);
 
 #ifdef __cplusplus
 }

@@ -381,6 +381,31 @@ def test_decode_nan_scales_stay_in_their_head(splits):
     assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
 
 
+@pytest.mark.parametrize('batch,splits', [(32, 4), (6, 3)])
+def test_decode_timeline(batch, splits):
+    """The per-wave timeline (xt_decode_timeline) of a launch of paired waves (32 rows x 4 KV heads x 4 splits) and of
+    one with 1 KV head per workgroup: every wave of every workgroup stamps its phases in order, exactly one workgroup
+    per (row, KV head group) merges the splits, and the outputs are those of the same launch without the timeline."""
+    pool, pt, idx, q = _small_case(seed=90 + batch, batch=batch)
+    seq = np.full(batch, 3008, np.int32)
+    args = (q.cuda(), pool.raw, pt.cuda(), idx.cuda(), _dev(seq), 128 ** -0.5)
+    plain = ops.sparse_decode(*args, page_size=64, splits=splits)
+    hpw, waves, units = ops.decode_shape(batch, 4, splits)
+    with ops.decode_timeline(units * waves + 16) as tl:
+        timed = ops.sparse_decode(*args, page_size=64, splits=splits)
+    assert torch.equal(plain.view(torch.int16), timed.view(torch.int16))
+    st = tl.stamps
+    assert not st[units * waves:].any()                        # nothing past the launch's waves
+    st = st[:units * waves].reshape(units, waves, 8)
+    reached = st[:, :, :7]                                      # every wave reaches phases 0..6 (splits > 1)
+    assert (reached > 0).all()
+    assert (np.diff(reached, axis=2) >= 0).all()
+    last = st[:, :, 7] > 0
+    assert (last.all(1) | ~last.any(1)).all()                   # all waves of a workgroup, or none
+    assert last.all(1).sum() == batch * (4 // hpw)              # one last arriver per (row, KV head group)
+    assert (st[:, :, 7][last] >= st[:, :, 6][last]).all()
+
+
 def test_interleaved_pool_equals_split_pool():
     """The same bytes in the interleaved layout (one buffer; per slot each head's [K row | V row], then each head's
     [K scales | V scales]) and in SGLang's four buffers give the same bits."""

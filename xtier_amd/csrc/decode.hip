@@ -36,6 +36,7 @@
 #include "xt_common.h"
 #include "xt_host.h"
 
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -116,7 +117,12 @@ struct DecodeArgs {
   int64_t n_units;                   // rows * kv_groups * splits workgroups, one per unit
   uint32_t xcd_units;                // n_units / 8
   uint32_t xcd_extra;                // n_units % 8
+  uint64_t* stamps;                  // per-wave timeline (xt_decode_timeline), NULL: off
+  uint32_t stamp_blocks;             // workgroups whose stamps fit the buffer
 };
+
+// The phases of the per-wave timeline, in stamp order.
+enum { kStEntry, kStSlots, kStStep0, kStLoop, kStSliceMerge, kStPartials, kStArrived, kStSplitMerge, kStamps };
 
 template <int D>
 struct Step {
@@ -546,6 +552,10 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
                "s"(a.table_stride), "s"(a.page_shift), "s"(a.page_size), "s"(a.pool_slots), "s"(a.idx_head_stride),
                "s"(a.block_shift), "s"(a.max_len), "s"(a.remap_shift), "s"(a.remap_mul));
   const uint32_t g = blockIdx.x;
+  // per-wave timeline (diagnostics, off unless xt_decode_timeline set a buffer): the first lane of every wave writes
+  // the 100 MHz constant clock at each phase; a branch uniform over the launch otherwise
+  const bool timeline = a.stamps != nullptr && g < a.stamp_blocks;
+  const uint64_t t_entry = timeline ? __builtin_amdgcn_s_memrealtime() : 0;
   const uint32_t xcd = g & 7u;
   const uint32_t u = xcd * a.xcd_units + min(xcd, a.xcd_extra) + (g >> 3);
   const uint32_t splits_u = (uint32_t)a.splits, groups_u = (uint32_t)a.kv_groups;
@@ -553,6 +563,18 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
   const int kvg = (int)((u / splits_u) % groups_u);
   const int row = (int)(u / splits_u / groups_u);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  uint64_t* const my_stamps = timeline ? a.stamps + ((uint64_t)g * W + wave) * kStamps : nullptr;
+  auto stamp = [&](int phase) {
+    if (timeline) {
+      const uint64_t t = __builtin_amdgcn_s_memrealtime();
+      if (lane == 0) my_stamps[phase] = t;
+    }
+  };
+  if (timeline && lane == 0) {   // phases a wave does not reach stay 0
+    my_stamps[kStEntry] = t_entry;
+#pragma unroll
+    for (int i = 1; i < kStamps; ++i) my_stamps[i] = 0;
+  }
   const int kvh = kvg * HPW + kWaveHeads * (wave % kHeadSets);   // the wave's (first) KV head
   const int slice = wave / kHeadSets;
   const bool active = kvh < a.kv_heads;
@@ -657,6 +679,7 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
     }
   }
   __syncthreads();
+  stamp(kStSlots);
 
   SoftmaxState<D> st;
   st.m = -__builtin_inff();
@@ -735,6 +758,7 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
     auto compute = [&](int step, const StepT& d) {
       if constexpr (PR) compute_step_pair(w, step, d, qb, smul, vtile, st);
       else compute_step<D, PS>(w, step, d, qb, smul, vtile, st);
+      if (step == 0) stamp(kStStep0);
     };
     int s0 = 0;
     for (; s0 + P < slice_steps; s0 += P) {
@@ -747,6 +771,7 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
 #pragma unroll
     for (int p = 0; p < P; ++p) compute(s0 + p, buf[p]);
   }
+  stamp(kStLoop);
   // the 4 lanes of a head hold disjoint key subsets of l
   float l_tot = sum4_lanes16(st.l);
 
@@ -771,6 +796,7 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
           a.lse[(int64_t)row * a.q_heads + head] =
               l_tot > 0.0f ? (st.m + __builtin_log2f(l_tot)) * kLn2 : -__builtin_inff();
       }
+      stamp(kStPartials);
       return;
     }
   }
@@ -791,6 +817,7 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
     mine[8 * G::kNT] = float4_t{st.m, l_tot, 0.0f, 0.0f};
   }
   __syncthreads();
+  stamp(kStSliceMerge);
   float* row_part = a.part + (int64_t)row * a.splits * a.q_heads * G::kPartStride;
   const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
       row_part, (short)0, a.splits > 1 ? (int)((int64_t)a.splits * a.q_heads * G::kPartStride * 4) : 0, 0x00020000);
@@ -856,6 +883,7 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
       }
     }
   }
+  stamp(kStPartials);
   if (a.splits == 1) return;
   // the last workgroup of (row, KV group) to arrive merges the partials (the split arrival of xt_common.h): each
   // thread merges the same pieces it wrote, in split order whichever workgroup arrives last (so the result does not
@@ -864,7 +892,9 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
   // reads zeros)
   __shared__ int s_last;
   int32_t* counter = a.counters + (int64_t)row * a.kv_groups + kvg;
-  if (!arrive_last(counter, a.splits, &s_last)) return;
+  const bool last = arrive_last(counter, a.splits, &s_last);
+  stamp(kStArrived);
+  if (!last) return;
   int heads_k[kUnits], d0s[kUnits];
   bool live_k[kUnits];
 #pragma unroll
@@ -940,6 +970,7 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
     }
   }
   reset_counter(counter);
+  stamp(kStSplitMerge);
 }
 
 }  // namespace
@@ -982,6 +1013,18 @@ static int decode_impl(const char* what, const void* q, int64_t q_row_stride, in
                        xt_stream_t stream);
 
 // Workspace: [arrival counters, kCounterBytes][partials [rows, splits, q_heads, dim + 4] FP32]
+
+// The per-wave timeline buffer of the decode launches (xt_decode_timeline); NULL: off.
+static std::atomic<uint64_t*> g_timeline{nullptr};
+static std::atomic<size_t> g_timeline_bytes{0};
+
+extern "C" int xt_decode_timeline(uint64_t* stamps, size_t bytes) {
+  if (stamps && (!aligned(stamps, 8) || bytes < 64))
+    return fail(XT_EINVAL, "xt_decode_timeline: the stamp buffer must be 8-byte aligned and hold one wave's 8 stamps");
+  g_timeline_bytes.store(stamps ? bytes : 0);
+  g_timeline.store(stamps);
+  return ok();
+}
 
 static bool supported_dim(int dim) { return dim == 64 || dim == 128 || dim == 256; }
 
@@ -1349,6 +1392,9 @@ static int decode_impl(const char* what, const void* q, int64_t q_row_stride, in
   a.n_units = (int64_t)rows * a.kv_groups * splits;
   a.xcd_units = (uint32_t)(a.n_units / 8);
   a.xcd_extra = (uint32_t)(a.n_units % 8);
+  a.stamps = g_timeline.load();
+  a.stamp_blocks = a.stamps ? (uint32_t)std::min<int64_t>(a.n_units, (int64_t)(g_timeline_bytes.load() / ((size_t)waves * 64)))
+                            : 0u;
   const int64_t launched = a.n_units;
   if (launched > 0x7FFFFFFFLL) return fail(XT_EUNSUPPORTED, "%s: %lld workgroups", what, (long long)launched);
 

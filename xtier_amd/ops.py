@@ -759,6 +759,51 @@ def clock_mhz(device='cuda', iters=20000):
     return 100.0 * core / real if real > 0 else None
 
 
+TIMELINE_PHASES = ('entry', 'slot list ready', 'first step computed', 'main loop done', 'slices merged',
+                   'partials issued', 'arrival counted', 'split merge done')
+
+
+def decode_shape(rows, kv_heads, splits, dim=128, shared_lists=True):
+    """The decode kernel's launch shape for these sizes, as xt_sparse_decode_nvfp4 derives it: (KV heads per
+    workgroup, waves per workgroup, workgroups). 4 KV heads when that alone fills the CUs, else 2, else 1 (per-head
+    index lists: 1); 8 waves while the workgroups fit one round on the CUs (head size 256: always 4)."""
+    cus = device_cus()
+    if not shared_lists:
+        hpw = 1
+    elif kv_heads % 4 == 0 and rows * (kv_heads // 4) * splits >= cus:
+        hpw = 4
+    elif kv_heads % 2 == 0 and rows * (kv_heads // 2) * splits >= cus:
+        hpw = 2
+    else:
+        hpw = 1
+    units = rows * -(-kv_heads // hpw) * splits
+    return hpw, (4 if units > cus or dim == 256 else 8), units
+
+
+class decode_timeline:
+    """Per-wave timeline of the decode launches made inside the block (xt_decode_timeline):
+
+        with ops.decode_timeline(max_waves) as tl:
+            ops.sparse_decode(...)
+        tl.stamps   # int64 [max_waves, 8]: row g * W + w is wave w of workgroup g (W waves per workgroup: 8 for
+                    # decode batches that fit one round of workgroups, else 4), column i the 100 MHz clock at
+                    # TIMELINE_PHASES[i] of the last launch (0: not reached; rows past the launch's waves: 0)"""
+
+    def __init__(self, max_waves, device='cuda'):
+        self._buf = torch.zeros(max_waves, len(TIMELINE_PHASES), dtype=torch.int64, device=device)
+        self.stamps = None
+
+    def __enter__(self):
+        _lib.check(_lib.lib().xt_decode_timeline(_ptr(self._buf), self._buf.numel() * 8), 'decode_timeline')
+        return self
+
+    def __exit__(self, *exc):
+        torch.cuda.synchronize(self._buf.device)
+        _lib.check(_lib.lib().xt_decode_timeline(None, 0), 'decode_timeline')
+        self.stamps = self._buf.cpu().numpy()
+        return False
+
+
 def ceiling_mfma(iters, blocks, device='cuda'):
     """The sustained MFMA rate alone (xt_ceiling_mfma): `blocks` x 4 wavefronts x `iters` x 4 independent
     v_mfma_f32_32x32x16_f16 (32768 flops each). Returns the per-thread check values, 64 * iters each."""
