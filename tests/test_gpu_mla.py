@@ -168,6 +168,22 @@ def test_mla_fewer_heads(heads):
     _check(out, lse, ref, ref_lse)
 
 
+@pytest.mark.parametrize('heads,splits', [(128, 8), (128, 10), (100, 9), (16, 4), (64, 3)])
+def test_mla_split_merge_head_and_split_counts(heads, splits):
+    """Key splits with head counts that pad the last 16-head wave, more splits than 16-head waves, and splits that
+    hold no key (700 keys over 10 splits of 96): every row against the oracle, and a second launch on the same
+    workspace gives the same bits."""
+    w, inp = _case(61 + splits, rows=6, heads=heads, topk=700)
+    pool = _pool(w, 15)
+    scale = 1 / math.sqrt(576)
+    ws = torch.zeros(ops.mla_workspace_bytes(w.rows, heads, splits), dtype=torch.uint8, device='cuda')
+    out, lse = ops.sparse_mla(inp.q, pool, inp.slots, None, None, scale, splits=splits, ws=ws)
+    ref, ref_lse = _ref(inp.q, pool, inp.slots, None, None, scale)
+    _check(out, lse, ref, ref_lse)
+    out2, _ = ops.sparse_mla(inp.q, pool, inp.slots, None, None, scale, splits=splits, ws=ws)
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+
+
 def test_mla_split_layout_equals_interleaved():
     w, inp = _case(41)
     a = _pool(w, 12, layout='interleaved')
