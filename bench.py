@@ -73,12 +73,13 @@ def cpu_threads():
 
 def time_steps(step, layers, steps, warmup):
     """Times exactly `steps` layer-steps. After `warmup` eager steps, a graph of g layer-steps (layer l on its own
-    pool, g = min(layers, steps // 5), so that at least five full replays are timed) is replayed steps // g times and a
-    graph of the remaining steps once, with HIP events on the launching stream around each replay. Returns (ms per
-    layer-step over the whole timed region, per-layer-step µs of each full replay, g: the pools the timed region
-    rotates)."""
+    pool) is replayed steps // g times and a graph of the remaining steps once, with HIP events on the launching stream
+    around each replay. g = min(layers, max(8, steps // 5), steps): at least 8 pools when there are (a rotation of the
+    decode workloads then gathers more than the 256 MB MALL holds, so no launch finds the previous replay's records
+    there), and up to steps // 5, so that longer runs time at least five full replays. Returns (ms per layer-step over
+    the whole timed region, per-layer-step µs of each full replay, g: the pools the timed region rotates)."""
     import torch
-    g_len = max(1, min(layers, steps // 5 if steps >= 5 else steps))
+    g_len = max(1, min(layers, max(8, steps // 5), steps))
     for i in range(warmup):
         step(i % g_len)
     torch.cuda.synchronize()
