@@ -350,6 +350,31 @@ def test_decode_two_kv_heads_per_workgroup(splits):
     assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
 
 
+@pytest.mark.parametrize('kv,qh,batch', [(4, 16, 32), (2, 16, 64), (8, 64, 16), (4, 8, 32)])
+def test_decode_paired_waves_head_layouts(kv, qh, batch):
+    """Launches of 256 workgroups of 2 KV heads (8 waves each, one wave per pair of KV heads): GQA groups of 8, 4 and 2
+    (columns past the group are padding), one pair (2 KV heads) and four pairs (8 KV heads), with -1 holes and a
+    short row: every row against the oracle, on SGLang's split pool and on the interleaved pool bit for bit."""
+    pool, pt, idx, q = _small_case(seed=kv * 100 + qh, batch=batch, heads=kv, qh=qh)
+    assert ops.decode_shape(batch, kv, 4)[:3] == (2, 8, 256)
+    idx = idx.numpy().copy()
+    idx[1, ::6] = -1
+    seq = np.full(batch, 3008, np.int32)
+    seq[2] = 1100
+    scale = 128 ** -0.5
+    lse = torch.empty(batch, qh, dtype=torch.float32, device='cuda')
+    out = ops.sparse_decode(q.cuda(), pool.raw, pt.cuda(), _dev(idx), _dev(seq), scale, page_size=64, lse=lse,
+                            splits=4)
+    ref, flash, lse_ref = _oracle(pool.raw, bf16_numpy(q), pt.numpy(), 64, np.arange(batch), idx, None, seq, scale)
+    _check(out, ref, flash)
+    assert np.abs(lse.cpu().numpy() - lse_ref).max() < 2e-3
+    il = KVPool(pool.raw[0].shape[0], kv, 128, layout='interleaved', gk=pool.raw[4].clone(), gv=pool.raw[5].clone())
+    for dst, src in zip((il.k_pay, il.v_pay, il.k_sf, il.v_sf), pool.raw[:4]):
+        dst.copy_(src)
+    out2 = ops.sparse_decode(q.cuda(), il.raw, pt.cuda(), _dev(idx), _dev(seq), scale, page_size=64, splits=4)
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+
+
 @pytest.mark.parametrize('splits', [4, 5])
 def test_decode_nan_scales_stay_in_their_head(splits):
     """A NaN E4M3 scale byte (0x7F / 0xFF) in a live key's row reaches exactly the outputs the oracle makes NaN: a K
