@@ -477,6 +477,15 @@ def run_block(args, w, ops, workloads):
     gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
     log(f'{w.name}: {ms * 1e3:.2f} us per layer-step, {gbs:.0f} GB/s algorithmic ({gbs / HBM_PEAK_GBS:.1%} of '
         f'{HBM_PEAK_GBS:.0f}), splits {splits}')
+    timeline = None
+    if args.timeline:   # one launch on the pool used half a rotation ago, as for the token-index decode
+        hpw, waves, units = ops.decode_shape(w.batch, w.kv_heads, splits, w.dim, shared_lists=False)
+        torch.cuda.synchronize()
+        with ops.decode_timeline(units * waves) as tl:
+            step(rot // 2)
+        timeline = timeline_summary(tl.stamps, waves, ops.TIMELINE_PHASES)
+        timeline['shape'] = {'kv_heads_per_workgroup': hpw, 'waves_per_workgroup': waves, 'workgroups': units}
+        log('timeline: ' + json.dumps(timeline))
     record = {
         'metric': 'NVFP4-KV block-sparse decode HBM GB/s', 'value': round(gbs, 1), 'unit': 'GB/s', 'n_gpus': 1,
         'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per, rot), 'higher_is_better': True,
@@ -489,6 +498,8 @@ def run_block(args, w, ops, workloads):
                      'frac': round(gbs / HBM_PEAK_GBS, 4), 'traffic': None},
         'cpu_baseline': None if args.no_cpu_baseline else block_cpu(pools[0], inp, w, args.cpu_seconds),
     }
+    if timeline is not None:
+        record['timeline'] = timeline
     emit(record)
 
 
@@ -1113,7 +1124,8 @@ def main():
     p.add_argument('--no-layout-compare', action='store_true',
                    help='decode workloads: skip timing the same step on the other pool layout')
     p.add_argument('--timeline', action='store_true',
-                   help='decode workloads: after the timed region, one more launch with the per-wave timeline '
+                   help='decode workloads (token and block indices): after the timed region, one more launch with the '
+                        'per-wave timeline '
                         '(xt_decode_timeline) and its phase times in the record')
     p.add_argument('--copy-calibration', type=int, default=0, metavar='MIB',
                    help='only copy MIB MiB between two device buffers 8 times (the known-size kernel that scales the '
