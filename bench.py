@@ -108,7 +108,7 @@ def time_steps(step, layers, steps, warmup):
     return ev[0].elapsed_time(ev[-1]) / steps, per, g_len
 
 
-def timeline_summary(stamps, waves, phases):
+def timeline_summary(stamps, waves, phases, loop_phase='main loop done'):
     """Phase times of one decode launch from its per-wave stamps (100 MHz ticks, rows g * waves + w): per phase the
     p10 / p50 / p90 / max over the waves that reached it, in µs from the earliest wave's entry; and the spread of the
     main loop's end within a workgroup (its last wave minus its first)."""
@@ -119,6 +119,8 @@ def timeline_summary(stamps, waves, phases):
     t0 = st[:, :, 0].min()
     out = {'unit': 'µs from the first wave entry of the launch (100 MHz clock)', 'phases': {}}
     for i, name in enumerate(phases):
+        if name.startswith('('):
+            continue
         col = st[:, :, i].ravel()
         col = col[col > 0]
         if col.size == 0:
@@ -127,7 +129,7 @@ def timeline_summary(stamps, waves, phases):
         out['phases'][name] = {'waves': int(col.size), 'p10': round(float(np.percentile(rel, 10)), 2),
                                'p50': round(float(np.percentile(rel, 50)), 2),
                                'p90': round(float(np.percentile(rel, 90)), 2), 'max': round(float(rel.max()), 2)}
-    loop = st[:, :, 3]
+    loop = st[:, :, list(phases).index(loop_phase)]
     ok = (loop > 0).all(1)
     if ok.any():
         d = (loop[ok].max(1) - loop[ok].min(1)) / 100.0
@@ -379,6 +381,15 @@ def run_mla(args, w, ops, workloads):
     gbs = w.algorithmic_bytes() / (ms * 1e-3) / 1e9
     log(f'{w.name}: {ms * 1e3:.1f} us per step, {tflops:.1f} TFLOP/s ({tflops / MFMA_PEAK_TFLOPS:.1%} of '
         f'{MFMA_PEAK_TFLOPS:.0f}), {gbs:.0f} GB/s gathered, splits {splits}')
+    timeline = None
+    if args.timeline:   # one more launch (decode: on the cache used half a rotation ago) with the per-wave stamps
+        units = w.rows * splits
+        torch.cuda.synchronize()
+        with ops.decode_timeline(units * 8, kind='mla') as tl:
+            step(rot // 2)
+        timeline = timeline_summary(tl.stamps, 8, ops.MLA_TIMELINE_PHASES)
+        timeline['shape'] = {'waves_per_workgroup': 8, 'workgroups': units, 'splits': splits}
+        log('timeline: ' + json.dumps(timeline))
     record = {
         'metric': 'NVFP4 sparse MLA attention TFLOP/s', 'value': round(tflops, 2), 'unit': 'TFLOP/s', 'n_gpus': 1,
         'steps': steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 6), 'timing': spread(per, rot), 'higher_is_better': True,
@@ -392,6 +403,8 @@ def run_mla(args, w, ops, workloads):
                      'frac': round(tflops / MFMA_PEAK_TFLOPS, 4), 'traffic': None},
         'cpu_baseline': None if args.no_cpu_baseline else mla_cpu(pools[0], inp, w, scale, args.cpu_seconds),
     }
+    if timeline is not None:
+        record['timeline'] = timeline
     emit(record)
 
 
@@ -1124,9 +1137,9 @@ def main():
     p.add_argument('--no-layout-compare', action='store_true',
                    help='decode workloads: skip timing the same step on the other pool layout')
     p.add_argument('--timeline', action='store_true',
-                   help='decode workloads (token and block indices): after the timed region, one more launch with the '
+                   help='decode and sparse-MLA workloads: after the timed region, one more launch with the '
                         'per-wave timeline '
-                        '(xt_decode_timeline) and its phase times in the record')
+                        '(xt_decode_timeline, xt_mla_timeline) and its phase times in the record')
     p.add_argument('--copy-calibration', type=int, default=0, metavar='MIB',
                    help='only copy MIB MiB between two device buffers 8 times (the known-size kernel that scales the '
                         'FETCH_SIZE / WRITE_SIZE counters), then exit')

@@ -359,3 +359,21 @@ def test_mla_latent_magnitudes_over_three_decades(top):
     assert max_rel < 1e-2 and rms_rel < 4e-3, (max_rel, rms_rel)
     # scores here reach ~15: the FP16 rounding of the scaled query (2^-11 relative) moves the LSE in proportion
     assert np.all(np.abs(lse.cpu().numpy() - ref_lse) <= 2e-3 + 2.0 ** -10 * np.abs(ref_lse))
+
+
+@pytest.mark.parametrize('splits', [1, 2])
+def test_mla_timeline(splits):
+    """The per-wave timeline of the sparse MLA kernel (xt_mla_timeline): every wave of every (row, split) workgroup
+    stamps its phases in order, and the outputs are those of the same launch without the timeline."""
+    w, inp = _case(81, rows=6)
+    pool = _pool(w, 17)
+    scale = 1 / math.sqrt(576)
+    plain, _ = ops.sparse_mla(inp.q, pool, inp.slots, None, None, scale, splits=splits)
+    units = w.rows * splits
+    with ops.decode_timeline(units * 8 + 8, kind='mla') as tl:
+        timed, _ = ops.sparse_mla(inp.q, pool, inp.slots, None, None, scale, splits=splits)
+    assert torch.equal(plain.view(torch.int16), timed.view(torch.int16))
+    st = tl.stamps
+    assert not st[units * 8:].any()
+    st = st[:units * 8, :6]
+    assert (st > 0).all() and (np.diff(st, axis=1) >= 0).all()

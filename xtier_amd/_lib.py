@@ -84,6 +84,7 @@ SIGNATURES = {
     'xt_ceiling_mfma': (_I, [_P, ctypes.c_int, ctypes.c_int, _P]),
     'xt_clock_probe': (_I, [_P, ctypes.c_int, _P]),
     'xt_decode_timeline': (_I, [_P, _Z]),
+    'xt_mla_timeline': (_I, [_P, _Z]),
     'xt_ceiling_launch': (_I, [ctypes.c_int, _P]),
     'xt_ceiling_split_merge': (_I, [_P, ctypes.c_int, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P]),
     'xt_qsa_indexer_logits': (_I, [_P, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P,

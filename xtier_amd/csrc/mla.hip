@@ -36,6 +36,9 @@
 #include "xt_common.h"
 #include "xt_host.h"
 
+#include <algorithm>
+#include <atomic>
+
 namespace xt {
 namespace {
 
@@ -72,6 +75,8 @@ constexpr int kSlotIters = 11;           // slot list entries per thread: (max k
 template <int F>
 constexpr int kQTile = (kQChunks<F> - kQReg<F>) * kMHeads * kQRow * 2;
 constexpr int kRescaleM = 8;
+// The phases of the per-wave timeline (xt_mla_timeline), in stamp order.
+enum { kMsEntry, kMsSlots, kMsQuery, kMsTile0, kMsLoop, kMsOut, kMlaStamps = 8 };
 
 struct CacheDev {
   const uint8_t* pay;                // NVFP4: latent payload; V4: the page buffer
@@ -103,6 +108,8 @@ struct MlaArgs {
                                      // normalized by its own sum
   float* ml;                         // [rows, splits, heads, 2]: the split's running max (log2 domain) and sum
   uint32_t xcd_units, xcd_extra;
+  uint64_t* stamps;                  // per-wave timeline (xt_mla_timeline), NULL: off
+  uint32_t stamp_blocks;             // workgroups whose stamps fit the buffer
   int o32;                           // NVFP4: every cache has fewer than 2^24 slots and all its rows within 2^32
                                      // bytes, so record offsets are one 24-bit multiply-add (else 64-bit arithmetic)
 };
@@ -289,7 +296,9 @@ __device__ inline int64_t part_index(const MlaArgs& a, int64_t row, int split, i
   return ((((row * a.splits + split) * waves + wave) * 16 + k) * 64 + lane) * 8;
 }
 
-template <int F, bool TWO>
+// TL: the per-wave timeline build (xt_mla_timeline), launched only while a stamp buffer is set, so the kernel the
+// serving path runs carries none of its instructions or registers.
+template <int F, bool TWO, bool TL>
 __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
   constexpr int kQC = kQChunks<F>, kQR = kQReg<F>, kLatC = kLatChunks<F>;
   extern __shared__ __align__(16) uint8_t lds[];
@@ -298,6 +307,10 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
                "s"(a.len[0]), "s"(a.len[1]), "s"(a.q), "s"(a.q_rs), "s"(a.q_hs), "s"(a.heads));
   // XCD-aware numbering as in the decode kernel: a row's splits run on one XCD
   const uint32_t gidx = blockIdx.x;
+  // per-wave timeline (diagnostics, off unless xt_mla_timeline set a buffer): the first lane of every wave writes the
+  // 100 MHz constant clock at each phase (kMlaStamps per wave); a branch uniform over the launch otherwise
+  const bool timeline = TL && gidx < a.stamp_blocks;
+  const uint64_t t_entry = timeline ? __builtin_amdgcn_s_memrealtime() : 0;
   const uint32_t xcd = gidx & 7u;
   const uint32_t u = xcd * a.xcd_units + min(xcd, a.xcd_extra) + (gidx >> 3);
   const int split = (int)(u % (uint32_t)a.splits);
@@ -305,6 +318,20 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hl = lane & 15, j = lane >> 4;
   const int head = 16 * wave + hl;
   const bool head_live = head < a.heads;
+  // (the wave's stamp address is formed at each stamp from values the loop keeps anyway: kept live across the main
+  // loop it would take registers the loop needs)
+  auto stamp = [&](int phase) {
+    if (timeline) {
+      const uint64_t t = __builtin_amdgcn_s_memrealtime();
+      if ((hl | j) == 0) a.stamps[((uint64_t)gidx * kMWaves + wave) * kMlaStamps + phase] = t;
+    }
+  };
+  if (timeline && lane == 0) {   // phases a wave does not reach stay 0
+    uint64_t* const my_stamps = a.stamps + ((uint64_t)gidx * kMWaves + wave) * kMlaStamps;
+    my_stamps[kMsEntry] = t_entry;
+#pragma unroll
+    for (int i = 1; i < kMlaStamps; ++i) my_stamps[i] = 0;
+  }
 
   // two K tiles: step n computes on tile n % 2 while the next step's keys are dequantized into the other
   uint16_t* ktiles = reinterpret_cast<uint16_t*>(lds);
@@ -344,6 +371,7 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
     if (i < total) slots[i] = e;
   }
   __syncthreads();
+  stamp(kMsSlots);
 
   // B operands of q.k, chunks 0..kQR-1 in registers, the rest in LDS: NVFP4, FP16 of q * 2^-e, exact, with 2^e per
   // head from its largest magnitude (pow2_query_scale), and scale * log2(e) * 2^e applied to the FP32 scores; V4, q
@@ -411,10 +439,12 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
   for (int i = 0; i < 32; ++i) acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   Raw<F> raw;
+  stamp(kMsQuery);
   load_raw<F, TWO>(a, slots, 0, raw);
   dequant<F, TWO>(a, slots, 0, raw, ktiles);
   if (a.steps > 1) load_raw<F, TWO>(a, slots, 1, raw);
   __syncthreads();
+  stamp(kMsTile0);
   for (int step = 0; step < a.steps; ++step) {
     const uint16_t* kt = ktiles + (step & 1) * (kKTile<F> / 2);
     // the next step's keys into the other tile (its readers finished before the previous barrier; after the last step
@@ -506,22 +536,39 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
     }
     __syncthreads();
   }
+  stamp(kMsLoop);
   // the 4 lanes of a head hold disjoint key subsets of l
   const float l_tot = sum4_lanes16(l);
 
   if (a.splits == 1) {
-    if (!head_live) return;
+    // the wave's 16 heads x 512 dims, normalized, staged in LDS as head rows of 1 KiB (the key and query tiles are
+    // free: every wave passed the last step's barrier), then written back a head row per store instruction (64
+    // lanes x 16 bytes); from the accumulators' lane order each store would scatter 4-byte pieces over 16 rows
+    if (16 * wave >= a.heads) return;   // no live head in this wave
     const float m_use = (m == -__builtin_inff()) ? 0.0f : m;
     float total = l_tot;
-    if (a.sink) total += __builtin_amdgcn_exp2f(a.sink[head] * kLog2e - m_use);
+    if (a.sink) total += __builtin_amdgcn_exp2f(a.sink[min(head, a.heads - 1)] * kLog2e - m_use);
     const float inv = l_tot > 0.0f ? (TWO ? fmaxf(g0, g1) : g0) / total : 0.0f;
+    uint16_t* stage = reinterpret_cast<uint16_t*>(lds) + wave * 16 * kDl;
 #pragma unroll
     for (int dt = 0; dt < 32; ++dt) {
-      const float v[4] = {acc[dt][0] * inv, acc[dt][1] * inv, acc[dt][2] * inv, acc[dt][3] * inv};
-      store_vals(a, row, head, 16 * dt + 4 * j, v, 4);
+      const float v0 = acc[dt][0] * inv, v1 = acc[dt][1] * inv, v2 = acc[dt][2] * inv, v3 = acc[dt][3] * inv;
+      const uint32_t w0 = a.out_dtype == XT_DTYPE_BF16 ? (f32_to_bf16_bits(v0) | (f32_to_bf16_bits(v1) << 16))
+                                                       : (f32_to_f16_bits(v0) | (f32_to_f16_bits(v1) << 16));
+      const uint32_t w1 = a.out_dtype == XT_DTYPE_BF16 ? (f32_to_bf16_bits(v2) | (f32_to_bf16_bits(v3) << 16))
+                                                       : (f32_to_f16_bits(v2) | (f32_to_f16_bits(v3) << 16));
+      *reinterpret_cast<uint2*>(stage + hl * kDl + 16 * dt + 4 * j) = make_uint2(w0, w1);
     }
-    if (a.lse && j == 0)
+    if (head_live && a.lse && j == 0)
       a.lse[row * a.heads + head] = l_tot > 0.0f ? (m + __builtin_log2f(l_tot)) * kLn2 : -__builtin_inff();
+    // (the stage is this wave's own: its LDS writes complete before its reads, no barrier)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const uint4 x = *reinterpret_cast<const uint4*>(stage + r * kDl + 8 * lane);
+      if (16 * wave + r < a.heads)
+        *reinterpret_cast<uint4*>(a.out + row * a.o_rs + (int64_t)(16 * wave + r) * a.o_hs + 8 * lane) = x;
+    }
+    stamp(kMsOut);
     return;
   }
   // 2. the split's output normalized by its own sum (NVFP4: FP16, a convex combination of e2m1 * e4m3 values, so at
@@ -549,6 +596,7 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
   }
   if (head_live && j == 0)
     *reinterpret_cast<float2*>(a.ml + (((int64_t)row * a.splits + split) * a.heads + head) * 2) = float2{m, l_tot};
+  stamp(kMsOut);
 }
 
 // Split merge: thread = (row, wave w, dim-tile pair k, lane) of the partials' lane order: head 16w + lane % 16, dims
@@ -683,6 +731,10 @@ size_t mla_workspace_bytes(int rows, int heads, int splits, size_t part_elem) {
   return kCounterBytes + (size_t)rows * splits * (padded * kDl * part_elem + heads * 2 * sizeof(float));
 }
 
+// The per-wave timeline buffer of the MLA launches (xt_mla_timeline); NULL: off.
+std::atomic<uint64_t*> g_mla_timeline{nullptr};
+std::atomic<size_t> g_mla_timeline_bytes{0};
+
 // Everything but the caches: checks, key lists, split sizing, workspace carving and the launches.
 template <int F>
 int mla_launch(const char* what, MlaArgs& a, bool extra, const void* q, int64_t q_row_stride, int64_t q_head_stride,
@@ -733,15 +785,26 @@ int mla_launch(const char* what, MlaArgs& a, bool extra, const void* q, int64_t 
   if (n_units > 0x7FFFFFFFLL) return fail(XT_EUNSUPPORTED, "%s: %lld workgroups", what, (long long)n_units);
   a.xcd_units = (uint32_t)(n_units / 8);
   a.xcd_extra = (uint32_t)(n_units % 8);
-  const void* fn = extra ? reinterpret_cast<const void*>(&mla_kernel<F, true>)
-                         : reinterpret_cast<const void*>(&mla_kernel<F, false>);
+  a.stamps = g_mla_timeline.load();
+  a.stamp_blocks = a.stamps ? (uint32_t)std::min<int64_t>(
+                                  n_units, (int64_t)(g_mla_timeline_bytes.load() / ((size_t)kMWaves * kMlaStamps * 8)))
+                            : 0u;
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)n_units), block(64 * kMWaves);
+  const bool tl = a.stamps != nullptr;
+  const void* fn = extra ? (tl ? reinterpret_cast<const void*>(&mla_kernel<F, true, true>)
+                               : reinterpret_cast<const void*>(&mla_kernel<F, true, false>))
+                         : (tl ? reinterpret_cast<const void*>(&mla_kernel<F, false, true>)
+                               : reinterpret_cast<const void*>(&mla_kernel<F, false, false>));
   if (int e = allow_lds(fn, lds_bytes, what)) return e;
-  if (extra)
-    hipLaunchKernelGGL((mla_kernel<F, true>), dim3((unsigned)n_units), dim3(64 * kMWaves), lds_bytes,
-                       reinterpret_cast<hipStream_t>(stream), a);
+  if (extra && tl)
+    hipLaunchKernelGGL((mla_kernel<F, true, true>), grid, block, lds_bytes, st, a);
+  else if (extra)
+    hipLaunchKernelGGL((mla_kernel<F, true, false>), grid, block, lds_bytes, st, a);
+  else if (tl)
+    hipLaunchKernelGGL((mla_kernel<F, false, true>), grid, block, lds_bytes, st, a);
   else
-    hipLaunchKernelGGL((mla_kernel<F, false>), dim3((unsigned)n_units), dim3(64 * kMWaves), lds_bytes,
-                       reinterpret_cast<hipStream_t>(stream), a);
+    hipLaunchKernelGGL((mla_kernel<F, false, false>), grid, block, lds_bytes, st, a);
   if (splits > 1) {
     const int64_t threads = (int64_t)rows * ((heads + 15) / 16) * 16 * 64;   // (row, wave, dim-tile pair, lane)
     hipLaunchKernelGGL(mla_merge_kernel<F>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
@@ -781,6 +844,14 @@ using namespace xt;
 
 // Workspace: [kCounterBytes, unused here: the counter region of the decode entry points][partial outputs [rows,
 // splits, heads, 512] FP16 (NVFP4) or FP32 (V4)][partial max and sum [rows, splits, heads, 2] FP32]
+
+extern "C" int xt_mla_timeline(uint64_t* stamps, size_t bytes) {
+  if (stamps && (!aligned(stamps, 8) || bytes < 64))
+    return fail(XT_EINVAL, "xt_mla_timeline: the stamp buffer must be 8-byte aligned and hold one wave's 8 stamps");
+  g_mla_timeline_bytes.store(stamps ? bytes : 0);
+  g_mla_timeline.store(stamps);
+  return ok();
+}
 
 extern "C" size_t xt_sparse_mla_workspace_bytes(int rows, int heads, int splits) {
   return mla_workspace_bytes(rows, heads, splits, 2);

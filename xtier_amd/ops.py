@@ -780,6 +780,10 @@ def decode_shape(rows, kv_heads, splits, dim=128, shared_lists=True):
     return hpw, (4 if units > cus or dim == 256 else 8), units
 
 
+MLA_TIMELINE_PHASES = ('entry', 'slot list ready', 'query ready', 'first key tile ready', 'main loop done',
+                       'outputs or partials issued', '(unused)', '(unused)')
+
+
 class decode_timeline:
     """Per-wave timeline of the decode launches made inside the block (xt_decode_timeline):
 
@@ -787,19 +791,22 @@ class decode_timeline:
             ops.sparse_decode(...)
         tl.stamps   # int64 [max_waves, 8]: row g * W + w is wave w of workgroup g (W waves per workgroup: 8 for
                     # decode batches that fit one round of workgroups, else 4), column i the 100 MHz clock at
-                    # TIMELINE_PHASES[i] of the last launch (0: not reached; rows past the launch's waves: 0)"""
+                    # TIMELINE_PHASES[i] of the last launch (0: not reached; rows past the launch's waves: 0)
 
-    def __init__(self, max_waves, device='cuda'):
+    kind='mla': the sparse MLA launches instead (xt_mla_timeline; W = 8, phases MLA_TIMELINE_PHASES)."""
+
+    def __init__(self, max_waves, device='cuda', kind='decode'):
         self._buf = torch.zeros(max_waves, len(TIMELINE_PHASES), dtype=torch.int64, device=device)
+        self._set = 'xt_mla_timeline' if kind == 'mla' else 'xt_decode_timeline'
         self.stamps = None
 
     def __enter__(self):
-        _lib.check(_lib.lib().xt_decode_timeline(_ptr(self._buf), self._buf.numel() * 8), 'decode_timeline')
+        _lib.check(getattr(_lib.lib(), self._set)(_ptr(self._buf), self._buf.numel() * 8), self._set)
         return self
 
     def __exit__(self, *exc):
         torch.cuda.synchronize(self._buf.device)
-        _lib.check(_lib.lib().xt_decode_timeline(None, 0), 'decode_timeline')
+        _lib.check(getattr(_lib.lib(), self._set)(None, 0), self._set)
         self.stamps = self._buf.cpu().numpy()
         return False
 
