@@ -491,7 +491,8 @@ int xt_decode_timeline(uint64_t* stamps, size_t bytes);
 /* xt_mla_timeline: the same for the sparse MLA kernel (xt_sparse_mla_nvfp4, xt_sparse_mla_fp8; no counterpart in the
  * reference): 8 stamps per wavefront of its 8-wave workgroups, stamps[(g * 8 + w) * 8 + i], i = 0 entry, 1 the split's
  * slot list in LDS, 2 the query operands ready, 3 the first key tile dequantized, 4 the main loop done, 5 the outputs
- * (one split) or partials issued (waves without live heads: 0); 6 and 7 read 0. NULL turns it off (the default). */
+ * (one split) or partials issued (waves without live heads: 0), 6 (one split) the outputs staged in LDS, before 5;
+ * 7 reads 0. NULL turns it off (the default). */
 int xt_mla_timeline(uint64_t* stamps, size_t bytes);
 
 #ifdef __cplusplus

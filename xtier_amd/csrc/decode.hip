@@ -516,12 +516,8 @@ __device__ inline void compute_step_pair(const WaveCtx& w, int step, const PairS
 __device__ inline void store_out(const DecodeArgs& a, int row, int head, int d0, const float* v, int n) {
   uint16_t* o = a.out + (int64_t)row * a.o_rs + (int64_t)head * a.o_hs + d0;
   for (int e = 0; e < n; e += 2) {
-    uint32_t packed;
-    if (a.out_dtype == XT_DTYPE_BF16)
-      packed = f32_to_bf16_bits(v[e]) | (f32_to_bf16_bits(v[e + 1]) << 16);
-    else
-      packed = f32_to_f16_bits(v[e]) | (f32_to_f16_bits(v[e + 1]) << 16);
-    *reinterpret_cast<uint32_t*>(o + e) = packed;
+    *reinterpret_cast<uint32_t*>(o + e) =
+        a.out_dtype == XT_DTYPE_BF16 ? pack2_16<true>(v[e], v[e + 1]) : pack2_16<false>(v[e], v[e + 1]);
   }
 }
 

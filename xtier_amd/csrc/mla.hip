@@ -76,7 +76,7 @@ template <int F>
 constexpr int kQTile = (kQChunks<F> - kQReg<F>) * kMHeads * kQRow * 2;
 constexpr int kRescaleM = 8;
 // The phases of the per-wave timeline (xt_mla_timeline), in stamp order.
-enum { kMsEntry, kMsSlots, kMsQuery, kMsTile0, kMsLoop, kMsOut, kMlaStamps = 8 };
+enum { kMsEntry, kMsSlots, kMsQuery, kMsTile0, kMsLoop, kMsOut, kMsStaged, kMlaStamps = 8 };
 
 struct CacheDev {
   const uint8_t* pay;                // NVFP4: latent payload; V4: the page buffer
@@ -275,16 +275,15 @@ __device__ inline void dequant(const MlaArgs& a, const int32_t* slots, int step,
   }
 }
 
-__device__ inline void store_vals(const MlaArgs& a, int64_t row, int head, int d0, const float* v, int n) {
-  uint16_t* o = a.out + row * a.o_rs + (int64_t)head * a.o_hs + d0;
-  for (int e = 0; e < n; e += 2) {
-    uint32_t packed;
-    if (a.out_dtype == XT_DTYPE_BF16)
-      packed = f32_to_bf16_bits(v[e]) | (f32_to_bf16_bits(v[e + 1]) << 16);
-    else
-      packed = f32_to_f16_bits(v[e]) | (f32_to_f16_bits(v[e + 1]) << 16);
-    *reinterpret_cast<uint32_t*>(o + e) = packed;
-  }
+// A wave's 16 heads x 512 output dims (accumulator acc[dt][r]: head hl, dim 16 dt + 4 j + r), times inv, as head
+// rows of 1 KiB in LDS. The 16-byte pieces of row r sit at piece index ^ r: rows are 1 KiB apart, so unswizzled the 16
+// heads of a write would all fall on the same banks; swizzled, each half-wave's write covers 64 distinct banks.
+template <bool BF>
+__device__ inline void stage_rows(uint16_t* stage, const float4_t (&acc)[32], float inv, int hl, int j) {
+#pragma unroll
+  for (int dt = 0; dt < 32; ++dt)
+    *reinterpret_cast<uint2*>(stage + hl * kDl + 8 * ((2 * dt + (j >> 1)) ^ hl) + 4 * (j & 1)) =
+        make_uint2(pack2_16<BF>(acc[dt][0] * inv, acc[dt][1] * inv), pack2_16<BF>(acc[dt][2] * inv, acc[dt][3] * inv));
 }
 
 
@@ -448,10 +447,11 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
   for (int step = 0; step < a.steps; ++step) {
     const uint16_t* kt = ktiles + (step & 1) * (kKTile<F> / 2);
     // the next step's keys into the other tile (its readers finished before the previous barrier; after the last step
-    // it is the padding step, all zeros, never read), then the raw records of the step after (the last one again at
-    // the end): no branch, so the compiler can interleave this VALU work with the MFMAs below
+    // it is the padding step, all zeros, never read), then the raw records of the step after, if there is one (a
+    // branch uniform over the launch: on the last two steps it skips loads whose records were already read, which the
+    // epilogue would otherwise wait for before reusing their registers; the padding step's dequant ignores them)
     dequant<F, TWO>(a, slots, step + 1, raw, ktiles + ((step + 1) & 1) * (kKTile<F> / 2));
-    load_raw<F, TWO>(a, slots, min(step + 2, a.steps - 1), raw);
+    if (step + 2 < a.steps) load_raw<F, TWO>(a, slots, step + 2, raw);
     const uint32_t valid = (uint32_t)__builtin_amdgcn_ballot_w64(lane < kMSteps &&
                                                                   entry_valid(slots[step * kMSteps + (lane & 31)]));
     // S^T for the two 16-key tiles, one MFMA chain each. The K fragments (and LDS-resident query chunks) of chunk
@@ -543,30 +543,27 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
   if (a.splits == 1) {
     // the wave's 16 heads x 512 dims, normalized, staged in LDS as head rows of 1 KiB (the key and query tiles are
     // free: every wave passed the last step's barrier), then written back a head row per store instruction (64
-    // lanes x 16 bytes); from the accumulators' lane order each store would scatter 4-byte pieces over 16 rows
+    // lanes x 16 bytes, the pieces of head row r at piece index ^ r); from the accumulators' lane order each store
+    // would scatter 4-byte pieces over 16 rows
     if (16 * wave >= a.heads) return;   // no live head in this wave
     const float m_use = (m == -__builtin_inff()) ? 0.0f : m;
     float total = l_tot;
     if (a.sink) total += __builtin_amdgcn_exp2f(a.sink[min(head, a.heads - 1)] * kLog2e - m_use);
     const float inv = l_tot > 0.0f ? (TWO ? fmaxf(g0, g1) : g0) / total : 0.0f;
     uint16_t* stage = reinterpret_cast<uint16_t*>(lds) + wave * 16 * kDl;
-#pragma unroll
-    for (int dt = 0; dt < 32; ++dt) {
-      const float v0 = acc[dt][0] * inv, v1 = acc[dt][1] * inv, v2 = acc[dt][2] * inv, v3 = acc[dt][3] * inv;
-      const uint32_t w0 = a.out_dtype == XT_DTYPE_BF16 ? (f32_to_bf16_bits(v0) | (f32_to_bf16_bits(v1) << 16))
-                                                       : (f32_to_f16_bits(v0) | (f32_to_f16_bits(v1) << 16));
-      const uint32_t w1 = a.out_dtype == XT_DTYPE_BF16 ? (f32_to_bf16_bits(v2) | (f32_to_bf16_bits(v3) << 16))
-                                                       : (f32_to_f16_bits(v2) | (f32_to_f16_bits(v3) << 16));
-      *reinterpret_cast<uint2*>(stage + hl * kDl + 16 * dt + 4 * j) = make_uint2(w0, w1);
-    }
+    if (a.out_dtype == XT_DTYPE_BF16)
+      stage_rows<true>(stage, acc, inv, hl, j);
+    else
+      stage_rows<false>(stage, acc, inv, hl, j);
     if (head_live && a.lse && j == 0)
       a.lse[row * a.heads + head] = l_tot > 0.0f ? (m + __builtin_log2f(l_tot)) * kLn2 : -__builtin_inff();
+    stamp(kMsStaged);
     // (the stage is this wave's own: its LDS writes complete before its reads, no barrier)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const uint4 x = *reinterpret_cast<const uint4*>(stage + r * kDl + 8 * lane);
       if (16 * wave + r < a.heads)
-        *reinterpret_cast<uint4*>(a.out + row * a.o_rs + (int64_t)(16 * wave + r) * a.o_hs + 8 * lane) = x;
+        *reinterpret_cast<uint4*>(a.out + row * a.o_rs + (int64_t)(16 * wave + r) * a.o_hs + 8 * (lane ^ r)) = x;
     }
     stamp(kMsOut);
     return;
@@ -605,7 +602,8 @@ __global__ void __launch_bounds__(512) mla_kernel(const MlaArgs a) {
 // a running maximum across groups, so the usual four splits cost one round trip; a wave's loads of one split are one
 // contiguous run. A workgroup (256 threads: row, w, four consecutive k) holds 16 heads x 128 dims of output; it
 // stages them in LDS and writes each head's 256 bytes as 16 consecutive 16-byte pieces (written straight from the
-// lane order, every store instruction would scatter 64 pieces of 4 bytes over 16 head rows).
+// lane order, every store instruction would scatter 64 pieces of 4 bytes over 16 head rows). In the stage the pieces
+// of head row h sit at piece index ^ h, which spreads the 16 heads of an LDS write over distinct banks.
 template <int F>
 __global__ void __launch_bounds__(256) mla_merge_kernel(const MlaArgs a, int rows) {
   __shared__ __align__(16) uint16_t tile[16][128];
@@ -675,21 +673,19 @@ __global__ void __launch_bounds__(256) mla_merge_kernel(const MlaArgs a, int row
   const float inv = l_run > 0.0f ? gout / total : 0.0f;
   uint32_t pk[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float v0 = o[2 * e] * inv, v1 = o[2 * e + 1] * inv;
-    pk[e] = a.out_dtype == XT_DTYPE_BF16 ? (f32_to_bf16_bits(v0) | (f32_to_bf16_bits(v1) << 16))
-                                         : (f32_to_f16_bits(v0) | (f32_to_f16_bits(v1) << 16));
-  }
+  for (int e = 0; e < 4; ++e)
+    pk[e] = a.out_dtype == XT_DTYPE_BF16 ? pack2_16<true>(o[2 * e] * inv, o[2 * e + 1] * inv)
+                                         : pack2_16<false>(o[2 * e] * inv, o[2 * e + 1] * inv);
   const int c0 = d0 - 32 * k0;   // this thread's dims within the workgroup's 128: c0 .. c0+3 and c0+16 .. c0+19
-  *reinterpret_cast<uint2*>(&tile[hl][c0]) = make_uint2(pk[0], pk[1]);
-  *reinterpret_cast<uint2*>(&tile[hl][c0 + 16]) = make_uint2(pk[2], pk[3]);
+  *reinterpret_cast<uint2*>(&tile[hl][8 * ((c0 >> 3) ^ hl) + (c0 & 7)]) = make_uint2(pk[0], pk[1]);
+  *reinterpret_cast<uint2*>(&tile[hl][8 * (((c0 + 16) >> 3) ^ hl) + (c0 & 7)]) = make_uint2(pk[2], pk[3]);
   if (live && a.lse && d0 == 0)
     a.lse[(int64_t)row * a.heads + head] = l_run > 0.0f ? (mu + __builtin_log2f(l_run)) * kLn2 : -__builtin_inff();
   __syncthreads();
   // thread u: head 16 w + u / 16, dims 32 k0 + 8 (u % 16) .. +7
   const int sh = (int)threadIdx.x >> 4, sc = (int)threadIdx.x & 15;
   if (16 * w + sh < a.heads)
-    *reinterpret_cast<uint4*>(a.out + (int64_t)row * a.o_rs + (int64_t)(16 * w + sh) * a.o_hs + 32 * k0 + 8 * sc) =
+    *reinterpret_cast<uint4*>(a.out + (int64_t)row * a.o_rs + (int64_t)(16 * w + sh) * a.o_hs + 32 * k0 + 8 * (sc ^ sh)) =
         *reinterpret_cast<const uint4*>(&tile[sh][8 * sc]);
 }
 

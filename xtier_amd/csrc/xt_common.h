@@ -184,12 +184,19 @@ __device__ float uniform_load_f32(const float* p);
 __device__ float sum4_lanes16(float x);
 #endif
 
-// FP32 -> BF16 bits, round to nearest even; NaN -> quiet NaN with its sign.
+// FP32 -> BF16 bits, round to nearest even; NaN -> a quiet NaN with its sign. On the device this is gfx950's
+// v_cvt_pk_bf16_f32 (one instruction, two values when the compiler pairs the calls; denormals kept, as the kernels
+// run with FP32 denormals on), whose NaN keeps the top of its payload; the host spells the rounding out and returns
+// the canonical 0x7FC0.
 __host__ __device__ inline uint32_t f32_to_bf16_bits(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+#else
   uint32_t b;
   __builtin_memcpy(&b, &f, 4);
   if ((b & 0x7FFFFFFFu) > 0x7F800000u) return ((b >> 16) & 0x8000u) | 0x7FC0u;
   return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+#endif
 }
 __host__ __device__ inline float bf16_bits_to_f32(uint32_t h) {
   const uint32_t b = h << 16;
@@ -202,6 +209,21 @@ __host__ __device__ inline uint32_t f32_to_f16_bits(float f) {
   uint16_t u;
   __builtin_memcpy(&u, &h, 2);
   return u;
+}
+// Two FP32 values -> two BF16 (BF) or FP16 values, round to nearest even, `lo` in bits 0..15. On the device: one
+// v_cvt_pk_bf16_f32, or two v_cvt_f16_f32 and a pack.
+template <bool BF>
+__host__ __device__ inline uint32_t pack2_16(float lo, float hi) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  if constexpr (BF) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(float2_t{lo, hi}, bf16x2_t));
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(float2_t{lo, hi}, half2_t));
+  }
+#else
+  return BF ? f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16) : f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+#endif
 }
 
 }  // namespace xt

@@ -781,7 +781,7 @@ def decode_shape(rows, kv_heads, splits, dim=128, shared_lists=True):
 
 
 MLA_TIMELINE_PHASES = ('entry', 'slot list ready', 'query ready', 'first key tile ready', 'main loop done',
-                       'outputs or partials issued', '(unused)', '(unused)')
+                       'outputs or partials issued', 'outputs staged (one split)', '(unused)')
 
 
 class decode_timeline:
