@@ -674,7 +674,16 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
       }
     }
   }
-  __syncthreads();
+  // With one wave per slice and 64-key slices (the batch decode's paired waves, the one-KV-head shapes), thread 64 w + l
+  // wrote key 64 w + l, so every wave reads only the slots its own lanes wrote: LDS keeps a wave's accesses in order,
+  // and the wave goes on to its first K/V loads without waiting for the other waves' table loads. (A condition
+  // uniform over the workgroup.)
+  if (kHeadSets == 1 && slice_steps * KS == 64) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  } else {
+    __syncthreads();
+  }
   stamp(kStSlots);
 
   SoftmaxState<D> st;
