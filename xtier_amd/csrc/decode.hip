@@ -602,16 +602,17 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
   const int64_t irow = a.idx_rows ? uniform_load(a.idx_rows + row) : row;
   const int32_t* ip = a.indices + irow * a.idx_stride + (int64_t)kvg * a.idx_head_stride;
   const int bmask = (1 << a.block_shift) - 1;
-  // Loads that are not needed read a valid stand-in address (the row's length) instead of sitting in a branch:
-  // a branch around a load compiles to a wait right after it, which would serialize the batch.
+  // Lanes whose key is past the split read a valid stand-in address (the row's length) instead of sitting in a
+  // per-lane branch (its select would wait for the load right after it, serializing the batch); batches with no key
+  // of the split issue no loads at all (a branch uniform over the workgroup). The loaded words stay raw until every
+  // batch is issued.
   const int32_t* len_p = a.seq_lens + row;
-  int32_t pos[kSlotBatch];
+  int32_t ev[kSlotBatch];
 #pragma unroll
   for (int b = 0; b < kSlotBatch; ++b) {
     const int i = b * kThreads + (int)threadIdx.x, k = t0 + i;
-    const int32_t e0 = *((i < kmax) ? ip + (k >> a.block_shift) : len_p);
-    const int32_t e = (i < kmax) ? e0 : -1;
-    pos[b] = e < 0 ? -1 : (e << a.block_shift) + (k & bmask);
+    ev[b] = -1;
+    if (b == 0 || b * kThreads < kmax) ev[b] = *((i < kmax) ? ip + (k >> a.block_shift) : len_p);
   }
   // the row's count, length, causal limit and table row, and the global scales: scalar loads from addresses valid
   // whether or not the optional arrays are given (a missing one reads the row's length and is ignored), so none waits
@@ -635,6 +636,13 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
     const int64_t trow = a.row_req ? (int64_t)(((uint64_t)(uint32_t)req_hi << 32) | (uint32_t)req_lo) : row;
     const int32_t* tp = a.table + trow * a.table_stride;
     const int total = kSlices * slice_steps * KS;
+    int32_t pos[kSlotBatch];
+#pragma unroll
+    for (int b = 0; b < kSlotBatch; ++b) {
+      const int i = b * kThreads + (int)threadIdx.x, k = t0 + i;
+      const int32_t e = (i < kmax) ? ev[b] : -1;
+      pos[b] = e < 0 ? -1 : (e << a.block_shift) + (k & bmask);
+    }
     for (int i0 = 0;;) {
       // validity and table offsets of all kSlotBatch keys first, then their table loads back to back (a use of an
       // index between two table loads would wait for the earlier table load too)
@@ -648,9 +656,9 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
         toff[b] = a.page_shift >= 0 ? (tpos >> a.page_shift) : tpos / a.page_size;
       }
 #pragma unroll
-      for (int b = 0; b < kSlotBatch; ++b) {
-        const int32_t t = *(ok[b] ? tp + toff[b] : len_p);
-        ent[b] = ok[b] ? t : -1;
+      for (int b = 0; b < kSlotBatch; ++b) {   // (a lane with ok[b] false reads the stand-in; its entry is unused)
+        ent[b] = -1;
+        if (b == 0 || i0 + b * kThreads < n) ent[b] = *(ok[b] ? tp + toff[b] : len_p);
       }
 #pragma unroll
       for (int b = 0; b < kSlotBatch; ++b) {
