@@ -369,11 +369,12 @@ def run_mla(args, w, ops, workloads):
     ws = ops.workspace('cuda', ops.mla_workspace_bytes(w.rows, w.heads, splits, v4=w.fmt == 'fp8_v4'))
     out = torch.empty(w.rows, w.heads, 512, dtype=torch.bfloat16, device='cuda')
     lse = torch.empty(w.rows, w.heads, dtype=torch.float32, device='cuda')
+    lengths = torch.full((w.rows,), w.topk, dtype=torch.int32, device='cuda') if args.mla_lengths else None
     torch.cuda.synchronize()
     log(f'built {layers} latent caches of {w.slots} tokens in {time.time() - t0:.1f} s')
 
     def step(layer):
-        ops.sparse_mla(inp.q, pools[layer], inp.slots, None, None, scale, out=out, lse=lse, splits=splits, ws=ws)
+        ops.sparse_mla(inp.q, pools[layer], inp.slots, lengths, None, scale, out=out, lse=lse, splits=splits, ws=ws)
 
     steps = max(1, args.steps)
     ms, per, rot = time_steps(step, layers, steps, max(1, args.warmup))
@@ -397,7 +398,8 @@ def run_mla(args, w, ops, workloads):
         'config': {'workload': w.name, 'rows': w.rows, 'heads': w.heads, 'latent': w.latent, 'rope': w.rope,
                    'context': w.ctx, 'topk': w.topk, 'causal': w.causal,
                    'kv_format': 'fp8 v4 pages' if w.fmt == 'fp8_v4' else 'nvfp4 latent + bf16 rope',
-                   'layers_rotated': rot, 'splits': splits, 'cache_layout': args.layout},
+                   'layers_rotated': rot, 'splits': splits, 'cache_layout': args.layout,
+                   'list_lengths': bool(args.mla_lengths)},
         'us_per_step': round(ms * 1e3, 2), 'gathered_gbs': round(gbs, 1),
         'roofline': {'bound': 'mfma', 'achieved': round(tflops, 2), 'peak': MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
                      'frac': round(tflops / MFMA_PEAK_TFLOPS, 4), 'traffic': None},
@@ -1136,6 +1138,9 @@ def main():
     p.add_argument('--no-cpu-baseline', action='store_true')
     p.add_argument('--no-layout-compare', action='store_true',
                    help='decode workloads: skip timing the same step on the other pool layout')
+    p.add_argument('--mla-lengths', action='store_true',
+                   help='sparse-MLA workloads: pass per-row list lengths (every list full), as the DeepSeek hook '
+                        'passes topk_length')
     p.add_argument('--timeline', action='store_true',
                    help='decode and sparse-MLA workloads: after the timed region, one more launch with the '
                         'per-wave timeline '
