@@ -141,7 +141,8 @@ int xt_qsa_valid_counts(const int32_t* seq_lens, const int32_t* indices, int64_t
 /* --- fused sparse attention over the NVFP4 pool ------------------------------------------------------------------ */
 
 /* Device workspace the fused decode needs for `rows` query rows, q_heads heads of size dim and `splits` key splits
- * (split-K partials: running max, sum and unnormalized output per row, split and head). 0 on a bad argument. */
+ * (split-K partials: running max, sum and the output normalized by the split's sum, in FP16, per row, split and head;
+ * the size reserves room for FP32 outputs). 0 on a bad argument. */
 size_t xt_sparse_decode_workspace_bytes(int rows, int q_heads, int dim, int splits);
 
 /* Fused NVFP4 sparse GQA attention, one query per row (decode, verify, or a chunked prefill with one row per query

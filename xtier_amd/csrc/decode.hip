@@ -64,7 +64,8 @@ struct Geo {
   static constexpr int kVRow = kPay + 16;              // LDS bytes per key in the V transpose tile (80 at D = 128:
                                                        // no bank conflicts)
   static constexpr int kWaveLds = kStep * kVRow + kStep * kSf;   // V tile + V scale tile per wave
-  static constexpr int kPartStride = D + 4;            // floats per partial (split, head): accumulators, max, sum, pad
+  static constexpr int kPartBytes = 2 * D + 16;        // bytes per partial (split, head): D FP16 outputs normalized
+                                                       // by the split's sum, then FP32 max, sum and pad
   static constexpr int kMergeRow = 32 * kNT + 4;       // floats per lane in the slice merge: accumulators, max, sum, pad
   static constexpr int kPrefetch = D >= 256 ? 1 : 2;   // steps of loads in flight per wave (D = 256: registers;
                                                        // batch-32 decode: 2 steps 19.1 us, 4 steps 20.1 us)
@@ -112,7 +113,8 @@ struct DecodeArgs {
   int64_t o_rs, o_hs;
   int out_dtype;
   float* lse;
-  float* part;                       // [rows, splits, q_heads, D + 4]: accumulators, max (log2), sum
+  float* part;                       // [rows, splits, q_heads] records of 2 D + 16 bytes: D FP16 outputs normalized by
+                                     // the split's sum, max (log2), sum, pad (the workspace holds D + 4 floats each)
   int32_t* counters;                 // [rows * kv_groups] arrivals per (row, KV group); zero between launches
   int64_t n_units;                   // rows * kv_groups * splits workgroups, one per unit
   uint32_t xcd_units;                // n_units / 8
@@ -831,9 +833,9 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
   }
   __syncthreads();
   stamp(kStSliceMerge);
-  float* row_part = a.part + (int64_t)row * a.splits * a.q_heads * G::kPartStride;
+  uint8_t* row_part = reinterpret_cast<uint8_t*>(a.part) + (int64_t)row * a.splits * a.q_heads * G::kPartBytes;
   const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-      row_part, (short)0, a.splits > 1 ? (int)((int64_t)a.splits * a.q_heads * G::kPartStride * 4) : 0, 0x00020000);
+      row_part, (short)0, a.splits > 1 ? (int)((int64_t)a.splits * a.q_heads * G::kPartBytes) : 0, 0x00020000);
   const float gv = gv_v;
   constexpr int kParts = 8 * G::kNT;   // 4-dim pieces per lane
   constexpr int kUnits = (kHeadSets * 64 * kParts + kThreads - 1) / kThreads;   // pieces per thread
@@ -885,14 +887,19 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
       store_out(a, row, head, d0, v, 4);
       if (a.lse && d0 == 0)
         a.lse[(int64_t)row * a.q_heads + head] = l > 0.0f ? (mx + __builtin_log2f(l)) * kLn2 : -__builtin_inff();
-    } else {               // 3. partials of this row, written through
-      const int at = ((split * a.q_heads + head) * G::kPartStride) * 4;
-      store_partial(pr, at + d0 * 4, o);
-      if (d0 == 0) store_partial(pr, at + D * 4, float4_t{mx, l, 0.0f, 0.0f});
-      if constexpr (kKeep) {
+    } else {               // 3. partials of this row, written through: the output normalized by the split's own
+                           //    sum (a convex combination of e2m1 * e4m3 values, at most 2688 in magnitude) as FP16
+      const int at = (split * a.q_heads + head) * G::kPartBytes;
+      const float inv_l = l > 0.0f ? 1.0f / l : 0.0f;
+      const float4_t on = o * inv_l;
+      store_partial_h4(pr, at + d0 * 2, on);
+      if (d0 == 0) store_partial(pr, at + 2 * D, float4_t{mx, l, 0.0f, 0.0f});
+      if constexpr (kKeep) {   // rounded as the others' are read back, so the merge does not depend on who merges
         keep_m[k] = mx;
         keep_l[k] = l;
-        keep_o[k] = o;
+        const half2_t h0 = __builtin_convertvector(float2_t{on[0], on[1]}, half2_t);
+        const half2_t h1 = __builtin_convertvector(float2_t{on[2], on[3]}, half2_t);
+        keep_o[k] = float4_t{(float)h0[0], (float)h0[1], (float)h1[0], (float)h1[1]};
       }
     }
   }
@@ -939,9 +946,9 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const bool other = live_k[kb + b] && s0 + i < a.splits && (!kKeep || s0 + i != split);
-          const int at = other ? ((s0 + i) * a.q_heads + heads_k[kb + b]) * G::kPartStride * 4 : 0x7FFF0000;
-          ml[b][i] = load_partial(pr, at + D * 4);
-          x[b][i] = load_partial(pr, at + d0s[kb + b] * 4);
+          const int at = other ? ((s0 + i) * a.q_heads + heads_k[kb + b]) * G::kPartBytes : 0x7FFF0000;
+          ml[b][i] = load_partial(pr, at + 2 * D);
+          x[b][i] = load_partial_h4(pr, at + d0s[kb + b] * 2);
         }
 #pragma unroll
       for (int b = 0; b < kBatch; ++b) {
@@ -962,10 +969,10 @@ __global__ void __launch_bounds__(64 * W, (W == 4 && HPW == 4 && D <= 128) ? 3 :
         l_run[b] *= alpha;
         o[b] *= alpha;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float wgt = __builtin_amdgcn_exp2f(ml[b][i][0] - mu);
-          l_run[b] += wgt * ml[b][i][1];
-          o[b] += wgt * x[b][i];
+        for (int i = 0; i < 4; ++i) {   // the partials are normalized: weight 2^(m - mu) * l
+          const float wl = __builtin_amdgcn_exp2f(ml[b][i][0] - mu) * ml[b][i][1];
+          l_run[b] += wl;
+          o[b] += wl * x[b][i];
         }
         m_run[b] = mc;
       }

@@ -149,6 +149,22 @@ __device__ inline float4_t load_partial(__amdgpu_buffer_rsrc_t r, int byte_off) 
   const xt_u32x4_t w = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 17 /* sc0 sc1 */);
   return float4_t{__uint_as_float(w[0]), __uint_as_float(w[1]), __uint_as_float(w[2]), __uint_as_float(w[3])};
 }
+// The same for four values held as FP16 (8 bytes): RNE on the way out, exact on the way back.
+__device__ inline void store_partial_h4(__amdgpu_buffer_rsrc_t r, int byte_off, float4_t v) {
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  const half2_t a = __builtin_convertvector(float2_t{v[0], v[1]}, half2_t);
+  const half2_t b = __builtin_convertvector(float2_t{v[2], v[3]}, half2_t);
+  const u32x2_t w = {__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
+  __builtin_amdgcn_raw_buffer_store_b64(w, r, byte_off, 0, 16 /* sc1 */);
+}
+__device__ inline float4_t load_partial_h4(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  const u32x2_t w = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 17 /* sc0 sc1 */);
+  // (the words go through scalars: a bit cast of a vector element directly has read element 0 here)
+  const uint32_t w0 = w[0], w1 = w[1];
+  const half2_t a = __builtin_bit_cast(half2_t, w0), b = __builtin_bit_cast(half2_t, w1);
+  return float4_t{(float)a[0], (float)a[1], (float)b[0], (float)b[1]};
+}
 // Called by every thread after its partial stores. True in every thread of the workgroup that arrived last among
 // `splits`. `flag` is a __shared__ int of the caller.
 __device__ inline bool arrive_last(int32_t* counter, int splits, int* flag) {
@@ -167,6 +183,8 @@ __device__ inline void reset_counter(int32_t* counter) {
 __device__ float2_t pow2_query_scale(float qmax);
 __device__ void store_partial(__amdgpu_buffer_rsrc_t r, int byte_off, float4_t v);
 __device__ float4_t load_partial(__amdgpu_buffer_rsrc_t r, int byte_off);
+__device__ void store_partial_h4(__amdgpu_buffer_rsrc_t r, int byte_off, float4_t v);
+__device__ float4_t load_partial_h4(__amdgpu_buffer_rsrc_t r, int byte_off);
 __device__ bool arrive_last(int32_t* counter, int splits, int* flag);
 __device__ void reset_counter(int32_t* counter);
 template <int SEL>
