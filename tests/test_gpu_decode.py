@@ -406,6 +406,34 @@ def test_decode_nan_scales_stay_in_their_head(splits):
     assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
 
 
+@pytest.mark.parametrize('splits', [2, 4, 7])
+def test_decode_partials_at_the_value_limit(splits):
+    """Every V value at +-6 x 448 (E2M1 code +-6.0 under the largest finite E4M3 scale byte, 0x7E): a split's output
+    normalized by its own sum, which its FP16 partial holds before the V global scale is applied, reaches 2688 in
+    magnitude (dims 0..63 are +2688 in every key, so every split's partial and the output are exactly that times
+    the global scale, 1/4096 here; the other dims have random signs). Against the oracle, with 2, 4 and 7 key
+    splits."""
+    pool, pt, idx, q = _small_case(seed=83, batch=8)
+    v_pay, v_sf = pool.raw[1], pool.raw[3]          # [slots, 4 heads, 64] payload bytes, [slots, 4 heads, 8] scales
+    gen = torch.Generator().manual_seed(5)
+    signs = torch.randint(0, 2, (v_pay.shape[0], v_pay.shape[1], 128), generator=gen, dtype=torch.uint8)
+    signs[:, :, :64] = 0
+    nib = (7 | (signs << 3)).to(torch.uint8)        # 0x7: +6.0, 0xF: -6.0
+    v_pay.copy_((nib[:, :, 0::2] | (nib[:, :, 1::2] << 4)).cuda())
+    v_sf.fill_(0x7E)
+    pool.raw[5].fill_(1.0 / 4096)                   # applied after the merge: outputs up to 0.65625, partials 2688
+    seq = np.full(8, 3008, np.int32)
+    scale = 128 ** -0.5
+    out = ops.sparse_decode(q.cuda(), pool.raw, pt.cuda(), idx.cuda(), _dev(seq), scale, page_size=64, splits=splits)
+    ref, flash, _ = _oracle(pool.raw, bf16_numpy(q), pt.numpy(), 64, np.arange(8), idx.numpy(), None, seq, scale)
+    gv = float(pool.raw[5].item())
+    assert np.allclose(ref[:, :, :64], 2688.0 * gv)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    assert np.array_equal(got[:, :, :64], np.full_like(got[:, :, :64], float(torch.tensor(2688.0 * gv).bfloat16())))
+    _check(out, ref, flash)
+
+
 @pytest.mark.parametrize('batch,splits', [(32, 4), (6, 3)])
 def test_decode_timeline(batch, splits):
     """The per-wave timeline (xt_decode_timeline) of a launch of paired waves (32 rows x 4 KV heads x 4 splits) and of
