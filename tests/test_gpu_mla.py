@@ -86,6 +86,24 @@ def test_mla_small(splits, use_sink):
     _check(out, lse, ref, ref_lse)
 
 
+@pytest.mark.parametrize('splits', [1, 3])
+def test_mla_fp16_output(splits):
+    """An FP16 output tensor (the one-split epilogue's swizzled LDS stage and the split merge's, both converting by
+    RNE): within the tolerance of the oracle, and within an FP16 plus a BF16 rounding (bounded by 2^-7 of the larger
+    magnitude, 2^-25 below FP16's normal range) of the same call's BF16 output, with the same LSE."""
+    w, inp = _case(20261107 + splits, rows=6, heads=72)    # 72 heads: a wave with 8 padding heads
+    pool = _pool(w, 11)
+    scale = 1 / math.sqrt(576)
+    out16 = torch.empty(w.rows, w.heads, 512, dtype=torch.float16, device='cuda')
+    o16, lse16 = ops.sparse_mla(inp.q, pool, inp.slots, None, None, scale, out=out16, splits=splits)
+    ob, lseb = ops.sparse_mla(inp.q, pool, inp.slots, None, None, scale, splits=splits)
+    ref, ref_lse = _ref(inp.q, pool, inp.slots, None, None, scale)
+    _check(o16, lse16, ref, ref_lse)
+    a, b = o16.float(), ob.float()
+    assert torch.equal(lse16, lseb)
+    assert ((a - b).abs() <= torch.maximum(a.abs(), b.abs()) * 2.0 ** -7 + 2.0 ** -25).all()
+
+
 @pytest.mark.parametrize('mag', [1e-4, 1e3, 1e6, 'mixed'])
 def test_mla_query_magnitudes(mag):
     """Queries far from unit size (|q| ~ 1e-4, 1e3, 1e6, beyond FP16's range once scaled by scale * log2(e), and rows
